@@ -1,0 +1,251 @@
+/*
+ * neurocell_hip.h - C ABI of the MI355X (gfx950 / CDNA4) Neurocell v2 VNN propagation step.
+ *
+ * One extern "C" entry point per kernel family of the reference's operator layer.  Every
+ * entry point:
+ *   - takes a hipStream_t as `void* stream` (NULL = the default stream);
+ *   - takes device pointers only (row-major, contiguous; NCHW planes; complex spectra as
+ *     interleaved float pairs (re, im) in (fft_h, fft_w/2+1) row-major layout);
+ *   - never allocates, never synchronises the host, and never copies host<->device, so a
+ *     caller may capture it in a HIP graph; scratch comes in through (ws, ws_bytes), sized
+ *     by the matching *_workspace_size() query;
+ *   - returns NC_OK (0) or a negative NC_ERR_* status (or a positive hipError_t when a
+ *     launch fails); it never throws across the ABI;
+ *   - is deterministic: every reduction (over pixels, directions M, batch B or FFT bins)
+ *     runs in a fixed order, with no atomics.
+ *
+ * Citations name the reference operator (path:line in shakes76/neurocell-v2) whose forward or
+ * custom-VJP rule the entry point replaces.
+ */
+#ifndef NEUROCELL_HIP_H_
+#define NEUROCELL_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NC_ABI_VERSION 1
+
+/* Status codes. */
+#define NC_OK 0
+#define NC_ERR_INVALID_ARGUMENT (-1)
+#define NC_ERR_UNSUPPORTED (-2)
+#define NC_ERR_WORKSPACE (-3)
+
+/* Activation ids: kernels_pallas.py:76-99 (_resolve_activation_spec). */
+#define NC_ACT_IDENTITY 0
+#define NC_ACT_TANH 1
+#define NC_ACT_SIGMOID 2
+#define NC_ACT_RELU 3
+#define NC_ACT_LEAKY_RELU 4
+#define NC_ACT_GELU 5
+
+/* Codd modes: params.py:23-28 (SUPPORTED_CODD_MODES, same order). */
+#define NC_CODD_CONTINUOUS 0
+#define NC_CODD_ANNEALED 1
+#define NC_CODD_STE_BINARY 2
+#define NC_CODD_STE_TERNARY 3
+
+/*
+ * Static chip geometry for the pre-step fusion (topology.py:109-284 ChipTopology2D plus the
+ * adaptive crop of adaptive_mask.py:164-197).  The active sub-ROI is [r0, r1) x [c0, c1) in
+ * ROI coordinates; (0, roi_h, 0, roi_w) when uncropped.
+ */
+typedef struct nc_chip_desc {
+    int32_t H, W;          /* grid */
+    int32_t kh, kw;        /* Green's-filter size (odd) */
+    int32_t M;             /* directions */
+    int32_t pad_h, pad_w;  /* ROI offset in the grid (VALID: (kh-1)/2, (kw-1)/2) */
+    int32_t roi_h, roi_w;  /* full ROI */
+    int32_t r0, r1, c0, c1;/* active sub-ROI */
+} nc_chip_desc;
+
+int nc_version(void);
+const char* nc_strerror(int status);
+
+/* ---------------- piece 1: pre-step Codd fusion ---------------------------------------- */
+
+/*
+ * compute_codd_state_probs + precompute_step_params forward (params.py:31-80, 220-322) and
+ * the border template of propagator.py:355-361.
+ * In : cell (3,H,W) = [W, B, S_raw]; io_mask, out_weight_mask (H,W) u8; port_rc (2,P) int32
+ *      ROI (uncropped) row then column indices of the P output-port cells.
+ * Out: w_eff, s_eff, b_roi (h,w) for the active sub-ROI (h = r1-r0, w = c1-c0);
+ *      border_patch (h+kh-1, w+kw-1) = act(B)*s_prob with the ROI zeroed, cut at grid
+ *      offset (r0, c0); port_params (3,P) = [w_eff_out, s_eff_out, b_out]; optional (NULL
+ *      to skip) full-grid s_prob, border_2d = act(B)*s_prob and w_pinned, each (H,W).
+ * inv_tau is 1/max(tau, 1e-4) rounded to float32 (params.py:63).
+ */
+int nc_codd_fuse_fwd(void* stream, const nc_chip_desc* chip, const float* cell,
+                     const uint8_t* io_mask, const uint8_t* out_weight_mask, int codd_mode,
+                     float inv_tau, float active_threshold, int hard_pin_io, int act,
+                     float neg_slope, int n_port, const int32_t* port_rc, float* w_eff,
+                     float* s_eff, float* b_roi, float* border_patch, float* port_params,
+                     float* s_prob, float* border_2d, float* w_pinned);
+
+/*
+ * Reverse of nc_codd_fuse_fwd (the autodiff of params.py:220-322 and of the STE forms of
+ * params.py:58-80).  Any gradient input may be NULL (zero).  Writes g_cell (3,H,W).
+ */
+int nc_codd_fuse_bwd(void* stream, const nc_chip_desc* chip, const float* cell,
+                     const uint8_t* io_mask, const uint8_t* out_weight_mask, int codd_mode,
+                     float inv_tau, float active_threshold, int hard_pin_io, int act,
+                     float neg_slope, int n_port, const int32_t* port_rc, const float* g_w_eff,
+                     const float* g_s_eff, const float* g_b_roi, const float* g_border_patch,
+                     const float* g_port_params, float* g_cell);
+
+/* ---------------- piece 2: Green's-function convolution (spectral) -------------------- */
+
+/*
+ * precompute_filter_rfft2 / hoist_filter_rfft2(_nopad) forward (kernels_greens.py:240-259,
+ * kernels_pallas.py:1582-1604): ghat (M, fft_h, fft_w/2+1) complex = rfft2 of the flipped
+ * filters (M,1,kh,kw).
+ */
+int nc_filter_spectrum_fwd(void* stream, int M, int kh, int kw, int fft_h, int fft_w,
+                           const float* filters, float* ghat);
+
+/*
+ * rfft2_unshifted_filter_grad_to_oihw (kernels_pallas.py:1558-1579), the backward of
+ * hoist_filter_rfft2_nopad: irfft2(dghat) rolled by (shift_h, shift_w), cropped to
+ * (kh,kw) and flipped.  g_filters (M,1,kh,kw) is overwritten, or added to when accumulate.
+ * dghat follows the reference's (JAX) complex-cotangent convention, dL/dRe - i dL/dIm;
+ * conj_in != 0 takes it in the conjugate (PyTorch autograd) convention instead.
+ */
+int nc_filter_spectrum_bwd(void* stream, int M, int kh, int kw, int fft_h, int fft_w,
+                           int shift_h, int shift_w, const float* dghat, float* g_filters,
+                           int accumulate, int conj_in);
+
+/*
+ * Overlap-save spectral cross-correlation forward: conv2d_pruned_rfft_roi_step /
+ * conv2d_roi_rfft_step forward (kernels_pallas.py:1759-1791, kernels_greens.py:316-360) and,
+ * with pad = (kh-1, kw-1), conv2d_valid_rfft_precomputed (kernels_greens.py:403-425) and the
+ * hoisted border conv (propagator.py:362-366).
+ * x (B, hin, win) real, placed at the spectral origin; z (B, M, hout, wout) =
+ * irfft2(rfft2(x) * ghat)[pad_h : pad_h+hout, pad_w : pad_w+wout].  xhat (B, fft_h,
+ * fft_w/2+1) complex (the saved cell_freq residual) is written when non-NULL.
+ * Supported spectral grids: fft_h, fft_w in {16, 32, 64}.
+ */
+int nc_fftconv_fwd(void* stream, int B, int M, int hin, int win, int hout, int wout, int pad_h,
+                   int pad_w, int fft_h, int fft_w, const float* x, const float* ghat, float* z,
+                   float* xhat);
+
+/* Workspace bytes needed by nc_fftconv_bwd for these shapes. */
+size_t nc_fftconv_bwd_workspace_size(int B, int M, int fft_h, int fft_w);
+
+/*
+ * Unshifted Plancherel backward of the spectral correlation (kernels_pallas.py:1794-1821):
+ * ghat_g = rfft2(gz) at the origin;
+ *   dx = irfft2(sum_m ghat_g * conj(ghat)) rolled by (pad_h, pad_w), cropped (hin, win)
+ *        (written only when need_dx; dx may be NULL otherwise);
+ *   dghat = sum_b ghat_g * conj(xhat)   (M, fft_h, fft_w/2+1) complex, overwritten or added
+ *        to when accumulate - the B-reduction runs in the frequency domain, in fixed order;
+ *        conj_dghat != 0 writes its conjugate (the PyTorch autograd convention).
+ */
+int nc_fftconv_bwd(void* stream, int B, int M, int hin, int win, int hout, int wout, int pad_h,
+                   int pad_w, int fft_h, int fft_w, const float* gz, const float* xhat,
+                   const float* ghat, int need_dx, float* dx, float* dghat, int accumulate,
+                   int conj_dghat, void* ws, size_t ws_bytes);
+
+/* ---------------- piece 3: hidden-step epilogue and output-port epilogue --------------- */
+
+/* Workspace bytes for nc_epilogue_fwd / nc_epilogue_bwd at these shapes. */
+size_t nc_epilogue_workspace_size(int B, int M, int h, int w);
+
+/*
+ * pallas_fused_roi_step_epilogue forward (kernels_pallas.py:663-866):
+ *   zhat = standardize(z + (has_border ? delta : 0)) per (b, m) plane (two-pass population
+ *   variance, eps 1e-5); out = w_eff * sum_m zhat + s_eff * sum_m act(zhat + b_roi).
+ * z (B,M,h,w), delta (M,h,w), w_eff/s_eff/b_roi (h,w) -> out (B,h,w), mean/rstd (B,M).
+ * N = h*w <= 8192 runs a single pass per sample; larger planes run the tiled (B,M,tiles)
+ * Chan parallel-variance pipeline.
+ */
+int nc_epilogue_fwd(void* stream, int B, int M, int h, int w, int act, float neg_slope,
+                    int has_border, const float* z, const float* delta, const float* w_eff,
+                    const float* s_eff, const float* b_roi, float* out, float* mean, float* rstd,
+                    void* ws, size_t ws_bytes);
+
+/*
+ * pallas_fused_roi_step_epilogue backward rule (kernels_pallas.py:869-1064): writes gz
+ * (B,M,h,w), gdb = sum_b gz (M,h,w) when has_border (gdb may be NULL otherwise) and
+ * gw/gs/gb (h,w).  gw/gs/gb are overwritten, or added to when accumulate_params; gdb is
+ * overwritten, or added to when accumulate_gdb (a d-step reverse pass sums both over steps).
+ */
+int nc_epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg_slope,
+                    int has_border, const float* z, const float* delta, const float* w_eff,
+                    const float* s_eff, const float* b_roi, const float* mean, const float* rstd,
+                    const float* gy, float* gz, float* gdb, float* gw, float* gs, float* gb,
+                    int accumulate_params, int accumulate_gdb, void* ws, size_t ws_bytes);
+
+/*
+ * pallas_standardize_output_port + pallas_fused_output_port_epilogue forward
+ * (kernels_pallas.py:1256-1347, 1510-1551): per-plane (mean, rstd) over the whole (h,w)
+ * plane, standardisation of the P port cells only (port_idx (P) int32 flat indices into the
+ * (h,w) plane, in port order), then the port Codd algebra.  port_params (3,P) =
+ * [w_eff_out, s_eff_out, b_out].  Writes out (B,P), zo (B,M,P), mean/rstd (B,M) and, when
+ * final_act != identity, pre (B,P) (the pre-activation residual).  Planes above 8192 pixels use
+ * the tiled Chan statistics and need ws (nc_epilogue_workspace_size bytes).
+ */
+int nc_port_fwd(void* stream, int B, int M, int h, int w, int has_border, int final_act,
+                float neg_slope, int n_port, const int32_t* port_idx, const float* z,
+                const float* delta, const float* port_params, float* out, float* zo,
+                float* mean, float* rstd, float* pre, void* ws, size_t ws_bytes);
+
+/*
+ * Backward of nc_port_fwd (kernels_pallas.py:1350-1504, 1538-1551): dense
+ * gz = -rstd*(c1 + zhat*c2) plus rstd*g scattered at the port cells in registers; gdb =
+ * sum_b gz when has_border; gdb and g_port_params (3,P) overwritten, or added to when
+ * accumulate_params.
+ */
+int nc_port_bwd(void* stream, int B, int M, int h, int w, int has_border, int final_act,
+                float neg_slope, int n_port, const int32_t* port_idx, const float* z,
+                const float* delta, const float* port_params, const float* zo,
+                const float* mean, const float* rstd, const float* pre, const float* g_out,
+                float* gz, float* gdb, float* g_port_params, int accumulate_params, void* ws,
+                size_t ws_bytes);
+
+/* ---------------- piece 4: adaptive active-region bucketing ---------------------------- */
+
+/*
+ * _compute_adaptive_mask_tensors (adaptive_mask.py:200-315) over the full ROI: writes
+ * stats[8] = {r_eff_h, r_eff_w, salient_count, any_active, r0, r1, c0, c1} and the dilated
+ * active mask (roi_h, roi_w) u8.  act_roi (roi_h, roi_w) may be NULL.  The bucket
+ * quantisation (adaptive_mask.py:105-161) is host integer logic on these 8 values.
+ */
+int nc_adaptive_stats(void* stream, const nc_chip_desc* chip, const float* cell,
+                      const float* filters, const uint8_t* io_mask_roi, const float* act_roi,
+                      int margin_h, int margin_w, float salience_threshold, float bias_threshold,
+                      float filter_threshold, float activity_threshold, int32_t* stats,
+                      uint8_t* dilated);
+
+/* ---------------- orchestration helpers ------------------------------------------------- */
+
+/*
+ * inject_inputs_roi_2d (propagator.py:135-191) as a gather: roi[b, i] = inputs[b, src[i]]
+ * when src[i] >= 0, else 0, for the n_roi cells of the (cropped) ROI.  The host builds src
+ * from the port geometry once (later ports win on overlap, as the reference's sequential
+ * .at[].set does).
+ */
+int nc_inject_roi(void* stream, int B, int n_in, const float* inputs, int n_roi,
+                  const int32_t* src, float* roi);
+
+/* default_mse_loss (trainer.py:57-61): loss[0] = mean((pred-target)^2); g_pred = 2(pred-target)/n. */
+int nc_mse_loss(void* stream, int n, const float* pred, const float* target, float* loss,
+                float* g_pred);
+
+/*
+ * optax.adamw update with its default arguments as used by VNNTrainer (trainer.py:101-106):
+ * count[0] += 1; m,v moments; bias correction by count; p -= lr[0] * (mhat/(sqrt(vhat)+eps)
+ * + weight_decay * p).  count and lr live in device memory so a captured graph replays it.
+ */
+int nc_adamw_step(void* stream, int n, float* p, const float* g, float* m, float* v,
+                  int32_t* count, const float* lr, float b1, float b2, float eps,
+                  float weight_decay);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NEUROCELL_HIP_H_ */

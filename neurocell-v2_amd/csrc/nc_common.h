@@ -1,0 +1,122 @@
+// Shared device helpers for the gfx950 VNN kernels: activations, complex arithmetic,
+// deterministic wave64 / workgroup reductions, launch-status plumbing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/neurocell_hip.h"
+
+#define NC_DEV __device__ __forceinline__
+#define NC_WAVE 64
+
+// Status of a launch sequence: the first failing HIP call's code, else NC_OK.
+#define NC_CHECK_LAUNCH()                                  \
+    do {                                                   \
+        hipError_t _e = hipGetLastError();                 \
+        if (_e != hipSuccess) return (int)_e;              \
+    } while (0)
+
+static inline hipStream_t nc_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---------------------------------------------------------------------------------------
+// Activations (kernels_pallas.py:111-156).  `act` is one of NC_ACT_*.
+// ---------------------------------------------------------------------------------------
+
+NC_DEV float nc_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+NC_DEV float nc_act(float x, int act, float neg_slope) {
+    switch (act) {
+        case NC_ACT_TANH: return tanhf(x);
+        case NC_ACT_SIGMOID: return nc_sigmoid(x);
+        case NC_ACT_RELU: return fmaxf(x, 0.0f);
+        case NC_ACT_LEAKY_RELU: return x >= 0.0f ? x : neg_slope * x;
+        case NC_ACT_GELU: {
+            const float c = 0.7978845608028654f;  // sqrt(2/pi)
+            return 0.5f * x * (1.0f + tanhf(c * (x + 0.044715f * x * x * x)));
+        }
+        default: return x;
+    }
+}
+
+// Value and derivative together.
+NC_DEV float nc_act_d(float x, int act, float neg_slope, float* y) {
+    switch (act) {
+        case NC_ACT_TANH: {
+            float t = tanhf(x);
+            *y = t;
+            return 1.0f - t * t;
+        }
+        case NC_ACT_SIGMOID: {
+            float s = nc_sigmoid(x);
+            *y = s;
+            return s * (1.0f - s);
+        }
+        case NC_ACT_RELU:
+            *y = fmaxf(x, 0.0f);
+            return x > 0.0f ? 1.0f : 0.0f;
+        case NC_ACT_LEAKY_RELU:
+            *y = x >= 0.0f ? x : neg_slope * x;
+            return x >= 0.0f ? 1.0f : neg_slope;
+        case NC_ACT_GELU: {
+            const float c = 0.7978845608028654f;
+            float x2 = x * x;
+            float th = tanhf(c * (x + 0.044715f * x2 * x));
+            float du = c * (1.0f + 3.0f * 0.044715f * x2);
+            *y = 0.5f * x * (1.0f + th);
+            return 0.5f * (1.0f + th) + 0.5f * x * (1.0f - th * th) * du;
+        }
+        default:
+            *y = x;
+            return 1.0f;
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// Complex helpers (float2 = re, im)
+// ---------------------------------------------------------------------------------------
+
+typedef float2 cpx;
+NC_DEV cpx cmk(float r, float i) { return make_float2(r, i); }
+NC_DEV cpx cadd(cpx a, cpx b) { return make_float2(a.x + b.x, a.y + b.y); }
+NC_DEV cpx csub(cpx a, cpx b) { return make_float2(a.x - b.x, a.y - b.y); }
+NC_DEV cpx cmul(cpx a, cpx b) { return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x); }
+// a * conj(b)
+NC_DEV cpx cmulc(cpx a, cpx b) { return make_float2(a.x * b.x + a.y * b.y, a.y * b.x - a.x * b.y); }
+NC_DEV cpx cconj(cpx a) { return make_float2(a.x, -a.y); }
+NC_DEV cpx cscale(cpx a, float s) { return make_float2(a.x * s, a.y * s); }
+NC_DEV cpx cmul_i(cpx a) { return make_float2(-a.y, a.x); }      // i * a
+NC_DEV cpx cmul_negi(cpx a) { return make_float2(a.y, -a.x); }   // -i * a
+
+// ---------------------------------------------------------------------------------------
+// Deterministic reductions.  A wave64 butterfly (xor shuffles) followed by a fixed-order
+// sum over the waves of the workgroup through LDS.  Every lane returns the same value.
+// ---------------------------------------------------------------------------------------
+
+NC_DEV float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, NC_WAVE);
+    return v;
+}
+
+// Sums K values per thread across the workgroup; `red` must hold K * (blockDim.x / 64) floats.
+// On return vals[k] holds the workgroup total for every thread.  Contains two barriers.
+template <int K>
+NC_DEV void block_sum(float* vals, float* red) {
+    const int lane = threadIdx.x & (NC_WAVE - 1);
+    const int wave = threadIdx.x >> 6;
+    const int nwave = (blockDim.x + NC_WAVE - 1) >> 6;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        float s = wave_sum(vals[k]);
+        if (lane == 0) red[k * nwave + wave] = s;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        float s = 0.0f;
+        for (int w = 0; w < nwave; ++w) s += red[k * nwave + w];
+        vals[k] = s;
+    }
+    __syncthreads();
+}

@@ -1,0 +1,868 @@
+// Piece 3: pure-ROI fused hidden-step epilogue and the output-port epilogue.
+//
+// Single pass (N = h*w <= 8192), one workgroup per sample b (kernels_pallas.py:163-291):
+//   every thread owns PPT pixels of the plane for a chunk of MC directions in registers;
+//   the MC plane sums (then the MC centred sums of squares) are reduced across the
+//   workgroup at once (wave64 butterflies + a fixed-order cross-wave sum), so the two-pass
+//   variance costs two block reductions per chunk, and z is read from HBM exactly once.
+// Tiled (N > 8192), the (B, M, tiles) Chan parallel-variance pipeline
+// (kernels_pallas.py:298-660): per-tile (s1, m2) -> exact Chan combine (recomputed by each
+// consumer in fixed order) -> per-(b, tile) standardise + Codd + M-reduction.
+// Output port (kernels_pallas.py:1076-1551): plane statistics, standardisation of the P
+// port cells only, and a backward whose sparse port scatter is applied in registers through
+// an LDS pixel->slot map, one workgroup per (b, tile).
+// B-reductions (gw/gs/gb, gdb, port parameters) are fixed-order column sums: no atomics.
+#include <algorithm>
+
+#include "nc_common.h"
+
+namespace {
+
+constexpr int kSingleMaxPix = 8192;  // kernels_pallas.py:56
+constexpr int kTileN = 1024;         // kernels_pallas.py:58
+constexpr int kPortTile = 2048;
+constexpr int kMaxM = 64;
+
+// ----------------------------------------------------------------------------------------
+// Single-pass forward: one workgroup per sample.
+// ----------------------------------------------------------------------------------------
+
+template <int NT, int PPT, int MC>
+__global__ __launch_bounds__(NT) void k_epi_fwd(int M, int N, int act, float slope, int hb,
+                                                const float* __restrict__ z,
+                                                const float* __restrict__ delta,
+                                                const float* __restrict__ w,
+                                                const float* __restrict__ s,
+                                                const float* __restrict__ bb,
+                                                float* __restrict__ out, float* __restrict__ mean,
+                                                float* __restrict__ rstd) {
+    __shared__ float red[MC * (NT / 64)];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    const float inv_n = 1.0f / (float)N;
+    float lin[PPT], ac[PPT], bv[PPT];
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+        const int p = tid + k * NT;
+        lin[k] = 0.f;
+        ac[k] = 0.f;
+        bv[k] = p < N ? bb[p] : 0.f;
+    }
+    for (int m0 = 0; m0 < M; m0 += MC) {
+        float zt[MC][PPT];
+        float sum[MC];
+#pragma unroll
+        for (int q = 0; q < MC; ++q) {
+            const int m = m0 + q;
+            sum[q] = 0.f;
+#pragma unroll
+            for (int k = 0; k < PPT; ++k) {
+                const int p = tid + k * NT;
+                float v = 0.f;
+                if (m < M && p < N) {
+                    v = z[((size_t)b * M + m) * N + p];
+                    if (hb) v += delta[(size_t)m * N + p];
+                }
+                zt[q][k] = v;
+                sum[q] += v;
+            }
+        }
+        block_sum<MC>(sum, red);
+        float mu[MC], sq[MC];
+#pragma unroll
+        for (int q = 0; q < MC; ++q) {
+            mu[q] = sum[q] * inv_n;
+            sq[q] = 0.f;
+#pragma unroll
+            for (int k = 0; k < PPT; ++k) {
+                const int p = tid + k * NT;
+                const float d = p < N ? zt[q][k] - mu[q] : 0.f;
+                sq[q] += d * d;
+            }
+        }
+        block_sum<MC>(sq, red);
+#pragma unroll
+        for (int q = 0; q < MC; ++q) {
+            const int m = m0 + q;
+            if (m >= M) break;
+            const float r = 1.0f / sqrtf(sq[q] * inv_n + 1e-5f);
+#pragma unroll
+            for (int k = 0; k < PPT; ++k) {
+                const float zn = (zt[q][k] - mu[q]) * r;
+                lin[k] += zn;
+                ac[k] += nc_act(zn + bv[k], act, slope);
+            }
+            if (tid == 0) {
+                mean[(size_t)b * M + m] = mu[q];
+                rstd[(size_t)b * M + m] = r;
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+        const int p = tid + k * NT;
+        if (p < N) out[(size_t)b * N + p] = w[p] * lin[k] + s[p] * ac[k];
+    }
+}
+
+// ----------------------------------------------------------------------------------------
+// Single-pass backward: gz, per-sample partial gw/gs/gb (reduced over B afterwards).
+// ----------------------------------------------------------------------------------------
+
+template <int NT, int PPT, int MC>
+__global__ __launch_bounds__(NT) void k_epi_bwd(
+    int M, int N, int act, float slope, int hb, const float* __restrict__ z,
+    const float* __restrict__ delta, const float* __restrict__ w, const float* __restrict__ s,
+    const float* __restrict__ bb, const float* __restrict__ mean, const float* __restrict__ rstd,
+    const float* __restrict__ gy, float* __restrict__ gz, float* __restrict__ pg) {
+    __shared__ float red[2 * MC * (NT / 64)];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    const float inv_n = 1.0f / (float)N;
+    float lin[PPT], ac[PPT], dbs[PPT], bv[PPT], wv[PPT], sv[PPT], g[PPT];
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+        const int p = tid + k * NT;
+        const bool in = p < N;
+        lin[k] = ac[k] = dbs[k] = 0.f;
+        bv[k] = in ? bb[p] : 0.f;
+        wv[k] = in ? w[p] : 0.f;
+        sv[k] = in ? s[p] : 0.f;
+        g[k] = in ? gy[(size_t)b * N + p] : 0.f;
+    }
+    for (int m0 = 0; m0 < M; m0 += MC) {
+        float zn[MC][PPT], gzn[MC][PPT];
+        float c[2 * MC];
+        float mr[MC], rr[MC];
+#pragma unroll
+        for (int q = 0; q < MC; ++q) {
+            const int m = m0 + q;
+            const bool mv = m < M;
+            mr[q] = mv ? mean[(size_t)b * M + m] : 0.f;
+            rr[q] = mv ? rstd[(size_t)b * M + m] : 0.f;
+            c[q] = c[MC + q] = 0.f;
+#pragma unroll
+            for (int k = 0; k < PPT; ++k) {
+                const int p = tid + k * NT;
+                float v = 0.f, gn = 0.f, nz = 0.f;
+                if (mv && p < N) {
+                    v = z[((size_t)b * M + m) * N + p];
+                    if (hb) v += delta[(size_t)m * N + p];
+                    nz = (v - mr[q]) * rr[q];
+                    float a;
+                    const float da = nc_act_d(nz + bv[k], act, slope, &a);
+                    gn = g[k] * (wv[k] + sv[k] * da);
+                    lin[k] += nz;
+                    ac[k] += a;
+                    dbs[k] += sv[k] * g[k] * da;
+                }
+                zn[q][k] = nz;
+                gzn[q][k] = gn;
+                c[q] += gn;
+                c[MC + q] += gn * nz;
+            }
+        }
+        block_sum<2 * MC>(c, red);
+#pragma unroll
+        for (int q = 0; q < MC; ++q) {
+            const int m = m0 + q;
+            if (m >= M) break;
+            const float c1 = c[q] * inv_n, c2 = c[MC + q] * inv_n;
+#pragma unroll
+            for (int k = 0; k < PPT; ++k) {
+                const int p = tid + k * NT;
+                if (p < N)
+                    gz[((size_t)b * M + m) * N + p] = rr[q] * (gzn[q][k] - c1 - zn[q][k] * c2);
+            }
+        }
+    }
+    const size_t BN = (size_t)gridDim.x * N;
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+        const int p = tid + k * NT;
+        if (p < N) {
+            pg[(size_t)b * N + p] = g[k] * lin[k];
+            pg[BN + (size_t)b * N + p] = g[k] * ac[k];
+            pg[2 * BN + (size_t)b * N + p] = dbs[k];
+        }
+    }
+}
+
+// out[r*X + x] = (acc ? out : 0) + sum_b in[(r*B + b)*X + x]  (fixed order over b)
+__global__ void k_batch_reduce(int R, int B, int X, const float* __restrict__ in,
+                               float* __restrict__ out, int accumulate) {
+    const int x = blockIdx.x * blockDim.x + threadIdx.x;
+    const int r = blockIdx.y;
+    if (x >= X) return;
+    const float* src = in + (size_t)r * B * X + x;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    int b = 0;
+    for (; b + 4 <= B; b += 4) {
+        a0 += src[(size_t)b * X];
+        a1 += src[(size_t)(b + 1) * X];
+        a2 += src[(size_t)(b + 2) * X];
+        a3 += src[(size_t)(b + 3) * X];
+    }
+    for (; b < B; ++b) a0 += src[(size_t)b * X];
+    const float t = (a0 + a1) + (a2 + a3);
+    float* o = out + (size_t)r * X + x;
+    *o = accumulate ? *o + t : t;
+}
+
+// ----------------------------------------------------------------------------------------
+// Tiled (Chan) pipeline for N > 8192.
+// ----------------------------------------------------------------------------------------
+
+constexpr int kTileNT = 256;
+constexpr int kTilePPT = kTileN / kTileNT;
+
+// Per-(b, m, tile) sum and centred sum of squares; stats layout (2, B, M, T).
+__global__ __launch_bounds__(kTileNT) void k_tile_stats(int M, int N, int T, int hb,
+                                                        const float* __restrict__ z,
+                                                        const float* __restrict__ delta,
+                                                        float* __restrict__ stats) {
+    __shared__ float red[kTileNT / 64];
+    const int t = blockIdx.x, m = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+    const int base = t * kTileN;
+    const int nt = min(kTileN, N - base);
+    float v[kTilePPT];
+    float s1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < kTilePPT; ++k) {
+        const int i = tid + k * kTileNT;
+        float x = 0.f;
+        if (i < nt) {
+            x = z[((size_t)b * M + m) * N + base + i];
+            if (hb) x += delta[(size_t)m * N + base + i];
+        }
+        v[k] = x;
+        s1 += x;
+    }
+    block_sum<1>(&s1, red);
+    const float mu = s1 / (float)nt;
+    float m2 = 0.f;
+#pragma unroll
+    for (int k = 0; k < kTilePPT; ++k) {
+        const int i = tid + k * kTileNT;
+        const float d = i < nt ? v[k] - mu : 0.f;
+        m2 += d * d;
+    }
+    block_sum<1>(&m2, red);
+    if (tid == 0) {
+        const size_t BMT = (size_t)gridDim.z * M * T;
+        const size_t o = ((size_t)b * M + m) * T + t;
+        stats[o] = s1;
+        stats[BMT + o] = m2;
+    }
+}
+
+// Chan combine of the T tile statistics of plane (b, m), fixed order.
+NC_DEV void chan_combine(const float* stats, size_t BMT, int b, int m, int M, int N, int T,
+                         float* mean, float* rstd) {
+    const float* s1 = stats + ((size_t)b * M + m) * T;
+    const float* m2 = s1 + BMT;
+    float tot = 0.f;
+    for (int t = 0; t < T; ++t) tot += s1[t];
+    const float mu = tot / (float)N;
+    float var = 0.f;
+    for (int t = 0; t < T; ++t) {
+        const int nt = min(kTileN, N - t * kTileN);
+        const float d = s1[t] / (float)nt - mu;
+        var += m2[t] + (float)nt * d * d;
+    }
+    *mean = mu;
+    *rstd = 1.0f / sqrtf(var / (float)N + 1e-5f);
+}
+
+// Per-(tile, b): statistics from the Chan partials, then standardise + Codd + sum over M.
+__global__ __launch_bounds__(kTileNT) void k_tile_fwd(int B, int M, int N, int T, int act,
+                                                      float slope, int hb,
+                                                      const float* __restrict__ z,
+                                                      const float* __restrict__ delta,
+                                                      const float* __restrict__ w,
+                                                      const float* __restrict__ s,
+                                                      const float* __restrict__ bb,
+                                                      const float* __restrict__ stats,
+                                                      float* __restrict__ out,
+                                                      float* __restrict__ mean,
+                                                      float* __restrict__ rstd) {
+    __shared__ float smu[kMaxM], srs[kMaxM];
+    const int t = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    const size_t BMT = (size_t)B * M * T;
+    for (int m = tid; m < M; m += kTileNT) {
+        float mu, r;
+        chan_combine(stats, BMT, b, m, M, N, T, &mu, &r);
+        smu[m] = mu;
+        srs[m] = r;
+        if (t == 0) {
+            mean[(size_t)b * M + m] = mu;
+            rstd[(size_t)b * M + m] = r;
+        }
+    }
+    __syncthreads();
+    const int base = t * kTileN;
+    const int nt = min(kTileN, N - base);
+#pragma unroll
+    for (int k = 0; k < kTilePPT; ++k) {
+        const int i = tid + k * kTileNT;
+        if (i >= nt) continue;
+        const int p = base + i;
+        const float bvv = bb[p];
+        float lin = 0.f, ac = 0.f;
+        for (int m = 0; m < M; ++m) {
+            float v = z[((size_t)b * M + m) * N + p];
+            if (hb) v += delta[(size_t)m * N + p];
+            const float zn = (v - smu[m]) * srs[m];
+            lin += zn;
+            ac += nc_act(zn + bvv, act, slope);
+        }
+        out[(size_t)b * N + p] = w[p] * lin + s[p] * ac;
+    }
+}
+
+// Backward stage 1 per (tile, b): per-tile partial c1/c2 (layout (2, B, M, T)) and the
+// per-sample gw/gs/gb partials pg (3, B, N).
+__global__ __launch_bounds__(kTileNT) void k_tile_bwd1(
+    int B, int M, int N, int T, int act, float slope, int hb, const float* __restrict__ z,
+    const float* __restrict__ delta, const float* __restrict__ w, const float* __restrict__ s,
+    const float* __restrict__ bb, const float* __restrict__ mean, const float* __restrict__ rstd,
+    const float* __restrict__ gy, float* __restrict__ cpart, float* __restrict__ pg) {
+    __shared__ float red[2 * (kTileNT / 64)];
+    const int t = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    const int base = t * kTileN;
+    const int nt = min(kTileN, N - base);
+    float lin[kTilePPT], ac[kTilePPT], dbs[kTilePPT], g[kTilePPT], wv[kTilePPT], sv[kTilePPT],
+        bv[kTilePPT];
+#pragma unroll
+    for (int k = 0; k < kTilePPT; ++k) {
+        const int i = tid + k * kTileNT;
+        const bool in = i < nt;
+        const int p = base + i;
+        lin[k] = ac[k] = dbs[k] = 0.f;
+        g[k] = in ? gy[(size_t)b * N + p] : 0.f;
+        wv[k] = in ? w[p] : 0.f;
+        sv[k] = in ? s[p] : 0.f;
+        bv[k] = in ? bb[p] : 0.f;
+    }
+    const size_t BMT = (size_t)B * M * T;
+    for (int m = 0; m < M; ++m) {
+        const float mu = mean[(size_t)b * M + m], r = rstd[(size_t)b * M + m];
+        float c[2] = {0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < kTilePPT; ++k) {
+            const int i = tid + k * kTileNT;
+            if (i >= nt) continue;
+            const int p = base + i;
+            float v = z[((size_t)b * M + m) * N + p];
+            if (hb) v += delta[(size_t)m * N + p];
+            const float zn = (v - mu) * r;
+            float a;
+            const float da = nc_act_d(zn + bv[k], act, slope, &a);
+            const float gn = g[k] * (wv[k] + sv[k] * da);
+            lin[k] += zn;
+            ac[k] += a;
+            dbs[k] += sv[k] * g[k] * da;
+            c[0] += gn;
+            c[1] += gn * zn;
+        }
+        block_sum<2>(c, red);
+        if (tid == 0) {
+            const size_t o = ((size_t)b * M + m) * T + t;
+            cpart[o] = c[0];
+            cpart[BMT + o] = c[1];
+        }
+    }
+    const size_t BN = (size_t)B * N;
+#pragma unroll
+    for (int k = 0; k < kTilePPT; ++k) {
+        const int i = tid + k * kTileNT;
+        if (i >= nt) continue;
+        const int p = base + i;
+        pg[(size_t)b * N + p] = g[k] * lin[k];
+        pg[BN + (size_t)b * N + p] = g[k] * ac[k];
+        pg[2 * BN + (size_t)b * N + p] = dbs[k];
+    }
+}
+
+// Backward stage 2 per (tile, m, b): gz = rstd * (gzn - c1 - zn * c2).
+__global__ __launch_bounds__(kTileNT) void k_tile_bwd2(
+    int B, int M, int N, int T, int act, float slope, int hb, const float* __restrict__ z,
+    const float* __restrict__ delta, const float* __restrict__ w, const float* __restrict__ s,
+    const float* __restrict__ bb, const float* __restrict__ mean, const float* __restrict__ rstd,
+    const float* __restrict__ gy, const float* __restrict__ cpart, float* __restrict__ gz) {
+    const int t = blockIdx.x, m = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+    const size_t BMT = (size_t)B * M * T;
+    const float* c1p = cpart + ((size_t)b * M + m) * T;
+    const float* c2p = c1p + BMT;
+    float c1 = 0.f, c2 = 0.f;
+    for (int u = 0; u < T; ++u) {
+        c1 += c1p[u];
+        c2 += c2p[u];
+    }
+    c1 /= (float)N;
+    c2 /= (float)N;
+    const float mu = mean[(size_t)b * M + m], r = rstd[(size_t)b * M + m];
+    const int base = t * kTileN;
+    const int nt = min(kTileN, N - base);
+#pragma unroll
+    for (int k = 0; k < kTilePPT; ++k) {
+        const int i = tid + k * kTileNT;
+        if (i >= nt) continue;
+        const int p = base + i;
+        float v = z[((size_t)b * M + m) * N + p];
+        if (hb) v += delta[(size_t)m * N + p];
+        const float zn = (v - mu) * r;
+        float a;
+        const float da = nc_act_d(zn + bb[p], act, slope, &a);
+        const float gn = gy[(size_t)b * N + p] * (w[p] + s[p] * da);
+        gz[((size_t)b * M + m) * N + p] = r * (gn - c1 - zn * c2);
+    }
+}
+
+// ----------------------------------------------------------------------------------------
+// Output port.
+// ----------------------------------------------------------------------------------------
+
+// Single-pass plane statistics for all M of sample b into LDS (N <= 8192).
+template <int NT, int PPT, int MC>
+NC_DEV void plane_stats(int b, int M, int N, int hb, const float* __restrict__ z,
+                        const float* __restrict__ delta, float* smu, float* srs, float* red) {
+    const int tid = threadIdx.x;
+    const float inv_n = 1.0f / (float)N;
+    for (int m0 = 0; m0 < M; m0 += MC) {
+        float zt[MC][PPT], sum[MC], sq[MC];
+#pragma unroll
+        for (int q = 0; q < MC; ++q) {
+            const int m = m0 + q;
+            sum[q] = 0.f;
+#pragma unroll
+            for (int k = 0; k < PPT; ++k) {
+                const int p = tid + k * NT;
+                float v = 0.f;
+                if (m < M && p < N) {
+                    v = z[((size_t)b * M + m) * N + p];
+                    if (hb) v += delta[(size_t)m * N + p];
+                }
+                zt[q][k] = v;
+                sum[q] += v;
+            }
+        }
+        block_sum<MC>(sum, red);
+#pragma unroll
+        for (int q = 0; q < MC; ++q) {
+            sq[q] = 0.f;
+            const float mu = sum[q] * inv_n;
+#pragma unroll
+            for (int k = 0; k < PPT; ++k) {
+                const int p = tid + k * NT;
+                const float d = p < N ? zt[q][k] - mu : 0.f;
+                sq[q] += d * d;
+            }
+        }
+        block_sum<MC>(sq, red);
+        if (tid == 0) {
+#pragma unroll
+            for (int q = 0; q < MC; ++q)
+                if (m0 + q < M) {
+                    smu[m0 + q] = sum[q] * inv_n;
+                    srs[m0 + q] = 1.0f / sqrtf(sq[q] * inv_n + 1e-5f);
+                }
+        }
+    }
+    __syncthreads();
+}
+
+// Gather + port algebra for sample b once smu/srs are known.
+NC_DEV void port_gather(int b, int M, int N, int P, int hb, int fact, float slope,
+                        const int* __restrict__ pidx, const float* __restrict__ z,
+                        const float* __restrict__ delta, const float* __restrict__ pp,
+                        const float* smu, const float* srs, float* szo,
+                        float* __restrict__ out, float* __restrict__ zo,
+                        float* __restrict__ pre) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    for (int q = tid; q < M * P; q += nt) {
+        const int m = q / P, k = q % P;
+        const int e = pidx[k];
+        float v = z[((size_t)b * M + m) * N + e];
+        if (hb) v += delta[(size_t)m * N + e];
+        const float zn = (v - smu[m]) * srs[m];
+        szo[q] = zn;
+        zo[(size_t)b * M * P + q] = zn;
+    }
+    __syncthreads();
+    for (int k = tid; k < P; k += nt) {
+        const float wo = pp[k], so = pp[P + k], bo = pp[2 * P + k];
+        float lin = 0.f, ac = 0.f;
+        for (int m = 0; m < M; ++m) {
+            const float v = szo[m * P + k];
+            lin += v;
+            if (fact != NC_ACT_IDENTITY) ac += nc_act(v + bo, fact, slope);
+        }
+        float o;
+        if (fact == NC_ACT_IDENTITY) {
+            o = (wo + so) * lin + (float)M * so * bo;
+        } else {
+            const float y = wo * lin + so * ac;
+            pre[(size_t)b * P + k] = y;
+            o = nc_act(y, fact, slope);
+        }
+        out[(size_t)b * P + k] = o;
+    }
+}
+
+template <int NT, int PPT, int MC>
+__global__ __launch_bounds__(NT) void k_port_fwd(int M, int N, int P, int hb, int fact,
+                                                 float slope, const int* __restrict__ pidx,
+                                                 const float* __restrict__ z,
+                                                 const float* __restrict__ delta,
+                                                 const float* __restrict__ pp,
+                                                 float* __restrict__ out, float* __restrict__ zo,
+                                                 float* __restrict__ mean,
+                                                 float* __restrict__ rstd,
+                                                 float* __restrict__ pre) {
+    HIP_DYNAMIC_SHARED(float, szo)  // M*P
+    __shared__ float smu[kMaxM], srs[kMaxM];
+    __shared__ float red[MC * (NT / 64)];
+    const int b = blockIdx.x;
+    plane_stats<NT, PPT, MC>(b, M, N, hb, z, delta, smu, srs, red);
+    for (int m = threadIdx.x; m < M; m += NT) {
+        mean[(size_t)b * M + m] = smu[m];
+        rstd[(size_t)b * M + m] = srs[m];
+    }
+    port_gather(b, M, N, P, hb, fact, slope, pidx, z, delta, pp, smu, srs, szo, out, zo, pre);
+}
+
+// Large planes: Chan partials (k_tile_stats) -> per-sample combine + gather.
+__global__ __launch_bounds__(256) void k_port_fwd_tiled(
+    int B, int M, int N, int T, int P, int hb, int fact, float slope,
+    const int* __restrict__ pidx, const float* __restrict__ z, const float* __restrict__ delta,
+    const float* __restrict__ pp, const float* __restrict__ stats, float* __restrict__ out,
+    float* __restrict__ zo, float* __restrict__ mean, float* __restrict__ rstd,
+    float* __restrict__ pre) {
+    HIP_DYNAMIC_SHARED(float, szo)
+    __shared__ float smu[kMaxM], srs[kMaxM];
+    const int b = blockIdx.x;
+    const size_t BMT = (size_t)B * M * T;
+    for (int m = threadIdx.x; m < M; m += blockDim.x) {
+        float mu, r;
+        chan_combine(stats, BMT, b, m, M, N, T, &mu, &r);
+        smu[m] = mu;
+        srs[m] = r;
+        mean[(size_t)b * M + m] = mu;
+        rstd[(size_t)b * M + m] = r;
+    }
+    __syncthreads();
+    port_gather(b, M, N, P, hb, fact, slope, pidx, z, delta, pp, smu, srs, szo, out, zo, pre);
+}
+
+// Port backward per (tile, b): port cotangents, (c1, c2), dense gz with the sparse port term
+// added in registers via an LDS pixel->slot map; per-sample port-parameter partials
+// ppart (3, B, P) written by tile 0.
+__global__ __launch_bounds__(256) void k_port_bwd(
+    int M, int N, int P, int hb, int fact, float slope, const int* __restrict__ pidx,
+    const float* __restrict__ z, const float* __restrict__ delta, const float* __restrict__ pp,
+    const float* __restrict__ zo, const float* __restrict__ mean, const float* __restrict__ rstd,
+    const float* __restrict__ pre, const float* __restrict__ gout, float* __restrict__ gz,
+    float* __restrict__ ppart) {
+    HIP_DYNAMIC_SHARED(float, dyn)
+    float* gzo = dyn;                          // M*P: port cotangent per (m, k)
+    float* gsum = dyn + M * P;                 // M*P: summed per first-occurrence slot
+    int* slot = reinterpret_cast<int*>(dyn + 2 * M * P);  // kPortTile
+    __shared__ float c1s[kMaxM], c2s[kMaxM], smu[kMaxM], srs[kMaxM];
+    __shared__ int first[256];
+    const int t = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, nt = blockDim.x;
+    const int B = gridDim.y;
+    const float* zob = zo + (size_t)b * M * P;
+    // 1. port cotangents
+    for (int q = tid; q < M * P; q += nt) {
+        const int m = q / P, k = q % P;
+        const float wo = pp[k], so = pp[P + k], bo = pp[2 * P + k];
+        const float go = gout[(size_t)b * P + k];
+        float v;
+        if (fact == NC_ACT_IDENTITY) {
+            v = go * (wo + so);
+        } else {
+            float a;
+            const float gp = go * nc_act_d(pre[(size_t)b * P + k], fact, slope, &a);
+            v = gp * (wo + so * nc_act_d(zob[q] + bo, fact, slope, &a));
+        }
+        gzo[q] = v;
+        gsum[q] = 0.f;
+    }
+    for (int m = tid; m < M; m += nt) {
+        smu[m] = mean[(size_t)b * M + m];
+        srs[m] = rstd[(size_t)b * M + m];
+    }
+    const int base = t * kPortTile;
+    const int ntile = min(kPortTile, N - base);
+    for (int i = tid; i < ntile; i += nt) slot[i] = -1;
+    __syncthreads();
+    // 2. first-occurrence slots of the port cells inside this tile (sequential: duplicates
+    //    of a coordinate port add up, as the reference's .at[].add does)
+    if (tid == 0) {
+        for (int k = 0; k < P; ++k) {
+            const int e = pidx[k] - base;
+            int f = -1;
+            if (e >= 0 && e < ntile) {
+                if (slot[e] < 0) slot[e] = k;
+                f = slot[e];
+            }
+            first[k] = f;
+        }
+    }
+    __syncthreads();
+    for (int m = tid; m < M; m += nt) {
+        float a1 = 0.f, a2 = 0.f;
+        for (int k = 0; k < P; ++k) {
+            const float g = gzo[m * P + k];
+            a1 += g;
+            a2 += g * zob[m * P + k];
+            if (first[k] >= 0) gsum[m * P + first[k]] += g;
+        }
+        c1s[m] = a1 / (float)N;
+        c2s[m] = a2 / (float)N;
+    }
+    __syncthreads();
+    // 3. dense gz for this tile
+    for (int m = 0; m < M; ++m) {
+        const float mu = smu[m], r = srs[m], c1 = c1s[m], c2 = c2s[m];
+        for (int i = tid; i < ntile; i += nt) {
+            const int p = base + i;
+            float v = z[((size_t)b * M + m) * N + p];
+            if (hb) v += delta[(size_t)m * N + p];
+            const float zn = (v - mu) * r;
+            float gv = -r * (c1 + zn * c2);
+            const int sl = slot[i];
+            if (sl >= 0) gv += r * gsum[m * P + sl];
+            gz[((size_t)b * M + m) * N + p] = gv;
+        }
+    }
+    // 4. per-sample port-parameter partials
+    if (t == 0) {
+        for (int k = tid; k < P; k += nt) {
+            const float wo = pp[k], so = pp[P + k], bo = pp[2 * P + k];
+            const float go = gout[(size_t)b * P + k];
+            float lin = 0.f, ac = 0.f, gbv = 0.f;
+            float gp = go;
+            if (fact != NC_ACT_IDENTITY) {
+                float a;
+                gp = go * nc_act_d(pre[(size_t)b * P + k], fact, slope, &a);
+            }
+            for (int m = 0; m < M; ++m) {
+                const float v = zob[m * P + k];
+                lin += v;
+                if (fact != NC_ACT_IDENTITY) {
+                    float a;
+                    const float da = nc_act_d(v + bo, fact, slope, &a);
+                    ac += a;
+                    gbv += gp * so * da;
+                }
+            }
+            float gw, gs, gb;
+            if (fact == NC_ACT_IDENTITY) {
+                gw = gp * lin;
+                gs = gp * (lin + (float)M * bo);
+                gb = gp * (float)M * so;
+            } else {
+                gw = gp * lin;
+                gs = gp * ac;
+                gb = gbv;
+            }
+            ppart[(size_t)b * P + k] = gw;
+            ppart[((size_t)B + b) * P + k] = gs;
+            ppart[((size_t)2 * B + b) * P + k] = gb;
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------------------
+// Launch configuration
+// ----------------------------------------------------------------------------------------
+
+struct SingleCfg {
+    int nt, ppt;
+};
+
+SingleCfg single_cfg(int N) {
+    if (N <= 256) return {256, 1};
+    if (N <= 512) return {256, 2};
+    if (N <= 768) return {256, 3};
+    if (N <= 1024) return {256, 4};
+    if (N <= 2048) return {512, 4};
+    if (N <= 4096) return {1024, 4};
+    return {1024, 8};
+}
+
+int tiles_of(int N) { return (N + kTileN - 1) / kTileN; }
+
+// Forward-style kernels keep MC=16 directions of PPT pixels in registers; the backward keeps
+// two such tiles (zhat and its cotangent), so it runs MC=8.
+#define NC_SINGLE_DISPATCH(N_, MCF, KER, ...)                                               \
+    do {                                                                                    \
+        SingleCfg c_ = single_cfg(N_);                                                      \
+        if (c_.nt == 256 && c_.ppt == 1) hipLaunchKernelGGL((KER<256, 1, MCF>), __VA_ARGS__); \
+        else if (c_.nt == 256 && c_.ppt == 2) hipLaunchKernelGGL((KER<256, 2, MCF>), __VA_ARGS__); \
+        else if (c_.nt == 256 && c_.ppt == 3) hipLaunchKernelGGL((KER<256, 3, MCF>), __VA_ARGS__); \
+        else if (c_.nt == 256 && c_.ppt == 4) hipLaunchKernelGGL((KER<256, 4, MCF>), __VA_ARGS__); \
+        else if (c_.nt == 512) hipLaunchKernelGGL((KER<512, 4, MCF>), __VA_ARGS__);          \
+        else if (c_.ppt == 4) hipLaunchKernelGGL((KER<1024, 4, MCF>), __VA_ARGS__);          \
+        else hipLaunchKernelGGL((KER<1024, 8, 8>), __VA_ARGS__);                           \
+    } while (0)
+
+}  // namespace
+
+extern "C" {
+
+size_t nc_epilogue_workspace_size(int B, int M, int h, int w) {
+    if (B <= 0 || M <= 0 || h <= 0 || w <= 0) return 0;
+    const size_t N = (size_t)h * w;
+    const size_t T = tiles_of((int)N);
+    size_t pg = 3 * (size_t)B * N;
+    size_t st = 4 * (size_t)B * M * T;
+    size_t pport = 3 * (size_t)B * 256;
+    return (pg + st + pport) * sizeof(float);
+}
+
+int nc_epilogue_fwd(void* stream, int B, int M, int h, int w, int act, float neg_slope,
+                    int has_border, const float* z, const float* delta, const float* w_eff,
+                    const float* s_eff, const float* b_roi, float* out, float* mean, float* rstd,
+                    void* ws, size_t ws_bytes) {
+    if (B <= 0 || M <= 0 || M > kMaxM || h <= 0 || w <= 0 || !z || !w_eff || !s_eff ||
+        !b_roi || !out || !mean || !rstd || (has_border && !delta) || act < 0 || act > 5)
+        return NC_ERR_INVALID_ARGUMENT;
+    hipStream_t st = nc_stream(stream);
+    const int N = h * w;
+    if (N <= kSingleMaxPix) {
+        NC_SINGLE_DISPATCH(N, 16, k_epi_fwd, dim3(B), dim3(c_.nt), 0, st, M, N, act, neg_slope,
+                           has_border, z, delta, w_eff, s_eff, b_roi, out, mean, rstd);
+        NC_CHECK_LAUNCH();
+        return NC_OK;
+    }
+    if (ws_bytes < nc_epilogue_workspace_size(B, M, h, w) || !ws) return NC_ERR_WORKSPACE;
+    const int T = tiles_of(N);
+    float* stats = reinterpret_cast<float*>(ws) + 3 * (size_t)B * N;
+    hipLaunchKernelGGL(k_tile_stats, dim3(T, M, B), dim3(kTileNT), 0, st, M, N, T, has_border,
+                       z, delta, stats);
+    NC_CHECK_LAUNCH();
+    hipLaunchKernelGGL(k_tile_fwd, dim3(T, B), dim3(kTileNT), 0, st, B, M, N, T, act,
+                       neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, stats, out, mean,
+                       rstd);
+    NC_CHECK_LAUNCH();
+    return NC_OK;
+}
+
+int nc_epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg_slope,
+                    int has_border, const float* z, const float* delta, const float* w_eff,
+                    const float* s_eff, const float* b_roi, const float* mean, const float* rstd,
+                    const float* gy, float* gz, float* gdb, float* gw, float* gs, float* gb,
+                    int accumulate_params, int accumulate_gdb, void* ws, size_t ws_bytes) {
+    if (B <= 0 || M <= 0 || M > kMaxM || h <= 0 || w <= 0 || !z || !w_eff || !s_eff ||
+        !b_roi || !mean || !rstd || !gy || !gz || !gw || !gs || !gb ||
+        (has_border && (!delta || !gdb)) || act < 0 || act > 5)
+        return NC_ERR_INVALID_ARGUMENT;
+    if (ws_bytes < nc_epilogue_workspace_size(B, M, h, w) || !ws) return NC_ERR_WORKSPACE;
+    hipStream_t st = nc_stream(stream);
+    const int N = h * w;
+    float* pg = reinterpret_cast<float*>(ws);
+    if (N <= kSingleMaxPix) {
+        NC_SINGLE_DISPATCH(N, 8, k_epi_bwd, dim3(B), dim3(c_.nt), 0, st, M, N, act, neg_slope,
+                           has_border, z, delta, w_eff, s_eff, b_roi, mean, rstd, gy, gz, pg);
+        NC_CHECK_LAUNCH();
+    } else {
+        const int T = tiles_of(N);
+        float* cpart = pg + 3 * (size_t)B * N;
+        hipLaunchKernelGGL(k_tile_bwd1, dim3(T, B), dim3(kTileNT), 0, st, B, M, N, T, act,
+                           neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, mean, rstd, gy,
+                           cpart, pg);
+        NC_CHECK_LAUNCH();
+        hipLaunchKernelGGL(k_tile_bwd2, dim3(T, M, B), dim3(kTileNT), 0, st, B, M, N, T, act,
+                           neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, mean, rstd, gy,
+                           cpart, gz);
+        NC_CHECK_LAUNCH();
+    }
+    // parameter gradients: sum over B of the per-sample partials (gw, gs, gb are 3 rows)
+    float* dst[3] = {gw, gs, gb};
+    for (int r = 0; r < 3; ++r) {
+        hipLaunchKernelGGL(k_batch_reduce, dim3((N + 255) / 256, 1), dim3(256), 0, st, 1, B, N,
+                           pg + (size_t)r * B * N, dst[r], accumulate_params);
+        NC_CHECK_LAUNCH();
+    }
+    if (has_border) {
+        hipLaunchKernelGGL(k_batch_reduce, dim3((M * N + 255) / 256, 1), dim3(256), 0, st, 1, B,
+                           M * N, gz, gdb, accumulate_gdb);
+        NC_CHECK_LAUNCH();
+    }
+    return NC_OK;
+}
+
+static int port_check(int B, int M, int h, int w, int P, const int32_t* port_idx,
+                      const float* z, int hb, const float* delta, int fact) {
+    if (B <= 0 || M <= 0 || M > kMaxM || h <= 0 || w <= 0 || P <= 0 || P > 256 ||
+        M * P > 8192 || !port_idx || !z || (hb && !delta) || fact < 0 || fact > 5)
+        return NC_ERR_INVALID_ARGUMENT;
+    return NC_OK;
+}
+
+int nc_port_fwd(void* stream, int B, int M, int h, int w, int has_border, int final_act,
+                float neg_slope, int n_port, const int32_t* port_idx, const float* z,
+                const float* delta, const float* port_params, float* out, float* zo,
+                float* mean, float* rstd, float* pre, void* ws, size_t ws_bytes) {
+    int rc = port_check(B, M, h, w, n_port, port_idx, z, has_border, delta, final_act);
+    if (rc != NC_OK) return rc;
+    if (!port_params || !out || !zo || !mean || !rstd ||
+        (final_act != NC_ACT_IDENTITY && !pre))
+        return NC_ERR_INVALID_ARGUMENT;
+    hipStream_t st = nc_stream(stream);
+    const int N = h * w;
+    const size_t shm = (size_t)M * n_port * sizeof(float);
+    if (N <= kSingleMaxPix) {
+        NC_SINGLE_DISPATCH(N, 16, k_port_fwd, dim3(B), dim3(c_.nt), shm, st, M, N, n_port,
+                           has_border, final_act, neg_slope, port_idx, z, delta, port_params,
+                           out, zo, mean, rstd, pre);
+        NC_CHECK_LAUNCH();
+        return NC_OK;
+    }
+    if (ws_bytes < nc_epilogue_workspace_size(B, M, h, w) || !ws) return NC_ERR_WORKSPACE;
+    const int T = tiles_of(N);
+    float* stats = reinterpret_cast<float*>(ws) + 3 * (size_t)B * N;
+    hipLaunchKernelGGL(k_tile_stats, dim3(T, M, B), dim3(kTileNT), 0, st, M, N, T, has_border,
+                       z, delta, stats);
+    NC_CHECK_LAUNCH();
+    hipLaunchKernelGGL(k_port_fwd_tiled, dim3(B), dim3(256), shm, st, B, M, N, T, n_port,
+                       has_border, final_act, neg_slope, port_idx, z, delta, port_params,
+                       stats, out, zo, mean, rstd, pre);
+    NC_CHECK_LAUNCH();
+    return NC_OK;
+}
+
+int nc_port_bwd(void* stream, int B, int M, int h, int w, int has_border, int final_act,
+                float neg_slope, int n_port, const int32_t* port_idx, const float* z,
+                const float* delta, const float* port_params, const float* zo,
+                const float* mean, const float* rstd, const float* pre, const float* g_out,
+                float* gz, float* gdb, float* g_port_params, int accumulate_params, void* ws,
+                size_t ws_bytes) {
+    int rc = port_check(B, M, h, w, n_port, port_idx, z, has_border, delta, final_act);
+    if (rc != NC_OK) return rc;
+    if (!port_params || !zo || !mean || !rstd || !g_out || !gz || !g_port_params ||
+        (has_border && !gdb) || (final_act != NC_ACT_IDENTITY && !pre))
+        return NC_ERR_INVALID_ARGUMENT;
+    if (ws_bytes < nc_epilogue_workspace_size(B, M, h, w) || !ws) return NC_ERR_WORKSPACE;
+    hipStream_t st = nc_stream(stream);
+    const int N = h * w;
+    const int T = (N + kPortTile - 1) / kPortTile;
+    float* ppart = reinterpret_cast<float*>(ws);
+    const size_t shm = (size_t)2 * M * n_port * sizeof(float) + (size_t)kPortTile * sizeof(int);
+    hipLaunchKernelGGL(k_port_bwd, dim3(T, B), dim3(256), shm, st, M, N, n_port, has_border,
+                       final_act, neg_slope, port_idx, z, delta, port_params, zo, mean, rstd,
+                       pre, g_out, gz, ppart);
+    NC_CHECK_LAUNCH();
+    hipLaunchKernelGGL(k_batch_reduce, dim3((n_port + 255) / 256, 3), dim3(256), 0, st, 3, B,
+                       n_port, ppart, g_port_params, accumulate_params);
+    NC_CHECK_LAUNCH();
+    if (has_border) {
+        hipLaunchKernelGGL(k_batch_reduce, dim3((M * N + 255) / 256, 1), dim3(256), 0, st, 1, B,
+                           M * N, gz, gdb, accumulate_params);
+        NC_CHECK_LAUNCH();
+    }
+    return NC_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,75 @@
+"""ctypes declarations of the C ABI in ``include/neurocell_hip.h``.
+
+``declare(lib)`` attaches argtypes/restypes to a loaded ``ctypes.CDLL`` so every call is
+type-checked at the boundary.  ``ENTRY_POINTS`` lists every exported symbol the header
+declares; the loader checks all of them on load.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+P = C.c_void_p
+I = C.c_int
+F = C.c_float
+SZ = C.c_size_t
+
+NC_OK = 0
+NC_ERR_INVALID_ARGUMENT = -1
+NC_ERR_UNSUPPORTED = -2
+NC_ERR_WORKSPACE = -3
+
+ACT_IDS = {"identity": 0, "tanh": 1, "sigmoid": 2, "relu": 3, "leaky_relu": 4, "gelu": 5}
+CODD_IDS = {"continuous": 0, "annealed": 1, "ste_binary": 2, "ste_ternary": 3}
+
+
+class ChipDesc(C.Structure):
+    """Mirror of ``nc_chip_desc``."""
+    _fields_ = [(n, C.c_int32) for n in (
+        "H", "W", "kh", "kw", "M", "pad_h", "pad_w", "roi_h", "roi_w", "r0", "r1", "c0", "c1")]
+
+
+_SIGS = {
+    "nc_version": (I, []),
+    "nc_strerror": (C.c_char_p, [I]),
+    "nc_codd_fuse_fwd": (I, [P, C.POINTER(ChipDesc), P, P, P, I, F, F, I, I, F, I, P, P, P, P,
+                             P, P, P, P, P]),
+    "nc_codd_fuse_bwd": (I, [P, C.POINTER(ChipDesc), P, P, P, I, F, F, I, I, F, I, P, P, P, P,
+                             P, P, P]),
+    "nc_filter_spectrum_fwd": (I, [P, I, I, I, I, I, P, P]),
+    "nc_filter_spectrum_bwd": (I, [P, I, I, I, I, I, I, I, P, P, I, I]),
+    "nc_fftconv_fwd": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, P]),
+    "nc_fftconv_bwd_workspace_size": (SZ, [I, I, I, I]),
+    "nc_fftconv_bwd": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, I, P, P, I, I, P, SZ]),
+    "nc_epilogue_workspace_size": (SZ, [I, I, I, I]),
+    "nc_epilogue_fwd": (I, [P, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, SZ]),
+    "nc_epilogue_bwd": (I, [P, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, P, P, P, P, I,
+                            I, P, SZ]),
+    "nc_port_fwd": (I, [P, I, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, P, SZ]),
+    "nc_port_bwd": (I, [P, I, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, P, P, P, I, P,
+                        SZ]),
+    "nc_adaptive_stats": (I, [P, C.POINTER(ChipDesc), P, P, P, P, I, I, F, F, F, F, P, P]),
+    "nc_inject_roi": (I, [P, I, I, P, I, P, P]),
+    "nc_mse_loss": (I, [P, I, P, P, P, P]),
+    "nc_adamw_step": (I, [P, I, P, P, P, P, P, P, F, F, F, F]),
+}
+
+ENTRY_POINTS = tuple(_SIGS)
+
+
+class NeurocellError(RuntimeError):
+    """A C-ABI call returned a non-zero status."""
+
+
+def declare(lib: C.CDLL) -> C.CDLL:
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+def check(lib: C.CDLL, status: int, what: str) -> None:
+    if status != NC_OK:
+        msg = lib.nc_strerror(status)
+        raise NeurocellError(f"{what} failed with status {status}: "
+                             f"{msg.decode() if msg else '?'}")

@@ -1,0 +1,374 @@
+"""Step executor: the VNN propagation step (propagator.py:209-682) and its reverse pass as a
+fixed sequence of C-ABI launches over persistent device buffers.
+
+A ``StepPlan`` is built once per (topology, batch size, active sub-ROI, activations) bucket --
+the analogue of the reference's per-bbox jit cache (trainer.py:164-248).  It owns every
+intermediate in HBM (laid out NCHW, fp32; spectra complex64 as (fft_h, fft_w/2+1)), so a
+forward, a backward or a whole train step allocates nothing and issues no memset: callers may
+capture it in a HIP graph (``torch.cuda.CUDAGraph``) and replay it.
+
+Forward (pure ROI + hoisted border theorem, propagator.py:1-9, 343-682):
+    codd fusion -> filter spectrum -> border conv (B=1, VALID) -> inject ->
+    d-1 x [spectral conv -> hidden epilogue] -> spectral conv -> port epilogue
+Reverse: port bwd -> d x [spectral conv bwd (dx, dG in the frequency domain)
+    -> hidden epilogue bwd] -> filter-spectrum bwd -> border conv bwd -> codd fusion bwd.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+from . import _abi
+from ._lib import NeurocellError, call, ptr, stream_ptr, require_device
+from .topology import ChipTopology2D, CoordinatePortSpec
+
+_SUPPORTED_FFT = (16, 32, 64)
+
+
+def _npow2(x: int) -> int:
+    return 1 << (int(x) - 1).bit_length()
+
+
+def act_id(activate) -> tuple[int, float]:
+    """Maps an activation (name, None, or a callable with a matching ``__name__``) to the
+    kernel id and leaky slope, as kernels_pallas.py:76-99 resolves it."""
+    if activate is None:
+        return _abi.ACT_IDS["identity"], 1.0
+    if isinstance(activate, str):
+        name = activate
+    else:
+        name = getattr(activate, "__name__", "")
+        kw = getattr(activate, "keywords", None)
+        if name == "" and getattr(activate, "func", None) is not None:
+            name = getattr(activate.func, "__name__", "")
+        if name == "leaky_relu" and kw:
+            return _abi.ACT_IDS["leaky_relu"], float(kw.get("negative_slope", 0.01))
+    if name not in _abi.ACT_IDS:
+        raise ValueError(f"Unsupported activation function: {activate}")
+    return _abi.ACT_IDS[name], (0.01 if name == "leaky_relu" else 0.0)
+
+
+def port_input_shapes(inputs, topology: ChipTopology2D) -> list:
+    """Per-port (ih, iw) as written into the grid (propagator.py:88-100, 124-130: a 3-D
+    per-port input is written with its own shape)."""
+    if isinstance(inputs, (list, tuple)):
+        arrs = list(inputs)
+        shapes = []
+        for a, p in zip(arrs, topology.in_ports):
+            if isinstance(p, CoordinatePortSpec):
+                shapes.append((p.num_points, 1))
+            elif a.ndim == 3:
+                shapes.append((int(a.shape[1]), int(a.shape[2])))
+            else:
+                shapes.append(tuple(p.size))
+        return shapes
+    if len(topology.in_ports) == 1:
+        p = topology.in_ports[0]
+        if inputs.ndim == 2 or (inputs.ndim == 3 and tuple(inputs.shape[1:]) == tuple(p.size)):
+            if isinstance(p, CoordinatePortSpec):
+                return [(p.num_points, 1)]
+            return [tuple(inputs.shape[1:]) if inputs.ndim == 3 else tuple(p.size)]
+    shapes = []
+    for i, p in enumerate(topology.in_ports):
+        if isinstance(p, CoordinatePortSpec):
+            shapes.append((p.num_points, 1))
+        else:
+            sub = inputs[:, i]
+            shapes.append((int(sub.shape[1]), int(sub.shape[2])) if sub.ndim == 3
+                          else tuple(p.size))
+    return shapes
+
+
+def flatten_inputs(inputs, topology: ChipTopology2D) -> torch.Tensor:
+    """Concatenates the per-port inputs into one (B, n_in) fp32 device tensor."""
+    if isinstance(inputs, (list, tuple)):
+        parts = [a.reshape(a.shape[0], -1) for a in inputs]
+    elif len(topology.in_ports) == 1 and (inputs.ndim == 2 or (
+            inputs.ndim == 3 and tuple(inputs.shape[1:]) == tuple(topology.in_ports[0].size))):
+        parts = [inputs.reshape(inputs.shape[0], -1)]
+    else:
+        parts = [inputs[:, i].reshape(inputs.shape[0], -1)
+                 for i in range(len(topology.in_ports))]
+    x = torch.cat(parts, dim=1) if len(parts) > 1 else parts[0]
+    if x.dtype != torch.float32:
+        raise NeurocellError(f"inputs must be float32, got {x.dtype}")
+    if not x.is_cuda:
+        raise NeurocellError("inputs must already be resident on the device")
+    return x.contiguous()
+
+
+class StepPlan:
+    """Launch plan and persistent buffers for one (topology, B, sub-ROI) bucket."""
+
+    def __init__(self, topology: ChipTopology2D, batch_size: int, port_shapes: list,
+                 roi_bbox=None, activate="tanh", final_activate=None, hard_pin_io=False,
+                 training=True, device=None):
+        if topology.padding_mode != "VALID":
+            raise NeurocellError("the MI355X path implements the VALID pure-ROI propagation; "
+                                 f"padding_mode={topology.padding_mode} is not supported")
+        if not topology.out_in_roi:
+            raise NeurocellError("output port outside the active ROI is not supported")
+        self.device = device or require_device()
+        self.topo = topology
+        self.B = int(batch_size)
+        self.training = bool(training)
+        self.hard_pin_io = bool(hard_pin_io)
+        self.act, self.slope = act_id(activate)
+        self.fact, self.fslope = act_id(final_activate)
+        H, W = topology.grid_shape
+        kh, kw = topology.kernel_size
+        M, d = topology.directions, topology.depth
+        roi_h, roi_w = topology.roi_shape
+        r0, r1, c0, c1 = roi_bbox if roi_bbox is not None else (0, roi_h, 0, roi_w)
+        self.bbox = (int(r0), int(r1), int(c0), int(c1))
+        self.cropped = roi_bbox is not None and self.bbox != (0, roi_h, 0, roi_w)
+        h, w = r1 - r0, c1 - c0
+        self.H, self.W, self.kh, self.kw, self.M, self.d = H, W, kh, kw, M, d
+        self.h, self.w, self.N = h, w, h * w
+        if self.cropped:
+            self.fft = (_npow2(h + kh - 1), _npow2(w + kw - 1))  # adaptive_mask.py:177-180
+        else:
+            self.fft = tuple(topology.fft_shape)
+        fh, fw = self.fft
+        if fh not in _SUPPORTED_FFT or fw not in _SUPPORTED_FFT:
+            raise NeurocellError(f"spectral grid {self.fft} is not supported yet "
+                                 f"(supported sizes {_SUPPORTED_FFT})")
+        if h + kh - 1 > fh or w + kw - 1 > fw:
+            raise NeurocellError("linear correlation does not fit the spectral grid")
+        self.F = fh * (fw // 2 + 1)
+        self.cp = ((kh - 1) // 2, (kw - 1) // 2)
+        self.Hp, self.Wp = h + kh - 1, w + kw - 1
+        self.chip = _abi.ChipDesc(H, W, kh, kw, M, topology.pad_h, topology.pad_w, roi_h, roi_w,
+                                  r0, r1, c0, c1)
+        # output port cells
+        rows, cols = topology.out_cells_roi()
+        if ((rows < r0) | (rows >= r1) | (cols < c0) | (cols >= c1)).any():
+            raise NeurocellError("output port lies outside the active sub-ROI")
+        self.P = int(rows.size)
+        self.out_size = tuple(topology.out_port.size)
+        dev = self.device
+        self.port_rc = torch.tensor(np.stack([rows, cols]).astype(np.int32), device=dev)
+        self.port_idx = torch.tensor(((rows - r0) * w + (cols - c0)).astype(np.int32),
+                                     device=dev)
+        self.io_mask = torch.tensor(topology.io_state_mask.astype(np.uint8), device=dev)
+        self.owm = torch.tensor(topology.out_weight_mask.astype(np.uint8), device=dev)
+        # input injection map (gather form)
+        self.port_shapes = [tuple(int(v) for v in s) for s in port_shapes]
+        src, self.t0_grid = self._inject_map()
+        self.n_in = int(sum(a * b for a, b in self.port_shapes))
+        self.src = torch.tensor(src, device=dev)
+        self._alloc()
+
+    # ------------------------------------------------------------------ geometry helpers
+    def _inject_map(self):
+        """propagator.py:135-191: ROI gather map when every port fits the (cropped) ROI, else
+        the full-grid t=0 map (propagator.py:347-352)."""
+        t = self.topo
+        r0, r1, c0, c1 = self.bbox
+        min_r, max_r = t.pad_h + r0, t.pad_h + r1
+        min_c, max_c = t.pad_w + c0, t.pad_w + c1
+        fits = t.in_in_roi
+        if fits:
+            for port, (ih, iw) in zip(t.in_ports, self.port_shapes):
+                if isinstance(port, CoordinatePortSpec):
+                    if not all(min_r <= r < max_r and min_c <= c < max_c for r, c in port.coords):
+                        fits = False
+                else:
+                    pr, pc = port.offset
+                    if pr < min_r or pc < min_c or pr + ih > max_r or pc + iw > max_c:
+                        fits = False
+        if fits:
+            base_r, base_c, hh, ww = min_r, min_c, self.h, self.w
+        else:
+            if self.cropped:
+                raise NeurocellError("inputs outside a cropped sub-ROI are not supported")
+            if self.H > self.fft[0] or self.W > self.fft[1]:
+                raise NeurocellError("full-grid t=0 step does not fit the spectral grid")
+            base_r, base_c, hh, ww = 0, 0, self.H, self.W
+        src = np.full(hh * ww, -1, np.int32)
+        e = 0
+        for port, (ih, iw) in zip(t.in_ports, self.port_shapes):
+            if isinstance(port, CoordinatePortSpec):
+                for k, (r, c) in enumerate(port.coords):
+                    src[(r - base_r) * ww + (c - base_c)] = e + k
+                e += port.num_points
+                continue
+            pr, pc = port.offset
+            for i in range(ih):
+                for j in range(iw):
+                    src[(pr - base_r + i) * ww + (pc - base_c + j)] = e + i * iw + j
+            e += ih * iw
+        return src, not fits
+
+    def _alloc(self):
+        dev, B, M, d, h, w, F = self.device, self.B, self.M, self.d, self.h, self.w, self.F
+        f = dict(device=dev, dtype=torch.float32)
+        c = dict(device=dev, dtype=torch.complex64)
+        self.w_eff = torch.empty(h, w, **f)
+        self.s_eff = torch.empty(h, w, **f)
+        self.b_roi = torch.empty(h, w, **f)
+        self.patch = torch.empty(self.Hp, self.Wp, **f)
+        self.pp = torch.empty(3, self.P, **f)
+        self.ghat = torch.empty(M, F, **c)
+        self.delta = torch.empty(M, h, w, **f)
+        self.patch_hat = torch.empty(1, F, **c)
+        t0_shape = (B, self.H, self.W) if self.t0_grid else (B, h, w)
+        self.x0 = torch.empty(*t0_shape, **f)
+        nz = d if self.training else 1
+        self.xs = [self.x0] + [torch.empty(B, h, w, **f) for _ in range(d - 1)]
+        self.zs = [torch.empty(B, M, h, w, **f) for _ in range(nz)]
+        self.xhat = [torch.empty(B, F, **c) for _ in range(d)] if self.training else None
+        self.mean = [torch.empty(B, M, **f) for _ in range(d)]
+        self.rstd = [torch.empty(B, M, **f) for _ in range(d)]
+        self.out = torch.empty(B, self.P, **f)
+        self.zo = torch.empty(B, M, self.P, **f)
+        self.pre = torch.empty(B, self.P, **f) if self.fact != 0 else None
+        n_ep = _abi_size("nc_epilogue_workspace_size", B, M, h, w)
+        self.ws_epi = torch.empty(max(1, n_ep // 4), **f)
+        if self.training:
+            n_fc = max(_abi_size("nc_fftconv_bwd_workspace_size", B, M, *self.fft),
+                       _abi_size("nc_fftconv_bwd_workspace_size", 1, M, *self.fft))
+            self.ws_fc = torch.empty(max(1, n_fc // 4), **f)
+            self.gz = torch.empty(B, M, h, w, **f)
+            self.gy = [torch.empty(B, h, w, **f) for _ in range(2)]
+            self.gdelta = torch.empty(M, h, w, **f)
+            self.dghat = torch.empty(M, F, **c)
+            self.dghat_v = torch.empty(M, F, **c)
+            self.gw = torch.empty(h, w, **f)
+            self.gs = torch.empty(h, w, **f)
+            self.gb = torch.empty(h, w, **f)
+            self.gpp = torch.empty(3, self.P, **f)
+            self.gpatch = torch.empty(self.Hp, self.Wp, **f)
+            self.g_out = torch.empty(B, self.P, **f)
+            self.loss = torch.empty(1, **f)
+
+    # ------------------------------------------------------------------ forward
+    def forward(self, cell: torch.Tensor, filt: torch.Tensor, x_flat: torch.Tensor,
+                codd_mode: str = "continuous", inv_tau: float = 1.0,
+                active_threshold: float = 0.6) -> torch.Tensor:
+        """Runs the d-step forward for inputs (B, n_in); returns the (B, P) port outputs."""
+        s = stream_ptr()
+        B, M, h, w = self.B, self.M, self.h, self.w
+        fh, fw = self.fft
+        if tuple(x_flat.shape) != (B, self.n_in):
+            raise NeurocellError(f"inputs must be ({B}, {self.n_in}), got {tuple(x_flat.shape)}")
+        mode = _abi.CODD_IDS[codd_mode]
+        call("nc_codd_fuse_fwd", s, self.chip, ptr(cell), ptr(self.io_mask), ptr(self.owm), mode,
+             inv_tau, active_threshold, int(self.hard_pin_io), self.act, self.slope, self.P,
+             ptr(self.port_rc), ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
+             ptr(self.patch), ptr(self.pp), None, None, None)
+        call("nc_filter_spectrum_fwd", s, M, self.kh, self.kw, fh, fw, ptr(filt), ptr(self.ghat))
+        if self.d > 1:  # hoisted B=1 VALID border conv (propagator.py:362-366)
+            call("nc_fftconv_fwd", s, 1, M, self.Hp, self.Wp, h, w, self.kh - 1, self.kw - 1,
+                 fh, fw, ptr(self.patch), ptr(self.ghat), ptr(self.delta), ptr(self.patch_hat))
+        n_cells = self.x0[0].numel()
+        call("nc_inject_roi", s, B, self.n_in, ptr(x_flat), n_cells, ptr(self.src), ptr(self.x0))
+        for t in range(self.d):
+            last = t == self.d - 1
+            z = self.zs[t if self.training else 0]
+            xh = self.xhat[t] if self.training else None
+            if t == 0 and self.t0_grid:
+                r0, _, c0, _ = self.bbox
+                call("nc_fftconv_fwd", s, B, M, self.H, self.W, h, w, self.kh - 1 + r0,
+                     self.kw - 1 + c0, fh, fw, ptr(self.x0), ptr(self.ghat), ptr(z), ptr(xh))
+            else:
+                call("nc_fftconv_fwd", s, B, M, h, w, h, w, self.cp[0], self.cp[1], fh, fw,
+                     ptr(self.xs[t]), ptr(self.ghat), ptr(z), ptr(xh))
+            hb = int(t > 0)
+            if not last:
+                call("nc_epilogue_fwd", s, B, M, h, w, self.act, self.slope, hb, ptr(z),
+                     ptr(self.delta), ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
+                     ptr(self.xs[t + 1]), ptr(self.mean[t]), ptr(self.rstd[t]),
+                     ptr(self.ws_epi), self.ws_epi.numel() * 4)
+            else:
+                call("nc_port_fwd", s, B, M, h, w, hb, self.fact, self.fslope, self.P,
+                     ptr(self.port_idx), ptr(z), ptr(self.delta), ptr(self.pp), ptr(self.out),
+                     ptr(self.zo), ptr(self.mean[t]), ptr(self.rstd[t]), ptr(self.pre),
+                     ptr(self.ws_epi), self.ws_epi.numel() * 4)
+        return self.out
+
+    # ------------------------------------------------------------------ reverse
+    def backward(self, cell: torch.Tensor, filt: torch.Tensor, g_out: torch.Tensor,
+                 g_cell: torch.Tensor, g_filt: torch.Tensor, codd_mode: str = "continuous",
+                 inv_tau: float = 1.0, active_threshold: float = 0.6) -> None:
+        """Reverse pass of the last ``forward``: writes g_cell (3,H,W) and g_filt (M,1,kh,kw)."""
+        if not self.training:
+            raise NeurocellError("plan was built for evaluation only")
+        s = stream_ptr()
+        B, M, h, w, d = self.B, self.M, self.h, self.w, self.d
+        fh, fw = self.fft
+        ws_ep, n_ep = ptr(self.ws_epi), self.ws_epi.numel() * 4
+        ws_fc, n_fc = ptr(self.ws_fc), self.ws_fc.numel() * 4
+        t = d - 1
+        hb = int(d > 1)
+        call("nc_port_bwd", s, B, M, h, w, hb, self.fact, self.fslope, self.P, ptr(self.port_idx),
+             ptr(self.zs[t]), ptr(self.delta), ptr(self.pp), ptr(self.zo), ptr(self.mean[t]),
+             ptr(self.rstd[t]), ptr(self.pre), ptr(g_out), ptr(self.gz),
+             ptr(self.gdelta) if hb else None, ptr(self.gpp), 0, ws_ep, n_ep)
+        first_epi = True
+        valid_acc = 0
+        for t in range(d - 1, -1, -1):
+            gy = self.gy[t % 2]
+            need_dx = int(t > 0)
+            if t == 0 and self.t0_grid:  # VALID full-grid step: its own spectral shift
+                r0, _, c0, _ = self.bbox
+                call("nc_fftconv_bwd", s, B, M, self.H, self.W, h, w, self.kh - 1 + r0,
+                     self.kw - 1 + c0, fh, fw, ptr(self.gz), ptr(self.xhat[0]), ptr(self.ghat),
+                     0, None, ptr(self.dghat_v), 0, 0, ws_fc, n_fc)
+                valid_acc = 1
+            else:
+                call("nc_fftconv_bwd", s, B, M, h, w, h, w, self.cp[0], self.cp[1], fh, fw,
+                     ptr(self.gz), ptr(self.xhat[t]), ptr(self.ghat), need_dx,
+                     ptr(gy) if need_dx else None, ptr(self.dghat), int(t < d - 1), 0, ws_fc,
+                     n_fc)
+            if t == 0:
+                break
+            te = t - 1
+            hbe = int(te > 0)
+            call("nc_epilogue_bwd", s, B, M, h, w, self.act, self.slope, hbe, ptr(self.zs[te]),
+                 ptr(self.delta), ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
+                 ptr(self.mean[te]), ptr(self.rstd[te]), ptr(gy), ptr(self.gz),
+                 ptr(self.gdelta) if hbe else None, ptr(self.gw), ptr(self.gs), ptr(self.gb),
+                 int(not first_epi), 1, ws_ep, n_ep)  # gdelta already holds the port's share
+            first_epi = False
+        only_t0_grid = self.t0_grid and d == 1
+        if not only_t0_grid:
+            call("nc_filter_spectrum_bwd", s, M, self.kh, self.kw, fh, fw, self.cp[0],
+                 self.cp[1], ptr(self.dghat), ptr(g_filt), 0, 0)
+        g_patch = None
+        if d > 1:  # border conv reverse (same VALID shift as the full-grid t=0 step)
+            call("nc_fftconv_bwd", s, 1, M, self.Hp, self.Wp, h, w, self.kh - 1, self.kw - 1, fh,
+                 fw, ptr(self.gdelta), ptr(self.patch_hat), ptr(self.ghat), 1, ptr(self.gpatch),
+                 ptr(self.dghat_v), valid_acc, 0, ws_fc, n_fc)
+            valid_acc = 1
+            g_patch = ptr(self.gpatch)
+        if valid_acc:
+            call("nc_filter_spectrum_bwd", s, M, self.kh, self.kw, fh, fw, self.kh - 1,
+                 self.kw - 1, ptr(self.dghat_v), ptr(g_filt), int(not only_t0_grid), 0)
+        has_epi = d > 1
+        mode = _abi.CODD_IDS[codd_mode]
+        call("nc_codd_fuse_bwd", s, self.chip, ptr(cell), ptr(self.io_mask), ptr(self.owm), mode,
+             inv_tau, active_threshold, int(self.hard_pin_io), self.act, self.slope, self.P,
+             ptr(self.port_rc), ptr(self.gw) if has_epi else None,
+             ptr(self.gs) if has_epi else None, ptr(self.gb) if has_epi else None, g_patch,
+             ptr(self.gpp), ptr(g_cell))
+
+    # ------------------------------------------------------------------ loss
+    def mse(self, target: torch.Tensor) -> torch.Tensor:
+        """default_mse_loss (trainer.py:57-61) on the port outputs: writes loss and g_out."""
+        call("nc_mse_loss", stream_ptr(), self.B * self.P, ptr(self.out), ptr(target),
+             ptr(self.loss), ptr(self.g_out))
+        return self.loss
+
+
+def _abi_size(name: str, *args) -> int:
+    from ._lib import lib
+    return int(getattr(lib(), name)(*args))
+
+
+def inv_tau_f32(state_temperature: float) -> float:
+    """1 / max(tau, 1e-4) evaluated in float32 (params.py:63)."""
+    t = np.float32(max(np.float32(state_temperature), np.float32(1e-4)))
+    return float(np.float32(1.0) / t)

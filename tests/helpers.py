@@ -1,0 +1,32 @@
+"""Shared helpers for the parity tests."""
+import numpy as np
+
+
+def rel_l2(a, b) -> float:
+    a = np.asarray(a, dtype=np.complex128 if np.iscomplexobj(a) else np.float64)
+    b = np.asarray(b, dtype=np.complex128 if np.iscomplexobj(b) else np.float64)
+    return float(np.linalg.norm((a - b).ravel()) / (np.linalg.norm(b.ravel()) + 1e-30))
+
+
+def alu_case(seed, B, out_width=2, depth=4, kernel_size=(23, 13), directions=16):
+    """Benchmark-config-0 style inputs: W~N(0,0.1), B~N(0,0.01), S~N(0,1) on (3,62,62),
+    filters ~N(0, 1/K) (variance 1/K), 8-bit operand bits + 3-bit opcode as {0,1} cells."""
+    from oracle import vnn_oracle as O
+    rng = np.random.default_rng(seed)
+    geom = O.alu_geometry(kernel_size=kernel_size, directions=directions, depth=depth,
+                          out_width=out_width)
+    H, W = geom.grid_shape
+    kh, kw = kernel_size
+    cell = np.stack([rng.normal(0, 0.1, (H, W)), rng.normal(0, 0.01, (H, W)),
+                     rng.normal(0, 1.0, (H, W))]).astype(np.float32)
+    filt = rng.normal(0, 1.0 / np.sqrt(kh * kw), (directions, 1, kh, kw)).astype(np.float32)
+    a = rng.integers(0, 256, size=B, dtype=np.uint8)
+    b = rng.integers(0, 256, size=B, dtype=np.uint8)
+    op = rng.integers(0, 8, size=B, dtype=np.uint8)
+    x = np.zeros((B, 3, 8, 1), np.float32)
+    x[:, 0, :, 0] = np.unpackbits(a[:, None], axis=1)
+    x[:, 1, :, 0] = np.unpackbits(b[:, None], axis=1)
+    x[:, 2, :, 0] = np.unpackbits(op[:, None], axis=1)
+    oh, ow = geom.out_size
+    y = rng.integers(0, 2, size=(B, oh, ow)).astype(np.float32)
+    return geom, cell, filt, x, y

@@ -1,0 +1,359 @@
+"""Entry-point parity cases for the C ABI, run on two backends:
+
+* ``HostBackend``: NumPy host buffers against the CPU-emulated build of the kernel sources
+  (``tests/emu``) - checks the kernels' indexing and arithmetic without a GPU;
+* ``DeviceBackend``: torch device tensors against the gfx950 library on the MI355X.
+
+Every case compares the entry point with the float64 oracle on the same seeded inputs and
+returns {name: rel-L2 error}; the bars are fp32-level (see ``TOL``).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from oracle import vnn_oracle as O
+from helpers import rel_l2
+from neurocell import _abi
+
+TOL = 2e-6  # fp32 arithmetic against the float64 oracle, per entry point
+
+
+class HostBackend:
+    def __init__(self, lib):
+        self.lib = lib
+
+    def put(self, a, dtype=np.float32):
+        return np.ascontiguousarray(np.asarray(a), dtype=dtype)
+
+    def zeros(self, shape, dtype=np.float32):
+        return np.zeros(shape, dtype)
+
+    def ptr(self, t):
+        return None if t is None else t.ctypes.data_as(C.c_void_p)
+
+    def get(self, t):
+        return np.asarray(t)
+
+    def stream(self):
+        return None
+
+    def sync(self):
+        pass
+
+
+class DeviceBackend:
+    def __init__(self, lib):
+        import torch
+        self.lib = lib
+        self.torch = torch
+        self.dev = torch.device("cuda")
+
+    def put(self, a, dtype=np.float32):
+        return self.torch.from_numpy(np.ascontiguousarray(np.asarray(a), dtype=dtype)).to(self.dev)
+
+    def zeros(self, shape, dtype=np.float32):
+        t = {np.float32: self.torch.float32, np.int32: self.torch.int32,
+             np.uint8: self.torch.uint8}[dtype]
+        return self.torch.zeros(shape, dtype=t, device=self.dev)
+
+    def ptr(self, t):
+        return None if t is None else C.c_void_p(t.data_ptr())
+
+    def get(self, t):
+        self.torch.cuda.synchronize()
+        return t.cpu().numpy()
+
+    def stream(self):
+        return C.c_void_p(self.torch.cuda.current_stream().cuda_stream)
+
+    def sync(self):
+        self.torch.cuda.synchronize()
+
+
+def _ok(be, status, what):
+    _abi.check(be.lib, status, what)
+
+
+def _cplx(a):
+    a = np.asarray(a)
+    return a[..., 0] + 1j * a[..., 1]
+
+
+def case_fftconv(be, B=3, M=5, hin=10, win=12, kh=5, kw=3, FH=16, FW=16, seed=0):
+    """Spectral correlation forward/backward and the filter spectrum, SAME-ROI shift."""
+    rng = np.random.default_rng(seed)
+    ph, pw = (kh - 1) // 2, (kw - 1) // 2
+    x = rng.normal(size=(B, hin, win)).astype(np.float32)
+    g = rng.normal(size=(M, 1, kh, kw)).astype(np.float32)
+    gz = rng.normal(size=(B, M, hin, win)).astype(np.float32)
+    L, s = be.lib, be.stream()
+    xd, gd = be.put(x), be.put(g)
+    ghat = be.zeros((M, FH, FW // 2 + 1, 2))
+    _ok(be, L.nc_filter_spectrum_fwd(s, M, kh, kw, FH, FW, be.ptr(gd), be.ptr(ghat)), "spec")
+    z = be.zeros((B, M, hin, win))
+    xhat = be.zeros((B, FH, FW // 2 + 1, 2))
+    _ok(be, L.nc_fftconv_fwd(s, B, M, hin, win, hin, win, ph, pw, FH, FW, be.ptr(xd),
+                             be.ptr(ghat), be.ptr(z), be.ptr(xhat)), "fwd")
+    ws = be.zeros((L.nc_fftconv_bwd_workspace_size(B, M, FH, FW) // 4 + 1,))
+    dx = be.zeros((B, hin, win))
+    dgh = be.zeros((M, FH, FW // 2 + 1, 2))
+    gzd = be.put(gz)
+    _ok(be, L.nc_fftconv_bwd(s, B, M, hin, win, hin, win, ph, pw, FH, FW, be.ptr(gzd),
+                             be.ptr(xhat), be.ptr(ghat), 1, be.ptr(dx), be.ptr(dgh), 0, 0,
+                             be.ptr(ws), ws.nbytes if hasattr(ws, "nbytes") else
+                             ws.numel() * 4), "bwd")
+    gf = be.zeros((M, 1, kh, kw))
+    _ok(be, L.nc_filter_spectrum_bwd(s, M, kh, kw, FH, FW, ph, pw, be.ptr(dgh), be.ptr(gf), 0,
+                                     0), "specbwd")
+    dxr, dgr = O.conv2d_bwd_direct(gz, x, g[:, 0], (ph, pw))
+    return {
+        "ghat": rel_l2(_cplx(be.get(ghat)), O.filter_spectrum(g[:, 0], (FH, FW))),
+        "xhat": rel_l2(_cplx(be.get(xhat)), np.fft.rfft2(x.astype(np.float64), s=(FH, FW))),
+        "z": rel_l2(be.get(z), O.conv2d_direct(x, g[:, 0], (ph, pw))),
+        "dx": rel_l2(be.get(dx), dxr),
+        "dG": rel_l2(be.get(gf)[:, 0], dgr),
+        "dghat": rel_l2(_cplx(be.get(dgh)),
+                        O.conv2d_fft_unshifted_bwd(gz, x, g[:, 0], (ph, pw), (FH, FW))[1]),
+    }
+
+
+def case_border_conv(be, M=4, h=12, w=10, kh=7, kw=5, FH=32, FW=16, seed=1):
+    """VALID correlation of a (h+kh-1, w+kw-1) patch: the hoisted border conv and its reverse."""
+    rng = np.random.default_rng(seed)
+    L, s = be.lib, be.stream()
+    Hp, Wp = h + kh - 1, w + kw - 1
+    patch = rng.normal(size=(1, Hp, Wp)).astype(np.float32)
+    g = rng.normal(size=(M, 1, kh, kw)).astype(np.float32)
+    gd = be.put(g)
+    ghat = be.zeros((M, FH, FW // 2 + 1, 2))
+    _ok(be, L.nc_filter_spectrum_fwd(s, M, kh, kw, FH, FW, be.ptr(gd), be.ptr(ghat)), "spec")
+    dl = be.zeros((1, M, h, w))
+    phat = be.zeros((1, FH, FW // 2 + 1, 2))
+    pd = be.put(patch)
+    _ok(be, L.nc_fftconv_fwd(s, 1, M, Hp, Wp, h, w, kh - 1, kw - 1, FH, FW, be.ptr(pd),
+                             be.ptr(ghat), be.ptr(dl), be.ptr(phat)), "fwd")
+    gdl = rng.normal(size=(1, M, h, w)).astype(np.float32)
+    gdd = be.put(gdl)
+    gp = be.zeros((1, Hp, Wp))
+    dgh = be.zeros((M, FH, FW // 2 + 1, 2))
+    ws = be.zeros((L.nc_fftconv_bwd_workspace_size(1, M, FH, FW) // 4 + 1,))
+    nb = ws.nbytes if hasattr(ws, "nbytes") else ws.numel() * 4
+    _ok(be, L.nc_fftconv_bwd(s, 1, M, Hp, Wp, h, w, kh - 1, kw - 1, FH, FW, be.ptr(gdd),
+                             be.ptr(phat), be.ptr(ghat), 1, be.ptr(gp), be.ptr(dgh), 0, 0,
+                             be.ptr(ws), nb), "bwd")
+    gf = be.zeros((M, 1, kh, kw))
+    _ok(be, L.nc_filter_spectrum_bwd(s, M, kh, kw, FH, FW, kh - 1, kw - 1, be.ptr(dgh),
+                                     be.ptr(gf), 0, 0), "specbwd")
+    gpr, ggr = O.conv2d_bwd_direct(gdl, patch, g[:, 0], (0, 0))
+    return {"delta": rel_l2(be.get(dl), O.conv2d_direct(patch, g[:, 0], (0, 0))),
+            "dpatch": rel_l2(be.get(gp), gpr), "dG": rel_l2(be.get(gf)[:, 0], ggr)}
+
+
+def case_epilogue(be, B=3, M=5, h=10, w=12, act="tanh", has_border=1, seed=2):
+    """Hidden-step epilogue forward/backward (single-pass N <= 8192, tiled above)."""
+    rng = np.random.default_rng(seed)
+    L, s = be.lib, be.stream()
+    z = (rng.normal(size=(B, M, h, w)) * 2 + 0.5).astype(np.float32)
+    d = rng.normal(size=(M, h, w)).astype(np.float32)
+    wv = rng.normal(size=(h, w)).astype(np.float32)
+    sv = rng.uniform(size=(h, w)).astype(np.float32)
+    bv = rng.normal(size=(h, w)).astype(np.float32)
+    gy = rng.normal(size=(B, h, w)).astype(np.float32)
+    zd, dd, wd, sd, bd, gyd = (be.put(a) for a in (z, d, wv, sv, bv, gy))
+    out, mean, rstd = be.zeros((B, h, w)), be.zeros((B, M)), be.zeros((B, M))
+    ws = be.zeros((L.nc_epilogue_workspace_size(B, M, h, w) // 4 + 1,))
+    nb = ws.nbytes if hasattr(ws, "nbytes") else ws.numel() * 4
+    aid = _abi.ACT_IDS[act]
+    _ok(be, L.nc_epilogue_fwd(s, B, M, h, w, aid, 0.01, has_border, be.ptr(zd), be.ptr(dd),
+                              be.ptr(wd), be.ptr(sd), be.ptr(bd), be.ptr(out), be.ptr(mean),
+                              be.ptr(rstd), be.ptr(ws), nb), "epi")
+    gz, gdb = be.zeros((B, M, h, w)), be.zeros((M, h, w))
+    gw, gs, gb = be.zeros((h, w)), be.zeros((h, w)), be.zeros((h, w))
+    _ok(be, L.nc_epilogue_bwd(s, B, M, h, w, aid, 0.01, has_border, be.ptr(zd), be.ptr(dd),
+                              be.ptr(wd), be.ptr(sd), be.ptr(bd), be.ptr(mean), be.ptr(rstd),
+                              be.ptr(gyd), be.ptr(gz), be.ptr(gdb), be.ptr(gw), be.ptr(gs),
+                              be.ptr(gb), 0, 0, be.ptr(ws), nb), "epib")
+    o_r, m_r, r_r = O.epilogue_fwd(z, d, wv, sv, bv, act, bool(has_border))
+    r = O.epilogue_bwd(z, d, wv, sv, bv, m_r, r_r, gy, act, bool(has_border))
+    res = {"out": rel_l2(be.get(out), o_r), "mean": rel_l2(be.get(mean), m_r),
+           "rstd": rel_l2(be.get(rstd), r_r)}
+    for k, a, b in zip(("gz", "gdb", "gw", "gs", "gb"), (gz, gdb, gw, gs, gb), r):
+        if k == "gdb" and not has_border:
+            continue
+        res[k] = rel_l2(be.get(a), b)
+    return res
+
+
+def case_port(be, B=3, M=5, h=10, w=12, rows=(2, 3, 4, 2), cols=(5, 5, 5, 5), fact=None,
+              seed=3):
+    """Output-port forward/backward (rect-like and coordinate ports, duplicates included)."""
+    rng = np.random.default_rng(seed)
+    L, s = be.lib, be.stream()
+    P = len(rows)
+    idx = np.array([r * w + c for r, c in zip(rows, cols)], np.int32)
+    z = rng.normal(size=(B, M, h, w)).astype(np.float32)
+    d = rng.normal(size=(M, h, w)).astype(np.float32)
+    pp = rng.normal(size=(3, P)).astype(np.float32)
+    go = rng.normal(size=(B, P)).astype(np.float32)
+    idd, zd, dd, ppd, god = be.put(idx, np.int32), be.put(z), be.put(d), be.put(pp), be.put(go)
+    out, zo = be.zeros((B, P)), be.zeros((B, M, P))
+    mean, rstd, pre = be.zeros((B, M)), be.zeros((B, M)), be.zeros((B, P))
+    ws = be.zeros((L.nc_epilogue_workspace_size(B, M, h, w) // 4 + 1,))
+    nb = ws.nbytes if hasattr(ws, "nbytes") else ws.numel() * 4
+    fid = _abi.ACT_IDS["identity" if fact is None else fact]
+    _ok(be, L.nc_port_fwd(s, B, M, h, w, 1, fid, 0.01, P, be.ptr(idd), be.ptr(zd), be.ptr(dd),
+                          be.ptr(ppd), be.ptr(out), be.ptr(zo), be.ptr(mean), be.ptr(rstd),
+                          be.ptr(pre), be.ptr(ws), nb), "portf")
+    gz, gdb, gpp = be.zeros((B, M, h, w)), be.zeros((M, h, w)), be.zeros((3, P))
+    _ok(be, L.nc_port_bwd(s, B, M, h, w, 1, fid, 0.01, P, be.ptr(idd), be.ptr(zd), be.ptr(dd),
+                          be.ptr(ppd), be.ptr(zo), be.ptr(mean), be.ptr(rstd), be.ptr(pre),
+                          be.ptr(god), be.ptr(gz), be.ptr(gdb), be.ptr(gpp), 0, be.ptr(ws), nb),
+        "portb")
+    R, Cc = np.array(rows), np.array(cols)
+    o_r, aux = O.port_fwd(z, d, R, Cc, (P, 1), pp[0][:, None], pp[1][:, None], pp[2][:, None],
+                          True, fact)
+    r = O.port_bwd(z, d, R, Cc, (P, 1), pp[0][:, None], pp[1][:, None], pp[2][:, None], aux,
+                   go[:, :, None], True, fact)
+    g = be.get(gpp)
+    return {"out": rel_l2(be.get(out), o_r[:, :, 0]), "zo": rel_l2(be.get(zo), aux["zo"][..., 0]),
+            "gz": rel_l2(be.get(gz), r[0]), "gdb": rel_l2(be.get(gdb), r[1]),
+            "gw_out": rel_l2(g[0], r[2][:, 0]), "gs_out": rel_l2(g[1], r[3][:, 0]),
+            "gb_out": rel_l2(g[2], r[4][:, 0])}
+
+
+def case_codd(be, mode="continuous", bbox=None, hard_pin=0, tau=0.1, seed=4):
+    """Pre-step Codd fusion forward and reverse on the ALU geometry (16-cell output port)."""
+    rng = np.random.default_rng(seed)
+    L, s = be.lib, be.stream()
+    geom = O.alu_geometry(out_width=2)
+    H, W = geom.grid_shape
+    kh, kw = geom.kernel_size
+    M = geom.directions
+    cell = (rng.normal(size=(3, H, W)) * np.array([0.1, 0.3, 1.0])[:, None, None]).astype(
+        np.float32)
+    rows, cols = geom.out_cells_roi
+    P = len(rows)
+    r0, r1, c0, c1 = bbox or (0, geom.roi_shape[0], 0, geom.roi_shape[1])
+    chip = _abi.ChipDesc(H, W, kh, kw, M, geom.pad_h, geom.pad_w, *geom.roi_shape, r0, r1, c0, c1)
+    h, w = r1 - r0, c1 - c0
+    cd = be.put(cell)
+    io = be.put(geom.io_state_mask, np.uint8)
+    owm = be.put(geom.out_weight_mask, np.uint8)
+    prc = be.put(np.stack([rows, cols]), np.int32)
+    we, se, br = be.zeros((h, w)), be.zeros((h, w)), be.zeros((h, w))
+    patch, pp = be.zeros((h + kh - 1, w + kw - 1)), be.zeros((3, P))
+    sp_, b2d, wp = be.zeros((H, W)), be.zeros((H, W)), be.zeros((H, W))
+    mid, it = _abi.CODD_IDS[mode], O.inv_tau_f32(tau)
+    _ok(be, L.nc_codd_fuse_fwd(s, C.byref(chip), be.ptr(cd), be.ptr(io), be.ptr(owm), mid, it,
+                               0.6, hard_pin, 1, 0.01, P, be.ptr(prc), be.ptr(we), be.ptr(se),
+                               be.ptr(br), be.ptr(patch), be.ptr(pp), be.ptr(sp_), be.ptr(b2d),
+                               be.ptr(wp)), "codd")
+    sp = O.precompute_step_params(cell, geom, "tanh", bool(hard_pin), bbox, mode, tau, 0.6)
+    fwd_got = np.concatenate([be.get(a).ravel() for a in (we, se, br, patch, pp)])
+    fwd_ref = np.concatenate([np.ravel(a) for a in (
+        sp["w_eff_roi"], sp["s_eff_roi"], sp["b_roi"], O.border_patch(sp["border_2d"], geom, bbox),
+        sp["w_eff_out"], sp["s_eff_out"], sp["b_out"])])
+    gi = [rng.normal(size=(h, w)).astype(np.float32) for _ in range(3)]
+    gpatch = rng.normal(size=(h + kh - 1, w + kw - 1)).astype(np.float32)
+    gpp = rng.normal(size=(3, P)).astype(np.float32)
+    gid = [be.put(a) for a in gi]
+    gpd, gppd = be.put(gpatch), be.put(gpp)
+    gcell = be.zeros((3, H, W))
+    _ok(be, L.nc_codd_fuse_bwd(s, C.byref(chip), be.ptr(cd), be.ptr(io), be.ptr(owm), mid, it,
+                               0.6, hard_pin, 1, 0.01, P, be.ptr(prc), *[be.ptr(a) for a in gid],
+                               be.ptr(gpd), be.ptr(gppd), be.ptr(gcell)), "coddb")
+    gbd = np.zeros((H, W))
+    gbd[r0:r0 + gpatch.shape[0], c0:c0 + gpatch.shape[1]] = gpatch
+    gbd[geom.pad_h:H - geom.pad_h, geom.pad_w:W - geom.pad_w] = 0
+    oh, ow = geom.out_size
+    ref = O.precompute_step_params_vjp(
+        cell, geom, dict(w_eff_roi=gi[0], s_eff_roi=gi[1], b_roi=gi[2], border_2d=gbd,
+                         w_eff_out=gpp[0].reshape(oh, ow), s_eff_out=gpp[1].reshape(oh, ow),
+                         b_out=gpp[2].reshape(oh, ow)),
+        "tanh", bool(hard_pin), bbox, mode, tau, 0.6)
+    return {"fwd": rel_l2(fwd_got, fwd_ref), "s_prob": rel_l2(be.get(sp_), sp["s_prob"]),
+            "border_2d": rel_l2(be.get(b2d), sp["border_2d"]),
+            "w_pinned": rel_l2(be.get(wp), sp["w_pinned"]), "g_cell": rel_l2(be.get(gcell), ref)}
+
+
+def case_adaptive(be, seed=5):
+    """Adaptive-mask statistics: the 8 integers and the dilated mask are compared exactly
+    (returned as mismatch counts)."""
+    rng = np.random.default_rng(seed)
+    L, s = be.lib, be.stream()
+    geom = O.alu_geometry(out_width=2)
+    H, W = geom.grid_shape
+    kh, kw = geom.kernel_size
+    M = geom.directions
+    hv, wv = geom.roi_shape
+    cell = (rng.normal(size=(3, H, W)) * np.array([0.1, 0.3, 1.0])[:, None, None]).astype(
+        np.float32)
+    cell[1, 20, 30], cell[2, 20, 30] = 0.8, 2.0
+    env = np.exp(-((np.arange(kh)[:, None] - 11) ** 2 / 8.0 + (np.arange(kw)[None] - 6) ** 2 / 4.0))
+    filt = (rng.normal(size=(M, 1, kh, kw)) * env[None, None]).astype(np.float32)
+    chip = _abi.ChipDesc(H, W, kh, kw, M, geom.pad_h, geom.pad_w, hv, wv, 0, hv, 0, wv)
+    io_roi = geom.io_state_mask[geom.pad_h:H - geom.pad_h, geom.pad_w:W - geom.pad_w]
+    st, dil = be.zeros((8,), np.int32), be.zeros((hv, wv), np.uint8)
+    # operands stay referenced until the (asynchronous) launch has completed
+    cd, fd, iod = be.put(cell), be.put(filt), be.put(io_roi, np.uint8)
+    _ok(be, L.nc_adaptive_stats(s, C.byref(chip), be.ptr(cd), be.ptr(fd), be.ptr(iod), None, 4, 4,
+                                2.5, 0.05, 0.05, 1e-3, be.ptr(st), be.ptr(dil)), "adaptive")
+    st_r, dil_r = O.adaptive_mask_stats(cell, filt, io_roi, geom, (4, 4))
+    return {"stats_mismatch": float((be.get(st) != st_r).sum()),
+            "mask_mismatch": float((be.get(dil).astype(bool) != dil_r).sum())}
+
+
+def case_helpers(be, seed=6):
+    """Input injection (exact), MSE loss and three AdamW steps."""
+    rng = np.random.default_rng(seed)
+    L, s = be.lib, be.stream()
+    B, n_in, n_roi = 4, 24, 200
+    inp = rng.normal(size=(B, n_in)).astype(np.float32)
+    src = np.full(n_roi, -1, np.int32)
+    src[[5, 77, 199]] = [0, 3, 23]
+    roi = be.zeros((B, n_roi))
+    inpd, srcd = be.put(inp), be.put(src, np.int32)
+    _ok(be, L.nc_inject_roi(s, B, n_in, be.ptr(inpd), n_roi, be.ptr(srcd), be.ptr(roi)), "inject")
+    ref = np.zeros((B, n_roi), np.float32)
+    ref[:, [5, 77, 199]] = inp[:, [0, 3, 23]]
+    pr = rng.normal(size=100).astype(np.float32)
+    tg = rng.normal(size=100).astype(np.float32)
+    loss, gp = be.zeros((1,)), be.zeros((100,))
+    prd, tgd = be.put(pr), be.put(tg)
+    _ok(be, L.nc_mse_loss(s, 100, be.ptr(prd), be.ptr(tgd), be.ptr(loss), be.ptr(gp)), "mse")
+    l_r, g_r = O.mse_loss(pr, tg)
+    p0 = rng.normal(size=50).astype(np.float32)
+    g = rng.normal(size=50).astype(np.float32)
+    p, gd = be.put(p0), be.put(g)
+    m, v, cnt = be.zeros((50,)), be.zeros((50,)), be.zeros((1,), np.int32)
+    lr = be.put(np.array([0.01], np.float32))
+    pr_, mr, vr, cr = p0.astype(np.float64), 0.0, 0.0, 0
+    for _ in range(3):
+        _ok(be, L.nc_adamw_step(s, 50, be.ptr(p), be.ptr(gd), be.ptr(m), be.ptr(v), be.ptr(cnt),
+                                be.ptr(lr), 0.9, 0.999, 1e-8, 1e-4), "adamw")
+        pr_, mr, vr, cr = O.adamw_step(pr_, g.astype(np.float64), mr, vr, cr, 0.01)
+    return {"inject_mismatch": float((be.get(roi) != ref).sum()),
+            "mse": abs(float(be.get(loss)[0]) - l_r) / l_r, "g_mse": rel_l2(be.get(gp), g_r),
+            "adamw": rel_l2(be.get(p), pr_), "count_mismatch": float(be.get(cnt)[0] != 3)}
+
+
+EPILOGUE_SHAPES = [
+    # (B, M, h, w, act, has_border): single pass, tiled Chan (> 8192 px, partial last tile)
+    (3, 5, 10, 12, "tanh", 1),
+    (2, 16, 40, 50, "tanh", 0),
+    (2, 3, 24, 32, "sigmoid", 1),
+    (2, 4, 20, 40, "leaky_relu", 1),
+    (2, 3, 33, 47, "relu", 1),
+    (2, 3, 96, 100, "gelu", 1),
+    (1, 2, 90, 92, "identity", 0),
+]
+
+PORT_SHAPES = [
+    (3, 5, 10, 12, (2, 3, 4, 2), (5, 5, 5, 5), None),
+    (2, 16, 40, 50, tuple(range(16, 24)) * 2, (35,) * 8 + (36,) * 8, None),
+    (2, 3, 96, 100, (10, 50, 95), (3, 99, 0), "tanh"),
+]
+
+CODD_CASES = [(m, b, hp) for m in O.CODD_MODES for b in (None, (6, 30, 10, 42)) for hp in (0, 1)]

@@ -1,0 +1,69 @@
+"""Entry-point parity on the MI355X: each C-ABI kernel family against the float64 oracle."""
+import pytest
+
+from kernel_cases import (CODD_CASES, EPILOGUE_SHAPES, PORT_SHAPES, TOL, DeviceBackend,
+                          case_adaptive, case_border_conv, case_codd, case_epilogue,
+                          case_fftconv, case_helpers, case_port)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def be():
+    from neurocell._lib import load_library
+    return DeviceBackend(load_library())
+
+
+def _assert_small(res, tol=TOL):
+    bad = {k: v for k, v in res.items() if not v < tol}
+    assert not bad, f"parity errors above {tol}: {bad} (all: {res})"
+
+
+@pytest.mark.parametrize("FH,FW,hin,win,kh,kw", [
+    (16, 16, 10, 12, 5, 3), (64, 64, 40, 50, 23, 13), (64, 64, 24, 32, 23, 13),
+    (32, 64, 20, 50, 9, 13), (64, 32, 41, 19, 21, 13)])
+def test_fftconv(be, FH, FW, hin, win, kh, kw):
+    _assert_small(case_fftconv(be, B=4, M=6, hin=hin, win=win, kh=kh, kw=kw, FH=FH, FW=FW))
+
+
+def test_fftconv_alu_batch(be):
+    _assert_small(case_fftconv(be, B=128, M=16, hin=40, win=50, kh=23, kw=13, FH=64, FW=64))
+
+
+@pytest.mark.parametrize("h,w,kh,kw,FH,FW", [(12, 10, 7, 5, 32, 16), (40, 50, 23, 13, 64, 64),
+                                             (24, 32, 23, 13, 64, 64)])
+def test_border_conv(be, h, w, kh, kw, FH, FW):
+    _assert_small(case_border_conv(be, M=16, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW))
+
+
+@pytest.mark.parametrize("shape", EPILOGUE_SHAPES)
+def test_epilogue(be, shape):
+    B, M, h, w, act, hb = shape
+    _assert_small(case_epilogue(be, B, M, h, w, act, hb))
+
+
+def test_epilogue_alu_batch(be):
+    _assert_small(case_epilogue(be, 128, 16, 40, 50, "tanh", 1))
+
+
+@pytest.mark.parametrize("shape", PORT_SHAPES)
+def test_port(be, shape):
+    B, M, h, w, rows, cols, fact = shape
+    _assert_small(case_port(be, B, M, h, w, rows, cols, fact))
+
+
+@pytest.mark.parametrize("mode,bbox,hard_pin", CODD_CASES)
+def test_codd(be, mode, bbox, hard_pin):
+    # the (1 - s) cancellation at pinned output cells is an fp32 property of the reference too
+    _assert_small(case_codd(be, mode, bbox, hard_pin), tol=1e-5)
+
+
+def test_adaptive_stats(be):
+    res = case_adaptive(be)
+    assert res == {"stats_mismatch": 0.0, "mask_mismatch": 0.0}, res
+
+
+def test_helpers(be):
+    res = case_helpers(be)
+    assert res["inject_mismatch"] == 0 and res["count_mismatch"] == 0, res
+    _assert_small({k: res[k] for k in ("mse", "g_mse", "adamw")})

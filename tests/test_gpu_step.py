@@ -1,0 +1,98 @@
+"""Whole-step parity on the MI355X: the d-step pure-ROI forward and its reverse pass through
+the C-ABI (StepPlan) against the float64 oracle (``oracle.propagate_vjp``), on the benchmark
+geometries at oracle-friendly batch sizes.
+
+Bars: forward port outputs rel-L2 <= 1e-5, parameter gradients
+(W, B, S and Green's filters) rel-L2 <= 1e-4.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import alu_case, rel_l2
+from oracle import vnn_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+FWD_TOL = 1e-5
+GRAD_TOL = 1e-4
+
+
+def run_plan(topo, cell, filt, x, g_out, mode="continuous", tau=1.0, bbox=None,
+             final_act=None, hard_pin=False):
+    from neurocell.engine import StepPlan, flatten_inputs, inv_tau_f32, port_input_shapes
+    dev = torch.device("cuda")
+    xt = torch.from_numpy(x).to(dev)
+    plan = StepPlan(topo, x.shape[0], port_input_shapes(xt, topo), roi_bbox=bbox,
+                    final_activate=final_act, hard_pin_io=hard_pin, training=True)
+    c = torch.from_numpy(cell).to(dev)
+    f = torch.from_numpy(filt).to(dev)
+    it = inv_tau_f32(tau)
+    out = plan.forward(c, f, flatten_inputs(xt, topo), codd_mode=mode, inv_tau=it)
+    gc = torch.empty_like(c)
+    gf = torch.empty_like(f)
+    plan.backward(c, f, torch.from_numpy(g_out.reshape(x.shape[0], -1)).to(dev), gc, gf,
+                  codd_mode=mode, inv_tau=it)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), gc.cpu().numpy(), gf.cpu().numpy()
+
+
+def check(geom, topo, cell, filt, x, mode, tau, bbox, final_act=None, hard_pin=False, seed=0):
+    B = x.shape[0]
+    rng = np.random.default_rng(seed + 100)
+    g_out = rng.normal(size=(B,) + geom.out_size).astype(np.float32)
+    out, gc, gf = run_plan(topo, cell, filt, x, g_out, mode, tau, bbox, final_act, hard_pin)
+    r_out, r_gc, r_gf = O.propagate_vjp(cell, filt, x, geom, g_out, act="tanh",
+                                        final_act=final_act, hard_pin_io=hard_pin,
+                                        roi_bbox=bbox, mode=mode, tau=tau)
+    errs = {"out": rel_l2(out, r_out.reshape(B, -1)), "gW": rel_l2(gc[0], r_gc[0]),
+            "gB": rel_l2(gc[1], r_gc[1]), "gS": rel_l2(gc[2], r_gc[2]),
+            "gG": rel_l2(gf, r_gf)}
+    assert errs["out"] < FWD_TOL, errs
+    for k in ("gW", "gB", "gS", "gG"):
+        assert errs[k] < GRAD_TOL, errs
+    return errs
+
+
+@pytest.mark.parametrize("mode,tau,bbox", [
+    ("continuous", 1.0, None),            # config 0 (train)
+    ("ste_ternary", 0.1, None),           # config 1 (eval mode, gradients still checked)
+    ("annealed", 0.1, None),
+    ("ste_binary", 0.1, (6, 30, 10, 42)),  # config 4 (adaptive 24x32 crop)
+    ("continuous", 1.0, (6, 30, 10, 42)),
+])
+def test_alu_step_parity(mode, tau, bbox):
+    from neurocell.topology import ChipTopology2D
+    geom, cell, filt, x, _ = alu_case(0, B=16)
+    topo = ChipTopology2D.alu_chip(out_width=2)
+    check(geom, topo, cell, filt, x, mode, tau, bbox)
+
+
+@pytest.mark.parametrize("depth", [1, 2, 3])
+def test_depths(depth):
+    from neurocell.topology import ChipTopology2D
+    geom, cell, filt, x, _ = alu_case(1, B=8, depth=depth)
+    topo = ChipTopology2D.alu_chip(out_width=2, depth=depth)
+    check(geom, topo, cell, filt, x, "continuous", 1.0, None)
+
+
+def test_final_activation_and_hard_pin():
+    from neurocell.topology import ChipTopology2D
+    geom, cell, filt, x, _ = alu_case(2, B=8)
+    topo = ChipTopology2D.alu_chip(out_width=2)
+    check(geom, topo, cell, filt, x, "annealed", 0.3, None, final_act="tanh", hard_pin=True)
+
+
+def test_trained_checkpoint_parameters():
+    """The reference's shipped 62x62 ALU checkpoint (tests/golden/alu_arithmetic_cells.npz,
+    filters stored IHWO) through the standard 8x1 output port."""
+    import os
+    from neurocell.topology import ChipTopology2D
+    path = os.path.join(os.path.dirname(__file__), "golden", "alu_arithmetic_cells.npz")
+    with np.load(path, allow_pickle=False) as d:
+        cell = np.stack([d["weights"], d["biases"], d["states"]]).astype(np.float32)
+        filt = np.ascontiguousarray(np.transpose(d["filters"], (3, 0, 1, 2))).astype(np.float32)
+    geom = O.alu_geometry(out_width=1)
+    topo = ChipTopology2D.alu_chip()
+    _, _, _, x, _ = alu_case(3, B=16, out_width=1)
+    check(geom, topo, cell, filt, x, "continuous", 1.0, None)
