@@ -1,0 +1,282 @@
+#!/usr/bin/env python3
+"""Benchmark of the VNN propagation step on one MI355X (BASELINE.json metric).
+
+Workload: 62x62 ALU chip, ROI 40x50, K = 23x13, M = 16 Green's filters,
+d = 4, B = 128, fp32, continuous Codd mode, output port widened to 8x2 = 16 target cells.
+A *step* is one optimiser step of the reference's VNNTrainer.train_step: forward, MSE loss,
+reverse pass and the AdamW update, on a batch already resident in HBM.  The whole step is
+captured once in a HIP graph and replayed.
+
+Also reported: eval samples/s (config 1: B = 1024, ste_ternary, tau = 0.1, forward only, and
+the same at B = 128), per-kernel-family device times with their roofline against 8 TB/s, and
+the CPU baseline (the float32 NumPy/scipy.fft restatement in ``oracle/``, timed on this
+host's cores).  Prints exactly one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "neurocell-v2_amd"))
+
+METRIC = "train ms/step & eval samples/s at 62x62 ALU B=128; % of HBM roofline"
+HBM_PEAK_GBS = 8000.0
+
+
+def synthetic_config0(seed, B, codd_bits=3):
+    """BASELINE config 0 inputs: W~N(0,0.1), B~N(0,0.01), S~N(0,1) on (3,62,62); filters
+    ~N(0,1/K) (variance 1/K, K = 299); two uniform 8-bit operands and a 3-bit opcode as
+    {0,1} port cells; 16 seeded random target bits."""
+    rng = np.random.default_rng(seed)
+    H = W = 62
+    kh, kw, M = 23, 13, 16
+    cell = np.stack([rng.normal(0, 0.1, (H, W)), rng.normal(0, 0.01, (H, W)),
+                     rng.normal(0, 1.0, (H, W))]).astype(np.float32)
+    filt = rng.normal(0, 1.0 / np.sqrt(kh * kw), (M, 1, kh, kw)).astype(np.float32)
+    a = rng.integers(0, 256, size=B, dtype=np.uint8)
+    b = rng.integers(0, 256, size=B, dtype=np.uint8)
+    op = rng.integers(0, 1 << codd_bits, size=B, dtype=np.uint8)
+    x = np.zeros((B, 3, 8, 1), np.float32)
+    x[:, 0, :, 0] = np.unpackbits(a[:, None], axis=1)
+    x[:, 1, :, 0] = np.unpackbits(b[:, None], axis=1)
+    x[:, 2, :, 0] = np.unpackbits(op[:, None], axis=1)
+    y = rng.integers(0, 2, size=(B, 8, 2)).astype(np.float32)
+    return cell, filt, x, y
+
+
+def algorithmic_bytes(B, M, N, F, hb=1, dx=1, P=16):
+    """Per-call algorithmic bytes (each interface operand counted once, 4 B/f32, 8 B/c64)."""
+    return {
+        "fftconv_fwd": 4 * B * N + 8 * M * F + 4 * B * M * N,
+        "fftconv_bwd": 4 * B * M * N + 4 * B * N + 8 * M * F + dx * 4 * B * N + 16 * M * F,
+        "epilogue_fwd": 4 * (B * M * N + hb * M * N + 3 * N + B * N + 2 * B * M),
+        "epilogue_bwd": 4 * (2 * B * M * N + 2 * hb * M * N + 6 * N + 2 * B * M + B * N),
+        "port_fwd": 4 * (B * M * N + hb * M * N + 2 * B * M + B * M * P),
+        "port_bwd": 4 * (2 * B * M * N + 2 * hb * M * N + 4 * B * M + B * M * P),
+    }
+
+
+def time_family(fn, reps, torch):
+    """Average device time of fn() over reps back-to-back launches on the current stream."""
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps * 1e3  # us
+
+
+def kernel_families(ts, torch, reps):
+    """Device time per call of each C-ABI family at the step's shapes (after a step, so every
+    operand holds real data)."""
+    from neurocell._lib import call, ptr, stream_ptr
+    p = ts.plan
+    B, M, h, w = p.B, p.M, p.h, p.w
+    fh, fw = p.fft
+    t = 1
+    s = stream_ptr
+    ws_ep, n_ep = ptr(p.ws_epi), p.ws_epi.numel() * 4
+    ws_fc, n_fc = ptr(p.ws_fc), p.ws_fc.numel() * 4
+    fams = {
+        "fftconv_fwd": lambda: call("nc_fftconv_fwd", s(), B, M, h, w, h, w, p.cp[0], p.cp[1],
+                                    fh, fw, ptr(p.xs[t]), ptr(p.ghat), ptr(p.zs[t]),
+                                    ptr(p.xhat[t])),
+        "fftconv_bwd": lambda: call("nc_fftconv_bwd", s(), B, M, h, w, h, w, p.cp[0], p.cp[1],
+                                    fh, fw, ptr(p.gz), ptr(p.xhat[t]), ptr(p.ghat), 1,
+                                    ptr(p.gy[0]), ptr(p.dghat), 0, 0, ws_fc, n_fc),
+        "epilogue_fwd": lambda: call("nc_epilogue_fwd", s(), B, M, h, w, p.act, p.slope, 1,
+                                     ptr(p.zs[t]), ptr(p.delta), ptr(p.w_eff), ptr(p.s_eff),
+                                     ptr(p.b_roi), ptr(p.xs[t + 1]), ptr(p.mean[t]),
+                                     ptr(p.rstd[t]), ws_ep, n_ep),
+        "epilogue_bwd": lambda: call("nc_epilogue_bwd", s(), B, M, h, w, p.act, p.slope, 1,
+                                     ptr(p.zs[t]), ptr(p.delta), ptr(p.w_eff), ptr(p.s_eff),
+                                     ptr(p.b_roi), ptr(p.mean[t]), ptr(p.rstd[t]),
+                                     ptr(p.gy[1]), ptr(p.gz), ptr(p.gdelta), ptr(p.gw),
+                                     ptr(p.gs), ptr(p.gb), 0, 0, ws_ep, n_ep),
+        "port_fwd": lambda: call("nc_port_fwd", s(), B, M, h, w, 1, p.fact, p.fslope, p.P,
+                                 ptr(p.port_idx), ptr(p.zs[-1]), ptr(p.delta), ptr(p.pp),
+                                 ptr(p.out), ptr(p.zo), ptr(p.mean[-1]), ptr(p.rstd[-1]),
+                                 ptr(p.pre), ws_ep, n_ep),
+        "port_bwd": lambda: call("nc_port_bwd", s(), B, M, h, w, 1, p.fact, p.fslope, p.P,
+                                 ptr(p.port_idx), ptr(p.zs[-1]), ptr(p.delta), ptr(p.pp),
+                                 ptr(p.zo), ptr(p.mean[-1]), ptr(p.rstd[-1]), ptr(p.pre),
+                                 ptr(p.g_out), ptr(p.gz), ptr(p.gdelta), ptr(p.gpp), 0, ws_ep,
+                                 n_ep),
+    }
+    per_step = {"fftconv_fwd": p.d, "fftconv_bwd": p.d, "epilogue_fwd": p.d - 1,
+                "epilogue_bwd": p.d - 1, "port_fwd": 1, "port_bwd": 1}
+    return {k: (time_family(f, reps, torch), per_step[k]) for k, f in fams.items()}
+
+
+def cpu_baseline(seed, B, budget_s):
+    """Float32 NumPy + scipy.fft restatement (oracle/) of one config-0 train step on this
+    host's cores: forward, MSE loss, reverse pass and AdamW.  Timed over a bounded sample."""
+    from oracle import vnn_oracle as O
+    cores = len(os.sched_getaffinity(0))
+    cell, filt, x, y = synthetic_config0(seed, B)
+    geom = O.alu_geometry(out_width=2)
+    m = np.zeros(cell.size + filt.size, np.float32)
+    v = np.zeros_like(m)
+    theta = np.concatenate([cell.ravel(), filt.ravel()])
+    times = []
+    with O.precision(np.float32, workers=cores):
+        t_end = time.perf_counter() + budget_s
+        count = 0
+        while True:
+            t0 = time.perf_counter()
+            c = theta[:cell.size].reshape(cell.shape)
+            f = theta[cell.size:].reshape(filt.shape)
+            fwd = O.propagate(c, f, x, geom)
+            _, g_out = O.mse_loss(fwd[0], y)
+            _, gc, gf = O.propagate_vjp(c, f, x, geom, g_out.astype(np.float32), fwd=fwd)
+            g = np.concatenate([gc.ravel(), gf.ravel()]).astype(np.float32)
+            theta, m, v, count = O.adamw_step(theta, g, m, v, count, 1e-3)
+            theta = theta.astype(np.float32)
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() > t_end and len(times) >= 2:
+                break
+    return {"value": round(1e3 * float(np.median(times)), 3), "unit": "ms/step", "cores": cores,
+            "kind": "port",
+            "sample": f"{len(times)} config-0 train steps (B={B}, fwd+bwd+AdamW), float32 "
+                      f"NumPy + scipy.fft restatement in oracle/, scipy.fft workers={cores}, "
+                      "median reported"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
+    ap.add_argument("--no-graph", action="store_true", help="launch eagerly, no HIP graph")
+    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline")
+    ap.add_argument("--kernel-reps", type=int, default=200)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on exactly one GPU (--gpus {args.gpus} requested); "
+              "the data-parallel sharding over B is described in DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from neurocell.engine import (EvalState, ParamState, StepPlan, TrainState, flatten_inputs,
+                                  port_input_shapes)
+    from neurocell.topology import ChipTopology2D
+
+    dev = torch.device("cuda")
+    topo = ChipTopology2D.alu_chip(n=8, kernel_size=(23, 13), directions=16, depth=4,
+                                   out_width=2)
+    B = 128
+    cell, filt, x, y = synthetic_config0(0, B)
+    xt = torch.from_numpy(x).to(dev)
+    plan = StepPlan(topo, B, port_input_shapes(xt, topo), training=True)
+    ps = ParamState(torch.from_numpy(cell).to(dev), torch.from_numpy(filt).to(dev),
+                    learning_rate=1e-3)
+    ts = TrainState(plan, ps)
+    ts.x.copy_(flatten_inputs(xt, topo))
+    ts.y.copy_(torch.from_numpy(y.reshape(B, -1)).to(dev))
+    if not args.no_graph:
+        ts.capture()
+    for _ in range(args.warmup):
+        ts.step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        ts.step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    dev_ms = e0.elapsed_time(e1) / args.steps
+    loss = float(ts.plan.loss.item())
+    if not np.isfinite(loss):
+        raise RuntimeError(f"non-finite loss {loss}")
+
+    # evaluation throughput (config 1 and config 0 batch)
+    evals = {}
+    for name, eb, mode, tau in (("config1_B1024_ste_ternary", 1024, "ste_ternary", 0.1),
+                                ("B128_continuous", 128, "continuous", 1.0)):
+        _, _, xe, _ = synthetic_config0(1, eb)
+        xet = torch.from_numpy(xe).to(dev)
+        ep = StepPlan(topo, eb, port_input_shapes(xet, topo), training=False)
+        es = EvalState(ep, ps.cell, ps.filt, codd_mode=mode, state_temperature=tau)
+        es.x.copy_(flatten_inputs(xet, topo))
+        if not args.no_graph:
+            es.capture()
+        reps = max(20, args.steps // 2)
+        for _ in range(5):
+            es.run()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            es.run()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / reps
+        evals[name] = {"ms_per_batch": round(ms, 4), "samples_per_s": round(eb / ms * 1e3, 1)}
+
+    # per-family device times and the roofline of the dominant one
+    fams = kernel_families(ts, torch, args.kernel_reps)
+    F = plan.F
+    ab = algorithmic_bytes(B, plan.M, plan.N, F, P=plan.P)
+    share = {k: us * n for k, (us, n) in fams.items()}
+    dom = max(share, key=share.get)
+    us = fams[dom][0]
+    achieved = ab[dom] / (us * 1e-6) / 1e9
+    kernels = {k: {"us_per_call": round(us_, 2), "calls_per_step": n,
+                   "algorithmic_MB": round(ab[k] / 1e6, 3),
+                   "GBps": round(ab[k] / (us_ * 1e-6) / 1e9, 1),
+                   "frac_hbm": round(ab[k] / (us_ * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+               for k, (us_, n) in fams.items()}
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic_config0.json")
+    if os.path.exists(tpath):
+        with open(tpath) as fh:
+            traffic = json.load(fh).get(dom)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(0, B, args.cpu_budget)
+
+    rec = {
+        "metric": METRIC,
+        "value": round(wall_ms, 4),
+        "unit": "ms/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded BASELINE config-0 distributions; resident in HBM)",
+        "config": {"workload": "config0: 62x62 ALU, ROI 40x50, K=23x13, M=16, d=4, B=128, "
+                               "fp32, continuous Codd, 16-cell output port; train step = "
+                               "fwd + MSE + bwd + AdamW, HIP-graph replay",
+                   "global_batch": B, "grid": [62, 62], "roi": [40, 50], "kernel": [23, 13],
+                   "directions": 16, "depth": 4, "fft": list(plan.fft),
+                   "graph": not args.no_graph},
+        "device_ms_per_step": round(dev_ms, 4),
+        "final_loss": round(loss, 6),
+        "eval": evals,
+        "eval_samples_per_s": evals["config1_B1024_ste_ternary"]["samples_per_s"],
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec))
+
+
+if __name__ == "__main__":
+    main()

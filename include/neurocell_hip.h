@@ -187,6 +187,8 @@ int nc_epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg
  * [w_eff_out, s_eff_out, b_out].  Writes out (B,P), zo (B,M,P), mean/rstd (B,M) and, when
  * final_act != identity, pre (B,P) (the pre-activation residual).  Planes above 8192 pixels use
  * the tiled Chan statistics and need ws (nc_epilogue_workspace_size bytes).
+ * port_params == NULL is pallas_standardize_output_port alone (kernels_pallas.py:1284-1347):
+ * only zo, mean and rstd are written; out, pre and final_act are ignored.
  */
 int nc_port_fwd(void* stream, int B, int M, int h, int w, int has_border, int final_act,
                 float neg_slope, int n_port, const int32_t* port_idx, const float* z,
@@ -197,7 +199,8 @@ int nc_port_fwd(void* stream, int B, int M, int h, int w, int has_border, int fi
  * Backward of nc_port_fwd (kernels_pallas.py:1350-1504, 1538-1551): dense
  * gz = -rstd*(c1 + zhat*c2) plus rstd*g scattered at the port cells in registers; gdb =
  * sum_b gz when has_border; gdb and g_port_params (3,P) overwritten, or added to when
- * accumulate_params.
+ * accumulate_params.  With port_params == NULL (standardisation only, kernels_pallas.py:
+ * 1350-1504) g_out is the (B,M,P) cotangent of zo and g_port_params is not touched.
  */
 int nc_port_bwd(void* stream, int B, int M, int h, int w, int has_border, int final_act,
                 float neg_slope, int n_port, const int32_t* port_idx, const float* z,
@@ -236,12 +239,23 @@ int nc_mse_loss(void* stream, int n, const float* pred, const float* target, flo
                 float* g_pred);
 
 /*
- * optax.adamw update with its default arguments as used by VNNTrainer (trainer.py:101-106):
- * count[0] += 1; m,v moments; bias correction by count; p -= lr[0] * (mhat/(sqrt(vhat)+eps)
- * + weight_decay * p).  count and lr live in device memory so a captured graph replays it.
+ * One batch of VNNTrainer.evaluate_packed (trainer.py:49-54, 122-138): for each sample b the 8
+ * port outputs out[b, 0..7] are rounded half-to-even, saturated to uint8 (NaN -> 0) and packed
+ * MSB-first (BIT_WEIGHTS_U8, trainer.py:20) into preds_packed[b] (may be NULL); then
+ * acc[0] += mean_b(preds_packed[b] == y_packed[b]) in fp32.  n_out must be 8.
+ */
+int nc_packed_accuracy(void* stream, int B, int n_out, const float* out,
+                       const uint8_t* y_packed, uint8_t* preds_packed, float* acc);
+
+/*
+ * optax.adamw(learning_rate) update as applied by VNNTrainer (trainer.py:101-106): with
+ * c = count[0] (the number of earlier updates), m,v moments, bias correction by c+1, and
+ * p -= lr[min(c, n_lr-1)] * (mhat/(sqrt(vhat)+eps) + weight_decay * p); then count[0] = c+1.
+ * ``lr`` is a device table of the learning-rate schedule evaluated at 0..n_lr-1 (n_lr = 1 for a
+ * constant rate; later steps reuse the last entry), so a captured graph replays the schedule.
  */
 int nc_adamw_step(void* stream, int n, float* p, const float* g, float* m, float* v,
-                  int32_t* count, const float* lr, float b1, float b2, float eps,
+                  int32_t* count, const float* lr, int n_lr, float b1, float b2, float eps,
                   float weight_decay);
 
 #ifdef __cplusplus

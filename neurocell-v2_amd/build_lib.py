@@ -17,7 +17,7 @@ OUT = os.path.join(HERE, "neurocell", "libneurocell_hip.so")
 BUILD = os.path.join(HERE, "_build")
 SOURCES = ("nc_codd.hip", "nc_epilogue.hip", "nc_spectral.hip")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-FLAGS = ["-O3", "-std=c++17", "--offload-arch=gfx950", "-fPIC",
+FLAGS = ["-O3", "-std=c++20", "--offload-arch=gfx950", "-fPIC",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 

@@ -153,7 +153,7 @@ __global__ __launch_bounds__(kAdNT) void k_adaptive(
     uint8_t* __restrict__ dil) {
     HIP_DYNAMIC_SHARED(uint8_t, smask)  // 2 * roi_h * roi_w: seed, row-dilated
     __shared__ float red[6 * (kAdNT / 64)];
-    __shared__ float peak_s[kAdNT / 64];
+    __shared__ float peak_s[kAdNT / 64 + 1];
     const int tid = threadIdx.x;
     const int K = c.kh * c.kw, HW = c.H * c.W;
     const int hv = c.roi_h, wv = c.roi_w, N = hv * wv;
@@ -196,7 +196,7 @@ __global__ __launch_bounds__(kAdNT) void k_adaptive(
             v[3] += fabsf(w) * sp;
         }
     }
-    block_sum<4>(v, red);
+    block_sum<4, kAdNT>(v, red);
     const float upd_cnt = fmaxf(1.f, v[0]), nonio_cnt = fmaxf(1.f, v[2]);
     const float b_mean = v[1] / upd_cnt, w_mean = v[3] / nonio_cnt;
     float q2[2] = {0.f, 0.f};
@@ -213,7 +213,7 @@ __global__ __launch_bounds__(kAdNT) void k_adaptive(
             q2[1] += d * d;
         }
     }
-    block_sum<2>(q2, red);
+    block_sum<2, kAdNT>(q2, red);
     const float b_std = sqrtf(q2[0] / upd_cnt), w_std = sqrtf(q2[1] / nonio_cnt);
     // 3. seed mask
     float cnt = 0.f;
@@ -275,7 +275,7 @@ __global__ __launch_bounds__(kAdNT) void k_adaptive(
         red[5 * 16 + wave] = rw;
     }
     float cv[1] = {cnt};
-    block_sum<1>(cv, peak_s);  // barriers also publish red[]
+    block_sum<1, kAdNT>(cv, peak_s);  // barriers also publish red[]
     if (tid == 0) {
         float a0 = hv, a1 = -1.f, a2 = wv, a3 = -1.f, a4 = 0.f, a5 = 0.f;
         for (int w_ = 0; w_ < kAdNT / 64; ++w_) {
@@ -313,7 +313,7 @@ __global__ void k_inject(int B, int n_in, const float* __restrict__ in, int n_ro
 __global__ __launch_bounds__(1024) void k_mse(int n, const float* __restrict__ pred,
                                               const float* __restrict__ tgt,
                                               float* __restrict__ loss, float* __restrict__ g) {
-    __shared__ float red[16];
+    __shared__ float red[1024 / 64 + 1];
     const float inv_n = 1.0f / (float)n;
     float acc[1] = {0.f};
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
@@ -321,17 +321,44 @@ __global__ __launch_bounds__(1024) void k_mse(int n, const float* __restrict__ p
         acc[0] += d * d;
         g[i] = 2.0f * d * inv_n;
     }
-    block_sum<1>(acc, red);
+    block_sum<1, 1024>(acc, red);
     if (threadIdx.x == 0) loss[0] = acc[0] * inv_n;
+}
+
+// One workgroup walks the batch: byte = sum_j sat_u8(rint(out[b,j])) << (7-j), compared
+// with the packed label; the matching count is exact in fp32 (B < 2^24), so the fp32
+// batch mean and the running sum reproduce a sequential scan carry.
+__global__ __launch_bounds__(1024) void k_packed_acc(int B, const float* __restrict__ out,
+                                                     const uint8_t* __restrict__ y,
+                                                     uint8_t* __restrict__ preds,
+                                                     float* __restrict__ acc) {
+    __shared__ float red[1024 / 64 + 1];
+    float hit[1] = {0.f};
+    for (int b = threadIdx.x; b < B; b += blockDim.x) {
+        unsigned byte = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float r = rintf(out[(size_t)b * 8 + j]);
+            const unsigned q = r > 0.f ? (r < 255.f ? (unsigned)r : 255u) : 0u;  // NaN -> 0
+            byte += q << (7 - j);
+        }
+        byte &= 0xffu;
+        if (preds) preds[b] = (uint8_t)byte;
+        hit[0] += byte == (unsigned)y[b] ? 1.f : 0.f;
+    }
+    block_sum<1, 1024>(hit, red);
+    if (threadIdx.x == 0) acc[0] = acc[0] + hit[0] / (float)B;
 }
 
 __global__ void k_adamw(int n, float* __restrict__ p, const float* __restrict__ g,
                         float* __restrict__ m, float* __restrict__ v,
-                        const int* __restrict__ count, const float* __restrict__ lr, float b1,
-                        float b2, float eps, float wd) {
+                        const int* __restrict__ count, const float* __restrict__ lr, int n_lr,
+                        float b1, float b2, float eps, float wd) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    const float t = (float)(count[0] + 1);
+    const int c = count[0];
+    const float rate = lr[c < n_lr ? c : n_lr - 1];
+    const float t = (float)(c + 1);
     const float gi = g[i];
     const float mi = (1.0f - b1) * gi + b1 * m[i];
     const float vi = (1.0f - b2) * gi * gi + b2 * v[i];
@@ -340,7 +367,7 @@ __global__ void k_adamw(int n, float* __restrict__ p, const float* __restrict__ 
     const float mh = mi / (1.0f - powf(b1, t));
     const float vh = vi / (1.0f - powf(b2, t));
     const float u = mh / (sqrtf(vh) + eps) + wd * p[i];
-    p[i] = p[i] - lr[0] * u;
+    p[i] = p[i] - rate * u;
 }
 
 __global__ void k_count_inc(int* count) {
@@ -451,13 +478,23 @@ int nc_mse_loss(void* stream, int n, const float* pred, const float* target, flo
     return NC_OK;
 }
 
+int nc_packed_accuracy(void* stream, int B, int n_out, const float* out,
+                       const uint8_t* y_packed, uint8_t* preds_packed, float* acc) {
+    if (B <= 0 || n_out != 8 || !out || !y_packed || !acc) return NC_ERR_INVALID_ARGUMENT;
+    hipLaunchKernelGGL(k_packed_acc, dim3(1), dim3(1024), 0, nc_stream(stream), B, out, y_packed,
+                       preds_packed, acc);
+    NC_CHECK_LAUNCH();
+    return NC_OK;
+}
+
 int nc_adamw_step(void* stream, int n, float* p, const float* g, float* m, float* v,
-                  int32_t* count, const float* lr, float b1, float b2, float eps,
+                  int32_t* count, const float* lr, int n_lr, float b1, float b2, float eps,
                   float weight_decay) {
-    if (n <= 0 || !p || !g || !m || !v || !count || !lr) return NC_ERR_INVALID_ARGUMENT;
+    if (n <= 0 || n_lr <= 0 || !p || !g || !m || !v || !count || !lr)
+        return NC_ERR_INVALID_ARGUMENT;
     hipStream_t st = nc_stream(stream);
     hipLaunchKernelGGL(k_adamw, dim3((n + 255) / 256), dim3(256), 0, st, n, p, g, m, v, count, lr,
-                       b1, b2, eps, weight_decay);
+                       n_lr, b1, b2, eps, weight_decay);
     NC_CHECK_LAUNCH();
     hipLaunchKernelGGL(k_count_inc, dim3(1), dim3(64), 0, st, count);
     NC_CHECK_LAUNCH();

@@ -39,6 +39,63 @@ NC_DEV float nc_act(float x, int act, float neg_slope) {
     }
 }
 
+// Compile-time activation: kernels are instantiated per activation so the hot loops carry
+// no per-element dispatch.
+template <int ACT>
+NC_DEV float act_f(float x, float neg_slope) {
+    if constexpr (ACT == NC_ACT_TANH) return tanhf(x);
+    else if constexpr (ACT == NC_ACT_SIGMOID) return nc_sigmoid(x);
+    else if constexpr (ACT == NC_ACT_RELU) return fmaxf(x, 0.0f);
+    else if constexpr (ACT == NC_ACT_LEAKY_RELU) return x >= 0.0f ? x : neg_slope * x;
+    else if constexpr (ACT == NC_ACT_GELU) {
+        const float c = 0.7978845608028654f;
+        return 0.5f * x * (1.0f + tanhf(c * (x + 0.044715f * x * x * x)));
+    } else return x;
+}
+
+template <int ACT>
+NC_DEV float act_fd(float x, float neg_slope, float* y) {
+    if constexpr (ACT == NC_ACT_TANH) {
+        const float t = tanhf(x);
+        *y = t;
+        return 1.0f - t * t;
+    } else if constexpr (ACT == NC_ACT_SIGMOID) {
+        const float s = nc_sigmoid(x);
+        *y = s;
+        return s * (1.0f - s);
+    } else if constexpr (ACT == NC_ACT_RELU) {
+        *y = fmaxf(x, 0.0f);
+        return x > 0.0f ? 1.0f : 0.0f;
+    } else if constexpr (ACT == NC_ACT_LEAKY_RELU) {
+        *y = x >= 0.0f ? x : neg_slope * x;
+        return x >= 0.0f ? 1.0f : neg_slope;
+    } else if constexpr (ACT == NC_ACT_GELU) {
+        const float c = 0.7978845608028654f;
+        const float x2 = x * x;
+        const float th = tanhf(c * (x + 0.044715f * x2 * x));
+        const float du = c * (1.0f + 3.0f * 0.044715f * x2);
+        *y = 0.5f * x * (1.0f + th);
+        return 0.5f * (1.0f + th) + 0.5f * x * (1.0f - th * th) * du;
+    } else {
+        *y = x;
+        return 1.0f;
+    }
+}
+
+// Runs `f.template operator()<ACT>()` for the runtime activation id (host-side dispatch).
+template <class F>
+inline int dispatch_act(int act, F&& f) {
+    switch (act) {
+        case NC_ACT_IDENTITY: return f.template operator()<NC_ACT_IDENTITY>();
+        case NC_ACT_TANH: return f.template operator()<NC_ACT_TANH>();
+        case NC_ACT_SIGMOID: return f.template operator()<NC_ACT_SIGMOID>();
+        case NC_ACT_RELU: return f.template operator()<NC_ACT_RELU>();
+        case NC_ACT_LEAKY_RELU: return f.template operator()<NC_ACT_LEAKY_RELU>();
+        case NC_ACT_GELU: return f.template operator()<NC_ACT_GELU>();
+        default: return NC_ERR_INVALID_ARGUMENT;
+    }
+}
+
 // Value and derivative together.
 NC_DEV float nc_act_d(float x, int act, float neg_slope, float* y) {
     switch (act) {
@@ -99,24 +156,31 @@ NC_DEV float wave_sum(float v) {
     return v;
 }
 
-// Sums K values per thread across the workgroup; `red` must hold K * (blockDim.x / 64) floats.
-// On return vals[k] holds the workgroup total for every thread.  Contains two barriers.
-template <int K>
+// Sums K values per thread across a workgroup of NT threads; `red` must hold K * NT/64
+// floats.  Wave totals go to LDS, then thread k < K sums the NT/64 wave totals of value k in
+// fixed order and publishes it.  On return vals[k] is the workgroup total in every thread.
+// Contains two barriers.
+template <int K, int NT>
 NC_DEV void block_sum(float* vals, float* red) {
+    constexpr int NW = NT / NC_WAVE;
+    static_assert(NW * NC_WAVE == NT, "workgroup must be whole waves");
     const int lane = threadIdx.x & (NC_WAVE - 1);
     const int wave = threadIdx.x >> 6;
-    const int nwave = (blockDim.x + NC_WAVE - 1) >> 6;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
         float s = wave_sum(vals[k]);
-        if (lane == 0) red[k * nwave + wave] = s;
+        if (lane == 0) red[k * NW + wave] = s;
+    }
+    __syncthreads();
+    if (threadIdx.x < K) {
+        const int k = threadIdx.x;
+        float s = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) s += red[k * NW + w];
+        red[K * NW + k] = s;
     }
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-        float s = 0.0f;
-        for (int w = 0; w < nwave; ++w) s += red[k * nwave + w];
-        vals[k] = s;
-    }
-    __syncthreads();
+    for (int k = 0; k < K; ++k) vals[k] = red[K * NW + k];
+    __syncthreads();  // red may be reused right away
 }

@@ -27,8 +27,8 @@ constexpr int kMaxM = 64;
 // Single-pass forward: one workgroup per sample.
 // ----------------------------------------------------------------------------------------
 
-template <int NT, int PPT, int MC>
-__global__ __launch_bounds__(NT) void k_epi_fwd(int M, int N, int act, float slope, int hb,
+template <int NT, int PPT, int MC, int ACT>
+__global__ __launch_bounds__(NT) void k_epi_fwd(int M, int N, float slope, int hb,
                                                 const float* __restrict__ z,
                                                 const float* __restrict__ delta,
                                                 const float* __restrict__ w,
@@ -36,7 +36,7 @@ __global__ __launch_bounds__(NT) void k_epi_fwd(int M, int N, int act, float slo
                                                 const float* __restrict__ bb,
                                                 float* __restrict__ out, float* __restrict__ mean,
                                                 float* __restrict__ rstd) {
-    __shared__ float red[MC * (NT / 64)];
+    __shared__ float red[MC * (NT / 64) + MC];
     const int b = blockIdx.x, tid = threadIdx.x;
     const float inv_n = 1.0f / (float)N;
     float lin[PPT], ac[PPT], bv[PPT];
@@ -45,28 +45,30 @@ __global__ __launch_bounds__(NT) void k_epi_fwd(int M, int N, int act, float slo
         const int p = tid + k * NT;
         lin[k] = 0.f;
         ac[k] = 0.f;
-        bv[k] = p < N ? bb[p] : 0.f;
+        bv[k] = bb[min(p, N - 1)];
     }
     for (int m0 = 0; m0 < M; m0 += MC) {
         float zt[MC][PPT];
         float sum[MC];
+        // unconditional (clamped) loads keep all MC*PPT requests in flight together
 #pragma unroll
         for (int q = 0; q < MC; ++q) {
-            const int m = m0 + q;
+            const int m = min(m0 + q, M - 1);
             sum[q] = 0.f;
 #pragma unroll
             for (int k = 0; k < PPT; ++k) {
-                const int p = tid + k * NT;
-                float v = 0.f;
-                if (m < M && p < N) {
-                    v = z[((size_t)b * M + m) * N + p];
-                    if (hb) v += delta[(size_t)m * N + p];
-                }
+                const int pc = min(tid + k * NT, N - 1);
+                float v = z[((size_t)b * M + m) * N + pc];
+                if (hb) v += delta[(size_t)m * N + pc];
                 zt[q][k] = v;
-                sum[q] += v;
             }
         }
-        block_sum<MC>(sum, red);
+#pragma unroll
+        for (int q = 0; q < MC; ++q)
+#pragma unroll
+            for (int k = 0; k < PPT; ++k)
+                sum[q] += (m0 + q < M && tid + k * NT < N) ? zt[q][k] : 0.f;
+        block_sum<MC, NT>(sum, red);
         float mu[MC], sq[MC];
 #pragma unroll
         for (int q = 0; q < MC; ++q) {
@@ -74,12 +76,11 @@ __global__ __launch_bounds__(NT) void k_epi_fwd(int M, int N, int act, float slo
             sq[q] = 0.f;
 #pragma unroll
             for (int k = 0; k < PPT; ++k) {
-                const int p = tid + k * NT;
-                const float d = p < N ? zt[q][k] - mu[q] : 0.f;
+                const float d = tid + k * NT < N ? zt[q][k] - mu[q] : 0.f;
                 sq[q] += d * d;
             }
         }
-        block_sum<MC>(sq, red);
+        block_sum<MC, NT>(sq, red);
 #pragma unroll
         for (int q = 0; q < MC; ++q) {
             const int m = m0 + q;
@@ -89,7 +90,7 @@ __global__ __launch_bounds__(NT) void k_epi_fwd(int M, int N, int act, float slo
             for (int k = 0; k < PPT; ++k) {
                 const float zn = (zt[q][k] - mu[q]) * r;
                 lin[k] += zn;
-                ac[k] += nc_act(zn + bv[k], act, slope);
+                ac[k] += act_f<ACT>(zn + bv[k], slope);
             }
             if (tid == 0) {
                 mean[(size_t)b * M + m] = mu[q];
@@ -108,25 +109,26 @@ __global__ __launch_bounds__(NT) void k_epi_fwd(int M, int N, int act, float slo
 // Single-pass backward: gz, per-sample partial gw/gs/gb (reduced over B afterwards).
 // ----------------------------------------------------------------------------------------
 
-template <int NT, int PPT, int MC>
+template <int NT, int PPT, int MC, int ACT>
 __global__ __launch_bounds__(NT) void k_epi_bwd(
-    int M, int N, int act, float slope, int hb, const float* __restrict__ z,
+    int M, int N, float slope, int hb, const float* __restrict__ z,
     const float* __restrict__ delta, const float* __restrict__ w, const float* __restrict__ s,
     const float* __restrict__ bb, const float* __restrict__ mean, const float* __restrict__ rstd,
     const float* __restrict__ gy, float* __restrict__ gz, float* __restrict__ pg) {
-    __shared__ float red[2 * MC * (NT / 64)];
+    __shared__ float red[2 * MC * (NT / 64) + 2 * MC];
     const int b = blockIdx.x, tid = threadIdx.x;
     const float inv_n = 1.0f / (float)N;
     float lin[PPT], ac[PPT], dbs[PPT], bv[PPT], wv[PPT], sv[PPT], g[PPT];
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
         const int p = tid + k * NT;
+        const int pc = min(p, N - 1);
         const bool in = p < N;
         lin[k] = ac[k] = dbs[k] = 0.f;
-        bv[k] = in ? bb[p] : 0.f;
-        wv[k] = in ? w[p] : 0.f;
-        sv[k] = in ? s[p] : 0.f;
-        g[k] = in ? gy[(size_t)b * N + p] : 0.f;
+        bv[k] = bb[pc];
+        wv[k] = w[pc];
+        sv[k] = s[pc];
+        g[k] = in ? gy[(size_t)b * N + pc] : 0.f;  // zero cotangent outside the plane
     }
     for (int m0 = 0; m0 < M; m0 += MC) {
         float zn[MC][PPT], gzn[MC][PPT];
@@ -134,22 +136,28 @@ __global__ __launch_bounds__(NT) void k_epi_bwd(
         float mr[MC], rr[MC];
 #pragma unroll
         for (int q = 0; q < MC; ++q) {
-            const int m = m0 + q;
-            const bool mv = m < M;
-            mr[q] = mv ? mean[(size_t)b * M + m] : 0.f;
-            rr[q] = mv ? rstd[(size_t)b * M + m] : 0.f;
+            const int m = min(m0 + q, M - 1);
+            mr[q] = mean[(size_t)b * M + m];
+            rr[q] = rstd[(size_t)b * M + m];
+#pragma unroll
+            for (int k = 0; k < PPT; ++k) {
+                const int pc = min(tid + k * NT, N - 1);
+                float v = z[((size_t)b * M + m) * N + pc];
+                if (hb) v += delta[(size_t)m * N + pc];
+                zn[q][k] = v;
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < MC; ++q) {
+            const bool mv = m0 + q < M;
             c[q] = c[MC + q] = 0.f;
 #pragma unroll
             for (int k = 0; k < PPT; ++k) {
-                const int p = tid + k * NT;
-                float v = 0.f, gn = 0.f, nz = 0.f;
-                if (mv && p < N) {
-                    v = z[((size_t)b * M + m) * N + p];
-                    if (hb) v += delta[(size_t)m * N + p];
-                    nz = (v - mr[q]) * rr[q];
-                    float a;
-                    const float da = nc_act_d(nz + bv[k], act, slope, &a);
-                    gn = g[k] * (wv[k] + sv[k] * da);
+                const float nz = (zn[q][k] - mr[q]) * rr[q];
+                float a;
+                const float da = act_fd<ACT>(nz + bv[k], slope, &a);
+                const float gn = mv ? g[k] * (wv[k] + sv[k] * da) : 0.f;
+                if (mv) {
                     lin[k] += nz;
                     ac[k] += a;
                     dbs[k] += sv[k] * g[k] * da;
@@ -160,7 +168,7 @@ __global__ __launch_bounds__(NT) void k_epi_bwd(
                 c[MC + q] += gn * nz;
             }
         }
-        block_sum<2 * MC>(c, red);
+        block_sum<2 * MC, NT>(c, red);
 #pragma unroll
         for (int q = 0; q < MC; ++q) {
             const int m = m0 + q;
@@ -186,25 +194,40 @@ __global__ __launch_bounds__(NT) void k_epi_bwd(
     }
 }
 
-// out[r*X + x] = (acc ? out : 0) + sum_b in[(r*B + b)*X + x]  (fixed order over b)
-__global__ void k_batch_reduce(int R, int B, int X, const float* __restrict__ in,
-                               float* __restrict__ out, int accumulate) {
-    const int x = blockIdx.x * blockDim.x + threadIdx.x;
+// out[r*X + x] = (acc ? out : 0) + sum_b in[(r*B + b)*X + x].  Each workgroup owns 64
+// columns; its 16 waves sum fixed contiguous slices of the batch (coalesced rows) and the
+// 16 slice sums are added in fixed order, so the result is deterministic.
+constexpr int kRedParts = 16;
+__global__ __launch_bounds__(64 * kRedParts) void k_batch_reduce(int R, int B, int X,
+                                                                const float* __restrict__ in,
+                                                                float* __restrict__ out,
+                                                                int accumulate) {
+    __shared__ float part[kRedParts][64];
+    const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
+    const int x = blockIdx.x * 64 + lane;
     const int r = blockIdx.y;
-    if (x >= X) return;
-    const float* src = in + (size_t)r * B * X + x;
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-    int b = 0;
-    for (; b + 4 <= B; b += 4) {
-        a0 += src[(size_t)b * X];
-        a1 += src[(size_t)(b + 1) * X];
-        a2 += src[(size_t)(b + 2) * X];
-        a3 += src[(size_t)(b + 3) * X];
+    const int b0 = (B * q) / kRedParts, b1 = (B * (q + 1)) / kRedParts;
+    float s = 0.f;
+    if (x < X) {
+        const float* src = in + (size_t)r * B * X + x;
+        float a0 = 0.f, a1 = 0.f;
+        int b = b0;
+        for (; b + 2 <= b1; b += 2) {
+            a0 += src[(size_t)b * X];
+            a1 += src[(size_t)(b + 1) * X];
+        }
+        if (b < b1) a0 += src[(size_t)b * X];
+        s = a0 + a1;
     }
-    for (; b < B; ++b) a0 += src[(size_t)b * X];
-    const float t = (a0 + a1) + (a2 + a3);
-    float* o = out + (size_t)r * X + x;
-    *o = accumulate ? *o + t : t;
+    part[q][lane] = s;
+    __syncthreads();
+    if (q == 0 && x < X) {
+        float t = 0.f;
+#pragma unroll
+        for (int k = 0; k < kRedParts; ++k) t += part[k][lane];
+        float* o = out + (size_t)r * X + x;
+        *o = accumulate ? *o + t : t;
+    }
 }
 
 // ----------------------------------------------------------------------------------------
@@ -219,7 +242,7 @@ __global__ __launch_bounds__(kTileNT) void k_tile_stats(int M, int N, int T, int
                                                         const float* __restrict__ z,
                                                         const float* __restrict__ delta,
                                                         float* __restrict__ stats) {
-    __shared__ float red[kTileNT / 64];
+    __shared__ float red[kTileNT / 64 + 1];
     const int t = blockIdx.x, m = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
     const int base = t * kTileN;
     const int nt = min(kTileN, N - base);
@@ -236,7 +259,7 @@ __global__ __launch_bounds__(kTileNT) void k_tile_stats(int M, int N, int T, int
         v[k] = x;
         s1 += x;
     }
-    block_sum<1>(&s1, red);
+    block_sum<1, kTileNT>(&s1, red);
     const float mu = s1 / (float)nt;
     float m2 = 0.f;
 #pragma unroll
@@ -245,7 +268,7 @@ __global__ __launch_bounds__(kTileNT) void k_tile_stats(int M, int N, int T, int
         const float d = i < nt ? v[k] - mu : 0.f;
         m2 += d * d;
     }
-    block_sum<1>(&m2, red);
+    block_sum<1, kTileNT>(&m2, red);
     if (tid == 0) {
         const size_t BMT = (size_t)gridDim.z * M * T;
         const size_t o = ((size_t)b * M + m) * T + t;
@@ -273,8 +296,9 @@ NC_DEV void chan_combine(const float* stats, size_t BMT, int b, int m, int M, in
 }
 
 // Per-(tile, b): statistics from the Chan partials, then standardise + Codd + sum over M.
-__global__ __launch_bounds__(kTileNT) void k_tile_fwd(int B, int M, int N, int T, int act,
-                                                      float slope, int hb,
+template <int ACT>
+__global__ __launch_bounds__(kTileNT) void k_tile_fwd(int B, int M, int N, int T, float slope,
+                                                      int hb,
                                                       const float* __restrict__ z,
                                                       const float* __restrict__ delta,
                                                       const float* __restrict__ w,
@@ -312,7 +336,7 @@ __global__ __launch_bounds__(kTileNT) void k_tile_fwd(int B, int M, int N, int T
             if (hb) v += delta[(size_t)m * N + p];
             const float zn = (v - smu[m]) * srs[m];
             lin += zn;
-            ac += nc_act(zn + bvv, act, slope);
+            ac += act_f<ACT>(zn + bvv, slope);
         }
         out[(size_t)b * N + p] = w[p] * lin + s[p] * ac;
     }
@@ -320,12 +344,13 @@ __global__ __launch_bounds__(kTileNT) void k_tile_fwd(int B, int M, int N, int T
 
 // Backward stage 1 per (tile, b): per-tile partial c1/c2 (layout (2, B, M, T)) and the
 // per-sample gw/gs/gb partials pg (3, B, N).
+template <int ACT>
 __global__ __launch_bounds__(kTileNT) void k_tile_bwd1(
-    int B, int M, int N, int T, int act, float slope, int hb, const float* __restrict__ z,
+    int B, int M, int N, int T, float slope, int hb, const float* __restrict__ z,
     const float* __restrict__ delta, const float* __restrict__ w, const float* __restrict__ s,
     const float* __restrict__ bb, const float* __restrict__ mean, const float* __restrict__ rstd,
     const float* __restrict__ gy, float* __restrict__ cpart, float* __restrict__ pg) {
-    __shared__ float red[2 * (kTileNT / 64)];
+    __shared__ float red[2 * (kTileNT / 64) + 2];
     const int t = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
     const int base = t * kTileN;
     const int nt = min(kTileN, N - base);
@@ -355,7 +380,7 @@ __global__ __launch_bounds__(kTileNT) void k_tile_bwd1(
             if (hb) v += delta[(size_t)m * N + p];
             const float zn = (v - mu) * r;
             float a;
-            const float da = nc_act_d(zn + bv[k], act, slope, &a);
+            const float da = act_fd<ACT>(zn + bv[k], slope, &a);
             const float gn = g[k] * (wv[k] + sv[k] * da);
             lin[k] += zn;
             ac[k] += a;
@@ -363,7 +388,7 @@ __global__ __launch_bounds__(kTileNT) void k_tile_bwd1(
             c[0] += gn;
             c[1] += gn * zn;
         }
-        block_sum<2>(c, red);
+        block_sum<2, kTileNT>(c, red);
         if (tid == 0) {
             const size_t o = ((size_t)b * M + m) * T + t;
             cpart[o] = c[0];
@@ -383,8 +408,9 @@ __global__ __launch_bounds__(kTileNT) void k_tile_bwd1(
 }
 
 // Backward stage 2 per (tile, m, b): gz = rstd * (gzn - c1 - zn * c2).
+template <int ACT>
 __global__ __launch_bounds__(kTileNT) void k_tile_bwd2(
-    int B, int M, int N, int T, int act, float slope, int hb, const float* __restrict__ z,
+    int B, int M, int N, int T, float slope, int hb, const float* __restrict__ z,
     const float* __restrict__ delta, const float* __restrict__ w, const float* __restrict__ s,
     const float* __restrict__ bb, const float* __restrict__ mean, const float* __restrict__ rstd,
     const float* __restrict__ gy, const float* __restrict__ cpart, float* __restrict__ gz) {
@@ -411,7 +437,7 @@ __global__ __launch_bounds__(kTileNT) void k_tile_bwd2(
         if (hb) v += delta[(size_t)m * N + p];
         const float zn = (v - mu) * r;
         float a;
-        const float da = nc_act_d(zn + bb[p], act, slope, &a);
+        const float da = act_fd<ACT>(zn + bb[p], slope, &a);
         const float gn = gy[(size_t)b * N + p] * (w[p] + s[p] * da);
         gz[((size_t)b * M + m) * N + p] = r * (gn - c1 - zn * c2);
     }
@@ -445,7 +471,7 @@ NC_DEV void plane_stats(int b, int M, int N, int hb, const float* __restrict__ z
                 sum[q] += v;
             }
         }
-        block_sum<MC>(sum, red);
+        block_sum<MC, NT>(sum, red);
 #pragma unroll
         for (int q = 0; q < MC; ++q) {
             sq[q] = 0.f;
@@ -457,7 +483,7 @@ NC_DEV void plane_stats(int b, int M, int N, int hb, const float* __restrict__ z
                 sq[q] += d * d;
             }
         }
-        block_sum<MC>(sq, red);
+        block_sum<MC, NT>(sq, red);
         if (tid == 0) {
 #pragma unroll
             for (int q = 0; q < MC; ++q)
@@ -487,6 +513,7 @@ NC_DEV void port_gather(int b, int M, int N, int P, int hb, int fact, float slop
         szo[q] = zn;
         zo[(size_t)b * M * P + q] = zn;
     }
+    if (!pp) return;  // standardisation only (uniform across the block)
     __syncthreads();
     for (int k = tid; k < P; k += nt) {
         const float wo = pp[k], so = pp[P + k], bo = pp[2 * P + k];
@@ -520,7 +547,7 @@ __global__ __launch_bounds__(NT) void k_port_fwd(int M, int N, int P, int hb, in
                                                  float* __restrict__ pre) {
     HIP_DYNAMIC_SHARED(float, szo)  // M*P
     __shared__ float smu[kMaxM], srs[kMaxM];
-    __shared__ float red[MC * (NT / 64)];
+    __shared__ float red[MC * (NT / 64) + MC];
     const int b = blockIdx.x;
     plane_stats<NT, PPT, MC>(b, M, N, hb, z, delta, smu, srs, red);
     for (int m = threadIdx.x; m < M; m += NT) {
@@ -571,8 +598,13 @@ __global__ __launch_bounds__(256) void k_port_bwd(
     const int t = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, nt = blockDim.x;
     const int B = gridDim.y;
     const float* zob = zo + (size_t)b * M * P;
-    // 1. port cotangents
+    // 1. port cotangents (given directly as (B,M,P) in standardisation-only mode)
     for (int q = tid; q < M * P; q += nt) {
+        gsum[q] = 0.f;
+        if (!pp) {
+            gzo[q] = gout[(size_t)b * M * P + q];
+            continue;
+        }
         const int m = q / P, k = q % P;
         const float wo = pp[k], so = pp[P + k], bo = pp[2 * P + k];
         const float go = gout[(size_t)b * P + k];
@@ -585,7 +617,6 @@ __global__ __launch_bounds__(256) void k_port_bwd(
             v = gp * (wo + so * nc_act_d(zob[q] + bo, fact, slope, &a));
         }
         gzo[q] = v;
-        gsum[q] = 0.f;
     }
     for (int m = tid; m < M; m += nt) {
         smu[m] = mean[(size_t)b * M + m];
@@ -636,7 +667,7 @@ __global__ __launch_bounds__(256) void k_port_bwd(
         }
     }
     // 4. per-sample port-parameter partials
-    if (t == 0) {
+    if (t == 0 && pp) {
         for (int k = tid; k < P; k += nt) {
             const float wo = pp[k], so = pp[P + k], bo = pp[2 * P + k];
             const float go = gout[(size_t)b * P + k];
@@ -695,16 +726,29 @@ int tiles_of(int N) { return (N + kTileN - 1) / kTileN; }
 
 // Forward-style kernels keep MC=16 directions of PPT pixels in registers; the backward keeps
 // two such tiles (zhat and its cotangent), so it runs MC=8.
-#define NC_SINGLE_DISPATCH(N_, MCF, KER, ...)                                               \
-    do {                                                                                    \
-        SingleCfg c_ = single_cfg(N_);                                                      \
-        if (c_.nt == 256 && c_.ppt == 1) hipLaunchKernelGGL((KER<256, 1, MCF>), __VA_ARGS__); \
-        else if (c_.nt == 256 && c_.ppt == 2) hipLaunchKernelGGL((KER<256, 2, MCF>), __VA_ARGS__); \
-        else if (c_.nt == 256 && c_.ppt == 3) hipLaunchKernelGGL((KER<256, 3, MCF>), __VA_ARGS__); \
-        else if (c_.nt == 256 && c_.ppt == 4) hipLaunchKernelGGL((KER<256, 4, MCF>), __VA_ARGS__); \
-        else if (c_.nt == 512) hipLaunchKernelGGL((KER<512, 4, MCF>), __VA_ARGS__);          \
-        else if (c_.ppt == 4) hipLaunchKernelGGL((KER<1024, 4, MCF>), __VA_ARGS__);          \
-        else hipLaunchKernelGGL((KER<1024, 8, 8>), __VA_ARGS__);                           \
+#define NC_SINGLE_DISPATCH(N_, MCF, KER, ...)                                                    \
+    do {                                                                                         \
+        SingleCfg c_ = single_cfg(N_);                                                           \
+        if (c_.nt == 256 && c_.ppt == 1) hipLaunchKernelGGL((KER<256, 1, MCF, ACT>), __VA_ARGS__); \
+        else if (c_.nt == 256 && c_.ppt == 2) hipLaunchKernelGGL((KER<256, 2, MCF, ACT>), __VA_ARGS__); \
+        else if (c_.nt == 256 && c_.ppt == 3) hipLaunchKernelGGL((KER<256, 3, MCF, ACT>), __VA_ARGS__); \
+        else if (c_.nt == 256 && c_.ppt == 4) hipLaunchKernelGGL((KER<256, 4, MCF, ACT>), __VA_ARGS__); \
+        else if (c_.nt == 512) hipLaunchKernelGGL((KER<512, 4, MCF, ACT>), __VA_ARGS__);          \
+        else if (c_.ppt == 4) hipLaunchKernelGGL((KER<1024, 4, MCF, ACT>), __VA_ARGS__);          \
+        else hipLaunchKernelGGL((KER<1024, 8, 8, ACT>), __VA_ARGS__);                           \
+    } while (0)
+
+// The port forward has no per-pixel activation: its template slot is a placeholder.
+#define NC_PORT_DISPATCH(N_, KER, ...)                                                           \
+    do {                                                                                         \
+        SingleCfg c_ = single_cfg(N_);                                                           \
+        if (c_.nt == 256 && c_.ppt == 1) hipLaunchKernelGGL((KER<256, 1, 16>), __VA_ARGS__);      \
+        else if (c_.nt == 256 && c_.ppt == 2) hipLaunchKernelGGL((KER<256, 2, 16>), __VA_ARGS__); \
+        else if (c_.nt == 256 && c_.ppt == 3) hipLaunchKernelGGL((KER<256, 3, 16>), __VA_ARGS__); \
+        else if (c_.nt == 256 && c_.ppt == 4) hipLaunchKernelGGL((KER<256, 4, 16>), __VA_ARGS__); \
+        else if (c_.nt == 512) hipLaunchKernelGGL((KER<512, 4, 16>), __VA_ARGS__);               \
+        else if (c_.ppt == 4) hipLaunchKernelGGL((KER<1024, 4, 16>), __VA_ARGS__);               \
+        else hipLaunchKernelGGL((KER<1024, 8, 8>), __VA_ARGS__);                                \
     } while (0)
 
 }  // namespace
@@ -731,10 +775,12 @@ int nc_epilogue_fwd(void* stream, int B, int M, int h, int w, int act, float neg
     hipStream_t st = nc_stream(stream);
     const int N = h * w;
     if (N <= kSingleMaxPix) {
-        NC_SINGLE_DISPATCH(N, 16, k_epi_fwd, dim3(B), dim3(c_.nt), 0, st, M, N, act, neg_slope,
-                           has_border, z, delta, w_eff, s_eff, b_roi, out, mean, rstd);
-        NC_CHECK_LAUNCH();
-        return NC_OK;
+        return dispatch_act(act, [&]<int ACT>() {
+            NC_SINGLE_DISPATCH(N, 16, k_epi_fwd, dim3(B), dim3(c_.nt), 0, st, M, N, neg_slope,
+                               has_border, z, delta, w_eff, s_eff, b_roi, out, mean, rstd);
+            NC_CHECK_LAUNCH();
+            return NC_OK;
+        });
     }
     if (ws_bytes < nc_epilogue_workspace_size(B, M, h, w) || !ws) return NC_ERR_WORKSPACE;
     const int T = tiles_of(N);
@@ -742,11 +788,13 @@ int nc_epilogue_fwd(void* stream, int B, int M, int h, int w, int act, float neg
     hipLaunchKernelGGL(k_tile_stats, dim3(T, M, B), dim3(kTileNT), 0, st, M, N, T, has_border,
                        z, delta, stats);
     NC_CHECK_LAUNCH();
-    hipLaunchKernelGGL(k_tile_fwd, dim3(T, B), dim3(kTileNT), 0, st, B, M, N, T, act,
-                       neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, stats, out, mean,
-                       rstd);
-    NC_CHECK_LAUNCH();
-    return NC_OK;
+    return dispatch_act(act, [&]<int ACT>() {
+        hipLaunchKernelGGL((k_tile_fwd<ACT>), dim3(T, B), dim3(kTileNT), 0, st, B, M, N, T,
+                           neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, stats, out,
+                           mean, rstd);
+        NC_CHECK_LAUNCH();
+        return NC_OK;
+    });
 }
 
 int nc_epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg_slope,
@@ -762,32 +810,37 @@ int nc_epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg
     hipStream_t st = nc_stream(stream);
     const int N = h * w;
     float* pg = reinterpret_cast<float*>(ws);
-    if (N <= kSingleMaxPix) {
-        NC_SINGLE_DISPATCH(N, 8, k_epi_bwd, dim3(B), dim3(c_.nt), 0, st, M, N, act, neg_slope,
-                           has_border, z, delta, w_eff, s_eff, b_roi, mean, rstd, gy, gz, pg);
-        NC_CHECK_LAUNCH();
-    } else {
+    int rc = dispatch_act(act, [&]<int ACT>() {
+        if (N <= kSingleMaxPix) {
+            NC_SINGLE_DISPATCH(N, 8, k_epi_bwd, dim3(B), dim3(c_.nt), 0, st, M, N, neg_slope,
+                               has_border, z, delta, w_eff, s_eff, b_roi, mean, rstd, gy, gz,
+                               pg);
+            NC_CHECK_LAUNCH();
+            return NC_OK;
+        }
         const int T = tiles_of(N);
         float* cpart = pg + 3 * (size_t)B * N;
-        hipLaunchKernelGGL(k_tile_bwd1, dim3(T, B), dim3(kTileNT), 0, st, B, M, N, T, act,
+        hipLaunchKernelGGL((k_tile_bwd1<ACT>), dim3(T, B), dim3(kTileNT), 0, st, B, M, N, T,
                            neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, mean, rstd, gy,
                            cpart, pg);
         NC_CHECK_LAUNCH();
-        hipLaunchKernelGGL(k_tile_bwd2, dim3(T, M, B), dim3(kTileNT), 0, st, B, M, N, T, act,
+        hipLaunchKernelGGL((k_tile_bwd2<ACT>), dim3(T, M, B), dim3(kTileNT), 0, st, B, M, N, T,
                            neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, mean, rstd, gy,
                            cpart, gz);
         NC_CHECK_LAUNCH();
-    }
-    // parameter gradients: sum over B of the per-sample partials (gw, gs, gb are 3 rows)
+        return NC_OK;
+    });
+    if (rc != NC_OK) return rc;
+    // parameter gradients: sum over B of the per-sample partials (gw, gs, gb rows)
     float* dst[3] = {gw, gs, gb};
     for (int r = 0; r < 3; ++r) {
-        hipLaunchKernelGGL(k_batch_reduce, dim3((N + 255) / 256, 1), dim3(256), 0, st, 1, B, N,
-                           pg + (size_t)r * B * N, dst[r], accumulate_params);
+        hipLaunchKernelGGL(k_batch_reduce, dim3((N + 63) / 64, 1), dim3(64 * kRedParts), 0, st,
+                           1, B, N, pg + (size_t)r * B * N, dst[r], accumulate_params);
         NC_CHECK_LAUNCH();
     }
     if (has_border) {
-        hipLaunchKernelGGL(k_batch_reduce, dim3((M * N + 255) / 256, 1), dim3(256), 0, st, 1, B,
-                           M * N, gz, gdb, accumulate_gdb);
+        hipLaunchKernelGGL(k_batch_reduce, dim3((M * N + 63) / 64, 1), dim3(64 * kRedParts), 0,
+                           st, 1, B, M * N, gz, gdb, accumulate_gdb);
         NC_CHECK_LAUNCH();
     }
     return NC_OK;
@@ -807,14 +860,14 @@ int nc_port_fwd(void* stream, int B, int M, int h, int w, int has_border, int fi
                 float* mean, float* rstd, float* pre, void* ws, size_t ws_bytes) {
     int rc = port_check(B, M, h, w, n_port, port_idx, z, has_border, delta, final_act);
     if (rc != NC_OK) return rc;
-    if (!port_params || !out || !zo || !mean || !rstd ||
-        (final_act != NC_ACT_IDENTITY && !pre))
+    if (!zo || !mean || !rstd || (port_params && !out) ||
+        (port_params && final_act != NC_ACT_IDENTITY && !pre))
         return NC_ERR_INVALID_ARGUMENT;
     hipStream_t st = nc_stream(stream);
     const int N = h * w;
     const size_t shm = (size_t)M * n_port * sizeof(float);
     if (N <= kSingleMaxPix) {
-        NC_SINGLE_DISPATCH(N, 16, k_port_fwd, dim3(B), dim3(c_.nt), shm, st, M, N, n_port,
+        NC_PORT_DISPATCH(N, k_port_fwd, dim3(B), dim3(c_.nt), shm, st, M, N, n_port,
                            has_border, final_act, neg_slope, port_idx, z, delta, port_params,
                            out, zo, mean, rstd, pre);
         NC_CHECK_LAUNCH();
@@ -841,8 +894,8 @@ int nc_port_bwd(void* stream, int B, int M, int h, int w, int has_border, int fi
                 size_t ws_bytes) {
     int rc = port_check(B, M, h, w, n_port, port_idx, z, has_border, delta, final_act);
     if (rc != NC_OK) return rc;
-    if (!port_params || !zo || !mean || !rstd || !g_out || !gz || !g_port_params ||
-        (has_border && !gdb) || (final_act != NC_ACT_IDENTITY && !pre))
+    if (!zo || !mean || !rstd || !g_out || !gz || (port_params && !g_port_params) ||
+        (has_border && !gdb) || (port_params && final_act != NC_ACT_IDENTITY && !pre))
         return NC_ERR_INVALID_ARGUMENT;
     if (ws_bytes < nc_epilogue_workspace_size(B, M, h, w) || !ws) return NC_ERR_WORKSPACE;
     hipStream_t st = nc_stream(stream);
@@ -854,12 +907,14 @@ int nc_port_bwd(void* stream, int B, int M, int h, int w, int has_border, int fi
                        final_act, neg_slope, port_idx, z, delta, port_params, zo, mean, rstd,
                        pre, g_out, gz, ppart);
     NC_CHECK_LAUNCH();
-    hipLaunchKernelGGL(k_batch_reduce, dim3((n_port + 255) / 256, 3), dim3(256), 0, st, 3, B,
-                       n_port, ppart, g_port_params, accumulate_params);
-    NC_CHECK_LAUNCH();
+    if (port_params) {
+        hipLaunchKernelGGL(k_batch_reduce, dim3((n_port + 63) / 64, 3), dim3(64 * kRedParts), 0,
+                           st, 3, B, n_port, ppart, g_port_params, accumulate_params);
+        NC_CHECK_LAUNCH();
+    }
     if (has_border) {
-        hipLaunchKernelGGL(k_batch_reduce, dim3((M * N + 255) / 256, 1), dim3(256), 0, st, 1, B,
-                           M * N, gz, gdb, accumulate_params);
+        hipLaunchKernelGGL(k_batch_reduce, dim3((M * N + 63) / 64, 1), dim3(64 * kRedParts), 0,
+                           st, 1, B, M * N, gz, gdb, accumulate_params);
         NC_CHECK_LAUNCH();
     }
     return NC_OK;

@@ -126,12 +126,22 @@ NC_DEV void dft_reg(cpx* v) {
     }
 }
 
-// W_N^e from the 256-point table (0 <= e < N).
+// W_N^e from the 256-point table (0 <= e < N); `tw` is the table's LDS copy.
 template <int N, bool INV>
-NC_DEV cpx twiddle(int e) {
-    cpx w = NC_TW256[e * (256 / N)];
+NC_DEV cpx twiddle(int e, const cpx* tw) {
+    cpx w = tw[e * (256 / N)];
     if (INV) w.y = -w.y;
     return w;
+}
+
+// Copies the twiddle table into LDS (256 cpx); callers barrier before first use.
+NC_DEV void load_twiddles(cpx* tw) {
+    for (int i = threadIdx.x; i < NC_TW_N; i += blockDim.x) tw[i] = NC_TW256[i];
+}
+
+// Cooperative, coalesced copy of an (h x w) row-major plane into LDS (as floats).
+NC_DEV void stage_plane(const float* __restrict__ src, int n, float* dst) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) dst[i] = src[i];
 }
 
 // ---------------------------------------------------------------------------------------
@@ -149,13 +159,13 @@ struct GroupFft {
 };
 
 template <int N, bool INV>
-NC_DEV void gfft_stage1(cpx* v, int t, cpx* scr) {
+NC_DEV void gfft_stage1(cpx* v, int t, cpx* scr, const cpx* tw) {
     using F = GroupFft<N>;
     dft_reg<F::E, INV>(v);
 #pragma unroll
     for (int k1 = 0; k1 < F::E; ++k1) {
         cpx y = v[k1];
-        if (k1 > 0) y = cmul(y, twiddle<N, INV>(t * k1));
+        if (k1 > 0) y = cmul(y, twiddle<N, INV>(t * k1, tw));
         scr[k1 * (F::G + 1) + t] = y;
     }
 }
@@ -201,7 +211,8 @@ struct Plane {
 // load(r, c) is called only for r < hin, c < win.  Result: S[kh*SP + kw], kh < FH,
 // kw <= FW/2.  Must be called by all NT threads (contains barriers; ends with one).
 template <int FH, int FW, class Load>
-NC_DEV void plane_rfft2(Load load, int hin, int win, cpx* S, cpx* Zb, cpx* scr) {
+NC_DEV void plane_rfft2(Load load, int hin, int win, cpx* S, cpx* Zb, cpx* scr,
+                        const cpx* tw) {
     using P = Plane<FH, FW>;
     constexpr int EW = P::GW::E, GW = P::GW::G, EH = P::GH::E, GH = P::GH::G;
     constexpr int SP = P::SP;
@@ -226,7 +237,7 @@ NC_DEV void plane_rfft2(Load load, int hin, int win, cpx* S, cpx* Zb, cpx* scr) 
                 }
                 v[n1] = cmk(a, b);
             }
-            gfft_stage1<FW, false>(v, t, scr + g * P::GW::SCR);
+            gfft_stage1<FW, false>(v, t, scr + g * P::GW::SCR, tw);
         }
         __syncthreads();
         if (on) {
@@ -263,7 +274,7 @@ NC_DEV void plane_rfft2(Load load, int hin, int win, cpx* S, cpx* Zb, cpx* scr) 
                 }
                 v[n1] = val;
             }
-            gfft_stage1<FH, false>(v, t, scr + g * P::GH::SCR);
+            gfft_stage1<FH, false>(v, t, scr + g * P::GH::SCR, tw);
         }
         __syncthreads();
         if (on) {
@@ -307,7 +318,7 @@ NC_DEV void plane_rfft2(Load load, int hin, int win, cpx* S, cpx* Zb, cpx* scr) 
 // (contains barriers; ends with one).
 template <int FH, int FW, class Spec, class Store>
 NC_DEV void plane_irfft2(Spec spec, int row0, int hout, int col0, int wout, float scale,
-                         Store store, cpx* Tb, cpx* scr) {
+                         Store store, cpx* Tb, cpx* scr, const cpx* tw) {
     using P = Plane<FH, FW>;
     constexpr int EW = P::GW::E, GW = P::GW::G, EH = P::GH::E, GH = P::GH::G;
     constexpr int SP = P::SP;
@@ -330,7 +341,7 @@ NC_DEV void plane_irfft2(Spec spec, int row0, int hout, int col0, int wout, floa
                     v[n1] = spec(kh, kw);
                 }
             }
-            gfft_stage1<FH, true>(v, t, scr + g * P::GH::SCR);
+            gfft_stage1<FH, true>(v, t, scr + g * P::GH::SCR, tw);
         }
         __syncthreads();
         if (on) {
@@ -375,7 +386,7 @@ NC_DEV void plane_irfft2(Spec spec, int row0, int hout, int col0, int wout, floa
                 }
                 v[n1] = cadd(a, cmul_i(b));
             }
-            gfft_stage1<FW, true>(v, t, scr + g * P::GW::SCR);
+            gfft_stage1<FW, true>(v, t, scr + g * P::GW::SCR, tw);
         }
         __syncthreads();
         if (on) {

@@ -23,7 +23,13 @@ struct Smem {
     using P = Plane<FH, FW>;
     cpx work[P::WORK];
     cpx scr[P::SCRN];
+    cpx tw[NC_TW_N];
 };
+
+// Every kernel starts by copying the twiddle table into LDS.
+#define NC_SPECTRAL_PROLOGUE(sm) \
+    load_twiddles(sm.tw);        \
+    __syncthreads()
 
 // ----------------------------------------------------------------------------------------
 // Filter spectrum (kernels_greens.py:240-259) and its backward (kernels_pallas.py:1558-1579)
@@ -35,11 +41,12 @@ __global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_filter_spectrum_fwd(
     using P = Plane<FH, FW>;
     __shared__ cpx S[P::F];
     __shared__ Smem<FH, FW> sm;
+    NC_SPECTRAL_PROLOGUE(sm);
     const int m = blockIdx.x;
     const float* g = filt + (size_t)m * kh * kw;
     // flipped filter: x[r][c] = G[kh-1-r][kw-1-c]
     plane_rfft2<FH, FW>([&](int r, int c) { return g[(kh - 1 - r) * kw + (kw - 1 - c)]; },
-                        kh, kw, S, sm.work, sm.scr);
+                        kh, kw, S, sm.work, sm.scr, sm.tw);
     for (int e = threadIdx.x; e < P::F; e += P::NT) ghat[(size_t)m * P::F + e] = S[e];
 }
 
@@ -49,6 +56,7 @@ __global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_filter_spectrum_bwd(
     float* __restrict__ gfilt, int accumulate, int conj_in) {
     using P = Plane<FH, FW>;
     __shared__ Smem<FH, FW> sm;
+    NC_SPECTRAL_PROLOGUE(sm);
     const int m = blockIdx.x;
     const cpx* d = dghat + (size_t)m * P::F;
     float* out = gfilt + (size_t)m * kh * kw;
@@ -59,13 +67,12 @@ __global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_filter_spectrum_bwd(
             cpx v = d[a * P::SP + b];
             return conj_in ? cconj(v) : v;
         },
-        row0, kh, col0, kw,
-        1.0f / (float)(FH * FW),
+        row0, kh, col0, kw, 1.0f / (float)(FH * FW),
         [&](int i, int j, float v) {
             float* o = out + (kh - 1 - i) * kw + (kw - 1 - j);
             *o = accumulate ? *o + v : v;
         },
-        sm.work, sm.scr);
+        sm.work, sm.scr, sm.tw);
 }
 
 // ----------------------------------------------------------------------------------------
@@ -81,12 +88,17 @@ __global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_fftconv_fwd(
     __shared__ cpx S[P::F];
     __shared__ Smem<FH, FW> sm;
     __shared__ float O[FH * FW];
+    NC_SPECTRAL_PROLOGUE(sm);
     const int b = blockIdx.x;
     const int m0 = blockIdx.y * mc;
     const int m1 = min(M, m0 + mc);
-    const float* xb = x + (size_t)b * hin * win;
-    plane_rfft2<FH, FW>([&](int r, int c) { return xb[r * win + c]; }, hin, win, S, sm.work,
-                        sm.scr);
+    // stage the sample's plane (coalesced) into S, which the row pass reads before the
+    // column pass overwrites it with the spectrum
+    float* Sf = reinterpret_cast<float*>(S);
+    stage_plane(x + (size_t)b * hin * win, hin * win, Sf);
+    __syncthreads();
+    plane_rfft2<FH, FW>([&](int r, int c) { return Sf[r * win + c]; }, hin, win, S, sm.work,
+                        sm.scr, sm.tw);
     if (xhat != nullptr && blockIdx.y == 0)
         for (int e = threadIdx.x; e < P::F; e += P::NT) xhat[(size_t)b * P::F + e] = S[e];
     const int npix = hout * wout;
@@ -96,7 +108,7 @@ __global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_fftconv_fwd(
         plane_irfft2<FH, FW>(
             [&](int a, int c) { return cmul(S[a * P::SP + c], G[a * P::SP + c]); }, ph, hout,
             pw, wout, scale, [&](int i, int j, float v) { O[i * wout + j] = v; }, sm.work,
-            sm.scr);
+            sm.scr, sm.tw);
         float* zo = z + ((size_t)b * M + m) * npix;
         for (int e = threadIdx.x; e < npix; e += P::NT) zo[e] = O[e];
         // O is rewritten only after the next inverse's column phase barriers.
@@ -116,20 +128,22 @@ __global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_fftconv_bwd_dx(
     __shared__ cpx S[P::F];
     __shared__ cpx A[P::F];
     __shared__ Smem<FH, FW> sm;
+    NC_SPECTRAL_PROLOGUE(sm);
     const int b = blockIdx.x;
     const int m0 = blockIdx.y * ms_size;
     const int m1 = min(M, m0 + ms_size);
     const int npix = hout * wout;
+    float* Sf = reinterpret_cast<float*>(S);
     for (int e = threadIdx.x; e < P::F; e += P::NT) A[e] = cmk(0.f, 0.f);
     for (int m = m0; m < m1; ++m) {
-        const float* g = gz + ((size_t)b * M + m) * npix;
-        plane_rfft2<FH, FW>([&](int r, int c) { return g[r * wout + c]; }, hout, wout, S,
-                            sm.work, sm.scr);
+        stage_plane(gz + ((size_t)b * M + m) * npix, npix, Sf);
+        __syncthreads();
+        plane_rfft2<FH, FW>([&](int r, int c) { return Sf[r * wout + c]; }, hout, wout, S,
+                            sm.work, sm.scr, sm.tw);
         const cpx* G = ghat + (size_t)m * P::F;
         for (int e = threadIdx.x; e < P::F; e += P::NT) A[e] = cadd(A[e], cmulc(S[e], G[e]));
-        // the next plane_rfft2 writes S only after its first internal barrier
+        __syncthreads();  // S is restaged by the next direction
     }
-    __syncthreads();
     if (part != nullptr) {  // M split across workgroups: emit the partial spectrum
         cpx* dst = part + ((size_t)b * gridDim.y + blockIdx.y) * P::F;
         for (int e = threadIdx.x; e < P::F; e += P::NT) dst[e] = A[e];
@@ -139,7 +153,7 @@ __global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_fftconv_bwd_dx(
     plane_irfft2<FH, FW>(
         [&](int a, int c) { return A[a * P::SP + c]; }, (FH - ph) & (FH - 1), hin,
         (FW - pw) & (FW - 1), win, 1.0f / (float)(FH * FW),
-        [&](int i, int j, float v) { d[i * win + j] = v; }, sm.work, sm.scr);
+        [&](int i, int j, float v) { d[i * win + j] = v; }, sm.work, sm.scr, sm.tw);
 }
 
 template <int FH, int FW>
@@ -149,6 +163,7 @@ __global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_fftconv_bwd_dx_fin(
     using P = Plane<FH, FW>;
     __shared__ cpx A[P::F];
     __shared__ Smem<FH, FW> sm;
+    NC_SPECTRAL_PROLOGUE(sm);
     const int b = blockIdx.x;
     const cpx* src = part + (size_t)b * nsplit * P::F;
     for (int e = threadIdx.x; e < P::F; e += P::NT) {
@@ -161,7 +176,7 @@ __global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_fftconv_bwd_dx_fin(
     plane_irfft2<FH, FW>(
         [&](int a, int c) { return A[a * P::SP + c]; }, (FH - ph) & (FH - 1), hin,
         (FW - pw) & (FW - 1), win, 1.0f / (float)(FH * FW),
-        [&](int i, int j, float v) { d[i * win + j] = v; }, sm.work, sm.scr);
+        [&](int i, int j, float v) { d[i * win + j] = v; }, sm.work, sm.scr, sm.tw);
 }
 
 template <int FH, int FW>
@@ -172,23 +187,27 @@ __global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_fftconv_bwd_dg(
     constexpr int PER = (P::F + P::NT - 1) / P::NT;
     __shared__ cpx S[P::F];
     __shared__ Smem<FH, FW> sm;
+    NC_SPECTRAL_PROLOGUE(sm);
     const int m = blockIdx.x;
     const int b0 = blockIdx.y * bc;
     const int b1 = min(B, b0 + bc);
     const int npix = hout * wout;
+    float* Sf = reinterpret_cast<float*>(S);
     cpx acc[PER];
 #pragma unroll
     for (int u = 0; u < PER; ++u) acc[u] = cmk(0.f, 0.f);
     for (int b = b0; b < b1; ++b) {
-        const float* g = gz + ((size_t)b * M + m) * npix;
-        plane_rfft2<FH, FW>([&](int r, int c) { return g[r * wout + c]; }, hout, wout, S,
-                            sm.work, sm.scr);
+        stage_plane(gz + ((size_t)b * M + m) * npix, npix, Sf);
+        __syncthreads();
+        plane_rfft2<FH, FW>([&](int r, int c) { return Sf[r * wout + c]; }, hout, wout, S,
+                            sm.work, sm.scr, sm.tw);
         const cpx* X = xhat + (size_t)b * P::F;
 #pragma unroll
         for (int u = 0; u < PER; ++u) {
             const int e = threadIdx.x + u * P::NT;
             if (e < P::F) acc[u] = cadd(acc[u], cmulc(S[e], X[e]));
         }
+        __syncthreads();  // S is restaged by the next sample
     }
     cpx* dst = part + ((size_t)blockIdx.y * M + m) * P::F;
 #pragma unroll

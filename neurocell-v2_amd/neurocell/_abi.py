@@ -50,7 +50,8 @@ _SIGS = {
     "nc_adaptive_stats": (I, [P, C.POINTER(ChipDesc), P, P, P, P, I, I, F, F, F, F, P, P]),
     "nc_inject_roi": (I, [P, I, I, P, I, P, P]),
     "nc_mse_loss": (I, [P, I, P, P, P, P]),
-    "nc_adamw_step": (I, [P, I, P, P, P, P, P, P, F, F, F, F]),
+    "nc_packed_accuracy": (I, [P, I, I, P, P, P, P]),
+    "nc_adamw_step": (I, [P, I, P, P, P, P, P, P, I, F, F, F, F]),
 }
 
 ENTRY_POINTS = tuple(_SIGS)

@@ -15,7 +15,7 @@ Reverse: port bwd -> d x [spectral conv bwd (dx, dG in the frequency domain)
 """
 from __future__ import annotations
 
-import math
+import copy
 
 import numpy as np
 import torch
@@ -244,6 +244,12 @@ class StepPlan:
             self.g_out = torch.empty(B, self.P, **f)
             self.loss = torch.empty(1, **f)
 
+    def fresh(self) -> "StepPlan":
+        """A plan sharing this one's static maps with its own activation buffers."""
+        p = copy.copy(self)
+        p._alloc()
+        return p
+
     # ------------------------------------------------------------------ forward
     def forward(self, cell: torch.Tensor, filt: torch.Tensor, x_flat: torch.Tensor,
                 codd_mode: str = "continuous", inv_tau: float = 1.0,
@@ -356,11 +362,13 @@ class StepPlan:
              ptr(self.gpp), ptr(g_cell))
 
     # ------------------------------------------------------------------ loss
-    def mse(self, target: torch.Tensor) -> torch.Tensor:
-        """default_mse_loss (trainer.py:57-61) on the port outputs: writes loss and g_out."""
+    def mse(self, target: torch.Tensor, loss: torch.Tensor | None = None) -> torch.Tensor:
+        """default_mse_loss (trainer.py:57-61) on the port outputs: writes the loss (into
+        ``loss`` when given, a one-element device view) and g_out."""
+        loss = self.loss if loss is None else loss
         call("nc_mse_loss", stream_ptr(), self.B * self.P, ptr(self.out), ptr(target),
-             ptr(self.loss), ptr(self.g_out))
-        return self.loss
+             ptr(loss), ptr(self.g_out))
+        return loss
 
 
 def _abi_size(name: str, *args) -> int:
@@ -372,3 +380,124 @@ def inv_tau_f32(state_temperature: float) -> float:
     """1 / max(tau, 1e-4) evaluated in float32 (params.py:63)."""
     t = np.float32(max(np.float32(state_temperature), np.float32(1e-4)))
     return float(np.float32(1.0) / t)
+
+
+class ParamState:
+    """Flat fp32 parameters (cell_params (3,H,W) then greens_filters (M,1,kh,kw)), their
+    gradient and the AdamW moments, shared by every train-step bucket.  The step count and
+    learning rate live in device memory so a captured step graph replays them."""
+
+    def __init__(self, cell_params: torch.Tensor, filters: torch.Tensor,
+                 learning_rate: float = 1e-3, b1: float = 0.9, b2: float = 0.999,
+                 eps: float = 1e-8, weight_decay: float = 1e-4):
+        dev = cell_params.device
+        nc, nf = cell_params.numel(), filters.numel()
+        self.n = nc + nf
+        self.theta = torch.empty(self.n, device=dev, dtype=torch.float32)
+        self.theta[:nc].copy_(cell_params.reshape(-1))
+        self.theta[nc:].copy_(filters.reshape(-1))
+        self.cell = self.theta[:nc].view(cell_params.shape)
+        self.filt = self.theta[nc:].view(filters.shape)
+        self.grad = torch.zeros_like(self.theta)
+        self.g_cell = self.grad[:nc].view(cell_params.shape)
+        self.g_filt = self.grad[nc:].view(filters.shape)
+        self.m = torch.zeros_like(self.theta)
+        self.v = torch.zeros_like(self.theta)
+        self.count = torch.zeros(1, device=dev, dtype=torch.int32)
+        self.set_learning_rate(learning_rate)
+        self.hyper = (float(b1), float(b2), float(eps), float(weight_decay))
+
+    def set_learning_rate(self, learning_rate) -> None:
+        """A float, or a device/host table of the schedule at steps 0..n-1 (the last entry
+        holds for later steps).  Replacing the table invalidates captured graphs."""
+        t = torch.as_tensor(learning_rate, dtype=torch.float32).reshape(-1)
+        self.lr = t.to(self.theta.device).contiguous()
+
+    def adamw(self) -> None:
+        b1, b2, eps, wd = self.hyper
+        call("nc_adamw_step", stream_ptr(), self.n, ptr(self.theta), ptr(self.grad), ptr(self.m),
+             ptr(self.v), ptr(self.count), ptr(self.lr), self.lr.numel(), b1, b2, eps, wd)
+
+
+class TrainState:
+    """One optimiser step of VNNTrainer.train_step (trainer.py:101-106) on a StepPlan:
+    forward -> MSE loss -> reverse pass -> AdamW, over persistent buffers (static batch
+    buffers ``x`` (B, n_in) and ``y`` (B, P)).  ``capture()`` records the whole step in a HIP
+    graph that ``step()`` replays."""
+
+    def __init__(self, plan: StepPlan, params: ParamState, codd_mode: str = "continuous",
+                 state_temperature: float = 1.0, active_threshold: float = 0.6):
+        self.plan = plan
+        self.p = params
+        dev = plan.device
+        self.x = torch.zeros(plan.B, plan.n_in, device=dev, dtype=torch.float32)
+        self.y = torch.zeros(plan.B, plan.P, device=dev, dtype=torch.float32)
+        self.codd = (codd_mode, inv_tau_f32(state_temperature), float(active_threshold))
+        self.graph = None
+
+    def launch(self, x: torch.Tensor | None = None, y: torch.Tensor | None = None,
+               loss: torch.Tensor | None = None) -> None:
+        """Issues the step's launches on the current stream (no host synchronisation) for the
+        batch ``x`` (B, n_in) / ``y`` (B, P), by default the static buffers."""
+        pl, ps = self.plan, self.p
+        mode, it, thr = self.codd
+        pl.forward(ps.cell, ps.filt, self.x if x is None else x, codd_mode=mode, inv_tau=it,
+                   active_threshold=thr)
+        pl.mse(self.y if y is None else y, loss)
+        pl.backward(ps.cell, ps.filt, pl.g_out, ps.g_cell, ps.g_filt, codd_mode=mode,
+                    inv_tau=it, active_threshold=thr)
+        ps.adamw()
+
+    def capture(self) -> None:
+        """Records one step into a HIP graph.  The warm-up launch on a side stream is a real
+        optimiser step."""
+        self.graph = _capture(self.launch)
+
+    def step(self) -> torch.Tensor:
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self.launch()
+        return self.plan.loss
+
+
+def _capture(fn):
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
+class EvalState:
+    """Forward-only evaluation (VNNTrainer.evaluate_packed's apply, trainer.py:122-138) on an
+    evaluation StepPlan, with optional HIP-graph capture."""
+
+    def __init__(self, plan: StepPlan, cell_params: torch.Tensor, filters: torch.Tensor,
+                 codd_mode: str = "continuous", state_temperature: float = 1.0,
+                 active_threshold: float = 0.6):
+        self.plan = plan
+        self.cell = cell_params
+        self.filt = filters
+        self.x = torch.zeros(plan.B, plan.n_in, device=plan.device, dtype=torch.float32)
+        self.codd = (codd_mode, inv_tau_f32(state_temperature), float(active_threshold))
+        self.graph = None
+
+    def launch(self) -> torch.Tensor:
+        mode, it, thr = self.codd
+        return self.plan.forward(self.cell, self.filt, self.x, codd_mode=mode, inv_tau=it,
+                                 active_threshold=thr)
+
+    def capture(self) -> None:
+        self.graph = _capture(self.launch)
+
+    def run(self) -> torch.Tensor:
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self.launch()
+        return self.plan.out

@@ -1,0 +1,129 @@
+"""Propagation entry point: ``propagate_vnn_2d`` (propagator.py:209-734) on the gfx950 path.
+
+Every accepted ``backend`` string routes to the single MI355X implementation (the step
+executor in ``engine.py``: spectral correlation + fused epilogues), so the name set and its
+validation are kept for API compatibility (propagator.py:58-65, 231-234).  The whole d-step
+forward is one autograd node whose backward is the executor's reverse pass (the chain of
+the reference's custom VJPs), giving gradients w.r.t. ``params.cell_params`` and
+``params.greens_filters``.
+"""
+from __future__ import annotations
+
+import torch
+
+from ._lib import NeurocellError
+from .engine import StepPlan, flatten_inputs, inv_tau_f32, port_input_shapes
+from .topology import ChipTopology2D, CoordinatePortSpec
+
+SUPPORTED_BACKENDS = ("auto", "nchw_direct", "rfft_hoisted", "nchw_rfft_bwd", "pallas_fused",
+                      "pallas_sram")
+
+
+def select_optimal_backend(topology: ChipTopology2D) -> str:
+    """propagator.py:68-85 cost model, kept for API compatibility: on MI355X every backend
+    string runs the same spectral + fused-epilogue path, whose grid the topology fixes."""
+    kh, kw = topology.kernel_size
+    roi_h, roi_w = topology.roi_shape
+    if roi_h * roi_w < 256:
+        return "nchw_direct"
+    fh, fw = topology.fft_shape
+    fits = (roi_h + kh - 1 <= fh) and (roi_w + kw - 1 <= fw)
+    if topology.padding_mode != "CIRCULAR" and kh * kw > 512 and fits:
+        return "pallas_sram"
+    return "pallas_fused"
+
+
+class _PlanCache:
+    """Static launch plans per (topology, B, sub-ROI, port shapes, activations)."""
+
+    def __init__(self):
+        self.plans = {}
+
+    def get(self, topology, B, port_shapes, roi_bbox, activate, final_activate, hard_pin_io,
+            training, device):
+        key = (id(topology), topology, B, tuple(port_shapes), roi_bbox, str(activate),
+               str(final_activate), bool(hard_pin_io), bool(training), str(device))
+        p = self.plans.get(key)
+        if p is None:
+            p = self.plans[key] = StepPlan(topology, B, port_shapes, roi_bbox=roi_bbox,
+                                           activate=activate, final_activate=final_activate,
+                                           hard_pin_io=hard_pin_io, training=training,
+                                           device=device)
+        return p
+
+
+_PLANS = _PlanCache()
+
+
+class _Propagate(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, cell, filt, x_flat, plan, codd, need_grad):
+        mode, it, thr = codd
+        cell, filt = cell.contiguous(), filt.contiguous()
+        # each call owns its activations so several graphs can be alive at once
+        run = plan.fresh() if need_grad else plan
+        out = run.forward(cell, filt, x_flat, codd_mode=mode, inv_tau=it,
+                          active_threshold=thr).clone()
+        ctx.run, ctx.codd = run, codd
+        ctx.save_for_backward(cell, filt)
+        return out
+
+    @staticmethod
+    def backward(ctx, g_out):
+        cell, filt = ctx.saved_tensors
+        mode, it, thr = ctx.codd
+        g_cell = torch.empty_like(cell)
+        g_filt = torch.empty_like(filt)
+        ctx.run.backward(cell, filt, g_out.contiguous(), g_cell, g_filt, codd_mode=mode,
+                         inv_tau=it, active_threshold=thr)
+        ctx.run = None
+        return g_cell, g_filt, None, None, None, None
+
+
+def propagate_vnn_2d(params, inputs, topology: ChipTopology2D, activate="tanh",
+                     final_activate=None, norm: bool = True, sharpen_filter=None,
+                     gated_filters: bool = False, hard_pin_io: bool = False,
+                     backend: str = "nchw_direct", return_universe: bool = False,
+                     spatial_mask=None, codd_mode: str = "continuous",
+                     state_temperature: float = 1.0, active_threshold: float = 0.6):
+    """propagator.py:209-734: (B, out_h, out_w) port predictions, differentiable w.r.t. the
+    VNNParams leaves.  ``spatial_mask`` (an AdaptiveMaskSpec) runs on its cropped sub-ROI."""
+    if backend not in SUPPORTED_BACKENDS:
+        raise ValueError(f"Unsupported backend '{backend}'; choose from {SUPPORTED_BACKENDS}.")
+    from .params import SUPPORTED_CODD_MODES
+    if codd_mode not in SUPPORTED_CODD_MODES:
+        raise ValueError(f"Unsupported codd_mode '{codd_mode}'; choose from "
+                         f"{SUPPORTED_CODD_MODES}.")
+    if not norm:
+        raise NeurocellError("norm=False is not part of the MI355X path")
+    if sharpen_filter is not None or gated_filters:
+        raise NeurocellError("sharpen_filter / gated_filters are not part of the MI355X path")
+    if return_universe:
+        raise NeurocellError("return_universe=True is not supported yet on the MI355X path")
+    roi_bbox = None
+    if spatial_mask is not None and not spatial_mask.is_full_roi:
+        roi_bbox = tuple(int(v) for v in spatial_mask.roi_bbox)
+    x_flat = flatten_inputs(inputs, topology)
+    cell, filt = params.cell_params, params.greens_filters
+    need_grad = torch.is_grad_enabled() and (cell.requires_grad or filt.requires_grad)
+    plan = _PLANS.get(topology, x_flat.shape[0], port_input_shapes(inputs, topology), roi_bbox,
+                      activate, final_activate, hard_pin_io, need_grad, cell.device)
+    codd = (codd_mode, inv_tau_f32(float(state_temperature)), float(active_threshold))
+    out = _Propagate.apply(cell, filt, x_flat, plan, codd, need_grad)
+    oh, ow = topology.out_port.size
+    return out.reshape(out.shape[0], oh, ow)
+
+
+def inject_inputs_roi_2d(inputs, topology: ChipTopology2D, dtype=torch.float32, roi_bbox=None):
+    """propagator.py:135-191: (roi_cells, True) when every port fits the (cropped) ROI, else
+    (None, False).  Runs the executor's gather kernel."""
+    from ._lib import call, ptr, stream_ptr
+    x_flat = flatten_inputs(inputs, topology)
+    plan = _PLANS.get(topology, x_flat.shape[0], port_input_shapes(inputs, topology), roi_bbox,
+                      "tanh", None, False, False, x_flat.device)
+    if plan.t0_grid:
+        return None, False
+    roi = torch.empty(x_flat.shape[0], plan.h, plan.w, device=x_flat.device, dtype=dtype)
+    call("nc_inject_roi", stream_ptr(), x_flat.shape[0], plan.n_in, ptr(x_flat), plan.h * plan.w,
+         ptr(plan.src), ptr(roi))
+    return roi, True

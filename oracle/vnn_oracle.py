@@ -49,6 +49,32 @@ except ImportError:  # pragma: no cover
         return np.fft.irfft2(x, s=s, axes=(-2, -1))
 
 WORKERS = 1
+_DTYPE = [np.float64]
+
+
+def _dt():
+    """Working float dtype (float64 for checking; float32 for the timed CPU baseline)."""
+    return _DTYPE[0]
+
+
+class precision:
+    """``with precision(np.float32, workers=n):`` runs the oracle in float32 with n FFT
+    workers (the CPU-baseline configuration)."""
+
+    def __init__(self, dtype, workers=None):
+        self.dtype, self.workers = dtype, workers
+
+    def __enter__(self):
+        global WORKERS
+        self._saved = (_DTYPE[0], WORKERS)
+        _DTYPE[0] = self.dtype
+        if self.workers is not None:
+            WORKERS = self.workers
+        return self
+
+    def __exit__(self, *exc):
+        global WORKERS
+        _DTYPE[0], WORKERS = self._saved
 
 CODD_MODES = ("continuous", "annealed", "ste_binary", "ste_ternary")
 EPS = 1e-5  # kernels_pallas.py:205 (rsqrt(var + 1e-5)), epilogue.py:25
@@ -208,7 +234,7 @@ def codd_state_probs(s_raw, io_mask, hard_pin_io=False, mode="continuous", tau=1
     """params.py:31-80.  Returns (s_prob, ds_prob/ds_raw) elementwise."""
     if mode not in CODD_MODES:
         raise ValueError(f"Unsupported codd_mode '{mode}'")
-    s_raw = np.asarray(s_raw, dtype=np.float64)
+    s_raw = np.asarray(s_raw, dtype=_dt())
     s_base = s_raw if hard_pin_io else np.where(io_mask, 1.0, s_raw)
     if mode == "continuous":
         p = sigmoid(s_base)
@@ -237,7 +263,7 @@ def precompute_step_params(cell, geom: Geometry, act="tanh", hard_pin_io=False, 
     H, W = geom.grid_shape
     rh, rw = geom.pad_h, geom.pad_w
     inv_M = 1.0 / float(geom.directions)
-    w_raw, b_full, s_raw = (np.asarray(c, np.float64) for c in cell)
+    w_raw, b_full, s_raw = (np.asarray(c, _dt()) for c in cell)
     w_pinned = np.where(geom.out_weight_mask, 1.0, w_raw)
     s_prob, ds = codd_state_probs(s_raw, geom.io_state_mask, hard_pin_io, mode, tau,
                                   active_threshold)
@@ -276,9 +302,9 @@ def precompute_step_params_vjp(cell, geom: Geometry, grads: dict, act="tanh", ha
                                 active_threshold)
     s_prob, ds = sp["s_prob"], sp["ds_prob"]
     b_full, w_pinned = sp["b_full"], sp["w_pinned"]
-    g_weff = np.zeros((hv, wv))
-    g_seff = np.zeros((hv, wv))
-    g_broi = np.zeros((hv, wv))
+    g_weff = np.zeros((hv, wv), _dt())
+    g_seff = np.zeros((hv, wv), _dt())
+    g_broi = np.zeros((hv, wv), _dt())
     r0, r1, c0, c1 = roi_bbox if roi_bbox is not None else (0, hv, 0, wv)
     if "w_eff_roi" in grads:
         g_weff[r0:r1, c0:c1] += grads["w_eff_roi"]
@@ -291,15 +317,15 @@ def precompute_step_params_vjp(cell, geom: Geometry, grads: dict, act="tanh", ha
         if key in grads:
             np.add.at(dst, (rows, cols), np.asarray(grads[key]).reshape(-1))
     roi = (slice(rh, H - rh), slice(rw, W - rw))
-    g_wp = np.zeros((H, W))
-    g_sp = np.zeros((H, W))
-    g_b = np.zeros((H, W))
+    g_wp = np.zeros((H, W), _dt())
+    g_sp = np.zeros((H, W), _dt())
+    g_b = np.zeros((H, W), _dt())
     s_roi = s_prob[roi]
     g_wp[roi] += inv_M * (1.0 - s_roi) * g_weff
     g_sp[roi] += -inv_M * w_pinned[roi] * g_weff + inv_M * g_seff
     g_b[roi] += g_broi
     if "border_2d" in grads:
-        gbd = np.asarray(grads["border_2d"], np.float64)
+        gbd = np.asarray(grads["border_2d"], _dt())
         g_b += act_deriv(b_full, act) * s_prob * gbd
         g_sp += act_fwd(b_full, act) * gbd
     g_w = np.where(geom.out_weight_mask, 0.0, g_wp)
@@ -320,9 +346,9 @@ def inject_inputs_roi(port_inputs, geom: Geometry, roi_bbox=None):
     min_r, max_r = geom.pad_h + b_r0, geom.pad_h + b_r1
     min_c, max_c = geom.pad_w + b_c0, geom.pad_w + b_c1
     B = np.asarray(port_inputs[0]).shape[0]
-    out = np.zeros((B, b_r1 - b_r0, b_c1 - b_c0))
+    out = np.zeros((B, b_r1 - b_r0, b_c1 - b_c0), _dt())
     for inp, port in zip(port_inputs, geom.in_ports):
-        inp = np.asarray(inp, np.float64)
+        inp = np.asarray(inp, _dt())
         kind, a, *b = port
         if kind == "coords":
             for k, (r, c) in enumerate(a):
@@ -363,15 +389,15 @@ def split_ports(inputs, geom: Geometry):
 def conv2d_direct(x, g, pad):
     """Brute-force zero-padded cross-correlation, ``lax.conv_general_dilated`` semantics
     (kernels_greens.py:177-217): x (B,Hi,Wi), g (M,Kh,Kw), pad (ph,pw) -> (B,M,Ho,Wo)."""
-    x = np.asarray(x, np.float64)
-    g = np.asarray(g, np.float64)
+    x = np.asarray(x, _dt())
+    g = np.asarray(g, _dt())
     B, Hi, Wi = x.shape
     M, Kh, Kw = g.shape
     ph, pw = pad
-    xp = np.zeros((B, Hi + 2 * ph, Wi + 2 * pw))
+    xp = np.zeros((B, Hi + 2 * ph, Wi + 2 * pw), _dt())
     xp[:, ph:ph + Hi, pw:pw + Wi] = x
     Ho, Wo = Hi + 2 * ph - Kh + 1, Wi + 2 * pw - Kw + 1
-    out = np.zeros((B, M, Ho, Wo))
+    out = np.zeros((B, M, Ho, Wo), _dt())
     for u in range(Kh):
         for v in range(Kw):
             out += xp[:, None, u:u + Ho, v:v + Wo] * g[None, :, u, v, None, None]
@@ -380,7 +406,7 @@ def conv2d_direct(x, g, pad):
 
 def filter_spectrum(g, fft_shape):
     """``precompute_filter_rfft2`` (kernels_greens.py:240-259): rfft2 of the flipped filters."""
-    return _rfft2(np.flip(np.asarray(g, np.float64), axis=(-2, -1)), fft_shape, WORKERS)
+    return _rfft2(np.flip(np.asarray(g, _dt()), axis=(-2, -1)), fft_shape, WORKERS)
 
 
 def conv2d_fft(x, g, pad, out_shape, fft_shape):
@@ -422,14 +448,14 @@ def filter_grad_from_unshifted(dGh, kernel_size, pad, fft_shape):
 
 def conv2d_bwd_direct(gz, x, g, pad):
     """True gradient of :func:`conv2d_direct` by brute force: returns (dx, dg)."""
-    gz = np.asarray(gz, np.float64)
-    x = np.asarray(x, np.float64)
-    g = np.asarray(g, np.float64)
+    gz = np.asarray(gz, _dt())
+    x = np.asarray(x, _dt())
+    g = np.asarray(g, _dt())
     B, Hi, Wi = x.shape
     M, Kh, Kw = g.shape
     ph, pw = pad
     Ho, Wo = gz.shape[-2:]
-    xp = np.zeros((B, Hi + 2 * ph, Wi + 2 * pw))
+    xp = np.zeros((B, Hi + 2 * ph, Wi + 2 * pw), _dt())
     xp[:, ph:ph + Hi, pw:pw + Wi] = x
     dxp = np.zeros_like(xp)
     dg = np.zeros_like(g)
@@ -454,8 +480,8 @@ def standardize_stats(zt):
 def epilogue_fwd(z, delta, w, s, b, act="tanh", has_border=True, neg_slope=0.01):
     """``pallas_fused_roi_step_epilogue`` forward (kernels_pallas.py:163-218, 663-690;
     XLA twin epilogue.py:28-56).  Returns (out (B,Hv,Wv), mean (B,M), rstd (B,M))."""
-    z = np.asarray(z, np.float64)
-    d = np.asarray(delta, np.float64).reshape((-1,) + z.shape[-3:])[0]
+    z = np.asarray(z, _dt())
+    d = np.asarray(delta, _dt()).reshape((-1,) + z.shape[-3:])[0]
     zt = z + d[None] if has_border else z
     mean, rstd = standardize_stats(zt)
     zn = (zt - mean[..., None, None]) * rstd[..., None, None]
@@ -466,8 +492,8 @@ def epilogue_fwd(z, delta, w, s, b, act="tanh", has_border=True, neg_slope=0.01)
 def epilogue_bwd(z, delta, w, s, b, mean, rstd, gy, act="tanh", has_border=True, neg_slope=0.01):
     """``_pallas_roi_epilogue_bwd_rule`` (kernels_pallas.py:221-291, 869-918).
     Returns (gz, gdb (M,Hv,Wv), gw, gs, gb)."""
-    z = np.asarray(z, np.float64)
-    d = np.asarray(delta, np.float64).reshape((-1,) + z.shape[-3:])[0]
+    z = np.asarray(z, _dt())
+    d = np.asarray(delta, _dt()).reshape((-1,) + z.shape[-3:])[0]
     zt = z + d[None] if has_border else z
     zn = (zt - mean[..., None, None]) * rstd[..., None, None]
     a = act_fwd(zn + b, act, neg_slope)
@@ -489,8 +515,8 @@ def port_fwd(z, delta, rows, cols, out_size, w_out, s_out, b_out, has_border=Tru
     """``pallas_standardize_output_port`` + ``pallas_fused_output_port_epilogue``
     (kernels_pallas.py:1284-1347, 1510-1551; XLA twin epilogue.py:82-128).
     Returns (out (B,oh,ow), aux)."""
-    z = np.asarray(z, np.float64)
-    d = np.asarray(delta, np.float64).reshape((-1,) + z.shape[-3:])[0]
+    z = np.asarray(z, _dt())
+    d = np.asarray(delta, _dt()).reshape((-1,) + z.shape[-3:])[0]
     zt = z + d[None] if has_border else z
     mean, rstd = standardize_stats(zt)
     B, M = z.shape[:2]
@@ -510,8 +536,8 @@ def port_bwd(z, delta, rows, cols, out_size, w_out, s_out, b_out, aux, g_out, ha
              final_act=None):
     """Backward of :func:`port_fwd` (kernels_pallas.py:1350-1504 plus the jnp port algebra
     of :1538-1551).  Returns (gz, gdb, g_w_out, g_s_out, g_b_out)."""
-    z = np.asarray(z, np.float64)
-    d = np.asarray(delta, np.float64).reshape((-1,) + z.shape[-3:])[0]
+    z = np.asarray(z, _dt())
+    d = np.asarray(delta, _dt()).reshape((-1,) + z.shape[-3:])[0]
     zt = z + d[None] if has_border else z
     mean, rstd, zo = aux["mean"], aux["rstd"], aux["zo"]
     B, M = z.shape[:2]
@@ -551,7 +577,7 @@ def border_patch(border_2d, geom: Geometry, roi_bbox=None):
     H, W = geom.grid_shape
     kh, kw = geom.kernel_size
     rh, rw = geom.pad_h, geom.pad_w
-    bo = np.array(border_2d, np.float64)
+    bo = np.array(border_2d, _dt())
     bo[rh:H - rh, rw:W - rw] = 0.0
     if roi_bbox is not None:
         r0, r1, c0, c1 = roi_bbox
@@ -564,8 +590,8 @@ def propagate(cell, filters, inputs, geom: Geometry, act="tanh", final_act=None,
               active_threshold=0.6, conv="fft"):
     """Pure-ROI forward of ``propagate_vnn_2d`` for the VALID pallas backends
     (propagator.py:252-682).  ``filters`` is (M,1,Kh,Kw).  Returns (out, cache)."""
-    cell = np.asarray(cell, np.float64)
-    g = np.asarray(filters, np.float64)[:, 0]
+    cell = np.asarray(cell, _dt())
+    g = np.asarray(filters, _dt())[:, 0]
     kh, kw = geom.kernel_size
     pad = ((kh - 1) // 2, (kw - 1) // 2)
     d = geom.depth
@@ -609,13 +635,15 @@ def propagate(cell, filters, inputs, geom: Geometry, act="tanh", final_act=None,
 
 def propagate_vjp(cell, filters, inputs, geom: Geometry, g_out, act="tanh", final_act=None,
                   hard_pin_io=False, roi_bbox=None, mode="continuous", tau=1.0,
-                  active_threshold=0.6):
+                  active_threshold=0.6, fwd=None):
     """Reverse pass of :func:`propagate`: the chain of the reference's custom VJPs
     (kernels_pallas.py:1350-1504, 869-1064, 1794-1821, 1558-1579; propagator.py autodiff of
     the border conv and params.py autodiff of the pre-step fusion).
-    Returns (out, g_cell (3,H,W), g_filters (M,1,Kh,Kw))."""
-    out, c = propagate(cell, filters, inputs, geom, act, final_act, hard_pin_io, roi_bbox,
-                       mode, tau, active_threshold)
+    ``fwd`` may pass the (out, cache) of a matching :func:`propagate` call to skip the
+    forward.  Returns (out, g_cell (3,H,W), g_filters (M,1,Kh,Kw))."""
+    out, c = fwd if fwd is not None else propagate(
+        cell, filters, inputs, geom, act, final_act, hard_pin_io, roi_bbox, mode, tau,
+        active_threshold)
     sp, g, pad, fs = c["sp"], c["g"], c["pad"], c["fft_shape"]
     d = geom.depth
     kh, kw = geom.kernel_size
@@ -627,7 +655,7 @@ def propagate_vjp(cell, filters, inputs, geom: Geometry, g_out, act="tanh", fina
     hb_final = d > 1
     gz, gdb, g_wo, g_so, g_bo = port_bwd(c["zs"][-1], c["delta"], c["rows"], c["cols"],
                                          geom.out_size, sp["w_eff_out"], sp["s_eff_out"],
-                                         sp["b_out"], c["aux"], np.asarray(g_out, np.float64),
+                                         sp["b_out"], c["aux"], np.asarray(g_out, _dt()),
                                          hb_final, final_act)
     g_delta += gdb
     dGh = np.zeros((M, fs[0], fs[1] // 2 + 1), complex)
@@ -656,7 +684,7 @@ def propagate_vjp(cell, filters, inputs, geom: Geometry, g_out, act="tanh", fina
             g_bp[u:u + hv, v:v + wv] += np.einsum("mij,m->ij", g_delta, g[:, u, v])
             g_filt[:, u, v] += np.einsum("mij,ij->m", g_delta, bp[u:u + hv, v:v + wv])
     H, W = geom.grid_shape
-    g_border = np.zeros((H, W))
+    g_border = np.zeros((H, W), _dt())
     r0, c0 = (roi_bbox[0], roi_bbox[2]) if roi_bbox is not None else (0, 0)
     g_border[r0:r0 + Hp, c0:c0 + Wp] = g_bp
     rh, rw = geom.pad_h, geom.pad_w
@@ -675,17 +703,17 @@ def propagate_full_grid(cell, filters, inputs, geom: Geometry, act="tanh", final
     correlation of the whole (B,H,W) grid, standardized, zero-padded back, Codd-gated and
     averaged over M.  Used to pin the pure-ROI + hoisted-border decomposition."""
     sp = precompute_step_params(cell, geom, act, hard_pin_io, None, mode, tau, active_threshold)
-    g = np.asarray(filters, np.float64)[:, 0]
+    g = np.asarray(filters, _dt())[:, 0]
     H, W = geom.grid_shape
     rh, rw = geom.pad_h, geom.pad_w
     M = geom.directions
     ports = split_ports(inputs, geom)
     B = np.asarray(ports[0]).shape[0]
-    cells = np.zeros((B, H, W))
+    cells = np.zeros((B, H, W), _dt())
     for inp, port in zip(ports, geom.in_ports):
         kind, a, *b = port
         (r0, c0) = a
-        inp = np.asarray(inp, np.float64)
+        inp = np.asarray(inp, _dt())
         ih, iw = inp.shape[1:] if inp.ndim == 3 else b[0]
         cells[:, r0:r0 + ih, c0:c0 + iw] = inp.reshape(B, ih, iw)
     w, bb, s = sp["w_pinned"], sp["b_full"], sp["s_prob"]
@@ -694,7 +722,7 @@ def propagate_full_grid(cell, filters, inputs, geom: Geometry, act="tanh", final
         zv = conv2d_direct(cells, g, (0, 0))
         mean, rstd = standardize_stats(zv)
         zn = (zv - mean[..., None, None]) * rstd[..., None, None]
-        zp = np.zeros((B, M, H, W))
+        zp = np.zeros((B, M, H, W), _dt())
         zp[:, :, rh:H - rh, rw:W - rw] = zn
         lin = zp * w * (1.0 - s)
         nl = (zp + bb) * s if a is None else act_fwd(zp + bb, a) * s
@@ -746,7 +774,7 @@ def adaptive_mask_stats(cell, filters, io_mask_roi, geom: Geometry, margin=(4, 4
                         act_roi=None, activity_threshold=1e-3):
     """``_compute_adaptive_mask_tensors`` (adaptive_mask.py:200-315): returns
     (stats int[8] = [r_eff_h, r_eff_w, salient, any_active, r0, r1, c0, c1], dilated mask)."""
-    g = np.abs(np.asarray(filters, np.float64)[:, 0])
+    g = np.abs(np.asarray(filters, _dt())[:, 0])
     kh, kw = g.shape[-2:]
     mpt = g.max(0)
     active = mpt >= filter_threshold * mpt.max() + 1e-12
@@ -758,9 +786,9 @@ def adaptive_mask_stats(cell, filters, io_mask_roi, geom: Geometry, margin=(4, 4
     rh, rw = geom.pad_h, geom.pad_w
     hv, wv = geom.roi_shape
     cell = np.asarray(cell, np.float32)
-    w_roi = cell[0, rh:rh + hv, rw:rw + wv].astype(np.float64)
-    b_roi = cell[1, rh:rh + hv, rw:rw + wv].astype(np.float64)
-    s_roi = cell[2, rh:rh + hv, rw:rw + wv].astype(np.float64)
+    w_roi = cell[0, rh:rh + hv, rw:rw + wv].astype(_dt())
+    b_roi = cell[1, rh:rh + hv, rw:rw + wv].astype(_dt())
+    s_roi = cell[2, rh:rh + hv, rw:rw + wv].astype(_dt())
     sp = sigmoid(s_roi)
     non_io = ~io_mask_roi
     non_io_count = max(1.0, float(non_io.sum()))
@@ -801,8 +829,8 @@ def adaptive_mask_stats(cell, filters, io_mask_roi, geom: Geometry, margin=(4, 4
 
 def mse_loss(logits, targets):
     """``default_mse_loss`` (trainer.py:57-61): mean squared error and its gradient."""
-    logits = np.asarray(logits, np.float64)
-    targets = np.asarray(targets, np.float64).reshape(logits.shape)
+    logits = np.asarray(logits, _dt())
+    targets = np.asarray(targets, _dt()).reshape(logits.shape)
     diff = logits - targets
     return float((diff ** 2).mean()), 2.0 * diff / diff.size
 

@@ -1,0 +1,45 @@
+"""Builds the CPU-emulated C ABI (tests/emu/_build/libnc_emu.so) from the same kernel
+sources as the gfx950 library, with g++ and the emulation shim in tests/emu/hip/."""
+import concurrent.futures as cf
+import os
+import subprocess
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+CSRC = os.path.join(ROOT, "neurocell-v2_amd", "csrc")
+OUT_DIR = os.path.join(HERE, "_build")
+LIB = os.path.join(OUT_DIR, "libnc_emu.so")
+SOURCES = [os.path.join(CSRC, f) for f in ("nc_codd.hip", "nc_epilogue.hip", "nc_spectral.hip")]
+FLAGS = ["g++", "-std=c++20", "-O1", "-fPIC", "-pthread", "-I", HERE]
+
+
+def _stale() -> bool:
+    if not os.path.exists(LIB):
+        return True
+    deps = SOURCES + [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
+    deps += [os.path.join(HERE, "hip", "hip_runtime.h"), os.path.join(HERE, "emu_main.cpp"),
+             os.path.join(ROOT, "include", "neurocell_hip.h")]
+    t = os.path.getmtime(LIB)
+    return any(os.path.getmtime(d) > t for d in deps)
+
+
+def _obj(src):
+    obj = os.path.join(OUT_DIR, os.path.basename(src) + ".o")
+    lang = ["-x", "c++"] if src.endswith(".hip") else []
+    subprocess.run(FLAGS + lang + ["-c", src, "-o", obj], check=True, capture_output=True)
+    return obj
+
+
+def build() -> str:
+    if not _stale():
+        return LIB
+    os.makedirs(OUT_DIR, exist_ok=True)
+    with cf.ThreadPoolExecutor(4) as ex:
+        objs = list(ex.map(_obj, SOURCES + [os.path.join(HERE, "emu_main.cpp")]))
+    subprocess.run(["g++", "-shared", "-pthread", "-o", LIB + ".tmp", *objs], check=True)
+    os.replace(LIB + ".tmp", LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build())

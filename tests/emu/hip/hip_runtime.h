@@ -1,0 +1,53 @@
+// CPU emulation of the HIP device model for tests: runs the kernel sources of
+// neurocell-v2_amd/csrc with one std::thread per work-item and a std::barrier per
+// workgroup, so their indexing, synchronisation and arithmetic can be checked against the
+// oracle without a GPU.  Test infrastructure only; the product never loads it.
+#pragma once
+#include <algorithm>
+#include <barrier>
+#include <cmath>
+#include <cstddef>
+#include <cstdint>
+#include <functional>
+#include <thread>
+#include <vector>
+#define __device__
+#define __host__
+#define __forceinline__ inline
+#define __constant__
+#define __shared__ static
+#define __global__
+#define __launch_bounds__(...)
+#define HIP_DYNAMIC_SHARED(type, var) static type var[1 << 17];
+struct float2 {
+    float x, y;
+};
+inline float2 make_float2(float a, float b) { return float2{a, b}; }
+struct dim3 {
+    unsigned x, y, z;
+    dim3(unsigned a = 1, unsigned b = 1, unsigned c = 1) : x(a), y(b), z(c) {}
+};
+extern thread_local dim3 threadIdx;
+extern dim3 blockDim, blockIdx, gridDim;
+extern std::barrier<>* g_bar;
+inline void __syncthreads() { g_bar->arrive_and_wait(); }
+// Cross-lane exchange; every work-item of the workgroup must call it together.
+inline float __shfl_xor(float v, int off, int) {
+    static float buf[1024];
+    const int t = threadIdx.x;
+    buf[t] = v;
+    __syncthreads();
+    const float r = buf[t ^ off];
+    __syncthreads();
+    return r;
+}
+typedef int hipError_t;
+typedef void* hipStream_t;
+#define hipSuccess 0
+inline hipError_t hipGetLastError() { return 0; }
+inline const char* hipGetErrorString(hipError_t) { return "emulated"; }
+using std::max;
+using std::min;
+void emu_launch(std::function<void()> f, dim3 g, dim3 b);
+#define hipLaunchKernelGGL(K, G, BK, SHM, ST, ...) \
+    emu_launch([&] { K(__VA_ARGS__); }, dim3(G), dim3(BK))

@@ -328,12 +328,15 @@ def case_helpers(be, seed=6):
     g = rng.normal(size=50).astype(np.float32)
     p, gd = be.put(p0), be.put(g)
     m, v, cnt = be.zeros((50,)), be.zeros((50,)), be.zeros((1,), np.int32)
-    lr = be.put(np.array([0.01], np.float32))
+    # a two-entry schedule table: steps 0 and >=1 use 0.01 and 0.02
+    lr_tab = np.array([0.01, 0.02], np.float32)
+    lr = be.put(lr_tab)
     pr_, mr, vr, cr = p0.astype(np.float64), 0.0, 0.0, 0
-    for _ in range(3):
+    for k in range(3):
         _ok(be, L.nc_adamw_step(s, 50, be.ptr(p), be.ptr(gd), be.ptr(m), be.ptr(v), be.ptr(cnt),
-                                be.ptr(lr), 0.9, 0.999, 1e-8, 1e-4), "adamw")
-        pr_, mr, vr, cr = O.adamw_step(pr_, g.astype(np.float64), mr, vr, cr, 0.01)
+                                be.ptr(lr), 2, 0.9, 0.999, 1e-8, 1e-4), "adamw")
+        pr_, mr, vr, cr = O.adamw_step(pr_, g.astype(np.float64), mr, vr, cr,
+                                       float(lr_tab[min(k, 1)]))
     return {"inject_mismatch": float((be.get(roi) != ref).sum()),
             "mse": abs(float(be.get(loss)[0]) - l_r) / l_r, "g_mse": rel_l2(be.get(gp), g_r),
             "adamw": rel_l2(be.get(p), pr_), "count_mismatch": float(be.get(cnt)[0] != 3)}

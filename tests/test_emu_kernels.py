@@ -1,0 +1,59 @@
+"""CPU parity of the kernel *sources*: the C ABI built with g++ against a CPU emulation of the
+HIP device model (tests/emu), checked against the float64 oracle on small shapes.  These run
+without a GPU; the same cases run on the MI355X in test_gpu_kernels.py."""
+import ctypes
+
+import pytest
+
+from kernel_cases import (CODD_CASES, TOL, HostBackend, case_adaptive, case_border_conv,
+                          case_codd, case_epilogue, case_fftconv, case_helpers, case_port)
+
+
+@pytest.fixture(scope="module")
+def be():
+    from emu.build_emu import build
+    from neurocell import _abi
+    return HostBackend(_abi.declare(ctypes.CDLL(build())))
+
+
+def _assert_small(res, tol=TOL):
+    bad = {k: v for k, v in res.items() if not v < tol}
+    assert not bad, f"parity errors above {tol}: {bad} (all: {res})"
+
+
+@pytest.mark.parametrize("FH,FW,hin,win,kh,kw", [(16, 16, 10, 12, 5, 3), (32, 64, 20, 50, 9, 13)])
+def test_fftconv(be, FH, FW, hin, win, kh, kw):
+    _assert_small(case_fftconv(be, B=2, M=3, hin=hin, win=win, kh=kh, kw=kw, FH=FH, FW=FW))
+
+
+def test_border_conv(be):
+    _assert_small(case_border_conv(be))
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 10, 12, "tanh", 1), (2, 3, 20, 40, "leaky_relu", 0),
+                                   (1, 2, 96, 90, "gelu", 1)])
+def test_epilogue(be, shape):
+    _assert_small(case_epilogue(be, *shape))
+
+
+@pytest.mark.parametrize("shape", [
+    (2, 3, 10, 12, (2, 3, 4, 2), (5, 5, 5, 5), None),
+    (1, 2, 96, 100, (10, 50, 95), (3, 99, 0), "tanh")])
+def test_port(be, shape):
+    B, M, h, w, rows, cols, fact = shape
+    _assert_small(case_port(be, B, M, h, w, rows, cols, fact))
+
+
+@pytest.mark.parametrize("mode,bbox,hard_pin", CODD_CASES[::3])
+def test_codd(be, mode, bbox, hard_pin):
+    _assert_small(case_codd(be, mode, bbox, hard_pin), tol=1e-5)
+
+
+def test_adaptive_stats(be):
+    assert case_adaptive(be) == {"stats_mismatch": 0.0, "mask_mismatch": 0.0}
+
+
+def test_helpers(be):
+    res = case_helpers(be)
+    assert res["inject_mismatch"] == 0 and res["count_mismatch"] == 0, res
+    _assert_small({k: res[k] for k in ("mse", "g_mse", "adamw")})

@@ -1,0 +1,397 @@
+"""Python API parity on the MI355X: the reference-named operators, propagation, model and
+trainer (all running the HIP kernels through the C ABI) against the float64 oracle, plus
+graph-replay checks of the trainer against its own eager launches.
+
+Bars: forward rel-L2 <= 1e-5, gradients rel-L2 <= 1e-4; optimiser
+trajectories (AdamW normalises each update, so tiny gradients are amplified) <= 1e-3 on the
+parameter change; graph replays bit-identical to eager launches.
+"""
+import types
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import alu_case, rel_l2
+from oracle import vnn_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+FWD_TOL = 1e-5
+GRAD_TOL = 1e-4
+TRAJ_TOL = 1e-3
+CROP = (6, 30, 10, 42)
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+def mask(bbox):
+    return None if bbox is None else types.SimpleNamespace(roi_bbox=bbox, is_full_roi=False)
+
+
+# ------------------------------------------------------------------ operators
+
+@pytest.mark.parametrize("act,hb", [("tanh", True), ("gelu", False), ("leaky_relu", True)])
+def test_roi_epilogue_autograd(act, hb):
+    from neurocell import pallas_fused_roi_step_epilogue
+    rng = np.random.default_rng(1)
+    B, M, h, w = 3, 4, 20, 24
+    z = rng.normal(size=(B, M, h, w)).astype(np.float32)
+    d = rng.normal(size=(1, M, h, w)).astype(np.float32)
+    ws, ss, bs = (rng.normal(size=(h, w)).astype(np.float32) for _ in range(3))
+    gy = rng.normal(size=(B, h, w)).astype(np.float32)
+    ts = [dev(a).requires_grad_() for a in (z, d, ws, ss, bs)]
+    out = pallas_fused_roi_step_epilogue(*ts, activate=act, has_border=hb)
+    out.backward(dev(gy))
+    r_out, mean, rstd = O.epilogue_fwd(z, d, ws, ss, bs, act, hb)
+    r = O.epilogue_bwd(z, d, ws, ss, bs, mean, rstd, gy, act, hb)
+    assert rel_l2(host(out), r_out) < FWD_TOL
+    for t, ref in zip(ts, (r[0], r[1][None], r[2], r[3], r[4])):
+        if not hb and t is ts[1]:
+            continue
+        assert rel_l2(host(t.grad), ref) < GRAD_TOL
+
+
+@pytest.mark.parametrize("coord", [False, True])
+def test_standardize_output_port(coord):
+    from neurocell import pallas_standardize_output_port
+    rng = np.random.default_rng(2)
+    B, M, h, w = 3, 5, 16, 20
+    z = rng.normal(size=(B, M, h, w)).astype(np.float32)
+    d = rng.normal(size=(1, M, h, w)).astype(np.float32)
+    if coord:
+        rows, cols = (1, 5, 5, 9, 15), (2, 7, 7, 0, 19)  # a repeated cell adds up
+        off, size = (rows, cols), (5, 1)
+    else:
+        off, size = (4, 11), (3, 2)
+        rr, cc = np.meshgrid(np.arange(3) + 4, np.arange(2) + 11, indexing="ij")
+        rows, cols = tuple(rr.ravel()), tuple(cc.ravel())
+    zt, dt = dev(z).requires_grad_(), dev(d).requires_grad_()
+    zo = pallas_standardize_output_port(zt, dt, off, size, True)
+    g = rng.normal(size=tuple(zo.shape)).astype(np.float32)
+    zo.backward(dev(g))
+    # float64 autograd restatement of standardize(z + delta) sampled at the port cells
+    z64 = torch.from_numpy(z).double().requires_grad_()
+    d64 = torch.from_numpy(d).double().requires_grad_()
+    tot = z64 + d64
+    mu = tot.mean(dim=(-2, -1), keepdim=True)
+    var = ((tot - mu) ** 2).mean(dim=(-2, -1), keepdim=True)
+    ref = ((tot - mu) / torch.sqrt(var + 1e-5))[:, :, list(rows), list(cols)]
+    ref = ref.reshape(B, M, *size)
+    ref.backward(torch.from_numpy(g).double())
+    assert rel_l2(host(zo), ref.detach().numpy()) < FWD_TOL
+    assert rel_l2(host(zt.grad), z64.grad.numpy()) < GRAD_TOL
+    assert rel_l2(host(dt.grad), d64.grad.numpy()) < GRAD_TOL
+
+
+def _conv_case(seed=3, B=2, M=3, h=20, w=24, kh=7, kw=5):
+    rng = np.random.default_rng(seed)
+    x = rng.normal(size=(B, h, w)).astype(np.float32)
+    g = rng.normal(size=(M, 1, kh, kw)).astype(np.float32)
+    gz = rng.normal(size=(B, M, h, w)).astype(np.float32)
+    pad = ((kh - 1) // 2, (kw - 1) // 2)
+    return x, g, gz, pad
+
+
+def _check_conv(fn):
+    x, g, gz, pad = _conv_case()
+    xt, gt = dev(x).requires_grad_(), dev(g).requires_grad_()
+    z = fn(xt, gt, pad)
+    z.backward(dev(gz))
+    with O.precision(np.float64):
+        r_z = O.conv2d_direct(x, g[:, 0], pad)
+        r_dx, r_dg = O.conv2d_bwd_direct(gz, x, g[:, 0], pad)
+    assert rel_l2(host(z), r_z) < FWD_TOL
+    assert rel_l2(host(xt.grad), r_dx) < GRAD_TOL
+    assert rel_l2(host(gt.grad)[:, 0], r_dg) < GRAD_TOL
+
+
+def test_pruned_rfft_chain():
+    from neurocell import conv2d_pruned_rfft_roi_step, hoist_filter_rfft2_nopad
+    fs = (32, 32)
+
+    def fn(x, g, pad):
+        kf = hoist_filter_rfft2_nopad(g, g.shape[-2:], pad, fs)
+        return conv2d_pruned_rfft_roi_step(x, kf, x.shape[-2:], pad, fs, True)
+    _check_conv(fn)
+
+
+def test_hybrid_nopad_chain():
+    from neurocell import conv2d_hybrid_nopad_roi_step, hoist_filter_rfft2_zero_nopad
+    fs = (32, 32)
+
+    def fn(x, g, pad):
+        token = hoist_filter_rfft2_zero_nopad(g, g.shape[-2:], pad, fs)
+        return conv2d_hybrid_nopad_roi_step(x, g.detach(), token, pad, fs, True)
+    _check_conv(fn)
+
+
+def test_small_kernel_step():
+    from neurocell import conv2d_small_kernel_roi_step
+    _check_conv(lambda x, g, pad: conv2d_small_kernel_roi_step(x, g, pad, True))
+
+
+@pytest.mark.parametrize("padding", ["VALID", "SAME"])
+def test_batched_nchw(padding):
+    from neurocell import conv2d_batched_nchw
+    x, g, _, pad = _conv_case(seed=4)
+    z = conv2d_batched_nchw(dev(x[:, None]), dev(g), padding=padding)
+    with O.precision(np.float64):
+        if padding == "SAME":
+            ref = O.conv2d_direct(x, g[:, 0], pad)
+        else:
+            ref = O.conv2d_direct(x, g[:, 0], (0, 0))
+    assert rel_l2(host(z), ref) < FWD_TOL
+
+
+@pytest.mark.parametrize("mode,bbox", [("continuous", None), ("ste_ternary", CROP),
+                                       ("annealed", None)])
+def test_precompute_step_params_autograd(mode, bbox):
+    from neurocell import precompute_step_params, VNNParams
+    from neurocell.topology import ChipTopology2D
+    geom, cell, filt, _, _ = alu_case(5, B=1)
+    topo = ChipTopology2D.alu_chip(out_width=2)
+    ct = dev(cell).requires_grad_()
+    sp = precompute_step_params(VNNParams(ct, dev(filt)), topo, roi_bbox=bbox, codd_mode=mode,
+                                state_temperature=0.3)
+    ref = O.precompute_step_params(cell, geom, roi_bbox=bbox, mode=mode, tau=0.3)
+    rng = np.random.default_rng(6)
+    keys = ("w_eff_roi", "s_eff_roi", "b_roi", "w_eff_out", "s_eff_out", "b_out")
+    grads = {k: rng.normal(size=ref[k].shape) for k in keys}
+    loss = 0
+    for k in keys:
+        assert rel_l2(host(getattr(sp, k)), ref[k]) < FWD_TOL, k
+        loss = loss + (getattr(sp, k) * dev(grads[k].astype(np.float32))).sum()
+    assert rel_l2(host(sp.s_prob), ref["s_prob"]) < FWD_TOL
+    loss.backward()
+    r_g = O.precompute_step_params_vjp(cell, geom, grads, roi_bbox=bbox, mode=mode, tau=0.3)
+    assert rel_l2(host(ct.grad), r_g) < GRAD_TOL
+
+
+@pytest.mark.parametrize("mode", ["continuous", "annealed", "ste_binary", "ste_ternary"])
+def test_codd_state_probs_autograd(mode):
+    from neurocell import compute_codd_state_probs
+    geom, cell, _, _, _ = alu_case(7, B=1)
+    s = dev(cell[2]).requires_grad_()
+    p = compute_codd_state_probs(s, geom.io_state_mask, codd_mode=mode, state_temperature=0.5)
+    g = np.random.default_rng(8).normal(size=p.shape).astype(np.float32)
+    p.backward(dev(g))
+    rp, rd = O.codd_state_probs(cell[2], geom.io_state_mask, mode=mode, tau=0.5)
+    assert rel_l2(host(p), rp) < FWD_TOL
+    assert rel_l2(host(s.grad), rd * g) < GRAD_TOL
+
+
+# ------------------------------------------------------------------ propagation
+
+@pytest.mark.parametrize("mode,tau,bbox", [("continuous", 1.0, None), ("ste_ternary", 0.1, CROP)])
+def test_propagate_autograd(mode, tau, bbox):
+    from neurocell import VNNParams, propagate_vnn_2d
+    from neurocell.topology import ChipTopology2D
+    geom, cell, filt, x, _ = alu_case(9, B=8)
+    topo = ChipTopology2D.alu_chip(out_width=2)
+    p = VNNParams(dev(cell).requires_grad_(), dev(filt).requires_grad_())
+    out = propagate_vnn_2d(p, dev(x), topo, codd_mode=mode, state_temperature=tau,
+                           spatial_mask=mask(bbox))
+    g = np.random.default_rng(10).normal(size=tuple(out.shape)).astype(np.float32)
+    out.backward(dev(g))
+    r_out, r_gc, r_gf = O.propagate_vjp(cell, filt, x, geom, g, roi_bbox=bbox, mode=mode,
+                                        tau=tau)
+    assert rel_l2(host(out), r_out) < FWD_TOL
+    assert rel_l2(host(p.cell_params.grad), r_gc) < GRAD_TOL
+    assert rel_l2(host(p.greens_filters.grad), r_gf) < GRAD_TOL
+
+
+def test_two_live_graphs():
+    """Two forwards kept alive before their backwards (each call owns its activations)."""
+    from neurocell import VNNParams, propagate_vnn_2d
+    from neurocell.topology import ChipTopology2D
+    geom, cell, filt, x, _ = alu_case(11, B=8)
+    topo = ChipTopology2D.alu_chip(out_width=2)
+    p = VNNParams(dev(cell).requires_grad_(), dev(filt).requires_grad_())
+    o1 = propagate_vnn_2d(p, dev(x[:4].copy()), topo)
+    o2 = propagate_vnn_2d(p, dev(x[4:].copy()), topo)
+    (o1.sum() + 2.0 * o2.sum()).backward()
+    g = np.ones((8,) + geom.out_size, np.float32)
+    g[4:] = 2.0
+    _, r_gc, r_gf = O.propagate_vjp(cell, filt, x, geom, g)
+    assert rel_l2(host(p.cell_params.grad), r_gc) < GRAD_TOL
+    assert rel_l2(host(p.greens_filters.grad), r_gf) < GRAD_TOL
+
+
+# ------------------------------------------------------------------ model
+
+def test_model_checkpoint_and_states(tmp_path):
+    from neurocell import VonNeumannNetwork
+    from neurocell.topology import ChipTopology2D
+    geom, _, _, x, _ = alu_case(12, B=4)
+    topo = ChipTopology2D.alu_chip(out_width=2)
+    model = VonNeumannNetwork(topo, codd_mode="ste_ternary", state_temperature=0.2)
+    params = model.init(42)
+    assert params.cell_params.shape == (3, 62, 62) and params.greens_filters.shape == (16, 1, 23, 13)
+    f = tmp_path / "ck.npz"
+    model.save_checkpoint(str(f), params, note=np.int32(7))
+    back = VonNeumannNetwork.load_checkpoint(str(f))
+    assert torch.equal(back.cell_params, params.cell_params)
+    assert torch.equal(back.greens_filters, params.greens_filters)
+    cell, filt = host(params.cell_params), host(params.greens_filters)
+    out = model.apply(params, dev(x))
+    r_out, _ = O.propagate(cell, filt, x, geom, mode="ste_ternary", tau=0.2)
+    assert rel_l2(host(out), r_out) < FWD_TOL
+    s = model.effective_states(params)
+    r_s, _ = O.codd_state_probs(cell[2], geom.io_state_mask, mode="ste_ternary", tau=0.2)
+    assert rel_l2(host(s), r_s) < FWD_TOL
+    th = host(VonNeumannNetwork.threshold_states(params.states))
+    sr = cell[2]
+    ref = np.where(sr >= 0.6, 2.0, sr)
+    ref = np.where((ref > 0) & (ref < 0.6), 1.0, ref)
+    assert np.array_equal(th, ref.astype(np.float32))
+
+
+# ------------------------------------------------------------------ trainer
+
+def _oracle_steps(cell, filt, xs, ys, geom, lr, n, bbox=None, mode="continuous", tau=1.0):
+    p = np.concatenate([cell.ravel(), filt.ravel()]).astype(np.float64)
+    m = np.zeros_like(p)
+    v = np.zeros_like(p)
+    nc = cell.size
+    losses = []
+    for i in range(n):
+        c = p[:nc].reshape(cell.shape).astype(np.float32)
+        f = p[nc:].reshape(filt.shape).astype(np.float32)
+        out, _ = O.propagate(c, f, xs[i], geom, roi_bbox=bbox, mode=mode, tau=tau)
+        loss, g_out = O.mse_loss(out, ys[i])
+        _, gc, gf = O.propagate_vjp(c, f, xs[i], geom, g_out, roi_bbox=bbox, mode=mode, tau=tau)
+        g = np.concatenate([gc.ravel(), gf.ravel()])
+        p, m, v, _ = O.adamw_step(p, g, m, v, i, lr(i) if callable(lr) else lr)
+        losses.append(loss)
+    return p[:nc].reshape(cell.shape), p[nc:].reshape(filt.shape), np.array(losses)
+
+
+def _trainer_case(seed, nb, B=8, out_width=2):
+    from neurocell.topology import ChipTopology2D
+    geom, cell, filt, _, _ = alu_case(seed, B=1, out_width=out_width)
+    xs, ys = [], []
+    for i in range(nb):
+        _, _, _, x, y = alu_case(seed * 100 + i, B=B, out_width=out_width)
+        xs.append(x)
+        ys.append(y)
+    return geom, ChipTopology2D.alu_chip(out_width=out_width), cell, filt, np.stack(xs), \
+        np.stack(ys)
+
+
+@pytest.mark.parametrize("variant", ["plain", "adaptive", "annealed"])
+def test_trainer_steps_vs_oracle(variant):
+    from neurocell import VNNParams, VNNTrainer, VonNeumannNetwork, adamw
+    from neurocell import warmup_cosine_decay_schedule as wcd
+    geom, topo, cell, filt, xs, ys = _trainer_case(13, nb=2)
+    sched = wcd(0.001, 0.03, 1, 10, 0.0005)
+    model = VonNeumannNetwork(topo)
+    tr = VNNTrainer(model.apply, adamw(sched), batch_size=8)
+    params = VNNParams(dev(cell), dev(filt))
+    state = tr.optimizer.init(params)
+    bbox, mode, tau = None, "continuous", 1.0
+    losses = []
+    for i in range(2):
+        if variant == "plain":
+            params, state, loss = tr.train_step(params, state, dev(xs[i]), dev(ys[i]))
+        elif variant == "adaptive":
+            bbox = CROP
+            params, state, loss = tr.train_step_adaptive(params, state, dev(xs[i]), dev(ys[i]),
+                                                         mask(bbox))
+        else:
+            mode, tau = "ste_ternary", 0.5
+            params, state, loss = tr.train_step_annealed(params, state, dev(xs[i]), dev(ys[i]),
+                                                         state_temperature=tau, codd_mode=mode)
+        losses.append(float(loss))
+    r_c, r_f, r_l = _oracle_steps(cell, filt, xs, ys, geom, sched, 2, bbox, mode, tau)
+    assert rel_l2(losses, r_l) < FWD_TOL
+    assert rel_l2(host(params.cell_params) - cell, r_c - cell) < TRAJ_TOL
+    assert rel_l2(host(params.greens_filters) - filt, r_f - filt) < TRAJ_TOL
+    assert int(state.count.item()) == 2
+
+
+def test_trainer_graph_replay_matches_eager():
+    """Epoch graphs (first call eager, second captured, later replayed) against a trainer that
+    always launches eagerly: bit-identical parameters, moments and losses, with eager work and
+    synchronisations between replays."""
+    from neurocell import VNNParams, VNNTrainer, VonNeumannNetwork, adamw
+    _, topo, cell, filt, xs, ys = _trainer_case(14, nb=3)
+    model = VonNeumannNetwork(topo)
+    res = []
+    for use_graphs in (True, False):
+        tr = VNNTrainer(model.apply, adamw(0.01), batch_size=8, use_graphs=use_graphs)
+        params = VNNParams(dev(cell), dev(filt))
+        state = tr.optimizer.init(params)
+        x, y = dev(xs), dev(ys)
+        ep = []
+        for e in range(4):
+            params, state, loss = tr.train_epoch(params, state, x, y)
+            torch.cuda.synchronize()
+            ep.append(float(loss))
+            _ = torch.ones(1000, device="cuda").sum()  # unrelated eager work between replays
+        res.append((host(params.cell_params), host(params.greens_filters),
+                    host(state.mu.cell_params), np.array(ep)))
+    for a, b in zip(*res):
+        assert np.array_equal(a, b)
+
+
+def test_trainer_generic_path_matches_fused():
+    from neurocell import (VNNParams, VNNTrainer, VonNeumannNetwork, adamw, default_mse_loss)
+    _, topo, cell, filt, xs, ys = _trainer_case(15, nb=2)
+    model = VonNeumannNetwork(topo)
+    outs = []
+    for loss_fn in (None, default_mse_loss):
+        tr = VNNTrainer(model.apply, adamw(0.01), batch_size=8, loss_fn=loss_fn)
+        assert tr.fused == (loss_fn is None)
+        params = VNNParams(dev(cell), dev(filt))
+        state = tr.optimizer.init(params)
+        params, state, loss = tr.train_epoch(params, state, dev(xs), dev(ys))
+        outs.append((host(params.cell_params), host(params.greens_filters), float(loss)))
+    (c0, f0, l0), (c1, f1, l1) = outs
+    assert abs(l0 - l1) <= 1e-5 * abs(l1)
+    assert rel_l2(c0 - cell, c1 - cell) < TRAJ_TOL
+    assert rel_l2(f0 - filt, f1 - filt) < TRAJ_TOL
+
+
+def test_evaluate_packed_and_metric():
+    from neurocell import VNNParams, VNNTrainer, VonNeumannNetwork, adamw
+    geom, topo, cell, filt, xs, ys = _trainer_case(16, nb=2, out_width=1)
+    model = VonNeumannNetwork(topo)
+    tr = VNNTrainer(model.apply, adamw(0.01), batch_size=8)
+    params = VNNParams(dev(cell), dev(filt))
+    ref_out = np.stack([O.propagate(cell, filt, xs[i], geom)[0] for i in range(2)])
+    bits = np.clip(np.round(ref_out.reshape(2, 8, 8)), 0, 255).astype(np.int64)
+    ref_pred = (bits * np.array([128, 64, 32, 16, 8, 4, 2, 1])).sum(-1) % 256
+    rng = np.random.default_rng(17)
+    y_packed = np.where(rng.random((2, 8)) < 0.5, ref_pred, rng.integers(0, 256, (2, 8)))
+    y_packed = y_packed.astype(np.uint8)[..., None]
+    acc, preds = tr.evaluate_packed(params, dev(xs), dev(y_packed))
+    near_half = np.abs(np.abs(ref_out - np.round(ref_out)) - 0.5) < 1e-4
+    ok = ~near_half.reshape(2, 8, 8).any(-1)
+    assert np.array_equal(host(preds)[..., 0][ok], ref_pred[ok])
+    hits = (host(preds) == y_packed).mean(axis=(1, 2))
+    assert abs(float(acc) - float(hits.mean())) < 1e-6
+    m = tr.evaluate_metric(params, dev(xs), dev(ys.reshape(2, 8, 8)))
+    r_m = np.mean([(np.round(ref_out[i].reshape(8, 8)) == np.round(ys[i].reshape(8, 8))).mean()
+                   for i in range(2)])
+    assert abs(float(m) - r_m) < 1e-6
+
+
+def test_train_epochs_runs():
+    from neurocell import VNNParams, VNNTrainer, VonNeumannNetwork, adamw
+    _, topo, cell, filt, xs, ys = _trainer_case(18, nb=3)
+    model = VonNeumannNetwork(topo)
+    tr = VNNTrainer(model.apply, adamw(0.01), batch_size=8)
+    params = VNNParams(dev(cell), dev(filt))
+    state = tr.optimizer.init(params)
+    x = dev(xs.reshape(24, 3, 8, 1))
+    y = dev(ys.reshape(24, 8, 2))
+    params, state, losses = tr.train_epochs(params, state, x, y, rng=0, num_epochs=3)
+    assert losses.shape == (3,) and torch.isfinite(losses).all()
+    assert int(state.count.item()) == 9
