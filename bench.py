@@ -160,6 +160,11 @@ def main():
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly, no HIP graph")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline")
     ap.add_argument("--kernel-reps", type=int, default=200)
+    ap.add_argument("--no-eval", action="store_true", help="skip the evaluation legs")
+    ap.add_argument("--families-only", action="store_true",
+                    help="profiling aid: one eager train step, a 256 MiB device copy (the "
+                         "traffic-counter calibration), then --kernel-reps calls of each "
+                         "kernel family; prints a one-line note, no JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU (--gpus {args.gpus} requested); "
@@ -183,6 +188,17 @@ def main():
     ts = TrainState(plan, ps)
     ts.x.copy_(flatten_inputs(xt, topo))
     ts.y.copy_(torch.from_numpy(y.reshape(B, -1)).to(dev))
+    if args.families_only:
+        ts.step()
+        src = torch.empty(64 << 20, device=dev, dtype=torch.float32).normal_()
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        fams = kernel_families(ts, torch, args.kernel_reps)
+        torch.cuda.synchronize()
+        print("families-only: copy 256 MiB x3; " + ", ".join(
+            f"{k} {us:.1f} us" for k, (us, _) in fams.items()))
+        return
     if not args.no_graph:
         ts.capture()
     for _ in range(args.warmup):
@@ -203,8 +219,10 @@ def main():
 
     # evaluation throughput (config 1 and config 0 batch)
     evals = {}
-    for name, eb, mode, tau in (("config1_B1024_ste_ternary", 1024, "ste_ternary", 0.1),
-                                ("B128_continuous", 128, "continuous", 1.0)):
+    eval_cases = () if args.no_eval else (
+        ("config1_B1024_ste_ternary", 1024, "ste_ternary", 0.1),
+        ("B128_continuous", 128, "continuous", 1.0))
+    for name, eb, mode, tau in eval_cases:
         _, _, xe, _ = synthetic_config0(1, eb)
         xet = torch.from_numpy(xe).to(dev)
         ep = StepPlan(topo, eb, port_input_shapes(xet, topo), training=False)
@@ -240,7 +258,10 @@ def main():
     tpath = os.path.join(ROOT, "profiles", "traffic_config0.json")
     if os.path.exists(tpath):
         with open(tpath) as fh:
-            traffic = json.load(fh).get(dom)
+            entry = json.load(fh).get(dom)
+        # HBM bytes per launch from the FETCH_SIZE / WRITE_SIZE counter passes, scaled by
+        # what the counters read for a plain 256 MiB copy
+        traffic = entry.get("traffic_bytes") if isinstance(entry, dict) else None
 
     cpu = None
     if not args.no_cpu:
@@ -268,7 +289,8 @@ def main():
         "device_ms_per_step": round(dev_ms, 4),
         "final_loss": round(loss, 6),
         "eval": evals,
-        "eval_samples_per_s": evals["config1_B1024_ste_ternary"]["samples_per_s"],
+        "eval_samples_per_s": (evals["config1_B1024_ste_ternary"]["samples_per_s"]
+                               if evals else None),
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
