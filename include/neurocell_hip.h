@@ -125,7 +125,8 @@ int nc_filter_spectrum_bwd(void* stream, int M, int kh, int kw, int fft_h, int f
  * hoisted border conv (propagator.py:362-366).
  * x (B, hin, win) real, placed at the spectral origin; z (B, M, hout, wout) =
  * irfft2(rfft2(x) * ghat)[pad_h : pad_h+hout, pad_w : pad_w+wout].  xhat (B, fft_h,
- * fft_w/2+1) complex (the saved cell_freq residual) is written when non-NULL.
+ * fft_w/2+1) complex receives the cell spectra (the saved cell_freq residual); it is required
+ * (the correlation reads it back).
  * Supported spectral grids: fft_h, fft_w in {16, 32, 64}.
  */
 int nc_fftconv_fwd(void* stream, int B, int M, int hin, int win, int hout, int wout, int pad_h,

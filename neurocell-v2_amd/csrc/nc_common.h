@@ -8,6 +8,14 @@
 #include "../../include/neurocell_hip.h"
 
 #define NC_DEV __device__ __forceinline__
+
+// Compiler scheduling pins: NC_PIN(x) makes x a value that must exist at this point (in a
+// VGPR), NC_FENCE() keeps memory operations on their side.  Both emit no instruction.  (A
+// test harness that compiles these sources for the CPU predefines them.)
+#ifndef NC_PIN
+#define NC_PIN(x) asm volatile("" : "+v"(x))
+#define NC_FENCE() asm volatile("" ::: "memory")
+#endif
 #define NC_WAVE 64
 
 // Status of a launch sequence: the first failing HIP call's code, else NC_OK.

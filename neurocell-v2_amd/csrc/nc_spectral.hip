@@ -1,20 +1,27 @@
-// Piece 2: Green's-function convolution as LDS-resident, row-pruned overlap-save rfft2.
+// Piece 2: Green's-function convolution as row-pruned overlap-save rfft2 correlation.
 //
-// Kernels (one (FH x FW) plane per workgroup step, FH, FW in {16, 32, 64}):
-//   k_filter_spectrum_fwd  grid (M)           ghat_m = rfft2(flip(G_m))
-//   k_filter_spectrum_bwd  grid (M)           dG_m = flip(crop(roll(irfft2(dghat_m))))
-//   k_fftconv_fwd          grid (B, M/MC)     xhat_b once per workgroup, then for each m:
-//                                             z_bm = irfft2(xhat_b * ghat_m) (cropped window)
-//   k_fftconv_bwd_dx       grid (B, MS)       A_b = sum_m rfft2(gz_bm) * conj(ghat_m) over an
-//                                             M-split; with MS == 1 the inverse runs in place
-//   k_fftconv_bwd_dx_fin   grid (B)           sums the MS partial spectra (fixed order), irfft2
-//   k_fftconv_bwd_dg       grid (M, NBC)      D_m = sum_b rfft2(gz_bm) * conj(xhat_b) over a
-//                                             B-chunk (kept in registers)
-//   k_fftconv_bwd_dg_fin   grid (M, F/256)    sums the NBC chunk partials in fixed order
+// Spectral grids of 16, 32 or 64 points per axis run wavefront-level transforms (nc_wave.h):
+// one 64-lane wavefront owns PPW = 128 / FW planes, every 1D transform lives in one lane's
+// registers and one LDS transposition separates the passes.  Spectra are (FH, FW/2+1)
+// complex64 half-spectra in HBM; partial spectra use the packed (FH, FW/2) layout whose
+// column 0 carries DC + i*Nyquist.
+//
+//   k_wrfft2<FLIP>        grid (planes/PPW)        half-spectra of real planes: the cell spectra
+//                                                  xhat_b and (FLIP) ghat_m = rfft2(flip(G_m))
+//   k_wconv_fwd           grid (B*M/PPW)           z_bm = irfft2(xhat_b * ghat_m), cropped window
+//   k_wbwd_dx             grid (M/PPW, B)          sum over the wave's directions of
+//                                                  rfft2(gz_bm) * conj(ghat_m)
+//   k_wbwd_dx_fin         grid (B/PPW)             fixed-order sum of those partials, irfft2 with
+//                                                  the unshifted roll -> dx_b
+//   k_wbwd_dg             grid (M/PPW, chunks)     sum over a B-chunk of rfft2(gz_bm) * conj(xhat_b)
+//                                                  (registers)
+//   k_wbwd_dg_fin         grid (F/256, M)          fixed-order sum over chunks, unpacked -> dghat
+//   k_filter_spectrum_bwd grid (M)                 dG_m = flip(crop(roll(irfft2(dghat_m))))
 // No atomics anywhere: the M- and B-reductions are two-stage trees in the frequency domain.
 #include <algorithm>
+#include <cstdint>
 
-#include "nc_fft.h"
+#include "nc_wave.h"
 
 namespace {
 
@@ -26,29 +33,14 @@ struct Smem {
     cpx tw[NC_TW_N];
 };
 
-// Every kernel starts by copying the twiddle table into LDS.
+// Every workgroup-FFT kernel starts by copying the twiddle table into LDS.
 #define NC_SPECTRAL_PROLOGUE(sm) \
     load_twiddles(sm.tw);        \
     __syncthreads()
 
 // ----------------------------------------------------------------------------------------
-// Filter spectrum (kernels_greens.py:240-259) and its backward (kernels_pallas.py:1558-1579)
+// Filter spectrum backward (kernels_pallas.py:1558-1579)
 // ----------------------------------------------------------------------------------------
-
-template <int FH, int FW>
-__global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_filter_spectrum_fwd(
-    int kh, int kw, const float* __restrict__ filt, cpx* __restrict__ ghat) {
-    using P = Plane<FH, FW>;
-    __shared__ cpx S[P::F];
-    __shared__ Smem<FH, FW> sm;
-    NC_SPECTRAL_PROLOGUE(sm);
-    const int m = blockIdx.x;
-    const float* g = filt + (size_t)m * kh * kw;
-    // flipped filter: x[r][c] = G[kh-1-r][kw-1-c]
-    plane_rfft2<FH, FW>([&](int r, int c) { return g[(kh - 1 - r) * kw + (kw - 1 - c)]; },
-                        kh, kw, S, sm.work, sm.scr, sm.tw);
-    for (int e = threadIdx.x; e < P::F; e += P::NT) ghat[(size_t)m * P::F + e] = S[e];
-}
 
 template <int FH, int FW>
 __global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_filter_spectrum_bwd(
@@ -76,156 +68,227 @@ __global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_filter_spectrum_bwd(
 }
 
 // ----------------------------------------------------------------------------------------
-// Forward correlation (kernels_pallas.py:1779-1791; kernels_greens.py:316-343)
+// Wavefront kernels (one 64-lane wavefront per workgroup)
 // ----------------------------------------------------------------------------------------
 
-template <int FH, int FW>
-__global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_fftconv_fwd(
-    int M, int mc, int hin, int win, int hout, int wout, int ph, int pw,
-    const float* __restrict__ x, const cpx* __restrict__ ghat, float* __restrict__ z,
-    cpx* __restrict__ xhat) {
-    using P = Plane<FH, FW>;
-    __shared__ cpx S[P::F];
-    __shared__ Smem<FH, FW> sm;
-    __shared__ float O[FH * FW];
-    NC_SPECTRAL_PROLOGUE(sm);
-    const int b = blockIdx.x;
-    const int m0 = blockIdx.y * mc;
-    const int m1 = min(M, m0 + mc);
-    // stage the sample's plane (coalesced) into S, which the row pass reads before the
-    // column pass overwrites it with the spectrum
-    float* Sf = reinterpret_cast<float*>(S);
-    stage_plane(x + (size_t)b * hin * win, hin * win, Sf);
+// Half-spectra of nplanes real (hin x win) planes stored back to back in x (FLIP: the plane
+// is read flipped in both axes, which turns the correlation filter into a convolution
+// kernel, kernels_greens.py:240-259).  out: (nplanes, FH, FW/2+1).
+template <int FH, int FW, bool FLIP>
+__global__ __launch_bounds__(64) void k_wrfft2(int nplanes, int hin, int win, int s_off, int vec,
+                                               const float* __restrict__ x,
+                                               cpx* __restrict__ out) {
+    using W = WGeo<FH, FW>;
+    HIP_DYNAMIC_SHARED(float, lds)
+    cpx* T = reinterpret_cast<cpx*>(lds);
+    float* S = lds + s_off;
+    const int lane = threadIdx.x;
+    const int g0 = blockIdx.x * W::PPW;
+    const int np = min(W::PPW, nplanes - g0);
+    istage<FW, W::PPW, FLIP>(x + (size_t)g0 * hin * win, (size_t)hin * win, np, hin, win,
+                             vec != 0, S);
     __syncthreads();
-    plane_rfft2<FH, FW>([&](int r, int c) { return Sf[r * win + c]; }, hin, win, S, sm.work,
-                        sm.scr, sm.tw);
-    if (xhat != nullptr && blockIdx.y == 0)
-        for (int e = threadIdx.x; e < P::F; e += P::NT) xhat[(size_t)b * P::F + e] = S[e];
-    const int npix = hout * wout;
-    const float scale = 1.0f / (float)(FH * FW);
-    for (int m = m0; m < m1; ++m) {
-        const cpx* G = ghat + (size_t)m * P::F;
-        plane_irfft2<FH, FW>(
-            [&](int a, int c) { return cmul(S[a * P::SP + c], G[a * P::SP + c]); }, ph, hout,
-            pw, wout, scale, [&](int i, int j, float v) { O[i * wout + j] = v; }, sm.work,
-            sm.scr, sm.tw);
-        float* zo = z + ((size_t)b * M + m) * npix;
-        for (int e = threadIdx.x; e < npix; e += P::NT) zo[e] = O[e];
-        // O is rewritten only after the next inverse's column phase barriers.
-    }
-}
-
-// ----------------------------------------------------------------------------------------
-// Backward: dx (M-reduction) and dghat (B-reduction), kernels_pallas.py:1794-1821
-// ----------------------------------------------------------------------------------------
-
-template <int FH, int FW>
-__global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_fftconv_bwd_dx(
-    int M, int ms_size, int hin, int win, int hout, int wout, int ph, int pw,
-    const float* __restrict__ gz, const cpx* __restrict__ ghat, cpx* __restrict__ part,
-    float* __restrict__ dx) {
-    using P = Plane<FH, FW>;
-    __shared__ cpx S[P::F];
-    __shared__ cpx A[P::F];
-    __shared__ Smem<FH, FW> sm;
-    NC_SPECTRAL_PROLOGUE(sm);
-    const int b = blockIdx.x;
-    const int m0 = blockIdx.y * ms_size;
-    const int m1 = min(M, m0 + ms_size);
-    const int npix = hout * wout;
-    float* Sf = reinterpret_cast<float*>(S);
-    for (int e = threadIdx.x; e < P::F; e += P::NT) A[e] = cmk(0.f, 0.f);
-    for (int m = m0; m < m1; ++m) {
-        stage_plane(gz + ((size_t)b * M + m) * npix, npix, Sf);
-        __syncthreads();
-        plane_rfft2<FH, FW>([&](int r, int c) { return Sf[r * wout + c]; }, hout, wout, S,
-                            sm.work, sm.scr, sm.tw);
-        const cpx* G = ghat + (size_t)m * P::F;
-        for (int e = threadIdx.x; e < P::F; e += P::NT) A[e] = cadd(A[e], cmulc(S[e], G[e]));
-        __syncthreads();  // S is restaged by the next direction
-    }
-    if (part != nullptr) {  // M split across workgroups: emit the partial spectrum
-        cpx* dst = part + ((size_t)b * gridDim.y + blockIdx.y) * P::F;
-        for (int e = threadIdx.x; e < P::F; e += P::NT) dst[e] = A[e];
-        return;
-    }
-    float* d = dx + (size_t)b * hin * win;
-    plane_irfft2<FH, FW>(
-        [&](int a, int c) { return A[a * P::SP + c]; }, (FH - ph) & (FH - 1), hin,
-        (FW - pw) & (FW - 1), win, 1.0f / (float)(FH * FW),
-        [&](int i, int j, float v) { d[i * win + j] = v; }, sm.work, sm.scr, sm.tw);
-}
-
-template <int FH, int FW>
-__global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_fftconv_bwd_dx_fin(
-    int nsplit, int hin, int win, int ph, int pw, const cpx* __restrict__ part,
-    float* __restrict__ dx) {
-    using P = Plane<FH, FW>;
-    __shared__ cpx A[P::F];
-    __shared__ Smem<FH, FW> sm;
-    NC_SPECTRAL_PROLOGUE(sm);
-    const int b = blockIdx.x;
-    const cpx* src = part + (size_t)b * nsplit * P::F;
-    for (int e = threadIdx.x; e < P::F; e += P::NT) {
-        cpx s = src[e];
-        for (int k = 1; k < nsplit; ++k) s = cadd(s, src[(size_t)k * P::F + e]);
-        A[e] = s;
-    }
+    wrow_fwd<FH, FW>(S, hin, T);
     __syncthreads();
-    float* d = dx + (size_t)b * hin * win;
-    plane_irfft2<FH, FW>(
-        [&](int a, int c) { return A[a * P::SP + c]; }, (FH - ph) & (FH - 1), hin,
-        (FW - pw) & (FW - 1), win, 1.0f / (float)(FH * FW),
-        [&](int i, int j, float v) { d[i * win + j] = v; }, sm.work, sm.scr, sm.tw);
-}
-
-template <int FH, int FW>
-__global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_fftconv_bwd_dg(
-    int B, int M, int bc, int hout, int wout, const float* __restrict__ gz,
-    const cpx* __restrict__ xhat, cpx* __restrict__ part) {
-    using P = Plane<FH, FW>;
-    constexpr int PER = (P::F + P::NT - 1) / P::NT;
-    __shared__ cpx S[P::F];
-    __shared__ Smem<FH, FW> sm;
-    NC_SPECTRAL_PROLOGUE(sm);
-    const int m = blockIdx.x;
-    const int b0 = blockIdx.y * bc;
-    const int b1 = min(B, b0 + bc);
-    const int npix = hout * wout;
-    float* Sf = reinterpret_cast<float*>(S);
-    cpx acc[PER];
+    cpx v[FH];
+    wcol_fwd<FH, FW>(T, hin, v);
+    const int ps = lane / W::NC, kc = lane % W::NC;
+    if (ps >= np) return;
+    cpx* o = out + (size_t)(g0 + ps) * W::F + kc;
+    if (kc == 0) {
 #pragma unroll
-    for (int u = 0; u < PER; ++u) acc[u] = cmk(0.f, 0.f);
-    for (int b = b0; b < b1; ++b) {
-        stage_plane(gz + ((size_t)b * M + m) * npix, npix, Sf);
-        __syncthreads();
-        plane_rfft2<FH, FW>([&](int r, int c) { return Sf[r * wout + c]; }, hout, wout, S,
-                            sm.work, sm.scr, sm.tw);
-        const cpx* X = xhat + (size_t)b * P::F;
-#pragma unroll
-        for (int u = 0; u < PER; ++u) {
-            const int e = threadIdx.x + u * P::NT;
-            if (e < P::F) acc[u] = cadd(acc[u], cmulc(S[e], X[e]));
+        for (int kh = 0; kh < FH; ++kh) {
+            const cpx c = v[kh], d = cconj(v[(FH - kh) & (FH - 1)]);
+            o[kh * W::SP] = cscale(cadd(c, d), 0.5f);
+            o[kh * W::SP + FW / 2] = cmul_negi(cscale(csub(c, d), 0.5f));
         }
-        __syncthreads();  // S is restaged by the next sample
-    }
-    cpx* dst = part + ((size_t)blockIdx.y * M + m) * P::F;
+    } else {
 #pragma unroll
-    for (int u = 0; u < PER; ++u) {
-        const int e = threadIdx.x + u * P::NT;
-        if (e < P::F) dst[e] = acc[u];
+        for (int kh = 0; kh < FH; ++kh) o[kh * W::SP] = v[kh];
     }
 }
 
-__global__ void k_fftconv_bwd_dg_fin(int nchunk, int M, int F, const cpx* __restrict__ part,
-                                     cpx* __restrict__ dghat, int accumulate, int conj_out) {
-    const int m = blockIdx.x;
-    const int e = blockIdx.y * blockDim.x + threadIdx.x;
-    if (e >= F) return;
-    cpx s = part[(size_t)m * F + e];
-    for (int k = 1; k < nchunk; ++k) s = cadd(s, part[((size_t)k * M + m) * F + e]);
+// Forward correlation (kernels_pallas.py:1779-1791; kernels_greens.py:316-343): plane
+// g = b*M + m of z (B, M, hout, wout) is irfft2(xhat_b * ghat_m) read from row ph, column pw.
+template <int FH, int FW>
+__global__ __launch_bounds__(64) void k_wconv_fwd(int nplanes, int M, int hout, int wout, int ph,
+                                                  int pw, int o_off, int nq_off, int vec,
+                                                  const cpx* __restrict__ xhat,
+                                                  const cpx* __restrict__ ghat,
+                                                  float* __restrict__ z) {
+    using W = WGeo<FH, FW>;
+    HIP_DYNAMIC_SHARED(float, lds)
+    cpx* T = reinterpret_cast<cpx*>(lds);
+    float* O = lds + o_off;
+    cpx* NQ = reinterpret_cast<cpx*>(lds) + nq_off;
+    const int lane = threadIdx.x, ps = lane / W::NC, kc = lane % W::NC;
+    const int g0 = blockIdx.x * W::PPW;
+    const int np = min(W::PPW, nplanes - g0);
+    const int g = g0 + min(ps, np - 1);
+    const int b = g / M, m = g - b * M;
+    const cpx* X = xhat + (size_t)b * W::F;
+    const cpx* G = ghat + (size_t)m * W::F;
+    cpx v[FH];
+#pragma unroll
+    for (int kh = 0; kh < FH; ++kh) v[kh] = cmul(X[kh * W::SP + kc], G[kh * W::SP + kc]);
+    // Nyquist-column products, spread over the lanes, for the packed column
+    for (int kh = kc; kh < FH; kh += W::NC)
+        NQ[ps * FH + kh] = cmul(X[kh * W::SP + FW / 2], G[kh * W::SP + FW / 2]);
+    __syncthreads();
+    if (kc == 0) {
+#pragma unroll
+        for (int kh = 0; kh < FH; ++kh) v[kh] = cadd(v[kh], cmul_i(NQ[ps * FH + kh]));
+    }
+    wcol_inv<FH, FW>(v, ph, hout, T);
+    __syncthreads();
+    wrow_inv<FH, FW>(T, pw, hout, 1.0f / (float)(FH * FW), O);
+    __syncthreads();
+    ostage_copy<FW>(O, np, hout, wout, z + (size_t)g0 * hout * wout);
+}
+
+// First stage of both reductions of the backward (kernels_pallas.py:1794-1821), in the packed
+// layout.  The wavefront transforms PPW planes of gz and sums their products with a conjugated
+// real-signal spectrum:
+//   DG == false (dx): planes (b, m = j*PPW + ps), reference ghat_m; part[b][j]   (grid MG x B)
+//   DG == true  (dG): planes (b = j*PPW + ps, m), reference xhat_b; part[j][m]   (grid M x BG)
+// Planes past the end are staged as zeros and contribute nothing.
+template <int FH, int FW, bool DG>
+__global__ __launch_bounds__(64) void k_wbwd_part(int B, int M, int hout, int wout, int s_off,
+                                                  int nq_off, int vec,
+                                                  const float* __restrict__ gz,
+                                                  const cpx* __restrict__ ref,
+                                                  cpx* __restrict__ part) {
+    using W = WGeo<FH, FW>;
+    HIP_DYNAMIC_SHARED(float, lds)
+    cpx* T = reinterpret_cast<cpx*>(lds);
+    float* S = lds + s_off;
+    cpx* NQ = reinterpret_cast<cpx*>(lds) + nq_off;
+    const int lane = threadIdx.x, ps = lane / W::NC, kc = lane % W::NC;
+    const size_t n = (size_t)hout * wout;
+    int b0, m0, np;
+    size_t pstride;
+    if (DG) {
+        m0 = blockIdx.x;
+        b0 = blockIdx.y * W::PPW;
+        np = min(W::PPW, B - b0);
+        pstride = (size_t)M * n;
+    } else {
+        b0 = blockIdx.y;
+        m0 = blockIdx.x * W::PPW;
+        np = min(W::PPW, M - m0);
+        pstride = n;
+    }
+    istage<FW, W::PPW, false>(gz + ((size_t)b0 * M + m0) * n, pstride, np, hout, wout, vec != 0,
+                              S);
+    const int q = min(ps, np - 1);
+    const cpx* R = ref + (size_t)(DG ? b0 + q : m0 + q) * W::F;
+    cpx r[FH];  // the reference column, loaded while the transform runs
+#pragma unroll
+    for (int kh = 0; kh < FH; ++kh) r[kh] = R[kh * W::SP + kc];
+    stage_nyquist<FH, FW>(
+        [&](int p) { return ref + (size_t)(DG ? b0 + min(p, np - 1) : m0 + min(p, np - 1)) * W::F; },
+        NQ);
+    __syncthreads();
+    wrow_fwd<FH, FW>(S, hout, T);
+    __syncthreads();
+    cpx v[FH];
+    wcol_fwd<FH, FW>(T, hout, v);
+    packed_mulc<FH>(v, r, kc, [&](int kh) { return NQ[ps * FH + kh]; });
+    // sum over the wavefront's planes, half a spectrum at a time, through T
+    constexpr int HH = FH / 2;
+    cpx* red = T;
+    cpx* dst = part + (DG ? ((size_t)blockIdx.y * M + m0) : ((size_t)b0 * gridDim.x + blockIdx.x)) *
+                          W::PF;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < HH; ++k) red[(ps * HH + k) * W::NC + kc] = v[h * HH + k];
+        __syncthreads();
+#pragma unroll
+        for (int e0 = 0; e0 < HH * W::NC; e0 += 64) {
+            const int e = e0 + lane;
+            cpx acc = red[e];
+#pragma unroll
+            for (int p = 1; p < W::PPW; ++p) acc = cadd(acc, red[p * HH * W::NC + e]);
+            dst[h * HH * W::NC + e] = acc;
+        }
+    }
+}
+
+// Fixed-order sum of n complex values p[0], p[stride], ... with eight independent chains
+// (combined in a fixed tree), so each thread keeps eight loads in flight.
+NC_DEV cpx sum_strided(const cpx* __restrict__ p, int n, size_t stride) {
+    cpx a[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) a[u] = cmk(0.f, 0.f);
+    int j = 0;
+    for (; j + 8 <= n; j += 8) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) a[u] = cadd(a[u], p[(size_t)(j + u) * stride]);
+    }
+    for (; j < n; ++j) a[0] = cadd(a[0], p[(size_t)j * stride]);
+    return cadd(cadd(cadd(a[0], a[1]), cadd(a[2], a[3])), cadd(cadd(a[4], a[5]), cadd(a[6], a[7])));
+}
+
+// out[i][e] = sum over j < nj of in[i * istride + j * jstride + e], e < len (grid (len/256, ni)).
+__global__ void k_psum(int nj, int len, size_t istride, size_t jstride, const cpx* __restrict__ in,
+                       cpx* __restrict__ out) {
+    const int i = blockIdx.y;
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= len) return;
+    out[(size_t)i * len + e] = sum_strided(in + (size_t)i * istride + e, nj, jstride);
+}
+
+// dx, second stage: the inverse of the summed packed spectrum of sample b with the unshifted
+// roll (kernels_pallas.py:1798-1812): rows from (FH - ph) mod FH, columns from (FW - pw) mod FW,
+// hin x win kept.
+template <int FH, int FW>
+__global__ __launch_bounds__(64) void k_wbwd_dx_fin(int B, int hin, int win, int ph, int pw,
+                                                    int o_off, int vec,
+                                                    const cpx* __restrict__ sum,
+                                                    float* __restrict__ dx) {
+    using W = WGeo<FH, FW>;
+    HIP_DYNAMIC_SHARED(float, lds)
+    cpx* T = reinterpret_cast<cpx*>(lds);
+    float* O = lds + o_off;
+    const int lane = threadIdx.x, ps = lane / W::NC, kc = lane % W::NC;
+    const int b0 = blockIdx.x * W::PPW;
+    const int np = min(W::PPW, B - b0);
+    const cpx* src = sum + (size_t)(b0 + min(ps, np - 1)) * W::PF + kc;
+    cpx v[FH];
+#pragma unroll
+    for (int kh = 0; kh < FH; ++kh) v[kh] = src[kh * W::NC];
+    wcol_inv<FH, FW>(v, (FH - ph) & (FH - 1), hin, T);
+    __syncthreads();
+    wrow_inv<FH, FW>(T, (FW - pw) & (FW - 1), hin, 1.0f / (float)(FH * FW), O);
+    __syncthreads();
+    ostage_copy<FW>(O, np, hin, win, dx + (size_t)b0 * hin * win);
+}
+
+// dghat, second stage: fixed-order sum over the chunks, packed column unpacked into the DC
+// and Nyquist columns; conj_out gives the conjugate convention, accumulate adds.
+template <int FH, int FW>
+__global__ void k_wbwd_dg_fin(int nchunk, int M, const cpx* __restrict__ part,
+                              cpx* __restrict__ dghat, int accumulate, int conj_out) {
+    using W = WGeo<FH, FW>;
+    const int m = blockIdx.y;
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= W::F) return;
+    const int kh = e / W::SP, kw = e - kh * W::SP;
+    auto sum = [&](int k, int col) {
+        return sum_strided(part + (size_t)m * W::PF + k * W::NC + col, nchunk,
+                           (size_t)M * W::PF);
+    };
+    cpx s;
+    if (kw == 0 || kw == FW / 2) {
+        const cpx a = sum(kh, 0), d = cconj(sum((FH - kh) & (FH - 1), 0));
+        s = kw == 0 ? cscale(cadd(a, d), 0.5f) : cmul_negi(cscale(csub(a, d), 0.5f));
+    } else {
+        s = sum(kh, kw);
+    }
     if (conj_out) s = cconj(s);
-    cpx* o = dghat + (size_t)m * F + e;
+    cpx* o = dghat + (size_t)m * W::F + e;
     *o = accumulate ? cadd(*o, s) : s;
 }
 
@@ -235,35 +298,90 @@ __global__ void k_fftconv_bwd_dg_fin(int nchunk, int M, int F, const cpx* __rest
 
 bool pow2_ok(int f) { return f == 16 || f == 32 || f == 64; }
 
-struct BwdSplit {
-    int ms;      // directions per dx workgroup
-    int nsplit;  // dx workgroups per sample
-    int bc;      // samples per dg workgroup
-    int nchunk;  // dg chunks
+// LDS of a wavefront transform over `rows` rows of PPW planes: the transposition buffer T
+// (rows + 2 with the trash and zero rows) and the real-valued staging (input or output), which
+// shares T's space when one row pass covers every row pair; then the Nyquist-column staging
+// (PPW x FH cpx).
+template <int FH, int FW>
+struct WLds {
+    size_t bytes;
+    int off;  // float offset of the staging area
+    int nq;   // cpx offset of the Nyquist staging
+    WLds(int rows, int cols, size_t at_least = 0) {
+        using W = WGeo<FH, FW>;
+        const size_t t = (size_t)W::PPW * (rows + 2) * W::PITCH * sizeof(cpx);
+        const size_t st = (size_t)std::max(ostage_floats(W::PPW, rows, FW),
+                                           istage_floats(W::PPW, rows, FW)) * sizeof(float);
+        const bool share = W::PPW * ((rows + 1) / 2) <= 64;
+        size_t main = std::max(share ? std::max(t, st) : t + st, at_least);
+        main = (main + 15) / 16 * 16;
+        off = share ? 0 : (int)(t / sizeof(float));
+        nq = (int)(main / sizeof(cpx));
+        bytes = main + (size_t)W::PPW * FH * sizeof(cpx);
+    }
 };
 
+// float4 moves need 16-byte aligned planes.
+inline int vec_ok(const void* p, size_t n) {
+    return (n % 4 == 0) && (reinterpret_cast<uintptr_t>(p) % 16 == 0);
+}
+
+template <class K>
+void lds_limit(K kernel, size_t bytes) {
+    if (bytes > 65536)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
+struct BwdSplit {
+    int mg;      // direction groups (dx partials per sample)
+    int nchunk;  // sample groups (dG partials per direction)
+};
+
+template <int FH, int FW>
 BwdSplit bwd_split(int B, int M) {
-    BwdSplit s;
-    int target = std::max(1, 512 / std::max(1, B));
-    s.nsplit = std::min(M, target);
-    s.ms = (M + s.nsplit - 1) / s.nsplit;
-    s.nsplit = (M + s.ms - 1) / s.ms;
-    int chunks = std::max(1, std::min(B, 256 / std::max(1, M)));
-    s.bc = (B + chunks - 1) / chunks;
-    s.nchunk = (B + s.bc - 1) / s.bc;
-    return s;
+    constexpr int PPW = WGeo<FH, FW>::PPW;
+    return BwdSplit{(M + PPW - 1) / PPW, (B + PPW - 1) / PPW};
+}
+
+template <int FH, int FW>
+size_t bwd_ws(int B, int M) {
+    BwdSplit s = bwd_split<FH, FW>(B, M);
+    return ((size_t)B * s.mg + (size_t)B + (size_t)s.nchunk * M) * WGeo<FH, FW>::PF * sizeof(cpx);
+}
+
+template <int FH, int FW>
+int launch_rfft2(hipStream_t st, int nplanes, int hin, int win, bool flip, const float* x,
+                 cpx* out) {
+    using W = WGeo<FH, FW>;
+    WLds<FH, FW> l(hin, win);
+    dim3 grid((nplanes + W::PPW - 1) / W::PPW);
+    if (flip) {
+        lds_limit(k_wrfft2<FH, FW, true>, l.bytes);
+        hipLaunchKernelGGL((k_wrfft2<FH, FW, true>), grid, dim3(64), l.bytes, st, nplanes, hin,
+                           win, l.off, vec_ok(x, (size_t)hin * win), x, out);
+    } else {
+        lds_limit(k_wrfft2<FH, FW, false>, l.bytes);
+        hipLaunchKernelGGL((k_wrfft2<FH, FW, false>), grid, dim3(64), l.bytes, st, nplanes, hin,
+                           win, l.off, vec_ok(x, (size_t)hin * win), x, out);
+    }
+    NC_CHECK_LAUNCH();
+    return NC_OK;
 }
 
 template <int FH, int FW>
 int launch_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph,
                int pw, const float* x, const float* ghat, float* z, float* xhat) {
-    using P = Plane<FH, FW>;
-    int mc = B >= 512 ? M : std::max(1, std::min(M, (M * B + 511) / 512));
-    mc = std::max(1, std::min(M, mc));
-    dim3 grid(B, (M + mc - 1) / mc);
-    hipLaunchKernelGGL((k_fftconv_fwd<FH, FW>), grid, dim3(P::NT), 0, st, M, mc, hin, win,
-                       hout, wout, ph, pw, x, reinterpret_cast<const cpx*>(ghat), z,
-                       reinterpret_cast<cpx*>(xhat));
+    using W = WGeo<FH, FW>;
+    int rc = launch_rfft2<FH, FW>(st, B, hin, win, false, x, reinterpret_cast<cpx*>(xhat));
+    if (rc != NC_OK) return rc;
+    WLds<FH, FW> l(hout, wout);
+    lds_limit(k_wconv_fwd<FH, FW>, l.bytes);
+    const int nplanes = B * M;
+    hipLaunchKernelGGL((k_wconv_fwd<FH, FW>), dim3((nplanes + W::PPW - 1) / W::PPW), dim3(64),
+                       l.bytes, st, nplanes, M, hout, wout, ph, pw, l.off, l.nq,
+                       vec_ok(z, (size_t)hout * wout),
+                       reinterpret_cast<const cpx*>(xhat), reinterpret_cast<const cpx*>(ghat), z);
     NC_CHECK_LAUNCH();
     return NC_OK;
 }
@@ -272,38 +390,42 @@ template <int FH, int FW>
 int launch_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph,
                int pw, const float* gz, const float* xhat, const float* ghat, int need_dx,
                float* dx, float* dghat, int accumulate, int conj_out, void* ws) {
-    using P = Plane<FH, FW>;
-    BwdSplit s = bwd_split(B, M);
+    using W = WGeo<FH, FW>;
+    BwdSplit s = bwd_split<FH, FW>(B, M);
     cpx* dxpart = reinterpret_cast<cpx*>(ws);
-    cpx* dgpart = dxpart + (size_t)B * s.nsplit * P::F;
-    const cpx* G = reinterpret_cast<const cpx*>(ghat);
+    cpx* dxsum = dxpart + (size_t)B * s.mg * W::PF;
+    cpx* dgpart = dxsum + (size_t)B * W::PF;
+    const WLds<FH, FW> lp(hout, wout, (size_t)64 * (FH / 2) * sizeof(cpx));
     if (need_dx) {
-        hipLaunchKernelGGL((k_fftconv_bwd_dx<FH, FW>), dim3(B, s.nsplit), dim3(P::NT), 0, st,
-                           M, s.ms, hin, win, hout, wout, ph, pw, gz, G,
-                           s.nsplit > 1 ? dxpart : nullptr, dx);
+        lds_limit(k_wbwd_part<FH, FW, false>, lp.bytes);
+        hipLaunchKernelGGL((k_wbwd_part<FH, FW, false>), dim3(s.mg, B), dim3(64), lp.bytes, st, B,
+                           M, hout, wout, lp.off, lp.nq, vec_ok(gz, (size_t)hout * wout), gz,
+                           reinterpret_cast<const cpx*>(ghat), dxpart);
         NC_CHECK_LAUNCH();
-        if (s.nsplit > 1) {
-            hipLaunchKernelGGL((k_fftconv_bwd_dx_fin<FH, FW>), dim3(B), dim3(P::NT), 0, st,
-                               s.nsplit, hin, win, ph, pw, dxpart, dx);
-            NC_CHECK_LAUNCH();
-        }
+        hipLaunchKernelGGL(k_psum, dim3((W::PF + 255) / 256, B), dim3(256), 0, st, s.mg, W::PF,
+                           (size_t)s.mg * W::PF, (size_t)W::PF, dxpart, dxsum);
+        NC_CHECK_LAUNCH();
+        const WLds<FH, FW> lf(hin, win);
+        lds_limit(k_wbwd_dx_fin<FH, FW>, lf.bytes);
+        hipLaunchKernelGGL((k_wbwd_dx_fin<FH, FW>), dim3((B + W::PPW - 1) / W::PPW), dim3(64),
+                           lf.bytes, st, B, hin, win, ph, pw, lf.off, vec_ok(dx, (size_t)hin * win),
+                           dxsum, dx);
+        NC_CHECK_LAUNCH();
     }
-    hipLaunchKernelGGL((k_fftconv_bwd_dg<FH, FW>), dim3(M, s.nchunk), dim3(P::NT), 0, st, B, M,
-                       s.bc, hout, wout, gz, reinterpret_cast<const cpx*>(xhat), dgpart);
+    lds_limit(k_wbwd_part<FH, FW, true>, lp.bytes);
+    hipLaunchKernelGGL((k_wbwd_part<FH, FW, true>), dim3(M, s.nchunk), dim3(64), lp.bytes, st, B,
+                       M, hout, wout, lp.off, lp.nq, vec_ok(gz, (size_t)hout * wout), gz,
+                       reinterpret_cast<const cpx*>(xhat), dgpart);
     NC_CHECK_LAUNCH();
-    hipLaunchKernelGGL(k_fftconv_bwd_dg_fin, dim3(M, (P::F + 255) / 256), dim3(256), 0, st,
-                       s.nchunk, M, P::F, dgpart, reinterpret_cast<cpx*>(dghat), accumulate,
-                       conj_out);
+    hipLaunchKernelGGL((k_wbwd_dg_fin<FH, FW>), dim3((W::F + 255) / 256, M), dim3(256), 0, st,
+                       s.nchunk, M, dgpart, reinterpret_cast<cpx*>(dghat), accumulate, conj_out);
     NC_CHECK_LAUNCH();
     return NC_OK;
 }
 
 template <int FH, int FW>
 int launch_spec_fwd(hipStream_t st, int M, int kh, int kw, const float* filters, float* ghat) {
-    hipLaunchKernelGGL((k_filter_spectrum_fwd<FH, FW>), dim3(M), dim3(Plane<FH, FW>::NT), 0, st,
-                       kh, kw, filters, reinterpret_cast<cpx*>(ghat));
-    NC_CHECK_LAUNCH();
-    return NC_OK;
+    return launch_rfft2<FH, FW>(st, M, kh, kw, true, filters, reinterpret_cast<cpx*>(ghat));
 }
 
 template <int FH, int FW>
@@ -313,6 +435,11 @@ int launch_spec_bwd(hipStream_t st, int M, int kh, int kw, int sh, int sw, const
                        kh, kw, sh, sw, reinterpret_cast<const cpx*>(dghat), g, acc, conj_in);
     NC_CHECK_LAUNCH();
     return NC_OK;
+}
+
+template <int FH, int FW>
+size_t launch_ws(int B, int M) {
+    return bwd_ws<FH, FW>(B, M);
 }
 
 #define NC_DISPATCH_FFT(FH_, FW_, CALL)                                   \
@@ -326,7 +453,6 @@ int launch_spec_bwd(hipStream_t st, int M, int kh, int kw, int sh, int sw, const
         if (FH_ == 64 && FW_ == 16) return CALL(64, 16);                  \
         if (FH_ == 64 && FW_ == 32) return CALL(64, 32);                  \
         if (FH_ == 64 && FW_ == 64) return CALL(64, 64);                  \
-        return NC_ERR_UNSUPPORTED;                                        \
     } while (0)
 
 }  // namespace
@@ -342,6 +468,7 @@ int nc_filter_spectrum_fwd(void* stream, int M, int kh, int kw, int fft_h, int f
 #define NC_CALL(A, Bv) launch_spec_fwd<A, Bv>(st, M, kh, kw, filters, ghat)
     NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
 #undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
 }
 
 int nc_filter_spectrum_bwd(void* stream, int M, int kh, int kw, int fft_h, int fft_w,
@@ -356,6 +483,7 @@ int nc_filter_spectrum_bwd(void* stream, int M, int kh, int kw, int fft_h, int f
     launch_spec_bwd<A, Bv>(st, M, kh, kw, shift_h, shift_w, dghat, g_filters, accumulate, conj_in)
     NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
 #undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
 }
 
 static int fftconv_check(int B, int M, int hin, int win, int hout, int wout, int ph, int pw,
@@ -373,19 +501,21 @@ int nc_fftconv_fwd(void* stream, int B, int M, int hin, int win, int hout, int w
                    float* xhat) {
     int rc = fftconv_check(B, M, hin, win, hout, wout, pad_h, pad_w, fft_h, fft_w);
     if (rc != NC_OK) return rc;
-    if (!x || !ghat || !z) return NC_ERR_INVALID_ARGUMENT;
+    if (!x || !ghat || !z || !xhat) return NC_ERR_INVALID_ARGUMENT;
     hipStream_t st = nc_stream(stream);
 #define NC_CALL(A, Bv) \
     launch_fwd<A, Bv>(st, B, M, hin, win, hout, wout, pad_h, pad_w, x, ghat, z, xhat)
     NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
 #undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
 }
 
 size_t nc_fftconv_bwd_workspace_size(int B, int M, int fft_h, int fft_w) {
-    if (B <= 0 || M <= 0 || fft_h <= 0 || fft_w <= 0) return 0;
-    BwdSplit s = bwd_split(B, M);
-    size_t F = (size_t)fft_h * (fft_w / 2 + 1);
-    return ((size_t)B * s.nsplit + (size_t)s.nchunk * M) * F * sizeof(float2);
+    if (B <= 0 || M <= 0 || !pow2_ok(fft_h) || !pow2_ok(fft_w)) return 0;
+#define NC_CALL(A, Bv) launch_ws<A, Bv>(B, M)
+    NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
+#undef NC_CALL
+    return 0;
 }
 
 int nc_fftconv_bwd(void* stream, int B, int M, int hin, int win, int hout, int wout, int pad_h,
@@ -403,6 +533,7 @@ int nc_fftconv_bwd(void* stream, int B, int M, int hin, int win, int hout, int w
                       dx, dghat, accumulate, conj_dghat, ws)
     NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
 #undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
 }
 
 }  // extern "C"

@@ -219,7 +219,8 @@ class StepPlan:
         nz = d if self.training else 1
         self.xs = [self.x0] + [torch.empty(B, h, w, **f) for _ in range(d - 1)]
         self.zs = [torch.empty(B, M, h, w, **f) for _ in range(nz)]
-        self.xhat = [torch.empty(B, F, **c) for _ in range(d)] if self.training else None
+        # cell spectra: one per step for the reverse pass, one shared buffer for evaluation
+        self.xhat = [torch.empty(B, F, **c) for _ in range(d if self.training else 1)]
         self.mean = [torch.empty(B, M, **f) for _ in range(d)]
         self.rstd = [torch.empty(B, M, **f) for _ in range(d)]
         self.out = torch.empty(B, self.P, **f)
@@ -274,7 +275,7 @@ class StepPlan:
         for t in range(self.d):
             last = t == self.d - 1
             z = self.zs[t if self.training else 0]
-            xh = self.xhat[t] if self.training else None
+            xh = self.xhat[t if self.training else 0]
             if t == 0 and self.t0_grid:
                 r0, _, c0, _ = self.bbox
                 call("nc_fftconv_fwd", s, B, M, self.H, self.W, h, w, self.kh - 1 + r0,

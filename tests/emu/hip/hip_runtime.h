@@ -23,6 +23,10 @@ struct float2 {
     float x, y;
 };
 inline float2 make_float2(float a, float b) { return float2{a, b}; }
+struct float4 {
+    float x, y, z, w;
+};
+inline float4 make_float4(float a, float b, float c, float d) { return float4{a, b, c, d}; }
 struct dim3 {
     unsigned x, y, z;
     dim3(unsigned a = 1, unsigned b = 1, unsigned c = 1) : x(a), y(b), z(c) {}
@@ -45,6 +49,11 @@ typedef int hipError_t;
 typedef void* hipStream_t;
 #define hipSuccess 0
 inline hipError_t hipGetLastError() { return 0; }
+enum { hipFuncAttributeMaxDynamicSharedMemorySize = 8 };
+#define __builtin_amdgcn_sched_barrier(mask) ((void)0)
+#define NC_PIN(x) ((void)0)
+#define NC_FENCE() ((void)0)
+inline hipError_t hipFuncSetAttribute(const void*, int, int) { return 0; }
 inline const char* hipGetErrorString(hipError_t) { return "emulated"; }
 using std::max;
 using std::min;
