@@ -127,7 +127,8 @@ int nc_filter_spectrum_bwd(void* stream, int M, int kh, int kw, int fft_h, int f
  * irfft2(rfft2(x) * ghat)[pad_h : pad_h+hout, pad_w : pad_w+wout].  xhat (B, fft_h,
  * fft_w/2+1) complex receives the cell spectra (the saved cell_freq residual); it is required
  * (the correlation reads it back).
- * Supported spectral grids: fft_h, fft_w in {16, 32, 64}.
+ * Supported spectral grids: fft_h, fft_w both in {16, 32, 64} (wavefront transforms) or
+ * both in {64, 128, 256} (workgroup transforms over LDS segments).
  */
 int nc_fftconv_fwd(void* stream, int B, int M, int hin, int win, int hout, int wout, int pad_h,
                    int pad_w, int fft_h, int fft_w, const float* x, const float* ghat, float* z,

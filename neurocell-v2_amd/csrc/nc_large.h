@@ -1,0 +1,28 @@
+// Internal interface between the C ABI entry points (nc_spectral.hip) and the large-grid
+// spectral kernels (nc_spectral_large.hip): FFT grids with an axis of 128 or 256 points and
+// both axes in {64, 128, 256}.  Arguments have the meaning of the matching nc_* entry points.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+
+bool nc_large_grid(int fft_h, int fft_w);
+
+int nc_large_filter_spectrum_fwd(hipStream_t st, int M, int kh, int kw, int fft_h, int fft_w,
+                                 const float* filters, float* ghat);
+
+int nc_large_filter_spectrum_bwd(hipStream_t st, int M, int kh, int kw, int fft_h, int fft_w,
+                                 int shift_h, int shift_w, const float* dghat, float* g_filters,
+                                 int accumulate, int conj_in);
+
+int nc_large_fftconv_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout,
+                         int pad_h, int pad_w, int fft_h, int fft_w, const float* x,
+                         const float* ghat, float* z, float* xhat);
+
+size_t nc_large_fftconv_bwd_ws(int B, int M, int fft_h, int fft_w);
+
+int nc_large_fftconv_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout,
+                         int pad_h, int pad_w, int fft_h, int fft_w, const float* gz,
+                         const float* xhat, const float* ghat, int need_dx, float* dx,
+                         float* dghat, int accumulate, int conj_dghat, void* ws);

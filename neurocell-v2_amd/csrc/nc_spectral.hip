@@ -21,6 +21,7 @@
 #include <algorithm>
 #include <cstdint>
 
+#include "nc_large.h"
 #include "nc_wave.h"
 
 namespace {
@@ -463,8 +464,10 @@ int nc_filter_spectrum_fwd(void* stream, int M, int kh, int kw, int fft_h, int f
                            const float* filters, float* ghat) {
     if (M <= 0 || kh <= 0 || kw <= 0 || kh > fft_h || kw > fft_w || !filters || !ghat)
         return NC_ERR_INVALID_ARGUMENT;
-    if (!pow2_ok(fft_h) || !pow2_ok(fft_w)) return NC_ERR_UNSUPPORTED;
     hipStream_t st = nc_stream(stream);
+    if (nc_large_grid(fft_h, fft_w))
+        return nc_large_filter_spectrum_fwd(st, M, kh, kw, fft_h, fft_w, filters, ghat);
+    if (!pow2_ok(fft_h) || !pow2_ok(fft_w)) return NC_ERR_UNSUPPORTED;
 #define NC_CALL(A, Bv) launch_spec_fwd<A, Bv>(st, M, kh, kw, filters, ghat)
     NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
 #undef NC_CALL
@@ -477,8 +480,11 @@ int nc_filter_spectrum_bwd(void* stream, int M, int kh, int kw, int fft_h, int f
     if (M <= 0 || kh <= 0 || kw <= 0 || kh > fft_h || kw > fft_w || !dghat || !g_filters ||
         shift_h < 0 || shift_w < 0)
         return NC_ERR_INVALID_ARGUMENT;
-    if (!pow2_ok(fft_h) || !pow2_ok(fft_w)) return NC_ERR_UNSUPPORTED;
     hipStream_t st = nc_stream(stream);
+    if (nc_large_grid(fft_h, fft_w))
+        return nc_large_filter_spectrum_bwd(st, M, kh, kw, fft_h, fft_w, shift_h, shift_w, dghat,
+                                            g_filters, accumulate, conj_in);
+    if (!pow2_ok(fft_h) || !pow2_ok(fft_w)) return NC_ERR_UNSUPPORTED;
 #define NC_CALL(A, Bv) \
     launch_spec_bwd<A, Bv>(st, M, kh, kw, shift_h, shift_w, dghat, g_filters, accumulate, conj_in)
     NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
@@ -491,7 +497,7 @@ static int fftconv_check(int B, int M, int hin, int win, int hout, int wout, int
     if (B <= 0 || M <= 0 || hin <= 0 || win <= 0 || hout <= 0 || wout <= 0 || ph < 0 ||
         pw < 0)
         return NC_ERR_INVALID_ARGUMENT;
-    if (!pow2_ok(fh) || !pow2_ok(fw)) return NC_ERR_UNSUPPORTED;
+    if (!(pow2_ok(fh) && pow2_ok(fw)) && !nc_large_grid(fh, fw)) return NC_ERR_UNSUPPORTED;
     if (hin > fh || win > fw || ph + hout > fh || pw + wout > fw) return NC_ERR_INVALID_ARGUMENT;
     return NC_OK;
 }
@@ -503,6 +509,9 @@ int nc_fftconv_fwd(void* stream, int B, int M, int hin, int win, int hout, int w
     if (rc != NC_OK) return rc;
     if (!x || !ghat || !z || !xhat) return NC_ERR_INVALID_ARGUMENT;
     hipStream_t st = nc_stream(stream);
+    if (nc_large_grid(fft_h, fft_w))
+        return nc_large_fftconv_fwd(st, B, M, hin, win, hout, wout, pad_h, pad_w, fft_h, fft_w, x,
+                                    ghat, z, xhat);
 #define NC_CALL(A, Bv) \
     launch_fwd<A, Bv>(st, B, M, hin, win, hout, wout, pad_h, pad_w, x, ghat, z, xhat)
     NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
@@ -511,7 +520,9 @@ int nc_fftconv_fwd(void* stream, int B, int M, int hin, int win, int hout, int w
 }
 
 size_t nc_fftconv_bwd_workspace_size(int B, int M, int fft_h, int fft_w) {
-    if (B <= 0 || M <= 0 || !pow2_ok(fft_h) || !pow2_ok(fft_w)) return 0;
+    if (B <= 0 || M <= 0) return 0;
+    if (nc_large_grid(fft_h, fft_w)) return nc_large_fftconv_bwd_ws(B, M, fft_h, fft_w);
+    if (!pow2_ok(fft_h) || !pow2_ok(fft_w)) return 0;
 #define NC_CALL(A, Bv) launch_ws<A, Bv>(B, M)
     NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
 #undef NC_CALL
@@ -528,6 +539,9 @@ int nc_fftconv_bwd(void* stream, int B, int M, int hin, int win, int hout, int w
     if (ws_bytes < nc_fftconv_bwd_workspace_size(B, M, fft_h, fft_w) || !ws)
         return NC_ERR_WORKSPACE;
     hipStream_t st = nc_stream(stream);
+    if (nc_large_grid(fft_h, fft_w))
+        return nc_large_fftconv_bwd(st, B, M, hin, win, hout, wout, pad_h, pad_w, fft_h, fft_w,
+                                    gz, xhat, ghat, need_dx, dx, dghat, accumulate, conj_dghat, ws);
 #define NC_CALL(A, Bv)                                                                     \
     launch_bwd<A, Bv>(st, B, M, hin, win, hout, wout, pad_h, pad_w, gz, xhat, ghat, need_dx, \
                       dx, dghat, accumulate, conj_dghat, ws)

@@ -1,0 +1,392 @@
+// Piece 2 on large spectral grids (an axis of 128 or 256 points; both axes in {64, 128, 256}):
+// the Green's-function correlation and its Plancherel backward with workgroup-level,
+// LDS-segmented transforms (nc_lfft.h).  Same operator semantics as the wavefront kernels of
+// nc_spectral.hip (kernels_pallas.py:1759-1826, kernels_greens.py:240-400); spectra are
+// (FH, FW/2+1) complex64 half-spectra.
+//
+//   k_lrfft2<FLIP>   grid (planes, column segments)  half-spectra of real planes: cell spectra
+//                                                    xhat_b, filter spectra (FLIP) and the
+//                                                    cotangent spectra rfft2(gz_bm)
+//   k_linv_conv      grid (B*M, row segments)        z_bm = irfft2(xhat_b * ghat_m), window
+//   k_lred<MC>       grid (F/256, M/MC)              one pass over rfft2(gz): per bin, the
+//                                                    fixed-order sums over m (dx partials per
+//                                                    direction chunk) and over b (dghat)
+//   k_linv_dx        grid (B, row segments)          dx_b = irfft2(sum of the chunk partials)
+//                                                    with the unshifted roll
+//   k_linv_filter    grid (M, row segments)          dG_m = flip(crop(roll(irfft2(dghat_m))))
+//
+// The backward materialises rfft2(gz) once (B*M half-spectra in the workspace) instead of
+// transforming every cotangent plane twice: at these sizes a transform costs ~2.5 MFLOP
+// per plane while re-reading its spectrum costs ~0.26 MB.  No atomics: both reductions are
+// fixed-order loops, so results are bit-reproducible.
+#include <algorithm>
+
+#include "nc_large.h"
+#include "nc_lfft.h"
+
+namespace {
+
+constexpr int kNT = 256;             // workgroup size of the transform kernels
+constexpr size_t kLdsMax = 163840;   // LDS per workgroup on gfx950
+constexpr int kRedMC = 16;           // directions per reduction workgroup
+
+template <int FH, int FW>
+using LG = LGeo<FH, FW, kNT>;
+
+// LDS carve-up of the transform kernels, in the order lfwd_lds_bytes / linv_lds_bytes count
+// it: twiddles | exchange scratch | (forward only) packed-column staging C0 | Y or T.
+struct LdsParts {
+    cpx* tw;
+    cpx* scr;
+    cpx* c0;
+    cpx* seg;
+};
+
+template <int FH, int FW, bool FWD>
+NC_DEV LdsParts lds_parts(float* lds) {
+    LdsParts p;
+    p.tw = reinterpret_cast<cpx*>(lds);
+    p.scr = p.tw + NC_TW_N;
+    p.c0 = FWD ? p.scr + LG<FH, FW>::SCR : nullptr;
+    p.seg = p.scr + LG<FH, FW>::SCR + (FWD ? FH : 0);
+    return p;
+}
+
+template <int FH, int FW, bool FLIP>
+__global__ __launch_bounds__(kNT) void k_lrfft2(int hin, int win, int cs, size_t pstride,
+                                                const float* __restrict__ x,
+                                                cpx* __restrict__ out) {
+    using L = LG<FH, FW>;
+    HIP_DYNAMIC_SHARED(float, lds)
+    const LdsParts P = lds_parts<FH, FW, true>(lds);
+    load_twiddles(P.tw);
+    __syncthreads();
+    const float* src = x + (size_t)blockIdx.x * pstride;
+    cpx* o = out + (size_t)blockIdx.x * L::F;
+    lplane_rfft2<FH, FW, kNT>(
+        [&](int r, int c) {
+            return FLIP ? src[(hin - 1 - r) * win + (win - 1 - c)] : src[r * win + c];
+        },
+        hin, win, (int)blockIdx.y * cs, cs,
+        [&](int kh, int kw, cpx v) { o[kh * L::SP + kw] = v; }, P.seg, P.c0, P.scr, P.tw);
+}
+
+// Packed column value of a half-spectrum at (kh, kw): DC + i*Nyquist for kw == 0.
+template <int FW, class S>
+NC_DEV cpx packed_at(S s, int kh, int kw) {
+    constexpr int SP = FW / 2 + 1;
+    if (kw == 0) return cadd(s(kh * SP), cmul_i(s(kh * SP + FW / 2)));
+    return s(kh * SP + kw);
+}
+
+// Forward correlation: plane g = b*M + m, output rows [i0, i0 + rs) of the hout x wout window
+// read from row ph, column pw of irfft2(xhat_b * ghat_m).
+template <int FH, int FW>
+__global__ __launch_bounds__(kNT) void k_linv_conv(int M, int hout, int wout, int ph, int pw,
+                                                   int rs, const cpx* __restrict__ xhat,
+                                                   const cpx* __restrict__ ghat,
+                                                   float* __restrict__ z) {
+    using L = LG<FH, FW>;
+    HIP_DYNAMIC_SHARED(float, lds)
+    const LdsParts P = lds_parts<FH, FW, false>(lds);
+    load_twiddles(P.tw);
+    __syncthreads();
+    const int g = blockIdx.x, b = g / M, m = g - b * M;
+    const int i0 = blockIdx.y * rs, rows = min(rs, hout - i0);
+    const cpx* X = xhat + (size_t)b * L::F;
+    const cpx* G = ghat + (size_t)m * L::F;
+    float* zo = z + (size_t)g * hout * wout + (size_t)i0 * wout;
+    lplane_irfft2<FH, FW, kNT>(
+        [&](int kh, int kw) {
+            return packed_at<FW>([&](int e) { return cmul(X[e], G[e]); }, kh, kw);
+        },
+        (ph + i0) & (FH - 1), rows, pw, wout, 1.0f / (float)(FH * FW),
+        [&](int i, int j, float v) { zo[i * wout + j] = v; }, P.seg, P.scr, P.tw);
+}
+
+// Both reductions of the backward in one pass over the cotangent spectra sp (B, M, F):
+//   dxpart[c][b] = sum over the chunk's directions m of sp_bm * conj(ghat_m)   (need_dx)
+//   dghat[m]     = (+=) sum over b of sp_bm * conj(xhat_b)  (conjugated when conj_out)
+// Thread = one bin; directions m0 .. m0+MC-1 of chunk c = blockIdx.y; b in increasing order.
+template <int MC>
+__global__ __launch_bounds__(256) void k_lred(int B, int M, int F, int need_dx,
+                                              const cpx* __restrict__ sp,
+                                              const cpx* __restrict__ xhat,
+                                              const cpx* __restrict__ ghat,
+                                              cpx* __restrict__ dxpart, cpx* __restrict__ dghat,
+                                              int accumulate, int conj_out) {
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= F) return;
+    const int m0 = blockIdx.y * MC;
+    const int nm = min(MC, M - m0);
+    cpx G[MC], acc[MC];
+#pragma unroll
+    for (int q = 0; q < MC; ++q) {
+        G[q] = ghat[(size_t)(m0 + min(q, nm - 1)) * F + e];
+        acc[q] = cmk(0.f, 0.f);
+    }
+    for (int b = 0; b < B; ++b) {
+        const cpx X = xhat[(size_t)b * F + e];
+        const cpx* s = sp + ((size_t)b * M + m0) * F + e;
+        cpx v[MC];
+#pragma unroll
+        for (int q = 0; q < MC; ++q) v[q] = s[(size_t)min(q, nm - 1) * F];
+        cpx d = cmk(0.f, 0.f);
+#pragma unroll
+        for (int q = 0; q < MC; ++q) {
+            if (q < nm) {
+                d = cadd(d, cmulc(v[q], G[q]));
+                acc[q] = cadd(acc[q], cmulc(v[q], X));
+            }
+        }
+        if (need_dx) dxpart[((size_t)blockIdx.y * B + b) * F + e] = d;
+    }
+#pragma unroll
+    for (int q = 0; q < MC; ++q) {
+        if (q < nm) {
+            const cpx v = conj_out ? cconj(acc[q]) : acc[q];
+            cpx* o = dghat + (size_t)(m0 + q) * F + e;
+            *o = accumulate ? cadd(*o, v) : v;
+        }
+    }
+}
+
+// dx, last stage: sample b's spectrum is the fixed-order sum of its nchunk partials; the
+// inverse applies the unshifted roll (kernels_pallas.py:1798-1812): rows from (FH - ph) mod FH,
+// columns from (FW - pw) mod FW, hin x win kept; rows [i0, i0 + rs) here.
+template <int FH, int FW>
+__global__ __launch_bounds__(kNT) void k_linv_dx(int B, int nchunk, int hin, int win, int ph,
+                                                 int pw, int rs, const cpx* __restrict__ part,
+                                                 float* __restrict__ dx) {
+    using L = LG<FH, FW>;
+    HIP_DYNAMIC_SHARED(float, lds)
+    const LdsParts P = lds_parts<FH, FW, false>(lds);
+    load_twiddles(P.tw);
+    __syncthreads();
+    const int b = blockIdx.x;
+    const int i0 = blockIdx.y * rs, rows = min(rs, hin - i0);
+    const cpx* src = part + (size_t)b * L::F;
+    const size_t cstride = (size_t)B * L::F;
+    float* o = dx + (size_t)b * hin * win + (size_t)i0 * win;
+    lplane_irfft2<FH, FW, kNT>(
+        [&](int kh, int kw) {
+            return packed_at<FW>(
+                [&](int e) {
+                    cpx s = src[e];
+                    for (int c = 1; c < nchunk; ++c) s = cadd(s, src[c * cstride + e]);
+                    return s;
+                },
+                kh, kw);
+        },
+        ((FH - ph) + i0) & (FH - 1), rows, (FW - pw) & (FW - 1), win, 1.0f / (float)(FH * FW),
+        [&](int i, int j, float v) { o[i * win + j] = v; }, P.seg, P.scr, P.tw);
+}
+
+// Filter spectrum backward (kernels_pallas.py:1558-1579): dG_m = flip(crop(roll(irfft2(.)))),
+// output rows [i0, i0 + rs) of the kh x kw crop.
+template <int FH, int FW>
+__global__ __launch_bounds__(kNT) void k_linv_filter(int kh, int kw, int shift_h, int shift_w,
+                                                     int rs, const cpx* __restrict__ dghat,
+                                                     float* __restrict__ gfilt, int accumulate,
+                                                     int conj_in) {
+    using L = LG<FH, FW>;
+    HIP_DYNAMIC_SHARED(float, lds)
+    const LdsParts P = lds_parts<FH, FW, false>(lds);
+    load_twiddles(P.tw);
+    __syncthreads();
+    const int m = blockIdx.x;
+    const int i0 = blockIdx.y * rs, rows = min(rs, kh - i0);
+    const cpx* d = dghat + (size_t)m * L::F;
+    float* out = gfilt + (size_t)m * kh * kw;
+    const int row0 = (FH - (shift_h % FH)) & (FH - 1);
+    const int col0 = (FW - (shift_w % FW)) & (FW - 1);
+    lplane_irfft2<FH, FW, kNT>(
+        [&](int a, int c) {
+            return packed_at<FW>(
+                [&](int e) { return conj_in ? cconj(d[e]) : d[e]; }, a, c);
+        },
+        (row0 + i0) & (FH - 1), rows, col0, kw, 1.0f / (float)(FH * FW),
+        [&](int i, int j, float v) {
+            float* o = out + (kh - 1 - (i0 + i)) * kw + (kw - 1 - j);
+            *o = accumulate ? *o + v : v;
+        },
+        P.seg, P.scr, P.tw);
+}
+
+// ----------------------------------------------------------------------------------------
+// Launch plumbing
+// ----------------------------------------------------------------------------------------
+
+template <class K>
+void set_lds(K kernel, size_t bytes) {
+    if (bytes > 65536)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
+// Packed columns per forward segment: the widest power-of-two share of FW/2 whose pair
+// buffer fits in LDS.
+template <int FH, int FW>
+int fwd_cols(int hin) {
+    int cs = LG<FH, FW>::NC;
+    while (cs > 1 && lfwd_lds_bytes<FH, FW, kNT>(hin, cs) > kLdsMax) cs >>= 1;
+    return cs;
+}
+
+// Output rows per inverse segment: rows split evenly into the fewest segments that fit.
+template <int FH, int FW>
+int inv_rows(int rows) {
+    for (int n = 1;; ++n) {
+        const int rs = (rows + n - 1) / n;
+        if (linv_lds_bytes<FH, FW, kNT>(rs) <= kLdsMax || rs == 1) return rs;
+    }
+}
+
+template <int FH, int FW>
+int rfft2_planes(hipStream_t st, int nplanes, int hin, int win, size_t pstride, bool flip,
+                 const float* x, cpx* out) {
+    const int cs = fwd_cols<FH, FW>(hin);
+    const size_t lds = lfwd_lds_bytes<FH, FW, kNT>(hin, cs);
+    if (lds > kLdsMax) return NC_ERR_UNSUPPORTED;
+    const dim3 grid(nplanes, LG<FH, FW>::NC / cs);
+    if (flip) {
+        set_lds(k_lrfft2<FH, FW, true>, lds);
+        hipLaunchKernelGGL((k_lrfft2<FH, FW, true>), grid, dim3(kNT), lds, st, hin, win, cs,
+                           pstride, x, out);
+    } else {
+        set_lds(k_lrfft2<FH, FW, false>, lds);
+        hipLaunchKernelGGL((k_lrfft2<FH, FW, false>), grid, dim3(kNT), lds, st, hin, win, cs,
+                           pstride, x, out);
+    }
+    NC_CHECK_LAUNCH();
+    return NC_OK;
+}
+
+template <int FH, int FW>
+int spec_fwd(hipStream_t st, int M, int kh, int kw, const float* filters, float* ghat) {
+    return rfft2_planes<FH, FW>(st, M, kh, kw, (size_t)kh * kw, true, filters,
+                                reinterpret_cast<cpx*>(ghat));
+}
+
+template <int FH, int FW>
+int spec_bwd(hipStream_t st, int M, int kh, int kw, int sh, int sw, const float* dghat,
+             float* g, int acc, int conj_in) {
+    const int rs = inv_rows<FH, FW>(kh);
+    const size_t lds = linv_lds_bytes<FH, FW, kNT>(rs);
+    set_lds(k_linv_filter<FH, FW>, lds);
+    hipLaunchKernelGGL((k_linv_filter<FH, FW>), dim3(M, (kh + rs - 1) / rs), dim3(kNT), lds, st,
+                       kh, kw, sh, sw, rs, reinterpret_cast<const cpx*>(dghat), g, acc, conj_in);
+    NC_CHECK_LAUNCH();
+    return NC_OK;
+}
+
+template <int FH, int FW>
+int conv_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph, int pw,
+             const float* x, const float* ghat, float* z, float* xhat) {
+    int rc = rfft2_planes<FH, FW>(st, B, hin, win, (size_t)hin * win, false, x,
+                                  reinterpret_cast<cpx*>(xhat));
+    if (rc != NC_OK) return rc;
+    const int rs = inv_rows<FH, FW>(hout);
+    const size_t lds = linv_lds_bytes<FH, FW, kNT>(rs);
+    set_lds(k_linv_conv<FH, FW>, lds);
+    hipLaunchKernelGGL((k_linv_conv<FH, FW>), dim3(B * M, (hout + rs - 1) / rs), dim3(kNT), lds,
+                       st, M, hout, wout, ph, pw, rs, reinterpret_cast<const cpx*>(xhat),
+                       reinterpret_cast<const cpx*>(ghat), z);
+    NC_CHECK_LAUNCH();
+    return NC_OK;
+}
+
+template <int FH, int FW>
+size_t bwd_ws(int B, int M) {
+    const int nchunk = (M + kRedMC - 1) / kRedMC;
+    return ((size_t)B * M + (size_t)nchunk * B) * LG<FH, FW>::F * sizeof(cpx);
+}
+
+template <int FH, int FW>
+int conv_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph, int pw,
+             const float* gz, const float* xhat, const float* ghat, int need_dx, float* dx,
+             float* dghat, int accumulate, int conj_out, void* ws) {
+    using L = LG<FH, FW>;
+    const int nchunk = (M + kRedMC - 1) / kRedMC;
+    cpx* sp = reinterpret_cast<cpx*>(ws);
+    cpx* part = sp + (size_t)B * M * L::F;
+    int rc = rfft2_planes<FH, FW>(st, B * M, hout, wout, (size_t)hout * wout, false, gz, sp);
+    if (rc != NC_OK) return rc;
+    hipLaunchKernelGGL((k_lred<kRedMC>), dim3((L::F + 255) / 256, nchunk), dim3(256), 0, st, B,
+                       M, L::F, need_dx, sp, reinterpret_cast<const cpx*>(xhat),
+                       reinterpret_cast<const cpx*>(ghat), part, reinterpret_cast<cpx*>(dghat),
+                       accumulate, conj_out);
+    NC_CHECK_LAUNCH();
+    if (need_dx) {
+        const int rs = inv_rows<FH, FW>(hin);
+        const size_t lds = linv_lds_bytes<FH, FW, kNT>(rs);
+        set_lds(k_linv_dx<FH, FW>, lds);
+        hipLaunchKernelGGL((k_linv_dx<FH, FW>), dim3(B, (hin + rs - 1) / rs), dim3(kNT), lds, st,
+                           B, nchunk, hin, win, ph, pw, rs, part, dx);
+        NC_CHECK_LAUNCH();
+    }
+    return NC_OK;
+}
+
+#define NC_DISPATCH_LARGE(FH_, FW_, CALL)                   \
+    do {                                                    \
+        if (FH_ == 64 && FW_ == 128) return CALL(64, 128);  \
+        if (FH_ == 64 && FW_ == 256) return CALL(64, 256);  \
+        if (FH_ == 128 && FW_ == 64) return CALL(128, 64);  \
+        if (FH_ == 128 && FW_ == 128) return CALL(128, 128); \
+        if (FH_ == 128 && FW_ == 256) return CALL(128, 256); \
+        if (FH_ == 256 && FW_ == 64) return CALL(256, 64);  \
+        if (FH_ == 256 && FW_ == 128) return CALL(256, 128); \
+        if (FH_ == 256 && FW_ == 256) return CALL(256, 256); \
+    } while (0)
+
+}  // namespace
+
+bool nc_large_grid(int fh, int fw) {
+    auto ok = [](int f) { return f == 64 || f == 128 || f == 256; };
+    return ok(fh) && ok(fw) && (fh > 64 || fw > 64);
+}
+
+int nc_large_filter_spectrum_fwd(hipStream_t st, int M, int kh, int kw, int fh, int fw,
+                                 const float* filters, float* ghat) {
+#define NC_CALL(A, Bv) spec_fwd<A, Bv>(st, M, kh, kw, filters, ghat)
+    NC_DISPATCH_LARGE(fh, fw, NC_CALL);
+#undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
+}
+
+int nc_large_filter_spectrum_bwd(hipStream_t st, int M, int kh, int kw, int fh, int fw, int sh,
+                                 int sw, const float* dghat, float* g, int acc, int conj_in) {
+#define NC_CALL(A, Bv) spec_bwd<A, Bv>(st, M, kh, kw, sh, sw, dghat, g, acc, conj_in)
+    NC_DISPATCH_LARGE(fh, fw, NC_CALL);
+#undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
+}
+
+int nc_large_fftconv_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout,
+                         int ph, int pw, int fh, int fw, const float* x, const float* ghat,
+                         float* z, float* xhat) {
+#define NC_CALL(A, Bv) conv_fwd<A, Bv>(st, B, M, hin, win, hout, wout, ph, pw, x, ghat, z, xhat)
+    NC_DISPATCH_LARGE(fh, fw, NC_CALL);
+#undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
+}
+
+size_t nc_large_fftconv_bwd_ws(int B, int M, int fh, int fw) {
+#define NC_CALL(A, Bv) bwd_ws<A, Bv>(B, M)
+    NC_DISPATCH_LARGE(fh, fw, NC_CALL);
+#undef NC_CALL
+    return 0;
+}
+
+int nc_large_fftconv_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout,
+                         int ph, int pw, int fh, int fw, const float* gz, const float* xhat,
+                         const float* ghat, int need_dx, float* dx, float* dghat, int accumulate,
+                         int conj_dghat, void* ws) {
+#define NC_CALL(A, Bv)                                                                     \
+    conv_bwd<A, Bv>(st, B, M, hin, win, hout, wout, ph, pw, gz, xhat, ghat, need_dx, dx, dghat, \
+                    accumulate, conj_dghat, ws)
+    NC_DISPATCH_LARGE(fh, fw, NC_CALL);
+#undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
+}

@@ -24,7 +24,14 @@ from . import _abi
 from ._lib import NeurocellError, call, ptr, stream_ptr, require_device
 from .topology import ChipTopology2D, CoordinatePortSpec
 
-_SUPPORTED_FFT = (16, 32, 64)
+_WAVE_FFT = (16, 32, 64)        # wavefront transforms (a plane per lane group)
+_LARGE_FFT = (64, 128, 256)     # workgroup transforms over LDS segments
+
+
+def spectral_grid_supported(fh: int, fw: int) -> bool:
+    """True when the C ABI has kernels for an (fh, fw) spectral grid."""
+    return ((fh in _WAVE_FFT and fw in _WAVE_FFT)
+            or (fh in _LARGE_FFT and fw in _LARGE_FFT))
 
 
 def _npow2(x: int) -> int:
@@ -132,9 +139,9 @@ class StepPlan:
         else:
             self.fft = tuple(topology.fft_shape)
         fh, fw = self.fft
-        if fh not in _SUPPORTED_FFT or fw not in _SUPPORTED_FFT:
-            raise NeurocellError(f"spectral grid {self.fft} is not supported yet "
-                                 f"(supported sizes {_SUPPORTED_FFT})")
+        if not spectral_grid_supported(fh, fw):
+            raise NeurocellError(f"spectral grid {self.fft} is not supported (both axes in "
+                                 f"{_WAVE_FFT} or both in {_LARGE_FFT})")
         if h + kh - 1 > fh or w + kw - 1 > fw:
             raise NeurocellError("linear correlation does not fit the spectral grid")
         self.F = fh * (fw // 2 + 1)

@@ -35,10 +35,9 @@ import torch
 
 from . import _abi
 from ._lib import NeurocellError, call, lib, ptr, stream_ptr
-from .engine import act_id
+from .engine import act_id, spectral_grid_supported
 from .topology import ChipTopology2D, CoordinatePortSpec
 
-_FFT_OK = (16, 32, 64)
 
 
 def _npow2(x):
@@ -255,8 +254,8 @@ def fused_output_port_epilogue(z_roi_bmhw, step_params, topology, final_activate
 # ------------------------------------------------------------------ spectra
 
 def _spec_ok(fft_shape):
-    if fft_shape[0] not in _FFT_OK or fft_shape[1] not in _FFT_OK:
-        raise NeurocellError(f"spectral grid {fft_shape} is not supported yet")
+    if not spectral_grid_supported(int(fft_shape[0]), int(fft_shape[1])):
+        raise NeurocellError(f"spectral grid {tuple(fft_shape)} is not supported")
 
 
 def precompute_filter_rfft2(filters_oihw, fft_shape=(64, 64)):

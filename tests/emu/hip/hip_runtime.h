@@ -18,7 +18,12 @@
 #define __shared__ static
 #define __global__
 #define __launch_bounds__(...)
-#define HIP_DYNAMIC_SHARED(type, var) static type var[1 << 17];
+// Dynamic LDS is one shared arena; a launch may touch only the bytes it requested (the rest
+// is poisoned with NaN bytes and checked after every workgroup: the device drops accesses past the
+// allocation).
+#define EMU_LDS_BYTES (1 << 19)
+extern unsigned char emu_dyn_lds[EMU_LDS_BYTES];
+#define HIP_DYNAMIC_SHARED(type, var) type* var = reinterpret_cast<type*>(emu_dyn_lds);
 struct float2 {
     float x, y;
 };
@@ -48,15 +53,17 @@ inline float __shfl_xor(float v, int off, int) {
 typedef int hipError_t;
 typedef void* hipStream_t;
 #define hipSuccess 0
-inline hipError_t hipGetLastError() { return 0; }
+hipError_t hipGetLastError();
 enum { hipFuncAttributeMaxDynamicSharedMemorySize = 8 };
 #define __builtin_amdgcn_sched_barrier(mask) ((void)0)
 #define NC_PIN(x) ((void)0)
 #define NC_FENCE() ((void)0)
 inline hipError_t hipFuncSetAttribute(const void*, int, int) { return 0; }
-inline const char* hipGetErrorString(hipError_t) { return "emulated"; }
+inline const char* hipGetErrorString(hipError_t e) {
+    return e == 1 ? "emulated launch touched LDS past its dynamic allocation" : "emulated";
+}
 using std::max;
 using std::min;
-void emu_launch(std::function<void()> f, dim3 g, dim3 b);
+void emu_launch(std::function<void()> f, dim3 g, dim3 b, size_t shm);
 #define hipLaunchKernelGGL(K, G, BK, SHM, ST, ...) \
-    emu_launch([&] { K(__VA_ARGS__); }, dim3(G), dim3(BK))
+    emu_launch([&] { K(__VA_ARGS__); }, dim3(G), dim3(BK), (size_t)(SHM))

@@ -30,3 +30,16 @@ def alu_case(seed, B, out_width=2, depth=4, kernel_size=(23, 13), directions=16)
     oh, ow = geom.out_size
     y = rng.integers(0, 2, size=(B, oh, ow)).astype(np.float32)
     return geom, cell, filt, x, y
+
+
+def config_geometry(cfg, depth=None, directions=None):
+    """The oracle's restatement of a benchmark config's chip (``neurocell.configs``)."""
+    from oracle import vnn_oracle as O
+    d = cfg.depth if depth is None else depth
+    m = cfg.directions if directions is None else directions
+    if cfg.in_port is None:
+        return O.alu_geometry(kernel_size=cfg.kernel, directions=m, depth=d, out_width=2)
+    (ir, ic), isz = cfg.in_port
+    (orr, oc), osz = cfg.out_port
+    return O.Geometry(tuple(cfg.grid), tuple(cfg.kernel), m, d,
+                      [("rect", (ir, ic), tuple(isz))], ("rect", (orr, oc), tuple(osz)))

@@ -29,6 +29,16 @@ def test_fftconv(be, FH, FW, hin, win, kh, kw):
     _assert_small(case_fftconv(be, B=2, M=3, hin=hin, win=win, kh=kh, kw=kw, FH=FH, FW=FW))
 
 
+@pytest.mark.parametrize("B,M,FH,FW,hin,win,kh,kw", [
+    (2, 3, 128, 128, 66, 60, 31, 21),     # one segment per pass
+    (1, 2, 64, 256, 30, 150, 13, 63),     # asymmetric grids
+    (2, 2, 256, 128, 150, 40, 63, 13),
+    (1, 2, 256, 256, 224, 224, 31, 31),   # config-3 planes: two column and two row segments
+    (2, 17, 128, 64, 40, 36, 9, 9)])      # two direction chunks in the backward reduction
+def test_fftconv_large(be, B, M, FH, FW, hin, win, kh, kw):
+    _assert_small(case_fftconv(be, B=B, M=M, hin=hin, win=win, kh=kh, kw=kw, FH=FH, FW=FW))
+
+
 def test_border_conv(be):
     _assert_small(case_border_conv(be))
 

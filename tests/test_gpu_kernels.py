@@ -26,12 +26,24 @@ def test_fftconv(be, FH, FW, hin, win, kh, kw):
     _assert_small(case_fftconv(be, B=4, M=6, hin=hin, win=win, kh=kh, kw=kw, FH=FH, FW=FW))
 
 
+@pytest.mark.parametrize("B,M,FH,FW,hin,win,kh,kw", [
+    (4, 6, 128, 128, 66, 66, 63, 63),     # config-2 literal planes
+    (2, 16, 256, 256, 112, 112, 63, 63),  # config-2 planes (one LDS segment per pass)
+    (2, 33, 256, 256, 224, 224, 31, 31),  # config-3 planes: two column / row segments, three
+                                          # direction chunks in the backward reduction
+    (3, 5, 64, 256, 30, 150, 13, 63), (3, 5, 256, 128, 150, 40, 63, 13)])
+def test_fftconv_large(be, B, M, FH, FW, hin, win, kh, kw):
+    _assert_small(case_fftconv(be, B=B, M=M, hin=hin, win=win, kh=kh, kw=kw, FH=FH, FW=FW))
+
+
 def test_fftconv_alu_batch(be):
     _assert_small(case_fftconv(be, B=128, M=16, hin=40, win=50, kh=23, kw=13, FH=64, FW=64))
 
 
 @pytest.mark.parametrize("h,w,kh,kw,FH,FW", [(12, 10, 7, 5, 32, 16), (40, 50, 23, 13, 64, 64),
-                                             (24, 32, 23, 13, 64, 64)])
+                                             (24, 32, 23, 13, 64, 64),
+                                             (112, 112, 63, 63, 256, 256),
+                                             (224, 224, 31, 31, 256, 256)])
 def test_border_conv(be, h, w, kh, kw, FH, FW):
     _assert_small(case_border_conv(be, M=16, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW))
 

@@ -96,3 +96,17 @@ def test_trained_checkpoint_parameters():
     topo = ChipTopology2D.alu_chip()
     _, _, _, x, _ = alu_case(3, B=16, out_width=1)
     check(geom, topo, cell, filt, x, "continuous", 1.0, None)
+
+
+@pytest.mark.parametrize("name,B,M", [("config2", 2, 8), ("config2_literal", 2, 8),
+                                      ("config3", 2, 8)])
+def test_large_grid_step_parity(name, B, M):
+    """Configs 2 and 3 (256x256 spectral grids, tiled epilogues; config 3 cropped to 224x224)
+    and the literal 128x128 config 2, at their full depth with a reduced batch and direction
+    count so the float64 oracle stays quick."""
+    from helpers import config_geometry
+    from neurocell.configs import CONFIGS
+    cfg = CONFIGS[name]
+    cell, filt, x, _ = cfg.synthetic(5, batch=B, directions=M)
+    check(config_geometry(cfg, directions=M), cfg.topology(directions=M), cell, filt, x,
+          cfg.codd_mode, cfg.tau, cfg.roi_bbox)

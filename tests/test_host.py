@@ -236,3 +236,32 @@ def test_backend_selection_and_validation():
     assert SUPPORTED_BACKENDS == ("auto", "nchw_direct", "rfft_hoisted", "nchw_rfft_bwd",
                                   "pallas_fused", "pallas_sram")
     assert select_optimal_backend(ChipTopology2D.alu_chip()) == "pallas_fused"
+
+
+@pytest.mark.parametrize("name", ["config0", "config1", "config2", "config2_literal", "config3",
+                                  "config4"])
+def test_benchmark_configs_geometry(name):
+    """Each benchmark workload's topology agrees with the oracle's restatement of it, its ports
+    lie inside the (cropped) ROI, and its spectral grid is one the C ABI covers."""
+    from helpers import config_geometry
+    from neurocell.configs import CONFIGS
+    from neurocell.engine import spectral_grid_supported
+    cfg = CONFIGS[name]
+    topo, geom = cfg.topology(), config_geometry(cfg)
+    assert topo.roi_shape == geom.roi_shape and tuple(topo.fft_shape) == geom.fft_shape
+    assert (topo.io_state_mask == geom.io_state_mask).all()
+    assert (topo.out_weight_mask == geom.out_weight_mask).all()
+    rows, cols = topo.out_cells_roi()
+    assert (rows == geom.out_cells_roi[0]).all() and (cols == geom.out_cells_roi[1]).all()
+    r0, r1, c0, c1 = cfg.roi_bbox or (0, topo.roi_shape[0], 0, topo.roi_shape[1])
+    assert rows.min() >= r0 and rows.max() < r1 and cols.min() >= c0 and cols.max() < c1
+    kh, kw = cfg.kernel
+    npow2 = lambda v: 1 << (v - 1).bit_length()
+    fft = (npow2(r1 - r0 + kh - 1), npow2(c1 - c0 + kw - 1))
+    assert spectral_grid_supported(*fft), fft
+    expect = {"config0": (64, 64), "config1": (64, 64), "config2": (256, 256),
+              "config2_literal": (128, 128), "config3": (256, 256), "config4": (64, 64)}
+    assert fft == expect[name]
+    cell, filt, x, y = cfg.synthetic(0, batch=2)
+    assert cell.shape == (3,) + topo.grid_shape and filt.shape == (cfg.directions, 1) + cfg.kernel
+    assert y.shape == (2,) + tuple(topo.out_port.size)
