@@ -29,25 +29,11 @@ METRIC = "train ms/step & eval samples/s at 62x62 ALU B=128; % of HBM roofline"
 HBM_PEAK_GBS = 8000.0
 
 
-def synthetic_config0(seed, B, codd_bits=3):
-    """BASELINE config 0 inputs: W~N(0,0.1), B~N(0,0.01), S~N(0,1) on (3,62,62); filters
-    ~N(0,1/K) (variance 1/K, K = 299); two uniform 8-bit operands and a 3-bit opcode as
-    {0,1} port cells; 16 seeded random target bits."""
-    rng = np.random.default_rng(seed)
-    H = W = 62
-    kh, kw, M = 23, 13, 16
-    cell = np.stack([rng.normal(0, 0.1, (H, W)), rng.normal(0, 0.01, (H, W)),
-                     rng.normal(0, 1.0, (H, W))]).astype(np.float32)
-    filt = rng.normal(0, 1.0 / np.sqrt(kh * kw), (M, 1, kh, kw)).astype(np.float32)
-    a = rng.integers(0, 256, size=B, dtype=np.uint8)
-    b = rng.integers(0, 256, size=B, dtype=np.uint8)
-    op = rng.integers(0, 1 << codd_bits, size=B, dtype=np.uint8)
-    x = np.zeros((B, 3, 8, 1), np.float32)
-    x[:, 0, :, 0] = np.unpackbits(a[:, None], axis=1)
-    x[:, 1, :, 0] = np.unpackbits(b[:, None], axis=1)
-    x[:, 2, :, 0] = np.unpackbits(op[:, None], axis=1)
-    y = rng.integers(0, 2, size=(B, 8, 2)).astype(np.float32)
-    return cell, filt, x, y
+def synthetic(name, seed, B=None):
+    """Seeded inputs of a BASELINE workload (neurocell.configs): W~N(0,0.1), B~N(0,0.01),
+    S~N(0,1) on (3,H,W); filters ~N(0,1/K) (variance 1/K); port inputs and target bits."""
+    from neurocell.configs import CONFIGS
+    return CONFIGS[name].synthetic(seed, batch=B)
 
 
 def algorithmic_bytes(B, M, N, F, hb=1, dx=1, P=16):
@@ -122,7 +108,7 @@ def cpu_baseline(seed, B, budget_s):
     host's cores: forward, MSE loss, reverse pass and AdamW.  Timed over a bounded sample."""
     from oracle import vnn_oracle as O
     cores = len(os.sched_getaffinity(0))
-    cell, filt, x, y = synthetic_config0(seed, B)
+    cell, filt, x, y = synthetic("config0", seed, B)
     geom = O.alu_geometry(out_width=2)
     m = np.zeros(cell.size + filt.size, np.float32)
     v = np.zeros_like(m)
@@ -151,6 +137,66 @@ def cpu_baseline(seed, B, budget_s):
                       "median reported"}
 
 
+def run_config(name, args, torch):
+    """Times one BASELINE workload at its full size (neurocell.configs): a HIP-graph-replayed
+    train step (or, for config 1, a forward evaluation batch) and each C-ABI kernel family at
+    the step's shapes.  Prints one JSON line; not the headline figure."""
+    from neurocell.configs import CONFIGS
+    from neurocell.engine import (EvalState, ParamState, StepPlan, TrainState, flatten_inputs,
+                                  port_input_shapes)
+    cfg = CONFIGS[name]
+    dev = torch.device("cuda")
+    topo = cfg.topology()
+    cell, filt, x, y = cfg.synthetic(0)
+    xt = torch.from_numpy(x).to(dev)
+    B = x.shape[0]
+    plan = StepPlan(topo, B, port_input_shapes(xt, topo), roi_bbox=cfg.roi_bbox,
+                    training=cfg.train)
+    ps = ParamState(torch.from_numpy(cell).to(dev), torch.from_numpy(filt).to(dev),
+                    learning_rate=1e-3)
+    if cfg.train:
+        st = TrainState(plan, ps, codd_mode=cfg.codd_mode, state_temperature=cfg.tau)
+        st.y.copy_(torch.from_numpy(y.reshape(B, -1)).to(dev))
+        run = st.step
+    else:
+        st = EvalState(plan, ps.cell, ps.filt, codd_mode=cfg.codd_mode,
+                       state_temperature=cfg.tau)
+        run = st.run
+    st.x.copy_(flatten_inputs(xt, topo))
+    if not args.no_graph:
+        st.capture()
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    rec = {"config": name, "batch": B, "grid": list(topo.grid_shape), "roi": [plan.h, plan.w],
+           "kernel": list(cfg.kernel), "directions": plan.M, "depth": plan.d,
+           "fft": list(plan.fft), "codd_mode": cfg.codd_mode, "train": cfg.train,
+           "steps": args.steps, "ms_per_step": round(wall_ms, 4),
+           "device_ms_per_step": round(e0.elapsed_time(e1) / args.steps, 4),
+           "samples_per_s": round(B / wall_ms * 1e3, 1)}
+    if cfg.train:
+        loss = float(plan.loss.item())
+        if not np.isfinite(loss):
+            raise RuntimeError(f"non-finite loss {loss}")
+        rec["final_loss"] = round(loss, 6)
+        fams = kernel_families(st, torch, args.kernel_reps)
+        ab = algorithmic_bytes(B, plan.M, plan.N, plan.F, P=plan.P)
+        rec["kernels"] = {k: {"us_per_call": round(us, 2), "calls_per_step": n,
+                              "algorithmic_MB": round(ab[k] / 1e6, 3),
+                              "GBps": round(ab[k] / (us * 1e-6) / 1e9, 1),
+                              "frac_hbm": round(ab[k] / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+                          for k, (us, n) in fams.items()}
+    print(json.dumps(rec))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -161,6 +207,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline")
     ap.add_argument("--kernel-reps", type=int, default=200)
     ap.add_argument("--no-eval", action="store_true", help="skip the evaluation legs")
+    ap.add_argument("--config", default=None,
+                    help="time one BASELINE workload of neurocell.configs at full size "
+                         "(config0..config4, config2_literal) instead of the headline line")
     ap.add_argument("--families-only", action="store_true",
                     help="profiling aid: one eager train step, a 256 MiB device copy (the "
                          "traffic-counter calibration), then --kernel-reps calls of each "
@@ -172,6 +221,9 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.config:
+        run_config(args.config, args, torch)
+        return
     from neurocell.engine import (EvalState, ParamState, StepPlan, TrainState, flatten_inputs,
                                   port_input_shapes)
     from neurocell.topology import ChipTopology2D
@@ -180,7 +232,7 @@ def main():
     topo = ChipTopology2D.alu_chip(n=8, kernel_size=(23, 13), directions=16, depth=4,
                                    out_width=2)
     B = 128
-    cell, filt, x, y = synthetic_config0(0, B)
+    cell, filt, x, y = synthetic("config0", 0, B)
     xt = torch.from_numpy(x).to(dev)
     plan = StepPlan(topo, B, port_input_shapes(xt, topo), training=True)
     ps = ParamState(torch.from_numpy(cell).to(dev), torch.from_numpy(filt).to(dev),
@@ -223,7 +275,7 @@ def main():
         ("config1_B1024_ste_ternary", 1024, "ste_ternary", 0.1),
         ("B128_continuous", 128, "continuous", 1.0))
     for name, eb, mode, tau in eval_cases:
-        _, _, xe, _ = synthetic_config0(1, eb)
+        _, _, xe, _ = synthetic("config1", 1, eb)
         xet = torch.from_numpy(xe).to(dev)
         ep = StepPlan(topo, eb, port_input_shapes(xet, topo), training=False)
         es = EvalState(ep, ps.cell, ps.filt, codd_mode=mode, state_temperature=tau)

@@ -23,6 +23,14 @@ constexpr int kTileN = 1024;         // kernels_pallas.py:58
 constexpr int kPortTile = 2048;
 constexpr int kMaxM = 64;
 
+// The border term z + hb * delta is read branch-free: with hb == 0 the kernels read z's own
+// (cached) pixels through `dl` and scale them by 0.  A uniform `if (hb)` inside the unrolled
+// element loops would make the compiler wait for every element's loads before issuing the
+// next ones, serialising the whole plane.
+NC_DEV const float* border_src(int hb, const float* delta, const float* z) {
+    return hb ? delta : z;
+}
+
 // ----------------------------------------------------------------------------------------
 // Single-pass forward: one workgroup per sample.
 // ----------------------------------------------------------------------------------------
@@ -39,13 +47,17 @@ __global__ __launch_bounds__(NT) void k_epi_fwd(int M, int N, float slope, int h
     __shared__ float red[MC * (NT / 64) + MC];
     const int b = blockIdx.x, tid = threadIdx.x;
     const float inv_n = 1.0f / (float)N;
-    float lin[PPT], ac[PPT], bv[PPT];
+    const float* dl = border_src(hb, delta, z);
+    const float hbf = hb ? 1.f : 0.f;
+    float lin[PPT], ac[PPT], bv[PPT], wv[PPT], sv[PPT];
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
-        const int p = tid + k * NT;
+        const int pc = min(tid + k * NT, N - 1);
         lin[k] = 0.f;
         ac[k] = 0.f;
-        bv[k] = bb[min(p, N - 1)];
+        bv[k] = bb[pc];
+        wv[k] = w[pc];
+        sv[k] = s[pc];
     }
     for (int m0 = 0; m0 < M; m0 += MC) {
         float zt[MC][PPT];
@@ -58,9 +70,7 @@ __global__ __launch_bounds__(NT) void k_epi_fwd(int M, int N, float slope, int h
 #pragma unroll
             for (int k = 0; k < PPT; ++k) {
                 const int pc = min(tid + k * NT, N - 1);
-                float v = z[((size_t)b * M + m) * N + pc];
-                if (hb) v += delta[(size_t)m * N + pc];
-                zt[q][k] = v;
+                zt[q][k] = z[((size_t)b * M + m) * N + pc] + hbf * dl[(size_t)m * N + pc];
             }
         }
 #pragma unroll
@@ -101,7 +111,7 @@ __global__ __launch_bounds__(NT) void k_epi_fwd(int M, int N, float slope, int h
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
         const int p = tid + k * NT;
-        if (p < N) out[(size_t)b * N + p] = w[p] * lin[k] + s[p] * ac[k];
+        if (p < N) out[(size_t)b * N + p] = wv[k] * lin[k] + sv[k] * ac[k];
     }
 }
 
@@ -118,6 +128,8 @@ __global__ __launch_bounds__(NT) void k_epi_bwd(
     __shared__ float red[2 * MC * (NT / 64) + 2 * MC];
     const int b = blockIdx.x, tid = threadIdx.x;
     const float inv_n = 1.0f / (float)N;
+    const float* dl = border_src(hb, delta, z);
+    const float hbf = hb ? 1.f : 0.f;
     float lin[PPT], ac[PPT], dbs[PPT], bv[PPT], wv[PPT], sv[PPT], g[PPT];
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
@@ -142,9 +154,7 @@ __global__ __launch_bounds__(NT) void k_epi_bwd(
 #pragma unroll
             for (int k = 0; k < PPT; ++k) {
                 const int pc = min(tid + k * NT, N - 1);
-                float v = z[((size_t)b * M + m) * N + pc];
-                if (hb) v += delta[(size_t)m * N + pc];
-                zn[q][k] = v;
+                zn[q][k] = z[((size_t)b * M + m) * N + pc] + hbf * dl[(size_t)m * N + pc];
             }
         }
 #pragma unroll
@@ -194,40 +204,68 @@ __global__ __launch_bounds__(NT) void k_epi_bwd(
     }
 }
 
-// out[r*X + x] = (acc ? out : 0) + sum_b in[(r*B + b)*X + x].  Each workgroup owns 64
-// columns; its 16 waves sum fixed contiguous slices of the batch (coalesced rows) and the
+// Fixed-order sums over the batch, several independent jobs per launch (blockIdx.y = job):
+// job.out[x] = (job.acc ? job.out[x] : 0) + sum_b job.in[b * job.X + x].  Each workgroup owns
+// 64 columns; its 16 waves sum fixed contiguous slices of the batch (coalesced rows) and the
 // 16 slice sums are added in fixed order, so the result is deterministic.
 constexpr int kRedParts = 16;
-__global__ __launch_bounds__(64 * kRedParts) void k_batch_reduce(int R, int B, int X,
-                                                                const float* __restrict__ in,
-                                                                float* __restrict__ out,
-                                                                int accumulate) {
+constexpr int kRedJobs = 4;
+
+struct RedJob {
+    const float* in;
+    float* out;
+    int X;
+    int acc;
+};
+
+struct RedJobs {
+    RedJob j[kRedJobs];
+};
+
+__global__ __launch_bounds__(64 * kRedParts) void k_batch_reduce(int B, RedJobs jobs) {
     __shared__ float part[kRedParts][64];
+    const RedJob J = jobs.j[blockIdx.y];
+    if ((int)blockIdx.x * 64 >= J.X) return;  // uniform over the workgroup
     const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
     const int x = blockIdx.x * 64 + lane;
-    const int r = blockIdx.y;
     const int b0 = (B * q) / kRedParts, b1 = (B * (q + 1)) / kRedParts;
     float s = 0.f;
-    if (x < X) {
-        const float* src = in + (size_t)r * B * X + x;
-        float a0 = 0.f, a1 = 0.f;
+    if (x < J.X) {
+        const float* src = J.in + x;
+        float a[4] = {0.f, 0.f, 0.f, 0.f};
         int b = b0;
-        for (; b + 2 <= b1; b += 2) {
-            a0 += src[(size_t)b * X];
-            a1 += src[(size_t)(b + 1) * X];
+        for (; b + 4 <= b1; b += 4) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) a[u] += src[(size_t)(b + u) * J.X];
         }
-        if (b < b1) a0 += src[(size_t)b * X];
-        s = a0 + a1;
+        for (; b < b1; ++b) a[0] += src[(size_t)b * J.X];
+        s = (a[0] + a[1]) + (a[2] + a[3]);
     }
     part[q][lane] = s;
     __syncthreads();
-    if (q == 0 && x < X) {
+    if (q == 0 && x < J.X) {
         float t = 0.f;
 #pragma unroll
         for (int k = 0; k < kRedParts; ++k) t += part[k][lane];
-        float* o = out + (size_t)r * X + x;
-        *o = accumulate ? *o + t : t;
+        float* o = J.out + x;
+        *o = J.acc ? *o + t : t;
     }
+}
+
+// Launches the non-empty jobs of `jobs` (in order) as one k_batch_reduce.
+int launch_batch_reduce(hipStream_t st, int B, const RedJob* jobs, int njobs) {
+    RedJobs pack{};
+    int n = 0, xmax = 0;
+    for (int i = 0; i < njobs; ++i) {
+        if (!jobs[i].in || jobs[i].X <= 0) continue;
+        pack.j[n++] = jobs[i];
+        xmax = std::max(xmax, jobs[i].X);
+    }
+    if (n == 0) return NC_OK;
+    hipLaunchKernelGGL(k_batch_reduce, dim3((xmax + 63) / 64, n), dim3(64 * kRedParts), 0, st, B,
+                       pack);
+    NC_CHECK_LAUNCH();
+    return NC_OK;
 }
 
 // ----------------------------------------------------------------------------------------
@@ -246,18 +284,18 @@ __global__ __launch_bounds__(kTileNT) void k_tile_stats(int M, int N, int T, int
     const int t = blockIdx.x, m = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
     const int base = t * kTileN;
     const int nt = min(kTileN, N - base);
+    const float* zp = z + ((size_t)b * M + m) * N + base;
+    const float* dp = border_src(hb, delta + (size_t)m * N, z + ((size_t)b * M + m) * N) + base;
+    const float hbf = hb ? 1.f : 0.f;
     float v[kTilePPT];
     float s1 = 0.f;
 #pragma unroll
     for (int k = 0; k < kTilePPT; ++k) {
         const int i = tid + k * kTileNT;
-        float x = 0.f;
-        if (i < nt) {
-            x = z[((size_t)b * M + m) * N + base + i];
-            if (hb) x += delta[(size_t)m * N + base + i];
-        }
-        v[k] = x;
-        s1 += x;
+        const int ic = min(i, nt - 1);
+        const float x = zp[ic] + hbf * dp[ic];
+        v[k] = i < nt ? x : 0.f;
+        s1 += v[k];
     }
     block_sum<1, kTileNT>(&s1, red);
     const float mu = s1 / (float)nt;
@@ -295,6 +333,9 @@ NC_DEV void chan_combine(const float* stats, size_t BMT, int b, int m, int M, in
     *rstd = 1.0f / sqrtf(var / (float)N + 1e-5f);
 }
 
+// Directions whose loads a tiled kernel keeps in flight together.
+constexpr int kTileMC = 4;
+
 // Per-(tile, b): statistics from the Chan partials, then standardise + Codd + sum over M.
 template <int ACT>
 __global__ __launch_bounds__(kTileNT) void k_tile_fwd(int B, int M, int N, int T, float slope,
@@ -321,25 +362,45 @@ __global__ __launch_bounds__(kTileNT) void k_tile_fwd(int B, int M, int N, int T
             rstd[(size_t)b * M + m] = r;
         }
     }
-    __syncthreads();
     const int base = t * kTileN;
     const int nt = min(kTileN, N - base);
+    const float* dl = border_src(hb, delta, z);
+    const float hbf = hb ? 1.f : 0.f;
+    int pc[kTilePPT];
+    float lin[kTilePPT], ac[kTilePPT], bv[kTilePPT], wv[kTilePPT], sv[kTilePPT];
 #pragma unroll
     for (int k = 0; k < kTilePPT; ++k) {
-        const int i = tid + k * kTileNT;
-        if (i >= nt) continue;
-        const int p = base + i;
-        const float bvv = bb[p];
-        float lin = 0.f, ac = 0.f;
-        for (int m = 0; m < M; ++m) {
-            float v = z[((size_t)b * M + m) * N + p];
-            if (hb) v += delta[(size_t)m * N + p];
-            const float zn = (v - smu[m]) * srs[m];
-            lin += zn;
-            ac += act_f<ACT>(zn + bvv, slope);
-        }
-        out[(size_t)b * N + p] = w[p] * lin + s[p] * ac;
+        pc[k] = base + min(tid + k * kTileNT, nt - 1);
+        lin[k] = ac[k] = 0.f;
+        bv[k] = bb[pc[k]];
+        wv[k] = w[pc[k]];
+        sv[k] = s[pc[k]];
     }
+    __syncthreads();
+    for (int m0 = 0; m0 < M; m0 += kTileMC) {
+        float v[kTileMC][kTilePPT];
+#pragma unroll
+        for (int q = 0; q < kTileMC; ++q) {
+            const int m = min(m0 + q, M - 1);
+#pragma unroll
+            for (int k = 0; k < kTilePPT; ++k)
+                v[q][k] = z[((size_t)b * M + m) * N + pc[k]] + hbf * dl[(size_t)m * N + pc[k]];
+        }
+#pragma unroll
+        for (int q = 0; q < kTileMC; ++q) {
+            if (m0 + q >= M) break;
+            const float mu = smu[m0 + q], r = srs[m0 + q];
+#pragma unroll
+            for (int k = 0; k < kTilePPT; ++k) {
+                const float zn = (v[q][k] - mu) * r;
+                lin[k] += zn;
+                ac[k] += act_f<ACT>(zn + bv[k], slope);
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kTilePPT; ++k)
+        if (tid + k * kTileNT < nt) out[(size_t)b * N + pc[k]] = wv[k] * lin[k] + sv[k] * ac[k];
 }
 
 // Backward stage 1 per (tile, b): per-tile partial c1/c2 (layout (2, B, M, T)) and the
@@ -350,60 +411,78 @@ __global__ __launch_bounds__(kTileNT) void k_tile_bwd1(
     const float* __restrict__ delta, const float* __restrict__ w, const float* __restrict__ s,
     const float* __restrict__ bb, const float* __restrict__ mean, const float* __restrict__ rstd,
     const float* __restrict__ gy, float* __restrict__ cpart, float* __restrict__ pg) {
-    __shared__ float red[2 * (kTileNT / 64) + 2];
+    __shared__ float red[2 * kTileMC * (kTileNT / 64) + 2 * kTileMC];
     const int t = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
     const int base = t * kTileN;
     const int nt = min(kTileN, N - base);
+    const float* dl = border_src(hb, delta, z);
+    const float hbf = hb ? 1.f : 0.f;
+    int pc[kTilePPT];
     float lin[kTilePPT], ac[kTilePPT], dbs[kTilePPT], g[kTilePPT], wv[kTilePPT], sv[kTilePPT],
         bv[kTilePPT];
 #pragma unroll
     for (int k = 0; k < kTilePPT; ++k) {
-        const int i = tid + k * kTileNT;
-        const bool in = i < nt;
-        const int p = base + i;
+        const bool in = tid + k * kTileNT < nt;
+        pc[k] = base + min(tid + k * kTileNT, nt - 1);
         lin[k] = ac[k] = dbs[k] = 0.f;
-        g[k] = in ? gy[(size_t)b * N + p] : 0.f;
-        wv[k] = in ? w[p] : 0.f;
-        sv[k] = in ? s[p] : 0.f;
-        bv[k] = in ? bb[p] : 0.f;
+        const float gv = gy[(size_t)b * N + pc[k]];
+        g[k] = in ? gv : 0.f;  // zero cotangent outside the tile
+        wv[k] = w[pc[k]];
+        sv[k] = s[pc[k]];
+        bv[k] = bb[pc[k]];
     }
     const size_t BMT = (size_t)B * M * T;
-    for (int m = 0; m < M; ++m) {
-        const float mu = mean[(size_t)b * M + m], r = rstd[(size_t)b * M + m];
-        float c[2] = {0.f, 0.f};
+    for (int m0 = 0; m0 < M; m0 += kTileMC) {
+        float v[kTileMC][kTilePPT], mu[kTileMC], r[kTileMC], c[2 * kTileMC];
 #pragma unroll
-        for (int k = 0; k < kTilePPT; ++k) {
-            const int i = tid + k * kTileNT;
-            if (i >= nt) continue;
-            const int p = base + i;
-            float v = z[((size_t)b * M + m) * N + p];
-            if (hb) v += delta[(size_t)m * N + p];
-            const float zn = (v - mu) * r;
-            float a;
-            const float da = act_fd<ACT>(zn + bv[k], slope, &a);
-            const float gn = g[k] * (wv[k] + sv[k] * da);
-            lin[k] += zn;
-            ac[k] += a;
-            dbs[k] += sv[k] * g[k] * da;
-            c[0] += gn;
-            c[1] += gn * zn;
+        for (int q = 0; q < kTileMC; ++q) {
+            const int m = min(m0 + q, M - 1);
+            mu[q] = mean[(size_t)b * M + m];
+            r[q] = rstd[(size_t)b * M + m];
+#pragma unroll
+            for (int k = 0; k < kTilePPT; ++k)
+                v[q][k] = z[((size_t)b * M + m) * N + pc[k]] + hbf * dl[(size_t)m * N + pc[k]];
         }
-        block_sum<2, kTileNT>(c, red);
-        if (tid == 0) {
-            const size_t o = ((size_t)b * M + m) * T + t;
-            cpart[o] = c[0];
-            cpart[BMT + o] = c[1];
+#pragma unroll
+        for (int q = 0; q < kTileMC; ++q) {
+            const bool mv = m0 + q < M;
+            c[q] = c[kTileMC + q] = 0.f;
+#pragma unroll
+            for (int k = 0; k < kTilePPT; ++k) {
+                const float zn = (v[q][k] - mu[q]) * r[q];
+                float a;
+                const float da = act_fd<ACT>(zn + bv[k], slope, &a);
+                const float gn = mv ? g[k] * (wv[k] + sv[k] * da) : 0.f;
+                if (mv) {
+                    lin[k] += zn;
+                    ac[k] += a;
+                    dbs[k] += sv[k] * g[k] * da;
+                }
+                c[q] += gn;
+                c[kTileMC + q] += gn * zn;
+            }
+        }
+        block_sum<2 * kTileMC, kTileNT>(c, red);
+        if (tid < kTileMC && m0 + tid < M) {
+            const size_t o = ((size_t)b * M + m0 + tid) * T + t;
+            float c1 = c[0], c2 = c[kTileMC];
+#pragma unroll
+            for (int q = 1; q < kTileMC; ++q)
+                if (tid == q) {
+                    c1 = c[q];
+                    c2 = c[kTileMC + q];
+                }
+            cpart[o] = c1;
+            cpart[BMT + o] = c2;
         }
     }
     const size_t BN = (size_t)B * N;
 #pragma unroll
     for (int k = 0; k < kTilePPT; ++k) {
-        const int i = tid + k * kTileNT;
-        if (i >= nt) continue;
-        const int p = base + i;
-        pg[(size_t)b * N + p] = g[k] * lin[k];
-        pg[BN + (size_t)b * N + p] = g[k] * ac[k];
-        pg[2 * BN + (size_t)b * N + p] = dbs[k];
+        if (tid + k * kTileNT >= nt) continue;
+        pg[(size_t)b * N + pc[k]] = g[k] * lin[k];
+        pg[BN + (size_t)b * N + pc[k]] = g[k] * ac[k];
+        pg[2 * BN + (size_t)b * N + pc[k]] = dbs[k];
     }
 }
 
@@ -418,6 +497,22 @@ __global__ __launch_bounds__(kTileNT) void k_tile_bwd2(
     const size_t BMT = (size_t)B * M * T;
     const float* c1p = cpart + ((size_t)b * M + m) * T;
     const float* c2p = c1p + BMT;
+    const int base = t * kTileN;
+    const int nt = min(kTileN, N - base);
+    const float* zp = z + ((size_t)b * M + m) * N;
+    const float* dp = border_src(hb, delta + (size_t)m * N, zp);
+    const float hbf = hb ? 1.f : 0.f;
+    int pc[kTilePPT];
+    float v[kTilePPT], bv[kTilePPT], g[kTilePPT], wv[kTilePPT], sv[kTilePPT];
+#pragma unroll
+    for (int k = 0; k < kTilePPT; ++k) {
+        pc[k] = base + min(tid + k * kTileNT, nt - 1);
+        v[k] = zp[pc[k]] + hbf * dp[pc[k]];
+        bv[k] = bb[pc[k]];
+        g[k] = gy[(size_t)b * N + pc[k]];
+        wv[k] = w[pc[k]];
+        sv[k] = s[pc[k]];
+    }
     float c1 = 0.f, c2 = 0.f;
     for (int u = 0; u < T; ++u) {
         c1 += c1p[u];
@@ -426,20 +521,13 @@ __global__ __launch_bounds__(kTileNT) void k_tile_bwd2(
     c1 /= (float)N;
     c2 /= (float)N;
     const float mu = mean[(size_t)b * M + m], r = rstd[(size_t)b * M + m];
-    const int base = t * kTileN;
-    const int nt = min(kTileN, N - base);
 #pragma unroll
     for (int k = 0; k < kTilePPT; ++k) {
-        const int i = tid + k * kTileNT;
-        if (i >= nt) continue;
-        const int p = base + i;
-        float v = z[((size_t)b * M + m) * N + p];
-        if (hb) v += delta[(size_t)m * N + p];
-        const float zn = (v - mu) * r;
+        const float zn = (v[k] - mu) * r;
         float a;
-        const float da = act_fd<ACT>(zn + bb[p], slope, &a);
-        const float gn = gy[(size_t)b * N + p] * (w[p] + s[p] * da);
-        gz[((size_t)b * M + m) * N + p] = r * (gn - c1 - zn * c2);
+        const float da = act_fd<ACT>(zn + bv[k], slope, &a);
+        const float gn = g[k] * (wv[k] + sv[k] * da);
+        if (tid + k * kTileNT < nt) gz[((size_t)b * M + m) * N + pc[k]] = r * (gn - c1 - zn * c2);
     }
 }
 
@@ -453,22 +541,26 @@ NC_DEV void plane_stats(int b, int M, int N, int hb, const float* __restrict__ z
                         const float* __restrict__ delta, float* smu, float* srs, float* red) {
     const int tid = threadIdx.x;
     const float inv_n = 1.0f / (float)N;
+    const float* dl = border_src(hb, delta, z);
+    const float hbf = hb ? 1.f : 0.f;
     for (int m0 = 0; m0 < M; m0 += MC) {
         float zt[MC][PPT], sum[MC], sq[MC];
 #pragma unroll
         for (int q = 0; q < MC; ++q) {
-            const int m = m0 + q;
+            const int m = min(m0 + q, M - 1);
+#pragma unroll
+            for (int k = 0; k < PPT; ++k) {
+                const int pc = min(tid + k * NT, N - 1);
+                zt[q][k] = z[((size_t)b * M + m) * N + pc] + hbf * dl[(size_t)m * N + pc];
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < MC; ++q) {
             sum[q] = 0.f;
 #pragma unroll
             for (int k = 0; k < PPT; ++k) {
-                const int p = tid + k * NT;
-                float v = 0.f;
-                if (m < M && p < N) {
-                    v = z[((size_t)b * M + m) * N + p];
-                    if (hb) v += delta[(size_t)m * N + p];
-                }
-                zt[q][k] = v;
-                sum[q] += v;
+                if (m0 + q >= M || tid + k * NT >= N) zt[q][k] = 0.f;
+                sum[q] += zt[q][k];
             }
         }
         block_sum<MC, NT>(sum, red);
@@ -507,8 +599,7 @@ NC_DEV void port_gather(int b, int M, int N, int P, int hb, int fact, float slop
     for (int q = tid; q < M * P; q += nt) {
         const int m = q / P, k = q % P;
         const int e = pidx[k];
-        float v = z[((size_t)b * M + m) * N + e];
-        if (hb) v += delta[(size_t)m * N + e];
+        const float v = z[((size_t)b * M + m) * N + e] + (hb ? delta[(size_t)m * N + e] : 0.f);
         const float zn = (v - smu[m]) * srs[m];
         szo[q] = zn;
         zo[(size_t)b * M * P + q] = zn;
@@ -580,10 +671,16 @@ __global__ __launch_bounds__(256) void k_port_fwd_tiled(
     port_gather(b, M, N, P, hb, fact, slope, pidx, z, delta, pp, smu, srs, szo, out, zo, pre);
 }
 
-// Port backward per (tile, b): port cotangents, (c1, c2), dense gz with the sparse port term
-// added in registers via an LDS pixel->slot map; per-sample port-parameter partials
-// ppart (3, B, P) written by tile 0.
-__global__ __launch_bounds__(256) void k_port_bwd(
+// Port backward per (tile, direction group, b): port cotangents and (c1, c2) of every
+// direction (cheap, recomputed by each workgroup), then the dense gz of the group's
+// kPortMC directions over the tile with the sparse port term added in registers through an
+// LDS pixel->slot map.  Workgroup (0, 0, b) also writes the per-sample port-parameter
+// partials ppart (3, B, P).
+constexpr int kPortNT = 256;
+constexpr int kPortPPT = kPortTile / kPortNT;
+constexpr int kPortMC = 4;
+
+__global__ __launch_bounds__(kPortNT) void k_port_bwd(
     int M, int N, int P, int hb, int fact, float slope, const int* __restrict__ pidx,
     const float* __restrict__ z, const float* __restrict__ delta, const float* __restrict__ pp,
     const float* __restrict__ zo, const float* __restrict__ mean, const float* __restrict__ rstd,
@@ -593,13 +690,13 @@ __global__ __launch_bounds__(256) void k_port_bwd(
     float* gzo = dyn;                          // M*P: port cotangent per (m, k)
     float* gsum = dyn + M * P;                 // M*P: summed per first-occurrence slot
     int* slot = reinterpret_cast<int*>(dyn + 2 * M * P);  // kPortTile
-    __shared__ float c1s[kMaxM], c2s[kMaxM], smu[kMaxM], srs[kMaxM];
+    __shared__ float c1s[kMaxM], c2s[kMaxM];
     __shared__ int first[256];
-    const int t = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, nt = blockDim.x;
-    const int B = gridDim.y;
+    const int t = blockIdx.x, mg = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+    const int B = gridDim.z;
     const float* zob = zo + (size_t)b * M * P;
     // 1. port cotangents (given directly as (B,M,P) in standardisation-only mode)
-    for (int q = tid; q < M * P; q += nt) {
+    for (int q = tid; q < M * P; q += kPortNT) {
         gsum[q] = 0.f;
         if (!pp) {
             gzo[q] = gout[(size_t)b * M * P + q];
@@ -618,13 +715,9 @@ __global__ __launch_bounds__(256) void k_port_bwd(
         }
         gzo[q] = v;
     }
-    for (int m = tid; m < M; m += nt) {
-        smu[m] = mean[(size_t)b * M + m];
-        srs[m] = rstd[(size_t)b * M + m];
-    }
     const int base = t * kPortTile;
     const int ntile = min(kPortTile, N - base);
-    for (int i = tid; i < ntile; i += nt) slot[i] = -1;
+    for (int i = tid; i < ntile; i += kPortNT) slot[i] = -1;
     __syncthreads();
     // 2. first-occurrence slots of the port cells inside this tile (sequential: duplicates
     //    of a coordinate port add up, as the reference's .at[].add does)
@@ -640,7 +733,7 @@ __global__ __launch_bounds__(256) void k_port_bwd(
         }
     }
     __syncthreads();
-    for (int m = tid; m < M; m += nt) {
+    for (int m = tid; m < M; m += kPortNT) {
         float a1 = 0.f, a2 = 0.f;
         for (int k = 0; k < P; ++k) {
             const float g = gzo[m * P + k];
@@ -652,23 +745,42 @@ __global__ __launch_bounds__(256) void k_port_bwd(
         c2s[m] = a2 / (float)N;
     }
     __syncthreads();
-    // 3. dense gz for this tile
-    for (int m = 0; m < M; ++m) {
-        const float mu = smu[m], r = srs[m], c1 = c1s[m], c2 = c2s[m];
-        for (int i = tid; i < ntile; i += nt) {
-            const int p = base + i;
-            float v = z[((size_t)b * M + m) * N + p];
-            if (hb) v += delta[(size_t)m * N + p];
-            const float zn = (v - mu) * r;
+    // 3. dense gz of this group's directions over the tile
+    const float* dl = border_src(hb, delta, z);
+    const float hbf = hb ? 1.f : 0.f;
+    const int m0 = mg * kPortMC;
+    int pc[kPortPPT], sl[kPortPPT];
+#pragma unroll
+    for (int k = 0; k < kPortPPT; ++k) {
+        const int i = min(tid + k * kPortNT, ntile - 1);
+        pc[k] = base + i;
+        sl[k] = slot[i];
+    }
+    float v[kPortMC][kPortPPT];
+#pragma unroll
+    for (int q = 0; q < kPortMC; ++q) {
+        const int m = min(m0 + q, M - 1);
+#pragma unroll
+        for (int k = 0; k < kPortPPT; ++k)
+            v[q][k] = z[((size_t)b * M + m) * N + pc[k]] + hbf * dl[(size_t)m * N + pc[k]];
+    }
+#pragma unroll
+    for (int q = 0; q < kPortMC; ++q) {
+        const int m = m0 + q;
+        if (m >= M) break;
+        const float mu = mean[(size_t)b * M + m], r = rstd[(size_t)b * M + m];
+        const float c1 = c1s[m], c2 = c2s[m];
+#pragma unroll
+        for (int k = 0; k < kPortPPT; ++k) {
+            const float zn = (v[q][k] - mu) * r;
             float gv = -r * (c1 + zn * c2);
-            const int sl = slot[i];
-            if (sl >= 0) gv += r * gsum[m * P + sl];
-            gz[((size_t)b * M + m) * N + p] = gv;
+            if (sl[k] >= 0) gv += r * gsum[m * P + sl[k]];
+            if (tid + k * kPortNT < ntile) gz[((size_t)b * M + m) * N + pc[k]] = gv;
         }
     }
     // 4. per-sample port-parameter partials
-    if (t == 0 && pp) {
-        for (int k = tid; k < P; k += nt) {
+    if (t == 0 && mg == 0 && pp) {
+        for (int k = tid; k < P; k += kPortNT) {
             const float wo = pp[k], so = pp[P + k], bo = pp[2 * P + k];
             const float go = gout[(size_t)b * P + k];
             float lin = 0.f, ac = 0.f, gbv = 0.f;
@@ -678,11 +790,11 @@ __global__ __launch_bounds__(256) void k_port_bwd(
                 gp = go * nc_act_d(pre[(size_t)b * P + k], fact, slope, &a);
             }
             for (int m = 0; m < M; ++m) {
-                const float v = zob[m * P + k];
-                lin += v;
+                const float v2 = zob[m * P + k];
+                lin += v2;
                 if (fact != NC_ACT_IDENTITY) {
                     float a;
-                    const float da = nc_act_d(v + bo, fact, slope, &a);
+                    const float da = nc_act_d(v2 + bo, fact, slope, &a);
                     ac += a;
                     gbv += gp * so * da;
                 }
@@ -724,18 +836,26 @@ SingleCfg single_cfg(int N) {
 
 int tiles_of(int N) { return (N + kTileN - 1) / kTileN; }
 
-// Forward-style kernels keep MC=16 directions of PPT pixels in registers; the backward keeps
-// two such tiles (zhat and its cotangent), so it runs MC=8.
-#define NC_SINGLE_DISPATCH(N_, MCF, KER, ...)                                                    \
+// Every thread keeps MC directions of its PPT pixels in registers (the backward two such
+// tiles: zhat and its cotangent), all loaded together.  MC shrinks as the workgroup grows so a
+// thread holds at most 64 plane values (32 in the backward) within its VGPR share.
+#define NC_SINGLE_DISPATCH(N_, BWD, KER, ...)                                                    \
     do {                                                                                         \
         SingleCfg c_ = single_cfg(N_);                                                           \
-        if (c_.nt == 256 && c_.ppt == 1) hipLaunchKernelGGL((KER<256, 1, MCF, ACT>), __VA_ARGS__); \
-        else if (c_.nt == 256 && c_.ppt == 2) hipLaunchKernelGGL((KER<256, 2, MCF, ACT>), __VA_ARGS__); \
-        else if (c_.nt == 256 && c_.ppt == 3) hipLaunchKernelGGL((KER<256, 3, MCF, ACT>), __VA_ARGS__); \
-        else if (c_.nt == 256 && c_.ppt == 4) hipLaunchKernelGGL((KER<256, 4, MCF, ACT>), __VA_ARGS__); \
-        else if (c_.nt == 512) hipLaunchKernelGGL((KER<512, 4, MCF, ACT>), __VA_ARGS__);          \
-        else if (c_.ppt == 4) hipLaunchKernelGGL((KER<1024, 4, MCF, ACT>), __VA_ARGS__);          \
-        else hipLaunchKernelGGL((KER<1024, 8, 8, ACT>), __VA_ARGS__);                           \
+        if (c_.nt == 256 && c_.ppt == 1)                                                         \
+            hipLaunchKernelGGL((KER<256, 1, BWD ? 8 : 16, ACT>), __VA_ARGS__);                   \
+        else if (c_.nt == 256 && c_.ppt == 2)                                                    \
+            hipLaunchKernelGGL((KER<256, 2, BWD ? 8 : 16, ACT>), __VA_ARGS__);                   \
+        else if (c_.nt == 256 && c_.ppt == 3)                                                    \
+            hipLaunchKernelGGL((KER<256, 3, BWD ? 8 : 16, ACT>), __VA_ARGS__);                   \
+        else if (c_.nt == 256 && c_.ppt == 4)                                                    \
+            hipLaunchKernelGGL((KER<256, 4, BWD ? 8 : 16, ACT>), __VA_ARGS__);                   \
+        else if (c_.nt == 512)                                                                   \
+            hipLaunchKernelGGL((KER<512, 4, BWD ? 8 : 16, ACT>), __VA_ARGS__);                   \
+        else if (c_.ppt == 4)                                                                    \
+            hipLaunchKernelGGL((KER<1024, 4, BWD ? 4 : 8, ACT>), __VA_ARGS__);                   \
+        else                                                                                     \
+            hipLaunchKernelGGL((KER<1024, 8, BWD ? 2 : 4, ACT>), __VA_ARGS__);                   \
     } while (0)
 
 // The port forward has no per-pixel activation: its template slot is a placeholder.
@@ -747,8 +867,8 @@ int tiles_of(int N) { return (N + kTileN - 1) / kTileN; }
         else if (c_.nt == 256 && c_.ppt == 3) hipLaunchKernelGGL((KER<256, 3, 16>), __VA_ARGS__); \
         else if (c_.nt == 256 && c_.ppt == 4) hipLaunchKernelGGL((KER<256, 4, 16>), __VA_ARGS__); \
         else if (c_.nt == 512) hipLaunchKernelGGL((KER<512, 4, 16>), __VA_ARGS__);               \
-        else if (c_.ppt == 4) hipLaunchKernelGGL((KER<1024, 4, 16>), __VA_ARGS__);               \
-        else hipLaunchKernelGGL((KER<1024, 8, 8>), __VA_ARGS__);                                \
+        else if (c_.ppt == 4) hipLaunchKernelGGL((KER<1024, 4, 8>), __VA_ARGS__);                \
+        else hipLaunchKernelGGL((KER<1024, 8, 4>), __VA_ARGS__);                                 \
     } while (0)
 
 }  // namespace
@@ -776,7 +896,7 @@ int nc_epilogue_fwd(void* stream, int B, int M, int h, int w, int act, float neg
     const int N = h * w;
     if (N <= kSingleMaxPix) {
         return dispatch_act(act, [&]<int ACT>() {
-            NC_SINGLE_DISPATCH(N, 16, k_epi_fwd, dim3(B), dim3(c_.nt), 0, st, M, N, neg_slope,
+            NC_SINGLE_DISPATCH(N, false, k_epi_fwd, dim3(B), dim3(c_.nt), 0, st, M, N, neg_slope,
                                has_border, z, delta, w_eff, s_eff, b_roi, out, mean, rstd);
             NC_CHECK_LAUNCH();
             return NC_OK;
@@ -812,7 +932,7 @@ int nc_epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg
     float* pg = reinterpret_cast<float*>(ws);
     int rc = dispatch_act(act, [&]<int ACT>() {
         if (N <= kSingleMaxPix) {
-            NC_SINGLE_DISPATCH(N, 8, k_epi_bwd, dim3(B), dim3(c_.nt), 0, st, M, N, neg_slope,
+            NC_SINGLE_DISPATCH(N, true, k_epi_bwd, dim3(B), dim3(c_.nt), 0, st, M, N, neg_slope,
                                has_border, z, delta, w_eff, s_eff, b_roi, mean, rstd, gy, gz,
                                pg);
             NC_CHECK_LAUNCH();
@@ -831,19 +951,13 @@ int nc_epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg
         return NC_OK;
     });
     if (rc != NC_OK) return rc;
-    // parameter gradients: sum over B of the per-sample partials (gw, gs, gb rows)
-    float* dst[3] = {gw, gs, gb};
-    for (int r = 0; r < 3; ++r) {
-        hipLaunchKernelGGL(k_batch_reduce, dim3((N + 63) / 64, 1), dim3(64 * kRedParts), 0, st,
-                           1, B, N, pg + (size_t)r * B * N, dst[r], accumulate_params);
-        NC_CHECK_LAUNCH();
-    }
-    if (has_border) {
-        hipLaunchKernelGGL(k_batch_reduce, dim3((M * N + 63) / 64, 1), dim3(64 * kRedParts), 0,
-                           st, 1, B, M * N, gz, gdb, accumulate_gdb);
-        NC_CHECK_LAUNCH();
-    }
-    return NC_OK;
+    // parameter gradients and the border cotangent: sums over B of the per-sample partials
+    // (gw, gs, gb rows of pg) and of gz, in one launch
+    const RedJob jobs[4] = {{pg, gw, N, accumulate_params},
+                            {pg + (size_t)B * N, gs, N, accumulate_params},
+                            {pg + 2 * (size_t)B * N, gb, N, accumulate_params},
+                            {has_border ? gz : nullptr, gdb, M * N, accumulate_gdb}};
+    return launch_batch_reduce(st, B, jobs, 4);
 }
 
 static int port_check(int B, int M, int h, int w, int P, const int32_t* port_idx,
@@ -903,21 +1017,21 @@ int nc_port_bwd(void* stream, int B, int M, int h, int w, int has_border, int fi
     const int T = (N + kPortTile - 1) / kPortTile;
     float* ppart = reinterpret_cast<float*>(ws);
     const size_t shm = (size_t)2 * M * n_port * sizeof(float) + (size_t)kPortTile * sizeof(int);
-    hipLaunchKernelGGL(k_port_bwd, dim3(T, B), dim3(256), shm, st, M, N, n_port, has_border,
+    hipLaunchKernelGGL(k_port_bwd, dim3(T, (M + kPortMC - 1) / kPortMC, B), dim3(kPortNT), shm,
+                       st, M, N, n_port, has_border,
                        final_act, neg_slope, port_idx, z, delta, port_params, zo, mean, rstd,
                        pre, g_out, gz, ppart);
     NC_CHECK_LAUNCH();
-    if (port_params) {
-        hipLaunchKernelGGL(k_batch_reduce, dim3((n_port + 63) / 64, 3), dim3(64 * kRedParts), 0,
-                           st, 3, B, n_port, ppart, g_port_params, accumulate_params);
-        NC_CHECK_LAUNCH();
-    }
-    if (has_border) {
-        hipLaunchKernelGGL(k_batch_reduce, dim3((M * N + 63) / 64, 1), dim3(64 * kRedParts), 0,
-                           st, 1, B, M * N, gz, gdb, accumulate_params);
-        NC_CHECK_LAUNCH();
-    }
-    return NC_OK;
+    // port-parameter gradients (3 rows of P) and the border cotangent, in one launch
+    const bool pj = port_params != nullptr;
+    const RedJob jobs[4] = {
+        {pj ? ppart : nullptr, g_port_params, n_port, accumulate_params},
+        {pj ? ppart + (size_t)B * n_port : nullptr, g_port_params + n_port, n_port,
+         accumulate_params},
+        {pj ? ppart + 2 * (size_t)B * n_port : nullptr, g_port_params + 2 * n_port, n_port,
+         accumulate_params},
+        {has_border ? gz : nullptr, gdb, M * N, accumulate_params}};
+    return launch_batch_reduce(st, B, jobs, 4);
 }
 
 }  // extern "C"
