@@ -153,7 +153,11 @@ int nc_fftconv_bwd(void* stream, int B, int M, int hin, int win, int hout, int w
 
 /* ---------------- piece 3: hidden-step epilogue and output-port epilogue --------------- */
 
-/* Workspace bytes for nc_epilogue_fwd / nc_epilogue_bwd at these shapes. */
+/*
+ * Workspace bytes for nc_epilogue_fwd / nc_epilogue_bwd / nc_port_fwd / nc_port_bwd at these
+ * shapes (partial results of the workgroups that share a sample, tile statistics, per-sample
+ * parameter-gradient partials).  Calls that overlap on one workspace race.
+ */
 size_t nc_epilogue_workspace_size(int B, int M, int h, int w);
 
 /*
@@ -187,8 +191,9 @@ int nc_epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg
  * plane, standardisation of the P port cells only (port_idx (P) int32 flat indices into the
  * (h,w) plane, in port order), then the port Codd algebra.  port_params (3,P) =
  * [w_eff_out, s_eff_out, b_out].  Writes out (B,P), zo (B,M,P), mean/rstd (B,M) and, when
- * final_act != identity, pre (B,P) (the pre-activation residual).  Planes above 8192 pixels use
- * the tiled Chan statistics and need ws (nc_epilogue_workspace_size bytes).
+ * final_act != identity, pre (B,P) (the pre-activation residual).  ws: nc_epilogue_workspace_size
+ * bytes (planes above 8192 pixels use it for the tiled Chan statistics, smaller batches for the
+ * split over directions).
  * port_params == NULL is pallas_standardize_output_port alone (kernels_pallas.py:1284-1347):
  * only zo, mean and rstd are written; out, pre and final_act are ignored.
  */

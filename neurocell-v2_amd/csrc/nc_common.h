@@ -49,6 +49,23 @@ NC_DEV float nc_tanh(float x) {
     return ax < 0.25f ? small : copysignf(big, x);
 }
 
+// tanh and its derivative.  For |x| >= 0.25 the derivative is r (2 - r) with
+// r = 2 / (exp(2|x|) + 1) = 1 - |tanh x|, which keeps full relative accuracy where tanh
+// saturates (1 - t*t from a rounded t would cancel).
+NC_DEV float nc_tanh_d(float x, float* y) {
+    const float ax = fabsf(x);
+    const float x2 = x * x;
+    float p = fmaf(x2, 62.0f / 2835.0f, -17.0f / 315.0f);
+    p = fmaf(x2, p, 2.0f / 15.0f);
+    p = fmaf(x2, p, -1.0f / 3.0f);
+    const float small = fmaf(x * x2, p, x);
+    const float e = __builtin_amdgcn_exp2f(ax * 2.8853900817779268f);
+    const float r = 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+    const bool sm = ax < 0.25f;
+    *y = sm ? small : copysignf(1.0f - r, x);
+    return sm ? fmaf(-small, small, 1.0f) : r * (2.0f - r);
+}
+
 NC_DEV float nc_act(float x, int act, float neg_slope) {
     switch (act) {
         case NC_ACT_TANH: return nc_tanh(x);
@@ -80,9 +97,7 @@ NC_DEV float act_f(float x, float neg_slope) {
 template <int ACT>
 NC_DEV float act_fd(float x, float neg_slope, float* y) {
     if constexpr (ACT == NC_ACT_TANH) {
-        const float t = nc_tanh(x);
-        *y = t;
-        return 1.0f - t * t;
+        return nc_tanh_d(x, y);
     } else if constexpr (ACT == NC_ACT_SIGMOID) {
         const float s = nc_sigmoid(x);
         *y = s;
@@ -123,11 +138,7 @@ inline int dispatch_act(int act, F&& f) {
 // Value and derivative together.
 NC_DEV float nc_act_d(float x, int act, float neg_slope, float* y) {
     switch (act) {
-        case NC_ACT_TANH: {
-            float t = nc_tanh(x);
-            *y = t;
-            return 1.0f - t * t;
-        }
+        case NC_ACT_TANH: return nc_tanh_d(x, y);
         case NC_ACT_SIGMOID: {
             float s = nc_sigmoid(x);
             *y = s;

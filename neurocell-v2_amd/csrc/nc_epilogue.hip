@@ -32,20 +32,28 @@ NC_DEV const float* border_src(int hb, const float* delta, const float* z) {
 }
 
 // ----------------------------------------------------------------------------------------
-// Single-pass forward: one workgroup per sample.
+// Single pass (N <= 8192): grid (B, G).  Workgroup (b, g) owns sample b's directions
+// [g * mpg, min(M, (g + 1) * mpg)), processed in chunks of MC held in registers.  With
+// G == 1 one workgroup owns the whole sample; at small batches the directions are split
+// over G workgroups so that every CU has work, and their partial sums over directions are
+// added in fixed order by a second launch (k_group_sum / k_port_combine): the kernel boundary
+// makes every XCD's partials visible without device-scope fences inside the kernel.
 // ----------------------------------------------------------------------------------------
 
 template <int NT, int PPT, int MC, int ACT>
-__global__ __launch_bounds__(NT) void k_epi_fwd(int M, int N, float slope, int hb,
+__global__ __launch_bounds__(NT) void k_epi_fwd(int M, int N, int mpg, float slope, int hb,
                                                 const float* __restrict__ z,
                                                 const float* __restrict__ delta,
                                                 const float* __restrict__ w,
                                                 const float* __restrict__ s,
                                                 const float* __restrict__ bb,
                                                 float* __restrict__ out, float* __restrict__ mean,
-                                                float* __restrict__ rstd) {
+                                                float* __restrict__ rstd,
+                                                float* __restrict__ part) {
     __shared__ float red[MC * (NT / 64) + MC];
-    const int b = blockIdx.x, tid = threadIdx.x;
+    const int b = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+    const int B = gridDim.x, G = gridDim.y;
+    const int mb = g * mpg, me = min(M, mb + mpg);
     const float inv_n = 1.0f / (float)N;
     const float* dl = border_src(hb, delta, z);
     const float hbf = hb ? 1.f : 0.f;
@@ -59,13 +67,13 @@ __global__ __launch_bounds__(NT) void k_epi_fwd(int M, int N, float slope, int h
         wv[k] = w[pc];
         sv[k] = s[pc];
     }
-    for (int m0 = 0; m0 < M; m0 += MC) {
+    for (int m0 = mb; m0 < me; m0 += MC) {
         float zt[MC][PPT];
         float sum[MC];
         // unconditional (clamped) loads keep all MC*PPT requests in flight together
 #pragma unroll
         for (int q = 0; q < MC; ++q) {
-            const int m = min(m0 + q, M - 1);
+            const int m = min(m0 + q, me - 1);
             sum[q] = 0.f;
 #pragma unroll
             for (int k = 0; k < PPT; ++k) {
@@ -77,7 +85,7 @@ __global__ __launch_bounds__(NT) void k_epi_fwd(int M, int N, float slope, int h
         for (int q = 0; q < MC; ++q)
 #pragma unroll
             for (int k = 0; k < PPT; ++k)
-                sum[q] += (m0 + q < M && tid + k * NT < N) ? zt[q][k] : 0.f;
+                sum[q] += (m0 + q < me && tid + k * NT < N) ? zt[q][k] : 0.f;
         block_sum<MC, NT>(sum, red);
         float mu[MC], sq[MC];
 #pragma unroll
@@ -94,7 +102,7 @@ __global__ __launch_bounds__(NT) void k_epi_fwd(int M, int N, float slope, int h
 #pragma unroll
         for (int q = 0; q < MC; ++q) {
             const int m = m0 + q;
-            if (m >= M) break;
+            if (m >= me) break;
             const float r = 1.0f / sqrtf(sq[q] * inv_n + 1e-5f);
 #pragma unroll
             for (int k = 0; k < PPT; ++k) {
@@ -108,47 +116,56 @@ __global__ __launch_bounds__(NT) void k_epi_fwd(int M, int N, float slope, int h
             }
         }
     }
+    float* dst = G == 1 ? out + (size_t)b * N : part + ((size_t)g * B + b) * N;
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
         const int p = tid + k * NT;
-        if (p < N) out[(size_t)b * N + p] = wv[k] * lin[k] + sv[k] * ac[k];
+        if (p < N) dst[p] = wv[k] * lin[k] + sv[k] * ac[k];
     }
 }
 
-// ----------------------------------------------------------------------------------------
-// Single-pass backward: gz, per-sample partial gw/gs/gb (reduced over B afterwards).
-// ----------------------------------------------------------------------------------------
+// out[i] = sum over g < G of part[g * n + i], fixed order (the split forward's combine).
+__global__ __launch_bounds__(256) void k_group_sum(int G, size_t n, const float* __restrict__ part,
+                                                   float* __restrict__ out) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float acc = part[i];
+    for (int q = 1; q < G; ++q) acc += part[(size_t)q * n + i];
+    out[i] = acc;
+}
 
+// Backward: gz of the workgroup's directions and its partial gw/gs/gb over them, written as
+// row (g, b) of pg (3, G*B, N) and reduced over all G*B rows afterwards.
 template <int NT, int PPT, int MC, int ACT>
 __global__ __launch_bounds__(NT) void k_epi_bwd(
-    int M, int N, float slope, int hb, const float* __restrict__ z,
+    int M, int N, int mpg, float slope, int hb, const float* __restrict__ z,
     const float* __restrict__ delta, const float* __restrict__ w, const float* __restrict__ s,
     const float* __restrict__ bb, const float* __restrict__ mean, const float* __restrict__ rstd,
     const float* __restrict__ gy, float* __restrict__ gz, float* __restrict__ pg) {
     __shared__ float red[2 * MC * (NT / 64) + 2 * MC];
-    const int b = blockIdx.x, tid = threadIdx.x;
+    const int b = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+    const int mb = g * mpg, me = min(M, mb + mpg);
     const float inv_n = 1.0f / (float)N;
     const float* dl = border_src(hb, delta, z);
     const float hbf = hb ? 1.f : 0.f;
-    float lin[PPT], ac[PPT], dbs[PPT], bv[PPT], wv[PPT], sv[PPT], g[PPT];
+    float lin[PPT], ac[PPT], dbs[PPT], bv[PPT], wv[PPT], sv[PPT], gv[PPT];
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
-        const int p = tid + k * NT;
-        const int pc = min(p, N - 1);
-        const bool in = p < N;
+        const int pc = min(tid + k * NT, N - 1);
         lin[k] = ac[k] = dbs[k] = 0.f;
         bv[k] = bb[pc];
         wv[k] = w[pc];
         sv[k] = s[pc];
-        g[k] = in ? gy[(size_t)b * N + pc] : 0.f;  // zero cotangent outside the plane
+        const float gl = gy[(size_t)b * N + pc];
+        gv[k] = tid + k * NT < N ? gl : 0.f;  // zero cotangent outside the plane
     }
-    for (int m0 = 0; m0 < M; m0 += MC) {
+    for (int m0 = mb; m0 < me; m0 += MC) {
         float zn[MC][PPT], gzn[MC][PPT];
         float c[2 * MC];
         float mr[MC], rr[MC];
 #pragma unroll
         for (int q = 0; q < MC; ++q) {
-            const int m = min(m0 + q, M - 1);
+            const int m = min(m0 + q, me - 1);
             mr[q] = mean[(size_t)b * M + m];
             rr[q] = rstd[(size_t)b * M + m];
 #pragma unroll
@@ -159,18 +176,18 @@ __global__ __launch_bounds__(NT) void k_epi_bwd(
         }
 #pragma unroll
         for (int q = 0; q < MC; ++q) {
-            const bool mv = m0 + q < M;
+            const bool mv = m0 + q < me;
             c[q] = c[MC + q] = 0.f;
 #pragma unroll
             for (int k = 0; k < PPT; ++k) {
                 const float nz = (zn[q][k] - mr[q]) * rr[q];
                 float a;
                 const float da = act_fd<ACT>(nz + bv[k], slope, &a);
-                const float gn = mv ? g[k] * (wv[k] + sv[k] * da) : 0.f;
+                const float gn = mv ? gv[k] * (wv[k] + sv[k] * da) : 0.f;
                 if (mv) {
                     lin[k] += nz;
                     ac[k] += a;
-                    dbs[k] += sv[k] * g[k] * da;
+                    dbs[k] += sv[k] * gv[k] * da;
                 }
                 zn[q][k] = nz;
                 gzn[q][k] = gn;
@@ -182,7 +199,7 @@ __global__ __launch_bounds__(NT) void k_epi_bwd(
 #pragma unroll
         for (int q = 0; q < MC; ++q) {
             const int m = m0 + q;
-            if (m >= M) break;
+            if (m >= me) break;
             const float c1 = c[q] * inv_n, c2 = c[MC + q] * inv_n;
 #pragma unroll
             for (int k = 0; k < PPT; ++k) {
@@ -192,20 +209,21 @@ __global__ __launch_bounds__(NT) void k_epi_bwd(
             }
         }
     }
-    const size_t BN = (size_t)gridDim.x * N;
+    const size_t GBN = (size_t)gridDim.y * gridDim.x * N;
+    const size_t row = ((size_t)g * gridDim.x + b) * N;
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
         const int p = tid + k * NT;
         if (p < N) {
-            pg[(size_t)b * N + p] = g[k] * lin[k];
-            pg[BN + (size_t)b * N + p] = g[k] * ac[k];
-            pg[2 * BN + (size_t)b * N + p] = dbs[k];
+            pg[row + p] = gv[k] * lin[k];
+            pg[GBN + row + p] = gv[k] * ac[k];
+            pg[2 * GBN + row + p] = dbs[k];
         }
     }
 }
 
-// Fixed-order sums over the batch, several independent jobs per launch (blockIdx.y = job):
-// job.out[x] = (job.acc ? job.out[x] : 0) + sum_b job.in[b * job.X + x].  Each workgroup owns
+// Fixed-order sums over rows, several independent jobs per launch (blockIdx.y = job):
+// job.out[x] = (job.acc ? job.out[x] : 0) + sum over r < job.rows of job.in[r * job.X + x].  Each workgroup owns
 // 64 columns; its 16 waves sum fixed contiguous slices of the batch (coalesced rows) and the
 // 16 slice sums are added in fixed order, so the result is deterministic.
 constexpr int kRedParts = 16;
@@ -216,15 +234,17 @@ struct RedJob {
     float* out;
     int X;
     int acc;
+    int rows;  // number of rows summed (the batch, or groups x batch)
 };
 
 struct RedJobs {
     RedJob j[kRedJobs];
 };
 
-__global__ __launch_bounds__(64 * kRedParts) void k_batch_reduce(int B, RedJobs jobs) {
+__global__ __launch_bounds__(64 * kRedParts) void k_batch_reduce(RedJobs jobs) {
     __shared__ float part[kRedParts][64];
     const RedJob J = jobs.j[blockIdx.y];
+    const int B = J.rows;
     if ((int)blockIdx.x * 64 >= J.X) return;  // uniform over the workgroup
     const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
     const int x = blockIdx.x * 64 + lane;
@@ -253,7 +273,7 @@ __global__ __launch_bounds__(64 * kRedParts) void k_batch_reduce(int B, RedJobs 
 }
 
 // Launches the non-empty jobs of `jobs` (in order) as one k_batch_reduce.
-int launch_batch_reduce(hipStream_t st, int B, const RedJob* jobs, int njobs) {
+int launch_batch_reduce(hipStream_t st, const RedJob* jobs, int njobs) {
     RedJobs pack{};
     int n = 0, xmax = 0;
     for (int i = 0; i < njobs; ++i) {
@@ -262,7 +282,7 @@ int launch_batch_reduce(hipStream_t st, int B, const RedJob* jobs, int njobs) {
         xmax = std::max(xmax, jobs[i].X);
     }
     if (n == 0) return NC_OK;
-    hipLaunchKernelGGL(k_batch_reduce, dim3((xmax + 63) / 64, n), dim3(64 * kRedParts), 0, st, B,
+    hipLaunchKernelGGL(k_batch_reduce, dim3((xmax + 63) / 64, n), dim3(64 * kRedParts), 0, st,
                        pack);
     NC_CHECK_LAUNCH();
     return NC_OK;
@@ -535,19 +555,19 @@ __global__ __launch_bounds__(kTileNT) void k_tile_bwd2(
 // Output port.
 // ----------------------------------------------------------------------------------------
 
-// Single-pass plane statistics for all M of sample b into LDS (N <= 8192).
+// Single-pass plane statistics of sample b's directions [mb, me) into LDS (N <= 8192).
 template <int NT, int PPT, int MC>
-NC_DEV void plane_stats(int b, int M, int N, int hb, const float* __restrict__ z,
+NC_DEV void plane_stats(int b, int M, int mb, int me, int N, int hb, const float* __restrict__ z,
                         const float* __restrict__ delta, float* smu, float* srs, float* red) {
     const int tid = threadIdx.x;
     const float inv_n = 1.0f / (float)N;
     const float* dl = border_src(hb, delta, z);
     const float hbf = hb ? 1.f : 0.f;
-    for (int m0 = 0; m0 < M; m0 += MC) {
+    for (int m0 = mb; m0 < me; m0 += MC) {
         float zt[MC][PPT], sum[MC], sq[MC];
 #pragma unroll
         for (int q = 0; q < MC; ++q) {
-            const int m = min(m0 + q, M - 1);
+            const int m = min(m0 + q, me - 1);
 #pragma unroll
             for (int k = 0; k < PPT; ++k) {
                 const int pc = min(tid + k * NT, N - 1);
@@ -559,7 +579,7 @@ NC_DEV void plane_stats(int b, int M, int N, int hb, const float* __restrict__ z
             sum[q] = 0.f;
 #pragma unroll
             for (int k = 0; k < PPT; ++k) {
-                if (m0 + q >= M || tid + k * NT >= N) zt[q][k] = 0.f;
+                if (m0 + q >= me || tid + k * NT >= N) zt[q][k] = 0.f;
                 sum[q] += zt[q][k];
             }
         }
@@ -579,7 +599,7 @@ NC_DEV void plane_stats(int b, int M, int N, int hb, const float* __restrict__ z
         if (tid == 0) {
 #pragma unroll
             for (int q = 0; q < MC; ++q)
-                if (m0 + q < M) {
+                if (m0 + q < me) {
                     smu[m0 + q] = sum[q] * inv_n;
                     srs[m0 + q] = 1.0f / sqrtf(sq[q] * inv_n + 1e-5f);
                 }
@@ -588,46 +608,76 @@ NC_DEV void plane_stats(int b, int M, int N, int hb, const float* __restrict__ z
     __syncthreads();
 }
 
-// Gather + port algebra for sample b once smu/srs are known.
-NC_DEV void port_gather(int b, int M, int N, int P, int hb, int fact, float slope,
-                        const int* __restrict__ pidx, const float* __restrict__ z,
-                        const float* __restrict__ delta, const float* __restrict__ pp,
-                        const float* smu, const float* srs, float* szo,
-                        float* __restrict__ out, float* __restrict__ zo,
-                        float* __restrict__ pre) {
+// Port algebra of one output cell from its direction sums (epilogue.py:82-128): lin = sum of
+// the standardised port values, ac = sum of act(value + b_out).
+NC_DEV float port_out(int M, int fact, float slope, float wo, float so, float bo, float lin,
+                      float ac, float* pre) {
+    if (fact == NC_ACT_IDENTITY) return (wo + so) * lin + (float)M * so * bo;
+    const float y = wo * lin + so * ac;
+    *pre = y;
+    return nc_act(y, fact, slope);
+}
+
+// Gather + port algebra for sample b's directions [mb, me) once smu/srs are known.  With G > 1
+// the direction sums go to part (2, G, B, P) and k_port_combine finishes the algebra.
+NC_DEV void port_gather(int b, int B, int M, int mb, int me, int G, int g, int N, int P, int hb,
+                        int fact, float slope, const int* __restrict__ pidx,
+                        const float* __restrict__ z, const float* __restrict__ delta,
+                        const float* __restrict__ pp, const float* smu, const float* srs,
+                        float* szo, float* __restrict__ out, float* __restrict__ zo,
+                        float* __restrict__ pre, float* __restrict__ part) {
     const int tid = threadIdx.x, nt = blockDim.x;
-    for (int q = tid; q < M * P; q += nt) {
-        const int m = q / P, k = q % P;
+    const int nm = me - mb;
+    for (int q = tid; q < nm * P; q += nt) {
+        const int m = mb + q / P, k = q % P;
         const int e = pidx[k];
         const float v = z[((size_t)b * M + m) * N + e] + (hb ? delta[(size_t)m * N + e] : 0.f);
         const float zn = (v - smu[m]) * srs[m];
         szo[q] = zn;
-        zo[(size_t)b * M * P + q] = zn;
+        zo[((size_t)b * M + m) * P + k] = zn;
     }
     if (!pp) return;  // standardisation only (uniform across the block)
     __syncthreads();
+    const size_t GBP = (size_t)G * B * P;
     for (int k = tid; k < P; k += nt) {
-        const float wo = pp[k], so = pp[P + k], bo = pp[2 * P + k];
+        const float bo = pp[2 * P + k];
         float lin = 0.f, ac = 0.f;
-        for (int m = 0; m < M; ++m) {
+        for (int m = 0; m < nm; ++m) {
             const float v = szo[m * P + k];
             lin += v;
             if (fact != NC_ACT_IDENTITY) ac += nc_act(v + bo, fact, slope);
         }
-        float o;
-        if (fact == NC_ACT_IDENTITY) {
-            o = (wo + so) * lin + (float)M * so * bo;
+        if (G == 1) {
+            out[(size_t)b * P + k] =
+                port_out(M, fact, slope, pp[k], pp[P + k], bo, lin, ac, pre + (size_t)b * P + k);
         } else {
-            const float y = wo * lin + so * ac;
-            pre[(size_t)b * P + k] = y;
-            o = nc_act(y, fact, slope);
+            part[((size_t)g * B + b) * P + k] = lin;
+            part[GBP + ((size_t)g * B + b) * P + k] = ac;
         }
-        out[(size_t)b * P + k] = o;
     }
 }
 
+// The split port forward's combine: direction sums over the G partials (fixed order), then the
+// port algebra; one thread per (b, k).
+__global__ __launch_bounds__(256) void k_port_combine(int B, int M, int P, int G, int fact,
+                                                      float slope, const float* __restrict__ pp,
+                                                      const float* __restrict__ part,
+                                                      float* __restrict__ out,
+                                                      float* __restrict__ pre) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= B * P) return;
+    const int k = i % P;
+    const size_t GBP = (size_t)G * B * P;
+    float lin = 0.f, ac = 0.f;
+    for (int q = 0; q < G; ++q) {
+        lin += part[(size_t)q * B * P + i];
+        ac += part[GBP + (size_t)q * B * P + i];
+    }
+    out[i] = port_out(M, fact, slope, pp[k], pp[P + k], pp[2 * P + k], lin, ac, pre + i);
+}
+
 template <int NT, int PPT, int MC>
-__global__ __launch_bounds__(NT) void k_port_fwd(int M, int N, int P, int hb, int fact,
+__global__ __launch_bounds__(NT) void k_port_fwd(int M, int N, int mpg, int P, int hb, int fact,
                                                  float slope, const int* __restrict__ pidx,
                                                  const float* __restrict__ z,
                                                  const float* __restrict__ delta,
@@ -635,17 +685,20 @@ __global__ __launch_bounds__(NT) void k_port_fwd(int M, int N, int P, int hb, in
                                                  float* __restrict__ out, float* __restrict__ zo,
                                                  float* __restrict__ mean,
                                                  float* __restrict__ rstd,
-                                                 float* __restrict__ pre) {
-    HIP_DYNAMIC_SHARED(float, szo)  // M*P
+                                                 float* __restrict__ pre,
+                                                 float* __restrict__ part) {
+    HIP_DYNAMIC_SHARED(float, szo)  // mpg*P
     __shared__ float smu[kMaxM], srs[kMaxM];
     __shared__ float red[MC * (NT / 64) + MC];
-    const int b = blockIdx.x;
-    plane_stats<NT, PPT, MC>(b, M, N, hb, z, delta, smu, srs, red);
-    for (int m = threadIdx.x; m < M; m += NT) {
+    const int b = blockIdx.x, g = blockIdx.y;
+    const int mb = g * mpg, me = min(M, mb + mpg);
+    plane_stats<NT, PPT, MC>(b, M, mb, me, N, hb, z, delta, smu, srs, red);
+    for (int m = mb + (int)threadIdx.x; m < me; m += NT) {
         mean[(size_t)b * M + m] = smu[m];
         rstd[(size_t)b * M + m] = srs[m];
     }
-    port_gather(b, M, N, P, hb, fact, slope, pidx, z, delta, pp, smu, srs, szo, out, zo, pre);
+    port_gather(b, gridDim.x, M, mb, me, gridDim.y, g, N, P, hb, fact, slope, pidx, z, delta, pp,
+                smu, srs, szo, out, zo, pre, part);
 }
 
 // Large planes: Chan partials (k_tile_stats) -> per-sample combine + gather.
@@ -668,7 +721,8 @@ __global__ __launch_bounds__(256) void k_port_fwd_tiled(
         rstd[(size_t)b * M + m] = r;
     }
     __syncthreads();
-    port_gather(b, M, N, P, hb, fact, slope, pidx, z, delta, pp, smu, srs, szo, out, zo, pre);
+    port_gather(b, B, M, 0, M, 1, 0, N, P, hb, fact, slope, pidx, z, delta, pp, smu, srs, szo,
+                out, zo, pre, nullptr);
 }
 
 // Port backward per (tile, direction group, b): port cotangents and (c1, c2) of every
@@ -836,39 +890,137 @@ SingleCfg single_cfg(int N) {
 
 int tiles_of(int N) { return (N + kTileN - 1) / kTileN; }
 
-// Every thread keeps MC directions of its PPT pixels in registers (the backward two such
-// tiles: zhat and its cotangent), all loaded together.  MC shrinks as the workgroup grows so a
-// thread holds at most 64 plane values (32 in the backward) within its VGPR share.
-#define NC_SINGLE_DISPATCH(N_, BWD, KER, ...)                                                    \
-    do {                                                                                         \
-        SingleCfg c_ = single_cfg(N_);                                                           \
-        if (c_.nt == 256 && c_.ppt == 1)                                                         \
-            hipLaunchKernelGGL((KER<256, 1, BWD ? 8 : 16, ACT>), __VA_ARGS__);                   \
-        else if (c_.nt == 256 && c_.ppt == 2)                                                    \
-            hipLaunchKernelGGL((KER<256, 2, BWD ? 8 : 16, ACT>), __VA_ARGS__);                   \
-        else if (c_.nt == 256 && c_.ppt == 3)                                                    \
-            hipLaunchKernelGGL((KER<256, 3, BWD ? 8 : 16, ACT>), __VA_ARGS__);                   \
-        else if (c_.nt == 256 && c_.ppt == 4)                                                    \
-            hipLaunchKernelGGL((KER<256, 4, BWD ? 8 : 16, ACT>), __VA_ARGS__);                   \
-        else if (c_.nt == 512)                                                                   \
-            hipLaunchKernelGGL((KER<512, 4, BWD ? 8 : 16, ACT>), __VA_ARGS__);                   \
-        else if (c_.ppt == 4)                                                                    \
-            hipLaunchKernelGGL((KER<1024, 4, BWD ? 4 : 8, ACT>), __VA_ARGS__);                   \
-        else                                                                                     \
-            hipLaunchKernelGGL((KER<1024, 8, BWD ? 2 : 4, ACT>), __VA_ARGS__);                   \
+// Direction split of the single-pass kernels.  Every thread keeps MC directions of its PPT
+// pixels in registers (the backward two such tiles: zhat and its cotangent), all loaded
+// together; MC shrinks as the workgroup grows so a thread stays within its VGPR share.  Below
+// kWideBatch samples one workgroup per sample leaves CUs idle, so the directions are split
+// over G workgroups of one MC chunk each (kSplitMC in the forward).
+constexpr int kWideBatch = 512;
+constexpr int kSplitMC = 4;
+
+struct DirPlan {
+    SingleCfg c;
+    int mc;   // directions per register chunk
+    int G;    // workgroups per sample
+    int mpg;  // directions per workgroup
+};
+
+DirPlan fwd_plan(int B, int M, int N) {
+    const SingleCfg c = single_cfg(N);
+    const int whole = c.nt <= 512 ? 16 : (c.ppt == 4 ? 8 : 4);
+    if (B >= kWideBatch || M <= kSplitMC) return {c, whole, 1, M};
+    return {c, kSplitMC, (M + kSplitMC - 1) / kSplitMC, kSplitMC};
+}
+
+DirPlan bwd_plan(int B, int M, int N) {
+    const SingleCfg c = single_cfg(N);
+    const int mc = c.nt <= 512 ? 8 : (c.ppt == 4 ? 4 : 2);
+    if (B >= kWideBatch || M <= mc || c.nt > 512) return {c, mc, 1, M};
+    return {c, mc, (M + mc - 1) / mc, mc};
+}
+
+// Workspace carve-up (floats, each region 256-byte aligned).
+struct EpiWs {
+    float* pg;        // (3, Gb*B, N) per-(group, sample) gw/gs/gb partials
+    float* stats;     // (4, B, M, T) tile statistics / backward (c1, c2) partials
+    float* pport;     // (3, B, 256) port-parameter partials
+    float* fpart;     // (Gf, B, N) forward partial outputs
+    float* portpart;  // (2, Gf, B, 256) port forward partial direction sums
+    size_t bytes;
+};
+
+EpiWs epi_ws(void* ws, int B, int M, int N) {
+    const bool single = N <= kSingleMaxPix;
+    const size_t Gf = single ? fwd_plan(B, M, N).G : 1;
+    const size_t Gb = single ? bwd_plan(B, M, N).G : 1;
+    const size_t T = tiles_of(N);
+    float* base = reinterpret_cast<float*>(ws);
+    size_t off = 0;
+    auto take = [&](size_t n) {
+        float* p = base ? base + off : nullptr;
+        off += (n + 63) / 64 * 64;
+        return p;
+    };
+    EpiWs e;
+    e.pg = take(3 * Gb * B * N);
+    e.stats = take(4 * (size_t)B * M * T);
+    e.pport = take(3 * (size_t)B * 256);
+    e.fpart = take(Gf * B * N);
+    e.portpart = take(2 * Gf * B * 256);
+    e.bytes = off * sizeof(float);
+    return e;
+}
+
+#define NC_LAUNCH_ACT(KER, NT_, PPT_, MC_, ...) \
+    hipLaunchKernelGGL((KER<NT_, PPT_, MC_, ACT>), __VA_ARGS__)
+
+// Forward-side dispatch over (NT, PPT, MC) of a DirPlan.
+#define NC_FWD_DISPATCH(P_, KER, ...)                                                           \
+    do {                                                                                        \
+        const SingleCfg c_ = P_.c;                                                              \
+        const bool w_ = P_.mc != kSplitMC;                                                      \
+        if (c_.nt == 256 && c_.ppt == 1) {                                                      \
+            if (w_) NC_LAUNCH_ACT(KER, 256, 1, 16, __VA_ARGS__);                                \
+            else NC_LAUNCH_ACT(KER, 256, 1, kSplitMC, __VA_ARGS__);                             \
+        } else if (c_.nt == 256 && c_.ppt == 2) {                                               \
+            if (w_) NC_LAUNCH_ACT(KER, 256, 2, 16, __VA_ARGS__);                                \
+            else NC_LAUNCH_ACT(KER, 256, 2, kSplitMC, __VA_ARGS__);                             \
+        } else if (c_.nt == 256 && c_.ppt == 3) {                                               \
+            if (w_) NC_LAUNCH_ACT(KER, 256, 3, 16, __VA_ARGS__);                                \
+            else NC_LAUNCH_ACT(KER, 256, 3, kSplitMC, __VA_ARGS__);                             \
+        } else if (c_.nt == 256 && c_.ppt == 4) {                                               \
+            if (w_) NC_LAUNCH_ACT(KER, 256, 4, 16, __VA_ARGS__);                                \
+            else NC_LAUNCH_ACT(KER, 256, 4, kSplitMC, __VA_ARGS__);                             \
+        } else if (c_.nt == 512) {                                                              \
+            if (w_) NC_LAUNCH_ACT(KER, 512, 4, 16, __VA_ARGS__);                                \
+            else NC_LAUNCH_ACT(KER, 512, 4, kSplitMC, __VA_ARGS__);                             \
+        } else if (c_.ppt == 4) {                                                               \
+            if (w_) NC_LAUNCH_ACT(KER, 1024, 4, 8, __VA_ARGS__);                                \
+            else NC_LAUNCH_ACT(KER, 1024, 4, kSplitMC, __VA_ARGS__);                            \
+        } else {                                                                                \
+            NC_LAUNCH_ACT(KER, 1024, 8, 4, __VA_ARGS__);                                        \
+        }                                                                                       \
     } while (0)
 
-// The port forward has no per-pixel activation: its template slot is a placeholder.
-#define NC_PORT_DISPATCH(N_, KER, ...)                                                           \
-    do {                                                                                         \
-        SingleCfg c_ = single_cfg(N_);                                                           \
-        if (c_.nt == 256 && c_.ppt == 1) hipLaunchKernelGGL((KER<256, 1, 16>), __VA_ARGS__);      \
-        else if (c_.nt == 256 && c_.ppt == 2) hipLaunchKernelGGL((KER<256, 2, 16>), __VA_ARGS__); \
-        else if (c_.nt == 256 && c_.ppt == 3) hipLaunchKernelGGL((KER<256, 3, 16>), __VA_ARGS__); \
-        else if (c_.nt == 256 && c_.ppt == 4) hipLaunchKernelGGL((KER<256, 4, 16>), __VA_ARGS__); \
-        else if (c_.nt == 512) hipLaunchKernelGGL((KER<512, 4, 16>), __VA_ARGS__);               \
-        else if (c_.ppt == 4) hipLaunchKernelGGL((KER<1024, 4, 8>), __VA_ARGS__);                \
-        else hipLaunchKernelGGL((KER<1024, 8, 4>), __VA_ARGS__);                                 \
+#define NC_BWD_DISPATCH(P_, KER, ...)                                                           \
+    do {                                                                                        \
+        const SingleCfg c_ = P_.c;                                                              \
+        if (c_.nt == 256 && c_.ppt == 1) NC_LAUNCH_ACT(KER, 256, 1, 8, __VA_ARGS__);            \
+        else if (c_.nt == 256 && c_.ppt == 2) NC_LAUNCH_ACT(KER, 256, 2, 8, __VA_ARGS__);       \
+        else if (c_.nt == 256 && c_.ppt == 3) NC_LAUNCH_ACT(KER, 256, 3, 8, __VA_ARGS__);       \
+        else if (c_.nt == 256 && c_.ppt == 4) NC_LAUNCH_ACT(KER, 256, 4, 8, __VA_ARGS__);       \
+        else if (c_.nt == 512) NC_LAUNCH_ACT(KER, 512, 4, 8, __VA_ARGS__);                      \
+        else if (c_.ppt == 4) NC_LAUNCH_ACT(KER, 1024, 4, 4, __VA_ARGS__);                      \
+        else NC_LAUNCH_ACT(KER, 1024, 8, 2, __VA_ARGS__);                                       \
+    } while (0)
+
+// The port forward has no per-pixel activation.
+#define NC_LAUNCH_PORT(NT_, PPT_, MC_, ...) hipLaunchKernelGGL((k_port_fwd<NT_, PPT_, MC_>), __VA_ARGS__)
+#define NC_PORT_DISPATCH(P_, ...)                                                               \
+    do {                                                                                        \
+        const SingleCfg c_ = P_.c;                                                              \
+        const bool w_ = P_.mc != kSplitMC;                                                      \
+        if (c_.nt == 256 && c_.ppt == 1) {                                                      \
+            if (w_) NC_LAUNCH_PORT(256, 1, 16, __VA_ARGS__);                                    \
+            else NC_LAUNCH_PORT(256, 1, kSplitMC, __VA_ARGS__);                                 \
+        } else if (c_.nt == 256 && c_.ppt == 2) {                                               \
+            if (w_) NC_LAUNCH_PORT(256, 2, 16, __VA_ARGS__);                                    \
+            else NC_LAUNCH_PORT(256, 2, kSplitMC, __VA_ARGS__);                                 \
+        } else if (c_.nt == 256 && c_.ppt == 3) {                                               \
+            if (w_) NC_LAUNCH_PORT(256, 3, 16, __VA_ARGS__);                                    \
+            else NC_LAUNCH_PORT(256, 3, kSplitMC, __VA_ARGS__);                                 \
+        } else if (c_.nt == 256 && c_.ppt == 4) {                                               \
+            if (w_) NC_LAUNCH_PORT(256, 4, 16, __VA_ARGS__);                                    \
+            else NC_LAUNCH_PORT(256, 4, kSplitMC, __VA_ARGS__);                                 \
+        } else if (c_.nt == 512) {                                                              \
+            if (w_) NC_LAUNCH_PORT(512, 4, 16, __VA_ARGS__);                                    \
+            else NC_LAUNCH_PORT(512, 4, kSplitMC, __VA_ARGS__);                                 \
+        } else if (c_.ppt == 4) {                                                               \
+            if (w_) NC_LAUNCH_PORT(1024, 4, 8, __VA_ARGS__);                                    \
+            else NC_LAUNCH_PORT(1024, 4, kSplitMC, __VA_ARGS__);                                \
+        } else {                                                                                \
+            NC_LAUNCH_PORT(1024, 8, 4, __VA_ARGS__);                                            \
+        }                                                                                       \
     } while (0)
 
 }  // namespace
@@ -877,12 +1029,7 @@ extern "C" {
 
 size_t nc_epilogue_workspace_size(int B, int M, int h, int w) {
     if (B <= 0 || M <= 0 || h <= 0 || w <= 0) return 0;
-    const size_t N = (size_t)h * w;
-    const size_t T = tiles_of((int)N);
-    size_t pg = 3 * (size_t)B * N;
-    size_t st = 4 * (size_t)B * M * T;
-    size_t pport = 3 * (size_t)B * 256;
-    return (pg + st + pport) * sizeof(float);
+    return epi_ws(nullptr, B, M, h * w).bytes;
 }
 
 int nc_epilogue_fwd(void* stream, int B, int M, int h, int w, int act, float neg_slope,
@@ -892,25 +1039,33 @@ int nc_epilogue_fwd(void* stream, int B, int M, int h, int w, int act, float neg
     if (B <= 0 || M <= 0 || M > kMaxM || h <= 0 || w <= 0 || !z || !w_eff || !s_eff ||
         !b_roi || !out || !mean || !rstd || (has_border && !delta) || act < 0 || act > 5)
         return NC_ERR_INVALID_ARGUMENT;
+    if (ws_bytes < nc_epilogue_workspace_size(B, M, h, w) || !ws) return NC_ERR_WORKSPACE;
     hipStream_t st = nc_stream(stream);
     const int N = h * w;
+    const EpiWs e = epi_ws(ws, B, M, N);
     if (N <= kSingleMaxPix) {
+        const DirPlan P = fwd_plan(B, M, N);
         return dispatch_act(act, [&]<int ACT>() {
-            NC_SINGLE_DISPATCH(N, false, k_epi_fwd, dim3(B), dim3(c_.nt), 0, st, M, N, neg_slope,
-                               has_border, z, delta, w_eff, s_eff, b_roi, out, mean, rstd);
+            NC_FWD_DISPATCH(P, k_epi_fwd, dim3(B, P.G), dim3(P.c.nt), 0, st, M, N, P.mpg,
+                            neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, out, mean, rstd,
+                            e.fpart);
             NC_CHECK_LAUNCH();
+            if (P.G > 1) {
+                const size_t n = (size_t)B * N;
+                hipLaunchKernelGGL(k_group_sum, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                                   st, P.G, n, e.fpart, out);
+                NC_CHECK_LAUNCH();
+            }
             return NC_OK;
         });
     }
-    if (ws_bytes < nc_epilogue_workspace_size(B, M, h, w) || !ws) return NC_ERR_WORKSPACE;
     const int T = tiles_of(N);
-    float* stats = reinterpret_cast<float*>(ws) + 3 * (size_t)B * N;
     hipLaunchKernelGGL(k_tile_stats, dim3(T, M, B), dim3(kTileNT), 0, st, M, N, T, has_border,
-                       z, delta, stats);
+                       z, delta, e.stats);
     NC_CHECK_LAUNCH();
     return dispatch_act(act, [&]<int ACT>() {
         hipLaunchKernelGGL((k_tile_fwd<ACT>), dim3(T, B), dim3(kTileNT), 0, st, B, M, N, T,
-                           neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, stats, out,
+                           neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, e.stats, out,
                            mean, rstd);
         NC_CHECK_LAUNCH();
         return NC_OK;
@@ -929,35 +1084,38 @@ int nc_epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg
     if (ws_bytes < nc_epilogue_workspace_size(B, M, h, w) || !ws) return NC_ERR_WORKSPACE;
     hipStream_t st = nc_stream(stream);
     const int N = h * w;
-    float* pg = reinterpret_cast<float*>(ws);
+    const EpiWs e = epi_ws(ws, B, M, N);
+    int rows = B;  // rows of each pg partial plane
     int rc = dispatch_act(act, [&]<int ACT>() {
         if (N <= kSingleMaxPix) {
-            NC_SINGLE_DISPATCH(N, true, k_epi_bwd, dim3(B), dim3(c_.nt), 0, st, M, N, neg_slope,
-                               has_border, z, delta, w_eff, s_eff, b_roi, mean, rstd, gy, gz,
-                               pg);
+            const DirPlan P = bwd_plan(B, M, N);
+            rows = P.G * B;
+            NC_BWD_DISPATCH(P, k_epi_bwd, dim3(B, P.G), dim3(P.c.nt), 0, st, M, N, P.mpg,
+                            neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, mean, rstd, gy,
+                            gz, e.pg);
             NC_CHECK_LAUNCH();
             return NC_OK;
         }
         const int T = tiles_of(N);
-        float* cpart = pg + 3 * (size_t)B * N;
         hipLaunchKernelGGL((k_tile_bwd1<ACT>), dim3(T, B), dim3(kTileNT), 0, st, B, M, N, T,
                            neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, mean, rstd, gy,
-                           cpart, pg);
+                           e.stats, e.pg);
         NC_CHECK_LAUNCH();
         hipLaunchKernelGGL((k_tile_bwd2<ACT>), dim3(T, M, B), dim3(kTileNT), 0, st, B, M, N, T,
                            neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, mean, rstd, gy,
-                           cpart, gz);
+                           e.stats, gz);
         NC_CHECK_LAUNCH();
         return NC_OK;
     });
     if (rc != NC_OK) return rc;
-    // parameter gradients and the border cotangent: sums over B of the per-sample partials
-    // (gw, gs, gb rows of pg) and of gz, in one launch
-    const RedJob jobs[4] = {{pg, gw, N, accumulate_params},
-                            {pg + (size_t)B * N, gs, N, accumulate_params},
-                            {pg + 2 * (size_t)B * N, gb, N, accumulate_params},
-                            {has_border ? gz : nullptr, gdb, M * N, accumulate_gdb}};
-    return launch_batch_reduce(st, B, jobs, 4);
+    // parameter gradients and the border cotangent: sums over the partial rows (gw, gs, gb
+    // planes of pg) and over B of gz, in one launch
+    const size_t RN = (size_t)rows * N;
+    const RedJob jobs[4] = {{e.pg, gw, N, accumulate_params, rows},
+                            {e.pg + RN, gs, N, accumulate_params, rows},
+                            {e.pg + 2 * RN, gb, N, accumulate_params, rows},
+                            {has_border ? gz : nullptr, gdb, M * N, accumulate_gdb, B}};
+    return launch_batch_reduce(st, jobs, 4);
 }
 
 static int port_check(int B, int M, int h, int w, int P, const int32_t* port_idx,
@@ -977,25 +1135,33 @@ int nc_port_fwd(void* stream, int B, int M, int h, int w, int has_border, int fi
     if (!zo || !mean || !rstd || (port_params && !out) ||
         (port_params && final_act != NC_ACT_IDENTITY && !pre))
         return NC_ERR_INVALID_ARGUMENT;
+    if (ws_bytes < nc_epilogue_workspace_size(B, M, h, w) || !ws) return NC_ERR_WORKSPACE;
     hipStream_t st = nc_stream(stream);
     const int N = h * w;
-    const size_t shm = (size_t)M * n_port * sizeof(float);
+    const EpiWs e = epi_ws(ws, B, M, N);
     if (N <= kSingleMaxPix) {
-        NC_PORT_DISPATCH(N, k_port_fwd, dim3(B), dim3(c_.nt), shm, st, M, N, n_port,
-                           has_border, final_act, neg_slope, port_idx, z, delta, port_params,
-                           out, zo, mean, rstd, pre);
+        const DirPlan P = fwd_plan(B, M, N);
+        const size_t shm = (size_t)P.mpg * n_port * sizeof(float);
+        NC_PORT_DISPATCH(P, dim3(B, P.G), dim3(P.c.nt), shm, st, M, N, P.mpg, n_port,
+                         has_border, final_act, neg_slope, port_idx, z, delta, port_params, out,
+                         zo, mean, rstd, pre, e.portpart);
         NC_CHECK_LAUNCH();
+        if (P.G > 1 && port_params) {
+            hipLaunchKernelGGL(k_port_combine, dim3((B * n_port + 255) / 256), dim3(256), 0, st, B,
+                               M, n_port, P.G, final_act, neg_slope, port_params, e.portpart, out,
+                               pre);
+            NC_CHECK_LAUNCH();
+        }
         return NC_OK;
     }
-    if (ws_bytes < nc_epilogue_workspace_size(B, M, h, w) || !ws) return NC_ERR_WORKSPACE;
     const int T = tiles_of(N);
-    float* stats = reinterpret_cast<float*>(ws) + 3 * (size_t)B * N;
     hipLaunchKernelGGL(k_tile_stats, dim3(T, M, B), dim3(kTileNT), 0, st, M, N, T, has_border,
-                       z, delta, stats);
+                       z, delta, e.stats);
     NC_CHECK_LAUNCH();
+    const size_t shm = (size_t)M * n_port * sizeof(float);
     hipLaunchKernelGGL(k_port_fwd_tiled, dim3(B), dim3(256), shm, st, B, M, N, T, n_port,
                        has_border, final_act, neg_slope, port_idx, z, delta, port_params,
-                       stats, out, zo, mean, rstd, pre);
+                       e.stats, out, zo, mean, rstd, pre);
     NC_CHECK_LAUNCH();
     return NC_OK;
 }
@@ -1015,23 +1181,23 @@ int nc_port_bwd(void* stream, int B, int M, int h, int w, int has_border, int fi
     hipStream_t st = nc_stream(stream);
     const int N = h * w;
     const int T = (N + kPortTile - 1) / kPortTile;
-    float* ppart = reinterpret_cast<float*>(ws);
+    const EpiWs e = epi_ws(ws, B, M, N);
+    float* ppart = e.pport;
     const size_t shm = (size_t)2 * M * n_port * sizeof(float) + (size_t)kPortTile * sizeof(int);
     hipLaunchKernelGGL(k_port_bwd, dim3(T, (M + kPortMC - 1) / kPortMC, B), dim3(kPortNT), shm,
-                       st, M, N, n_port, has_border,
-                       final_act, neg_slope, port_idx, z, delta, port_params, zo, mean, rstd,
-                       pre, g_out, gz, ppart);
+                       st, M, N, n_port, has_border, final_act, neg_slope, port_idx, z, delta,
+                       port_params, zo, mean, rstd, pre, g_out, gz, ppart);
     NC_CHECK_LAUNCH();
     // port-parameter gradients (3 rows of P) and the border cotangent, in one launch
     const bool pj = port_params != nullptr;
     const RedJob jobs[4] = {
-        {pj ? ppart : nullptr, g_port_params, n_port, accumulate_params},
+        {pj ? ppart : nullptr, g_port_params, n_port, accumulate_params, B},
         {pj ? ppart + (size_t)B * n_port : nullptr, g_port_params + n_port, n_port,
-         accumulate_params},
+         accumulate_params, B},
         {pj ? ppart + 2 * (size_t)B * n_port : nullptr, g_port_params + 2 * n_port, n_port,
-         accumulate_params},
-        {has_border ? gz : nullptr, gdb, M * N, accumulate_params}};
-    return launch_batch_reduce(st, B, jobs, 4);
+         accumulate_params, B},
+        {has_border ? gz : nullptr, gdb, M * N, accumulate_params, B}};
+    return launch_batch_reduce(st, jobs, 4);
 }
 
 }  // extern "C"

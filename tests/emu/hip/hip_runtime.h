@@ -57,6 +57,7 @@ hipError_t hipGetLastError();
 enum { hipFuncAttributeMaxDynamicSharedMemorySize = 8 };
 #define __builtin_amdgcn_sched_barrier(mask) ((void)0)
 #define __builtin_amdgcn_exp2f(x) exp2f(x)
+
 #define __builtin_amdgcn_rcpf(x) (1.0f / (x))
 #define NC_PIN(x) ((void)0)
 #define NC_FENCE() ((void)0)

@@ -44,13 +44,17 @@ def test_border_conv(be):
 
 
 @pytest.mark.parametrize("shape", [(2, 3, 10, 12, "tanh", 1), (2, 3, 20, 40, "leaky_relu", 0),
-                                   (1, 2, 96, 90, "gelu", 1)])
+                                   (1, 2, 96, 90, "gelu", 1),
+                                   # directions split over workgroups (forward groups of 4,
+                                   # backward groups of 8), the last group partial
+                                   (3, 9, 10, 12, "tanh", 1), (2, 17, 6, 7, "sigmoid", 0)])
 def test_epilogue(be, shape):
     _assert_small(case_epilogue(be, *shape))
 
 
 @pytest.mark.parametrize("shape", [
     (2, 3, 10, 12, (2, 3, 4, 2), (5, 5, 5, 5), None),
+    (3, 9, 10, 12, (2, 3, 4, 2), (5, 5, 5, 5), "tanh"),  # split port forward, ticket combine
     (1, 2, 96, 100, (10, 50, 95), (3, 99, 0), "tanh")])
 def test_port(be, shape):
     B, M, h, w, rows, cols, fact = shape
