@@ -9,13 +9,14 @@
 //   k_wrfft2<FLIP>        grid (planes/PPW)        half-spectra of real planes: the cell spectra
 //                                                  xhat_b and (FLIP) ghat_m = rfft2(flip(G_m))
 //   k_wconv_fwd           grid (B*M/PPW)           z_bm = irfft2(xhat_b * ghat_m), cropped window
-//   k_wbwd_dx             grid (M/PPW, B)          sum over the wave's directions of
-//                                                  rfft2(gz_bm) * conj(ghat_m)
+//   k_wbwd_part           grid (M/PPW, B)          rfft2(gz_bm) once per plane, stored for the
+//                                                  dG reduction; sum over the wave's directions
+//                                                  of rfft2(gz_bm) * conj(ghat_m) (dx partials)
 //   k_wbwd_dx_fin         grid (B/PPW)             fixed-order sum of those partials, irfft2 with
 //                                                  the unshifted roll -> dx_b
-//   k_wbwd_dg             grid (M/PPW, chunks)     sum over a B-chunk of rfft2(gz_bm) * conj(xhat_b)
-//                                                  (registers)
-//   k_wbwd_dg_fin         grid (F/256, M)          fixed-order sum over chunks, unpacked -> dghat
+//   k_wbwd_dg_red         grid (F/256, M, chunks)  fixed-order sums over sample chunks of the
+//                                                  stored spectra times conj(xhat_b), unpacked
+//   k_wbwd_dg_sum         grid (F/256, M)          fixed-order sum over the chunks -> dghat
 //   k_filter_spectrum_bwd grid (M)                 dG_m = flip(crop(roll(irfft2(dghat_m))))
 // No atomics anywhere: the M- and B-reductions are two-stage trees in the frequency domain.
 #include <algorithm>
@@ -25,6 +26,12 @@
 #include "nc_wave.h"
 
 namespace {
+
+// Plane pitch (cpx) of the stored cotangent half-spectra, padded to a multiple of 64.
+template <int FH, int FW>
+constexpr size_t spec_pitch() {
+    return ((size_t)WGeo<FH, FW>::F + 63) / 64 * 64;
+}
 
 template <int FH, int FW>
 struct Smem {
@@ -147,18 +154,18 @@ __global__ __launch_bounds__(64) void k_wconv_fwd(int nplanes, int M, int hout, 
     ostage_copy<FW>(O, np, hout, wout, z + (size_t)g0 * hout * wout);
 }
 
-// First stage of both reductions of the backward (kernels_pallas.py:1794-1821), in the packed
-// layout.  The wavefront transforms PPW planes of gz and sums their products with a conjugated
-// real-signal spectrum:
-//   DG == false (dx): planes (b, m = j*PPW + ps), reference ghat_m; part[b][j]   (grid MG x B)
-//   DG == true  (dG): planes (b = j*PPW + ps, m), reference xhat_b; part[j][m]   (grid M x BG)
-// Planes past the end are staged as zeros and contribute nothing.
-template <int FH, int FW, bool DG>
+// Backward first stage (kernels_pallas.py:1794-1821), in the packed layout.  Wavefront
+// (mg, b) transforms the gz planes (b, m = mg*PPW + ps) once; it stores each plane's
+// half-spectrum in spec (M, B, pitch) for the dG reduction (k_wbwd_dg_red) and, when need_dx, writes
+// part[b][mg] = sum over its planes of rfft2(gz_bm) * conj(ghat_m) for the dx chain.  Planes
+// past M are staged as zeros and contribute nothing.
+template <int FH, int FW>
 __global__ __launch_bounds__(64) void k_wbwd_part(int B, int M, int hout, int wout, int s_off,
-                                                  int nq_off, int vec,
+                                                  int nq_off, int vec, int need_dx,
                                                   const float* __restrict__ gz,
-                                                  const cpx* __restrict__ ref,
-                                                  cpx* __restrict__ part) {
+                                                  const cpx* __restrict__ ghat,
+                                                  cpx* __restrict__ part,
+                                                  cpx* __restrict__ spec) {
     using W = WGeo<FH, FW>;
     HIP_DYNAMIC_SHARED(float, lds)
     cpx* T = reinterpret_cast<cpx*>(lds);
@@ -166,40 +173,46 @@ __global__ __launch_bounds__(64) void k_wbwd_part(int B, int M, int hout, int wo
     cpx* NQ = reinterpret_cast<cpx*>(lds) + nq_off;
     const int lane = threadIdx.x, ps = lane / W::NC, kc = lane % W::NC;
     const size_t n = (size_t)hout * wout;
-    int b0, m0, np;
-    size_t pstride;
-    if (DG) {
-        m0 = blockIdx.x;
-        b0 = blockIdx.y * W::PPW;
-        np = min(W::PPW, B - b0);
-        pstride = (size_t)M * n;
-    } else {
-        b0 = blockIdx.y;
-        m0 = blockIdx.x * W::PPW;
-        np = min(W::PPW, M - m0);
-        pstride = n;
-    }
-    istage<FW, W::PPW, false>(gz + ((size_t)b0 * M + m0) * n, pstride, np, hout, wout, vec != 0,
-                              S);
+    const int b0 = blockIdx.y;
+    const int m0 = blockIdx.x * W::PPW;
+    const int np = min(W::PPW, M - m0);
+    istage<FW, W::PPW, false>(gz + ((size_t)b0 * M + m0) * n, n, np, hout, wout, vec != 0, S);
     const int q = min(ps, np - 1);
-    const cpx* R = ref + (size_t)(DG ? b0 + q : m0 + q) * W::F;
+    const cpx* R = ghat + (size_t)(m0 + q) * W::F;
     cpx r[FH];  // the reference column, loaded while the transform runs
+    if (need_dx) {
 #pragma unroll
-    for (int kh = 0; kh < FH; ++kh) r[kh] = R[kh * W::SP + kc];
-    stage_nyquist<FH, FW>(
-        [&](int p) { return ref + (size_t)(DG ? b0 + min(p, np - 1) : m0 + min(p, np - 1)) * W::F; },
-        NQ);
+        for (int kh = 0; kh < FH; ++kh) r[kh] = R[kh * W::SP + kc];
+        stage_nyquist<FH, FW>([&](int p) { return ghat + (size_t)(m0 + min(p, np - 1)) * W::F; },
+                              NQ);
+    }
     __syncthreads();
     wrow_fwd<FH, FW>(S, hout, T);
     __syncthreads();
     cpx v[FH];
     wcol_fwd<FH, FW>(T, hout, v);
+    if (ps < np) {
+        // half-spectrum of the plane: the lane of packed column 0 splits DC + i*Nyquist with
+        // its row mirrors (all in its registers) into the DC and Nyquist columns
+        cpx* o = spec + ((size_t)(m0 + ps) * B + b0) * spec_pitch<FH, FW>() + kc;
+        if (kc != 0) {
+#pragma unroll
+            for (int kh = 0; kh < FH; ++kh) o[kh * W::SP] = v[kh];
+        } else {
+#pragma unroll
+            for (int kh = 0; kh < FH; ++kh) {
+                const cpx c = v[kh], d = cconj(v[(FH - kh) & (FH - 1)]);
+                o[kh * W::SP] = cscale(cadd(c, d), 0.5f);
+                o[kh * W::SP + FW / 2] = cmul_negi(cscale(csub(c, d), 0.5f));
+            }
+        }
+    }
+    if (!need_dx) return;  // uniform over the launch
     packed_mulc<FH>(v, r, kc, [&](int kh) { return NQ[ps * FH + kh]; });
     // sum over the wavefront's planes, half a spectrum at a time, through T
     constexpr int HH = FH / 2;
     cpx* red = T;
-    cpx* dst = part + (DG ? ((size_t)blockIdx.y * M + m0) : ((size_t)b0 * gridDim.x + blockIdx.x)) *
-                          W::PF;
+    cpx* dst = part + ((size_t)b0 * gridDim.x + blockIdx.x) * W::PF;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         __syncthreads();
@@ -267,30 +280,63 @@ __global__ __launch_bounds__(64) void k_wbwd_dx_fin(int B, int hin, int win, int
     ostage_copy<FW>(O, np, hin, win, dx + (size_t)b0 * hin * win);
 }
 
-// dghat, second stage: fixed-order sum over the chunks, packed column unpacked into the DC
-// and Nyquist columns; conj_out gives the conjugate convention, accumulate adds.
+constexpr int kDgBatch = 16;  // samples whose loads a dG-reduction thread keeps in flight
+
+// dG reduction (kernels_pallas.py:1818-1820), first stage: over the samples of chunk
+// c = blockIdx.z, in increasing b, of rfft2(gz_bm) * conj(xhat_b), bin by bin, from the stored
+// half-spectra spec (M, B, pitch).  With one chunk the result goes to dghat directly
+// (conj_out: conjugate convention, accumulate: add); otherwise to part (chunks, M, F) for
+// k_wbwd_dg_sum.
 template <int FH, int FW>
-__global__ void k_wbwd_dg_fin(int nchunk, int M, const cpx* __restrict__ part,
-                              cpx* __restrict__ dghat, int accumulate, int conj_out) {
+__global__ __launch_bounds__(256) void k_wbwd_dg_red(int B, int M, int bper,
+                                                     const cpx* __restrict__ spec,
+                                                     const cpx* __restrict__ xhat,
+                                                     cpx* __restrict__ part,
+                                                     cpx* __restrict__ dghat, int accumulate,
+                                                     int conj_out) {
     using W = WGeo<FH, FW>;
-    const int m = blockIdx.y;
+    constexpr size_t SPP = spec_pitch<FH, FW>();
+    const int m = blockIdx.y, c = blockIdx.z;
     const int e = blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= W::F) return;
-    const int kh = e / W::SP, kw = e - kh * W::SP;
-    auto sum = [&](int k, int col) {
-        return sum_strided(part + (size_t)m * W::PF + k * W::NC + col, nchunk,
-                           (size_t)M * W::PF);
-    };
-    cpx s;
-    if (kw == 0 || kw == FW / 2) {
-        const cpx a = sum(kh, 0), d = cconj(sum((FH - kh) & (FH - 1), 0));
-        s = kw == 0 ? cscale(cadd(a, d), 0.5f) : cmul_negi(cscale(csub(a, d), 0.5f));
-    } else {
-        s = sum(kh, kw);
+    const int b0 = c * bper, b1 = min(B, b0 + bper);
+    const cpx* S = spec + (size_t)m * B * SPP + e;
+    const cpx* X = xhat + e;
+    cpx acc = cmk(0.f, 0.f);
+    for (int bb = b0; bb < b1; bb += kDgBatch) {
+        // the batch's loads are issued together (clamped), then added in increasing b
+        cpx u[kDgBatch], xv[kDgBatch];
+#pragma unroll
+        for (int j = 0; j < kDgBatch; ++j) {
+            const int b = min(bb + j, b1 - 1);
+            u[j] = S[(size_t)b * SPP];
+            xv[j] = X[(size_t)b * W::F];
+        }
+#pragma unroll
+        for (int j = 0; j < kDgBatch; ++j)
+            if (bb + j < b1) acc = cadd(acc, cmulc(u[j], xv[j]));
     }
-    if (conj_out) s = cconj(s);
-    cpx* o = dghat + (size_t)m * W::F + e;
-    *o = accumulate ? cadd(*o, s) : s;
+    if (gridDim.z == 1) {
+        if (conj_out) acc = cconj(acc);
+        cpx* o = dghat + (size_t)m * W::F + e;
+        *o = accumulate ? cadd(*o, acc) : acc;
+    } else {
+        part[((size_t)c * M + m) * W::F + e] = acc;
+    }
+}
+
+// dG reduction, second stage: dghat[m] (+)= sum over the chunks in order (grid (F/256, M)).
+__global__ __launch_bounds__(256) void k_wbwd_dg_sum(int nchunk, int M, int F,
+                                                     const cpx* __restrict__ part,
+                                                     cpx* __restrict__ dghat, int accumulate,
+                                                     int conj_out) {
+    const int m = blockIdx.y;
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= F) return;
+    cpx v = sum_strided(part + (size_t)m * F + e, nchunk, (size_t)M * F);
+    if (conj_out) v = cconj(v);
+    cpx* o = dghat + (size_t)m * F + e;
+    *o = accumulate ? cadd(*o, v) : v;
 }
 
 // ----------------------------------------------------------------------------------------
@@ -334,21 +380,31 @@ void lds_limit(K kernel, size_t bytes) {
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
 }
 
-struct BwdSplit {
-    int mg;      // direction groups (dx partials per sample)
-    int nchunk;  // sample groups (dG partials per direction)
-};
-
+// Direction groups of the backward: each wavefront transforms PPW planes of one sample.
 template <int FH, int FW>
-BwdSplit bwd_split(int B, int M) {
+int bwd_groups(int M) {
     constexpr int PPW = WGeo<FH, FW>::PPW;
-    return BwdSplit{(M + PPW - 1) / PPW, (B + PPW - 1) / PPW};
+    return (M + PPW - 1) / PPW;
 }
 
+// Sample chunks of the dG reduction: enough threads (about 2^18) to keep HBM busy.
+template <int FH, int FW>
+int dg_chunks(int B, int M) {
+    const int per = M * WGeo<FH, FW>::F;
+    const int by_threads = (262144 + per - 1) / per;
+    const int by_batch = (B + kDgBatch - 1) / kDgBatch;  // at most one load batch per chunk
+    return std::max(1, std::min(B, std::max(by_threads, by_batch)));
+}
+
+// Workspace: dx partials (B, MG, PF), their sums (B, PF), the cotangent half-spectra
+// (M, B, pitch) and the dG chunk partials (chunks, M, F).
 template <int FH, int FW>
 size_t bwd_ws(int B, int M) {
-    BwdSplit s = bwd_split<FH, FW>(B, M);
-    return ((size_t)B * s.mg + (size_t)B + (size_t)s.nchunk * M) * WGeo<FH, FW>::PF * sizeof(cpx);
+    using W = WGeo<FH, FW>;
+    const size_t mg = bwd_groups<FH, FW>(M);
+    const size_t nc = dg_chunks<FH, FW>(B, M);
+    return (((size_t)B * mg + (size_t)B) * W::PF + (size_t)M * B * spec_pitch<FH, FW>() +
+            nc * M * W::F) * sizeof(cpx);
 }
 
 template <int FH, int FW>
@@ -392,19 +448,19 @@ int launch_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wou
                int pw, const float* gz, const float* xhat, const float* ghat, int need_dx,
                float* dx, float* dghat, int accumulate, int conj_out, void* ws) {
     using W = WGeo<FH, FW>;
-    BwdSplit s = bwd_split<FH, FW>(B, M);
+    const int mg = bwd_groups<FH, FW>(M);
     cpx* dxpart = reinterpret_cast<cpx*>(ws);
-    cpx* dxsum = dxpart + (size_t)B * s.mg * W::PF;
-    cpx* dgpart = dxsum + (size_t)B * W::PF;
+    cpx* dxsum = dxpart + (size_t)B * mg * W::PF;
+    cpx* spec = dxsum + (size_t)B * W::PF;
     const WLds<FH, FW> lp(hout, wout, (size_t)64 * (FH / 2) * sizeof(cpx));
+    lds_limit(k_wbwd_part<FH, FW>, lp.bytes);
+    hipLaunchKernelGGL((k_wbwd_part<FH, FW>), dim3(mg, B), dim3(64), lp.bytes, st, B, M, hout,
+                       wout, lp.off, lp.nq, vec_ok(gz, (size_t)hout * wout), need_dx, gz,
+                       reinterpret_cast<const cpx*>(ghat), dxpart, spec);
+    NC_CHECK_LAUNCH();
     if (need_dx) {
-        lds_limit(k_wbwd_part<FH, FW, false>, lp.bytes);
-        hipLaunchKernelGGL((k_wbwd_part<FH, FW, false>), dim3(s.mg, B), dim3(64), lp.bytes, st, B,
-                           M, hout, wout, lp.off, lp.nq, vec_ok(gz, (size_t)hout * wout), gz,
-                           reinterpret_cast<const cpx*>(ghat), dxpart);
-        NC_CHECK_LAUNCH();
-        hipLaunchKernelGGL(k_psum, dim3((W::PF + 255) / 256, B), dim3(256), 0, st, s.mg, W::PF,
-                           (size_t)s.mg * W::PF, (size_t)W::PF, dxpart, dxsum);
+        hipLaunchKernelGGL(k_psum, dim3((W::PF + 255) / 256, B), dim3(256), 0, st, mg, W::PF,
+                           (size_t)mg * W::PF, (size_t)W::PF, dxpart, dxsum);
         NC_CHECK_LAUNCH();
         const WLds<FH, FW> lf(hin, win);
         lds_limit(k_wbwd_dx_fin<FH, FW>, lf.bytes);
@@ -413,14 +469,19 @@ int launch_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wou
                            dxsum, dx);
         NC_CHECK_LAUNCH();
     }
-    lds_limit(k_wbwd_part<FH, FW, true>, lp.bytes);
-    hipLaunchKernelGGL((k_wbwd_part<FH, FW, true>), dim3(M, s.nchunk), dim3(64), lp.bytes, st, B,
-                       M, hout, wout, lp.off, lp.nq, vec_ok(gz, (size_t)hout * wout), gz,
-                       reinterpret_cast<const cpx*>(xhat), dgpart);
+    constexpr int nthr = W::F;
+    const int nchunk = dg_chunks<FH, FW>(B, M);
+    const int bper = (B + nchunk - 1) / nchunk;
+    cpx* dgpart = spec + (size_t)M * B * spec_pitch<FH, FW>();
+    hipLaunchKernelGGL((k_wbwd_dg_red<FH, FW>), dim3((nthr + 255) / 256, M, nchunk), dim3(256), 0,
+                       st, B, M, bper, spec, reinterpret_cast<const cpx*>(xhat), dgpart,
+                       reinterpret_cast<cpx*>(dghat), accumulate, conj_out);
     NC_CHECK_LAUNCH();
-    hipLaunchKernelGGL((k_wbwd_dg_fin<FH, FW>), dim3((W::F + 255) / 256, M), dim3(256), 0, st,
-                       s.nchunk, M, dgpart, reinterpret_cast<cpx*>(dghat), accumulate, conj_out);
-    NC_CHECK_LAUNCH();
+    if (nchunk > 1) {
+        hipLaunchKernelGGL(k_wbwd_dg_sum, dim3((W::F + 255) / 256, M), dim3(256), 0, st, nchunk,
+                           M, W::F, dgpart, reinterpret_cast<cpx*>(dghat), accumulate, conj_out);
+        NC_CHECK_LAUNCH();
+    }
     return NC_OK;
 }
 
