@@ -103,6 +103,68 @@ def kernel_families(ts, torch, reps):
     return {k: (time_family(f, reps, torch), per_step[k]) for k, f in fams.items()}
 
 
+# C-ABI family of each kernel of a --families-only run (k_batch_reduce belongs to whichever
+# backward family launched it: the preceding kernel decides).
+_FAMILY_KERNELS = {
+    "fftconv_fwd": ("k_wrfft2", "k_wconv_fwd", "k_lrfft2", "k_linv_conv"),
+    "fftconv_bwd": ("k_wbwd_part", "k_psum", "k_wbwd_dx_fin", "k_wbwd_dg_red", "k_wbwd_dg_sum",
+                    "k_lred", "k_linv_dx"),
+    "epilogue_fwd": ("k_epi_fwd", "k_group_sum", "k_tile_stats", "k_tile_fwd"),
+    "epilogue_bwd": ("k_epi_bwd", "k_tile_bwd1", "k_tile_bwd2"),
+    "port_fwd": ("k_port_fwd", "k_port_combine", "k_port_fwd_tiled"),
+    "port_bwd": ("k_port_bwd",),
+}
+
+
+def traffic_summary(fetch_dir, write_dir, reps, out_path):
+    """HBM bytes per launch of each kernel family from two rocprofv3 counter passes (FETCH_SIZE,
+    WRITE_SIZE, KiB per dispatch) over `bench.py --families-only --kernel-reps reps`, scaled by
+    what the counters read for the run's 256 MiB device copies.  Writes out_path (JSON)."""
+    import csv
+
+    def load(d, counter):
+        rows = list(csv.DictReader(open(os.path.join(d, "run_counter_collection.csv"))))
+        per = {}
+        for r in rows:
+            if r["Counter_Name"] != counter:
+                continue
+            key = int(r["Dispatch_Id"])
+            name = r["Kernel_Name"].replace("(anonymous namespace)::", "").replace("void ", "")
+            per[key] = (name, per.get(key, ("", 0.0))[1] + float(r["Counter_Value"]))
+        return [per[k] for k in sorted(per)]
+
+    res = {}
+    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        seq = load(d, counter)
+        copies = [v for n, v in seq if "copyBuffer" in n and v > 1e5]
+        scale = (64 << 20) * 4 / (float(np.median(copies)) * 1024.0)
+        fam_kib, last = {}, None
+        start = max(i for i, (n, _) in enumerate(seq) if "copyBuffer" in n) + 1
+        for name, kib in seq[start:]:
+            fam = next((f for f, ks in _FAMILY_KERNELS.items()
+                        if any(name.startswith(k) for k in ks)), None)
+            if name.startswith("k_batch_reduce"):
+                fam = last
+            if fam is None:
+                continue
+            last = fam
+            fam_kib[fam] = fam_kib.get(fam, 0.0) + kib
+        res[counter] = {f: v * 1024.0 * scale / (reps + 1) for f, v in fam_kib.items()}
+        res[counter + "_scale"] = scale
+    ab = algorithmic_bytes(128, 16, 2000, 64 * 33, P=16)
+    out = {"_calibration": {"copy_bytes": (64 << 20) * 4, "fetch_scale": round(res["FETCH_SIZE_scale"], 4),
+                            "write_scale": round(res["WRITE_SIZE_scale"], 4),
+                            "calls_per_family": reps + 1}}
+    for f in _FAMILY_KERNELS:
+        fb, wb = res["FETCH_SIZE"].get(f, 0.0), res["WRITE_SIZE"].get(f, 0.0)
+        out[f] = {"fetch_bytes": int(fb), "write_bytes": int(wb), "traffic_bytes": int(fb + wb),
+                  "algorithmic_bytes": ab[f],
+                  "traffic_over_algorithmic": round((fb + wb) / ab[f], 2)}
+    with open(out_path, "w") as fh:
+        json.dump(out, fh, indent=1)
+    return out
+
+
 def cpu_baseline(seed, B, budget_s):
     """Float32 NumPy + scipy.fft restatement (oracle/) of one config-0 train step on this
     host's cores: forward, MSE loss, reverse pass and AdamW.  Timed over a bounded sample."""
@@ -210,6 +272,9 @@ def main():
     ap.add_argument("--config", default=None,
                     help="time one BASELINE workload of neurocell.configs at full size "
                          "(config0..config4, config2_literal) instead of the headline line")
+    ap.add_argument("--traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"), default=None,
+                    help="summarise two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) of a "
+                         "--families-only run into profiles/traffic_config0.json and exit")
     ap.add_argument("--families-only", action="store_true",
                     help="profiling aid: one eager train step, a 256 MiB device copy (the "
                          "traffic-counter calibration), then --kernel-reps calls of each "
@@ -220,6 +285,12 @@ def main():
               "the data-parallel sharding over B is described in DESIGN.md", file=sys.stderr)
         sys.exit(2)
 
+    if args.traffic:
+        out = traffic_summary(args.traffic[0], args.traffic[1], args.kernel_reps,
+                              os.path.join(ROOT, "profiles", "traffic_config0.json"))
+        print(json.dumps({k: v.get("traffic_over_algorithmic") for k, v in out.items()
+                          if k != "_calibration"}))
+        return
     import torch
     if args.config:
         run_config(args.config, args, torch)
