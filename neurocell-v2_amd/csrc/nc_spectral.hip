@@ -23,6 +23,7 @@
 #include <cstdint>
 
 #include "nc_large.h"
+#include "nc_pair.h"
 #include "nc_wave.h"
 
 namespace {
@@ -340,6 +341,105 @@ __global__ __launch_bounds__(256) void k_wbwd_dg_sum(int nchunk, int M, int F,
 }
 
 // ----------------------------------------------------------------------------------------
+// Lane-pair kernels for 64-wide grids (nc_pair.h): one plane per wavefront
+// ----------------------------------------------------------------------------------------
+
+template <int FH, int FW>
+constexpr bool pair_grid() {
+    return FW == 64 && (FH == 32 || FH == 64);
+}
+
+// LDS of a lane-pair plane over `rows` rows: T ((rows + 2) x PITCH cpx), sharing its space with
+// the real-valued input or output staging, then the Nyquist staging (FH cpx).
+struct PLds {
+    size_t bytes;
+    int nq;  // cpx offset of the Nyquist staging
+    PLds(int rows, int pitch, int fw, int fh) {
+        const size_t t = (size_t)(rows + 2) * pitch * sizeof(cpx);
+        const size_t o = (size_t)(rows + 1) * (fw + 1) * sizeof(float);
+        const size_t main = (std::max(t, o) + 15) / 16 * 16;
+        nq = (int)(main / sizeof(cpx));
+        bytes = main + (size_t)fh * sizeof(cpx);
+    }
+};
+
+// Half-spectra of real (hin x win) planes (FLIP: read rotated by 180 degrees, the filter
+// spectra of kernels_greens.py:240-259); one wavefront per plane.
+template <int FH, int FW, bool FLIP>
+__global__ __launch_bounds__(64) void k_prfft2(int hin, int win, int vec,
+                                               const float* __restrict__ x,
+                                               cpx* __restrict__ out) {
+    using P = PGeo<FH, FW>;
+    HIP_DYNAMIC_SHARED(float, lds)
+    cpx* T = reinterpret_cast<cpx*>(lds);
+    const size_t n = (size_t)hin * win;
+    istage<FW, 1, FLIP>(x + blockIdx.x * n, n, 1, hin, win, vec != 0, lds);
+    __syncthreads();
+    prow_fwd<FH, FW>(lds, hin, T);
+    __syncthreads();
+    cpx v[P::HH];
+    pcol_fwd<FH, FW>(T, hin, v);
+    cpx* o = out + (size_t)blockIdx.x * P::F;
+    pstore_half<FH, FW>(v, [&](int kh, int kw, cpx val) { o[kh * P::SP + kw] = val; });
+}
+
+// Forward correlation, one wavefront per plane g = b*M + m: z_bm = irfft2(xhat_b * ghat_m)
+// read from row ph, column pw (kernels_pallas.py:1779-1791; kernels_greens.py:316-343).
+template <int FH, int FW>
+__global__ __launch_bounds__(64) void k_pconv_fwd(int M, int hout, int wout, int ph, int pw,
+                                                  int nq_off, const cpx* __restrict__ xhat,
+                                                  const cpx* __restrict__ ghat,
+                                                  float* __restrict__ z) {
+    using P = PGeo<FH, FW>;
+    HIP_DYNAMIC_SHARED(float, lds)
+    cpx* T = reinterpret_cast<cpx*>(lds);
+    cpx* NQ = T + nq_off;
+    const int lane = threadIdx.x, kc = lane >> 1, t = lane & 1;
+    const int g = blockIdx.x, b = g / M, m = g - b * M;
+    const cpx* X = xhat + (size_t)b * P::F;
+    const cpx* G = ghat + (size_t)m * P::F;
+    if (lane < FH) NQ[lane] = cmul(X[lane * P::SP + FW / 2], G[lane * P::SP + FW / 2]);
+    cpx v[P::HH];
+#pragma unroll
+    for (int j = 0; j < P::HH; ++j) {
+        const int e = (2 * j + t) * P::SP + kc;
+        v[j] = cmul(X[e], G[e]);
+    }
+    __syncthreads();
+    if (kc == 0) {
+#pragma unroll
+        for (int j = 0; j < P::HH; ++j) v[j] = cadd(v[j], cmul_i(NQ[2 * j + t]));
+    }
+    pcol_inv<FH, FW>(v, ph, hout, T);
+    __syncthreads();
+    prow_inv<FH, FW>(T, pw, hout, 1.0f / (float)(FH * FW), lds);
+    __syncthreads();
+    ostage_copy<FW>(lds, 1, hout, wout, z + (size_t)g * hout * wout);
+}
+
+// dx, last stage: the inverse of sample b's summed packed spectrum with the unshifted roll
+// (kernels_pallas.py:1798-1812); one wavefront per sample.
+template <int FH, int FW>
+__global__ __launch_bounds__(64) void k_pdx_fin(int hin, int win, int ph, int pw,
+                                                const cpx* __restrict__ sum,
+                                                float* __restrict__ dx) {
+    using P = PGeo<FH, FW>;
+    HIP_DYNAMIC_SHARED(float, lds)
+    cpx* T = reinterpret_cast<cpx*>(lds);
+    const int lane = threadIdx.x, kc = lane >> 1, t = lane & 1;
+    const int b = blockIdx.x;
+    const cpx* src = sum + (size_t)b * P::PF + kc;
+    cpx v[P::HH];
+#pragma unroll
+    for (int j = 0; j < P::HH; ++j) v[j] = src[(2 * j + t) * P::NC];
+    pcol_inv<FH, FW>(v, (FH - ph) & (FH - 1), hin, T);
+    __syncthreads();
+    prow_inv<FH, FW>(T, (FW - pw) & (FW - 1), hin, 1.0f / (float)(FH * FW), lds);
+    __syncthreads();
+    ostage_copy<FW>(lds, 1, hin, win, dx + (size_t)b * hin * win);
+}
+
+// ----------------------------------------------------------------------------------------
 // Launch plumbing
 // ----------------------------------------------------------------------------------------
 
@@ -410,6 +510,21 @@ size_t bwd_ws(int B, int M) {
 template <int FH, int FW>
 int launch_rfft2(hipStream_t st, int nplanes, int hin, int win, bool flip, const float* x,
                  cpx* out) {
+    if constexpr (pair_grid<FH, FW>()) {
+        const PLds l(hin, PGeo<FH, FW>::PITCH, FW, FH);
+        const int vec = vec_ok(x, (size_t)hin * win);
+        if (flip) {
+            lds_limit(k_prfft2<FH, FW, true>, l.bytes);
+            hipLaunchKernelGGL((k_prfft2<FH, FW, true>), dim3(nplanes), dim3(64), l.bytes, st, hin,
+                               win, vec, x, out);
+        } else {
+            lds_limit(k_prfft2<FH, FW, false>, l.bytes);
+            hipLaunchKernelGGL((k_prfft2<FH, FW, false>), dim3(nplanes), dim3(64), l.bytes, st,
+                               hin, win, vec, x, out);
+        }
+        NC_CHECK_LAUNCH();
+        return NC_OK;
+    }
     using W = WGeo<FH, FW>;
     WLds<FH, FW> l(hin, win);
     dim3 grid((nplanes + W::PPW - 1) / W::PPW);
@@ -432,6 +547,15 @@ int launch_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wou
     using W = WGeo<FH, FW>;
     int rc = launch_rfft2<FH, FW>(st, B, hin, win, false, x, reinterpret_cast<cpx*>(xhat));
     if (rc != NC_OK) return rc;
+    if constexpr (pair_grid<FH, FW>()) {
+        const PLds l(hout, PGeo<FH, FW>::PITCH, FW, FH);
+        lds_limit(k_pconv_fwd<FH, FW>, l.bytes);
+        hipLaunchKernelGGL((k_pconv_fwd<FH, FW>), dim3(B * M), dim3(64), l.bytes, st, M, hout,
+                           wout, ph, pw, l.nq, reinterpret_cast<const cpx*>(xhat),
+                           reinterpret_cast<const cpx*>(ghat), z);
+        NC_CHECK_LAUNCH();
+        return NC_OK;
+    }
     WLds<FH, FW> l(hout, wout);
     lds_limit(k_wconv_fwd<FH, FW>, l.bytes);
     const int nplanes = B * M;
@@ -462,11 +586,18 @@ int launch_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wou
         hipLaunchKernelGGL(k_psum, dim3((W::PF + 255) / 256, B), dim3(256), 0, st, mg, W::PF,
                            (size_t)mg * W::PF, (size_t)W::PF, dxpart, dxsum);
         NC_CHECK_LAUNCH();
-        const WLds<FH, FW> lf(hin, win);
-        lds_limit(k_wbwd_dx_fin<FH, FW>, lf.bytes);
-        hipLaunchKernelGGL((k_wbwd_dx_fin<FH, FW>), dim3((B + W::PPW - 1) / W::PPW), dim3(64),
-                           lf.bytes, st, B, hin, win, ph, pw, lf.off, vec_ok(dx, (size_t)hin * win),
-                           dxsum, dx);
+        if constexpr (pair_grid<FH, FW>()) {
+            const PLds lf(hin, PGeo<FH, FW>::PITCH, FW, FH);
+            lds_limit(k_pdx_fin<FH, FW>, lf.bytes);
+            hipLaunchKernelGGL((k_pdx_fin<FH, FW>), dim3(B), dim3(64), lf.bytes, st, hin, win, ph,
+                               pw, dxsum, dx);
+        } else {
+            const WLds<FH, FW> lf(hin, win);
+            lds_limit(k_wbwd_dx_fin<FH, FW>, lf.bytes);
+            hipLaunchKernelGGL((k_wbwd_dx_fin<FH, FW>), dim3((B + W::PPW - 1) / W::PPW),
+                               dim3(64), lf.bytes, st, B, hin, win, ph, pw, lf.off,
+                               vec_ok(dx, (size_t)hin * win), dxsum, dx);
+        }
         NC_CHECK_LAUNCH();
     }
     constexpr int nthr = W::F;

@@ -50,6 +50,17 @@ inline float __shfl_xor(float v, int off, int) {
     __syncthreads();
     return r;
 }
+// DPP lane permutation; only quad_perm [1,0,3,2] (0xB1, swap within lane pairs) is used.
+inline int emu_dpp(int v, int ctrl) {
+    static int buf[1024];
+    const int t = threadIdx.x;
+    buf[t] = v;
+    __syncthreads();
+    const int r = ctrl == 0xB1 ? buf[t ^ 1] : v;
+    __syncthreads();
+    return r;
+}
+#define __builtin_amdgcn_update_dpp(old, src, ctrl, rm, bm, bc) emu_dpp((src), (ctrl))
 typedef int hipError_t;
 typedef void* hipStream_t;
 #define hipSuccess 0

@@ -24,7 +24,9 @@ def _assert_small(res, tol=TOL):
 @pytest.mark.parametrize("FH,FW,hin,win,kh,kw", [
     (16, 16, 10, 12, 5, 3), (32, 64, 20, 50, 9, 13),
     (16, 64, 9, 40, 7, 13),     # FH < FW/2: the Nyquist staging spans fewer rows than lanes
-    (64, 16, 50, 12, 13, 5)])   # several row passes per wavefront (no LDS sharing)
+    (64, 16, 50, 12, 13, 5),    # several row passes per wavefront (no LDS sharing)
+    (64, 64, 41, 50, 23, 13),   # lane-pair transforms, odd row count (an unpaired row)
+    (64, 64, 24, 32, 23, 13)])
 def test_fftconv(be, FH, FW, hin, win, kh, kw):
     _assert_small(case_fftconv(be, B=2, M=3, hin=hin, win=win, kh=kh, kw=kw, FH=FH, FW=FW))
 
