@@ -14,8 +14,10 @@
 //                Hermitian split of the packed pair needs each bin's mirror, which sits in the
 //                partner lane at slot N/2 - k: one DPP swap per bin.
 //
-// LDS: T holds the transposed half-spectrum rows (pitch FW/2 + 1 cpx) with a trash row and a
-// zero row as in nc_wave.h; stores are never predicated per element.
+// LDS: T holds the transposed half-spectrum rows (pitch FW/2 + 1 cpx).  The forward keeps the
+// live rows plus a trash row and a zero row (as in nc_wave.h); the inverse keeps all FH rows so
+// its stores have constant offsets, and the row pass applies the window's row offset.  Stores
+// are never predicated per element.
 #pragma once
 
 #include "nc_wave.h"
@@ -125,29 +127,25 @@ NC_DEV void pcol_fwd(const cpx* T, int rows, cpx* v) {
     fft_pair<FH, false>(v, t);
 }
 
-// Inverse column pass: v holds lane pair kc's packed spectrum column at rows 2j + t; output
-// rows i = (r - row0) mod FH < rows land in T (the others in the trash row `rows`).
+// Inverse column pass: v holds lane pair kc's packed spectrum column at rows 2j + t; every
+// output row r lands in T row r (T: FH x PITCH cpx), so each store has a constant offset; the
+// row pass applies the window's row offset.
 template <int FH, int FW>
-NC_DEV void pcol_inv(cpx* v, int row0, int rows, cpx* T) {
+NC_DEV void pcol_inv(cpx* v, cpx* T) {
     using P = PGeo<FH, FW>;
     const int lane = threadIdx.x & 63, kc = lane >> 1, t = lane & 1;
     fft_pair<FH, true>(v, t);
-    cpx* tc = T + kc;
-    const int base = t * P::HH;
+    cpx* tc = T + t * P::HH * P::PITCH + kc;
 #pragma unroll
-    for (int k = 0; k < P::HH; ++k) {
-        int i = (base + k - row0) & (FH - 1);
-        i = i < rows ? i : rows;
-        tc[i * P::PITCH] = v[k];
-    }
+    for (int k = 0; k < P::HH; ++k) tc[k * P::PITCH] = v[k];
 }
 
-// Inverse row pass: output rows [0, rows) of T (packed half-spectrum rows), times scale, into
-// the staging O (row i at O[i * (FW + 1)], every one of the FW columns stored at
-// (c - col0) mod FW; row `rows` is the trash row).  All lanes must call it; a barrier separates
-// the reads of T from the stores, so O may share LDS with T.
+// Inverse row pass: output rows i < rows, taken from T row (i + row0) mod FH (packed
+// half-spectrum rows), times scale, into the staging O (row i at O[i * (FW + 1)], every one of
+// the FW columns stored at (c - col0) mod FW; row `rows` is the trash row).  All lanes must call
+// it; a barrier separates the reads of T from the stores, so O may share LDS with T.
 template <int FH, int FW>
-NC_DEV void prow_inv(const cpx* T, int col0, int rows, float scale, float* O) {
+NC_DEV void prow_inv(const cpx* T, int row0, int col0, int rows, float scale, float* O) {
     using P = PGeo<FH, FW>;
     const int lane = threadIdx.x & 63, q0 = lane >> 1, t = lane & 1;
     const int NR = (rows + 1) >> 1;
@@ -155,8 +153,8 @@ NC_DEV void prow_inv(const cpx* T, int col0, int rows, float scale, float* O) {
     const int q = on ? q0 : 0;
     const int ib = q + NR;
     const bool hb = on && ib < rows;
-    const cpx* ta = T + q * P::PITCH;
-    const cpx* tb = T + (hb ? ib : q) * P::PITCH;
+    const cpx* ta = T + ((q + row0) & (FH - 1)) * P::PITCH;
+    const cpx* tb = T + (((hb ? ib : q) + row0) & (FH - 1)) * P::PITCH;
     const float bs = hb ? 1.f : 0.f;
     cpx v[P::HW];
 #pragma unroll
@@ -167,15 +165,15 @@ NC_DEV void prow_inv(const cpx* T, int col0, int rows, float scale, float* O) {
             a = t ? a1 : cmk(a0.x, 0.f);
             b = t ? b1 : cmk(b0.x, 0.f);
         } else if (j < P::HW / 2) {
-            a = ta[2 * j + t];
-            b = tb[2 * j + t];
+            a = (ta + t)[2 * j];
+            b = (tb + t)[2 * j];
         } else if (j == P::HW / 2) {  // column FW/2 + t: the packed Nyquist or conj(column FW/2 - 1)
             const cpx a0 = ta[0], b0 = tb[0], a1 = ta[P::HW - 1], b1 = tb[P::HW - 1];
             a = t ? cconj(a1) : cmk(a0.y, 0.f);
             b = t ? cconj(b1) : cmk(b0.y, 0.f);
         } else {
-            a = cconj(ta[FW - 2 * j - t]);
-            b = cconj(tb[FW - 2 * j - t]);
+            a = cconj((ta - t)[FW - 2 * j]);
+            b = cconj((tb - t)[FW - 2 * j]);
         }
         v[j] = cadd(a, cmul_i(cscale(b, bs)));
     }
@@ -190,6 +188,29 @@ NC_DEV void prow_inv(const cpx* T, int col0, int rows, float scale, float* O) {
         const int jj = (k + sh) & (FW - 1);
         oa[jj] = v[k].x * scale;
         ob[jj] = v[k].y * scale;
+    }
+}
+
+// Copies the staged output rows (rows x cols, row pitch FW + 1) to dst, contiguous: element
+// e = i * cols + j per lane, all 64 lanes busy (i = floor(e / cols) by a 20-bit reciprocal,
+// exact for e < 4096 and cols <= 64).
+template <int FW>
+NC_DEV void pstage_copy(const float* O, int rows, int cols, float* __restrict__ dst) {
+    const int lane = threadIdx.x & 63;
+    const int total = rows * cols;
+    const unsigned inv = ((1u << 20) + cols - 1) / cols;
+    constexpr int U = 8;
+    for (int e0 = lane; e0 < total; e0 += 64 * U) {
+        float v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int e = min(e0 + 64 * u, total - 1);
+            const int i = (int)(((unsigned)e * inv) >> 20);
+            v[u] = O[i * (FW + 1) + (e - i * cols)];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (e0 + 64 * u < total) dst[e0 + 64 * u] = v[u];
     }
 }
 

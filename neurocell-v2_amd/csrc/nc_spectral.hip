@@ -349,13 +349,14 @@ constexpr bool pair_grid() {
     return FW == 64 && (FH == 32 || FH == 64);
 }
 
-// LDS of a lane-pair plane over `rows` rows: T ((rows + 2) x PITCH cpx), sharing its space with
-// the real-valued input or output staging, then the Nyquist staging (FH cpx).
+// LDS of a lane-pair plane: T (forward: `rows` + 2 rows; inverse: all fh rows) of pitch cpx,
+// sharing its space with the real-valued input or output staging, then the Nyquist staging
+// (fh cpx).
 struct PLds {
     size_t bytes;
     int nq;  // cpx offset of the Nyquist staging
-    PLds(int rows, int pitch, int fw, int fh) {
-        const size_t t = (size_t)(rows + 2) * pitch * sizeof(cpx);
+    PLds(int rows, int pitch, int fw, int fh, bool inverse) {
+        const size_t t = (size_t)(inverse ? fh : rows + 2) * pitch * sizeof(cpx);
         const size_t o = (size_t)(rows + 1) * (fw + 1) * sizeof(float);
         const size_t main = (std::max(t, o) + 15) / 16 * 16;
         nq = (int)(main / sizeof(cpx));
@@ -410,11 +411,11 @@ __global__ __launch_bounds__(64) void k_pconv_fwd(int M, int hout, int wout, int
 #pragma unroll
         for (int j = 0; j < P::HH; ++j) v[j] = cadd(v[j], cmul_i(NQ[2 * j + t]));
     }
-    pcol_inv<FH, FW>(v, ph, hout, T);
+    pcol_inv<FH, FW>(v, T);
     __syncthreads();
-    prow_inv<FH, FW>(T, pw, hout, 1.0f / (float)(FH * FW), lds);
+    prow_inv<FH, FW>(T, ph, pw, hout, 1.0f / (float)(FH * FW), lds);
     __syncthreads();
-    ostage_copy<FW>(lds, 1, hout, wout, z + (size_t)g * hout * wout);
+    pstage_copy<FW>(lds, hout, wout, z + (size_t)g * hout * wout);
 }
 
 // dx, last stage: the inverse of sample b's summed packed spectrum with the unshifted roll
@@ -432,11 +433,12 @@ __global__ __launch_bounds__(64) void k_pdx_fin(int hin, int win, int ph, int pw
     cpx v[P::HH];
 #pragma unroll
     for (int j = 0; j < P::HH; ++j) v[j] = src[(2 * j + t) * P::NC];
-    pcol_inv<FH, FW>(v, (FH - ph) & (FH - 1), hin, T);
+    pcol_inv<FH, FW>(v, T);
     __syncthreads();
-    prow_inv<FH, FW>(T, (FW - pw) & (FW - 1), hin, 1.0f / (float)(FH * FW), lds);
+    prow_inv<FH, FW>(T, (FH - ph) & (FH - 1), (FW - pw) & (FW - 1), hin, 1.0f / (float)(FH * FW),
+                     lds);
     __syncthreads();
-    ostage_copy<FW>(lds, 1, hin, win, dx + (size_t)b * hin * win);
+    pstage_copy<FW>(lds, hin, win, dx + (size_t)b * hin * win);
 }
 
 // ----------------------------------------------------------------------------------------
@@ -511,7 +513,7 @@ template <int FH, int FW>
 int launch_rfft2(hipStream_t st, int nplanes, int hin, int win, bool flip, const float* x,
                  cpx* out) {
     if constexpr (pair_grid<FH, FW>()) {
-        const PLds l(hin, PGeo<FH, FW>::PITCH, FW, FH);
+        const PLds l(hin, PGeo<FH, FW>::PITCH, FW, FH, false);
         const int vec = vec_ok(x, (size_t)hin * win);
         if (flip) {
             lds_limit(k_prfft2<FH, FW, true>, l.bytes);
@@ -548,7 +550,7 @@ int launch_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wou
     int rc = launch_rfft2<FH, FW>(st, B, hin, win, false, x, reinterpret_cast<cpx*>(xhat));
     if (rc != NC_OK) return rc;
     if constexpr (pair_grid<FH, FW>()) {
-        const PLds l(hout, PGeo<FH, FW>::PITCH, FW, FH);
+        const PLds l(hout, PGeo<FH, FW>::PITCH, FW, FH, true);
         lds_limit(k_pconv_fwd<FH, FW>, l.bytes);
         hipLaunchKernelGGL((k_pconv_fwd<FH, FW>), dim3(B * M), dim3(64), l.bytes, st, M, hout,
                            wout, ph, pw, l.nq, reinterpret_cast<const cpx*>(xhat),
@@ -587,7 +589,7 @@ int launch_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wou
                            (size_t)mg * W::PF, (size_t)W::PF, dxpart, dxsum);
         NC_CHECK_LAUNCH();
         if constexpr (pair_grid<FH, FW>()) {
-            const PLds lf(hin, PGeo<FH, FW>::PITCH, FW, FH);
+            const PLds lf(hin, PGeo<FH, FW>::PITCH, FW, FH, true);
             lds_limit(k_pdx_fin<FH, FW>, lf.bytes);
             hipLaunchKernelGGL((k_pdx_fin<FH, FW>), dim3(B), dim3(64), lf.bytes, st, hin, win, ph,
                                pw, dxsum, dx);
