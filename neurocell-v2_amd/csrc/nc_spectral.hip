@@ -364,24 +364,99 @@ struct PLds {
     }
 };
 
+// Half-spectrum of one real (hin x win) plane src into o (FLIP: read rotated by 180 degrees);
+// the calling wavefront owns the plane.
+template <int FH, int FW, bool FLIP>
+NC_DEV void prfft2_plane(const float* __restrict__ src, int hin, int win, int vec, float* lds,
+                         cpx* __restrict__ o) {
+    using P = PGeo<FH, FW>;
+    cpx* T = reinterpret_cast<cpx*>(lds);
+    istage<FW, 1, FLIP>(src, (size_t)hin * win, 1, hin, win, vec != 0, lds);
+    __syncthreads();
+    prow_fwd<FH, FW>(lds, hin, T);
+    __syncthreads();
+    cpx v[P::HH];
+    pcol_fwd<FH, FW>(T, hin, v);
+    pstore_half<FH, FW>(v, [&](int kh, int kw, cpx val) { o[kh * P::SP + kw] = val; });
+}
+
 // Half-spectra of real (hin x win) planes (FLIP: read rotated by 180 degrees, the filter
 // spectra of kernels_greens.py:240-259); one wavefront per plane.
 template <int FH, int FW, bool FLIP>
 __global__ __launch_bounds__(64) void k_prfft2(int hin, int win, int vec,
                                                const float* __restrict__ x,
                                                cpx* __restrict__ out) {
+    HIP_DYNAMIC_SHARED(float, lds)
+    prfft2_plane<FH, FW, FLIP>(x + (size_t)blockIdx.x * hin * win, hin, win, vec, lds,
+                               out + (size_t)blockIdx.x * PGeo<FH, FW>::F);
+}
+
+// Backward, first stage (kernels_pallas.py:1794-1821): the half-spectrum of every cotangent
+// plane gz_bm (g = b*M + m) into spec (M, B, pitch), one wavefront per plane.
+template <int FH, int FW>
+__global__ __launch_bounds__(64) void k_pspec(int B, int M, int hout, int wout, int vec,
+                                              const float* __restrict__ gz,
+                                              cpx* __restrict__ spec) {
+    HIP_DYNAMIC_SHARED(float, lds)
+    const int g = blockIdx.x, b = g / M, m = g - b * M;
+    prfft2_plane<FH, FW, false>(gz + (size_t)g * hout * wout, hout, wout, vec, lds,
+                                spec + ((size_t)m * B + b) * spec_pitch<FH, FW>());
+}
+
+// Backward, dx reduction (kernels_pallas.py:1794-1812): dxs[b][e] = sum over m, in increasing
+// order, of spec[m][b][e] * conj(ghat_m[e]); one thread per (bin, sample), the loads of 16
+// directions in flight together.
+template <int FH, int FW>
+__global__ __launch_bounds__(256) void k_pdx_red(int B, int M, const cpx* __restrict__ spec,
+                                                 const cpx* __restrict__ ghat,
+                                                 cpx* __restrict__ dxs) {
+    using P = PGeo<FH, FW>;
+    constexpr int MC = 16;
+    constexpr size_t SPP = spec_pitch<FH, FW>();
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= P::F) return;
+    const int b = blockIdx.y;
+    cpx d = cmk(0.f, 0.f);
+    for (int m0 = 0; m0 < M; m0 += MC) {
+        cpx sv[MC], gv[MC];
+#pragma unroll
+        for (int q = 0; q < MC; ++q) {
+            const int m = min(m0 + q, M - 1);
+            sv[q] = spec[((size_t)m * B + b) * SPP + e];
+            gv[q] = ghat[(size_t)m * P::F + e];
+        }
+#pragma unroll
+        for (int q = 0; q < MC; ++q)
+            if (m0 + q < M) d = cadd(d, cmulc(sv[q], gv[q]));
+    }
+    dxs[(size_t)b * P::F + e] = d;
+}
+
+// dx, last stage: the inverse of sample b's dx half-spectrum with the unshifted roll
+// (kernels_pallas.py:1798-1812); one wavefront per sample.
+template <int FH, int FW>
+__global__ __launch_bounds__(64) void k_pdx_half(int hin, int win, int ph, int pw,
+                                                 const cpx* __restrict__ dxs,
+                                                 float* __restrict__ dx) {
     using P = PGeo<FH, FW>;
     HIP_DYNAMIC_SHARED(float, lds)
     cpx* T = reinterpret_cast<cpx*>(lds);
-    const size_t n = (size_t)hin * win;
-    istage<FW, 1, FLIP>(x + blockIdx.x * n, n, 1, hin, win, vec != 0, lds);
-    __syncthreads();
-    prow_fwd<FH, FW>(lds, hin, T);
-    __syncthreads();
+    const int lane = threadIdx.x, kc = lane >> 1, t = lane & 1;
+    const int b = blockIdx.x;
+    const cpx* src = dxs + (size_t)b * P::F;
     cpx v[P::HH];
-    pcol_fwd<FH, FW>(T, hin, v);
-    cpx* o = out + (size_t)blockIdx.x * P::F;
-    pstore_half<FH, FW>(v, [&](int kh, int kw, cpx val) { o[kh * P::SP + kw] = val; });
+#pragma unroll
+    for (int j = 0; j < P::HH; ++j) v[j] = src[(2 * j + t) * P::SP + kc];
+    if (kc == 0) {  // packed column 0: DC + i*Nyquist
+#pragma unroll
+        for (int j = 0; j < P::HH; ++j) v[j] = cadd(v[j], cmul_i(src[(2 * j + t) * P::SP + FW / 2]));
+    }
+    pcol_inv<FH, FW>(v, T);
+    __syncthreads();
+    prow_inv<FH, FW>(T, (FH - ph) & (FH - 1), (FW - pw) & (FW - 1), hin, 1.0f / (float)(FH * FW),
+                     lds);
+    __syncthreads();
+    pstage_copy<FW>(lds, hin, win, dx + (size_t)b * hin * win);
 }
 
 // Forward correlation, one wavefront per plane g = b*M + m: z_bm = irfft2(xhat_b * ghat_m)
@@ -416,29 +491,6 @@ __global__ __launch_bounds__(64) void k_pconv_fwd(int M, int hout, int wout, int
     prow_inv<FH, FW>(T, ph, pw, hout, 1.0f / (float)(FH * FW), lds);
     __syncthreads();
     pstage_copy<FW>(lds, hout, wout, z + (size_t)g * hout * wout);
-}
-
-// dx, last stage: the inverse of sample b's summed packed spectrum with the unshifted roll
-// (kernels_pallas.py:1798-1812); one wavefront per sample.
-template <int FH, int FW>
-__global__ __launch_bounds__(64) void k_pdx_fin(int hin, int win, int ph, int pw,
-                                                const cpx* __restrict__ sum,
-                                                float* __restrict__ dx) {
-    using P = PGeo<FH, FW>;
-    HIP_DYNAMIC_SHARED(float, lds)
-    cpx* T = reinterpret_cast<cpx*>(lds);
-    const int lane = threadIdx.x, kc = lane >> 1, t = lane & 1;
-    const int b = blockIdx.x;
-    const cpx* src = sum + (size_t)b * P::PF + kc;
-    cpx v[P::HH];
-#pragma unroll
-    for (int j = 0; j < P::HH; ++j) v[j] = src[(2 * j + t) * P::NC];
-    pcol_inv<FH, FW>(v, T);
-    __syncthreads();
-    prow_inv<FH, FW>(T, (FH - ph) & (FH - 1), (FW - pw) & (FW - 1), hin, 1.0f / (float)(FH * FW),
-                     lds);
-    __syncthreads();
-    pstage_copy<FW>(lds, hin, win, dx + (size_t)b * hin * win);
 }
 
 // ----------------------------------------------------------------------------------------
@@ -502,6 +554,13 @@ int dg_chunks(int B, int M) {
 // (M, B, pitch) and the dG chunk partials (chunks, M, F).
 template <int FH, int FW>
 size_t bwd_ws(int B, int M) {
+    if constexpr (pair_grid<FH, FW>()) {
+        // cotangent half-spectra (M, B, pitch), dx spectra (B, F), dG chunk partials
+        using P = PGeo<FH, FW>;
+        const size_t nc = dg_chunks<FH, FW>(B, M);
+        return ((size_t)M * B * spec_pitch<FH, FW>() + (size_t)B * P::F + nc * M * P::F) *
+               sizeof(cpx);
+    }
     using W = WGeo<FH, FW>;
     const size_t mg = bwd_groups<FH, FW>(M);
     const size_t nc = dg_chunks<FH, FW>(B, M);
@@ -570,9 +629,50 @@ int launch_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wou
 }
 
 template <int FH, int FW>
+int launch_pbwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph,
+                int pw, const float* gz, const float* xhat, const float* ghat, int need_dx,
+                float* dx, float* dghat, int accumulate, int conj_out, void* ws) {
+    using P = PGeo<FH, FW>;
+    cpx* spec = reinterpret_cast<cpx*>(ws);
+    cpx* dxs = spec + (size_t)M * B * spec_pitch<FH, FW>();
+    cpx* dgpart = dxs + (size_t)B * P::F;
+    const PLds ls(hout, P::PITCH, FW, FH, false);
+    lds_limit(k_pspec<FH, FW>, ls.bytes);
+    hipLaunchKernelGGL((k_pspec<FH, FW>), dim3(B * M), dim3(64), ls.bytes, st, B, M, hout, wout,
+                       vec_ok(gz, (size_t)hout * wout), gz, spec);
+    NC_CHECK_LAUNCH();
+    if (need_dx) {
+        hipLaunchKernelGGL((k_pdx_red<FH, FW>), dim3((P::F + 255) / 256, B), dim3(256), 0, st, B,
+                           M, spec, reinterpret_cast<const cpx*>(ghat), dxs);
+        NC_CHECK_LAUNCH();
+        const PLds lf(hin, P::PITCH, FW, FH, true);
+        lds_limit(k_pdx_half<FH, FW>, lf.bytes);
+        hipLaunchKernelGGL((k_pdx_half<FH, FW>), dim3(B), dim3(64), lf.bytes, st, hin, win, ph,
+                           pw, dxs, dx);
+        NC_CHECK_LAUNCH();
+    }
+    const int nchunk = dg_chunks<FH, FW>(B, M);
+    const int bper = (B + nchunk - 1) / nchunk;
+    const int nb = (B + bper - 1) / bper;
+    hipLaunchKernelGGL((k_wbwd_dg_red<FH, FW>), dim3((P::F + 255) / 256, M, nb), dim3(256), 0,
+                       st, B, M, bper, spec, reinterpret_cast<const cpx*>(xhat), dgpart,
+                       reinterpret_cast<cpx*>(dghat), accumulate, conj_out);
+    NC_CHECK_LAUNCH();
+    if (nb > 1) {
+        hipLaunchKernelGGL(k_wbwd_dg_sum, dim3((P::F + 255) / 256, M), dim3(256), 0, st, nb, M,
+                           P::F, dgpart, reinterpret_cast<cpx*>(dghat), accumulate, conj_out);
+        NC_CHECK_LAUNCH();
+    }
+    return NC_OK;
+}
+
+template <int FH, int FW>
 int launch_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph,
                int pw, const float* gz, const float* xhat, const float* ghat, int need_dx,
                float* dx, float* dghat, int accumulate, int conj_out, void* ws) {
+    if constexpr (pair_grid<FH, FW>())
+        return launch_pbwd<FH, FW>(st, B, M, hin, win, hout, wout, ph, pw, gz, xhat, ghat, need_dx,
+                                   dx, dghat, accumulate, conj_out, ws);
     using W = WGeo<FH, FW>;
     const int mg = bwd_groups<FH, FW>(M);
     cpx* dxpart = reinterpret_cast<cpx*>(ws);
@@ -588,18 +688,11 @@ int launch_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wou
         hipLaunchKernelGGL(k_psum, dim3((W::PF + 255) / 256, B), dim3(256), 0, st, mg, W::PF,
                            (size_t)mg * W::PF, (size_t)W::PF, dxpart, dxsum);
         NC_CHECK_LAUNCH();
-        if constexpr (pair_grid<FH, FW>()) {
-            const PLds lf(hin, PGeo<FH, FW>::PITCH, FW, FH, true);
-            lds_limit(k_pdx_fin<FH, FW>, lf.bytes);
-            hipLaunchKernelGGL((k_pdx_fin<FH, FW>), dim3(B), dim3(64), lf.bytes, st, hin, win, ph,
-                               pw, dxsum, dx);
-        } else {
-            const WLds<FH, FW> lf(hin, win);
-            lds_limit(k_wbwd_dx_fin<FH, FW>, lf.bytes);
-            hipLaunchKernelGGL((k_wbwd_dx_fin<FH, FW>), dim3((B + W::PPW - 1) / W::PPW),
-                               dim3(64), lf.bytes, st, B, hin, win, ph, pw, lf.off,
-                               vec_ok(dx, (size_t)hin * win), dxsum, dx);
-        }
+        const WLds<FH, FW> lf(hin, win);
+        lds_limit(k_wbwd_dx_fin<FH, FW>, lf.bytes);
+        hipLaunchKernelGGL((k_wbwd_dx_fin<FH, FW>), dim3((B + W::PPW - 1) / W::PPW), dim3(64),
+                           lf.bytes, st, B, hin, win, ph, pw, lf.off,
+                           vec_ok(dx, (size_t)hin * win), dxsum, dx);
         NC_CHECK_LAUNCH();
     }
     constexpr int nthr = W::F;
