@@ -151,6 +151,34 @@ int nc_fftconv_bwd(void* stream, int B, int M, int hin, int win, int hout, int w
                    const float* ghat, int need_dx, float* dx, float* dghat, int accumulate,
                    int conj_dghat, void* ws, size_t ws_bytes);
 
+/*
+ * nc_fftconv_bwd that also forms gz_hat_sum (M, fft_h, fft_w/2+1) complex = sum_b rfft2(gz_b)
+ * at the origin (overwritten, or added to when sum_accumulate; NULL skips it): the spectra of
+ * the batch-summed cotangent, which is the border cotangent sum_b gz of the hoisted border
+ * conv (propagator.py:362-366, the gdb of nc_epilogue_bwd / nc_port_bwd) in the frequency
+ * domain.  It is summed in the same pass as dghat, so the cotangent planes are not read again.
+ * No counterpart in the reference (which differentiates the border conv through JAX).
+ */
+int nc_fftconv_bwd_ex(void* stream, int B, int M, int hin, int win, int hout, int wout,
+                      int pad_h, int pad_w, int fft_h, int fft_w, const float* gz,
+                      const float* xhat, const float* ghat, int need_dx, float* dx, float* dghat,
+                      int accumulate, int conj_dghat, float* gz_hat_sum, int sum_accumulate,
+                      void* ws, size_t ws_bytes);
+
+/*
+ * nc_fftconv_bwd at B = 1 with the cotangent given by its spectra gz_hat (M, fft_h,
+ * fft_w/2+1) complex (e.g. the gz_hat_sum of nc_fftconv_bwd_ex): the backward of the hoisted
+ * border conv (propagator.py:362-366) without its cotangent planes.
+ *   dx = irfft2(sum_m gz_hat_m * conj(ghat_m)) rolled by (pad_h, pad_w), cropped (hin, win);
+ *   dghat (+)= gz_hat * conj(xhat) when dghat is not NULL (xhat: the (fft_h, fft_w/2+1)
+ *   input spectrum; conj_dghat as in nc_fftconv_bwd).
+ * ws: at least fft_h*(fft_w/2+1)*8 bytes (nc_fftconv_bwd_workspace_size(1, ...) suffices).
+ */
+int nc_fftconv_bwd_hat(void* stream, int M, int hin, int win, int pad_h, int pad_w, int fft_h,
+                       int fft_w, const float* gz_hat, const float* xhat, const float* ghat,
+                       float* dx, float* dghat, int accumulate, int conj_dghat, void* ws,
+                       size_t ws_bytes);
+
 /* ---------------- piece 3: hidden-step epilogue and output-port epilogue --------------- */
 
 /*
@@ -175,8 +203,8 @@ int nc_epilogue_fwd(void* stream, int B, int M, int h, int w, int act, float neg
 
 /*
  * pallas_fused_roi_step_epilogue backward rule (kernels_pallas.py:869-1064): writes gz
- * (B,M,h,w), gdb = sum_b gz (M,h,w) when has_border (gdb may be NULL otherwise) and
- * gw/gs/gb (h,w).  gw/gs/gb are overwritten, or added to when accumulate_params; gdb is
+ * (B,M,h,w), gdb = sum_b gz (M,h,w) when has_border and gdb is not NULL (a caller that forms
+ * the border cotangent from the spectra, nc_fftconv_bwd_ex, passes NULL) and gw/gs/gb (h,w).  gw/gs/gb are overwritten, or added to when accumulate_params; gdb is
  * overwritten, or added to when accumulate_gdb (a d-step reverse pass sums both over steps).
  */
 int nc_epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg_slope,
@@ -205,7 +233,7 @@ int nc_port_fwd(void* stream, int B, int M, int h, int w, int has_border, int fi
 /*
  * Backward of nc_port_fwd (kernels_pallas.py:1350-1504, 1538-1551): dense
  * gz = -rstd*(c1 + zhat*c2) plus rstd*g scattered at the port cells in registers; gdb =
- * sum_b gz when has_border; gdb and g_port_params (3,P) overwritten, or added to when
+ * sum_b gz when has_border and gdb is not NULL; gdb and g_port_params (3,P) overwritten, or added to when
  * accumulate_params.  With port_params == NULL (standardisation only, kernels_pallas.py:
  * 1350-1504) g_out is the (B,M,P) cotangent of zo and g_port_params is not touched.
  */

@@ -1079,7 +1079,7 @@ int nc_epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg
                     int accumulate_params, int accumulate_gdb, void* ws, size_t ws_bytes) {
     if (B <= 0 || M <= 0 || M > kMaxM || h <= 0 || w <= 0 || !z || !w_eff || !s_eff ||
         !b_roi || !mean || !rstd || !gy || !gz || !gw || !gs || !gb ||
-        (has_border && (!delta || !gdb)) || act < 0 || act > 5)
+        (has_border && !delta) || act < 0 || act > 5)
         return NC_ERR_INVALID_ARGUMENT;
     if (ws_bytes < nc_epilogue_workspace_size(B, M, h, w) || !ws) return NC_ERR_WORKSPACE;
     hipStream_t st = nc_stream(stream);
@@ -1114,7 +1114,7 @@ int nc_epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg
     const RedJob jobs[4] = {{e.pg, gw, N, accumulate_params, rows},
                             {e.pg + RN, gs, N, accumulate_params, rows},
                             {e.pg + 2 * RN, gb, N, accumulate_params, rows},
-                            {has_border ? gz : nullptr, gdb, M * N, accumulate_gdb, B}};
+                            {has_border && gdb ? gz : nullptr, gdb, M * N, accumulate_gdb, B}};
     return launch_batch_reduce(st, jobs, 4);
 }
 
@@ -1175,7 +1175,7 @@ int nc_port_bwd(void* stream, int B, int M, int h, int w, int has_border, int fi
     int rc = port_check(B, M, h, w, n_port, port_idx, z, has_border, delta, final_act);
     if (rc != NC_OK) return rc;
     if (!zo || !mean || !rstd || !g_out || !gz || (port_params && !g_port_params) ||
-        (has_border && !gdb) || (port_params && final_act != NC_ACT_IDENTITY && !pre))
+        (port_params && final_act != NC_ACT_IDENTITY && !pre))
         return NC_ERR_INVALID_ARGUMENT;
     if (ws_bytes < nc_epilogue_workspace_size(B, M, h, w) || !ws) return NC_ERR_WORKSPACE;
     hipStream_t st = nc_stream(stream);
@@ -1196,7 +1196,7 @@ int nc_port_bwd(void* stream, int B, int M, int h, int w, int has_border, int fi
          accumulate_params, B},
         {pj ? ppart + 2 * (size_t)B * n_port : nullptr, g_port_params + 2 * n_port, n_port,
          accumulate_params, B},
-        {has_border ? gz : nullptr, gdb, M * N, accumulate_params, B}};
+        {has_border && gdb ? gz : nullptr, gdb, M * N, accumulate_params, B}};
     return launch_batch_reduce(st, jobs, 4);
 }
 

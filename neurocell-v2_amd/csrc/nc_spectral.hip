@@ -287,14 +287,17 @@ constexpr int kDgBatch = 16;  // samples whose loads a dG-reduction thread keeps
 // c = blockIdx.z, in increasing b, of rfft2(gz_bm) * conj(xhat_b), bin by bin, from the stored
 // half-spectra spec (M, B, pitch).  With one chunk the result goes to dghat directly
 // (conj_out: conjugate convention, accumulate: add); otherwise to part (chunks, M, F) for
-// k_wbwd_dg_sum.
+// k_wbwd_dg_sum.  With ssum the plain sums over b of rfft2(gz_bm) are formed alongside (the
+// spectra of sum_b gz_bm, by linearity), into ssum (M, F) or the partial rows
+// part[chunks + c] (added to ssum when sum_acc).
 template <int FH, int FW>
 __global__ __launch_bounds__(256) void k_wbwd_dg_red(int B, int M, int bper,
                                                      const cpx* __restrict__ spec,
                                                      const cpx* __restrict__ xhat,
                                                      cpx* __restrict__ part,
                                                      cpx* __restrict__ dghat, int accumulate,
-                                                     int conj_out) {
+                                                     int conj_out, cpx* __restrict__ ssum,
+                                                     int sum_acc) {
     using W = WGeo<FH, FW>;
     constexpr size_t SPP = spec_pitch<FH, FW>();
     const int m = blockIdx.y, c = blockIdx.z;
@@ -303,7 +306,7 @@ __global__ __launch_bounds__(256) void k_wbwd_dg_red(int B, int M, int bper,
     const int b0 = c * bper, b1 = min(B, b0 + bper);
     const cpx* S = spec + (size_t)m * B * SPP + e;
     const cpx* X = xhat + e;
-    cpx acc = cmk(0.f, 0.f);
+    cpx acc = cmk(0.f, 0.f), sacc = cmk(0.f, 0.f);
     for (int bb = b0; bb < b1; bb += kDgBatch) {
         // the batch's loads are issued together (clamped), then added in increasing b
         cpx u[kDgBatch], xv[kDgBatch];
@@ -314,30 +317,105 @@ __global__ __launch_bounds__(256) void k_wbwd_dg_red(int B, int M, int bper,
             xv[j] = X[(size_t)b * W::F];
         }
 #pragma unroll
-        for (int j = 0; j < kDgBatch; ++j)
-            if (bb + j < b1) acc = cadd(acc, cmulc(u[j], xv[j]));
+        for (int j = 0; j < kDgBatch; ++j) {
+            if (bb + j < b1) {
+                acc = cadd(acc, cmulc(u[j], xv[j]));
+                sacc = cadd(sacc, u[j]);
+            }
+        }
     }
     if (gridDim.z == 1) {
         if (conj_out) acc = cconj(acc);
         cpx* o = dghat + (size_t)m * W::F + e;
         *o = accumulate ? cadd(*o, acc) : acc;
+        if (ssum) {
+            cpx* so = ssum + (size_t)m * W::F + e;
+            *so = sum_acc ? cadd(*so, sacc) : sacc;
+        }
     } else {
         part[((size_t)c * M + m) * W::F + e] = acc;
+        if (ssum) part[((size_t)(gridDim.z + c) * M + m) * W::F + e] = sacc;
     }
 }
 
-// dG reduction, second stage: dghat[m] (+)= sum over the chunks in order (grid (F/256, M)).
+// dG reduction, second stage: dghat[m] (+)= sum over the chunks in order (grid (F/256, M, 1));
+// with a second grid layer (blockIdx.z == 1) also ssum[m] (+)= the chunks' plain sums.
 __global__ __launch_bounds__(256) void k_wbwd_dg_sum(int nchunk, int M, int F,
                                                      const cpx* __restrict__ part,
                                                      cpx* __restrict__ dghat, int accumulate,
-                                                     int conj_out) {
+                                                     int conj_out, cpx* __restrict__ ssum,
+                                                     int sum_acc) {
     const int m = blockIdx.y;
     const int e = blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= F) return;
-    cpx v = sum_strided(part + (size_t)m * F + e, nchunk, (size_t)M * F);
-    if (conj_out) v = cconj(v);
-    cpx* o = dghat + (size_t)m * F + e;
-    *o = accumulate ? cadd(*o, v) : v;
+    if (blockIdx.z == 0) {
+        cpx v = sum_strided(part + (size_t)m * F + e, nchunk, (size_t)M * F);
+        if (conj_out) v = cconj(v);
+        cpx* o = dghat + (size_t)m * F + e;
+        *o = accumulate ? cadd(*o, v) : v;
+    } else {
+        const cpx v = sum_strided(part + ((size_t)nchunk * M + m) * F + e, nchunk, (size_t)M * F);
+        cpx* o = ssum + (size_t)m * F + e;
+        *o = sum_acc ? cadd(*o, v) : v;
+    }
+}
+
+// Backward of a one-sample correlation from its cotangent half-spectra S (M, F), the
+// spectra of gz (kernels_pallas.py:1794-1821 at B = 1): dghat[m] (+)= S_m * conj(xhat)
+// (conjugated when conj_out; skipped without dghat) and the dx spectrum sum over m, in
+// increasing order, of S_m * conj(ghat_m), into dxs: unpacked (FH, FW/2 + 1) or, with packed,
+// the (FH, FW/2) layout whose column 0 holds DC + i*Nyquist.  Thread = packed bin (kh, kc);
+// kc == 0 also carries column FW/2.
+__global__ __launch_bounds__(256) void k_hat_red(int M, int FH, int FWh, int packed,
+                                                 const cpx* __restrict__ S,
+                                                 const cpx* __restrict__ xhat,
+                                                 const cpx* __restrict__ ghat,
+                                                 cpx* __restrict__ dxs, cpx* __restrict__ dghat,
+                                                 int accumulate, int conj_out) {
+    constexpr int MC = 8;
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= FH * FWh) return;
+    const int kh = p / FWh, kc = p - kh * FWh;
+    const int F = FH * (FWh + 1);
+    const int e0 = kh * (FWh + 1) + kc, e1 = kh * (FWh + 1) + FWh;
+    const bool two = kc == 0;
+    const cpx X0 = dghat ? xhat[e0] : cmk(0.f, 0.f);
+    const cpx X1 = dghat ? xhat[e1] : cmk(0.f, 0.f);
+    cpx d0 = cmk(0.f, 0.f), d1 = cmk(0.f, 0.f);
+    for (int m0 = 0; m0 < M; m0 += MC) {
+        cpx s0[MC], s1[MC], g0[MC], g1[MC];
+#pragma unroll
+        for (int q = 0; q < MC; ++q) {
+            const size_t o = (size_t)min(m0 + q, M - 1) * F;
+            s0[q] = S[o + e0];
+            s1[q] = S[o + e1];
+            g0[q] = ghat[o + e0];
+            g1[q] = ghat[o + e1];
+        }
+#pragma unroll
+        for (int q = 0; q < MC; ++q) {
+            if (m0 + q >= M) break;
+            d0 = cadd(d0, cmulc(s0[q], g0[q]));
+            d1 = cadd(d1, cmulc(s1[q], g1[q]));
+            if (dghat) {
+                const size_t o = (size_t)(m0 + q) * F;
+                cpx v = cmulc(s0[q], X0);
+                if (conj_out) v = cconj(v);
+                dghat[o + e0] = accumulate ? cadd(dghat[o + e0], v) : v;
+                if (two) {
+                    cpx w = cmulc(s1[q], X1);
+                    if (conj_out) w = cconj(w);
+                    dghat[o + e1] = accumulate ? cadd(dghat[o + e1], w) : w;
+                }
+            }
+        }
+    }
+    if (packed) {
+        dxs[p] = two ? cadd(d0, cmul_i(d1)) : d0;
+    } else {
+        dxs[e0] = d0;
+        if (two) dxs[e1] = d1;
+    }
 }
 
 // ----------------------------------------------------------------------------------------
@@ -555,17 +633,18 @@ int dg_chunks(int B, int M) {
 template <int FH, int FW>
 size_t bwd_ws(int B, int M) {
     if constexpr (pair_grid<FH, FW>()) {
-        // cotangent half-spectra (M, B, pitch), dx spectra (B, F), dG chunk partials
+        // cotangent half-spectra (M, B, pitch), dx spectra (B, F), dG and spectrum-sum chunk
+        // partials
         using P = PGeo<FH, FW>;
         const size_t nc = dg_chunks<FH, FW>(B, M);
-        return ((size_t)M * B * spec_pitch<FH, FW>() + (size_t)B * P::F + nc * M * P::F) *
+        return ((size_t)M * B * spec_pitch<FH, FW>() + (size_t)B * P::F + 2 * nc * M * P::F) *
                sizeof(cpx);
     }
     using W = WGeo<FH, FW>;
     const size_t mg = bwd_groups<FH, FW>(M);
     const size_t nc = dg_chunks<FH, FW>(B, M);
     return (((size_t)B * mg + (size_t)B) * W::PF + (size_t)M * B * spec_pitch<FH, FW>() +
-            nc * M * W::F) * sizeof(cpx);
+            2 * nc * M * W::F) * sizeof(cpx);
 }
 
 template <int FH, int FW>
@@ -631,7 +710,8 @@ int launch_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wou
 template <int FH, int FW>
 int launch_pbwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph,
                 int pw, const float* gz, const float* xhat, const float* ghat, int need_dx,
-                float* dx, float* dghat, int accumulate, int conj_out, void* ws) {
+                float* dx, float* dghat, int accumulate, int conj_out, float* ssum, int sum_acc,
+                void* ws) {
     using P = PGeo<FH, FW>;
     cpx* spec = reinterpret_cast<cpx*>(ws);
     cpx* dxs = spec + (size_t)M * B * spec_pitch<FH, FW>();
@@ -654,13 +734,15 @@ int launch_pbwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wo
     const int nchunk = dg_chunks<FH, FW>(B, M);
     const int bper = (B + nchunk - 1) / nchunk;
     const int nb = (B + bper - 1) / bper;
+    cpx* sc = reinterpret_cast<cpx*>(ssum);
     hipLaunchKernelGGL((k_wbwd_dg_red<FH, FW>), dim3((P::F + 255) / 256, M, nb), dim3(256), 0,
                        st, B, M, bper, spec, reinterpret_cast<const cpx*>(xhat), dgpart,
-                       reinterpret_cast<cpx*>(dghat), accumulate, conj_out);
+                       reinterpret_cast<cpx*>(dghat), accumulate, conj_out, sc, sum_acc);
     NC_CHECK_LAUNCH();
     if (nb > 1) {
-        hipLaunchKernelGGL(k_wbwd_dg_sum, dim3((P::F + 255) / 256, M), dim3(256), 0, st, nb, M,
-                           P::F, dgpart, reinterpret_cast<cpx*>(dghat), accumulate, conj_out);
+        hipLaunchKernelGGL(k_wbwd_dg_sum, dim3((P::F + 255) / 256, M, sc ? 2 : 1), dim3(256), 0,
+                           st, nb, M, P::F, dgpart, reinterpret_cast<cpx*>(dghat), accumulate,
+                           conj_out, sc, sum_acc);
         NC_CHECK_LAUNCH();
     }
     return NC_OK;
@@ -669,10 +751,11 @@ int launch_pbwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wo
 template <int FH, int FW>
 int launch_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph,
                int pw, const float* gz, const float* xhat, const float* ghat, int need_dx,
-               float* dx, float* dghat, int accumulate, int conj_out, void* ws) {
+               float* dx, float* dghat, int accumulate, int conj_out, float* ssum, int sum_acc,
+               void* ws) {
     if constexpr (pair_grid<FH, FW>())
         return launch_pbwd<FH, FW>(st, B, M, hin, win, hout, wout, ph, pw, gz, xhat, ghat, need_dx,
-                                   dx, dghat, accumulate, conj_out, ws);
+                                   dx, dghat, accumulate, conj_out, ssum, sum_acc, ws);
     using W = WGeo<FH, FW>;
     const int mg = bwd_groups<FH, FW>(M);
     cpx* dxpart = reinterpret_cast<cpx*>(ws);
@@ -699,15 +782,37 @@ int launch_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wou
     const int nchunk = dg_chunks<FH, FW>(B, M);
     const int bper = (B + nchunk - 1) / nchunk;
     cpx* dgpart = spec + (size_t)M * B * spec_pitch<FH, FW>();
+    cpx* sc = reinterpret_cast<cpx*>(ssum);
     hipLaunchKernelGGL((k_wbwd_dg_red<FH, FW>), dim3((nthr + 255) / 256, M, nchunk), dim3(256), 0,
                        st, B, M, bper, spec, reinterpret_cast<const cpx*>(xhat), dgpart,
-                       reinterpret_cast<cpx*>(dghat), accumulate, conj_out);
+                       reinterpret_cast<cpx*>(dghat), accumulate, conj_out, sc, sum_acc);
     NC_CHECK_LAUNCH();
     if (nchunk > 1) {
-        hipLaunchKernelGGL(k_wbwd_dg_sum, dim3((W::F + 255) / 256, M), dim3(256), 0, st, nchunk,
-                           M, W::F, dgpart, reinterpret_cast<cpx*>(dghat), accumulate, conj_out);
+        hipLaunchKernelGGL(k_wbwd_dg_sum, dim3((W::F + 255) / 256, M, sc ? 2 : 1), dim3(256), 0,
+                           st, nchunk, M, W::F, dgpart, reinterpret_cast<cpx*>(dghat), accumulate,
+                           conj_out, sc, sum_acc);
         NC_CHECK_LAUNCH();
     }
+    return NC_OK;
+}
+
+// Inverse of a one-sample dx spectrum (unpacked for the lane-pair grids, packed otherwise, as
+// k_hat_red wrote it) with the unshifted roll.
+template <int FH, int FW>
+int launch_hat_dx(hipStream_t st, int hin, int win, int ph, int pw, const cpx* dxs, float* dx) {
+    if constexpr (pair_grid<FH, FW>()) {
+        const PLds lf(hin, PGeo<FH, FW>::PITCH, FW, FH, true);
+        lds_limit(k_pdx_half<FH, FW>, lf.bytes);
+        hipLaunchKernelGGL((k_pdx_half<FH, FW>), dim3(1), dim3(64), lf.bytes, st, hin, win, ph,
+                           pw, dxs, dx);
+        NC_CHECK_LAUNCH();
+        return NC_OK;
+    }
+    const WLds<FH, FW> lf(hin, win);
+    lds_limit(k_wbwd_dx_fin<FH, FW>, lf.bytes);
+    hipLaunchKernelGGL((k_wbwd_dx_fin<FH, FW>), dim3(1), dim3(64), lf.bytes, st, 1, hin, win, ph,
+                       pw, lf.off, vec_ok(dx, (size_t)hin * win), dxs, dx);
+    NC_CHECK_LAUNCH();
     return NC_OK;
 }
 
@@ -816,10 +921,11 @@ size_t nc_fftconv_bwd_workspace_size(int B, int M, int fft_h, int fft_w) {
     return 0;
 }
 
-int nc_fftconv_bwd(void* stream, int B, int M, int hin, int win, int hout, int wout, int pad_h,
-                   int pad_w, int fft_h, int fft_w, const float* gz, const float* xhat,
-                   const float* ghat, int need_dx, float* dx, float* dghat, int accumulate,
-                   int conj_dghat, void* ws, size_t ws_bytes) {
+int nc_fftconv_bwd_ex(void* stream, int B, int M, int hin, int win, int hout, int wout,
+                      int pad_h, int pad_w, int fft_h, int fft_w, const float* gz,
+                      const float* xhat, const float* ghat, int need_dx, float* dx, float* dghat,
+                      int accumulate, int conj_dghat, float* gz_hat_sum, int sum_accumulate,
+                      void* ws, size_t ws_bytes) {
     int rc = fftconv_check(B, M, hin, win, hout, wout, pad_h, pad_w, fft_h, fft_w);
     if (rc != NC_OK) return rc;
     if (!gz || !xhat || !ghat || !dghat || (need_dx && !dx)) return NC_ERR_INVALID_ARGUMENT;
@@ -828,10 +934,48 @@ int nc_fftconv_bwd(void* stream, int B, int M, int hin, int win, int hout, int w
     hipStream_t st = nc_stream(stream);
     if (nc_large_grid(fft_h, fft_w))
         return nc_large_fftconv_bwd(st, B, M, hin, win, hout, wout, pad_h, pad_w, fft_h, fft_w,
-                                    gz, xhat, ghat, need_dx, dx, dghat, accumulate, conj_dghat, ws);
+                                    gz, xhat, ghat, need_dx, dx, dghat, accumulate, conj_dghat,
+                                    gz_hat_sum, sum_accumulate, ws);
 #define NC_CALL(A, Bv)                                                                     \
     launch_bwd<A, Bv>(st, B, M, hin, win, hout, wout, pad_h, pad_w, gz, xhat, ghat, need_dx, \
-                      dx, dghat, accumulate, conj_dghat, ws)
+                      dx, dghat, accumulate, conj_dghat, gz_hat_sum, sum_accumulate, ws)
+    NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
+#undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
+}
+
+int nc_fftconv_bwd(void* stream, int B, int M, int hin, int win, int hout, int wout, int pad_h,
+                   int pad_w, int fft_h, int fft_w, const float* gz, const float* xhat,
+                   const float* ghat, int need_dx, float* dx, float* dghat, int accumulate,
+                   int conj_dghat, void* ws, size_t ws_bytes) {
+    return nc_fftconv_bwd_ex(stream, B, M, hin, win, hout, wout, pad_h, pad_w, fft_h, fft_w, gz,
+                             xhat, ghat, need_dx, dx, dghat, accumulate, conj_dghat, nullptr, 0,
+                             ws, ws_bytes);
+}
+
+int nc_fftconv_bwd_hat(void* stream, int M, int hin, int win, int pad_h, int pad_w, int fft_h,
+                       int fft_w, const float* gz_hat, const float* xhat, const float* ghat,
+                       float* dx, float* dghat, int accumulate, int conj_dghat, void* ws,
+                       size_t ws_bytes) {
+    if (M <= 0 || hin <= 0 || win <= 0 || pad_h < 0 || pad_w < 0 || hin > fft_h ||
+        win > fft_w || !gz_hat || !ghat || !dx || (dghat && !xhat))
+        return NC_ERR_INVALID_ARGUMENT;
+    if (!(pow2_ok(fft_h) && pow2_ok(fft_w)) && !nc_large_grid(fft_h, fft_w))
+        return NC_ERR_UNSUPPORTED;
+    const size_t F = (size_t)fft_h * (fft_w / 2 + 1);
+    if (ws_bytes < F * sizeof(cpx) || !ws) return NC_ERR_WORKSPACE;
+    hipStream_t st = nc_stream(stream);
+    const bool large = nc_large_grid(fft_h, fft_w);
+    const bool packed = !large && !(fft_w == 64 && (fft_h == 32 || fft_h == 64));
+    cpx* dxs = reinterpret_cast<cpx*>(ws);
+    const int np = fft_h * (fft_w / 2);
+    hipLaunchKernelGGL(k_hat_red, dim3((np + 255) / 256), dim3(256), 0, st, M, fft_h, fft_w / 2,
+                       packed ? 1 : 0, reinterpret_cast<const cpx*>(gz_hat),
+                       reinterpret_cast<const cpx*>(xhat), reinterpret_cast<const cpx*>(ghat),
+                       dxs, reinterpret_cast<cpx*>(dghat), accumulate, conj_dghat);
+    NC_CHECK_LAUNCH();
+    if (large) return nc_large_hat_dx(st, hin, win, pad_h, pad_w, fft_h, fft_w, dxs, dx);
+#define NC_CALL(A, Bv) launch_hat_dx<A, Bv>(st, hin, win, pad_h, pad_w, dxs, dx)
     NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
 #undef NC_CALL
     return NC_ERR_UNSUPPORTED;

@@ -107,6 +107,7 @@ __global__ __launch_bounds__(kNT) void k_linv_conv(int M, int hout, int wout, in
 // Both reductions of the backward in one pass over the cotangent spectra sp (B, M, F):
 //   dxpart[c][b] = sum over the chunk's directions m of sp_bm * conj(ghat_m)   (need_dx)
 //   dghat[m]     = (+=) sum over b of sp_bm * conj(xhat_b)  (conjugated when conj_out)
+//   ssum[m]      = (+=, sum_acc) sum over b of sp_bm, the spectrum of sum_b gz_bm  (with ssum)
 // Thread = one bin; directions m0 .. m0+MC-1 of chunk c = blockIdx.y; b in increasing order.
 template <int MC>
 __global__ __launch_bounds__(256) void k_lred(int B, int M, int F, int need_dx,
@@ -114,16 +115,18 @@ __global__ __launch_bounds__(256) void k_lred(int B, int M, int F, int need_dx,
                                               const cpx* __restrict__ xhat,
                                               const cpx* __restrict__ ghat,
                                               cpx* __restrict__ dxpart, cpx* __restrict__ dghat,
-                                              int accumulate, int conj_out) {
+                                              int accumulate, int conj_out,
+                                              cpx* __restrict__ ssum, int sum_acc) {
     const int e = blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= F) return;
     const int m0 = blockIdx.y * MC;
     const int nm = min(MC, M - m0);
-    cpx G[MC], acc[MC];
+    cpx G[MC], acc[MC], sacc[MC];
 #pragma unroll
     for (int q = 0; q < MC; ++q) {
         G[q] = ghat[(size_t)(m0 + min(q, nm - 1)) * F + e];
         acc[q] = cmk(0.f, 0.f);
+        sacc[q] = cmk(0.f, 0.f);
     }
     for (int b = 0; b < B; ++b) {
         const cpx X = xhat[(size_t)b * F + e];
@@ -137,6 +140,7 @@ __global__ __launch_bounds__(256) void k_lred(int B, int M, int F, int need_dx,
             if (q < nm) {
                 d = cadd(d, cmulc(v[q], G[q]));
                 acc[q] = cadd(acc[q], cmulc(v[q], X));
+                sacc[q] = cadd(sacc[q], v[q]);
             }
         }
         if (need_dx) dxpart[((size_t)blockIdx.y * B + b) * F + e] = d;
@@ -147,6 +151,10 @@ __global__ __launch_bounds__(256) void k_lred(int B, int M, int F, int need_dx,
             const cpx v = conj_out ? cconj(acc[q]) : acc[q];
             cpx* o = dghat + (size_t)(m0 + q) * F + e;
             *o = accumulate ? cadd(*o, v) : v;
+            if (ssum) {
+                cpx* so = ssum + (size_t)(m0 + q) * F + e;
+                *so = sum_acc ? cadd(*so, sacc[q]) : sacc[q];
+            }
         }
     }
 }
@@ -305,7 +313,7 @@ size_t bwd_ws(int B, int M) {
 template <int FH, int FW>
 int conv_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph, int pw,
              const float* gz, const float* xhat, const float* ghat, int need_dx, float* dx,
-             float* dghat, int accumulate, int conj_out, void* ws) {
+             float* dghat, int accumulate, int conj_out, float* ssum, int sum_acc, void* ws) {
     using L = LG<FH, FW>;
     const int nchunk = (M + kRedMC - 1) / kRedMC;
     cpx* sp = reinterpret_cast<cpx*>(ws);
@@ -315,7 +323,7 @@ int conv_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout,
     hipLaunchKernelGGL((k_lred<kRedMC>), dim3((L::F + 255) / 256, nchunk), dim3(256), 0, st, B,
                        M, L::F, need_dx, sp, reinterpret_cast<const cpx*>(xhat),
                        reinterpret_cast<const cpx*>(ghat), part, reinterpret_cast<cpx*>(dghat),
-                       accumulate, conj_out);
+                       accumulate, conj_out, reinterpret_cast<cpx*>(ssum), sum_acc);
     NC_CHECK_LAUNCH();
     if (need_dx) {
         const int rs = inv_rows<FH, FW>(hin);
@@ -325,6 +333,17 @@ int conv_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout,
                            B, nchunk, hin, win, ph, pw, rs, part, dx);
         NC_CHECK_LAUNCH();
     }
+    return NC_OK;
+}
+
+template <int FH, int FW>
+int hat_dx(hipStream_t st, int hin, int win, int ph, int pw, const cpx* dxs, float* dx) {
+    const int rs = inv_rows<FH, FW>(hin);
+    const size_t lds = linv_lds_bytes<FH, FW, kNT>(rs);
+    set_lds(k_linv_dx<FH, FW>, lds);
+    hipLaunchKernelGGL((k_linv_dx<FH, FW>), dim3(1, (hin + rs - 1) / rs), dim3(kNT), lds, st, 1, 1,
+                       hin, win, ph, pw, rs, dxs, dx);
+    NC_CHECK_LAUNCH();
     return NC_OK;
 }
 
@@ -382,10 +401,18 @@ size_t nc_large_fftconv_bwd_ws(int B, int M, int fh, int fw) {
 int nc_large_fftconv_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout,
                          int ph, int pw, int fh, int fw, const float* gz, const float* xhat,
                          const float* ghat, int need_dx, float* dx, float* dghat, int accumulate,
-                         int conj_dghat, void* ws) {
+                         int conj_dghat, float* gz_hat_sum, int sum_accumulate, void* ws) {
 #define NC_CALL(A, Bv)                                                                     \
     conv_bwd<A, Bv>(st, B, M, hin, win, hout, wout, ph, pw, gz, xhat, ghat, need_dx, dx, dghat, \
-                    accumulate, conj_dghat, ws)
+                    accumulate, conj_dghat, gz_hat_sum, sum_accumulate, ws)
+    NC_DISPATCH_LARGE(fh, fw, NC_CALL);
+#undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
+}
+
+int nc_large_hat_dx(hipStream_t st, int hin, int win, int ph, int pw, int fh, int fw,
+                    const void* dxs, float* dx) {
+#define NC_CALL(A, Bv) hat_dx<A, Bv>(st, hin, win, ph, pw, reinterpret_cast<const cpx*>(dxs), dx)
     NC_DISPATCH_LARGE(fh, fw, NC_CALL);
 #undef NC_CALL
     return NC_ERR_UNSUPPORTED;

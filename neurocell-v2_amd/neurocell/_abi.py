@@ -40,6 +40,9 @@ _SIGS = {
     "nc_fftconv_fwd": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, P]),
     "nc_fftconv_bwd_workspace_size": (SZ, [I, I, I, I]),
     "nc_fftconv_bwd": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, I, P, P, I, I, P, SZ]),
+    "nc_fftconv_bwd_ex": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, I, P, P, I, I, P, I, P,
+                              SZ]),
+    "nc_fftconv_bwd_hat": (I, [P, I, I, I, I, I, I, I, P, P, P, P, P, I, I, P, SZ]),
     "nc_epilogue_workspace_size": (SZ, [I, I, I, I]),
     "nc_epilogue_fwd": (I, [P, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, SZ]),
     "nc_epilogue_bwd": (I, [P, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, P, P, P, P, I,

@@ -12,6 +12,8 @@ Forward (pure ROI + hoisted border theorem, propagator.py:1-9, 343-682):
     d-1 x [spectral conv -> hidden epilogue] -> spectral conv -> port epilogue
 Reverse: port bwd -> d x [spectral conv bwd (dx, dG in the frequency domain)
     -> hidden epilogue bwd] -> filter-spectrum bwd -> border conv bwd -> codd fusion bwd.
+The border conv's cotangent sum_{t>=1} sum_b gz_t is formed in the frequency domain by the
+steps' dG reductions (linearity of rfft2), so the cotangent planes are not re-read for it.
 """
 from __future__ import annotations
 
@@ -241,7 +243,8 @@ class StepPlan:
             self.ws_fc = torch.empty(max(1, n_fc // 4), **f)
             self.gz = torch.empty(B, M, h, w, **f)
             self.gy = [torch.empty(B, h, w, **f) for _ in range(2)]
-            self.gdelta = torch.empty(M, h, w, **f)
+            # spectra of the border cotangent sum_b gz over the steps with the border term
+            self.gdelta_hat = torch.empty(M, F, **c)
             self.dghat = torch.empty(M, F, **c)
             self.dghat_v = torch.empty(M, F, **c)
             self.gw = torch.empty(h, w, **f)
@@ -319,8 +322,8 @@ class StepPlan:
         hb = int(d > 1)
         call("nc_port_bwd", s, B, M, h, w, hb, self.fact, self.fslope, self.P, ptr(self.port_idx),
              ptr(self.zs[t]), ptr(self.delta), ptr(self.pp), ptr(self.zo), ptr(self.mean[t]),
-             ptr(self.rstd[t]), ptr(self.pre), ptr(g_out), ptr(self.gz),
-             ptr(self.gdelta) if hb else None, ptr(self.gpp), 0, ws_ep, n_ep)
+             ptr(self.rstd[t]), ptr(self.pre), ptr(g_out), ptr(self.gz), None, ptr(self.gpp), 0,
+             ws_ep, n_ep)
         first_epi = True
         valid_acc = 0
         for t in range(d - 1, -1, -1):
@@ -333,10 +336,13 @@ class StepPlan:
                      0, None, ptr(self.dghat_v), 0, 0, ws_fc, n_fc)
                 valid_acc = 1
             else:
-                call("nc_fftconv_bwd", s, B, M, h, w, h, w, self.cp[0], self.cp[1], fh, fw,
+                # steps t >= 1 carried the border term: their cotangent's batch sum, summed
+                # over those steps in the frequency domain, is the border conv's cotangent
+                hbt = t > 0
+                call("nc_fftconv_bwd_ex", s, B, M, h, w, h, w, self.cp[0], self.cp[1], fh, fw,
                      ptr(self.gz), ptr(self.xhat[t]), ptr(self.ghat), need_dx,
-                     ptr(gy) if need_dx else None, ptr(self.dghat), int(t < d - 1), 0, ws_fc,
-                     n_fc)
+                     ptr(gy) if need_dx else None, ptr(self.dghat), int(t < d - 1), 0,
+                     ptr(self.gdelta_hat) if hbt else None, int(t < d - 1), ws_fc, n_fc)
             if t == 0:
                 break
             te = t - 1
@@ -344,8 +350,8 @@ class StepPlan:
             call("nc_epilogue_bwd", s, B, M, h, w, self.act, self.slope, hbe, ptr(self.zs[te]),
                  ptr(self.delta), ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
                  ptr(self.mean[te]), ptr(self.rstd[te]), ptr(gy), ptr(self.gz),
-                 ptr(self.gdelta) if hbe else None, ptr(self.gw), ptr(self.gs), ptr(self.gb),
-                 int(not first_epi), 1, ws_ep, n_ep)  # gdelta already holds the port's share
+                 None, ptr(self.gw), ptr(self.gs), ptr(self.gb), int(not first_epi), 1, ws_ep,
+                 n_ep)
             first_epi = False
         only_t0_grid = self.t0_grid and d == 1
         if not only_t0_grid:
@@ -353,8 +359,8 @@ class StepPlan:
                  self.cp[1], ptr(self.dghat), ptr(g_filt), 0, 0)
         g_patch = None
         if d > 1:  # border conv reverse (same VALID shift as the full-grid t=0 step)
-            call("nc_fftconv_bwd", s, 1, M, self.Hp, self.Wp, h, w, self.kh - 1, self.kw - 1, fh,
-                 fw, ptr(self.gdelta), ptr(self.patch_hat), ptr(self.ghat), 1, ptr(self.gpatch),
+            call("nc_fftconv_bwd_hat", s, M, self.Hp, self.Wp, self.kh - 1, self.kw - 1, fh, fw,
+                 ptr(self.gdelta_hat), ptr(self.patch_hat), ptr(self.ghat), ptr(self.gpatch),
                  ptr(self.dghat_v), valid_acc, 0, ws_fc, n_fc)
             valid_acc = 1
             g_patch = ptr(self.gpatch)

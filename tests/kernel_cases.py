@@ -100,10 +100,13 @@ def case_fftconv(be, B=3, M=5, hin=10, win=12, kh=5, kw=3, FH=16, FW=16, seed=0)
     dx = be.zeros((B, hin, win))
     dgh = be.zeros((M, FH, FW // 2 + 1, 2))
     gzd = be.put(gz)
-    _ok(be, L.nc_fftconv_bwd(s, B, M, hin, win, hin, win, ph, pw, FH, FW, be.ptr(gzd),
-                             be.ptr(xhat), be.ptr(ghat), 1, be.ptr(dx), be.ptr(dgh), 0, 0,
-                             be.ptr(ws), ws.nbytes if hasattr(ws, "nbytes") else
-                             ws.numel() * 4), "bwd")
+    # the batch-summed cotangent spectra: written by the first call, added to by the second
+    ssum = be.zeros((M, FH, FW // 2 + 1, 2))
+    nb = ws.nbytes if hasattr(ws, "nbytes") else ws.numel() * 4
+    for acc in (0, 1):
+        _ok(be, L.nc_fftconv_bwd_ex(s, B, M, hin, win, hin, win, ph, pw, FH, FW, be.ptr(gzd),
+                                    be.ptr(xhat), be.ptr(ghat), 1, be.ptr(dx), be.ptr(dgh), 0, 0,
+                                    be.ptr(ssum), acc, be.ptr(ws), nb), "bwd")
     gf = be.zeros((M, 1, kh, kw))
     _ok(be, L.nc_filter_spectrum_bwd(s, M, kh, kw, FH, FW, ph, pw, be.ptr(dgh), be.ptr(gf), 0,
                                      0), "specbwd")
@@ -116,6 +119,9 @@ def case_fftconv(be, B=3, M=5, hin=10, win=12, kh=5, kw=3, FH=16, FW=16, seed=0)
         "dG": rel_l2(be.get(gf)[:, 0], dgr),
         "dghat": rel_l2(_cplx(be.get(dgh)),
                         O.conv2d_fft_unshifted_bwd(gz, x, g[:, 0], (ph, pw), (FH, FW))[1]),
+        # linearity: sum_b rfft2(gz_b) = rfft2(sum_b gz_b), twice (the accumulate call)
+        "gz_hat_sum": rel_l2(_cplx(be.get(ssum)),
+                             2 * np.fft.rfft2(gz.astype(np.float64).sum(0), s=(FH, FW))),
     }
 
 
@@ -147,8 +153,29 @@ def case_border_conv(be, M=4, h=12, w=10, kh=7, kw=5, FH=32, FW=16, seed=1):
     _ok(be, L.nc_filter_spectrum_bwd(s, M, kh, kw, FH, FW, kh - 1, kw - 1, be.ptr(dgh),
                                      be.ptr(gf), 0, 0), "specbwd")
     gpr, ggr = O.conv2d_bwd_direct(gdl, patch, g[:, 0], (0, 0))
+    # the same reverse from the cotangent's spectra (nc_fftconv_bwd_hat), the spectra taken
+    # as the batch sum of a two-sample cotangent whose samples add up to gdl
+    half = rng.normal(size=(1, M, h, w)).astype(np.float32)
+    g2 = be.put(np.concatenate([half, gdl - half]))
+    ws2 = be.zeros((L.nc_fftconv_bwd_workspace_size(2, M, FH, FW) // 4 + 1,))
+    nb2 = ws2.nbytes if hasattr(ws2, "nbytes") else ws2.numel() * 4
+    x2 = be.zeros((2, FH, FW // 2 + 1, 2))
+    dgx = be.zeros((M, FH, FW // 2 + 1, 2))
+    ssum = be.zeros((M, FH, FW // 2 + 1, 2))
+    _ok(be, L.nc_fftconv_bwd_ex(s, 2, M, Hp, Wp, h, w, kh - 1, kw - 1, FH, FW, be.ptr(g2),
+                                be.ptr(x2), be.ptr(ghat), 0, None, be.ptr(dgx), 0, 0,
+                                be.ptr(ssum), 0, be.ptr(ws2), nb2), "bwd_ex")
+    gp2 = be.zeros((1, Hp, Wp))
+    dgh2 = be.zeros((M, FH, FW // 2 + 1, 2))
+    _ok(be, L.nc_fftconv_bwd_hat(s, M, Hp, Wp, kh - 1, kw - 1, FH, FW, be.ptr(ssum),
+                                 be.ptr(phat), be.ptr(ghat), be.ptr(gp2), be.ptr(dgh2), 0, 0,
+                                 be.ptr(ws), nb), "bwd_hat")
+    gf2 = be.zeros((M, 1, kh, kw))
+    _ok(be, L.nc_filter_spectrum_bwd(s, M, kh, kw, FH, FW, kh - 1, kw - 1, be.ptr(dgh2),
+                                     be.ptr(gf2), 0, 0), "specbwd2")
     return {"delta": rel_l2(be.get(dl), O.conv2d_direct(patch, g[:, 0], (0, 0))),
-            "dpatch": rel_l2(be.get(gp), gpr), "dG": rel_l2(be.get(gf)[:, 0], ggr)}
+            "dpatch": rel_l2(be.get(gp), gpr), "dG": rel_l2(be.get(gf)[:, 0], ggr),
+            "dpatch_hat": rel_l2(be.get(gp2), gpr), "dG_hat": rel_l2(be.get(gf2)[:, 0], ggr)}
 
 
 def case_epilogue(be, B=3, M=5, h=10, w=12, act="tanh", has_border=1, seed=2):

@@ -41,8 +41,12 @@ def test_fftconv_large(be, B, M, FH, FW, hin, win, kh, kw):
     _assert_small(case_fftconv(be, B=B, M=M, hin=hin, win=win, kh=kh, kw=kw, FH=FH, FW=FW))
 
 
-def test_border_conv(be):
-    _assert_small(case_border_conv(be))
+@pytest.mark.parametrize("FH,FW,h,w,kh,kw", [
+    (32, 16, 12, 10, 7, 5),      # wavefront transforms (packed dx spectrum)
+    (64, 64, 40, 50, 23, 13),    # lane-pair transforms
+    (128, 64, 60, 30, 31, 13)])  # workgroup transforms
+def test_border_conv(be, FH, FW, h, w, kh, kw):
+    _assert_small(case_border_conv(be, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW))
 
 
 @pytest.mark.parametrize("shape", [(2, 3, 10, 12, "tanh", 1), (2, 3, 20, 40, "leaky_relu", 0),
