@@ -36,13 +36,13 @@ def synthetic(name, seed, B=None):
     return CONFIGS[name].synthetic(seed, batch=B)
 
 
-def algorithmic_bytes(B, M, N, F, hb=1, dx=1, P=16):
+def algorithmic_bytes(B, M, N, F, hb=0, dx=1, P=16):
     """Per-call algorithmic bytes (each interface operand counted once, 4 B/f32, 8 B/c64).
-    fftconv_fwd: x in, ghat in, z out, xhat out.  fftconv_bwd: gz, xhat, ghat in, dx out,
-    dghat read-modify-write, the cotangent spectrum sum out.  The epilogue and port backward
-    read the border term (hb) but no longer write its cotangent (formed from the spectra)."""
+    fftconv_fwd: x in, the border spectrum and ghat in, z out, xhat out.  fftconv_bwd: gz,
+    xhat, ghat in, dx out, dghat read-modify-write, the cotangent spectrum sum out.  The
+    step's epilogues run without a border term (hb = 0: it is folded into the spectra)."""
     return {
-        "fftconv_fwd": 4 * B * N + 8 * M * F + 4 * B * M * N + 8 * B * F,
+        "fftconv_fwd": 4 * B * N + 8 * F + 8 * M * F + 4 * B * M * N + 8 * B * F,
         "fftconv_bwd": (4 * B * M * N + 8 * B * F + 8 * M * F + dx * 4 * B * N + 16 * M * F
                         + 8 * M * F),
         "epilogue_fwd": 4 * (B * M * N + hb * M * N + 3 * N + B * N + 2 * B * M),
@@ -77,28 +77,28 @@ def kernel_families(ts, torch, reps):
     ws_ep, n_ep = ptr(p.ws_epi), p.ws_epi.numel() * 4
     ws_fc, n_fc = ptr(p.ws_fc), p.ws_fc.numel() * 4
     fams = {
-        "fftconv_fwd": lambda: call("nc_fftconv_fwd", s(), B, M, h, w, h, w, p.cp[0], p.cp[1],
-                                    fh, fw, ptr(p.xs[t]), ptr(p.ghat), ptr(p.zs[t]),
-                                    ptr(p.xhat[t])),
+        "fftconv_fwd": lambda: call("nc_fftconv_fwd_ex", s(), B, M, h, w, h, w, p.cp[0],
+                                    p.cp[1], fh, fw, ptr(p.xs[t]), ptr(p.border_hat),
+                                    ptr(p.ghat), ptr(p.zs[t]), ptr(p.xhat[t])),
         "fftconv_bwd": lambda: call("nc_fftconv_bwd_ex", s(), B, M, h, w, h, w, p.cp[0],
                                     p.cp[1], fh, fw, ptr(p.gz), ptr(p.xhat[t]), ptr(p.ghat), 1,
                                     ptr(p.gy[0]), ptr(p.dghat), 0, 0, ptr(p.gdelta_hat), 0,
                                     ws_fc, n_fc),
-        "epilogue_fwd": lambda: call("nc_epilogue_fwd", s(), B, M, h, w, p.act, p.slope, 1,
-                                     ptr(p.zs[t]), ptr(p.delta), ptr(p.w_eff), ptr(p.s_eff),
+        "epilogue_fwd": lambda: call("nc_epilogue_fwd", s(), B, M, h, w, p.act, p.slope, 0,
+                                     ptr(p.zs[t]), None, ptr(p.w_eff), ptr(p.s_eff),
                                      ptr(p.b_roi), ptr(p.xs[t + 1]), ptr(p.mean[t]),
                                      ptr(p.rstd[t]), ws_ep, n_ep),
-        "epilogue_bwd": lambda: call("nc_epilogue_bwd", s(), B, M, h, w, p.act, p.slope, 1,
-                                     ptr(p.zs[t]), ptr(p.delta), ptr(p.w_eff), ptr(p.s_eff),
+        "epilogue_bwd": lambda: call("nc_epilogue_bwd", s(), B, M, h, w, p.act, p.slope, 0,
+                                     ptr(p.zs[t]), None, ptr(p.w_eff), ptr(p.s_eff),
                                      ptr(p.b_roi), ptr(p.mean[t]), ptr(p.rstd[t]),
                                      ptr(p.gy[1]), ptr(p.gz), None, ptr(p.gw),
                                      ptr(p.gs), ptr(p.gb), 0, 0, ws_ep, n_ep),
-        "port_fwd": lambda: call("nc_port_fwd", s(), B, M, h, w, 1, p.fact, p.fslope, p.P,
-                                 ptr(p.port_idx), ptr(p.zs[-1]), ptr(p.delta), ptr(p.pp),
+        "port_fwd": lambda: call("nc_port_fwd", s(), B, M, h, w, 0, p.fact, p.fslope, p.P,
+                                 ptr(p.port_idx), ptr(p.zs[-1]), None, ptr(p.pp),
                                  ptr(p.out), ptr(p.zo), ptr(p.mean[-1]), ptr(p.rstd[-1]),
                                  ptr(p.pre), ws_ep, n_ep),
-        "port_bwd": lambda: call("nc_port_bwd", s(), B, M, h, w, 1, p.fact, p.fslope, p.P,
-                                 ptr(p.port_idx), ptr(p.zs[-1]), ptr(p.delta), ptr(p.pp),
+        "port_bwd": lambda: call("nc_port_bwd", s(), B, M, h, w, 0, p.fact, p.fslope, p.P,
+                                 ptr(p.port_idx), ptr(p.zs[-1]), None, ptr(p.pp),
                                  ptr(p.zo), ptr(p.mean[-1]), ptr(p.rstd[-1]), ptr(p.pre),
                                  ptr(p.g_out), ptr(p.gz), None, ptr(p.gpp), 0, ws_ep,
                                  n_ep),

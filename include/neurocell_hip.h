@@ -134,6 +134,27 @@ int nc_fftconv_fwd(void* stream, int B, int M, int hin, int win, int hout, int w
                    int pad_w, int fft_h, int fft_w, const float* x, const float* ghat, float* z,
                    float* xhat);
 
+/*
+ * nc_fftconv_fwd with xhat_add (fft_h, fft_w/2+1) complex added to every sample's spectrum
+ * before the correlation (NULL: none); xhat receives the sums.  With xhat_add = the
+ * nc_plane_spectrum of the border patch shifted by (pad_h - (kh-1), pad_w - (kw-1)) mod the
+ * grid, z = the ROI correlation plus the hoisted border conv delta (propagator.py:362-366,
+ * 425-441) in one pass, and the reverse through nc_fftconv_bwd_ex carries the border's dG.
+ * No counterpart in the reference (which adds delta to every step's conv output).
+ */
+int nc_fftconv_fwd_ex(void* stream, int B, int M, int hin, int win, int hout, int wout,
+                      int pad_h, int pad_w, int fft_h, int fft_w, const float* x,
+                      const float* xhat_add, const float* ghat, float* z, float* xhat);
+
+/*
+ * Half-spectra (nplanes, fft_h, fft_w/2+1) complex of real (hin, win) planes placed at the
+ * origin of the spectral grid and circularly shifted by (shift_h, shift_w)
+ * (0 <= shift < grid): rfft2 times the phase ramp W^(kh*shift_h) W^(kw*shift_w), from exact
+ * table twiddles.  Supported grids as nc_fftconv_fwd.  No counterpart in the reference.
+ */
+int nc_plane_spectrum(void* stream, int nplanes, int hin, int win, int fft_h, int fft_w,
+                      int shift_h, int shift_w, const float* x, float* xhat);
+
 /* Workspace bytes needed by nc_fftconv_bwd for these shapes. */
 size_t nc_fftconv_bwd_workspace_size(int B, int M, int fft_h, int fft_w);
 

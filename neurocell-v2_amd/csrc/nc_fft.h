@@ -134,6 +134,32 @@ NC_DEV cpx twiddle(int e, const cpx* tw) {
     return w;
 }
 
+// What a forward half-spectrum kernel applies to each bin before storing it:
+//   kPostNone   the spectrum itself;
+//   kPostAdd    plus add[kh][kw], one (FH, FW/2+1) spectrum shared by every plane;
+//   kPostShift  times W_FH^(kh*sh) * W_FW^(kw*sw): the spectrum of the plane circularly
+//               shifted by (sh, sw) on the grid (0 <= sh < FH, 0 <= sw < FW).
+enum { kPostNone = 0, kPostAdd = 1, kPostShift = 2 };
+struct SpecPost {
+    const cpx* add;
+    int sh, sw;
+};
+
+// W_FH^(kh*sh) * W_FW^(kw*sw), the phase ramp of a circular shift (exact table twiddles).
+template <int FH, int FW>
+NC_DEV cpx spec_ramp(int kh, int kw, int sh, int sw) {
+    const float2 a = NC_TW256[((kh * sh) & (FH - 1)) * (NC_TW_N / FH)];
+    const float2 b = NC_TW256[((kw * sw) & (FW - 1)) * (NC_TW_N / FW)];
+    return cmul(cmk(a.x, a.y), cmk(b.x, b.y));
+}
+
+template <int POST, int FH, int FW>
+NC_DEV cpx spec_post(cpx v, int kh, int kw, const SpecPost& p) {
+    if constexpr (POST == kPostAdd) return cadd(v, p.add[kh * (FW / 2 + 1) + kw]);
+    if constexpr (POST == kPostShift) return cmul(v, spec_ramp<FH, FW>(kh, kw, p.sh, p.sw));
+    return v;
+}
+
 // Copies the twiddle table into LDS (256 cpx); callers barrier before first use.
 NC_DEV void load_twiddles(cpx* tw) {
     for (int i = threadIdx.x; i < NC_TW_N; i += blockDim.x) tw[i] = NC_TW256[i];

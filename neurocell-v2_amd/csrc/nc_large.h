@@ -18,7 +18,10 @@ int nc_large_filter_spectrum_bwd(hipStream_t st, int M, int kh, int kw, int fft_
 
 int nc_large_fftconv_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout,
                          int pad_h, int pad_w, int fft_h, int fft_w, const float* x,
-                         const float* ghat, float* z, float* xhat);
+                         const float* xhat_add, const float* ghat, float* z, float* xhat);
+
+int nc_large_plane_spectrum(hipStream_t st, int nplanes, int hin, int win, int fft_h, int fft_w,
+                            int shift_h, int shift_w, const float* x, float* xhat);
 
 size_t nc_large_fftconv_bwd_ws(int B, int M, int fft_h, int fft_w);
 

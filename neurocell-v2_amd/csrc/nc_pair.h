@@ -215,8 +215,9 @@ NC_DEV void pstage_copy(const float* O, int rows, int cols, float* __restrict__ 
 }
 
 // Half-spectrum store of a forward column pass: lane pair kc holds packed column kc at rows
-// t*FH/2 + k.  Column 0 (DC + i*Nyquist) is split with its row mirrors; store(kh, kw, value)
-// receives every bin of the half-spectrum.  All lanes take part in the swaps.
+// t*FH/2 + k.  Column 0 (DC + i*Nyquist) is split with its row mirrors; store(k, kh, kw, value)
+// receives every bin of the half-spectrum (k: the register slot, kh = t*FH/2 + k).  All lanes
+// take part in the swaps.
 template <int FH, int FW, class Store>
 NC_DEV void pstore_half(const cpx* v, Store store) {
     using P = PGeo<FH, FW>;
@@ -226,13 +227,13 @@ NC_DEV void pstore_half(const cpx* v, Store store) {
     const int base = t * P::HH;
     if (kc != 0) {
 #pragma unroll
-        for (int k = 0; k < P::HH; ++k) store(base + k, kc, v[k]);
+        for (int k = 0; k < P::HH; ++k) store(k, base + k, kc, v[k]);
     } else {
 #pragma unroll
         for (int k = 0; k < P::HH; ++k) {
             const cpx c = v[k], d = cconj(mr[k]);
-            store(base + k, 0, cscale(cadd(c, d), 0.5f));
-            store(base + k, FW / 2, cmul_negi(cscale(csub(c, d), 0.5f)));
+            store(k, base + k, 0, cscale(cadd(c, d), 0.5f));
+            store(k, base + k, FW / 2, cmul_negi(cscale(csub(c, d), 0.5f)));
         }
     }
 }

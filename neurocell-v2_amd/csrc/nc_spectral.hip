@@ -83,10 +83,10 @@ __global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_filter_spectrum_bwd(
 // Half-spectra of nplanes real (hin x win) planes stored back to back in x (FLIP: the plane
 // is read flipped in both axes, which turns the correlation filter into a convolution
 // kernel, kernels_greens.py:240-259).  out: (nplanes, FH, FW/2+1).
-template <int FH, int FW, bool FLIP>
+template <int FH, int FW, bool FLIP, int POST>
 __global__ __launch_bounds__(64) void k_wrfft2(int nplanes, int hin, int win, int s_off, int vec,
                                                const float* __restrict__ x,
-                                               cpx* __restrict__ out) {
+                                               cpx* __restrict__ out, SpecPost post) {
     using W = WGeo<FH, FW>;
     HIP_DYNAMIC_SHARED(float, lds)
     cpx* T = reinterpret_cast<cpx*>(lds);
@@ -108,12 +108,13 @@ __global__ __launch_bounds__(64) void k_wrfft2(int nplanes, int hin, int win, in
 #pragma unroll
         for (int kh = 0; kh < FH; ++kh) {
             const cpx c = v[kh], d = cconj(v[(FH - kh) & (FH - 1)]);
-            o[kh * W::SP] = cscale(cadd(c, d), 0.5f);
-            o[kh * W::SP + FW / 2] = cmul_negi(cscale(csub(c, d), 0.5f));
+            o[kh * W::SP] = spec_post<POST, FH, FW>(cscale(cadd(c, d), 0.5f), kh, 0, post);
+            o[kh * W::SP + FW / 2] =
+                spec_post<POST, FH, FW>(cmul_negi(cscale(csub(c, d), 0.5f)), kh, FW / 2, post);
         }
     } else {
 #pragma unroll
-        for (int kh = 0; kh < FH; ++kh) o[kh * W::SP] = v[kh];
+        for (int kh = 0; kh < FH; ++kh) o[kh * W::SP] = spec_post<POST, FH, FW>(v[kh], kh, kc, post);
     }
 }
 
@@ -442,31 +443,48 @@ struct PLds {
     }
 };
 
-// Half-spectrum of one real (hin x win) plane src into o (FLIP: read rotated by 180 degrees);
-// the calling wavefront owns the plane.
-template <int FH, int FW, bool FLIP>
+// Half-spectrum of one real (hin x win) plane src into o (FLIP: read rotated by 180 degrees),
+// each bin passed through spec_post<POST>; the calling wavefront owns the plane.  kPostAdd
+// loads the lane's added bins while the column transform runs, so no store waits on a load.
+template <int FH, int FW, bool FLIP, int POST>
 NC_DEV void prfft2_plane(const float* __restrict__ src, int hin, int win, int vec, float* lds,
-                         cpx* __restrict__ o) {
+                         cpx* __restrict__ o, const SpecPost& post) {
     using P = PGeo<FH, FW>;
+    constexpr int NA = POST == kPostAdd ? P::HH : 1;
     cpx* T = reinterpret_cast<cpx*>(lds);
     istage<FW, 1, FLIP>(src, (size_t)hin * win, 1, hin, win, vec != 0, lds);
     __syncthreads();
     prow_fwd<FH, FW>(lds, hin, T);
     __syncthreads();
+    cpx av[NA], an[NA];  // bins (t*HH + k, kc) and, for column 0's split, (t*HH + k, FW/2)
+    if constexpr (POST == kPostAdd) {
+        const int lane = threadIdx.x & 63, kc = lane >> 1, t = lane & 1;
+        const cpx* a = post.add + (size_t)t * P::HH * P::SP;
+#pragma unroll
+        for (int k = 0; k < P::HH; ++k) {
+            av[k] = a[k * P::SP + kc];
+            an[k] = a[k * P::SP + FW / 2];
+        }
+    }
     cpx v[P::HH];
     pcol_fwd<FH, FW>(T, hin, v);
-    pstore_half<FH, FW>(v, [&](int kh, int kw, cpx val) { o[kh * P::SP + kw] = val; });
+    pstore_half<FH, FW>(v, [&](int k, int kh, int kw, cpx val) {
+        if constexpr (POST == kPostAdd) val = cadd(val, kw == FW / 2 ? an[k] : av[k]);
+        if constexpr (POST == kPostShift) val = spec_post<POST, FH, FW>(val, kh, kw, post);
+        o[kh * P::SP + kw] = val;
+    });
 }
 
 // Half-spectra of real (hin x win) planes (FLIP: read rotated by 180 degrees, the filter
-// spectra of kernels_greens.py:240-259); one wavefront per plane.
-template <int FH, int FW, bool FLIP>
+// spectra of kernels_greens.py:240-259), post-processed by spec_post<POST>; one wavefront per
+// plane.
+template <int FH, int FW, bool FLIP, int POST>
 __global__ __launch_bounds__(64) void k_prfft2(int hin, int win, int vec,
                                                const float* __restrict__ x,
-                                               cpx* __restrict__ out) {
+                                               cpx* __restrict__ out, SpecPost post) {
     HIP_DYNAMIC_SHARED(float, lds)
-    prfft2_plane<FH, FW, FLIP>(x + (size_t)blockIdx.x * hin * win, hin, win, vec, lds,
-                               out + (size_t)blockIdx.x * PGeo<FH, FW>::F);
+    prfft2_plane<FH, FW, FLIP, POST>(x + (size_t)blockIdx.x * hin * win, hin, win, vec, lds,
+                                     out + (size_t)blockIdx.x * PGeo<FH, FW>::F, post);
 }
 
 // Backward, first stage (kernels_pallas.py:1794-1821): the half-spectrum of every cotangent
@@ -477,8 +495,9 @@ __global__ __launch_bounds__(64) void k_pspec(int B, int M, int hout, int wout, 
                                               cpx* __restrict__ spec) {
     HIP_DYNAMIC_SHARED(float, lds)
     const int g = blockIdx.x, b = g / M, m = g - b * M;
-    prfft2_plane<FH, FW, false>(gz + (size_t)g * hout * wout, hout, wout, vec, lds,
-                                spec + ((size_t)m * B + b) * spec_pitch<FH, FW>());
+    prfft2_plane<FH, FW, false, kPostNone>(gz + (size_t)g * hout * wout, hout, wout, vec, lds,
+                                           spec + ((size_t)m * B + b) * spec_pitch<FH, FW>(),
+                                           SpecPost{});
 }
 
 // Backward, dx reduction (kernels_pallas.py:1794-1812): dxs[b][e] = sum over m, in increasing
@@ -647,45 +666,48 @@ size_t bwd_ws(int B, int M) {
             2 * nc * M * W::F) * sizeof(cpx);
 }
 
-template <int FH, int FW>
-int launch_rfft2(hipStream_t st, int nplanes, int hin, int win, bool flip, const float* x,
-                 cpx* out) {
+template <int FH, int FW, bool FLIP, int POST>
+void launch_rfft2_k(hipStream_t st, int nplanes, int hin, int win, const float* x, cpx* out,
+                    const SpecPost& post) {
+    const int vec = vec_ok(x, (size_t)hin * win);
     if constexpr (pair_grid<FH, FW>()) {
         const PLds l(hin, PGeo<FH, FW>::PITCH, FW, FH, false);
-        const int vec = vec_ok(x, (size_t)hin * win);
-        if (flip) {
-            lds_limit(k_prfft2<FH, FW, true>, l.bytes);
-            hipLaunchKernelGGL((k_prfft2<FH, FW, true>), dim3(nplanes), dim3(64), l.bytes, st, hin,
-                               win, vec, x, out);
-        } else {
-            lds_limit(k_prfft2<FH, FW, false>, l.bytes);
-            hipLaunchKernelGGL((k_prfft2<FH, FW, false>), dim3(nplanes), dim3(64), l.bytes, st,
-                               hin, win, vec, x, out);
-        }
-        NC_CHECK_LAUNCH();
-        return NC_OK;
-    }
-    using W = WGeo<FH, FW>;
-    WLds<FH, FW> l(hin, win);
-    dim3 grid((nplanes + W::PPW - 1) / W::PPW);
-    if (flip) {
-        lds_limit(k_wrfft2<FH, FW, true>, l.bytes);
-        hipLaunchKernelGGL((k_wrfft2<FH, FW, true>), grid, dim3(64), l.bytes, st, nplanes, hin,
-                           win, l.off, vec_ok(x, (size_t)hin * win), x, out);
+        lds_limit(k_prfft2<FH, FW, FLIP, POST>, l.bytes);
+        hipLaunchKernelGGL((k_prfft2<FH, FW, FLIP, POST>), dim3(nplanes), dim3(64), l.bytes, st,
+                           hin, win, vec, x, out, post);
     } else {
-        lds_limit(k_wrfft2<FH, FW, false>, l.bytes);
-        hipLaunchKernelGGL((k_wrfft2<FH, FW, false>), grid, dim3(64), l.bytes, st, nplanes, hin,
-                           win, l.off, vec_ok(x, (size_t)hin * win), x, out);
+        using W = WGeo<FH, FW>;
+        WLds<FH, FW> l(hin, win);
+        lds_limit(k_wrfft2<FH, FW, FLIP, POST>, l.bytes);
+        hipLaunchKernelGGL((k_wrfft2<FH, FW, FLIP, POST>), dim3((nplanes + W::PPW - 1) / W::PPW),
+                           dim3(64), l.bytes, st, nplanes, hin, win, l.off, vec, x, out, post);
     }
+}
+
+// Half-spectra of nplanes real planes; flip (the filter spectra) takes no post-operation.
+template <int FH, int FW>
+int launch_rfft2(hipStream_t st, int nplanes, int hin, int win, bool flip, const float* x,
+                 cpx* out, int post_kind = kPostNone, const SpecPost& post = SpecPost{}) {
+    if (flip)
+        launch_rfft2_k<FH, FW, true, kPostNone>(st, nplanes, hin, win, x, out, post);
+    else if (post_kind == kPostAdd)
+        launch_rfft2_k<FH, FW, false, kPostAdd>(st, nplanes, hin, win, x, out, post);
+    else if (post_kind == kPostShift)
+        launch_rfft2_k<FH, FW, false, kPostShift>(st, nplanes, hin, win, x, out, post);
+    else
+        launch_rfft2_k<FH, FW, false, kPostNone>(st, nplanes, hin, win, x, out, post);
     NC_CHECK_LAUNCH();
     return NC_OK;
 }
 
 template <int FH, int FW>
 int launch_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph,
-               int pw, const float* x, const float* ghat, float* z, float* xhat) {
+               int pw, const float* x, const float* xhat_add, const float* ghat, float* z,
+               float* xhat) {
     using W = WGeo<FH, FW>;
-    int rc = launch_rfft2<FH, FW>(st, B, hin, win, false, x, reinterpret_cast<cpx*>(xhat));
+    const SpecPost post{reinterpret_cast<const cpx*>(xhat_add), 0, 0};
+    int rc = launch_rfft2<FH, FW>(st, B, hin, win, false, x, reinterpret_cast<cpx*>(xhat),
+                                  xhat_add ? kPostAdd : kPostNone, post);
     if (rc != NC_OK) return rc;
     if constexpr (pair_grid<FH, FW>()) {
         const PLds l(hout, PGeo<FH, FW>::PITCH, FW, FH, true);
@@ -894,18 +916,44 @@ static int fftconv_check(int B, int M, int hin, int win, int hout, int wout, int
     return NC_OK;
 }
 
-int nc_fftconv_fwd(void* stream, int B, int M, int hin, int win, int hout, int wout, int pad_h,
-                   int pad_w, int fft_h, int fft_w, const float* x, const float* ghat, float* z,
-                   float* xhat) {
+int nc_fftconv_fwd_ex(void* stream, int B, int M, int hin, int win, int hout, int wout,
+                      int pad_h, int pad_w, int fft_h, int fft_w, const float* x,
+                      const float* xhat_add, const float* ghat, float* z, float* xhat) {
     int rc = fftconv_check(B, M, hin, win, hout, wout, pad_h, pad_w, fft_h, fft_w);
     if (rc != NC_OK) return rc;
     if (!x || !ghat || !z || !xhat) return NC_ERR_INVALID_ARGUMENT;
     hipStream_t st = nc_stream(stream);
     if (nc_large_grid(fft_h, fft_w))
         return nc_large_fftconv_fwd(st, B, M, hin, win, hout, wout, pad_h, pad_w, fft_h, fft_w, x,
-                                    ghat, z, xhat);
+                                    xhat_add, ghat, z, xhat);
 #define NC_CALL(A, Bv) \
-    launch_fwd<A, Bv>(st, B, M, hin, win, hout, wout, pad_h, pad_w, x, ghat, z, xhat)
+    launch_fwd<A, Bv>(st, B, M, hin, win, hout, wout, pad_h, pad_w, x, xhat_add, ghat, z, xhat)
+    NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
+#undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
+}
+
+int nc_fftconv_fwd(void* stream, int B, int M, int hin, int win, int hout, int wout, int pad_h,
+                   int pad_w, int fft_h, int fft_w, const float* x, const float* ghat, float* z,
+                   float* xhat) {
+    return nc_fftconv_fwd_ex(stream, B, M, hin, win, hout, wout, pad_h, pad_w, fft_h, fft_w, x,
+                             nullptr, ghat, z, xhat);
+}
+
+int nc_plane_spectrum(void* stream, int nplanes, int hin, int win, int fft_h, int fft_w,
+                      int shift_h, int shift_w, const float* x, float* xhat) {
+    if (nplanes <= 0 || hin <= 0 || win <= 0 || hin > fft_h || win > fft_w || shift_h < 0 ||
+        shift_w < 0 || shift_h >= fft_h || shift_w >= fft_w || !x || !xhat)
+        return NC_ERR_INVALID_ARGUMENT;
+    hipStream_t st = nc_stream(stream);
+    if (nc_large_grid(fft_h, fft_w))
+        return nc_large_plane_spectrum(st, nplanes, hin, win, fft_h, fft_w, shift_h, shift_w, x,
+                                       xhat);
+    if (!pow2_ok(fft_h) || !pow2_ok(fft_w)) return NC_ERR_UNSUPPORTED;
+    const SpecPost post{nullptr, shift_h, shift_w};
+#define NC_CALL(A, Bv)                                                                   \
+    launch_rfft2<A, Bv>(st, nplanes, hin, win, false, x, reinterpret_cast<cpx*>(xhat), \
+                        kPostShift, post)
     NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
 #undef NC_CALL
     return NC_ERR_UNSUPPORTED;

@@ -52,10 +52,10 @@ NC_DEV LdsParts lds_parts(float* lds) {
     return p;
 }
 
-template <int FH, int FW, bool FLIP>
+template <int FH, int FW, bool FLIP, int POST>
 __global__ __launch_bounds__(kNT) void k_lrfft2(int hin, int win, int cs, size_t pstride,
                                                 const float* __restrict__ x,
-                                                cpx* __restrict__ out) {
+                                                cpx* __restrict__ out, SpecPost post) {
     using L = LG<FH, FW>;
     HIP_DYNAMIC_SHARED(float, lds)
     const LdsParts P = lds_parts<FH, FW, true>(lds);
@@ -68,7 +68,8 @@ __global__ __launch_bounds__(kNT) void k_lrfft2(int hin, int win, int cs, size_t
             return FLIP ? src[(hin - 1 - r) * win + (win - 1 - c)] : src[r * win + c];
         },
         hin, win, (int)blockIdx.y * cs, cs,
-        [&](int kh, int kw, cpx v) { o[kh * L::SP + kw] = v; }, P.seg, P.c0, P.scr, P.tw);
+        [&](int kh, int kw, cpx v) { o[kh * L::SP + kw] = spec_post<POST, FH, FW>(v, kh, kw, post); },
+        P.seg, P.c0, P.scr, P.tw);
 }
 
 // Packed column value of a half-spectrum at (kh, kw): DC + i*Nyquist for kw == 0.
@@ -250,22 +251,33 @@ int inv_rows(int rows) {
     }
 }
 
+template <int FH, int FW, bool FLIP, int POST>
+void rfft2_launch(hipStream_t st, dim3 grid, size_t lds, int hin, int win, int cs, size_t pstride,
+                  const float* x, cpx* out, const SpecPost& post) {
+    set_lds(k_lrfft2<FH, FW, FLIP, POST>, lds);
+    hipLaunchKernelGGL((k_lrfft2<FH, FW, FLIP, POST>), grid, dim3(kNT), lds, st, hin, win, cs,
+                       pstride, x, out, post);
+}
+
+// Half-spectra of nplanes real planes, each bin through spec_post<post_kind> (flip: the filter
+// spectra, no post-operation).
 template <int FH, int FW>
 int rfft2_planes(hipStream_t st, int nplanes, int hin, int win, size_t pstride, bool flip,
-                 const float* x, cpx* out) {
+                 const float* x, cpx* out, int post_kind = kPostNone,
+                 const SpecPost& post = SpecPost{}) {
     const int cs = fwd_cols<FH, FW>(hin);
     const size_t lds = lfwd_lds_bytes<FH, FW, kNT>(hin, cs);
     if (lds > kLdsMax) return NC_ERR_UNSUPPORTED;
     const dim3 grid(nplanes, LG<FH, FW>::NC / cs);
-    if (flip) {
-        set_lds(k_lrfft2<FH, FW, true>, lds);
-        hipLaunchKernelGGL((k_lrfft2<FH, FW, true>), grid, dim3(kNT), lds, st, hin, win, cs,
-                           pstride, x, out);
-    } else {
-        set_lds(k_lrfft2<FH, FW, false>, lds);
-        hipLaunchKernelGGL((k_lrfft2<FH, FW, false>), grid, dim3(kNT), lds, st, hin, win, cs,
-                           pstride, x, out);
-    }
+    if (flip)
+        rfft2_launch<FH, FW, true, kPostNone>(st, grid, lds, hin, win, cs, pstride, x, out, post);
+    else if (post_kind == kPostAdd)
+        rfft2_launch<FH, FW, false, kPostAdd>(st, grid, lds, hin, win, cs, pstride, x, out, post);
+    else if (post_kind == kPostShift)
+        rfft2_launch<FH, FW, false, kPostShift>(st, grid, lds, hin, win, cs, pstride, x, out,
+                                                post);
+    else
+        rfft2_launch<FH, FW, false, kPostNone>(st, grid, lds, hin, win, cs, pstride, x, out, post);
     NC_CHECK_LAUNCH();
     return NC_OK;
 }
@@ -290,9 +302,11 @@ int spec_bwd(hipStream_t st, int M, int kh, int kw, int sh, int sw, const float*
 
 template <int FH, int FW>
 int conv_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph, int pw,
-             const float* x, const float* ghat, float* z, float* xhat) {
+             const float* x, const float* xhat_add, const float* ghat, float* z, float* xhat) {
+    const SpecPost post{reinterpret_cast<const cpx*>(xhat_add), 0, 0};
     int rc = rfft2_planes<FH, FW>(st, B, hin, win, (size_t)hin * win, false, x,
-                                  reinterpret_cast<cpx*>(xhat));
+                                  reinterpret_cast<cpx*>(xhat), xhat_add ? kPostAdd : kPostNone,
+                                  post);
     if (rc != NC_OK) return rc;
     const int rs = inv_rows<FH, FW>(hout);
     const size_t lds = linv_lds_bytes<FH, FW, kNT>(rs);
@@ -383,9 +397,21 @@ int nc_large_filter_spectrum_bwd(hipStream_t st, int M, int kh, int kw, int fh, 
 }
 
 int nc_large_fftconv_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout,
-                         int ph, int pw, int fh, int fw, const float* x, const float* ghat,
-                         float* z, float* xhat) {
-#define NC_CALL(A, Bv) conv_fwd<A, Bv>(st, B, M, hin, win, hout, wout, ph, pw, x, ghat, z, xhat)
+                         int ph, int pw, int fh, int fw, const float* x, const float* xhat_add,
+                         const float* ghat, float* z, float* xhat) {
+#define NC_CALL(A, Bv) \
+    conv_fwd<A, Bv>(st, B, M, hin, win, hout, wout, ph, pw, x, xhat_add, ghat, z, xhat)
+    NC_DISPATCH_LARGE(fh, fw, NC_CALL);
+#undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
+}
+
+int nc_large_plane_spectrum(hipStream_t st, int nplanes, int hin, int win, int fh, int fw, int sh,
+                            int sw, const float* x, float* xhat) {
+    const SpecPost post{nullptr, sh, sw};
+#define NC_CALL(A, Bv)                                                                       \
+    rfft2_planes<A, Bv>(st, nplanes, hin, win, (size_t)hin * win, false, x,                \
+                        reinterpret_cast<cpx*>(xhat), kPostShift, post)
     NC_DISPATCH_LARGE(fh, fw, NC_CALL);
 #undef NC_CALL
     return NC_ERR_UNSUPPORTED;

@@ -38,6 +38,8 @@ _SIGS = {
     "nc_filter_spectrum_fwd": (I, [P, I, I, I, I, I, P, P]),
     "nc_filter_spectrum_bwd": (I, [P, I, I, I, I, I, I, I, P, P, I, I]),
     "nc_fftconv_fwd": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, P]),
+    "nc_fftconv_fwd_ex": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, P, P]),
+    "nc_plane_spectrum": (I, [P, I, I, I, I, I, I, I, P, P]),
     "nc_fftconv_bwd_workspace_size": (SZ, [I, I, I, I]),
     "nc_fftconv_bwd": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, I, P, P, I, I, P, SZ]),
     "nc_fftconv_bwd_ex": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, I, P, P, I, I, P, I, P,

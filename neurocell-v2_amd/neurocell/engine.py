@@ -8,8 +8,12 @@ forward, a backward or a whole train step allocates nothing and issues no memset
 capture it in a HIP graph (``torch.cuda.CUDAGraph``) and replay it.
 
 Forward (pure ROI + hoisted border theorem, propagator.py:1-9, 343-682):
-    codd fusion -> filter spectrum -> border conv (B=1, VALID) -> inject ->
+    codd fusion -> filter spectrum -> border-patch spectrum -> inject ->
     d-1 x [spectral conv -> hidden epilogue] -> spectral conv -> port epilogue
+The hoisted border conv's delta, added to every step t >= 1's conv output, is folded into
+those steps' correlations: the border patch's spectrum, phase-shifted from the VALID window
+onto the ROI window, is added to their cell spectra (z + delta = irfft2((xhat + phat) ghat)),
+so the epilogues see z + delta with no border term and the steps' dG carries the border's.
 Reverse: port bwd -> d x [spectral conv bwd (dx, dG in the frequency domain)
     -> hidden epilogue bwd] -> filter-spectrum bwd -> border conv bwd -> codd fusion bwd.
 The border conv's cotangent sum_{t>=1} sum_b gz_t is formed in the frequency domain by the
@@ -149,6 +153,9 @@ class StepPlan:
         self.F = fh * (fw // 2 + 1)
         self.cp = ((kh - 1) // 2, (kw - 1) // 2)
         self.Hp, self.Wp = h + kh - 1, w + kw - 1
+        # circular shift taking the border conv's VALID window (kh-1, kw-1) onto the ROI
+        # steps' window cp: the patch spectrum shifted by it joins every ROI step's spectrum
+        self.bshift = ((self.cp[0] - (kh - 1)) % fh, (self.cp[1] - (kw - 1)) % fw)
         self.chip = _abi.ChipDesc(H, W, kh, kw, M, topology.pad_h, topology.pad_w, roi_h, roi_w,
                                   r0, r1, c0, c1)
         # output port cells
@@ -221,8 +228,7 @@ class StepPlan:
         self.patch = torch.empty(self.Hp, self.Wp, **f)
         self.pp = torch.empty(3, self.P, **f)
         self.ghat = torch.empty(M, F, **c)
-        self.delta = torch.empty(M, h, w, **f)
-        self.patch_hat = torch.empty(1, F, **c)
+        self.border_hat = torch.empty(1, F, **c)  # shifted border-patch spectrum
         t0_shape = (B, self.H, self.W) if self.t0_grid else (B, h, w)
         self.x0 = torch.empty(*t0_shape, **f)
         nz = d if self.training else 1
@@ -277,9 +283,12 @@ class StepPlan:
              ptr(self.port_rc), ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
              ptr(self.patch), ptr(self.pp), None, None, None)
         call("nc_filter_spectrum_fwd", s, M, self.kh, self.kw, fh, fw, ptr(filt), ptr(self.ghat))
-        if self.d > 1:  # hoisted B=1 VALID border conv (propagator.py:362-366)
-            call("nc_fftconv_fwd", s, 1, M, self.Hp, self.Wp, h, w, self.kh - 1, self.kw - 1,
-                 fh, fw, ptr(self.patch), ptr(self.ghat), ptr(self.delta), ptr(self.patch_hat))
+        if self.d > 1:
+            # hoisted VALID border conv (propagator.py:362-366): its delta is added to every
+            # step t >= 1's correlation, so the patch spectrum (shifted onto the ROI window)
+            # joins those steps' cell spectra and their correlation yields z + delta directly
+            call("nc_plane_spectrum", s, 1, self.Hp, self.Wp, fh, fw, self.bshift[0],
+                 self.bshift[1], ptr(self.patch), ptr(self.border_hat))
         n_cells = self.x0[0].numel()
         call("nc_inject_roi", s, B, self.n_in, ptr(x_flat), n_cells, ptr(self.src), ptr(self.x0))
         for t in range(self.d):
@@ -291,17 +300,18 @@ class StepPlan:
                 call("nc_fftconv_fwd", s, B, M, self.H, self.W, h, w, self.kh - 1 + r0,
                      self.kw - 1 + c0, fh, fw, ptr(self.x0), ptr(self.ghat), ptr(z), ptr(xh))
             else:
-                call("nc_fftconv_fwd", s, B, M, h, w, h, w, self.cp[0], self.cp[1], fh, fw,
-                     ptr(self.xs[t]), ptr(self.ghat), ptr(z), ptr(xh))
-            hb = int(t > 0)
+                add = ptr(self.border_hat) if t > 0 else None
+                call("nc_fftconv_fwd_ex", s, B, M, h, w, h, w, self.cp[0], self.cp[1], fh, fw,
+                     ptr(self.xs[t]), add, ptr(self.ghat), ptr(z), ptr(xh))
+            # z already holds z + delta: the epilogues run without their border term
             if not last:
-                call("nc_epilogue_fwd", s, B, M, h, w, self.act, self.slope, hb, ptr(z),
-                     ptr(self.delta), ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
-                     ptr(self.xs[t + 1]), ptr(self.mean[t]), ptr(self.rstd[t]),
-                     ptr(self.ws_epi), self.ws_epi.numel() * 4)
+                call("nc_epilogue_fwd", s, B, M, h, w, self.act, self.slope, 0, ptr(z), None,
+                     ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi), ptr(self.xs[t + 1]),
+                     ptr(self.mean[t]), ptr(self.rstd[t]), ptr(self.ws_epi),
+                     self.ws_epi.numel() * 4)
             else:
-                call("nc_port_fwd", s, B, M, h, w, hb, self.fact, self.fslope, self.P,
-                     ptr(self.port_idx), ptr(z), ptr(self.delta), ptr(self.pp), ptr(self.out),
+                call("nc_port_fwd", s, B, M, h, w, 0, self.fact, self.fslope, self.P,
+                     ptr(self.port_idx), ptr(z), None, ptr(self.pp), ptr(self.out),
                      ptr(self.zo), ptr(self.mean[t]), ptr(self.rstd[t]), ptr(self.pre),
                      ptr(self.ws_epi), self.ws_epi.numel() * 4)
         return self.out
@@ -319,9 +329,8 @@ class StepPlan:
         ws_ep, n_ep = ptr(self.ws_epi), self.ws_epi.numel() * 4
         ws_fc, n_fc = ptr(self.ws_fc), self.ws_fc.numel() * 4
         t = d - 1
-        hb = int(d > 1)
-        call("nc_port_bwd", s, B, M, h, w, hb, self.fact, self.fslope, self.P, ptr(self.port_idx),
-             ptr(self.zs[t]), ptr(self.delta), ptr(self.pp), ptr(self.zo), ptr(self.mean[t]),
+        call("nc_port_bwd", s, B, M, h, w, 0, self.fact, self.fslope, self.P, ptr(self.port_idx),
+             ptr(self.zs[t]), None, ptr(self.pp), ptr(self.zo), ptr(self.mean[t]),
              ptr(self.rstd[t]), ptr(self.pre), ptr(g_out), ptr(self.gz), None, ptr(self.gpp), 0,
              ws_ep, n_ep)
         first_epi = True
@@ -346,9 +355,8 @@ class StepPlan:
             if t == 0:
                 break
             te = t - 1
-            hbe = int(te > 0)
-            call("nc_epilogue_bwd", s, B, M, h, w, self.act, self.slope, hbe, ptr(self.zs[te]),
-                 ptr(self.delta), ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
+            call("nc_epilogue_bwd", s, B, M, h, w, self.act, self.slope, 0, ptr(self.zs[te]),
+                 None, ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
                  ptr(self.mean[te]), ptr(self.rstd[te]), ptr(gy), ptr(self.gz),
                  None, ptr(self.gw), ptr(self.gs), ptr(self.gb), int(not first_epi), 1, ws_ep,
                  n_ep)
@@ -358,11 +366,12 @@ class StepPlan:
             call("nc_filter_spectrum_bwd", s, M, self.kh, self.kw, fh, fw, self.cp[0],
                  self.cp[1], ptr(self.dghat), ptr(g_filt), 0, 0)
         g_patch = None
-        if d > 1:  # border conv reverse (same VALID shift as the full-grid t=0 step)
+        if d > 1:
+            # border conv reverse: the patch gradient from the cotangent spectra (its dG came
+            # with the ROI steps' dghat, through their border-shifted cell spectra)
             call("nc_fftconv_bwd_hat", s, M, self.Hp, self.Wp, self.kh - 1, self.kw - 1, fh, fw,
-                 ptr(self.gdelta_hat), ptr(self.patch_hat), ptr(self.ghat), ptr(self.gpatch),
-                 ptr(self.dghat_v), valid_acc, 0, ws_fc, n_fc)
-            valid_acc = 1
+                 ptr(self.gdelta_hat), None, ptr(self.ghat), ptr(self.gpatch), None, 0, 0,
+                 ws_fc, n_fc)
             g_patch = ptr(self.gpatch)
         if valid_acc:
             call("nc_filter_spectrum_bwd", s, M, self.kh, self.kw, fh, fw, self.kh - 1,

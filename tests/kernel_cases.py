@@ -178,6 +178,58 @@ def case_border_conv(be, M=4, h=12, w=10, kh=7, kw=5, FH=32, FW=16, seed=1):
             "dpatch_hat": rel_l2(be.get(gp2), gpr), "dG_hat": rel_l2(be.get(gf2)[:, 0], ggr)}
 
 
+def case_border_fold(be, B=3, M=4, h=12, w=10, kh=7, kw=5, FH=32, FW=16, seed=5):
+    """The border conv folded into a SAME-ROI correlation: xhat_add = the patch spectrum
+    shifted onto the ROI window (nc_plane_spectrum), its reverse through nc_fftconv_bwd_ex
+    (dG of both terms, the cotangent spectrum sum) and nc_fftconv_bwd_hat (patch gradient)."""
+    rng = np.random.default_rng(seed)
+    L, s = be.lib, be.stream()
+    ph, pw = (kh - 1) // 2, (kw - 1) // 2
+    Hp, Wp = h + kh - 1, w + kw - 1
+    sh, sw = (ph - (kh - 1)) % FH, (pw - (kw - 1)) % FW
+    x = rng.normal(size=(B, h, w)).astype(np.float32)
+    patch = rng.normal(size=(1, Hp, Wp)).astype(np.float32)
+    g = rng.normal(size=(M, 1, kh, kw)).astype(np.float32)
+    gz = rng.normal(size=(B, M, h, w)).astype(np.float32)
+    ghat = be.zeros((M, FH, FW // 2 + 1, 2))
+    _ok(be, L.nc_filter_spectrum_fwd(s, M, kh, kw, FH, FW, be.ptr(be.put(g)), be.ptr(ghat)),
+        "spec")
+    padd = be.zeros((1, FH, FW // 2 + 1, 2))
+    _ok(be, L.nc_plane_spectrum(s, 1, Hp, Wp, FH, FW, sh, sw, be.ptr(be.put(patch)),
+                                be.ptr(padd)), "plane_spectrum")
+    z = be.zeros((B, M, h, w))
+    xhat = be.zeros((B, FH, FW // 2 + 1, 2))
+    _ok(be, L.nc_fftconv_fwd_ex(s, B, M, h, w, h, w, ph, pw, FH, FW, be.ptr(be.put(x)),
+                                be.ptr(padd), be.ptr(ghat), be.ptr(z), be.ptr(xhat)), "fwd_ex")
+    ws = be.zeros((L.nc_fftconv_bwd_workspace_size(B, M, FH, FW) // 4 + 1,))
+    nb = ws.nbytes if hasattr(ws, "nbytes") else ws.numel() * 4
+    dx = be.zeros((B, h, w))
+    dgh = be.zeros((M, FH, FW // 2 + 1, 2))
+    ssum = be.zeros((M, FH, FW // 2 + 1, 2))
+    _ok(be, L.nc_fftconv_bwd_ex(s, B, M, h, w, h, w, ph, pw, FH, FW, be.ptr(be.put(gz)),
+                                be.ptr(xhat), be.ptr(ghat), 1, be.ptr(dx), be.ptr(dgh), 0, 0,
+                                be.ptr(ssum), 0, be.ptr(ws), nb), "bwd_ex")
+    gf = be.zeros((M, 1, kh, kw))
+    _ok(be, L.nc_filter_spectrum_bwd(s, M, kh, kw, FH, FW, ph, pw, be.ptr(dgh), be.ptr(gf), 0,
+                                     0), "specbwd")
+    gp = be.zeros((1, Hp, Wp))
+    _ok(be, L.nc_fftconv_bwd_hat(s, M, Hp, Wp, kh - 1, kw - 1, FH, FW, be.ptr(ssum), None,
+                                 be.ptr(ghat), be.ptr(gp), None, 0, 0, be.ptr(ws), nb), "bwd_hat")
+    # references: the shifted spectrum from NumPy's rfft2 of the rolled plane; the rest from
+    # brute-force correlations of the two terms
+    grid = np.zeros((FH, FW))
+    grid[:Hp, :Wp] = patch[0]
+    shifted = np.fft.rfft2(np.roll(grid, (sh, sw), axis=(0, 1)))
+    gk = g[:, 0]
+    delta = O.conv2d_direct(patch, gk, (0, 0))                       # (1, M, h, w)
+    dxr, dgr = O.conv2d_bwd_direct(gz, x, gk, (ph, pw))
+    gpr, dgb = O.conv2d_bwd_direct(gz.astype(np.float64).sum(0, keepdims=True), patch, gk, (0, 0))
+    return {"shifted_spectrum": rel_l2(_cplx(be.get(padd))[0], shifted),
+            "z": rel_l2(be.get(z), O.conv2d_direct(x, gk, (ph, pw)) + delta),
+            "dx": rel_l2(be.get(dx), dxr), "dG": rel_l2(be.get(gf)[:, 0], dgr + dgb),
+            "dpatch": rel_l2(be.get(gp), gpr)}
+
+
 def case_epilogue(be, B=3, M=5, h=10, w=12, act="tanh", has_border=1, seed=2):
     """Hidden-step epilogue forward/backward (single-pass N <= 8192, tiled above)."""
     rng = np.random.default_rng(seed)

@@ -6,7 +6,8 @@ import ctypes
 import pytest
 
 from kernel_cases import (CODD_CASES, TOL, HostBackend, case_adaptive, case_border_conv,
-                          case_codd, case_epilogue, case_fftconv, case_helpers, case_port)
+                          case_border_fold, case_codd, case_epilogue, case_fftconv, case_helpers,
+                          case_port)
 
 
 @pytest.fixture(scope="module")
@@ -47,6 +48,12 @@ def test_fftconv_large(be, B, M, FH, FW, hin, win, kh, kw):
     (128, 64, 60, 30, 31, 13)])  # workgroup transforms
 def test_border_conv(be, FH, FW, h, w, kh, kw):
     _assert_small(case_border_conv(be, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW))
+
+
+@pytest.mark.parametrize("FH,FW,h,w,kh,kw", [
+    (32, 16, 12, 10, 7, 5), (64, 64, 40, 50, 23, 13), (128, 64, 60, 30, 31, 13)])
+def test_border_fold(be, FH, FW, h, w, kh, kw):
+    _assert_small(case_border_fold(be, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW))
 
 
 @pytest.mark.parametrize("shape", [(2, 3, 10, 12, "tanh", 1), (2, 3, 20, 40, "leaky_relu", 0),
