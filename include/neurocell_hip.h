@@ -155,6 +155,32 @@ int nc_fftconv_fwd_ex(void* stream, int B, int M, int hin, int win, int hout, in
 int nc_plane_spectrum(void* stream, int nplanes, int hin, int win, int fft_h, int fft_w,
                       int shift_h, int shift_w, const float* x, float* xhat);
 
+/* One job of nc_plane_spectra: the half-spectra of nplanes real (hin, win) planes. */
+typedef struct nc_spectrum_job {
+    const float* x;       /* (nplanes, hin, win) real planes */
+    float* xhat;          /* (nplanes, fft_h, fft_w/2+1) complex out */
+    const float* add;     /* NULL, or one (fft_h, fft_w/2+1) spectrum added to each plane's */
+    int nplanes, hin, win;
+    int flip;             /* planes read rotated by 180 degrees: the filter spectra */
+    int shift_h, shift_w; /* circular shift on the grid, as nc_plane_spectrum; 0 for none */
+} nc_spectrum_job;
+
+/*
+ * Up to 4 independent spectrum jobs in one call: each job is nc_filter_spectrum_fwd (flip),
+ * nc_plane_spectrum (shift), the spectra step of nc_fftconv_fwd_ex (add) or a plain rfft2 -
+ * at most one of flip / add / shift per job.  On the 64-wide lane-pair grids all jobs run in
+ * one launch.  No counterpart in the reference (which computes each spectrum in its own op).
+ */
+int nc_plane_spectra(void* stream, int fft_h, int fft_w, int n_jobs, const nc_spectrum_job* jobs);
+
+/*
+ * The correlation step of nc_fftconv_fwd from given cell spectra: z (B, M, hout, wout) =
+ * irfft2(xhat_b * ghat_m)[pad_h : pad_h+hout, pad_w : pad_w+wout] (kernels_pallas.py:
+ * 1779-1791), xhat (B, fft_h, fft_w/2+1) complex as nc_fftconv_fwd writes it.
+ */
+int nc_spectral_correlate(void* stream, int B, int M, int hout, int wout, int pad_h, int pad_w,
+                          int fft_h, int fft_w, const float* xhat, const float* ghat, float* z);
+
 /* Workspace bytes needed by nc_fftconv_bwd for these shapes. */
 size_t nc_fftconv_bwd_workspace_size(int B, int M, int fft_h, int fft_w);
 

@@ -23,6 +23,13 @@ int nc_large_fftconv_fwd(hipStream_t st, int B, int M, int hin, int win, int hou
 int nc_large_plane_spectrum(hipStream_t st, int nplanes, int hin, int win, int fft_h, int fft_w,
                             int shift_h, int shift_w, const float* x, float* xhat);
 
+struct nc_spectrum_job;
+int nc_large_plane_spectra(hipStream_t st, int fft_h, int fft_w, int n_jobs,
+                           const nc_spectrum_job* jobs);
+
+int nc_large_correlate(hipStream_t st, int B, int M, int hout, int wout, int pad_h, int pad_w,
+                       int fft_h, int fft_w, const float* xhat, const float* ghat, float* z);
+
 size_t nc_large_fftconv_bwd_ws(int B, int M, int fft_h, int fft_w);
 
 int nc_large_fftconv_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout,

@@ -700,15 +700,11 @@ int launch_rfft2(hipStream_t st, int nplanes, int hin, int win, bool flip, const
     return NC_OK;
 }
 
+// z_bm = irfft2(xhat_b * ghat_m), the (hout, wout) window from (ph, pw).
 template <int FH, int FW>
-int launch_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph,
-               int pw, const float* x, const float* xhat_add, const float* ghat, float* z,
-               float* xhat) {
+int launch_corr(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw,
+                const float* xhat, const float* ghat, float* z) {
     using W = WGeo<FH, FW>;
-    const SpecPost post{reinterpret_cast<const cpx*>(xhat_add), 0, 0};
-    int rc = launch_rfft2<FH, FW>(st, B, hin, win, false, x, reinterpret_cast<cpx*>(xhat),
-                                  xhat_add ? kPostAdd : kPostNone, post);
-    if (rc != NC_OK) return rc;
     if constexpr (pair_grid<FH, FW>()) {
         const PLds l(hout, PGeo<FH, FW>::PITCH, FW, FH, true);
         lds_limit(k_pconv_fwd<FH, FW>, l.bytes);
@@ -726,6 +722,89 @@ int launch_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wou
                        vec_ok(z, (size_t)hout * wout),
                        reinterpret_cast<const cpx*>(xhat), reinterpret_cast<const cpx*>(ghat), z);
     NC_CHECK_LAUNCH();
+    return NC_OK;
+}
+
+template <int FH, int FW>
+int launch_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph,
+               int pw, const float* x, const float* xhat_add, const float* ghat, float* z,
+               float* xhat) {
+    const SpecPost post{reinterpret_cast<const cpx*>(xhat_add), 0, 0};
+    int rc = launch_rfft2<FH, FW>(st, B, hin, win, false, x, reinterpret_cast<cpx*>(xhat),
+                                  xhat_add ? kPostAdd : kPostNone, post);
+    if (rc != NC_OK) return rc;
+    return launch_corr<FH, FW>(st, B, M, hout, wout, ph, pw, xhat, ghat, z);
+}
+
+// Several independent spectrum jobs (nc_plane_spectra) in one launch: block g runs plane
+// g - start[q] of the job q whose range holds g; each job's kind picks the transform variant.
+constexpr int kMaxSpecJobs = 4;
+struct SpecJobs {
+    const float* x[kMaxSpecJobs];
+    cpx* out[kMaxSpecJobs];
+    SpecPost post[kMaxSpecJobs];
+    int hin[kMaxSpecJobs], win[kMaxSpecJobs], vec[kMaxSpecJobs], kind[kMaxSpecJobs];
+    int start[kMaxSpecJobs + 1];
+    int n;
+};
+enum { kJobPlain = 0, kJobFlip = 1, kJobAdd = 2, kJobShift = 3 };
+
+template <int FH, int FW>
+__global__ __launch_bounds__(64) void k_pspectra(SpecJobs J) {
+    HIP_DYNAMIC_SHARED(float, lds)
+    const int g = blockIdx.x;
+    int q = 0;
+    while (q + 1 < J.n && g >= J.start[q + 1]) ++q;
+    const int i = g - J.start[q], hin = J.hin[q], win = J.win[q], vec = J.vec[q];
+    const float* src = J.x[q] + (size_t)i * hin * win;
+    cpx* o = J.out[q] + (size_t)i * PGeo<FH, FW>::F;
+    switch (J.kind[q]) {
+        case kJobFlip:
+            prfft2_plane<FH, FW, true, kPostNone>(src, hin, win, vec, lds, o, J.post[q]);
+            break;
+        case kJobAdd:
+            prfft2_plane<FH, FW, false, kPostAdd>(src, hin, win, vec, lds, o, J.post[q]);
+            break;
+        case kJobShift:
+            prfft2_plane<FH, FW, false, kPostShift>(src, hin, win, vec, lds, o, J.post[q]);
+            break;
+        default:
+            prfft2_plane<FH, FW, false, kPostNone>(src, hin, win, vec, lds, o, J.post[q]);
+    }
+}
+
+template <int FH, int FW>
+int launch_spectra(hipStream_t st, int n, const nc_spectrum_job* jobs) {
+    if constexpr (pair_grid<FH, FW>()) {
+        SpecJobs J{};
+        J.n = n;
+        size_t lds = 0;
+        for (int q = 0; q < n; ++q) {
+            const nc_spectrum_job& j = jobs[q];
+            J.x[q] = j.x;
+            J.out[q] = reinterpret_cast<cpx*>(j.xhat);
+            J.post[q] = SpecPost{reinterpret_cast<const cpx*>(j.add), j.shift_h, j.shift_w};
+            J.hin[q] = j.hin;
+            J.win[q] = j.win;
+            J.vec[q] = vec_ok(j.x, (size_t)j.hin * j.win);
+            J.kind[q] = j.flip ? kJobFlip : j.add ? kJobAdd : (j.shift_h | j.shift_w) ? kJobShift
+                                                                                       : kJobPlain;
+            J.start[q + 1] = J.start[q] + j.nplanes;
+            lds = std::max(lds, PLds(j.hin, PGeo<FH, FW>::PITCH, FW, FH, false).bytes);
+        }
+        lds_limit(k_pspectra<FH, FW>, lds);
+        hipLaunchKernelGGL((k_pspectra<FH, FW>), dim3(J.start[n]), dim3(64), lds, st, J);
+        NC_CHECK_LAUNCH();
+        return NC_OK;
+    }
+    for (int q = 0; q < n; ++q) {  // wavefront grids: one launch per job
+        const nc_spectrum_job& j = jobs[q];
+        const SpecPost post{reinterpret_cast<const cpx*>(j.add), j.shift_h, j.shift_w};
+        const int kind = j.add ? kPostAdd : (j.shift_h | j.shift_w) ? kPostShift : kPostNone;
+        const int rc = launch_rfft2<FH, FW>(st, j.nplanes, j.hin, j.win, j.flip != 0, j.x,
+                                            reinterpret_cast<cpx*>(j.xhat), kind, post);
+        if (rc != NC_OK) return rc;
+    }
     return NC_OK;
 }
 
@@ -954,6 +1033,40 @@ int nc_plane_spectrum(void* stream, int nplanes, int hin, int win, int fft_h, in
 #define NC_CALL(A, Bv)                                                                   \
     launch_rfft2<A, Bv>(st, nplanes, hin, win, false, x, reinterpret_cast<cpx*>(xhat), \
                         kPostShift, post)
+    NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
+#undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
+}
+
+int nc_plane_spectra(void* stream, int fft_h, int fft_w, int n_jobs, const nc_spectrum_job* jobs) {
+    if (n_jobs <= 0 || n_jobs > kMaxSpecJobs || !jobs) return NC_ERR_INVALID_ARGUMENT;
+    for (int q = 0; q < n_jobs; ++q) {
+        const nc_spectrum_job& j = jobs[q];
+        const int ops = (j.flip != 0) + (j.add != nullptr) + ((j.shift_h | j.shift_w) != 0);
+        if (!j.x || !j.xhat || j.nplanes <= 0 || j.hin <= 0 || j.win <= 0 || j.hin > fft_h ||
+            j.win > fft_w || j.shift_h < 0 || j.shift_w < 0 || j.shift_h >= fft_h ||
+            j.shift_w >= fft_w || ops > 1)
+            return NC_ERR_INVALID_ARGUMENT;
+    }
+    hipStream_t st = nc_stream(stream);
+    if (nc_large_grid(fft_h, fft_w))
+        return nc_large_plane_spectra(st, fft_h, fft_w, n_jobs, jobs);
+    if (!pow2_ok(fft_h) || !pow2_ok(fft_w)) return NC_ERR_UNSUPPORTED;
+#define NC_CALL(A, Bv) launch_spectra<A, Bv>(st, n_jobs, jobs)
+    NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
+#undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
+}
+
+int nc_spectral_correlate(void* stream, int B, int M, int hout, int wout, int pad_h, int pad_w,
+                          int fft_h, int fft_w, const float* xhat, const float* ghat, float* z) {
+    int rc = fftconv_check(B, M, 1, 1, hout, wout, pad_h, pad_w, fft_h, fft_w);
+    if (rc != NC_OK) return rc;
+    if (!xhat || !ghat || !z) return NC_ERR_INVALID_ARGUMENT;
+    hipStream_t st = nc_stream(stream);
+    if (nc_large_grid(fft_h, fft_w))
+        return nc_large_correlate(st, B, M, hout, wout, pad_h, pad_w, fft_h, fft_w, xhat, ghat, z);
+#define NC_CALL(A, Bv) launch_corr<A, Bv>(st, B, M, hout, wout, pad_h, pad_w, xhat, ghat, z)
     NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
 #undef NC_CALL
     return NC_ERR_UNSUPPORTED;

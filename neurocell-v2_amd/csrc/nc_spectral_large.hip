@@ -301,6 +301,10 @@ int spec_bwd(hipStream_t st, int M, int kh, int kw, int sh, int sw, const float*
 }
 
 template <int FH, int FW>
+int corr(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw, const float* xhat,
+         const float* ghat, float* z);
+
+template <int FH, int FW>
 int conv_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph, int pw,
              const float* x, const float* xhat_add, const float* ghat, float* z, float* xhat) {
     const SpecPost post{reinterpret_cast<const cpx*>(xhat_add), 0, 0};
@@ -308,6 +312,12 @@ int conv_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout,
                                   reinterpret_cast<cpx*>(xhat), xhat_add ? kPostAdd : kPostNone,
                                   post);
     if (rc != NC_OK) return rc;
+    return corr<FH, FW>(st, B, M, hout, wout, ph, pw, xhat, ghat, z);
+}
+
+template <int FH, int FW>
+int corr(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw, const float* xhat,
+         const float* ghat, float* z) {
     const int rs = inv_rows<FH, FW>(hout);
     const size_t lds = linv_lds_bytes<FH, FW, kNT>(rs);
     set_lds(k_linv_conv<FH, FW>, lds);
@@ -401,6 +411,33 @@ int nc_large_fftconv_fwd(hipStream_t st, int B, int M, int hin, int win, int hou
                          const float* ghat, float* z, float* xhat) {
 #define NC_CALL(A, Bv) \
     conv_fwd<A, Bv>(st, B, M, hin, win, hout, wout, ph, pw, x, xhat_add, ghat, z, xhat)
+    NC_DISPATCH_LARGE(fh, fw, NC_CALL);
+#undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
+}
+
+static int large_spectra_job(hipStream_t st, int fh, int fw, const nc_spectrum_job& j) {
+    const SpecPost post{reinterpret_cast<const cpx*>(j.add), j.shift_h, j.shift_w};
+    const int kind = j.add ? kPostAdd : (j.shift_h | j.shift_w) ? kPostShift : kPostNone;
+#define NC_CALL(A, Bv)                                                                      \
+    rfft2_planes<A, Bv>(st, j.nplanes, j.hin, j.win, (size_t)j.hin * j.win, j.flip != 0, j.x, \
+                        reinterpret_cast<cpx*>(j.xhat), kind, post)
+    NC_DISPATCH_LARGE(fh, fw, NC_CALL);
+#undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
+}
+
+int nc_large_plane_spectra(hipStream_t st, int fh, int fw, int n, const nc_spectrum_job* jobs) {
+    for (int q = 0; q < n; ++q) {  // one launch per job
+        const int rc = large_spectra_job(st, fh, fw, jobs[q]);
+        if (rc != NC_OK) return rc;
+    }
+    return NC_OK;
+}
+
+int nc_large_correlate(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw, int fh,
+                       int fw, const float* xhat, const float* ghat, float* z) {
+#define NC_CALL(A, Bv) corr<A, Bv>(st, B, M, hout, wout, ph, pw, xhat, ghat, z)
     NC_DISPATCH_LARGE(fh, fw, NC_CALL);
 #undef NC_CALL
     return NC_ERR_UNSUPPORTED;

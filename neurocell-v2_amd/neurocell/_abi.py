@@ -28,6 +28,22 @@ class ChipDesc(C.Structure):
         "H", "W", "kh", "kw", "M", "pad_h", "pad_w", "roi_h", "roi_w", "r0", "r1", "c0", "c1")]
 
 
+class SpectrumJob(C.Structure):
+    """Mirror of ``nc_spectrum_job``."""
+    _fields_ = [("x", C.c_void_p), ("xhat", C.c_void_p), ("add", C.c_void_p),
+                ("nplanes", C.c_int32), ("hin", C.c_int32), ("win", C.c_int32),
+                ("flip", C.c_int32), ("shift_h", C.c_int32), ("shift_w", C.c_int32)]
+
+
+def spectrum_jobs(*jobs):
+    """A ctypes array of SpectrumJob from (x, xhat, add, nplanes, hin, win, flip, sh, sw)
+    tuples (pointers as ints or c_void_p / None)."""
+    arr = (SpectrumJob * len(jobs))()
+    for i, j in enumerate(jobs):
+        arr[i] = SpectrumJob(*j)
+    return arr
+
+
 _SIGS = {
     "nc_version": (I, []),
     "nc_strerror": (C.c_char_p, [I]),
@@ -40,6 +56,8 @@ _SIGS = {
     "nc_fftconv_fwd": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, P]),
     "nc_fftconv_fwd_ex": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, P, P]),
     "nc_plane_spectrum": (I, [P, I, I, I, I, I, I, I, P, P]),
+    "nc_plane_spectra": (I, [P, I, I, I, C.POINTER(SpectrumJob)]),
+    "nc_spectral_correlate": (I, [P, I, I, I, I, I, I, I, I, P, P, P]),
     "nc_fftconv_bwd_workspace_size": (SZ, [I, I, I, I]),
     "nc_fftconv_bwd": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, I, P, P, I, I, P, SZ]),
     "nc_fftconv_bwd_ex": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, I, P, P, I, I, P, I, P,

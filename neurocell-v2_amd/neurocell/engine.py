@@ -282,27 +282,36 @@ class StepPlan:
              inv_tau, active_threshold, int(self.hard_pin_io), self.act, self.slope, self.P,
              ptr(self.port_rc), ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
              ptr(self.patch), ptr(self.pp), None, None, None)
-        call("nc_filter_spectrum_fwd", s, M, self.kh, self.kw, fh, fw, ptr(filt), ptr(self.ghat))
+        n_cells = self.x0[0].numel()
+        call("nc_inject_roi", s, B, self.n_in, ptr(x_flat), n_cells, ptr(self.src), ptr(self.x0))
+        # the independent spectra in one call: filter spectra (kernels_greens.py:240-259), the
+        # border patch's and the first step's cell spectra
+        x0h, x0w = (self.H, self.W) if self.t0_grid else (h, w)
+        xh0 = self.xhat[0]
+        jobs = [(_addr(filt), _addr(self.ghat), None, M, self.kh, self.kw, 1, 0, 0),
+                (_addr(self.x0), _addr(xh0), None, B, x0h, x0w, 0, 0, 0)]
         if self.d > 1:
             # hoisted VALID border conv (propagator.py:362-366): its delta is added to every
             # step t >= 1's correlation, so the patch spectrum (shifted onto the ROI window)
             # joins those steps' cell spectra and their correlation yields z + delta directly
-            call("nc_plane_spectrum", s, 1, self.Hp, self.Wp, fh, fw, self.bshift[0],
-                 self.bshift[1], ptr(self.patch), ptr(self.border_hat))
-        n_cells = self.x0[0].numel()
-        call("nc_inject_roi", s, B, self.n_in, ptr(x_flat), n_cells, ptr(self.src), ptr(self.x0))
+            jobs.append((_addr(self.patch), _addr(self.border_hat), None, 1, self.Hp, self.Wp, 0,
+                         self.bshift[0], self.bshift[1]))
+        call("nc_plane_spectra", s, fh, fw, len(jobs), _abi.spectrum_jobs(*jobs))
         for t in range(self.d):
             last = t == self.d - 1
             z = self.zs[t if self.training else 0]
             xh = self.xhat[t if self.training else 0]
-            if t == 0 and self.t0_grid:
-                r0, _, c0, _ = self.bbox
-                call("nc_fftconv_fwd", s, B, M, self.H, self.W, h, w, self.kh - 1 + r0,
-                     self.kw - 1 + c0, fh, fw, ptr(self.x0), ptr(self.ghat), ptr(z), ptr(xh))
+            if t == 0:
+                if self.t0_grid:  # VALID full-grid step: its own spectral shift
+                    r0, _, c0, _ = self.bbox
+                    p0 = (self.kh - 1 + r0, self.kw - 1 + c0)
+                else:
+                    p0 = self.cp
+                call("nc_spectral_correlate", s, B, M, h, w, p0[0], p0[1], fh, fw, ptr(xh0),
+                     ptr(self.ghat), ptr(z))
             else:
-                add = ptr(self.border_hat) if t > 0 else None
                 call("nc_fftconv_fwd_ex", s, B, M, h, w, h, w, self.cp[0], self.cp[1], fh, fw,
-                     ptr(self.xs[t]), add, ptr(self.ghat), ptr(z), ptr(xh))
+                     ptr(self.xs[t]), ptr(self.border_hat), ptr(self.ghat), ptr(z), ptr(xh))
             # z already holds z + delta: the epilogues run without their border term
             if not last:
                 call("nc_epilogue_fwd", s, B, M, h, w, self.act, self.slope, 0, ptr(z), None,
@@ -392,6 +401,11 @@ class StepPlan:
         call("nc_mse_loss", stream_ptr(), self.B * self.P, ptr(self.out), ptr(target),
              ptr(loss), ptr(self.g_out))
         return loss
+
+
+def _addr(t: torch.Tensor) -> int:
+    """Device address of a contiguous device tensor (for the ABI's job structs)."""
+    return ptr(t).value
 
 
 def _abi_size(name: str, *args) -> int:

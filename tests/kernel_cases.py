@@ -230,6 +230,44 @@ def case_border_fold(be, B=3, M=4, h=12, w=10, kh=7, kw=5, FH=32, FW=16, seed=5)
             "dpatch": rel_l2(be.get(gp), gpr)}
 
 
+def case_plane_spectra(be, B=3, M=4, h=12, w=10, kh=7, kw=5, FH=32, FW=16, seed=6):
+    """nc_plane_spectra with all four job kinds in one call (filter spectra, a shifted plane, a
+    plain and an added-to cell spectrum) and nc_spectral_correlate on its outputs."""
+    rng = np.random.default_rng(seed)
+    L, s = be.lib, be.stream()
+    ph, pw = (kh - 1) // 2, (kw - 1) // 2
+    Hp, Wp = h + kh - 1, w + kw - 1
+    sh, sw = 3 % FH, (FW - 2) % FW
+    x = rng.normal(size=(B, h, w)).astype(np.float32)
+    patch = rng.normal(size=(1, Hp, Wp)).astype(np.float32)
+    g = rng.normal(size=(M, 1, kh, kw)).astype(np.float32)
+    A = (rng.normal(size=(FH, FW // 2 + 1)) + 1j * rng.normal(size=(FH, FW // 2 + 1)))
+    Ad = be.put(np.stack([A.real, A.imag], -1))
+    xd, pd, gd = be.put(x), be.put(patch), be.put(g)
+    ghat = be.zeros((M, FH, FW // 2 + 1, 2))
+    phat = be.zeros((1, FH, FW // 2 + 1, 2))
+    xhat = be.zeros((B, FH, FW // 2 + 1, 2))
+    xhat2 = be.zeros((B, FH, FW // 2 + 1, 2))
+    a = lambda t: be.ptr(t).value
+    jobs = _abi.spectrum_jobs((a(gd), a(ghat), None, M, kh, kw, 1, 0, 0),
+                              (a(pd), a(phat), None, 1, Hp, Wp, 0, sh, sw),
+                              (a(xd), a(xhat), None, B, h, w, 0, 0, 0),
+                              (a(xd), a(xhat2), a(Ad), B, h, w, 0, 0, 0))
+    _ok(be, L.nc_plane_spectra(s, FH, FW, 4, jobs), "plane_spectra")
+    z = be.zeros((B, M, h, w))
+    _ok(be, L.nc_spectral_correlate(s, B, M, h, w, ph, pw, FH, FW, be.ptr(xhat), be.ptr(ghat),
+                                    be.ptr(z)), "correlate")
+    grid = np.zeros((FH, FW))
+    grid[:Hp, :Wp] = patch[0]
+    xs = np.fft.rfft2(x.astype(np.float64), s=(FH, FW))
+    return {"ghat": rel_l2(_cplx(be.get(ghat)), O.filter_spectrum(g[:, 0], (FH, FW))),
+            "shifted": rel_l2(_cplx(be.get(phat))[0],
+                              np.fft.rfft2(np.roll(grid, (sh, sw), axis=(0, 1)))),
+            "xhat": rel_l2(_cplx(be.get(xhat)), xs),
+            "xhat_add": rel_l2(_cplx(be.get(xhat2)), xs + A[None]),
+            "z": rel_l2(be.get(z), O.conv2d_direct(x, g[:, 0], (ph, pw)))}
+
+
 def case_epilogue(be, B=3, M=5, h=10, w=12, act="tanh", has_border=1, seed=2):
     """Hidden-step epilogue forward/backward (single-pass N <= 8192, tiled above)."""
     rng = np.random.default_rng(seed)

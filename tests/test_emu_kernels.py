@@ -7,7 +7,7 @@ import pytest
 
 from kernel_cases import (CODD_CASES, TOL, HostBackend, case_adaptive, case_border_conv,
                           case_border_fold, case_codd, case_epilogue, case_fftconv, case_helpers,
-                          case_port)
+                          case_plane_spectra, case_port)
 
 
 @pytest.fixture(scope="module")
@@ -54,6 +54,12 @@ def test_border_conv(be, FH, FW, h, w, kh, kw):
     (32, 16, 12, 10, 7, 5), (64, 64, 40, 50, 23, 13), (128, 64, 60, 30, 31, 13)])
 def test_border_fold(be, FH, FW, h, w, kh, kw):
     _assert_small(case_border_fold(be, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW))
+
+
+@pytest.mark.parametrize("FH,FW,h,w,kh,kw", [
+    (32, 16, 12, 10, 7, 5), (64, 64, 40, 50, 23, 13), (128, 64, 60, 30, 31, 13)])
+def test_plane_spectra(be, FH, FW, h, w, kh, kw):
+    _assert_small(case_plane_spectra(be, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW))
 
 
 @pytest.mark.parametrize("shape", [(2, 3, 10, 12, "tanh", 1), (2, 3, 20, 40, "leaky_relu", 0),

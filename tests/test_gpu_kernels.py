@@ -3,7 +3,8 @@ import pytest
 
 from kernel_cases import (CODD_CASES, EPILOGUE_SHAPES, PORT_SHAPES, TOL, DeviceBackend,
                           case_adaptive, case_border_conv, case_border_fold, case_codd,
-                          case_epilogue, case_fftconv, case_helpers, case_port)
+                          case_epilogue, case_fftconv, case_helpers, case_plane_spectra,
+                          case_port)
 
 pytestmark = pytest.mark.gpu
 
@@ -53,6 +54,13 @@ def test_border_conv(be, h, w, kh, kw, FH, FW):
                                                (2, 224, 224, 31, 31, 256, 256)])
 def test_border_fold(be, B, h, w, kh, kw, FH, FW):
     _assert_small(case_border_fold(be, B=B, M=16, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW))
+
+
+@pytest.mark.parametrize("B,h,w,kh,kw,FH,FW", [(3, 12, 10, 7, 5, 32, 16),
+                                               (128, 40, 50, 23, 13, 64, 64),
+                                               (2, 224, 224, 31, 31, 256, 256)])
+def test_plane_spectra(be, B, h, w, kh, kw, FH, FW):
+    _assert_small(case_plane_spectra(be, B=B, M=16, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW))
 
 
 @pytest.mark.parametrize("shape", EPILOGUE_SHAPES)
