@@ -147,6 +147,15 @@ int nc_fftconv_fwd_ex(void* stream, int B, int M, int hin, int win, int hout, in
                       const float* xhat_add, const float* ghat, float* z, float* xhat);
 
 /*
+ * nc_fftconv_fwd_ex with x given as n_parts partial planes x_parts (n_parts, B, hin, win):
+ * x = their sum in increasing order (the parts of nc_epilogue_fwd_parts).
+ */
+int nc_fftconv_fwd_parts(void* stream, int B, int M, int hin, int win, int hout, int wout,
+                         int pad_h, int pad_w, int fft_h, int fft_w, const float* x_parts,
+                         int n_parts, const float* xhat_add, const float* ghat, float* z,
+                         float* xhat);
+
+/*
  * Half-spectra (nplanes, fft_h, fft_w/2+1) complex of real (hin, win) planes placed at the
  * origin of the spectral grid and circularly shifted by (shift_h, shift_w)
  * (0 <= shift < grid): rfft2 times the phase ramp W^(kh*shift_h) W^(kw*shift_w), from exact
@@ -249,10 +258,28 @@ int nc_epilogue_fwd(void* stream, int B, int M, int h, int w, int act, float neg
                     void* ws, size_t ws_bytes);
 
 /*
+ * The number G >= 1 of partial output planes per sample that nc_epilogue_fwd_parts writes at
+ * these shapes (its workgroups split the directions into G groups at small batches).
+ */
+int nc_epilogue_fwd_partials(int B, int M, int h, int w);
+
+/*
+ * nc_epilogue_fwd leaving the direction groups' partial outputs uncombined: parts (G, B, h, w)
+ * with G = nc_epilogue_fwd_partials(B, M, h, w), whose sum over g in increasing order is out
+ * (bit for bit).  nc_fftconv_fwd_parts consumes them directly, so the combine costs no launch.
+ * No counterpart in the reference (whose epilogue is one fused op).
+ */
+int nc_epilogue_fwd_parts(void* stream, int B, int M, int h, int w, int act, float neg_slope,
+                          int has_border, const float* z, const float* delta, const float* w_eff,
+                          const float* s_eff, const float* b_roi, float* parts, float* mean,
+                          float* rstd, void* ws, size_t ws_bytes);
+
+/*
  * pallas_fused_roi_step_epilogue backward rule (kernels_pallas.py:869-1064): writes gz
  * (B,M,h,w), gdb = sum_b gz (M,h,w) when has_border and gdb is not NULL (a caller that forms
- * the border cotangent from the spectra, nc_fftconv_bwd_ex, passes NULL) and gw/gs/gb (h,w).  gw/gs/gb are overwritten, or added to when accumulate_params; gdb is
- * overwritten, or added to when accumulate_gdb (a d-step reverse pass sums both over steps).
+ * the border cotangent from the spectra, nc_fftconv_bwd_ex, passes NULL) and gw/gs/gb (h,w).
+ * gw/gs/gb are overwritten, or added to when accumulate_params; gdb is overwritten, or added
+ * to when accumulate_gdb (a d-step reverse pass sums both over steps).
  */
 int nc_epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg_slope,
                     int has_border, const float* z, const float* delta, const float* w_eff,
@@ -280,8 +307,8 @@ int nc_port_fwd(void* stream, int B, int M, int h, int w, int has_border, int fi
 /*
  * Backward of nc_port_fwd (kernels_pallas.py:1350-1504, 1538-1551): dense
  * gz = -rstd*(c1 + zhat*c2) plus rstd*g scattered at the port cells in registers; gdb =
- * sum_b gz when has_border and gdb is not NULL; gdb and g_port_params (3,P) overwritten, or added to when
- * accumulate_params.  With port_params == NULL (standardisation only, kernels_pallas.py:
+ * sum_b gz when has_border and gdb is not NULL; gdb and g_port_params (3,P) overwritten, or
+ * added to when accumulate_params.  With port_params == NULL (standardisation only, kernels_pallas.py:
  * 1350-1504) g_out is the (B,M,P) cotangent of zo and g_port_params is not touched.
  */
 int nc_port_bwd(void* stream, int B, int M, int h, int w, int has_border, int final_act,

@@ -1032,25 +1032,33 @@ size_t nc_epilogue_workspace_size(int B, int M, int h, int w) {
     return epi_ws(nullptr, B, M, h * w).bytes;
 }
 
-int nc_epilogue_fwd(void* stream, int B, int M, int h, int w, int act, float neg_slope,
-                    int has_border, const float* z, const float* delta, const float* w_eff,
-                    const float* s_eff, const float* b_roi, float* out, float* mean, float* rstd,
-                    void* ws, size_t ws_bytes) {
+int nc_epilogue_fwd_partials(int B, int M, int h, int w) {
+    if (B <= 0 || M <= 0 || h <= 0 || w <= 0) return 0;
+    return h * w <= kSingleMaxPix ? fwd_plan(B, M, h * w).G : 1;
+}
+
+// parts != nullptr: the G direction-group partial outputs go there, uncombined.
+static int epilogue_fwd(void* stream, int B, int M, int h, int w, int act, float neg_slope,
+                        int has_border, const float* z, const float* delta, const float* w_eff,
+                        const float* s_eff, const float* b_roi, float* out, float* parts,
+                        float* mean, float* rstd, void* ws, size_t ws_bytes) {
     if (B <= 0 || M <= 0 || M > kMaxM || h <= 0 || w <= 0 || !z || !w_eff || !s_eff ||
-        !b_roi || !out || !mean || !rstd || (has_border && !delta) || act < 0 || act > 5)
+        !b_roi || !(out || parts) || !mean || !rstd || (has_border && !delta) || act < 0 ||
+        act > 5)
         return NC_ERR_INVALID_ARGUMENT;
     if (ws_bytes < nc_epilogue_workspace_size(B, M, h, w) || !ws) return NC_ERR_WORKSPACE;
     hipStream_t st = nc_stream(stream);
     const int N = h * w;
     const EpiWs e = epi_ws(ws, B, M, N);
+    if (parts) out = parts;  // a single group (or the tiled pipeline) writes the output itself
     if (N <= kSingleMaxPix) {
         const DirPlan P = fwd_plan(B, M, N);
         return dispatch_act(act, [&]<int ACT>() {
             NC_FWD_DISPATCH(P, k_epi_fwd, dim3(B, P.G), dim3(P.c.nt), 0, st, M, N, P.mpg,
                             neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, out, mean, rstd,
-                            e.fpart);
+                            parts ? parts : e.fpart);
             NC_CHECK_LAUNCH();
-            if (P.G > 1) {
+            if (P.G > 1 && !parts) {
                 const size_t n = (size_t)B * N;
                 hipLaunchKernelGGL(k_group_sum, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
                                    st, P.G, n, e.fpart, out);
@@ -1070,6 +1078,24 @@ int nc_epilogue_fwd(void* stream, int B, int M, int h, int w, int act, float neg
         NC_CHECK_LAUNCH();
         return NC_OK;
     });
+}
+
+int nc_epilogue_fwd(void* stream, int B, int M, int h, int w, int act, float neg_slope,
+                    int has_border, const float* z, const float* delta, const float* w_eff,
+                    const float* s_eff, const float* b_roi, float* out, float* mean, float* rstd,
+                    void* ws, size_t ws_bytes) {
+    if (!out) return NC_ERR_INVALID_ARGUMENT;
+    return epilogue_fwd(stream, B, M, h, w, act, neg_slope, has_border, z, delta, w_eff, s_eff,
+                        b_roi, out, nullptr, mean, rstd, ws, ws_bytes);
+}
+
+int nc_epilogue_fwd_parts(void* stream, int B, int M, int h, int w, int act, float neg_slope,
+                          int has_border, const float* z, const float* delta, const float* w_eff,
+                          const float* s_eff, const float* b_roi, float* parts, float* mean,
+                          float* rstd, void* ws, size_t ws_bytes) {
+    if (!parts) return NC_ERR_INVALID_ARGUMENT;
+    return epilogue_fwd(stream, B, M, h, w, act, neg_slope, has_border, z, delta, w_eff, s_eff,
+                        b_roi, nullptr, parts, mean, rstd, ws, ws_bytes);
 }
 
 int nc_epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg_slope,

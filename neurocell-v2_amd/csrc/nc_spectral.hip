@@ -83,10 +83,11 @@ __global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_filter_spectrum_bwd(
 // Half-spectra of nplanes real (hin x win) planes stored back to back in x (FLIP: the plane
 // is read flipped in both axes, which turns the correlation filter into a convolution
 // kernel, kernels_greens.py:240-259).  out: (nplanes, FH, FW/2+1).
-template <int FH, int FW, bool FLIP, int POST>
+template <int FH, int FW, bool FLIP, int POST, int NP>
 __global__ __launch_bounds__(64) void k_wrfft2(int nplanes, int hin, int win, int s_off, int vec,
                                                const float* __restrict__ x,
-                                               cpx* __restrict__ out, SpecPost post) {
+                                               cpx* __restrict__ out, SpecPost post,
+                                               size_t qstride, int nq) {
     using W = WGeo<FH, FW>;
     HIP_DYNAMIC_SHARED(float, lds)
     cpx* T = reinterpret_cast<cpx*>(lds);
@@ -94,8 +95,8 @@ __global__ __launch_bounds__(64) void k_wrfft2(int nplanes, int hin, int win, in
     const int lane = threadIdx.x;
     const int g0 = blockIdx.x * W::PPW;
     const int np = min(W::PPW, nplanes - g0);
-    istage<FW, W::PPW, FLIP>(x + (size_t)g0 * hin * win, (size_t)hin * win, np, hin, win,
-                             vec != 0, S);
+    istage<FW, W::PPW, FLIP, NP>(x + (size_t)g0 * hin * win, (size_t)hin * win, np, hin, win,
+                                 vec != 0, S, qstride, nq);
     __syncthreads();
     wrow_fwd<FH, FW>(S, hin, T);
     __syncthreads();
@@ -428,6 +429,15 @@ constexpr bool pair_grid() {
     return FW == 64 && (FH == 32 || FH == 64);
 }
 
+// On the 64 x 64 grid the per-sample transforms (cell spectra, dx inverses, the few-plane
+// filter and border spectra) run as workgroup-per-plane segmented transforms: with one
+// wavefront per plane a B-plane job leaves most of the chip idle and its time is one
+// wavefront's latency; the B*M-plane correlation and cotangent spectra stay lane-pair.
+template <int FH, int FW>
+constexpr bool seg_grid() {
+    return FH == 64 && FW == 64;
+}
+
 // LDS of a lane-pair plane: T (forward: `rows` + 2 rows; inverse: all fh rows) of pitch cpx,
 // sharing its space with the real-valued input or output staging, then the Nyquist staging
 // (fh cpx).
@@ -446,13 +456,14 @@ struct PLds {
 // Half-spectrum of one real (hin x win) plane src into o (FLIP: read rotated by 180 degrees),
 // each bin passed through spec_post<POST>; the calling wavefront owns the plane.  kPostAdd
 // loads the lane's added bins while the column transform runs, so no store waits on a load.
-template <int FH, int FW, bool FLIP, int POST>
+template <int FH, int FW, bool FLIP, int POST, int NP = 1>
 NC_DEV void prfft2_plane(const float* __restrict__ src, int hin, int win, int vec, float* lds,
-                         cpx* __restrict__ o, const SpecPost& post) {
+                         cpx* __restrict__ o, const SpecPost& post, size_t qstride = 0,
+                         int nq = 1) {
     using P = PGeo<FH, FW>;
     constexpr int NA = POST == kPostAdd ? P::HH : 1;
     cpx* T = reinterpret_cast<cpx*>(lds);
-    istage<FW, 1, FLIP>(src, (size_t)hin * win, 1, hin, win, vec != 0, lds);
+    istage<FW, 1, FLIP, NP>(src, (size_t)hin * win, 1, hin, win, vec != 0, lds, qstride, nq);
     __syncthreads();
     prow_fwd<FH, FW>(lds, hin, T);
     __syncthreads();
@@ -478,13 +489,15 @@ NC_DEV void prfft2_plane(const float* __restrict__ src, int hin, int win, int ve
 // Half-spectra of real (hin x win) planes (FLIP: read rotated by 180 degrees, the filter
 // spectra of kernels_greens.py:240-259), post-processed by spec_post<POST>; one wavefront per
 // plane.
-template <int FH, int FW, bool FLIP, int POST>
+template <int FH, int FW, bool FLIP, int POST, int NP>
 __global__ __launch_bounds__(64) void k_prfft2(int hin, int win, int vec,
                                                const float* __restrict__ x,
-                                               cpx* __restrict__ out, SpecPost post) {
+                                               cpx* __restrict__ out, SpecPost post,
+                                               size_t qstride, int nq) {
     HIP_DYNAMIC_SHARED(float, lds)
-    prfft2_plane<FH, FW, FLIP, POST>(x + (size_t)blockIdx.x * hin * win, hin, win, vec, lds,
-                                     out + (size_t)blockIdx.x * PGeo<FH, FW>::F, post);
+    prfft2_plane<FH, FW, FLIP, POST, NP>(x + (size_t)blockIdx.x * hin * win, hin, win, vec, lds,
+                                         out + (size_t)blockIdx.x * PGeo<FH, FW>::F, post,
+                                         qstride, nq);
 }
 
 // Backward, first stage (kernels_pallas.py:1794-1821): the half-spectrum of every cotangent
@@ -666,36 +679,59 @@ size_t bwd_ws(int B, int M) {
             2 * nc * M * W::F) * sizeof(cpx);
 }
 
-template <int FH, int FW, bool FLIP, int POST>
+template <int FH, int FW, bool FLIP, int POST, int NP>
 void launch_rfft2_k(hipStream_t st, int nplanes, int hin, int win, const float* x, cpx* out,
-                    const SpecPost& post) {
-    const int vec = vec_ok(x, (size_t)hin * win);
+                    const SpecPost& post, size_t qstride, int nq) {
+    const int vec = vec_ok(x, (size_t)hin * win) && (nq == 1 || qstride % 4 == 0);
     if constexpr (pair_grid<FH, FW>()) {
         const PLds l(hin, PGeo<FH, FW>::PITCH, FW, FH, false);
-        lds_limit(k_prfft2<FH, FW, FLIP, POST>, l.bytes);
-        hipLaunchKernelGGL((k_prfft2<FH, FW, FLIP, POST>), dim3(nplanes), dim3(64), l.bytes, st,
-                           hin, win, vec, x, out, post);
+        lds_limit(k_prfft2<FH, FW, FLIP, POST, NP>, l.bytes);
+        hipLaunchKernelGGL((k_prfft2<FH, FW, FLIP, POST, NP>), dim3(nplanes), dim3(64), l.bytes,
+                           st, hin, win, vec, x, out, post, qstride, nq);
     } else {
         using W = WGeo<FH, FW>;
         WLds<FH, FW> l(hin, win);
-        lds_limit(k_wrfft2<FH, FW, FLIP, POST>, l.bytes);
-        hipLaunchKernelGGL((k_wrfft2<FH, FW, FLIP, POST>), dim3((nplanes + W::PPW - 1) / W::PPW),
-                           dim3(64), l.bytes, st, nplanes, hin, win, l.off, vec, x, out, post);
+        lds_limit(k_wrfft2<FH, FW, FLIP, POST, NP>, l.bytes);
+        hipLaunchKernelGGL((k_wrfft2<FH, FW, FLIP, POST, NP>),
+                           dim3((nplanes + W::PPW - 1) / W::PPW), dim3(64), l.bytes, st, nplanes,
+                           hin, win, l.off, vec, x, out, post, qstride, nq);
     }
 }
 
+template <int FH, int FW, int NP>
+void launch_rfft2_np(hipStream_t st, int nplanes, int hin, int win, const float* x, cpx* out,
+                     int post_kind, const SpecPost& post, size_t qstride, int nq) {
+    if (post_kind == kPostAdd)
+        launch_rfft2_k<FH, FW, false, kPostAdd, NP>(st, nplanes, hin, win, x, out, post, qstride,
+                                                    nq);
+    else if (post_kind == kPostShift)
+        launch_rfft2_k<FH, FW, false, kPostShift, NP>(st, nplanes, hin, win, x, out, post,
+                                                      qstride, nq);
+    else
+        launch_rfft2_k<FH, FW, false, kPostNone, NP>(st, nplanes, hin, win, x, out, post,
+                                                     qstride, nq);
+}
+
 // Half-spectra of nplanes real planes; flip (the filter spectra) takes no post-operation.
+// nparts > 1: each plane is the sum of nparts partial planes qstride floats apart.
 template <int FH, int FW>
 int launch_rfft2(hipStream_t st, int nplanes, int hin, int win, bool flip, const float* x,
-                 cpx* out, int post_kind = kPostNone, const SpecPost& post = SpecPost{}) {
+                 cpx* out, int post_kind = kPostNone, const SpecPost& post = SpecPost{},
+                 int nparts = 1, size_t qstride = 0) {
+    if constexpr (seg_grid<FH, FW>())
+        return nc_seg_rfft2(st, FH, FW, nplanes, hin, win, flip ? 1 : 0, x, out,
+                            post_kind == kPostAdd ? post.add : nullptr,
+                            post_kind == kPostShift ? post.sh : 0,
+                            post_kind == kPostShift ? post.sw : 0, nparts, qstride);
     if (flip)
-        launch_rfft2_k<FH, FW, true, kPostNone>(st, nplanes, hin, win, x, out, post);
-    else if (post_kind == kPostAdd)
-        launch_rfft2_k<FH, FW, false, kPostAdd>(st, nplanes, hin, win, x, out, post);
-    else if (post_kind == kPostShift)
-        launch_rfft2_k<FH, FW, false, kPostShift>(st, nplanes, hin, win, x, out, post);
+        launch_rfft2_k<FH, FW, true, kPostNone, 1>(st, nplanes, hin, win, x, out, post, 0, 1);
+    else if (nparts == 1)
+        launch_rfft2_np<FH, FW, 1>(st, nplanes, hin, win, x, out, post_kind, post, 0, 1);
+    else if (nparts == 4 && pair_grid<FH, FW>())
+        launch_rfft2_np<FH, FW, 4>(st, nplanes, hin, win, x, out, post_kind, post, qstride, 4);
     else
-        launch_rfft2_k<FH, FW, false, kPostNone>(st, nplanes, hin, win, x, out, post);
+        launch_rfft2_np<FH, FW, 0>(st, nplanes, hin, win, x, out, post_kind, post, qstride,
+                                   nparts);
     NC_CHECK_LAUNCH();
     return NC_OK;
 }
@@ -727,11 +763,12 @@ int launch_corr(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw
 
 template <int FH, int FW>
 int launch_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph,
-               int pw, const float* x, const float* xhat_add, const float* ghat, float* z,
-               float* xhat) {
+               int pw, const float* x, int nparts, const float* xhat_add, const float* ghat,
+               float* z, float* xhat) {
     const SpecPost post{reinterpret_cast<const cpx*>(xhat_add), 0, 0};
     int rc = launch_rfft2<FH, FW>(st, B, hin, win, false, x, reinterpret_cast<cpx*>(xhat),
-                                  xhat_add ? kPostAdd : kPostNone, post);
+                                  xhat_add ? kPostAdd : kPostNone, post, nparts,
+                                  (size_t)B * hin * win);
     if (rc != NC_OK) return rc;
     return launch_corr<FH, FW>(st, B, M, hout, wout, ph, pw, xhat, ghat, z);
 }
@@ -775,7 +812,9 @@ __global__ __launch_bounds__(64) void k_pspectra(SpecJobs J) {
 
 template <int FH, int FW>
 int launch_spectra(hipStream_t st, int n, const nc_spectrum_job* jobs) {
-    if constexpr (pair_grid<FH, FW>()) {
+    if constexpr (seg_grid<FH, FW>()) {
+        return nc_large_plane_spectra(st, FH, FW, n, jobs);
+    } else if constexpr (pair_grid<FH, FW>()) {
         SpecJobs J{};
         J.n = n;
         size_t lds = 0;
@@ -826,11 +865,16 @@ int launch_pbwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wo
         hipLaunchKernelGGL((k_pdx_red<FH, FW>), dim3((P::F + 255) / 256, B), dim3(256), 0, st, B,
                            M, spec, reinterpret_cast<const cpx*>(ghat), dxs);
         NC_CHECK_LAUNCH();
-        const PLds lf(hin, P::PITCH, FW, FH, true);
-        lds_limit(k_pdx_half<FH, FW>, lf.bytes);
-        hipLaunchKernelGGL((k_pdx_half<FH, FW>), dim3(B), dim3(64), lf.bytes, st, hin, win, ph,
-                           pw, dxs, dx);
-        NC_CHECK_LAUNCH();
+        if constexpr (seg_grid<FH, FW>()) {
+            const int rc = nc_seg_dx(st, B, hin, win, ph, pw, FH, FW, dxs, dx);
+            if (rc != NC_OK) return rc;
+        } else {
+            const PLds lf(hin, P::PITCH, FW, FH, true);
+            lds_limit(k_pdx_half<FH, FW>, lf.bytes);
+            hipLaunchKernelGGL((k_pdx_half<FH, FW>), dim3(B), dim3(64), lf.bytes, st, hin, win,
+                               ph, pw, dxs, dx);
+            NC_CHECK_LAUNCH();
+        }
     }
     const int nchunk = dg_chunks<FH, FW>(B, M);
     const int bper = (B + nchunk - 1) / nchunk;
@@ -901,7 +945,9 @@ int launch_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wou
 // k_hat_red wrote it) with the unshifted roll.
 template <int FH, int FW>
 int launch_hat_dx(hipStream_t st, int hin, int win, int ph, int pw, const cpx* dxs, float* dx) {
-    if constexpr (pair_grid<FH, FW>()) {
+    if constexpr (seg_grid<FH, FW>()) {
+        return nc_seg_dx(st, 1, hin, win, ph, pw, FH, FW, dxs, dx);
+    } else if constexpr (pair_grid<FH, FW>()) {
         const PLds lf(hin, PGeo<FH, FW>::PITCH, FW, FH, true);
         lds_limit(k_pdx_half<FH, FW>, lf.bytes);
         hipLaunchKernelGGL((k_pdx_half<FH, FW>), dim3(1), dim3(64), lf.bytes, st, hin, win, ph,
@@ -995,21 +1041,30 @@ static int fftconv_check(int B, int M, int hin, int win, int hout, int wout, int
     return NC_OK;
 }
 
-int nc_fftconv_fwd_ex(void* stream, int B, int M, int hin, int win, int hout, int wout,
-                      int pad_h, int pad_w, int fft_h, int fft_w, const float* x,
-                      const float* xhat_add, const float* ghat, float* z, float* xhat) {
+int nc_fftconv_fwd_parts(void* stream, int B, int M, int hin, int win, int hout, int wout,
+                         int pad_h, int pad_w, int fft_h, int fft_w, const float* x_parts,
+                         int n_parts, const float* xhat_add, const float* ghat, float* z,
+                         float* xhat) {
     int rc = fftconv_check(B, M, hin, win, hout, wout, pad_h, pad_w, fft_h, fft_w);
     if (rc != NC_OK) return rc;
-    if (!x || !ghat || !z || !xhat) return NC_ERR_INVALID_ARGUMENT;
+    if (!x_parts || n_parts <= 0 || !ghat || !z || !xhat) return NC_ERR_INVALID_ARGUMENT;
     hipStream_t st = nc_stream(stream);
     if (nc_large_grid(fft_h, fft_w))
-        return nc_large_fftconv_fwd(st, B, M, hin, win, hout, wout, pad_h, pad_w, fft_h, fft_w, x,
-                                    xhat_add, ghat, z, xhat);
-#define NC_CALL(A, Bv) \
-    launch_fwd<A, Bv>(st, B, M, hin, win, hout, wout, pad_h, pad_w, x, xhat_add, ghat, z, xhat)
+        return nc_large_fftconv_fwd(st, B, M, hin, win, hout, wout, pad_h, pad_w, fft_h, fft_w,
+                                    x_parts, n_parts, xhat_add, ghat, z, xhat);
+#define NC_CALL(A, Bv)                                                                      \
+    launch_fwd<A, Bv>(st, B, M, hin, win, hout, wout, pad_h, pad_w, x_parts, n_parts, xhat_add, \
+                      ghat, z, xhat)
     NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
 #undef NC_CALL
     return NC_ERR_UNSUPPORTED;
+}
+
+int nc_fftconv_fwd_ex(void* stream, int B, int M, int hin, int win, int hout, int wout,
+                      int pad_h, int pad_w, int fft_h, int fft_w, const float* x,
+                      const float* xhat_add, const float* ghat, float* z, float* xhat) {
+    return nc_fftconv_fwd_parts(stream, B, M, hin, win, hout, wout, pad_h, pad_w, fft_h, fft_w,
+                                x, 1, xhat_add, ghat, z, xhat);
 }
 
 int nc_fftconv_fwd(void* stream, int B, int M, int hin, int win, int hout, int wout, int pad_h,

@@ -52,24 +52,88 @@ NC_DEV LdsParts lds_parts(float* lds) {
     return p;
 }
 
-template <int FH, int FW, bool FLIP, int POST>
+// Half-spectrum of one real plane src, column segment [c0, c0 + cs), each bin through
+// spec_post<POST> into o.  NP > 1: each value is the sum of NP partial planes qstride floats
+// apart, in increasing order (NP == 0: nq of them).
+template <int FH, int FW, bool FLIP, int POST, int NP>
+NC_DEV void lplane_job(const float* __restrict__ src, int hin, int win, int c0, int cs,
+                       cpx* __restrict__ o, const SpecPost& post, size_t qstride, int nq,
+                       const LdsParts& P) {
+    using L = LG<FH, FW>;
+    lplane_rfft2<FH, FW, kNT>(
+        [&](int r, int c) {
+            if constexpr (FLIP) return src[(hin - 1 - r) * win + (win - 1 - c)];
+            const float* a = src + r * win + c;
+            float v = a[0];
+            if constexpr (NP > 1) {
+#pragma unroll
+                for (int q = 1; q < NP; ++q) v += a[q * qstride];
+            } else if constexpr (NP == 0) {
+                for (int q = 1; q < nq; ++q) v += a[q * qstride];
+            }
+            return v;
+        },
+        hin, win, c0, cs,
+        [&](int kh, int kw, cpx v) { o[kh * L::SP + kw] = spec_post<POST, FH, FW>(v, kh, kw, post); },
+        P.seg, P.c0, P.scr, P.tw);
+}
+
+template <int FH, int FW, bool FLIP, int POST, int NP>
 __global__ __launch_bounds__(kNT) void k_lrfft2(int hin, int win, int cs, size_t pstride,
                                                 const float* __restrict__ x,
-                                                cpx* __restrict__ out, SpecPost post) {
-    using L = LG<FH, FW>;
+                                                cpx* __restrict__ out, SpecPost post,
+                                                size_t qstride, int nq) {
     HIP_DYNAMIC_SHARED(float, lds)
     const LdsParts P = lds_parts<FH, FW, true>(lds);
     load_twiddles(P.tw);
     __syncthreads();
-    const float* src = x + (size_t)blockIdx.x * pstride;
-    cpx* o = out + (size_t)blockIdx.x * L::F;
-    lplane_rfft2<FH, FW, kNT>(
-        [&](int r, int c) {
-            return FLIP ? src[(hin - 1 - r) * win + (win - 1 - c)] : src[r * win + c];
-        },
-        hin, win, (int)blockIdx.y * cs, cs,
-        [&](int kh, int kw, cpx v) { o[kh * L::SP + kw] = spec_post<POST, FH, FW>(v, kh, kw, post); },
-        P.seg, P.c0, P.scr, P.tw);
+    lplane_job<FH, FW, FLIP, POST, NP>(x + (size_t)blockIdx.x * pstride, hin, win,
+                                        (int)blockIdx.y * cs, cs,
+                                        out + (size_t)blockIdx.x * LG<FH, FW>::F, post, qstride,
+                                        nq, P);
+}
+
+// Several independent spectrum jobs (nc_plane_spectra) in one launch: block (g, segment) runs
+// plane g - start[q] of the job q whose range holds g.
+constexpr int kMaxLJobs = 4;
+struct LJobs {
+    const float* x[kMaxLJobs];
+    cpx* out[kMaxLJobs];
+    SpecPost post[kMaxLJobs];
+    int hin[kMaxLJobs], win[kMaxLJobs], kind[kMaxLJobs];
+    int start[kMaxLJobs + 1];
+    int n, cs;
+};
+enum { kLPlain = 0, kLFlip = 1, kLAdd = 2, kLShift = 3 };
+
+template <int FH, int FW>
+__global__ __launch_bounds__(kNT) void k_lspectra(LJobs J) {
+    HIP_DYNAMIC_SHARED(float, lds)
+    const LdsParts P = lds_parts<FH, FW, true>(lds);
+    load_twiddles(P.tw);
+    __syncthreads();
+    const int g = blockIdx.x;
+    int q = 0;
+    while (q + 1 < J.n && g >= J.start[q + 1]) ++q;
+    const int i = g - J.start[q], hin = J.hin[q], win = J.win[q];
+    const float* src = J.x[q] + (size_t)i * hin * win;
+    cpx* o = J.out[q] + (size_t)i * LG<FH, FW>::F;
+    const int c0 = (int)blockIdx.y * J.cs;
+    switch (J.kind[q]) {
+        case kLFlip:
+            lplane_job<FH, FW, true, kPostNone, 1>(src, hin, win, c0, J.cs, o, J.post[q], 0, 1, P);
+            break;
+        case kLAdd:
+            lplane_job<FH, FW, false, kPostAdd, 1>(src, hin, win, c0, J.cs, o, J.post[q], 0, 1, P);
+            break;
+        case kLShift:
+            lplane_job<FH, FW, false, kPostShift, 1>(src, hin, win, c0, J.cs, o, J.post[q], 0, 1,
+                                                     P);
+            break;
+        default:
+            lplane_job<FH, FW, false, kPostNone, 1>(src, hin, win, c0, J.cs, o, J.post[q], 0, 1,
+                                                    P);
+    }
 }
 
 // Packed column value of a half-spectrum at (kh, kw): DC + i*Nyquist for kw == 0.
@@ -251,12 +315,27 @@ int inv_rows(int rows) {
     }
 }
 
+template <int FH, int FW, bool FLIP, int POST, int NP>
+void rfft2_launch_np(hipStream_t st, dim3 grid, size_t lds, int hin, int win, int cs,
+                     size_t pstride, const float* x, cpx* out, const SpecPost& post,
+                     size_t qstride, int nq) {
+    set_lds(k_lrfft2<FH, FW, FLIP, POST, NP>, lds);
+    hipLaunchKernelGGL((k_lrfft2<FH, FW, FLIP, POST, NP>), grid, dim3(kNT), lds, st, hin, win,
+                       cs, pstride, x, out, post, qstride, nq);
+}
+
 template <int FH, int FW, bool FLIP, int POST>
 void rfft2_launch(hipStream_t st, dim3 grid, size_t lds, int hin, int win, int cs, size_t pstride,
-                  const float* x, cpx* out, const SpecPost& post) {
-    set_lds(k_lrfft2<FH, FW, FLIP, POST>, lds);
-    hipLaunchKernelGGL((k_lrfft2<FH, FW, FLIP, POST>), grid, dim3(kNT), lds, st, hin, win, cs,
-                       pstride, x, out, post);
+                  const float* x, cpx* out, const SpecPost& post, size_t qstride, int nq) {
+    if (FLIP || nq == 1)
+        rfft2_launch_np<FH, FW, FLIP, POST, 1>(st, grid, lds, hin, win, cs, pstride, x, out, post,
+                                               0, 1);
+    else if (nq == 4)
+        rfft2_launch_np<FH, FW, false, POST, 4>(st, grid, lds, hin, win, cs, pstride, x, out,
+                                                post, qstride, 4);
+    else
+        rfft2_launch_np<FH, FW, false, POST, 0>(st, grid, lds, hin, win, cs, pstride, x, out,
+                                                post, qstride, nq);
 }
 
 // Half-spectra of nplanes real planes, each bin through spec_post<post_kind> (flip: the filter
@@ -264,20 +343,23 @@ void rfft2_launch(hipStream_t st, dim3 grid, size_t lds, int hin, int win, int c
 template <int FH, int FW>
 int rfft2_planes(hipStream_t st, int nplanes, int hin, int win, size_t pstride, bool flip,
                  const float* x, cpx* out, int post_kind = kPostNone,
-                 const SpecPost& post = SpecPost{}) {
+                 const SpecPost& post = SpecPost{}, int nq = 1, size_t qstride = 0) {
     const int cs = fwd_cols<FH, FW>(hin);
     const size_t lds = lfwd_lds_bytes<FH, FW, kNT>(hin, cs);
     if (lds > kLdsMax) return NC_ERR_UNSUPPORTED;
     const dim3 grid(nplanes, LG<FH, FW>::NC / cs);
     if (flip)
-        rfft2_launch<FH, FW, true, kPostNone>(st, grid, lds, hin, win, cs, pstride, x, out, post);
+        rfft2_launch<FH, FW, true, kPostNone>(st, grid, lds, hin, win, cs, pstride, x, out, post,
+                                              qstride, nq);
     else if (post_kind == kPostAdd)
-        rfft2_launch<FH, FW, false, kPostAdd>(st, grid, lds, hin, win, cs, pstride, x, out, post);
+        rfft2_launch<FH, FW, false, kPostAdd>(st, grid, lds, hin, win, cs, pstride, x, out, post,
+                                              qstride, nq);
     else if (post_kind == kPostShift)
         rfft2_launch<FH, FW, false, kPostShift>(st, grid, lds, hin, win, cs, pstride, x, out,
-                                                post);
+                                                post, qstride, nq);
     else
-        rfft2_launch<FH, FW, false, kPostNone>(st, grid, lds, hin, win, cs, pstride, x, out, post);
+        rfft2_launch<FH, FW, false, kPostNone>(st, grid, lds, hin, win, cs, pstride, x, out, post,
+                                               qstride, nq);
     NC_CHECK_LAUNCH();
     return NC_OK;
 }
@@ -306,11 +388,12 @@ int corr(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw, const
 
 template <int FH, int FW>
 int conv_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph, int pw,
-             const float* x, const float* xhat_add, const float* ghat, float* z, float* xhat) {
+             const float* x, int nq, const float* xhat_add, const float* ghat, float* z,
+             float* xhat) {
     const SpecPost post{reinterpret_cast<const cpx*>(xhat_add), 0, 0};
     int rc = rfft2_planes<FH, FW>(st, B, hin, win, (size_t)hin * win, false, x,
                                   reinterpret_cast<cpx*>(xhat), xhat_add ? kPostAdd : kPostNone,
-                                  post);
+                                  post, nq, (size_t)B * hin * win);
     if (rc != NC_OK) return rc;
     return corr<FH, FW>(st, B, M, hout, wout, ph, pw, xhat, ghat, z);
 }
@@ -360,16 +443,29 @@ int conv_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout,
     return NC_OK;
 }
 
+// dx_b = the inverse of B unpacked dx half-spectra (B, F) with the unshifted roll.
 template <int FH, int FW>
-int hat_dx(hipStream_t st, int hin, int win, int ph, int pw, const cpx* dxs, float* dx) {
+int seg_dx(hipStream_t st, int B, int hin, int win, int ph, int pw, const cpx* dxs, float* dx) {
     const int rs = inv_rows<FH, FW>(hin);
     const size_t lds = linv_lds_bytes<FH, FW, kNT>(rs);
     set_lds(k_linv_dx<FH, FW>, lds);
-    hipLaunchKernelGGL((k_linv_dx<FH, FW>), dim3(1, (hin + rs - 1) / rs), dim3(kNT), lds, st, 1, 1,
+    hipLaunchKernelGGL((k_linv_dx<FH, FW>), dim3(B, (hin + rs - 1) / rs), dim3(kNT), lds, st, B, 1,
                        hin, win, ph, pw, rs, dxs, dx);
     NC_CHECK_LAUNCH();
     return NC_OK;
 }
+
+template <int FH, int FW>
+int hat_dx(hipStream_t st, int hin, int win, int ph, int pw, const cpx* dxs, float* dx) {
+    return seg_dx<FH, FW>(st, 1, hin, win, ph, pw, dxs, dx);
+}
+
+// The segmented transforms also serve the 64 x 64 grid's per-sample jobs (nc_seg_*).
+#define NC_DISPATCH_SEG(FH_, FW_, CALL)                     \
+    do {                                                    \
+        if (FH_ == 64 && FW_ == 64) return CALL(64, 64);    \
+        NC_DISPATCH_LARGE(FH_, FW_, CALL);                  \
+    } while (0)
 
 #define NC_DISPATCH_LARGE(FH_, FW_, CALL)                   \
     do {                                                    \
@@ -407,32 +503,69 @@ int nc_large_filter_spectrum_bwd(hipStream_t st, int M, int kh, int kw, int fh, 
 }
 
 int nc_large_fftconv_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout,
-                         int ph, int pw, int fh, int fw, const float* x, const float* xhat_add,
-                         const float* ghat, float* z, float* xhat) {
+                         int ph, int pw, int fh, int fw, const float* x, int nq,
+                         const float* xhat_add, const float* ghat, float* z, float* xhat) {
 #define NC_CALL(A, Bv) \
-    conv_fwd<A, Bv>(st, B, M, hin, win, hout, wout, ph, pw, x, xhat_add, ghat, z, xhat)
+    conv_fwd<A, Bv>(st, B, M, hin, win, hout, wout, ph, pw, x, nq, xhat_add, ghat, z, xhat)
     NC_DISPATCH_LARGE(fh, fw, NC_CALL);
 #undef NC_CALL
     return NC_ERR_UNSUPPORTED;
 }
 
-static int large_spectra_job(hipStream_t st, int fh, int fw, const nc_spectrum_job& j) {
-    const SpecPost post{reinterpret_cast<const cpx*>(j.add), j.shift_h, j.shift_w};
-    const int kind = j.add ? kPostAdd : (j.shift_h | j.shift_w) ? kPostShift : kPostNone;
-#define NC_CALL(A, Bv)                                                                      \
-    rfft2_planes<A, Bv>(st, j.nplanes, j.hin, j.win, (size_t)j.hin * j.win, j.flip != 0, j.x, \
-                        reinterpret_cast<cpx*>(j.xhat), kind, post)
-    NC_DISPATCH_LARGE(fh, fw, NC_CALL);
-#undef NC_CALL
-    return NC_ERR_UNSUPPORTED;
+template <int FH, int FW>
+int spectra(hipStream_t st, int n, const nc_spectrum_job* jobs) {
+    if (n > kMaxLJobs) return NC_ERR_INVALID_ARGUMENT;
+    LJobs J{};
+    J.n = n;
+    int hmax = 1;
+    for (int q = 0; q < n; ++q) {
+        const nc_spectrum_job& j = jobs[q];
+        J.x[q] = j.x;
+        J.out[q] = reinterpret_cast<cpx*>(j.xhat);
+        J.post[q] = SpecPost{reinterpret_cast<const cpx*>(j.add), j.shift_h, j.shift_w};
+        J.hin[q] = j.hin;
+        J.win[q] = j.win;
+        J.kind[q] = j.flip ? kLFlip : j.add ? kLAdd : (j.shift_h | j.shift_w) ? kLShift : kLPlain;
+        J.start[q + 1] = J.start[q] + j.nplanes;
+        hmax = std::max(hmax, j.hin);
+    }
+    // one column segmentation for all jobs: the LDS need grows with the live rows
+    J.cs = fwd_cols<FH, FW>(hmax);
+    const size_t lds = lfwd_lds_bytes<FH, FW, kNT>(hmax, J.cs);
+    if (lds > kLdsMax) return NC_ERR_UNSUPPORTED;
+    set_lds(k_lspectra<FH, FW>, lds);
+    hipLaunchKernelGGL((k_lspectra<FH, FW>), dim3(J.start[n], LG<FH, FW>::NC / J.cs), dim3(kNT),
+                       lds, st, J);
+    NC_CHECK_LAUNCH();
+    return NC_OK;
 }
 
 int nc_large_plane_spectra(hipStream_t st, int fh, int fw, int n, const nc_spectrum_job* jobs) {
-    for (int q = 0; q < n; ++q) {  // one launch per job
-        const int rc = large_spectra_job(st, fh, fw, jobs[q]);
-        if (rc != NC_OK) return rc;
-    }
-    return NC_OK;
+#define NC_CALL(A, Bv) spectra<A, Bv>(st, n, jobs)
+    NC_DISPATCH_SEG(fh, fw, NC_CALL);
+#undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
+}
+
+int nc_seg_rfft2(hipStream_t st, int fh, int fw, int nplanes, int hin, int win, int flip,
+                 const float* x, void* xhat, const void* add, int sh, int sw, int nparts,
+                 size_t qstride) {
+    const SpecPost post{reinterpret_cast<const cpx*>(add), sh, sw};
+    const int kind = add ? kPostAdd : (sh | sw) ? kPostShift : kPostNone;
+#define NC_CALL(A, Bv)                                                                    \
+    rfft2_planes<A, Bv>(st, nplanes, hin, win, (size_t)hin * win, flip != 0, x,          \
+                        reinterpret_cast<cpx*>(xhat), kind, post, nparts, qstride)
+    NC_DISPATCH_SEG(fh, fw, NC_CALL);
+#undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
+}
+
+int nc_seg_dx(hipStream_t st, int B, int hin, int win, int ph, int pw, int fh, int fw,
+              const void* dxs, float* dx) {
+#define NC_CALL(A, Bv) seg_dx<A, Bv>(st, B, hin, win, ph, pw, reinterpret_cast<const cpx*>(dxs), dx)
+    NC_DISPATCH_SEG(fh, fw, NC_CALL);
+#undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
 }
 
 int nc_large_correlate(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw, int fh,

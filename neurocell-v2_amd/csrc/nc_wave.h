@@ -104,10 +104,39 @@ NC_DEV_HOST_INLINE int istage_floats(int ppw, int rows, int fw) { return ppw * r
 // missing planes are zero.  With vec (n = rows*cols and pstride multiples of 4, src 16-byte
 // aligned) the loads are float4s; every load of a batch is issued before the LDS scatter, so
 // a wavefront keeps many global loads in flight.  FLIP reads each plane rotated by 180
-// degrees (the reversed flat order).
-template <int FW, int PPW, bool FLIP>
+// degrees (the reversed flat order).  NP > 1: each value is the sum of NP partial planes
+// qstride floats apart, added in increasing order (NP == 0: nq of them, a runtime count).
+template <int FW, int PPW, bool FLIP, int NP = 1>
 NC_DEV void istage(const float* __restrict__ src, size_t pstride, int np, int rows, int cols,
-                   bool vec, float* S) {
+                   bool vec, float* S, size_t qstride = 0, int nq = 1) {
+    const int nparts = NP == 0 ? nq : NP;
+    auto ld = [&](const float* a) {
+        float v = a[0];
+        if constexpr (NP != 1) {
+#pragma unroll
+            for (int q = 1; q < (NP == 0 ? 1 : NP); ++q) v += a[q * qstride];
+            if constexpr (NP == 0)
+                for (int q = 1; q < nparts; ++q) v += a[q * qstride];
+        }
+        return v;
+    };
+    auto ld4 = [&](const float4* a) {
+        float4 v = a[0];
+        if constexpr (NP != 1) {
+            auto add = [&](int q) {
+                const float4 w = a[q * (qstride >> 2)];
+                v.x += w.x;
+                v.y += w.y;
+                v.z += w.z;
+                v.w += w.w;
+            };
+#pragma unroll
+            for (int q = 1; q < (NP == 0 ? 1 : NP); ++q) add(q);
+            if constexpr (NP == 0)
+                for (int q = 1; q < nparts; ++q) add(q);
+        }
+        return v;
+    };
     const int lane = threadIdx.x & 63;
     const int n = rows * cols;
     // zero padding columns [cols, FW) of every staged row
@@ -128,7 +157,7 @@ NC_DEV void istage(const float* __restrict__ src, size_t pstride, int np, int ro
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
                     const int e = e0 + 64 * u;
-                    t[p][u] = (p < np && e < n4) ? s4[e] : make_float4(0.f, 0.f, 0.f, 0.f);
+                    t[p][u] = (p < np && e < n4) ? ld4(s4 + e) : make_float4(0.f, 0.f, 0.f, 0.f);
                 }
             }
 #pragma unroll
@@ -163,7 +192,7 @@ NC_DEV void istage(const float* __restrict__ src, size_t pstride, int np, int ro
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int e = e0 + 64 * u;
-                t[p][u] = (p < np && e < n) ? src[p * pstride + (FLIP ? n - 1 - e : e)] : 0.f;
+                t[p][u] = (p < np && e < n) ? ld(src + p * pstride + (FLIP ? n - 1 - e : e)) : 0.f;
             }
 #pragma unroll
         for (int u = 0; u < U; ++u) {

@@ -55,6 +55,9 @@ _SIGS = {
     "nc_filter_spectrum_bwd": (I, [P, I, I, I, I, I, I, I, P, P, I, I]),
     "nc_fftconv_fwd": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, P]),
     "nc_fftconv_fwd_ex": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, P, P]),
+    "nc_fftconv_fwd_parts": (I, [P, I, I, I, I, I, I, I, I, I, I, P, I, P, P, P, P]),
+    "nc_epilogue_fwd_partials": (I, [I, I, I, I]),
+    "nc_epilogue_fwd_parts": (I, [P, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, SZ]),
     "nc_plane_spectrum": (I, [P, I, I, I, I, I, I, I, P, P]),
     "nc_plane_spectra": (I, [P, I, I, I, C.POINTER(SpectrumJob)]),
     "nc_spectral_correlate": (I, [P, I, I, I, I, I, I, I, I, P, P, P]),

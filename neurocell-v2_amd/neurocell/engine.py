@@ -232,7 +232,10 @@ class StepPlan:
         t0_shape = (B, self.H, self.W) if self.t0_grid else (B, h, w)
         self.x0 = torch.empty(*t0_shape, **f)
         nz = d if self.training else 1
-        self.xs = [self.x0] + [torch.empty(B, h, w, **f) for _ in range(d - 1)]
+        # step states t >= 1 as the epilogue's uncombined direction-group partials (G planes
+        # per sample, summed by the next step's transform as it loads them)
+        self.G = _abi_int("nc_epilogue_fwd_partials", B, M, h, w)
+        self.xs = [self.x0] + [torch.empty(self.G, B, h, w, **f) for _ in range(d - 1)]
         self.zs = [torch.empty(B, M, h, w, **f) for _ in range(nz)]
         # cell spectra: one per step for the reverse pass, one shared buffer for evaluation
         self.xhat = [torch.empty(B, F, **c) for _ in range(d if self.training else 1)]
@@ -310,11 +313,12 @@ class StepPlan:
                 call("nc_spectral_correlate", s, B, M, h, w, p0[0], p0[1], fh, fw, ptr(xh0),
                      ptr(self.ghat), ptr(z))
             else:
-                call("nc_fftconv_fwd_ex", s, B, M, h, w, h, w, self.cp[0], self.cp[1], fh, fw,
-                     ptr(self.xs[t]), ptr(self.border_hat), ptr(self.ghat), ptr(z), ptr(xh))
+                call("nc_fftconv_fwd_parts", s, B, M, h, w, h, w, self.cp[0], self.cp[1], fh,
+                     fw, ptr(self.xs[t]), self.G, ptr(self.border_hat), ptr(self.ghat), ptr(z),
+                     ptr(xh))
             # z already holds z + delta: the epilogues run without their border term
             if not last:
-                call("nc_epilogue_fwd", s, B, M, h, w, self.act, self.slope, 0, ptr(z), None,
+                call("nc_epilogue_fwd_parts", s, B, M, h, w, self.act, self.slope, 0, ptr(z), None,
                      ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi), ptr(self.xs[t + 1]),
                      ptr(self.mean[t]), ptr(self.rstd[t]), ptr(self.ws_epi),
                      self.ws_epi.numel() * 4)
@@ -406,6 +410,14 @@ class StepPlan:
 def _addr(t: torch.Tensor) -> int:
     """Device address of a contiguous device tensor (for the ABI's job structs)."""
     return ptr(t).value
+
+
+def _abi_int(name: str, *args) -> int:
+    from ._lib import lib
+    v = int(getattr(lib(), name)(*args))
+    if v <= 0:
+        raise NeurocellError(f"{name}{args} failed")
+    return v
 
 
 def _abi_size(name: str, *args) -> int:

@@ -303,6 +303,50 @@ def case_epilogue(be, B=3, M=5, h=10, w=12, act="tanh", has_border=1, seed=2):
     return res
 
 
+def case_epilogue_parts(be, B=3, M=9, h=10, w=12, kh=5, kw=3, FH=16, FW=16, seed=7):
+    """nc_epilogue_fwd_parts + nc_fftconv_fwd_parts against nc_epilogue_fwd + nc_fftconv_fwd:
+    the partial planes add up to the combined output and the correlation from them matches,
+    both bit for bit (the same fixed-order sums), and the output matches the oracle."""
+    rng = np.random.default_rng(seed)
+    L, s = be.lib, be.stream()
+    z = (rng.normal(size=(B, M, h, w)) * 2 + 0.5).astype(np.float32)
+    wv = rng.normal(size=(h, w)).astype(np.float32)
+    sv = rng.uniform(size=(h, w)).astype(np.float32)
+    bv = rng.normal(size=(h, w)).astype(np.float32)
+    g = rng.normal(size=(M, 1, kh, kw)).astype(np.float32)
+    zd, wd, sd, bd, gd = (be.put(a) for a in (z, wv, sv, bv, g))
+    G = L.nc_epilogue_fwd_partials(B, M, h, w)
+    ws = be.zeros((L.nc_epilogue_workspace_size(B, M, h, w) // 4 + 1,))
+    nb = ws.nbytes if hasattr(ws, "nbytes") else ws.numel() * 4
+    aid = _abi.ACT_IDS["tanh"]
+    out, parts = be.zeros((B, h, w)), be.zeros((G, B, h, w))
+    mean, rstd = be.zeros((B, M)), be.zeros((B, M))
+    _ok(be, L.nc_epilogue_fwd(s, B, M, h, w, aid, 0.01, 0, be.ptr(zd), None, be.ptr(wd),
+                              be.ptr(sd), be.ptr(bd), be.ptr(out), be.ptr(mean), be.ptr(rstd),
+                              be.ptr(ws), nb), "epi")
+    _ok(be, L.nc_epilogue_fwd_parts(s, B, M, h, w, aid, 0.01, 0, be.ptr(zd), None, be.ptr(wd),
+                                    be.ptr(sd), be.ptr(bd), be.ptr(parts), be.ptr(mean),
+                                    be.ptr(rstd), be.ptr(ws), nb), "epi_parts")
+    ph, pw = (kh - 1) // 2, (kw - 1) // 2
+    ghat = be.zeros((M, FH, FW // 2 + 1, 2))
+    _ok(be, L.nc_filter_spectrum_fwd(s, M, kh, kw, FH, FW, be.ptr(gd), be.ptr(ghat)), "spec")
+    z1, x1 = be.zeros((B, M, h, w)), be.zeros((B, FH, FW // 2 + 1, 2))
+    z2, x2 = be.zeros((B, M, h, w)), be.zeros((B, FH, FW // 2 + 1, 2))
+    _ok(be, L.nc_fftconv_fwd(s, B, M, h, w, h, w, ph, pw, FH, FW, be.ptr(out), be.ptr(ghat),
+                             be.ptr(z1), be.ptr(x1)), "fwd")
+    _ok(be, L.nc_fftconv_fwd_parts(s, B, M, h, w, h, w, ph, pw, FH, FW, be.ptr(parts), G, None,
+                                   be.ptr(ghat), be.ptr(z2), be.ptr(x2)), "fwd_parts")
+    o, p = be.get(out), be.get(parts)
+    acc = p[0].copy()
+    for q in range(1, G):
+        acc = acc + p[q]
+    o_r = O.epilogue_fwd(z, np.zeros((M, h, w), np.float32), wv, sv, bv, "tanh", False)[0]
+    return {"G": G, "out": rel_l2(o, o_r),
+            "parts_sum_mismatch": int((acc != o).sum()),
+            "z_mismatch": int((be.get(z1) != be.get(z2)).sum()),
+            "xhat_mismatch": int((be.get(x1) != be.get(x2)).sum())}
+
+
 def case_port(be, B=3, M=5, h=10, w=12, rows=(2, 3, 4, 2), cols=(5, 5, 5, 5), fact=None,
               seed=3):
     """Output-port forward/backward (rect-like and coordinate ports, duplicates included)."""

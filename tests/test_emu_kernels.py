@@ -6,8 +6,8 @@ import ctypes
 import pytest
 
 from kernel_cases import (CODD_CASES, TOL, HostBackend, case_adaptive, case_border_conv,
-                          case_border_fold, case_codd, case_epilogue, case_fftconv, case_helpers,
-                          case_plane_spectra, case_port)
+                          case_border_fold, case_codd, case_epilogue, case_epilogue_parts,
+                          case_fftconv, case_helpers, case_plane_spectra, case_port)
 
 
 @pytest.fixture(scope="module")
@@ -93,3 +93,11 @@ def test_helpers(be):
     res = case_helpers(be)
     assert res["inject_mismatch"] == 0 and res["count_mismatch"] == 0, res
     _assert_small({k: res[k] for k in ("mse", "g_mse", "adamw")})
+
+
+@pytest.mark.parametrize("B,M,h,w,FH,FW", [(3, 9, 10, 12, 16, 16), (2, 16, 40, 50, 64, 64)])
+def test_epilogue_parts(be, B, M, h, w, FH, FW):
+    res = case_epilogue_parts(be, B=B, M=M, h=h, w=w, kh=5, kw=3, FH=FH, FW=FW)
+    assert res["G"] >= 1 and res["out"] < TOL, res
+    assert res["parts_sum_mismatch"] == 0 and res["z_mismatch"] == 0, res
+    assert res["xhat_mismatch"] == 0, res

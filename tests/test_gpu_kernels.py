@@ -3,8 +3,8 @@ import pytest
 
 from kernel_cases import (CODD_CASES, EPILOGUE_SHAPES, PORT_SHAPES, TOL, DeviceBackend,
                           case_adaptive, case_border_conv, case_border_fold, case_codd,
-                          case_epilogue, case_fftconv, case_helpers, case_plane_spectra,
-                          case_port)
+                          case_epilogue, case_epilogue_parts, case_fftconv, case_helpers,
+                          case_plane_spectra, case_port)
 
 pytestmark = pytest.mark.gpu
 
@@ -94,3 +94,12 @@ def test_helpers(be):
     res = case_helpers(be)
     assert res["inject_mismatch"] == 0 and res["count_mismatch"] == 0, res
     _assert_small({k: res[k] for k in ("mse", "g_mse", "adamw")})
+
+
+@pytest.mark.parametrize("B,M,h,w,FH,FW", [(3, 9, 10, 12, 16, 16), (128, 16, 40, 50, 64, 64),
+                                          (5, 7, 12, 10, 32, 16)])
+def test_epilogue_parts(be, B, M, h, w, FH, FW):
+    res = case_epilogue_parts(be, B=B, M=M, h=h, w=w, kh=5, kw=3, FH=FH, FW=FW)
+    assert res["G"] >= 1 and res["out"] < TOL, res
+    assert res["parts_sum_mismatch"] == 0 and res["z_mismatch"] == 0, res
+    assert res["xhat_mismatch"] == 0, res
