@@ -80,10 +80,10 @@ def kernel_families(ts, torch, reps):
         "fftconv_fwd": lambda: call("nc_fftconv_fwd_parts", s(), B, M, h, w, h, w, p.cp[0],
                                     p.cp[1], fh, fw, ptr(p.xs[t]), p.G, ptr(p.border_hat),
                                     ptr(p.ghat), ptr(p.zs[t]), ptr(p.xhat[t])),
-        "fftconv_bwd": lambda: call("nc_fftconv_bwd_ex", s(), B, M, h, w, h, w, p.cp[0],
+        "fftconv_bwd": lambda: call("nc_fftconv_bwd_parts", s(), B, M, h, w, h, w, p.cp[0],
                                     p.cp[1], fh, fw, ptr(p.gz), ptr(p.xhat[t]), ptr(p.ghat), 1,
-                                    ptr(p.gy[0]), ptr(p.dghat), 0, 0, ptr(p.gdelta_hat), 0,
-                                    ws_fc, n_fc),
+                                    ptr(p.gy[0]), ptr(p.rows["dg"]), 0, 0, ptr(p.rows["gd"]),
+                                    0, ws_fc, n_fc),
         "epilogue_fwd": lambda: call("nc_epilogue_fwd_parts", s(), B, M, h, w, p.act, p.slope, 0,
                                      ptr(p.zs[t]), None, ptr(p.w_eff), ptr(p.s_eff),
                                      ptr(p.b_roi), ptr(p.xs[t + 1]), ptr(p.mean[t]),

@@ -235,6 +235,37 @@ int nc_fftconv_bwd_hat(void* stream, int M, int hin, int win, int pad_h, int pad
                        float* dx, float* dghat, int accumulate, int conj_dghat, void* ws,
                        size_t ws_bytes);
 
+/*
+ * The number of partial rows nc_fftconv_bwd_parts writes per output at these shapes (its
+ * sample chunks; 1 on the large grids).
+ */
+int nc_fftconv_bwd_partials(int B, int M, int fft_h, int fft_w);
+
+/*
+ * nc_fftconv_bwd_ex leaving the sample-chunk partials of dghat and gz_hat_sum unsummed:
+ * dghat_parts and gz_hat_sum_parts are row stacks (nparts, M, fft_h, fft_w/2+1) complex,
+ * nparts = nc_fftconv_bwd_partials(B, M, fft_h, fft_w); each call writes its rows (or adds to
+ * them, accumulate / sum_accumulate, conjugated per row with conj_dghat), so a d-step reverse
+ * pass sums its steps row by row and one nc_spectrum_rows_sum adds the rows at its end: no
+ * chunk-sum launch per step.
+ * No counterpart in the reference.
+ */
+int nc_fftconv_bwd_parts(void* stream, int B, int M, int hin, int win, int hout, int wout,
+                         int pad_h, int pad_w, int fft_h, int fft_w, const float* gz,
+                         const float* xhat, const float* ghat, int need_dx, float* dx,
+                         float* dghat_parts, int accumulate, int conj_dghat,
+                         float* gz_hat_sum_parts, int sum_accumulate, void* ws, size_t ws_bytes);
+
+/*
+ * Sums of row stacks: outs[j] (row_len floats) = the sum over the nparts rows of stacks[j]
+ * (nparts, row_len), in a fixed order (eight interleaved chains, then a tree), for up to 4
+ * stacks in one launch - the one reduction of the row stacks that nc_fftconv_bwd_parts
+ * accumulated over a reverse pass's steps.  row_len: even (complex values).
+ * No counterpart in the reference.
+ */
+int nc_spectrum_rows_sum(void* stream, int nparts, size_t row_len, int n_stacks,
+                         const float* const* stacks, float* const* outs);
+
 /* ---------------- piece 3: hidden-step epilogue and output-port epilogue --------------- */
 
 /*

@@ -65,7 +65,7 @@ __global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_filter_spectrum_bwd(
     const int col0 = (FW - (shift_w % FW)) & (FW - 1);
     plane_irfft2<FH, FW>(
         [&](int a, int b) {
-            cpx v = d[a * P::SP + b];
+            const cpx v = d[a * P::SP + b];
             return conj_in ? cconj(v) : v;
         },
         row0, kh, col0, kw, 1.0f / (float)(FH * FW),
@@ -292,6 +292,9 @@ constexpr int kDgBatch = 16;  // samples whose loads a dG-reduction thread keeps
 // k_wbwd_dg_sum.  With ssum the plain sums over b of rfft2(gz_bm) are formed alongside (the
 // spectra of sum_b gz_bm, by linearity), into ssum (M, F) or the partial rows
 // part[chunks + c] (added to ssum when sum_acc).
+// parts_mode: dghat and ssum are row stacks (chunks, M, F); chunk c's sums are written to (or
+// added to, accumulate / sum_acc) their row c, conjugated per row when conj_out, and no
+// chunk sum runs - the consumer adds the rows (nc_filter_spectrum_bwd_parts, ..._hat_parts).
 template <int FH, int FW>
 __global__ __launch_bounds__(256) void k_wbwd_dg_red(int B, int M, int bper,
                                                      const cpx* __restrict__ spec,
@@ -299,7 +302,7 @@ __global__ __launch_bounds__(256) void k_wbwd_dg_red(int B, int M, int bper,
                                                      cpx* __restrict__ part,
                                                      cpx* __restrict__ dghat, int accumulate,
                                                      int conj_out, cpx* __restrict__ ssum,
-                                                     int sum_acc) {
+                                                     int sum_acc, int parts_mode) {
     using W = WGeo<FH, FW>;
     constexpr size_t SPP = spec_pitch<FH, FW>();
     const int m = blockIdx.y, c = blockIdx.z;
@@ -326,12 +329,13 @@ __global__ __launch_bounds__(256) void k_wbwd_dg_red(int B, int M, int bper,
             }
         }
     }
-    if (gridDim.z == 1) {
+    if (gridDim.z == 1 || parts_mode) {
+        const size_t row = parts_mode ? (size_t)c * M : 0;
         if (conj_out) acc = cconj(acc);
-        cpx* o = dghat + (size_t)m * W::F + e;
+        cpx* o = dghat + (row + m) * W::F + e;
         *o = accumulate ? cadd(*o, acc) : acc;
         if (ssum) {
-            cpx* so = ssum + (size_t)m * W::F + e;
+            cpx* so = ssum + (row + m) * W::F + e;
             *so = sum_acc ? cadd(*so, sacc) : sacc;
         }
     } else {
@@ -360,6 +364,21 @@ __global__ __launch_bounds__(256) void k_wbwd_dg_sum(int nchunk, int M, int F,
         cpx* o = ssum + (size_t)m * F + e;
         *o = sum_acc ? cadd(*o, v) : v;
     }
+}
+
+// Row-stack sums (nc_spectrum_rows_sum): out_j[e] = the fixed-order sum over the nparts rows
+// of stack j at e (the same eight-chain tree as k_wbwd_dg_sum); grid (len/256, jobs).
+constexpr int kMaxRowJobs = 4;
+struct RowJobs {
+    const cpx* in[kMaxRowJobs];
+    cpx* out[kMaxRowJobs];
+};
+
+__global__ __launch_bounds__(256) void k_rows_sum(RowJobs J, int nparts, size_t len) {
+    const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= len) return;
+    const int j = blockIdx.y;
+    J.out[j][e] = sum_strided(J.in[j] + e, nparts, len);
 }
 
 // Backward of a one-sample correlation from its cotangent half-spectra S (M, F), the
@@ -679,6 +698,38 @@ size_t bwd_ws(int B, int M) {
             2 * nc * M * W::F) * sizeof(cpx);
 }
 
+// Sample chunks the dG reduction actually launches (its partial rows).
+template <int FH, int FW>
+int dg_parts(int B, int M) {
+    const int nchunk = dg_chunks<FH, FW>(B, M);
+    const int bper = (B + nchunk - 1) / nchunk;
+    return (B + bper - 1) / bper;
+}
+
+// The dG (and spectrum-sum) reduction over the stored cotangent spectra: into dghat / ssum
+// through the chunk partials dgpart and k_wbwd_dg_sum, or, parts_mode, into their row stacks.
+template <int FH, int FW>
+int launch_dg(hipStream_t st, int B, int M, const cpx* spec, const float* xhat, float* dghat,
+              int accumulate, int conj_out, float* ssum, int sum_acc, cpx* dgpart,
+              bool parts_mode) {
+    constexpr int F = WGeo<FH, FW>::F;
+    const int nb = dg_parts<FH, FW>(B, M);
+    const int bper = (B + nb - 1) / nb;
+    cpx* sc = reinterpret_cast<cpx*>(ssum);
+    hipLaunchKernelGGL((k_wbwd_dg_red<FH, FW>), dim3((F + 255) / 256, M, nb), dim3(256), 0, st, B,
+                       M, bper, spec, reinterpret_cast<const cpx*>(xhat), dgpart,
+                       reinterpret_cast<cpx*>(dghat), accumulate, conj_out, sc, sum_acc,
+                       parts_mode ? 1 : 0);
+    NC_CHECK_LAUNCH();
+    if (nb > 1 && !parts_mode) {
+        hipLaunchKernelGGL(k_wbwd_dg_sum, dim3((F + 255) / 256, M, sc ? 2 : 1), dim3(256), 0, st,
+                           nb, M, F, dgpart, reinterpret_cast<cpx*>(dghat), accumulate, conj_out,
+                           sc, sum_acc);
+        NC_CHECK_LAUNCH();
+    }
+    return NC_OK;
+}
+
 template <int FH, int FW, bool FLIP, int POST, int NP>
 void launch_rfft2_k(hipStream_t st, int nplanes, int hin, int win, const float* x, cpx* out,
                     const SpecPost& post, size_t qstride, int nq) {
@@ -851,7 +902,7 @@ template <int FH, int FW>
 int launch_pbwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph,
                 int pw, const float* gz, const float* xhat, const float* ghat, int need_dx,
                 float* dx, float* dghat, int accumulate, int conj_out, float* ssum, int sum_acc,
-                void* ws) {
+                bool parts_mode, void* ws) {
     using P = PGeo<FH, FW>;
     cpx* spec = reinterpret_cast<cpx*>(ws);
     cpx* dxs = spec + (size_t)M * B * spec_pitch<FH, FW>();
@@ -876,31 +927,19 @@ int launch_pbwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wo
             NC_CHECK_LAUNCH();
         }
     }
-    const int nchunk = dg_chunks<FH, FW>(B, M);
-    const int bper = (B + nchunk - 1) / nchunk;
-    const int nb = (B + bper - 1) / bper;
-    cpx* sc = reinterpret_cast<cpx*>(ssum);
-    hipLaunchKernelGGL((k_wbwd_dg_red<FH, FW>), dim3((P::F + 255) / 256, M, nb), dim3(256), 0,
-                       st, B, M, bper, spec, reinterpret_cast<const cpx*>(xhat), dgpart,
-                       reinterpret_cast<cpx*>(dghat), accumulate, conj_out, sc, sum_acc);
-    NC_CHECK_LAUNCH();
-    if (nb > 1) {
-        hipLaunchKernelGGL(k_wbwd_dg_sum, dim3((P::F + 255) / 256, M, sc ? 2 : 1), dim3(256), 0,
-                           st, nb, M, P::F, dgpart, reinterpret_cast<cpx*>(dghat), accumulate,
-                           conj_out, sc, sum_acc);
-        NC_CHECK_LAUNCH();
-    }
-    return NC_OK;
+    return launch_dg<FH, FW>(st, B, M, spec, xhat, dghat, accumulate, conj_out, ssum, sum_acc,
+                             dgpart, parts_mode);
 }
 
 template <int FH, int FW>
 int launch_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph,
                int pw, const float* gz, const float* xhat, const float* ghat, int need_dx,
                float* dx, float* dghat, int accumulate, int conj_out, float* ssum, int sum_acc,
-               void* ws) {
+               bool parts_mode, void* ws) {
     if constexpr (pair_grid<FH, FW>())
         return launch_pbwd<FH, FW>(st, B, M, hin, win, hout, wout, ph, pw, gz, xhat, ghat, need_dx,
-                                   dx, dghat, accumulate, conj_out, ssum, sum_acc, ws);
+                                   dx, dghat, accumulate, conj_out, ssum, sum_acc, parts_mode,
+                                   ws);
     using W = WGeo<FH, FW>;
     const int mg = bwd_groups<FH, FW>(M);
     cpx* dxpart = reinterpret_cast<cpx*>(ws);
@@ -923,22 +962,9 @@ int launch_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wou
                            vec_ok(dx, (size_t)hin * win), dxsum, dx);
         NC_CHECK_LAUNCH();
     }
-    constexpr int nthr = W::F;
-    const int nchunk = dg_chunks<FH, FW>(B, M);
-    const int bper = (B + nchunk - 1) / nchunk;
     cpx* dgpart = spec + (size_t)M * B * spec_pitch<FH, FW>();
-    cpx* sc = reinterpret_cast<cpx*>(ssum);
-    hipLaunchKernelGGL((k_wbwd_dg_red<FH, FW>), dim3((nthr + 255) / 256, M, nchunk), dim3(256), 0,
-                       st, B, M, bper, spec, reinterpret_cast<const cpx*>(xhat), dgpart,
-                       reinterpret_cast<cpx*>(dghat), accumulate, conj_out, sc, sum_acc);
-    NC_CHECK_LAUNCH();
-    if (nchunk > 1) {
-        hipLaunchKernelGGL(k_wbwd_dg_sum, dim3((W::F + 255) / 256, M, sc ? 2 : 1), dim3(256), 0,
-                           st, nchunk, M, W::F, dgpart, reinterpret_cast<cpx*>(dghat), accumulate,
-                           conj_out, sc, sum_acc);
-        NC_CHECK_LAUNCH();
-    }
-    return NC_OK;
+    return launch_dg<FH, FW>(st, B, M, spec, xhat, dghat, accumulate, conj_out, ssum, sum_acc,
+                             dgpart, parts_mode);
 }
 
 // Inverse of a one-sample dx spectrum (unpacked for the lane-pair grids, packed otherwise, as
@@ -1137,11 +1163,11 @@ size_t nc_fftconv_bwd_workspace_size(int B, int M, int fft_h, int fft_w) {
     return 0;
 }
 
-int nc_fftconv_bwd_ex(void* stream, int B, int M, int hin, int win, int hout, int wout,
-                      int pad_h, int pad_w, int fft_h, int fft_w, const float* gz,
-                      const float* xhat, const float* ghat, int need_dx, float* dx, float* dghat,
-                      int accumulate, int conj_dghat, float* gz_hat_sum, int sum_accumulate,
-                      void* ws, size_t ws_bytes) {
+static int fftconv_bwd(void* stream, int B, int M, int hin, int win, int hout, int wout,
+                       int pad_h, int pad_w, int fft_h, int fft_w, const float* gz,
+                       const float* xhat, const float* ghat, int need_dx, float* dx, float* dghat,
+                       int accumulate, int conj_dghat, float* gz_hat_sum, int sum_accumulate,
+                       bool parts, void* ws, size_t ws_bytes) {
     int rc = fftconv_check(B, M, hin, win, hout, wout, pad_h, pad_w, fft_h, fft_w);
     if (rc != NC_OK) return rc;
     if (!gz || !xhat || !ghat || !dghat || (need_dx && !dx)) return NC_ERR_INVALID_ARGUMENT;
@@ -1154,10 +1180,58 @@ int nc_fftconv_bwd_ex(void* stream, int B, int M, int hin, int win, int hout, in
                                     gz_hat_sum, sum_accumulate, ws);
 #define NC_CALL(A, Bv)                                                                     \
     launch_bwd<A, Bv>(st, B, M, hin, win, hout, wout, pad_h, pad_w, gz, xhat, ghat, need_dx, \
-                      dx, dghat, accumulate, conj_dghat, gz_hat_sum, sum_accumulate, ws)
+                      dx, dghat, accumulate, conj_dghat, gz_hat_sum, sum_accumulate, parts, ws)
     NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
 #undef NC_CALL
     return NC_ERR_UNSUPPORTED;
+}
+
+int nc_fftconv_bwd_ex(void* stream, int B, int M, int hin, int win, int hout, int wout,
+                      int pad_h, int pad_w, int fft_h, int fft_w, const float* gz,
+                      const float* xhat, const float* ghat, int need_dx, float* dx, float* dghat,
+                      int accumulate, int conj_dghat, float* gz_hat_sum, int sum_accumulate,
+                      void* ws, size_t ws_bytes) {
+    return fftconv_bwd(stream, B, M, hin, win, hout, wout, pad_h, pad_w, fft_h, fft_w, gz, xhat,
+                       ghat, need_dx, dx, dghat, accumulate, conj_dghat, gz_hat_sum,
+                       sum_accumulate, false, ws, ws_bytes);
+}
+
+int nc_spectrum_rows_sum(void* stream, int nparts, size_t row_len, int n_stacks,
+                         const float* const* stacks, float* const* outs) {
+    if (nparts <= 0 || row_len == 0 || row_len % 2 || n_stacks <= 0 ||
+        n_stacks > kMaxRowJobs || !stacks || !outs)
+        return NC_ERR_INVALID_ARGUMENT;
+    RowJobs J{};
+    for (int j = 0; j < n_stacks; ++j) {
+        if (!stacks[j] || !outs[j]) return NC_ERR_INVALID_ARGUMENT;
+        J.in[j] = reinterpret_cast<const cpx*>(stacks[j]);
+        J.out[j] = reinterpret_cast<cpx*>(outs[j]);
+    }
+    const size_t len = row_len / 2;
+    hipLaunchKernelGGL(k_rows_sum, dim3((unsigned)((len + 255) / 256), n_stacks), dim3(256), 0,
+                       nc_stream(stream), J, nparts, len);
+    NC_CHECK_LAUNCH();
+    return NC_OK;
+}
+
+int nc_fftconv_bwd_partials(int B, int M, int fft_h, int fft_w) {
+    if (B <= 0 || M <= 0) return 0;
+    if (nc_large_grid(fft_h, fft_w)) return 1;
+    if (!pow2_ok(fft_h) || !pow2_ok(fft_w)) return 0;
+#define NC_CALL(A, Bv) dg_parts<A, Bv>(B, M)
+    NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
+#undef NC_CALL
+    return 0;
+}
+
+int nc_fftconv_bwd_parts(void* stream, int B, int M, int hin, int win, int hout, int wout,
+                         int pad_h, int pad_w, int fft_h, int fft_w, const float* gz,
+                         const float* xhat, const float* ghat, int need_dx, float* dx,
+                         float* dghat_parts, int accumulate, int conj_dghat,
+                         float* gz_hat_sum_parts, int sum_accumulate, void* ws, size_t ws_bytes) {
+    return fftconv_bwd(stream, B, M, hin, win, hout, wout, pad_h, pad_w, fft_h, fft_w, gz, xhat,
+                       ghat, need_dx, dx, dghat_parts, accumulate, conj_dghat, gz_hat_sum_parts,
+                       sum_accumulate, true, ws, ws_bytes);
 }
 
 int nc_fftconv_bwd(void* stream, int B, int M, int hin, int win, int hout, int wout, int pad_h,

@@ -66,6 +66,10 @@ _SIGS = {
     "nc_fftconv_bwd_ex": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, I, P, P, I, I, P, I, P,
                               SZ]),
     "nc_fftconv_bwd_hat": (I, [P, I, I, I, I, I, I, I, P, P, P, P, P, I, I, P, SZ]),
+    "nc_fftconv_bwd_partials": (I, [I, I, I, I]),
+    "nc_fftconv_bwd_parts": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, I, P, P, I, I, P, I,
+                                 P, SZ]),
+    "nc_spectrum_rows_sum": (I, [P, I, SZ, I, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)]),
     "nc_epilogue_workspace_size": (SZ, [I, I, I, I]),
     "nc_epilogue_fwd": (I, [P, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, SZ]),
     "nc_epilogue_bwd": (I, [P, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, P, P, P, P, I,

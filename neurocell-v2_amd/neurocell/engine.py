@@ -22,6 +22,7 @@ steps' dG reductions (linearity of rfft2), so the cotangent planes are not re-re
 from __future__ import annotations
 
 import copy
+import ctypes as C
 
 import numpy as np
 import torch
@@ -252,10 +253,18 @@ class StepPlan:
             self.ws_fc = torch.empty(max(1, n_fc // 4), **f)
             self.gz = torch.empty(B, M, h, w, **f)
             self.gy = [torch.empty(B, h, w, **f) for _ in range(2)]
-            # spectra of the border cotangent sum_b gz over the steps with the border term
+            # frequency-domain gradient sums: the filter gradients (ROI steps, VALID full-grid
+            # step) and the spectra of the border cotangent sum_b gz over the steps with the
+            # border term, accumulated step by step as row stacks of the dG reductions' sample
+            # chunks and summed once after the last step
+            self.npart = _abi_int("nc_fftconv_bwd_partials", B, M, *self.fft)
             self.gdelta_hat = torch.empty(M, F, **c)
             self.dghat = torch.empty(M, F, **c)
             self.dghat_v = torch.empty(M, F, **c)
+            if self.npart > 1:
+                self.rows = {k: torch.empty(self.npart, M, F, **c) for k in ("dg", "dgv", "gd")}
+            else:  # a single row is the sum itself
+                self.rows = {"dg": self.dghat, "dgv": self.dghat_v, "gd": self.gdelta_hat}
             self.gw = torch.empty(h, w, **f)
             self.gs = torch.empty(h, w, **f)
             self.gb = torch.empty(h, w, **f)
@@ -353,18 +362,18 @@ class StepPlan:
             need_dx = int(t > 0)
             if t == 0 and self.t0_grid:  # VALID full-grid step: its own spectral shift
                 r0, _, c0, _ = self.bbox
-                call("nc_fftconv_bwd", s, B, M, self.H, self.W, h, w, self.kh - 1 + r0,
+                call("nc_fftconv_bwd_parts", s, B, M, self.H, self.W, h, w, self.kh - 1 + r0,
                      self.kw - 1 + c0, fh, fw, ptr(self.gz), ptr(self.xhat[0]), ptr(self.ghat),
-                     0, None, ptr(self.dghat_v), 0, 0, ws_fc, n_fc)
+                     0, None, ptr(self.rows["dgv"]), 0, 0, None, 0, ws_fc, n_fc)
                 valid_acc = 1
             else:
                 # steps t >= 1 carried the border term: their cotangent's batch sum, summed
                 # over those steps in the frequency domain, is the border conv's cotangent
                 hbt = t > 0
-                call("nc_fftconv_bwd_ex", s, B, M, h, w, h, w, self.cp[0], self.cp[1], fh, fw,
+                call("nc_fftconv_bwd_parts", s, B, M, h, w, h, w, self.cp[0], self.cp[1], fh, fw,
                      ptr(self.gz), ptr(self.xhat[t]), ptr(self.ghat), need_dx,
-                     ptr(gy) if need_dx else None, ptr(self.dghat), int(t < d - 1), 0,
-                     ptr(self.gdelta_hat) if hbt else None, int(t < d - 1), ws_fc, n_fc)
+                     ptr(gy) if need_dx else None, ptr(self.rows["dg"]), int(t < d - 1), 0,
+                     ptr(self.rows["gd"]) if hbt else None, int(t < d - 1), ws_fc, n_fc)
             if t == 0:
                 break
             te = t - 1
@@ -375,6 +384,13 @@ class StepPlan:
                  n_ep)
             first_epi = False
         only_t0_grid = self.t0_grid and d == 1
+        if self.npart > 1:  # the row stacks written above, summed in one launch
+            keys = ([] if only_t0_grid else ["dg"]) + (["dgv"] if valid_acc else []) + \
+                   (["gd"] if d > 1 else [])
+            outs = {"dg": self.dghat, "dgv": self.dghat_v, "gd": self.gdelta_hat}
+            stacks = (C.c_void_p * len(keys))(*[_addr(self.rows[k]) for k in keys])
+            dsts = (C.c_void_p * len(keys))(*[_addr(outs[k]) for k in keys])
+            call("nc_spectrum_rows_sum", s, self.npart, M * self.F * 2, len(keys), stacks, dsts)
         if not only_t0_grid:
             call("nc_filter_spectrum_bwd", s, M, self.kh, self.kw, fh, fw, self.cp[0],
                  self.cp[1], ptr(self.dghat), ptr(g_filt), 0, 0)

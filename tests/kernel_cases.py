@@ -110,8 +110,28 @@ def case_fftconv(be, B=3, M=5, hin=10, win=12, kh=5, kw=3, FH=16, FW=16, seed=0)
     gf = be.zeros((M, 1, kh, kw))
     _ok(be, L.nc_filter_spectrum_bwd(s, M, kh, kw, FH, FW, ph, pw, be.ptr(dgh), be.ptr(gf), 0,
                                      0), "specbwd")
+    # the row-stack variant: two accumulating calls, summed by the consumers
+    npart = L.nc_fftconv_bwd_partials(B, M, FH, FW)
+    dgp = be.zeros((npart, M, FH, FW // 2 + 1, 2))
+    sp = be.zeros((npart, M, FH, FW // 2 + 1, 2))
+    for acc in (0, 1):
+        _ok(be, L.nc_fftconv_bwd_parts(s, B, M, hin, win, hin, win, ph, pw, FH, FW, be.ptr(gzd),
+                                       be.ptr(xhat), be.ptr(ghat), 0, None, be.ptr(dgp), acc, 0,
+                                       be.ptr(sp), acc, be.ptr(ws), nb), "bwd_parts")
+    dgs = be.zeros((M, FH, FW // 2 + 1, 2))
+    ssm = be.zeros((M, FH, FW // 2 + 1, 2))
+    stacks = (C.c_void_p * 2)(be.ptr(dgp).value, be.ptr(sp).value)
+    outs = (C.c_void_p * 2)(be.ptr(dgs).value, be.ptr(ssm).value)
+    _ok(be, L.nc_spectrum_rows_sum(s, npart, M * FH * (FW // 2 + 1) * 2, 2, stacks, outs),
+        "rows_sum")
+    gf2 = be.zeros((M, 1, kh, kw))
+    _ok(be, L.nc_filter_spectrum_bwd(s, M, kh, kw, FH, FW, ph, pw, be.ptr(dgs), be.ptr(gf2), 0,
+                                     0), "specbwd_rows")
     dxr, dgr = O.conv2d_bwd_direct(gz, x, g[:, 0], (ph, pw))
     return {
+        "dG_parts": rel_l2(be.get(gf2)[:, 0], 2 * dgr),
+        "gz_hat_sum_parts": rel_l2(_cplx(be.get(ssm)),
+                                   2 * np.fft.rfft2(gz.astype(np.float64).sum(0), s=(FH, FW))),
         "ghat": rel_l2(_cplx(be.get(ghat)), O.filter_spectrum(g[:, 0], (FH, FW))),
         "xhat": rel_l2(_cplx(be.get(xhat)), np.fft.rfft2(x.astype(np.float64), s=(FH, FW))),
         "z": rel_l2(be.get(z), O.conv2d_direct(x, g[:, 0], (ph, pw))),
@@ -170,12 +190,28 @@ def case_border_conv(be, M=4, h=12, w=10, kh=7, kw=5, FH=32, FW=16, seed=1):
     _ok(be, L.nc_fftconv_bwd_hat(s, M, Hp, Wp, kh - 1, kw - 1, FH, FW, be.ptr(ssum),
                                  be.ptr(phat), be.ptr(ghat), be.ptr(gp2), be.ptr(dgh2), 0, 0,
                                  be.ptr(ws), nb), "bwd_hat")
+    # the same from row stacks (nc_fftconv_bwd_parts -> nc_fftconv_bwd_hat_parts)
+    npart = L.nc_fftconv_bwd_partials(2, M, FH, FW)
+    sp = be.zeros((npart, M, FH, FW // 2 + 1, 2))
+    dgxp = be.zeros((npart, M, FH, FW // 2 + 1, 2))
+    _ok(be, L.nc_fftconv_bwd_parts(s, 2, M, Hp, Wp, h, w, kh - 1, kw - 1, FH, FW, be.ptr(g2),
+                                   be.ptr(x2), be.ptr(ghat), 0, None, be.ptr(dgxp), 0, 0,
+                                   be.ptr(sp), 0, be.ptr(ws2), nb2), "bwd_parts")
+    ssm = be.zeros((M, FH, FW // 2 + 1, 2))
+    _ok(be, L.nc_spectrum_rows_sum(s, npart, M * FH * (FW // 2 + 1) * 2, 1,
+                                   (C.c_void_p * 1)(be.ptr(sp).value),
+                                   (C.c_void_p * 1)(be.ptr(ssm).value)), "rows_sum")
+    gp3 = be.zeros((1, Hp, Wp))
+    _ok(be, L.nc_fftconv_bwd_hat(s, M, Hp, Wp, kh - 1, kw - 1, FH, FW, be.ptr(ssm), None,
+                                 be.ptr(ghat), be.ptr(gp3), None, 0, 0, be.ptr(ws), nb),
+        "bwd_hat_rows")
     gf2 = be.zeros((M, 1, kh, kw))
     _ok(be, L.nc_filter_spectrum_bwd(s, M, kh, kw, FH, FW, kh - 1, kw - 1, be.ptr(dgh2),
                                      be.ptr(gf2), 0, 0), "specbwd2")
     return {"delta": rel_l2(be.get(dl), O.conv2d_direct(patch, g[:, 0], (0, 0))),
             "dpatch": rel_l2(be.get(gp), gpr), "dG": rel_l2(be.get(gf)[:, 0], ggr),
-            "dpatch_hat": rel_l2(be.get(gp2), gpr), "dG_hat": rel_l2(be.get(gf2)[:, 0], ggr)}
+            "dpatch_hat": rel_l2(be.get(gp2), gpr), "dG_hat": rel_l2(be.get(gf2)[:, 0], ggr),
+            "dpatch_hat_parts": rel_l2(be.get(gp3), gpr)}
 
 
 def case_border_fold(be, B=3, M=4, h=12, w=10, kh=7, kw=5, FH=32, FW=16, seed=5):
