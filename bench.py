@@ -88,19 +88,19 @@ def kernel_families(ts, torch, reps):
                                      ptr(p.zs[t]), None, ptr(p.w_eff), ptr(p.s_eff),
                                      ptr(p.b_roi), ptr(p.xs[t + 1]), ptr(p.mean[t]),
                                      ptr(p.rstd[t]), ws_ep, n_ep),
-        "epilogue_bwd": lambda: call("nc_epilogue_bwd", s(), B, M, h, w, p.act, p.slope, 0,
-                                     ptr(p.zs[t]), None, ptr(p.w_eff), ptr(p.s_eff),
+        "epilogue_bwd": lambda: call("nc_epilogue_bwd_parts", s(), B, M, h, w, p.act, p.slope,
+                                     0, ptr(p.zs[t]), None, ptr(p.w_eff), ptr(p.s_eff),
                                      ptr(p.b_roi), ptr(p.mean[t]), ptr(p.rstd[t]),
-                                     ptr(p.gy[1]), ptr(p.gz), None, ptr(p.gw),
-                                     ptr(p.gs), ptr(p.gb), 0, 0, ws_ep, n_ep),
+                                     ptr(p.gy[1]), ptr(p.gz), ptr(p.pg_rows),
+                                     p.pg_rows[0].numel(), ws_ep, n_ep),
         "port_fwd": lambda: call("nc_port_fwd", s(), B, M, h, w, 0, p.fact, p.fslope, p.P,
                                  ptr(p.port_idx), ptr(p.zs[-1]), None, ptr(p.pp),
                                  ptr(p.out), ptr(p.zo), ptr(p.mean[-1]), ptr(p.rstd[-1]),
                                  ptr(p.pre), ws_ep, n_ep),
-        "port_bwd": lambda: call("nc_port_bwd", s(), B, M, h, w, 0, p.fact, p.fslope, p.P,
-                                 ptr(p.port_idx), ptr(p.zs[-1]), None, ptr(p.pp),
+        "port_bwd": lambda: call("nc_port_bwd_parts", s(), B, M, h, w, 0, p.fact, p.fslope,
+                                 p.P, ptr(p.port_idx), ptr(p.zs[-1]), None, ptr(p.pp),
                                  ptr(p.zo), ptr(p.mean[-1]), ptr(p.rstd[-1]), ptr(p.pre),
-                                 ptr(p.g_out), ptr(p.gz), None, ptr(p.gpp), 0, ws_ep,
+                                 ptr(p.g_out), ptr(p.gz), ptr(p.pp_rows), B * p.P, ws_ep,
                                  n_ep),
     }
     per_step = {"fftconv_fwd": p.d, "fftconv_bwd": p.d, "epilogue_fwd": p.d - 1,

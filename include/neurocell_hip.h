@@ -246,8 +246,8 @@ int nc_fftconv_bwd_partials(int B, int M, int fft_h, int fft_w);
  * dghat_parts and gz_hat_sum_parts are row stacks (nparts, M, fft_h, fft_w/2+1) complex,
  * nparts = nc_fftconv_bwd_partials(B, M, fft_h, fft_w); each call writes its rows (or adds to
  * them, accumulate / sum_accumulate, conjugated per row with conj_dghat), so a d-step reverse
- * pass sums its steps row by row and one nc_spectrum_rows_sum adds the rows at its end: no
- * chunk-sum launch per step.
+ * pass sums its steps row by row and one nc_rows_sum adds the rows at its end: no chunk-sum
+ * launch per step.
  * No counterpart in the reference.
  */
 int nc_fftconv_bwd_parts(void* stream, int B, int M, int hin, int win, int hout, int wout,
@@ -256,15 +256,6 @@ int nc_fftconv_bwd_parts(void* stream, int B, int M, int hin, int win, int hout,
                          float* dghat_parts, int accumulate, int conj_dghat,
                          float* gz_hat_sum_parts, int sum_accumulate, void* ws, size_t ws_bytes);
 
-/*
- * Sums of row stacks: outs[j] (row_len floats) = the sum over the nparts rows of stacks[j]
- * (nparts, row_len), in a fixed order (eight interleaved chains, then a tree), for up to 4
- * stacks in one launch - the one reduction of the row stacks that nc_fftconv_bwd_parts
- * accumulated over a reverse pass's steps.  row_len: even (complex values).
- * No counterpart in the reference.
- */
-int nc_spectrum_rows_sum(void* stream, int nparts, size_t row_len, int n_stacks,
-                         const float* const* stacks, float* const* outs);
 
 /* ---------------- piece 3: hidden-step epilogue and output-port epilogue --------------- */
 
@@ -318,6 +309,22 @@ int nc_epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg
                     const float* gy, float* gz, float* gdb, float* gw, float* gs, float* gb,
                     int accumulate_params, int accumulate_gdb, void* ws, size_t ws_bytes);
 
+/* The partial rows per parameter plane nc_epilogue_bwd_parts writes at these shapes. */
+int nc_epilogue_bwd_partials(int B, int M, int h, int w);
+
+/*
+ * nc_epilogue_bwd leaving the parameter gradients as partial rows: gw rows at pg_rows, gs rows
+ * at pg_rows + plane_stride, gb rows at pg_rows + 2*plane_stride (each R x (h*w) floats,
+ * R = nc_epilogue_bwd_partials(B, M, h, w), plane_stride >= R*h*w); their row sums are
+ * gw / gs / gb.  A d-step reverse pass gives each step its own R rows of one stack and sums
+ * them all with one nc_rows_sum.  No border cotangent.  No counterpart in the reference.
+ */
+int nc_epilogue_bwd_parts(void* stream, int B, int M, int h, int w, int act, float neg_slope,
+                          int has_border, const float* z, const float* delta, const float* w_eff,
+                          const float* s_eff, const float* b_roi, const float* mean,
+                          const float* rstd, const float* gy, float* gz, float* pg_rows,
+                          size_t plane_stride, void* ws, size_t ws_bytes);
+
 /*
  * pallas_standardize_output_port + pallas_fused_output_port_epilogue forward
  * (kernels_pallas.py:1256-1347, 1510-1551): per-plane (mean, rstd) over the whole (h,w)
@@ -348,6 +355,35 @@ int nc_port_bwd(void* stream, int B, int M, int h, int w, int has_border, int fi
                 const float* mean, const float* rstd, const float* pre, const float* g_out,
                 float* gz, float* gdb, float* g_port_params, int accumulate_params, void* ws,
                 size_t ws_bytes);
+
+/*
+ * nc_port_bwd leaving the port-parameter gradients as partial rows: B rows of n_port floats
+ * for each of the three parameters, planes plane_stride (>= B*n_port) floats apart from
+ * pp_rows; their row sums are g_port_params.  Requires port_params; no border cotangent.
+ * No counterpart in the reference.
+ */
+int nc_port_bwd_parts(void* stream, int B, int M, int h, int w, int has_border, int final_act,
+                      float neg_slope, int n_port, const int32_t* port_idx, const float* z,
+                      const float* delta, const float* port_params, const float* zo,
+                      const float* mean, const float* rstd, const float* pre,
+                      const float* g_out, float* gz, float* pp_rows, size_t plane_stride,
+                      void* ws, size_t ws_bytes);
+
+/* One job of nc_rows_sum: out[x] (+)= sum over r < nrows of rows[r*len + x], x < len. */
+typedef struct nc_rows_job {
+    const float* rows;
+    float* out;
+    int len;
+    int accumulate;
+    int nrows;
+} nc_rows_job;
+
+/*
+ * Up to 10 row-stack sums in one launch, each in a fixed order (deterministic): the partial
+ * rows of nc_fftconv_bwd_parts (complex spectra as float pairs), nc_epilogue_bwd_parts and
+ * nc_port_bwd_parts, gathered over a reverse pass.  No counterpart in the reference.
+ */
+int nc_rows_sum(void* stream, int n_jobs, const nc_rows_job* jobs);
 
 /* ---------------- piece 4: adaptive active-region bucketing ---------------------------- */
 

@@ -141,7 +141,7 @@ __global__ __launch_bounds__(NT) void k_epi_bwd(
     int M, int N, int mpg, float slope, int hb, const float* __restrict__ z,
     const float* __restrict__ delta, const float* __restrict__ w, const float* __restrict__ s,
     const float* __restrict__ bb, const float* __restrict__ mean, const float* __restrict__ rstd,
-    const float* __restrict__ gy, float* __restrict__ gz, float* __restrict__ pg) {
+    const float* __restrict__ gy, float* __restrict__ gz, float* __restrict__ pg, size_t GBN) {
     __shared__ float red[2 * MC * (NT / 64) + 2 * MC];
     const int b = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
     const int mb = g * mpg, me = min(M, mb + mpg);
@@ -209,8 +209,7 @@ __global__ __launch_bounds__(NT) void k_epi_bwd(
             }
         }
     }
-    const size_t GBN = (size_t)gridDim.y * gridDim.x * N;
-    const size_t row = ((size_t)g * gridDim.x + b) * N;
+    const size_t row = ((size_t)g * gridDim.x + b) * N;  // GBN: the gw / gs / gb plane stride
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
         const int p = tid + k * NT;
@@ -223,11 +222,13 @@ __global__ __launch_bounds__(NT) void k_epi_bwd(
 }
 
 // Fixed-order sums over rows, several independent jobs per launch (blockIdx.y = job):
-// job.out[x] = (job.acc ? job.out[x] : 0) + sum over r < job.rows of job.in[r * job.X + x].  Each workgroup owns
-// 64 columns; its 16 waves sum fixed contiguous slices of the batch (coalesced rows) and the
-// 16 slice sums are added in fixed order, so the result is deterministic.
+// job.out[x] = (job.acc ? job.out[x] : 0) + sum over r < job.rows of job.in[r * job.X + x].
+// A workgroup's Q = blockDim.x / 64 waves form Q / qs column groups of 64 columns; the qs
+// waves of a group (qs from the job's row count, about 32 rows per wave) sum fixed contiguous
+// slices of its rows (coalesced) and the qs slice sums are added in fixed order, so the
+// result is deterministic for given shapes.
 constexpr int kRedParts = 16;
-constexpr int kRedJobs = 4;
+constexpr int kRedJobs = 10;
 
 struct RedJob {
     const float* in;
@@ -235,6 +236,7 @@ struct RedJob {
     int X;
     int acc;
     int rows;  // number of rows summed (the batch, or groups x batch)
+    int qs;    // waves per column group (set at launch)
 };
 
 struct RedJobs {
@@ -245,10 +247,11 @@ __global__ __launch_bounds__(64 * kRedParts) void k_batch_reduce(RedJobs jobs) {
     __shared__ float part[kRedParts][64];
     const RedJob J = jobs.j[blockIdx.y];
     const int B = J.rows;
-    if ((int)blockIdx.x * 64 >= J.X) return;  // uniform over the workgroup
-    const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
-    const int x = blockIdx.x * 64 + lane;
-    const int b0 = (B * q) / kRedParts, b1 = (B * (q + 1)) / kRedParts;
+    const int Q = blockDim.x >> 6, qs = J.qs, cols = (Q / qs) * 64;
+    if ((int)blockIdx.x * cols >= J.X) return;  // uniform over the workgroup
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, q = w % qs;
+    const int x = blockIdx.x * cols + (w / qs) * 64 + lane;
+    const int b0 = (B * q) / qs, b1 = (B * (q + 1)) / qs;
     float s = 0.f;
     if (x < J.X) {
         const float* src = J.in + x;
@@ -261,12 +264,11 @@ __global__ __launch_bounds__(64 * kRedParts) void k_batch_reduce(RedJobs jobs) {
         for (; b < b1; ++b) a[0] += src[(size_t)b * J.X];
         s = (a[0] + a[1]) + (a[2] + a[3]);
     }
-    part[q][lane] = s;
+    part[w][lane] = s;
     __syncthreads();
     if (q == 0 && x < J.X) {
         float t = 0.f;
-#pragma unroll
-        for (int k = 0; k < kRedParts; ++k) t += part[k][lane];
+        for (int k = 0; k < qs; ++k) t += part[w + k][lane];
         float* o = J.out + x;
         *o = J.acc ? *o + t : t;
     }
@@ -275,15 +277,26 @@ __global__ __launch_bounds__(64 * kRedParts) void k_batch_reduce(RedJobs jobs) {
 // Launches the non-empty jobs of `jobs` (in order) as one k_batch_reduce.
 int launch_batch_reduce(hipStream_t st, const RedJob* jobs, int njobs) {
     RedJobs pack{};
-    int n = 0, xmax = 0;
+    int n = 0, rmax = 0;
+    auto slices = [](int rows) {  // about 32 rows per wave, 1..16 waves
+        int q = 1;
+        while (q < kRedParts && q * 32 < rows) q *= 2;
+        return q;
+    };
     for (int i = 0; i < njobs; ++i) {
         if (!jobs[i].in || jobs[i].X <= 0) continue;
         pack.j[n++] = jobs[i];
-        xmax = std::max(xmax, jobs[i].X);
+        rmax = std::max(rmax, jobs[i].rows);
     }
     if (n == 0) return NC_OK;
-    hipLaunchKernelGGL(k_batch_reduce, dim3((xmax + 63) / 64, n), dim3(64 * kRedParts), 0, st,
-                       pack);
+    const int Q = slices(rmax);
+    int nblk = 0;
+    for (int i = 0; i < n; ++i) {
+        pack.j[i].qs = slices(pack.j[i].rows);
+        const int cols = (Q / pack.j[i].qs) * 64;
+        nblk = std::max(nblk, (pack.j[i].X + cols - 1) / cols);
+    }
+    hipLaunchKernelGGL(k_batch_reduce, dim3(nblk, n), dim3(64 * Q), 0, st, pack);
     NC_CHECK_LAUNCH();
     return NC_OK;
 }
@@ -430,7 +443,7 @@ __global__ __launch_bounds__(kTileNT) void k_tile_bwd1(
     int B, int M, int N, int T, float slope, int hb, const float* __restrict__ z,
     const float* __restrict__ delta, const float* __restrict__ w, const float* __restrict__ s,
     const float* __restrict__ bb, const float* __restrict__ mean, const float* __restrict__ rstd,
-    const float* __restrict__ gy, float* __restrict__ cpart, float* __restrict__ pg) {
+    const float* __restrict__ gy, float* __restrict__ cpart, float* __restrict__ pg, size_t BN) {
     __shared__ float red[2 * kTileMC * (kTileNT / 64) + 2 * kTileMC];
     const int t = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
     const int base = t * kTileN;
@@ -496,9 +509,8 @@ __global__ __launch_bounds__(kTileNT) void k_tile_bwd1(
             cpart[BMT + o] = c2;
         }
     }
-    const size_t BN = (size_t)B * N;
 #pragma unroll
-    for (int k = 0; k < kTilePPT; ++k) {
+    for (int k = 0; k < kTilePPT; ++k) {  // BN: the gw / gs / gb plane stride
         if (tid + k * kTileNT >= nt) continue;
         pg[(size_t)b * N + pc[k]] = g[k] * lin[k];
         pg[BN + (size_t)b * N + pc[k]] = g[k] * ac[k];
@@ -739,7 +751,7 @@ __global__ __launch_bounds__(kPortNT) void k_port_bwd(
     const float* __restrict__ z, const float* __restrict__ delta, const float* __restrict__ pp,
     const float* __restrict__ zo, const float* __restrict__ mean, const float* __restrict__ rstd,
     const float* __restrict__ pre, const float* __restrict__ gout, float* __restrict__ gz,
-    float* __restrict__ ppart) {
+    float* __restrict__ ppart, size_t pstride) {
     HIP_DYNAMIC_SHARED(float, dyn)
     float* gzo = dyn;                          // M*P: port cotangent per (m, k)
     float* gsum = dyn + M * P;                 // M*P: summed per first-occurrence slot
@@ -863,9 +875,9 @@ __global__ __launch_bounds__(kPortNT) void k_port_bwd(
                 gs = gp * ac;
                 gb = gbv;
             }
-            ppart[(size_t)b * P + k] = gw;
-            ppart[((size_t)B + b) * P + k] = gs;
-            ppart[((size_t)2 * B + b) * P + k] = gb;
+            ppart[(size_t)b * P + k] = gw;  // pstride: the three parameters' plane stride
+            ppart[pstride + (size_t)b * P + k] = gs;
+            ppart[2 * pstride + (size_t)b * P + k] = gb;
         }
     }
 }
@@ -1098,34 +1110,44 @@ int nc_epilogue_fwd_parts(void* stream, int B, int M, int h, int w, int act, flo
                         b_roi, nullptr, parts, mean, rstd, ws, ws_bytes);
 }
 
-int nc_epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg_slope,
-                    int has_border, const float* z, const float* delta, const float* w_eff,
-                    const float* s_eff, const float* b_roi, const float* mean, const float* rstd,
-                    const float* gy, float* gz, float* gdb, float* gw, float* gs, float* gb,
-                    int accumulate_params, int accumulate_gdb, void* ws, size_t ws_bytes) {
+int nc_epilogue_bwd_partials(int B, int M, int h, int w) {
+    if (B <= 0 || M <= 0 || h <= 0 || w <= 0) return 0;
+    return h * w <= kSingleMaxPix ? bwd_plan(B, M, h * w).G * B : B;
+}
+
+// pg_rows != nullptr: the gw / gs / gb partial rows go there (planes plane_stride floats
+// apart) and are not reduced; otherwise to the workspace, reduced into gw / gs / gb.
+static int epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg_slope,
+                        int has_border, const float* z, const float* delta, const float* w_eff,
+                        const float* s_eff, const float* b_roi, const float* mean,
+                        const float* rstd, const float* gy, float* gz, float* gdb, float* gw,
+                        float* gs, float* gb, int accumulate_params, int accumulate_gdb,
+                        float* pg_rows, size_t plane_stride, void* ws, size_t ws_bytes) {
     if (B <= 0 || M <= 0 || M > kMaxM || h <= 0 || w <= 0 || !z || !w_eff || !s_eff ||
-        !b_roi || !mean || !rstd || !gy || !gz || !gw || !gs || !gb ||
+        !b_roi || !mean || !rstd || !gy || !gz || (!pg_rows && (!gw || !gs || !gb)) ||
         (has_border && !delta) || act < 0 || act > 5)
         return NC_ERR_INVALID_ARGUMENT;
     if (ws_bytes < nc_epilogue_workspace_size(B, M, h, w) || !ws) return NC_ERR_WORKSPACE;
     hipStream_t st = nc_stream(stream);
     const int N = h * w;
     const EpiWs e = epi_ws(ws, B, M, N);
-    int rows = B;  // rows of each pg partial plane
+    const int rows = nc_epilogue_bwd_partials(B, M, h, w);  // rows of each pg partial plane
+    float* pg = pg_rows ? pg_rows : e.pg;
+    const size_t RN = pg_rows ? plane_stride : (size_t)rows * N;
+    if (pg_rows && plane_stride < (size_t)rows * N) return NC_ERR_INVALID_ARGUMENT;
     int rc = dispatch_act(act, [&]<int ACT>() {
         if (N <= kSingleMaxPix) {
             const DirPlan P = bwd_plan(B, M, N);
-            rows = P.G * B;
             NC_BWD_DISPATCH(P, k_epi_bwd, dim3(B, P.G), dim3(P.c.nt), 0, st, M, N, P.mpg,
                             neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, mean, rstd, gy,
-                            gz, e.pg);
+                            gz, pg, RN);
             NC_CHECK_LAUNCH();
             return NC_OK;
         }
         const int T = tiles_of(N);
         hipLaunchKernelGGL((k_tile_bwd1<ACT>), dim3(T, B), dim3(kTileNT), 0, st, B, M, N, T,
                            neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, mean, rstd, gy,
-                           e.stats, e.pg);
+                           e.stats, pg, RN);
         NC_CHECK_LAUNCH();
         hipLaunchKernelGGL((k_tile_bwd2<ACT>), dim3(T, M, B), dim3(kTileNT), 0, st, B, M, N, T,
                            neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, mean, rstd, gy,
@@ -1136,12 +1158,44 @@ int nc_epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg
     if (rc != NC_OK) return rc;
     // parameter gradients and the border cotangent: sums over the partial rows (gw, gs, gb
     // planes of pg) and over B of gz, in one launch
-    const size_t RN = (size_t)rows * N;
-    const RedJob jobs[4] = {{e.pg, gw, N, accumulate_params, rows},
-                            {e.pg + RN, gs, N, accumulate_params, rows},
-                            {e.pg + 2 * RN, gb, N, accumulate_params, rows},
+    const bool own = pg_rows == nullptr;
+    const RedJob jobs[4] = {{own ? pg : nullptr, gw, N, accumulate_params, rows},
+                            {own ? pg + RN : nullptr, gs, N, accumulate_params, rows},
+                            {own ? pg + 2 * RN : nullptr, gb, N, accumulate_params, rows},
                             {has_border && gdb ? gz : nullptr, gdb, M * N, accumulate_gdb, B}};
     return launch_batch_reduce(st, jobs, 4);
+}
+
+int nc_epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg_slope,
+                    int has_border, const float* z, const float* delta, const float* w_eff,
+                    const float* s_eff, const float* b_roi, const float* mean, const float* rstd,
+                    const float* gy, float* gz, float* gdb, float* gw, float* gs, float* gb,
+                    int accumulate_params, int accumulate_gdb, void* ws, size_t ws_bytes) {
+    return epilogue_bwd(stream, B, M, h, w, act, neg_slope, has_border, z, delta, w_eff, s_eff,
+                        b_roi, mean, rstd, gy, gz, gdb, gw, gs, gb, accumulate_params,
+                        accumulate_gdb, nullptr, 0, ws, ws_bytes);
+}
+
+int nc_epilogue_bwd_parts(void* stream, int B, int M, int h, int w, int act, float neg_slope,
+                          int has_border, const float* z, const float* delta, const float* w_eff,
+                          const float* s_eff, const float* b_roi, const float* mean,
+                          const float* rstd, const float* gy, float* gz, float* pg_rows,
+                          size_t plane_stride, void* ws, size_t ws_bytes) {
+    if (!pg_rows) return NC_ERR_INVALID_ARGUMENT;
+    return epilogue_bwd(stream, B, M, h, w, act, neg_slope, has_border, z, delta, w_eff, s_eff,
+                        b_roi, mean, rstd, gy, gz, nullptr, nullptr, nullptr, nullptr, 0, 0,
+                        pg_rows, plane_stride, ws, ws_bytes);
+}
+
+int nc_rows_sum(void* stream, int n_jobs, const nc_rows_job* jobs) {
+    if (n_jobs <= 0 || n_jobs > kRedJobs || !jobs) return NC_ERR_INVALID_ARGUMENT;
+    RedJob rj[kRedJobs];
+    for (int i = 0; i < n_jobs; ++i) {
+        const nc_rows_job& j = jobs[i];
+        if (!j.rows || !j.out || j.nrows <= 0 || j.len <= 0) return NC_ERR_INVALID_ARGUMENT;
+        rj[i] = RedJob{j.rows, j.out, j.len, j.accumulate, j.nrows, 1};
+    }
+    return launch_batch_reduce(nc_stream(stream), rj, n_jobs);
 }
 
 static int port_check(int B, int M, int h, int w, int P, const int32_t* port_idx,
@@ -1192,38 +1246,63 @@ int nc_port_fwd(void* stream, int B, int M, int h, int w, int has_border, int fi
     return NC_OK;
 }
 
+static int port_bwd(void* stream, int B, int M, int h, int w, int has_border, int final_act,
+                    float neg_slope, int n_port, const int32_t* port_idx, const float* z,
+                    const float* delta, const float* port_params, const float* zo,
+                    const float* mean, const float* rstd, const float* pre, const float* g_out,
+                    float* gz, float* gdb, float* g_port_params, int accumulate_params,
+                    float* pp_rows, size_t plane_stride, void* ws, size_t ws_bytes) {
+    int rc = port_check(B, M, h, w, n_port, port_idx, z, has_border, delta, final_act);
+    if (rc != NC_OK) return rc;
+    if (!zo || !mean || !rstd || !g_out || !gz ||
+        (port_params && !g_port_params && !pp_rows) ||
+        (port_params && final_act != NC_ACT_IDENTITY && !pre))
+        return NC_ERR_INVALID_ARGUMENT;
+    if (pp_rows && plane_stride < (size_t)B * n_port) return NC_ERR_INVALID_ARGUMENT;
+    if (ws_bytes < nc_epilogue_workspace_size(B, M, h, w) || !ws) return NC_ERR_WORKSPACE;
+    hipStream_t st = nc_stream(stream);
+    const int N = h * w;
+    const int T = (N + kPortTile - 1) / kPortTile;
+    const EpiWs e = epi_ws(ws, B, M, N);
+    float* ppart = pp_rows ? pp_rows : e.pport;
+    const size_t ps = pp_rows ? plane_stride : (size_t)B * n_port;
+    const size_t shm = (size_t)2 * M * n_port * sizeof(float) + (size_t)kPortTile * sizeof(int);
+    hipLaunchKernelGGL(k_port_bwd, dim3(T, (M + kPortMC - 1) / kPortMC, B), dim3(kPortNT), shm,
+                       st, M, N, n_port, has_border, final_act, neg_slope, port_idx, z, delta,
+                       port_params, zo, mean, rstd, pre, g_out, gz, ppart, ps);
+    NC_CHECK_LAUNCH();
+    // port-parameter gradients (3 rows of P) and the border cotangent, in one launch
+    const bool pj = port_params != nullptr && pp_rows == nullptr;
+    const RedJob jobs[4] = {
+        {pj ? ppart : nullptr, g_port_params, n_port, accumulate_params, B},
+        {pj ? ppart + ps : nullptr, g_port_params + n_port, n_port, accumulate_params, B},
+        {pj ? ppart + 2 * ps : nullptr, g_port_params + 2 * n_port, n_port, accumulate_params,
+         B},
+        {has_border && gdb ? gz : nullptr, gdb, M * N, accumulate_params, B}};
+    return launch_batch_reduce(st, jobs, 4);
+}
+
 int nc_port_bwd(void* stream, int B, int M, int h, int w, int has_border, int final_act,
                 float neg_slope, int n_port, const int32_t* port_idx, const float* z,
                 const float* delta, const float* port_params, const float* zo,
                 const float* mean, const float* rstd, const float* pre, const float* g_out,
                 float* gz, float* gdb, float* g_port_params, int accumulate_params, void* ws,
                 size_t ws_bytes) {
-    int rc = port_check(B, M, h, w, n_port, port_idx, z, has_border, delta, final_act);
-    if (rc != NC_OK) return rc;
-    if (!zo || !mean || !rstd || !g_out || !gz || (port_params && !g_port_params) ||
-        (port_params && final_act != NC_ACT_IDENTITY && !pre))
-        return NC_ERR_INVALID_ARGUMENT;
-    if (ws_bytes < nc_epilogue_workspace_size(B, M, h, w) || !ws) return NC_ERR_WORKSPACE;
-    hipStream_t st = nc_stream(stream);
-    const int N = h * w;
-    const int T = (N + kPortTile - 1) / kPortTile;
-    const EpiWs e = epi_ws(ws, B, M, N);
-    float* ppart = e.pport;
-    const size_t shm = (size_t)2 * M * n_port * sizeof(float) + (size_t)kPortTile * sizeof(int);
-    hipLaunchKernelGGL(k_port_bwd, dim3(T, (M + kPortMC - 1) / kPortMC, B), dim3(kPortNT), shm,
-                       st, M, N, n_port, has_border, final_act, neg_slope, port_idx, z, delta,
-                       port_params, zo, mean, rstd, pre, g_out, gz, ppart);
-    NC_CHECK_LAUNCH();
-    // port-parameter gradients (3 rows of P) and the border cotangent, in one launch
-    const bool pj = port_params != nullptr;
-    const RedJob jobs[4] = {
-        {pj ? ppart : nullptr, g_port_params, n_port, accumulate_params, B},
-        {pj ? ppart + (size_t)B * n_port : nullptr, g_port_params + n_port, n_port,
-         accumulate_params, B},
-        {pj ? ppart + 2 * (size_t)B * n_port : nullptr, g_port_params + 2 * n_port, n_port,
-         accumulate_params, B},
-        {has_border && gdb ? gz : nullptr, gdb, M * N, accumulate_params, B}};
-    return launch_batch_reduce(st, jobs, 4);
+    return port_bwd(stream, B, M, h, w, has_border, final_act, neg_slope, n_port, port_idx, z,
+                    delta, port_params, zo, mean, rstd, pre, g_out, gz, gdb, g_port_params,
+                    accumulate_params, nullptr, 0, ws, ws_bytes);
+}
+
+int nc_port_bwd_parts(void* stream, int B, int M, int h, int w, int has_border, int final_act,
+                      float neg_slope, int n_port, const int32_t* port_idx, const float* z,
+                      const float* delta, const float* port_params, const float* zo,
+                      const float* mean, const float* rstd, const float* pre,
+                      const float* g_out, float* gz, float* pp_rows, size_t plane_stride,
+                      void* ws, size_t ws_bytes) {
+    if (!pp_rows || !port_params) return NC_ERR_INVALID_ARGUMENT;
+    return port_bwd(stream, B, M, h, w, has_border, final_act, neg_slope, n_port, port_idx, z,
+                    delta, port_params, zo, mean, rstd, pre, g_out, gz, nullptr, nullptr, 0,
+                    pp_rows, plane_stride, ws, ws_bytes);
 }
 
 }  // extern "C"

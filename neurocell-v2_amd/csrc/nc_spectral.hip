@@ -366,21 +366,6 @@ __global__ __launch_bounds__(256) void k_wbwd_dg_sum(int nchunk, int M, int F,
     }
 }
 
-// Row-stack sums (nc_spectrum_rows_sum): out_j[e] = the fixed-order sum over the nparts rows
-// of stack j at e (the same eight-chain tree as k_wbwd_dg_sum); grid (len/256, jobs).
-constexpr int kMaxRowJobs = 4;
-struct RowJobs {
-    const cpx* in[kMaxRowJobs];
-    cpx* out[kMaxRowJobs];
-};
-
-__global__ __launch_bounds__(256) void k_rows_sum(RowJobs J, int nparts, size_t len) {
-    const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= len) return;
-    const int j = blockIdx.y;
-    J.out[j][e] = sum_strided(J.in[j] + e, nparts, len);
-}
-
 // Backward of a one-sample correlation from its cotangent half-spectra S (M, F), the
 // spectra of gz (kernels_pallas.py:1794-1821 at B = 1): dghat[m] (+)= S_m * conj(xhat)
 // (conjugated when conj_out; skipped without dghat) and the dx spectrum sum over m, in
@@ -1194,24 +1179,6 @@ int nc_fftconv_bwd_ex(void* stream, int B, int M, int hin, int win, int hout, in
     return fftconv_bwd(stream, B, M, hin, win, hout, wout, pad_h, pad_w, fft_h, fft_w, gz, xhat,
                        ghat, need_dx, dx, dghat, accumulate, conj_dghat, gz_hat_sum,
                        sum_accumulate, false, ws, ws_bytes);
-}
-
-int nc_spectrum_rows_sum(void* stream, int nparts, size_t row_len, int n_stacks,
-                         const float* const* stacks, float* const* outs) {
-    if (nparts <= 0 || row_len == 0 || row_len % 2 || n_stacks <= 0 ||
-        n_stacks > kMaxRowJobs || !stacks || !outs)
-        return NC_ERR_INVALID_ARGUMENT;
-    RowJobs J{};
-    for (int j = 0; j < n_stacks; ++j) {
-        if (!stacks[j] || !outs[j]) return NC_ERR_INVALID_ARGUMENT;
-        J.in[j] = reinterpret_cast<const cpx*>(stacks[j]);
-        J.out[j] = reinterpret_cast<cpx*>(outs[j]);
-    }
-    const size_t len = row_len / 2;
-    hipLaunchKernelGGL(k_rows_sum, dim3((unsigned)((len + 255) / 256), n_stacks), dim3(256), 0,
-                       nc_stream(stream), J, nparts, len);
-    NC_CHECK_LAUNCH();
-    return NC_OK;
 }
 
 int nc_fftconv_bwd_partials(int B, int M, int fft_h, int fft_w) {

@@ -44,6 +44,20 @@ def spectrum_jobs(*jobs):
     return arr
 
 
+class RowsJob(C.Structure):
+    """Mirror of ``nc_rows_job``."""
+    _fields_ = [("rows", C.c_void_p), ("out", C.c_void_p), ("len", C.c_int32),
+                ("accumulate", C.c_int32), ("nrows", C.c_int32)]
+
+
+def rows_jobs(*jobs):
+    """A ctypes array of RowsJob from (rows, out, len, accumulate, nrows) tuples."""
+    arr = (RowsJob * len(jobs))()
+    for i, j in enumerate(jobs):
+        arr[i] = RowsJob(*j)
+    return arr
+
+
 _SIGS = {
     "nc_version": (I, []),
     "nc_strerror": (C.c_char_p, [I]),
@@ -69,11 +83,16 @@ _SIGS = {
     "nc_fftconv_bwd_partials": (I, [I, I, I, I]),
     "nc_fftconv_bwd_parts": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, I, P, P, I, I, P, I,
                                  P, SZ]),
-    "nc_spectrum_rows_sum": (I, [P, I, SZ, I, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)]),
     "nc_epilogue_workspace_size": (SZ, [I, I, I, I]),
     "nc_epilogue_fwd": (I, [P, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, SZ]),
     "nc_epilogue_bwd": (I, [P, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, P, P, P, P, I,
                             I, P, SZ]),
+    "nc_epilogue_bwd_partials": (I, [I, I, I, I]),
+    "nc_epilogue_bwd_parts": (I, [P, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, P, SZ, P,
+                                  SZ]),
+    "nc_port_bwd_parts": (I, [P, I, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, P, P, SZ, P,
+                              SZ]),
+    "nc_rows_sum": (I, [P, I, C.POINTER(RowsJob)]),
     "nc_port_fwd": (I, [P, I, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, P, SZ]),
     "nc_port_bwd": (I, [P, I, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, P, P, P, I, P,
                         SZ]),

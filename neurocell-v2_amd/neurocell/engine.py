@@ -22,7 +22,6 @@ steps' dG reductions (linearity of rfft2), so the cotangent planes are not re-re
 from __future__ import annotations
 
 import copy
-import ctypes as C
 
 import numpy as np
 import torch
@@ -265,6 +264,12 @@ class StepPlan:
                 self.rows = {k: torch.empty(self.npart, M, F, **c) for k in ("dg", "dgv", "gd")}
             else:  # a single row is the sum itself
                 self.rows = {"dg": self.dghat, "dgv": self.dghat_v, "gd": self.gdelta_hat}
+            # parameter-gradient partial rows, summed in the same launch: R rows per hidden
+            # epilogue step for each of gw / gs / gb, B rows per port parameter
+            self.R = _abi_int("nc_epilogue_bwd_partials", B, M, h, w)
+            L = max(1, d - 1)
+            self.pg_rows = torch.empty(3, L * self.R, h * w, **f)
+            self.pp_rows = torch.empty(3, B, self.P, **f)
             self.gw = torch.empty(h, w, **f)
             self.gs = torch.empty(h, w, **f)
             self.gb = torch.empty(h, w, **f)
@@ -351,11 +356,12 @@ class StepPlan:
         ws_ep, n_ep = ptr(self.ws_epi), self.ws_epi.numel() * 4
         ws_fc, n_fc = ptr(self.ws_fc), self.ws_fc.numel() * 4
         t = d - 1
-        call("nc_port_bwd", s, B, M, h, w, 0, self.fact, self.fslope, self.P, ptr(self.port_idx),
-             ptr(self.zs[t]), None, ptr(self.pp), ptr(self.zo), ptr(self.mean[t]),
-             ptr(self.rstd[t]), ptr(self.pre), ptr(g_out), ptr(self.gz), None, ptr(self.gpp), 0,
-             ws_ep, n_ep)
-        first_epi = True
+        N, RN = h * w, self.R * h * w
+        call("nc_port_bwd_parts", s, B, M, h, w, 0, self.fact, self.fslope, self.P,
+             ptr(self.port_idx), ptr(self.zs[t]), None, ptr(self.pp), ptr(self.zo),
+             ptr(self.mean[t]), ptr(self.rstd[t]), ptr(self.pre), ptr(g_out), ptr(self.gz),
+             ptr(self.pp_rows), B * self.P, ws_ep, n_ep)
+        pg_plane = self.pg_rows[0].numel()
         valid_acc = 0
         for t in range(d - 1, -1, -1):
             gy = self.gy[t % 2]
@@ -376,21 +382,25 @@ class StepPlan:
                      ptr(self.rows["gd"]) if hbt else None, int(t < d - 1), ws_fc, n_fc)
             if t == 0:
                 break
-            te = t - 1
-            call("nc_epilogue_bwd", s, B, M, h, w, self.act, self.slope, 0, ptr(self.zs[te]),
-                 None, ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
+            te = t - 1  # its own R rows of the gw / gs / gb stacks
+            call("nc_epilogue_bwd_parts", s, B, M, h, w, self.act, self.slope, 0,
+                 ptr(self.zs[te]), None, ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
                  ptr(self.mean[te]), ptr(self.rstd[te]), ptr(gy), ptr(self.gz),
-                 None, ptr(self.gw), ptr(self.gs), ptr(self.gb), int(not first_epi), 1, ws_ep,
-                 n_ep)
-            first_epi = False
+                 _addr(self.pg_rows) + 4 * te * RN, pg_plane, ws_ep, n_ep)
         only_t0_grid = self.t0_grid and d == 1
-        if self.npart > 1:  # the row stacks written above, summed in one launch
+        # every row stack written above, summed in one launch
+        jobs = []
+        if self.npart > 1:
             keys = ([] if only_t0_grid else ["dg"]) + (["dgv"] if valid_acc else []) + \
                    (["gd"] if d > 1 else [])
             outs = {"dg": self.dghat, "dgv": self.dghat_v, "gd": self.gdelta_hat}
-            stacks = (C.c_void_p * len(keys))(*[_addr(self.rows[k]) for k in keys])
-            dsts = (C.c_void_p * len(keys))(*[_addr(outs[k]) for k in keys])
-            call("nc_spectrum_rows_sum", s, self.npart, M * self.F * 2, len(keys), stacks, dsts)
+            jobs += [(_addr(self.rows[k]), _addr(outs[k]), 2 * M * self.F, 0, self.npart)
+                     for k in keys]
+        if d > 1:
+            jobs += [(_addr(self.pg_rows[i]), _addr(g), N, 0, (d - 1) * self.R)
+                     for i, g in enumerate((self.gw, self.gs, self.gb))]
+        jobs += [(_addr(self.pp_rows[i]), _addr(self.gpp[i]), self.P, 0, B) for i in range(3)]
+        call("nc_rows_sum", s, len(jobs), _abi.rows_jobs(*jobs))
         if not only_t0_grid:
             call("nc_filter_spectrum_bwd", s, M, self.kh, self.kw, fh, fw, self.cp[0],
                  self.cp[1], ptr(self.dghat), ptr(g_filt), 0, 0)

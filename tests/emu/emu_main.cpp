@@ -30,20 +30,35 @@ void emu_launch(std::function<void()> f, dim3 g, dim3 b, size_t shm) {
     gridDim = g;
     blockDim = b;
     const int nt = b.x * b.y * b.z;
-    for (unsigned z = 0; z < g.z; ++z)
-        for (unsigned y = 0; y < g.y; ++y)
-            for (unsigned x = 0; x < g.x; ++x) {
-                blockIdx = dim3(x, y, z);
-                std::memset(emu_dyn_lds + shm, 0xFF, EMU_LDS_BYTES - shm);
-                std::barrier<> bar(nt);
-                g_bar = &bar;
-                std::vector<std::thread> th;
-                th.reserve(nt);
-                for (int t = 0; t < nt; ++t) th.emplace_back([&, t] {
-                    threadIdx = dim3(t);
-                    f();
-                });
-                for (auto& q : th) q.join();
-                if (!lds_tail_intact(shm)) g_last_error = 1;
+    const size_t nblocks = (size_t)g.x * g.y * g.z;
+    std::barrier<> bar(nt);
+    g_bar = &bar;
+    // One pool of nt work-item threads per launch steps through the workgroups (x fastest,
+    // then y, then z).  The step barrier's completion runs once between workgroups: it checks
+    // the finished workgroup's LDS tail and sets up the next one.
+    size_t next = 0;
+    bool started = false;
+    auto between = [&]() noexcept {
+        if (started && !lds_tail_intact(shm)) g_last_error = 1;
+        started = true;
+        if (next < nblocks) {
+            const size_t i = next++;
+            blockIdx = dim3((unsigned)(i % g.x), (unsigned)((i / g.x) % g.y),
+                            (unsigned)(i / ((size_t)g.x * g.y)));
+            std::memset(emu_dyn_lds + shm, 0xFF, EMU_LDS_BYTES - shm);
+        }
+    };
+    std::barrier<decltype(between)> step(nt, between);
+    std::vector<std::thread> th;
+    th.reserve(nt);
+    for (int t = 0; t < nt; ++t)
+        th.emplace_back([&, t] {
+            threadIdx = dim3(t);
+            for (size_t i = 0; i < nblocks; ++i) {
+                step.arrive_and_wait();
+                f();
             }
+            step.arrive_and_wait();  // the last workgroup's LDS check
+        });
+    for (auto& q : th) q.join();
 }

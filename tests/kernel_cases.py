@@ -120,10 +120,10 @@ def case_fftconv(be, B=3, M=5, hin=10, win=12, kh=5, kw=3, FH=16, FW=16, seed=0)
                                        be.ptr(sp), acc, be.ptr(ws), nb), "bwd_parts")
     dgs = be.zeros((M, FH, FW // 2 + 1, 2))
     ssm = be.zeros((M, FH, FW // 2 + 1, 2))
-    stacks = (C.c_void_p * 2)(be.ptr(dgp).value, be.ptr(sp).value)
-    outs = (C.c_void_p * 2)(be.ptr(dgs).value, be.ptr(ssm).value)
-    _ok(be, L.nc_spectrum_rows_sum(s, npart, M * FH * (FW // 2 + 1) * 2, 2, stacks, outs),
-        "rows_sum")
+    n2 = M * FH * (FW // 2 + 1) * 2
+    jobs = _abi.rows_jobs((be.ptr(dgp).value, be.ptr(dgs).value, n2, 0, npart),
+                          (be.ptr(sp).value, be.ptr(ssm).value, n2, 0, npart))
+    _ok(be, L.nc_rows_sum(s, 2, jobs), "rows_sum")
     gf2 = be.zeros((M, 1, kh, kw))
     _ok(be, L.nc_filter_spectrum_bwd(s, M, kh, kw, FH, FW, ph, pw, be.ptr(dgs), be.ptr(gf2), 0,
                                      0), "specbwd_rows")
@@ -198,9 +198,9 @@ def case_border_conv(be, M=4, h=12, w=10, kh=7, kw=5, FH=32, FW=16, seed=1):
                                    be.ptr(x2), be.ptr(ghat), 0, None, be.ptr(dgxp), 0, 0,
                                    be.ptr(sp), 0, be.ptr(ws2), nb2), "bwd_parts")
     ssm = be.zeros((M, FH, FW // 2 + 1, 2))
-    _ok(be, L.nc_spectrum_rows_sum(s, npart, M * FH * (FW // 2 + 1) * 2, 1,
-                                   (C.c_void_p * 1)(be.ptr(sp).value),
-                                   (C.c_void_p * 1)(be.ptr(ssm).value)), "rows_sum")
+    _ok(be, L.nc_rows_sum(s, 1, _abi.rows_jobs((be.ptr(sp).value, be.ptr(ssm).value,
+                                                M * FH * (FW // 2 + 1) * 2, 0, npart))),
+        "rows_sum")
     gp3 = be.zeros((1, Hp, Wp))
     _ok(be, L.nc_fftconv_bwd_hat(s, M, Hp, Wp, kh - 1, kw - 1, FH, FW, be.ptr(ssm), None,
                                  be.ptr(ghat), be.ptr(gp3), None, 0, 0, be.ptr(ws), nb),
@@ -332,6 +332,25 @@ def case_epilogue(be, B=3, M=5, h=10, w=12, act="tanh", has_border=1, seed=2):
     r = O.epilogue_bwd(z, d, wv, sv, bv, m_r, r_r, gy, act, bool(has_border))
     res = {"out": rel_l2(be.get(out), o_r), "mean": rel_l2(be.get(mean), m_r),
            "rstd": rel_l2(be.get(rstd), r_r)}
+    # the row-stack variant, written as the second of two steps' row blocks (padded plane
+    # stride) and summed by nc_rows_sum: the same reduction over the same rows, bit for bit
+    R = L.nc_epilogue_bwd_partials(B, M, h, w)
+    N = h * w
+    stride = 2 * R * N + 5
+    pg = be.zeros((3 * stride,))
+    gz2, gsum = be.zeros((B, M, h, w)), be.zeros((3, N))
+    a = lambda t, off=0: be.ptr(t).value + 4 * off
+    _ok(be, L.nc_epilogue_bwd_parts(s, B, M, h, w, aid, 0.01, has_border, be.ptr(zd), be.ptr(dd),
+                                    be.ptr(wd), be.ptr(sd), be.ptr(bd), be.ptr(mean),
+                                    be.ptr(rstd), be.ptr(gyd), be.ptr(gz2), a(pg, R * N), stride,
+                                    be.ptr(ws), nb), "epib_parts")
+    jobs = _abi.rows_jobs(*[(a(pg, i * stride + R * N), a(gsum, i * N), N, 0, R)
+                            for i in range(3)])
+    _ok(be, L.nc_rows_sum(s, 3, jobs), "rows_sum")
+    gsum = be.get(gsum)
+    res["parts_gz_mismatch"] = float((be.get(gz2) != be.get(gz)).sum())
+    res["parts_params_mismatch"] = float(sum((gsum[i] != be.get(t).reshape(-1)).sum()
+                                             for i, t in enumerate((gw, gs, gb))))
     for k, a, b in zip(("gz", "gdb", "gw", "gs", "gb"), (gz, gdb, gw, gs, gb), r):
         if k == "gdb" and not has_border:
             continue
@@ -414,10 +433,23 @@ def case_port(be, B=3, M=5, h=10, w=12, rows=(2, 3, 4, 2), cols=(5, 5, 5, 5), fa
     r = O.port_bwd(z, d, R, Cc, (P, 1), pp[0][:, None], pp[1][:, None], pp[2][:, None], aux,
                    go[:, :, None], True, fact)
     g = be.get(gpp)
+    # the row-stack variant (padded plane stride), summed by nc_rows_sum: the same reduction
+    # over the same rows, so bit for bit the same gradients
+    stride = B * P + 7
+    prow, gz2, gpp2 = be.zeros((3 * stride,)), be.zeros((B, M, h, w)), be.zeros((3, P))
+    _ok(be, L.nc_port_bwd_parts(s, B, M, h, w, 1, fid, 0.01, P, be.ptr(idd), be.ptr(zd),
+                                be.ptr(dd), be.ptr(ppd), be.ptr(zo), be.ptr(mean), be.ptr(rstd),
+                                be.ptr(pre), be.ptr(god), be.ptr(gz2), be.ptr(prow), stride,
+                                be.ptr(ws), nb), "portb_parts")
+    a = lambda t, off=0: be.ptr(t).value + 4 * off
+    jobs = _abi.rows_jobs(*[(a(prow, i * stride), a(gpp2, i * P), P, 0, B) for i in range(3)])
+    _ok(be, L.nc_rows_sum(s, 3, jobs), "rows_sum")
     return {"out": rel_l2(be.get(out), o_r[:, :, 0]), "zo": rel_l2(be.get(zo), aux["zo"][..., 0]),
             "gz": rel_l2(be.get(gz), r[0]), "gdb": rel_l2(be.get(gdb), r[1]),
             "gw_out": rel_l2(g[0], r[2][:, 0]), "gs_out": rel_l2(g[1], r[3][:, 0]),
-            "gb_out": rel_l2(g[2], r[4][:, 0])}
+            "gb_out": rel_l2(g[2], r[4][:, 0]),
+            "parts_gz_mismatch": float((be.get(gz2) != be.get(gz)).sum()),
+            "parts_gpp_mismatch": float((be.get(gpp2) != g).sum())}
 
 
 def case_codd(be, mode="continuous", bbox=None, hard_pin=0, tau=0.1, seed=4):
