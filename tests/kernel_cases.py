@@ -553,22 +553,27 @@ def case_helpers(be, seed=6):
     prd, tgd = be.put(pr), be.put(tg)
     _ok(be, L.nc_mse_loss(s, 100, be.ptr(prd), be.ptr(tgd), be.ptr(loss), be.ptr(gp)), "mse")
     l_r, g_r = O.mse_loss(pr, tg)
-    p0 = rng.normal(size=50).astype(np.float32)
-    g = rng.normal(size=50).astype(np.float32)
-    p, gd = be.put(p0), be.put(g)
-    m, v, cnt = be.zeros((50,)), be.zeros((50,)), be.zeros((1,), np.int32)
     # a two-entry schedule table: steps 0 and >=1 use 0.01 and 0.02
     lr_tab = np.array([0.01, 0.02], np.float32)
     lr = be.put(lr_tab)
-    pr_, mr, vr, cr = p0.astype(np.float64), 0.0, 0.0, 0
-    for k in range(3):
-        _ok(be, L.nc_adamw_step(s, 50, be.ptr(p), be.ptr(gd), be.ptr(m), be.ptr(v), be.ptr(cnt),
-                                be.ptr(lr), 2, 0.9, 0.999, 1e-8, 1e-4), "adamw")
-        pr_, mr, vr, cr = O.adamw_step(pr_, g.astype(np.float64), mr, vr, cr,
-                                       float(lr_tab[min(k, 1)]))
-    return {"inject_mismatch": float((be.get(roi) != ref).sum()),
-            "mse": abs(float(be.get(loss)[0]) - l_r) / l_r, "g_mse": rel_l2(be.get(gp), g_r),
-            "adamw": rel_l2(be.get(p), pr_), "count_mismatch": float(be.get(cnt)[0] != 3)}
+    res = {"inject_mismatch": float((be.get(roi) != ref).sum()),
+           "mse": abs(float(be.get(loss)[0]) - l_r) / l_r, "g_mse": rel_l2(be.get(gp), g_r)}
+    # one workgroup (small vectors) and the grid-wide update plus counter launch (large)
+    for n, tag in ((50, ""), (70000, "_large")):
+        p0 = rng.normal(size=n).astype(np.float32)
+        g = rng.normal(size=n).astype(np.float32)
+        p, gd = be.put(p0), be.put(g)
+        m, v, cnt = be.zeros((n,)), be.zeros((n,)), be.zeros((1,), np.int32)
+        pr_, mr, vr, cr = p0.astype(np.float64), 0.0, 0.0, 0
+        for k in range(3):
+            _ok(be, L.nc_adamw_step(s, n, be.ptr(p), be.ptr(gd), be.ptr(m), be.ptr(v),
+                                    be.ptr(cnt), be.ptr(lr), 2, 0.9, 0.999, 1e-8, 1e-4), "adamw")
+            pr_, mr, vr, cr = O.adamw_step(pr_, g.astype(np.float64), mr, vr, cr,
+                                           float(lr_tab[min(k, 1)]))
+        res["adamw" + tag] = rel_l2(be.get(p), pr_)
+        res["count_mismatch" + tag] = float(be.get(cnt)[0] != 3)
+    res["count_mismatch"] += res.pop("count_mismatch_large")
+    return res
 
 
 EPILOGUE_SHAPES = [

@@ -93,7 +93,7 @@ def test_adaptive_stats(be):
 def test_helpers(be):
     res = case_helpers(be)
     assert res["inject_mismatch"] == 0 and res["count_mismatch"] == 0, res
-    _assert_small({k: res[k] for k in ("mse", "g_mse", "adamw")})
+    _assert_small({k: res[k] for k in ("mse", "g_mse", "adamw", "adamw_large")})
 
 
 @pytest.mark.parametrize("B,M,h,w,FH,FW", [(3, 9, 10, 12, 16, 16), (128, 16, 40, 50, 64, 64),
