@@ -111,9 +111,10 @@ def kernel_families(ts, torch, reps):
 # C-ABI family of each kernel of a --families-only run (k_batch_reduce belongs to whichever
 # backward family launched it: the preceding kernel decides).
 _FAMILY_KERNELS = {
-    "fftconv_fwd": ("k_wrfft2", "k_wconv_fwd", "k_lrfft2", "k_linv_conv"),
+    "fftconv_fwd": ("k_wrfft2", "k_wconv_fwd", "k_lrfft2", "k_linv_conv", "k_prfft2",
+                    "k_pspectra", "k_lspectra", "k_pconv_fwd"),
     "fftconv_bwd": ("k_wbwd_part", "k_psum", "k_wbwd_dx_fin", "k_wbwd_dg_red", "k_wbwd_dg_sum",
-                    "k_lred", "k_linv_dx"),
+                    "k_lred", "k_linv_dx", "k_pspec", "k_pdx_red", "k_pdx_half"),
     "epilogue_fwd": ("k_epi_fwd", "k_group_sum", "k_tile_stats", "k_tile_fwd"),
     "epilogue_bwd": ("k_epi_bwd", "k_tile_bwd1", "k_tile_bwd2"),
     "port_fwd": ("k_port_fwd", "k_port_combine", "k_port_fwd_tiled"),
