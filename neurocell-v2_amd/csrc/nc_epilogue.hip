@@ -31,6 +31,25 @@ NC_DEV const float* border_src(int hb, const float* delta, const float* z) {
     return hb ? delta : z;
 }
 
+// t[q][k] = z[zi(q, k)] (+ delta[di(q, k)] when hb) for an MC x PPT register tile: the two
+// forms are whole unrolled loops behind one uniform branch, so either issues all its loads
+// together, and without the border term z is read once.
+template <int MC, int PPT, class ZI, class DI>
+NC_DEV void load_tile(float (&t)[MC][PPT], int hb, const float* __restrict__ z,
+                      const float* __restrict__ delta, ZI zi, DI di) {
+    if (hb) {
+#pragma unroll
+        for (int q = 0; q < MC; ++q)
+#pragma unroll
+            for (int k = 0; k < PPT; ++k) t[q][k] = z[zi(q, k)] + delta[di(q, k)];
+    } else {
+#pragma unroll
+        for (int q = 0; q < MC; ++q)
+#pragma unroll
+            for (int k = 0; k < PPT; ++k) t[q][k] = z[zi(q, k)];
+    }
+}
+
 // ----------------------------------------------------------------------------------------
 // Single pass (N <= 8192): grid (B, G).  Workgroup (b, g) owns sample b's directions
 // [g * mpg, min(M, (g + 1) * mpg)), processed in chunks of MC held in registers.  With
@@ -55,8 +74,6 @@ __global__ __launch_bounds__(NT) void k_epi_fwd(int M, int N, int mpg, float slo
     const int B = gridDim.x, G = gridDim.y;
     const int mb = g * mpg, me = min(M, mb + mpg);
     const float inv_n = 1.0f / (float)N;
-    const float* dl = border_src(hb, delta, z);
-    const float hbf = hb ? 1.f : 0.f;
     float lin[PPT], ac[PPT], bv[PPT], wv[PPT], sv[PPT];
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
@@ -71,16 +88,16 @@ __global__ __launch_bounds__(NT) void k_epi_fwd(int M, int N, int mpg, float slo
         float zt[MC][PPT];
         float sum[MC];
         // unconditional (clamped) loads keep all MC*PPT requests in flight together
+        load_tile<MC, PPT>(
+            zt, hb, z, delta,
+            [&](int q, int k) {
+                return ((size_t)b * M + min(m0 + q, me - 1)) * N + min(tid + k * NT, N - 1);
+            },
+            [&](int q, int k) {
+                return (size_t)min(m0 + q, me - 1) * N + min(tid + k * NT, N - 1);
+            });
 #pragma unroll
-        for (int q = 0; q < MC; ++q) {
-            const int m = min(m0 + q, me - 1);
-            sum[q] = 0.f;
-#pragma unroll
-            for (int k = 0; k < PPT; ++k) {
-                const int pc = min(tid + k * NT, N - 1);
-                zt[q][k] = z[((size_t)b * M + m) * N + pc] + hbf * dl[(size_t)m * N + pc];
-            }
-        }
+        for (int q = 0; q < MC; ++q) sum[q] = 0.f;
 #pragma unroll
         for (int q = 0; q < MC; ++q)
 #pragma unroll
@@ -146,8 +163,6 @@ __global__ __launch_bounds__(NT) void k_epi_bwd(
     const int b = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
     const int mb = g * mpg, me = min(M, mb + mpg);
     const float inv_n = 1.0f / (float)N;
-    const float* dl = border_src(hb, delta, z);
-    const float hbf = hb ? 1.f : 0.f;
     float lin[PPT], ac[PPT], dbs[PPT], bv[PPT], wv[PPT], sv[PPT], gv[PPT];
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
@@ -168,12 +183,15 @@ __global__ __launch_bounds__(NT) void k_epi_bwd(
             const int m = min(m0 + q, me - 1);
             mr[q] = mean[(size_t)b * M + m];
             rr[q] = rstd[(size_t)b * M + m];
-#pragma unroll
-            for (int k = 0; k < PPT; ++k) {
-                const int pc = min(tid + k * NT, N - 1);
-                zn[q][k] = z[((size_t)b * M + m) * N + pc] + hbf * dl[(size_t)m * N + pc];
-            }
         }
+        load_tile<MC, PPT>(
+            zn, hb, z, delta,
+            [&](int q, int k) {
+                return ((size_t)b * M + min(m0 + q, me - 1)) * N + min(tid + k * NT, N - 1);
+            },
+            [&](int q, int k) {
+                return (size_t)min(m0 + q, me - 1) * N + min(tid + k * NT, N - 1);
+            });
 #pragma unroll
         for (int q = 0; q < MC; ++q) {
             const bool mv = m0 + q < me;
@@ -573,19 +591,16 @@ NC_DEV void plane_stats(int b, int M, int mb, int me, int N, int hb, const float
                         const float* __restrict__ delta, float* smu, float* srs, float* red) {
     const int tid = threadIdx.x;
     const float inv_n = 1.0f / (float)N;
-    const float* dl = border_src(hb, delta, z);
-    const float hbf = hb ? 1.f : 0.f;
     for (int m0 = mb; m0 < me; m0 += MC) {
         float zt[MC][PPT], sum[MC], sq[MC];
-#pragma unroll
-        for (int q = 0; q < MC; ++q) {
-            const int m = min(m0 + q, me - 1);
-#pragma unroll
-            for (int k = 0; k < PPT; ++k) {
-                const int pc = min(tid + k * NT, N - 1);
-                zt[q][k] = z[((size_t)b * M + m) * N + pc] + hbf * dl[(size_t)m * N + pc];
-            }
-        }
+        load_tile<MC, PPT>(
+            zt, hb, z, delta,
+            [&](int q, int k) {
+                return ((size_t)b * M + min(m0 + q, me - 1)) * N + min(tid + k * NT, N - 1);
+            },
+            [&](int q, int k) {
+                return (size_t)min(m0 + q, me - 1) * N + min(tid + k * NT, N - 1);
+            });
 #pragma unroll
         for (int q = 0; q < MC; ++q) {
             sum[q] = 0.f;
@@ -759,7 +774,6 @@ __global__ __launch_bounds__(kPortNT) void k_port_bwd(
     __shared__ float c1s[kMaxM], c2s[kMaxM];
     __shared__ int first[256];
     const int t = blockIdx.x, mg = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
-    const int B = gridDim.z;
     const float* zob = zo + (size_t)b * M * P;
     // 1. port cotangents (given directly as (B,M,P) in standardisation-only mode)
     for (int q = tid; q < M * P; q += kPortNT) {
@@ -768,7 +782,7 @@ __global__ __launch_bounds__(kPortNT) void k_port_bwd(
             gzo[q] = gout[(size_t)b * M * P + q];
             continue;
         }
-        const int m = q / P, k = q % P;
+        const int k = q % P;
         const float wo = pp[k], so = pp[P + k], bo = pp[2 * P + k];
         const float go = gout[(size_t)b * P + k];
         float v;
@@ -812,8 +826,6 @@ __global__ __launch_bounds__(kPortNT) void k_port_bwd(
     }
     __syncthreads();
     // 3. dense gz of this group's directions over the tile
-    const float* dl = border_src(hb, delta, z);
-    const float hbf = hb ? 1.f : 0.f;
     const int m0 = mg * kPortMC;
     int pc[kPortPPT], sl[kPortPPT];
 #pragma unroll
@@ -823,13 +835,10 @@ __global__ __launch_bounds__(kPortNT) void k_port_bwd(
         sl[k] = slot[i];
     }
     float v[kPortMC][kPortPPT];
-#pragma unroll
-    for (int q = 0; q < kPortMC; ++q) {
-        const int m = min(m0 + q, M - 1);
-#pragma unroll
-        for (int k = 0; k < kPortPPT; ++k)
-            v[q][k] = z[((size_t)b * M + m) * N + pc[k]] + hbf * dl[(size_t)m * N + pc[k]];
-    }
+    load_tile<kPortMC, kPortPPT>(
+        v, hb, z, delta,
+        [&](int q, int k) { return ((size_t)b * M + min(m0 + q, M - 1)) * N + pc[k]; },
+        [&](int q, int k) { return (size_t)min(m0 + q, M - 1) * N + pc[k]; });
 #pragma unroll
     for (int q = 0; q < kPortMC; ++q) {
         const int m = m0 + q;
@@ -847,7 +856,7 @@ __global__ __launch_bounds__(kPortNT) void k_port_bwd(
     // 4. per-sample port-parameter partials
     if (t == 0 && mg == 0 && pp) {
         for (int k = tid; k < P; k += kPortNT) {
-            const float wo = pp[k], so = pp[P + k], bo = pp[2 * P + k];
+            const float so = pp[P + k], bo = pp[2 * P + k];
             const float go = gout[(size_t)b * P + k];
             float lin = 0.f, ac = 0.f, gbv = 0.f;
             float gp = go;
