@@ -194,7 +194,8 @@ int nc_spectral_correlate(void* stream, int B, int M, int hout, int wout, int pa
 size_t nc_fftconv_bwd_workspace_size(int B, int M, int fft_h, int fft_w);
 
 /*
- * Unshifted Plancherel backward of the spectral correlation (kernels_pallas.py:1794-1821):
+ * Unshifted Plancherel backward of the spectral correlation (kernels_pallas.py:1794-1821);
+ * on the 64-wide grids M <= 64 (NC_ERR_UNSUPPORTED above, as the epilogues):
  * ghat_g = rfft2(gz) at the origin;
  *   dx = irfft2(sum_m ghat_g * conj(ghat)) rolled by (pad_h, pad_w), cropped (hin, win)
  *        (written only when need_dx; dx may be NULL otherwise);

@@ -30,12 +30,13 @@ int nc_large_plane_spectra(hipStream_t st, int fft_h, int fft_w, int n_jobs,
 // The segmented (workgroup-per-plane) transforms on the 64 x 64 grid as well as the large ones,
 // for per-sample jobs where the wavefront-per-plane kernels leave most of the chip idle:
 // half-spectra of nplanes planes (each the sum of nparts partial planes qstride floats apart;
-// flip / add / shift as nc_spectrum_job) and the dx inverse of B unpacked dx spectra.
+// flip / add / shift as nc_spectrum_job) and the dx inverse of B unpacked dx spectra, each
+// the sum of nchunk partials (nchunk, B, F).
 int nc_seg_rfft2(hipStream_t st, int fft_h, int fft_w, int nplanes, int hin, int win, int flip,
                  const float* x, void* xhat, const void* add, int shift_h, int shift_w,
                  int nparts, size_t qstride);
-int nc_seg_dx(hipStream_t st, int B, int hin, int win, int pad_h, int pad_w, int fft_h, int fft_w,
-              const void* dx_spectra, float* dx);
+int nc_seg_dx(hipStream_t st, int B, int nchunk, int hin, int win, int pad_h, int pad_w,
+              int fft_h, int fft_w, const void* dx_spectra, float* dx);
 
 int nc_large_correlate(hipStream_t st, int B, int M, int hout, int wout, int pad_h, int pad_w,
                        int fft_h, int fft_w, const float* xhat, const float* ghat, float* z);

@@ -517,39 +517,88 @@ __global__ __launch_bounds__(64) void k_pspec(int B, int M, int hout, int wout, 
                                            SpecPost{});
 }
 
-// Backward, dx reduction (kernels_pallas.py:1794-1812): dxs[b][e] = sum over m, in increasing
-// order, of spec[m][b][e] * conj(ghat_m[e]); one thread per (bin, sample), the loads of 16
-// directions in flight together.
-template <int FH, int FW>
-__global__ __launch_bounds__(256) void k_pdx_red(int B, int M, const cpx* __restrict__ spec,
-                                                 const cpx* __restrict__ ghat,
-                                                 cpx* __restrict__ dxs) {
+// Backward, both frequency-domain reductions in one pass over the stored cotangent spectra
+// spec (M, B, pitch) (kernels_pallas.py:1794-1821).  Workgroup = 64 bins x 4 waves, wave g
+// owning the directions [g*MG, (g+1)*MG); blockIdx.y = sample chunk c:
+//   dxs[b][e]      = sum over m of spec_mb * conj(ghat_m): each wave sums its directions
+//                    (increasing m), the four wave sums are added in order through LDS
+//   dgrow[c][m][e] (+)= sum over the chunk's samples, increasing, of spec_mb * conj(xhat_b)
+//                    (conjugated when conj_out)
+//   srow[c][m][e]  (+)= sum over the chunk's samples of spec_mb (with srow)
+// Each spectrum value is read once for both sums; kPBB samples' loads are in flight together.
+constexpr int kPBB = 4;
+
+template <int FH, int FW, int MG>
+__global__ __launch_bounds__(256) void k_pbwd_red(int B, int M, int bper, int need_dx,
+                                                  const cpx* __restrict__ spec,
+                                                  const cpx* __restrict__ xhat,
+                                                  const cpx* __restrict__ ghat,
+                                                  cpx* __restrict__ dxs, cpx* __restrict__ dgrow,
+                                                  int accumulate, int conj_out,
+                                                  cpx* __restrict__ srow, int sum_acc) {
     using P = PGeo<FH, FW>;
-    constexpr int MC = 16;
     constexpr size_t SPP = spec_pitch<FH, FW>();
-    const int e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= P::F) return;
-    const int b = blockIdx.y;
-    cpx d = cmk(0.f, 0.f);
-    for (int m0 = 0; m0 < M; m0 += MC) {
-        cpx sv[MC], gv[MC];
+    __shared__ cpx red[4][kPBB][64];
+    const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
+    const int e0 = blockIdx.x * 64 + lane, e = min(e0, P::F - 1);
+    const int c = blockIdx.y;
+    const int m0 = g * MG, nm = max(0, min(MG, M - m0));
+    const int b0 = c * bper, b1 = min(B, b0 + bper);
+    cpx G[MG], dg[MG], sg[MG];
 #pragma unroll
-        for (int q = 0; q < MC; ++q) {
-            const int m = min(m0 + q, M - 1);
-            sv[q] = spec[((size_t)m * B + b) * SPP + e];
-            gv[q] = ghat[(size_t)m * P::F + e];
+    for (int q = 0; q < MG; ++q) {
+        G[q] = ghat[(size_t)min(m0 + q, M - 1) * P::F + e];
+        dg[q] = sg[q] = cmk(0.f, 0.f);
+    }
+    for (int bb = b0; bb < b1; bb += kPBB) {
+        cpx u[kPBB][MG], xv[kPBB];
+#pragma unroll
+        for (int j = 0; j < kPBB; ++j) {
+            const int b = min(bb + j, b1 - 1);
+            xv[j] = xhat[(size_t)b * P::F + e];
+#pragma unroll
+            for (int q = 0; q < MG; ++q)
+                u[j][q] = spec[((size_t)min(m0 + q, M - 1) * B + b) * SPP + e];
         }
 #pragma unroll
-        for (int q = 0; q < MC; ++q)
-            if (m0 + q < M) d = cadd(d, cmulc(sv[q], gv[q]));
+        for (int j = 0; j < kPBB; ++j) {
+            cpx d = cmk(0.f, 0.f);
+            const bool on = bb + j < b1;
+#pragma unroll
+            for (int q = 0; q < MG; ++q) {
+                if (q < nm && on) {
+                    d = cadd(d, cmulc(u[j][q], G[q]));
+                    dg[q] = cadd(dg[q], cmulc(u[j][q], xv[j]));
+                    sg[q] = cadd(sg[q], u[j][q]);
+                }
+            }
+            red[g][j][lane] = d;
+        }
+        __syncthreads();
+        if (need_dx) {  // wave g finishes samples j = g, g + 4, ...: the four wave sums in order
+            for (int j = g; j < kPBB && bb + j < b1; j += 4) {
+                const cpx v = cadd(cadd(cadd(red[0][j][lane], red[1][j][lane]), red[2][j][lane]),
+                                   red[3][j][lane]);
+                if (e0 < P::F) dxs[(size_t)(bb + j) * P::F + e0] = v;
+            }
+        }
+        __syncthreads();
     }
-    dxs[(size_t)b * P::F + e] = d;
+    if (e0 >= P::F) return;
+#pragma unroll
+    for (int q = 0; q < MG; ++q) {
+        if (q >= nm) break;
+        const size_t o = ((size_t)c * M + m0 + q) * P::F + e0;
+        const cpx v = conj_out ? cconj(dg[q]) : dg[q];
+        dgrow[o] = accumulate ? cadd(dgrow[o], v) : v;
+        if (srow) srow[o] = sum_acc ? cadd(srow[o], sg[q]) : sg[q];
+    }
 }
 
 // dx, last stage: the inverse of sample b's dx half-spectrum with the unshifted roll
 // (kernels_pallas.py:1798-1812); one wavefront per sample.
 template <int FH, int FW>
-__global__ __launch_bounds__(64) void k_pdx_half(int hin, int win, int ph, int pw,
+__global__ __launch_bounds__(64) void k_pdx_half(int hin, int win, int ph, int pw, int ng,
                                                  const cpx* __restrict__ dxs,
                                                  float* __restrict__ dx) {
     using P = PGeo<FH, FW>;
@@ -558,12 +607,18 @@ __global__ __launch_bounds__(64) void k_pdx_half(int hin, int win, int ph, int p
     const int lane = threadIdx.x, kc = lane >> 1, t = lane & 1;
     const int b = blockIdx.x;
     const cpx* src = dxs + (size_t)b * P::F;
+    const size_t gs = (size_t)gridDim.x * P::F;  // the ng direction-group partials, in order
+    auto at = [&](int e) {
+        cpx a = src[e];
+        for (int q = 1; q < ng; ++q) a = cadd(a, src[q * gs + e]);
+        return a;
+    };
     cpx v[P::HH];
 #pragma unroll
-    for (int j = 0; j < P::HH; ++j) v[j] = src[(2 * j + t) * P::SP + kc];
+    for (int j = 0; j < P::HH; ++j) v[j] = at((2 * j + t) * P::SP + kc);
     if (kc == 0) {  // packed column 0: DC + i*Nyquist
 #pragma unroll
-        for (int j = 0; j < P::HH; ++j) v[j] = cadd(v[j], cmul_i(src[(2 * j + t) * P::SP + FW / 2]));
+        for (int j = 0; j < P::HH; ++j) v[j] = cadd(v[j], cmul_i(at((2 * j + t) * P::SP + FW / 2)));
     }
     pcol_inv<FH, FW>(v, T);
     __syncthreads();
@@ -655,9 +710,14 @@ int bwd_groups(int M) {
     return (M + PPW - 1) / PPW;
 }
 
-// Sample chunks of the dG reduction: enough threads (about 2^18) to keep HBM busy.
+// Sample chunks of the dG reduction.  Lane-pair grids (the fused k_pbwd_red): chunks of
+// kPChunk samples, which measured best against the larger row stacks they leave.  Otherwise
+// enough threads (about 2^18) to keep HBM busy, at most one load batch per chunk.
+constexpr int kPChunk = 8;
+
 template <int FH, int FW>
 int dg_chunks(int B, int M) {
+    if (pair_grid<FH, FW>()) return std::max(1, (B + kPChunk - 1) / kPChunk);
     const int per = M * WGeo<FH, FW>::F;
     const int by_threads = (262144 + per - 1) / per;
     const int by_batch = (B + kDgBatch - 1) / kDgBatch;  // at most one load batch per chunk
@@ -670,7 +730,7 @@ template <int FH, int FW>
 size_t bwd_ws(int B, int M) {
     if constexpr (pair_grid<FH, FW>()) {
         // cotangent half-spectra (M, B, pitch), dx spectra (B, F), dG and spectrum-sum chunk
-        // partials
+        // rows
         using P = PGeo<FH, FW>;
         const size_t nc = dg_chunks<FH, FW>(B, M);
         return ((size_t)M * B * spec_pitch<FH, FW>() + (size_t)B * P::F + 2 * nc * M * P::F) *
@@ -889,31 +949,56 @@ int launch_pbwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wo
                 float* dx, float* dghat, int accumulate, int conj_out, float* ssum, int sum_acc,
                 bool parts_mode, void* ws) {
     using P = PGeo<FH, FW>;
+    const int nb = dg_parts<FH, FW>(B, M);
+    const int bper = (B + nb - 1) / nb;
     cpx* spec = reinterpret_cast<cpx*>(ws);
     cpx* dxs = spec + (size_t)M * B * spec_pitch<FH, FW>();
-    cpx* dgpart = dxs + (size_t)B * P::F;
+    cpx* rows = dxs + (size_t)B * P::F;  // chunk rows when they are not the caller's
     const PLds ls(hout, P::PITCH, FW, FH, false);
     lds_limit(k_pspec<FH, FW>, ls.bytes);
     hipLaunchKernelGGL((k_pspec<FH, FW>), dim3(B * M), dim3(64), ls.bytes, st, B, M, hout, wout,
                        vec_ok(gz, (size_t)hout * wout), gz, spec);
     NC_CHECK_LAUNCH();
-    if (need_dx) {
-        hipLaunchKernelGGL((k_pdx_red<FH, FW>), dim3((P::F + 255) / 256, B), dim3(256), 0, st, B,
-                           M, spec, reinterpret_cast<const cpx*>(ghat), dxs);
+    // the chunk rows: the caller's row stacks, the outputs themselves (one chunk), or the
+    // workspace rows summed below
+    const bool direct = parts_mode || nb == 1;
+    cpx* dgr = direct ? reinterpret_cast<cpx*>(dghat) : rows;
+    cpx* sr = ssum ? (direct ? reinterpret_cast<cpx*>(ssum) : rows + (size_t)nb * M * P::F)
+                   : nullptr;
+    // four waves per workgroup, MG = ceil(M / 4) directions each
+    const dim3 grid((P::F + 63) / 64, nb);
+#define NC_PBWD(MG_)                                                                            \
+    hipLaunchKernelGGL((k_pbwd_red<FH, FW, MG_>), grid, dim3(256), 0, st, B, M, bper, need_dx,  \
+                       spec, reinterpret_cast<const cpx*>(xhat),                                \
+                       reinterpret_cast<const cpx*>(ghat), dxs, dgr, direct ? accumulate : 0,   \
+                       direct ? conj_out : 0, sr, direct ? sum_acc : 0)
+    if (M <= 4) NC_PBWD(1);
+    else if (M <= 8) NC_PBWD(2);
+    else if (M <= 16) NC_PBWD(4);
+    else if (M <= 32) NC_PBWD(8);
+    else if (M <= 64) NC_PBWD(16);
+    else return NC_ERR_UNSUPPORTED;  // more directions than the epilogues take (kMaxM)
+#undef NC_PBWD
+    NC_CHECK_LAUNCH();
+    if (!direct) {
+        hipLaunchKernelGGL(k_wbwd_dg_sum, dim3((P::F + 255) / 256, M, ssum ? 2 : 1), dim3(256), 0,
+                           st, nb, M, P::F, rows, reinterpret_cast<cpx*>(dghat), accumulate,
+                           conj_out, reinterpret_cast<cpx*>(ssum), sum_acc);
         NC_CHECK_LAUNCH();
+    }
+    if (need_dx) {
         if constexpr (seg_grid<FH, FW>()) {
-            const int rc = nc_seg_dx(st, B, hin, win, ph, pw, FH, FW, dxs, dx);
+            const int rc = nc_seg_dx(st, B, 1, hin, win, ph, pw, FH, FW, dxs, dx);
             if (rc != NC_OK) return rc;
         } else {
             const PLds lf(hin, P::PITCH, FW, FH, true);
             lds_limit(k_pdx_half<FH, FW>, lf.bytes);
             hipLaunchKernelGGL((k_pdx_half<FH, FW>), dim3(B), dim3(64), lf.bytes, st, hin, win,
-                               ph, pw, dxs, dx);
+                               ph, pw, 1, dxs, dx);
             NC_CHECK_LAUNCH();
         }
     }
-    return launch_dg<FH, FW>(st, B, M, spec, xhat, dghat, accumulate, conj_out, ssum, sum_acc,
-                             dgpart, parts_mode);
+    return NC_OK;
 }
 
 template <int FH, int FW>
@@ -957,12 +1042,12 @@ int launch_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wou
 template <int FH, int FW>
 int launch_hat_dx(hipStream_t st, int hin, int win, int ph, int pw, const cpx* dxs, float* dx) {
     if constexpr (seg_grid<FH, FW>()) {
-        return nc_seg_dx(st, 1, hin, win, ph, pw, FH, FW, dxs, dx);
+        return nc_seg_dx(st, 1, 1, hin, win, ph, pw, FH, FW, dxs, dx);
     } else if constexpr (pair_grid<FH, FW>()) {
         const PLds lf(hin, PGeo<FH, FW>::PITCH, FW, FH, true);
         lds_limit(k_pdx_half<FH, FW>, lf.bytes);
         hipLaunchKernelGGL((k_pdx_half<FH, FW>), dim3(1), dim3(64), lf.bytes, st, hin, win, ph,
-                           pw, dxs, dx);
+                           pw, 1, dxs, dx);
         NC_CHECK_LAUNCH();
         return NC_OK;
     }

@@ -227,7 +227,8 @@ __global__ __launch_bounds__(256) void k_lred(int B, int M, int F, int need_dx,
 // dx, last stage: sample b's spectrum is the fixed-order sum of its nchunk partials; the
 // inverse applies the unshifted roll (kernels_pallas.py:1798-1812): rows from (FH - ph) mod FH,
 // columns from (FW - pw) mod FW, hin x win kept; rows [i0, i0 + rs) here.
-template <int FH, int FW>
+// NCH > 0: a compile-time count of nchunk, so the partials' loads are issued together.
+template <int FH, int FW, int NCH>
 __global__ __launch_bounds__(kNT) void k_linv_dx(int B, int nchunk, int hin, int win, int ph,
                                                  int pw, int rs, const cpx* __restrict__ part,
                                                  float* __restrict__ dx) {
@@ -246,7 +247,12 @@ __global__ __launch_bounds__(kNT) void k_linv_dx(int B, int nchunk, int hin, int
             return packed_at<FW>(
                 [&](int e) {
                     cpx s = src[e];
-                    for (int c = 1; c < nchunk; ++c) s = cadd(s, src[c * cstride + e]);
+                    if constexpr (NCH > 0) {
+#pragma unroll
+                        for (int c = 1; c < NCH; ++c) s = cadd(s, src[c * cstride + e]);
+                    } else {
+                        for (int c = 1; c < nchunk; ++c) s = cadd(s, src[c * cstride + e]);
+                    }
                     return s;
                 },
                 kh, kw);
@@ -418,6 +424,10 @@ size_t bwd_ws(int B, int M) {
 }
 
 template <int FH, int FW>
+int seg_dx(hipStream_t st, int B, int nchunk, int hin, int win, int ph, int pw, const cpx* dxs,
+           float* dx);
+
+template <int FH, int FW>
 int conv_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph, int pw,
              const float* gz, const float* xhat, const float* ghat, int need_dx, float* dx,
              float* dghat, int accumulate, int conj_out, float* ssum, int sum_acc, void* ws) {
@@ -432,32 +442,38 @@ int conv_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout,
                        reinterpret_cast<const cpx*>(ghat), part, reinterpret_cast<cpx*>(dghat),
                        accumulate, conj_out, reinterpret_cast<cpx*>(ssum), sum_acc);
     NC_CHECK_LAUNCH();
-    if (need_dx) {
-        const int rs = inv_rows<FH, FW>(hin);
-        const size_t lds = linv_lds_bytes<FH, FW, kNT>(rs);
-        set_lds(k_linv_dx<FH, FW>, lds);
-        hipLaunchKernelGGL((k_linv_dx<FH, FW>), dim3(B, (hin + rs - 1) / rs), dim3(kNT), lds, st,
-                           B, nchunk, hin, win, ph, pw, rs, part, dx);
-        NC_CHECK_LAUNCH();
-    }
+    if (need_dx) return seg_dx<FH, FW>(st, B, nchunk, hin, win, ph, pw, part, dx);
     return NC_OK;
 }
 
-// dx_b = the inverse of B unpacked dx half-spectra (B, F) with the unshifted roll.
-template <int FH, int FW>
-int seg_dx(hipStream_t st, int B, int hin, int win, int ph, int pw, const cpx* dxs, float* dx) {
+// dx_b = the inverse of the sum of nchunk (nchunk, B, F) unpacked dx half-spectra, with the
+// unshifted roll.
+template <int FH, int FW, int NCH>
+void seg_dx_launch(hipStream_t st, int B, int nchunk, int hin, int win, int ph, int pw,
+                   const cpx* dxs, float* dx) {
     const int rs = inv_rows<FH, FW>(hin);
     const size_t lds = linv_lds_bytes<FH, FW, kNT>(rs);
-    set_lds(k_linv_dx<FH, FW>, lds);
-    hipLaunchKernelGGL((k_linv_dx<FH, FW>), dim3(B, (hin + rs - 1) / rs), dim3(kNT), lds, st, B, 1,
-                       hin, win, ph, pw, rs, dxs, dx);
+    set_lds(k_linv_dx<FH, FW, NCH>, lds);
+    hipLaunchKernelGGL((k_linv_dx<FH, FW, NCH>), dim3(B, (hin + rs - 1) / rs), dim3(kNT), lds, st,
+                       B, nchunk, hin, win, ph, pw, rs, dxs, dx);
+}
+
+template <int FH, int FW>
+int seg_dx(hipStream_t st, int B, int nchunk, int hin, int win, int ph, int pw, const cpx* dxs,
+           float* dx) {
+    if (nchunk == 1)
+        seg_dx_launch<FH, FW, 1>(st, B, nchunk, hin, win, ph, pw, dxs, dx);
+    else if (nchunk == 4)
+        seg_dx_launch<FH, FW, 4>(st, B, nchunk, hin, win, ph, pw, dxs, dx);
+    else
+        seg_dx_launch<FH, FW, 0>(st, B, nchunk, hin, win, ph, pw, dxs, dx);
     NC_CHECK_LAUNCH();
     return NC_OK;
 }
 
 template <int FH, int FW>
 int hat_dx(hipStream_t st, int hin, int win, int ph, int pw, const cpx* dxs, float* dx) {
-    return seg_dx<FH, FW>(st, 1, hin, win, ph, pw, dxs, dx);
+    return seg_dx<FH, FW>(st, 1, 1, hin, win, ph, pw, dxs, dx);
 }
 
 // The segmented transforms also serve the 64 x 64 grid's per-sample jobs (nc_seg_*).
@@ -560,9 +576,10 @@ int nc_seg_rfft2(hipStream_t st, int fh, int fw, int nplanes, int hin, int win, 
     return NC_ERR_UNSUPPORTED;
 }
 
-int nc_seg_dx(hipStream_t st, int B, int hin, int win, int ph, int pw, int fh, int fw,
+int nc_seg_dx(hipStream_t st, int B, int nchunk, int hin, int win, int ph, int pw, int fh, int fw,
               const void* dxs, float* dx) {
-#define NC_CALL(A, Bv) seg_dx<A, Bv>(st, B, hin, win, ph, pw, reinterpret_cast<const cpx*>(dxs), dx)
+#define NC_CALL(A, Bv) \
+    seg_dx<A, Bv>(st, B, nchunk, hin, win, ph, pw, reinterpret_cast<const cpx*>(dxs), dx)
     NC_DISPATCH_SEG(fh, fw, NC_CALL);
 #undef NC_CALL
     return NC_ERR_UNSUPPORTED;
