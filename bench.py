@@ -38,11 +38,17 @@ def synthetic(name, seed, B=None):
 
 def algorithmic_bytes(B, M, N, F, hb=0, dx=1, P=16):
     """Per-call algorithmic bytes (each interface operand counted once, 4 B/f32, 8 B/c64).
-    fftconv_fwd: x in, the border spectrum and ghat in, z out, xhat out.  fftconv_bwd: gz,
-    xhat, ghat in, dx out, dghat read-modify-write, the cotangent spectrum sum out.  The
-    step's epilogues run without a border term (hb = 0: it is folded into the spectra)."""
+    spectra: the state x in (once, however many partial planes hold it), the border spectrum
+    in, xhat out.  conv_epilogue_fwd: xhat and ghat in, w/s/b in, z out (training), the
+    step's output x' out (once), mean/rstd out.  correlate: xhat, ghat in, z out.
+    fftconv_bwd: gz, xhat, ghat in, dx out, dghat read-modify-write, the cotangent spectrum
+    sum out.  The step's epilogues run without a border term (hb = 0: it is folded into the
+    spectra)."""
     return {
-        "fftconv_fwd": 4 * B * N + 8 * F + 8 * M * F + 4 * B * M * N + 8 * B * F,
+        "spectra": 4 * B * N + 8 * F + 8 * B * F,
+        "conv_epilogue_fwd": 8 * B * F + 8 * M * F + 12 * N + 4 * B * M * N + 4 * B * N
+                             + 8 * B * M,
+        "correlate": 8 * B * F + 8 * M * F + 4 * B * M * N,
         "fftconv_bwd": (4 * B * M * N + 8 * B * F + 8 * M * F + dx * 4 * B * N + 16 * M * F
                         + 8 * M * F),
         "epilogue_fwd": 4 * (B * M * N + hb * M * N + 3 * N + B * N + 2 * B * M),
@@ -77,17 +83,19 @@ def kernel_families(ts, torch, reps):
     ws_ep, n_ep = ptr(p.ws_epi), p.ws_epi.numel() * 4
     ws_fc, n_fc = ptr(p.ws_fc), p.ws_fc.numel() * 4
     fams = {
-        "fftconv_fwd": lambda: call("nc_fftconv_fwd_parts", s(), B, M, h, w, h, w, p.cp[0],
-                                    p.cp[1], fh, fw, ptr(p.xs[t]), p.G, ptr(p.border_hat),
-                                    ptr(p.ghat), ptr(p.zs[t]), ptr(p.xhat[t])),
+        "spectra": lambda: call("nc_fftconv_spectra", s(), B, h, w, fh, fw, ptr(p.xs[t]), p.G,
+                                ptr(p.border_hat), ptr(p.xhat[t])),
+        "conv_epilogue_fwd": lambda: call("nc_fftconv_epilogue_fwd", s(), B, M, h, w, p.cp[0],
+                                          p.cp[1], fh, fw, ptr(p.xhat[t]), ptr(p.ghat), p.act,
+                                          p.slope, ptr(p.w_eff), ptr(p.s_eff), ptr(p.b_roi),
+                                          ptr(p.zs[t]), ptr(p.xs[t + 1]), ptr(p.mean[t]),
+                                          ptr(p.rstd[t]), ws_ep, n_ep),
+        "correlate": lambda: call("nc_spectral_correlate", s(), B, M, h, w, p.cp[0], p.cp[1],
+                                  fh, fw, ptr(p.xhat[t]), ptr(p.ghat), ptr(p.zs[t])),
         "fftconv_bwd": lambda: call("nc_fftconv_bwd_parts", s(), B, M, h, w, h, w, p.cp[0],
                                     p.cp[1], fh, fw, ptr(p.gz), ptr(p.xhat[t]), ptr(p.ghat), 1,
                                     ptr(p.gy[0]), ptr(p.rows["dg"]), 0, 0, ptr(p.rows["gd"]),
                                     0, ws_fc, n_fc),
-        "epilogue_fwd": lambda: call("nc_epilogue_fwd_parts", s(), B, M, h, w, p.act, p.slope, 0,
-                                     ptr(p.zs[t]), None, ptr(p.w_eff), ptr(p.s_eff),
-                                     ptr(p.b_roi), ptr(p.xs[t + 1]), ptr(p.mean[t]),
-                                     ptr(p.rstd[t]), ws_ep, n_ep),
         "epilogue_bwd": lambda: call("nc_epilogue_bwd_parts", s(), B, M, h, w, p.act, p.slope,
                                      0, ptr(p.zs[t]), None, ptr(p.w_eff), ptr(p.s_eff),
                                      ptr(p.b_roi), ptr(p.mean[t]), ptr(p.rstd[t]),
@@ -103,19 +111,20 @@ def kernel_families(ts, torch, reps):
                                  ptr(p.g_out), ptr(p.gz), ptr(p.pp_rows), B * p.P, ws_ep,
                                  n_ep),
     }
-    per_step = {"fftconv_fwd": p.d, "fftconv_bwd": p.d, "epilogue_fwd": p.d - 1,
-                "epilogue_bwd": p.d - 1, "port_fwd": 1, "port_bwd": 1}
+    per_step = {"spectra": p.d - 1, "conv_epilogue_fwd": p.d - 1, "correlate": 1,
+                "fftconv_bwd": p.d, "epilogue_bwd": p.d - 1, "port_fwd": 1, "port_bwd": 1}
     return {k: (time_family(f, reps, torch), per_step[k]) for k, f in fams.items()}
 
 
 # C-ABI family of each kernel of a --families-only run (k_batch_reduce belongs to whichever
 # backward family launched it: the preceding kernel decides).
 _FAMILY_KERNELS = {
-    "fftconv_fwd": ("k_wrfft2", "k_wconv_fwd", "k_lrfft2", "k_linv_conv", "k_prfft2",
-                    "k_pspectra", "k_lspectra", "k_pconv_fwd"),
+    "spectra": ("k_wrfft2", "k_lrfft2", "k_prfft2"),
+    "conv_epilogue_fwd": ("k_pconv_epi", "k_epi_fwd", "k_group_sum", "k_tile_stats",
+                          "k_tile_fwd"),
+    "correlate": ("k_wconv_fwd", "k_linv_conv", "k_pconv_fwd"),
     "fftconv_bwd": ("k_wbwd_part", "k_psum", "k_wbwd_dx_fin", "k_wbwd_dg_red", "k_wbwd_dg_sum",
-                    "k_lred", "k_linv_dx", "k_pspec", "k_pdx_red", "k_pdx_half"),
-    "epilogue_fwd": ("k_epi_fwd", "k_group_sum", "k_tile_stats", "k_tile_fwd"),
+                    "k_lred", "k_linv_dx", "k_pspec", "k_pbwd_red", "k_pdx_half"),
     "epilogue_bwd": ("k_epi_bwd", "k_tile_bwd1", "k_tile_bwd2"),
     "port_fwd": ("k_port_fwd", "k_port_combine", "k_port_fwd_tiled"),
     "port_bwd": ("k_port_bwd",),

@@ -298,6 +298,38 @@ int nc_epilogue_fwd_parts(void* stream, int B, int M, int h, int w, int act, flo
                           float* rstd, void* ws, size_t ws_bytes);
 
 /*
+ * The cell spectra of one propagation step: xhat (B, fft_h, fft_w/2+1) complex = rfft2 of
+ * the cell state x = sum over q < n_parts of x_parts[q] (n_parts, B, hin, win), summed in
+ * increasing q, plus xhat_add (one (fft_h, fft_w/2+1) spectrum, or NULL) - the first half of
+ * nc_fftconv_fwd_parts (kernels_pallas.py:1779-1791).  No counterpart in the reference.
+ */
+int nc_fftconv_spectra(void* stream, int B, int hin, int win, int fft_h, int fft_w,
+                       const float* x_parts, int n_parts, const float* xhat_add, float* xhat);
+
+/*
+ * The number G >= 1 of partial output planes per sample that nc_fftconv_epilogue_fwd writes:
+ * ceil(M/4) where the fused kernel runs (the 64-wide grids, planes whose staging fits), else
+ * nc_epilogue_fwd_partials(B, M, h, w).
+ */
+int nc_fftconv_epilogue_partials(int B, int M, int h, int w, int fft_h, int fft_w);
+
+/*
+ * The correlation step (nc_spectral_correlate) and the hidden-step epilogue without a border
+ * term (nc_epilogue_fwd_parts with has_border = 0) as one operation - kernels_pallas.py:
+ * 1779-1791 followed by 163-291: parts (G, B, hout, wout) with G =
+ * nc_fftconv_epilogue_partials, mean/rstd (B, M).  z (B, M, hout, wout) receives the
+ * correlation when not NULL (a training forward keeps it for the backward); on the 64-wide
+ * grids it may be NULL (evaluation), elsewhere it is required as the epilogue's input.  ws:
+ * nc_epilogue_workspace_size(B, M, hout, wout) bytes where the fused kernel does not run
+ * (unused, may be NULL, where it does).  No counterpart in the reference (two ops there).
+ */
+int nc_fftconv_epilogue_fwd(void* stream, int B, int M, int hout, int wout, int pad_h,
+                            int pad_w, int fft_h, int fft_w, const float* xhat,
+                            const float* ghat, int act, float neg_slope, const float* w_eff,
+                            const float* s_eff, const float* b_roi, float* z, float* parts,
+                            float* mean, float* rstd, void* ws, size_t ws_bytes);
+
+/*
  * pallas_fused_roi_step_epilogue backward rule (kernels_pallas.py:869-1064): writes gz
  * (B,M,h,w), gdb = sum_b gz (M,h,w) when has_border and gdb is not NULL (a caller that forms
  * the border cotangent from the spectra, nc_fftconv_bwd_ex, passes NULL) and gw/gs/gb (h,w).

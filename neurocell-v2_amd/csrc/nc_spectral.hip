@@ -662,6 +662,131 @@ __global__ __launch_bounds__(64) void k_pconv_fwd(int M, int hout, int wout, int
     pstage_copy<FW>(lds, hout, wout, z + (size_t)g * hout * wout);
 }
 
+// Forward correlation fused with the hidden-step epilogue (kernels_pallas.py:1779-1791 then
+// 163-291): workgroup (b, g) of 4 wavefronts, wavefront w computing the plane m = 4g + w as
+// k_pconv_fwd does (storing it to z when z is given), then its plane statistics (mean, then
+// the centred sum of squares: population variance, eps 1e-5), zhat and act(zhat + b_roi).
+// Each wavefront leaves (zhat, act) in its own LDS region; the workgroup adds the four in
+// increasing m and writes the direction group's partial output
+// parts[g][b] = w_eff * sum zhat + s_eff * sum act, the layout of nc_epilogue_fwd_parts.
+// NE >= ceil(N / 64) plane values per lane; every loop runs NE (or NE / 4) times with clamped
+// loads, so a wavefront's loads issue together.
+template <int FH, int FW, int ACT, int NE>
+__global__ __launch_bounds__(256, 2) void k_pconv_epi(int B, int M, int hout, int wout, int ph,
+                                                   int pw, int nq_off, int region, float slope,
+                                                   const cpx* __restrict__ xhat,
+                                                   const cpx* __restrict__ ghat,
+                                                   const float* __restrict__ w_eff,
+                                                   const float* __restrict__ s_eff,
+                                                   const float* __restrict__ b_roi,
+                                                   float* __restrict__ z,
+                                                   float* __restrict__ parts,
+                                                   float* __restrict__ mean,
+                                                   float* __restrict__ rstd) {
+    using P = PGeo<FH, FW>;
+    constexpr int NC = NE / 4;  // output pixels per thread in the combine
+    HIP_DYNAMIC_SHARED(float, ldsall)
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float* lds = ldsall + (size_t)wv * region;
+    cpx* T = reinterpret_cast<cpx*>(lds);
+    cpx* NQ = T + nq_off;
+    const int b = blockIdx.x, g = blockIdx.y;
+    // the idle wavefronts of the last group (4g + w >= M) repeat direction M - 1, store
+    // nothing and leave zeros in their region, so control flow stays uniform
+    const int m = min(g * 4 + wv, M - 1);
+    const bool live = g * 4 + wv < M;
+    const int N = hout * wout;
+    const float inv_n = 1.0f / (float)N;
+    const int kc = lane >> 1, t = lane & 1;
+    const cpx* X = xhat + (size_t)b * P::F;
+    const cpx* Gm = ghat + (size_t)m * P::F;
+    if (lane < FH) NQ[lane] = cmul(X[lane * P::SP + FW / 2], Gm[lane * P::SP + FW / 2]);
+    cpx v[P::HH];
+#pragma unroll
+    for (int j = 0; j < P::HH; ++j) {
+        const int e = (2 * j + t) * P::SP + kc;
+        v[j] = cmul(X[e], Gm[e]);
+    }
+    __syncthreads();
+    if (kc == 0) {
+#pragma unroll
+        for (int j = 0; j < P::HH; ++j) v[j] = cadd(v[j], cmul_i(NQ[2 * j + t]));
+    }
+    pcol_inv<FH, FW>(v, T);
+    __syncthreads();
+    prow_inv<FH, FW>(T, ph, pw, hout, 1.0f / (float)(FH * FW), lds);
+    __syncthreads();
+    // the per-pixel parameters, requested together; their latency hides behind the statistics
+    float bv[NE], wq[NC], sq_[NC];
+#pragma unroll
+    for (int i = 0; i < NE; ++i) bv[i] = b_roi[min(lane + 64 * i, N - 1)];
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+        const int e = min((int)threadIdx.x + 256 * i, N - 1);
+        wq[i] = w_eff[e];
+        sq_[i] = s_eff[e];
+    }
+    // the plane, element e = lane + 64 i at (e / wout, e % wout) of the staging
+    const unsigned inv = ((1u << 20) + wout - 1) / wout;
+    float zv[NE];
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+        const int e = min(lane + 64 * i, N - 1);
+        const int r = (int)(((unsigned)e * inv) >> 20);
+        zv[i] = lds[r * (FW + 1) + (e - r * wout)];
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < NE; ++i) sum += lane + 64 * i < N ? zv[i] : 0.f;
+    if (z && live) {
+        float* zo = z + ((size_t)b * M + m) * N;
+#pragma unroll
+        for (int i = 0; i < NE; ++i)
+            if (lane + 64 * i < N) zo[lane + 64 * i] = zv[i];
+    }
+    const float mu = wave_sum(sum) * inv_n;
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+        const float d = lane + 64 * i < N ? zv[i] - mu : 0.f;
+        ss += d * d;
+    }
+    const float r = 1.0f / sqrtf(wave_sum(ss) * inv_n + 1e-5f);
+    if (lane == 0 && live) {
+        mean[(size_t)b * M + m] = mu;
+        rstd[(size_t)b * M + m] = r;
+    }
+    // (zhat, act) replace the staging in this wavefront's region: every lane has read the
+    // plane above, and one wavefront's LDS operations complete in order
+    const float on = live ? 1.f : 0.f;
+    float* L = lds;
+    float* A = lds + N;
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+        const int e = lane + 64 * i;
+        const float zn = (zv[i] - mu) * r;
+        const float a = act_f<ACT>(zn + bv[i], slope);
+        if (e < N) {
+            L[e] = zn * on;
+            A[e] = a * on;
+        }
+    }
+    __syncthreads();
+    float* out = parts + ((size_t)g * B + b) * N;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+        const int e = (int)threadIdx.x + 256 * i;
+        const int ec = min(e, N - 1);
+        float lin = ldsall[ec], ac = ldsall[N + ec];
+#pragma unroll
+        for (int q = 1; q < 4; ++q) {
+            lin += ldsall[(size_t)q * region + ec];
+            ac += ldsall[(size_t)q * region + N + ec];
+        }
+        if (e < N) out[e] = wq[i] * lin + sq_[i] * ac;
+    }
+}
+
 // ----------------------------------------------------------------------------------------
 // Launch plumbing
 // ----------------------------------------------------------------------------------------
@@ -855,6 +980,68 @@ int launch_corr(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw
                        reinterpret_cast<const cpx*>(xhat), reinterpret_cast<const cpx*>(ghat), z);
     NC_CHECK_LAUNCH();
     return NC_OK;
+}
+
+// Per-wavefront LDS region (floats) of the fused correlation + hidden epilogue: the inverse
+// transform's staging, or the plane's (zhat, act) pair, whichever is larger; 0 when four
+// regions do not fit one workgroup's LDS.
+template <int FH, int FW>
+int corr_epi_region(int hout, int wout) {
+    const PLds l(hout, PGeo<FH, FW>::PITCH, FW, FH, true);
+    const size_t fl = std::max(l.bytes / sizeof(float), (size_t)2 * hout * wout);
+    const size_t region = (fl + 15) / 16 * 16;
+    return 4 * region * sizeof(float) <= 163840 ? (int)region : 0;
+}
+
+int corr_epi_region(int fft_h, int fft_w, int hout, int wout) {
+    if (fft_w != 64 || hout <= 0 || wout <= 0 || hout > fft_h || wout > fft_w) return 0;
+    if (fft_h == 64) return corr_epi_region<64, 64>(hout, wout);
+    if (fft_h == 32) return corr_epi_region<32, 64>(hout, wout);
+    return 0;
+}
+
+// The fused correlation + hidden epilogue on the lane-pair grids; false when the plane is
+// too large for the per-wavefront LDS region (the caller falls back).
+template <int FH, int FW>
+bool launch_corr_epi(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw, int act,
+                     float slope, const float* xhat, const float* ghat, const float* w_eff,
+                     const float* s_eff, const float* b_roi, float* z, float* parts,
+                     float* mean, float* rstd) {
+    if constexpr (!pair_grid<FH, FW>()) {
+        return false;
+    } else {
+        const PLds l(hout, PGeo<FH, FW>::PITCH, FW, FH, true);
+        const int region = corr_epi_region<FH, FW>(hout, wout);
+        if (region == 0) return false;
+        const size_t bytes = (size_t)4 * region * sizeof(float);
+        const dim3 grid(B, (M + 3) / 4);
+        const int N = hout * wout;
+#define NC_CE2(A_, NE_)                                                                        \
+    do {                                                                                       \
+        lds_limit(k_pconv_epi<FH, FW, A_, NE_>, bytes);                                        \
+        hipLaunchKernelGGL((k_pconv_epi<FH, FW, A_, NE_>), grid, dim3(256), bytes, st, B, M,   \
+                           hout, wout, ph, pw, l.nq, region, slope,                            \
+                           reinterpret_cast<const cpx*>(xhat),                                 \
+                           reinterpret_cast<const cpx*>(ghat), w_eff, s_eff, b_roi, z, parts,  \
+                           mean, rstd);                                                        \
+    } while (0)
+#define NC_CE(A_)                                                        \
+    do {                                                                 \
+        if (FH * FW > 2048 && N > 2048) NC_CE2(A_, FH * FW / 64);       \
+        else NC_CE2(A_, 32);                                             \
+    } while (0)
+        switch (act) {
+            case NC_ACT_TANH: NC_CE(NC_ACT_TANH); break;
+            case NC_ACT_SIGMOID: NC_CE(NC_ACT_SIGMOID); break;
+            case NC_ACT_RELU: NC_CE(NC_ACT_RELU); break;
+            case NC_ACT_LEAKY_RELU: NC_CE(NC_ACT_LEAKY_RELU); break;
+            case NC_ACT_GELU: NC_CE(NC_ACT_GELU); break;
+            default: NC_CE(NC_ACT_IDENTITY);
+        }
+#undef NC_CE
+#undef NC_CE2
+        return true;
+    }
 }
 
 template <int FH, int FW>
@@ -1221,6 +1408,67 @@ int nc_spectral_correlate(void* stream, int B, int M, int hout, int wout, int pa
     NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
 #undef NC_CALL
     return NC_ERR_UNSUPPORTED;
+}
+
+int nc_fftconv_spectra(void* stream, int B, int hin, int win, int fft_h, int fft_w,
+                       const float* x_parts, int n_parts, const float* xhat_add, float* xhat) {
+    if (B <= 0 || hin <= 0 || win <= 0 || hin > fft_h || win > fft_w || !x_parts ||
+        n_parts <= 0 || !xhat)
+        return NC_ERR_INVALID_ARGUMENT;
+    hipStream_t st = nc_stream(stream);
+    const size_t qs = (size_t)B * hin * win;
+    if (nc_large_grid(fft_h, fft_w))
+        return nc_seg_rfft2(st, fft_h, fft_w, B, hin, win, 0, x_parts, xhat, xhat_add, 0, 0,
+                            n_parts, qs);
+    if (!pow2_ok(fft_h) || !pow2_ok(fft_w)) return NC_ERR_UNSUPPORTED;
+    const SpecPost post{reinterpret_cast<const cpx*>(xhat_add), 0, 0};
+#define NC_CALL(A, Bv)                                                                   \
+    launch_rfft2<A, Bv>(st, B, hin, win, false, x_parts, reinterpret_cast<cpx*>(xhat), \
+                        xhat_add ? kPostAdd : kPostNone, post, n_parts, qs)
+    NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
+#undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
+}
+
+int nc_fftconv_epilogue_partials(int B, int M, int h, int w, int fft_h, int fft_w) {
+    if (B <= 0 || M <= 0 || h <= 0 || w <= 0) return 0;
+    if (corr_epi_region(fft_h, fft_w, h, w) > 0) return (M + 3) / 4;
+    return nc_epilogue_fwd_partials(B, M, h, w);
+}
+
+int nc_fftconv_epilogue_fwd(void* stream, int B, int M, int hout, int wout, int pad_h,
+                            int pad_w, int fft_h, int fft_w, const float* xhat,
+                            const float* ghat, int act, float neg_slope, const float* w_eff,
+                            const float* s_eff, const float* b_roi, float* z, float* parts,
+                            float* mean, float* rstd, void* ws, size_t ws_bytes) {
+    int rc = fftconv_check(B, M, 1, 1, hout, wout, pad_h, pad_w, fft_h, fft_w);
+    if (rc != NC_OK) return rc;
+    if (!xhat || !ghat || !w_eff || !s_eff || !b_roi || !parts || !mean || !rstd || act < 0 ||
+        act > 5)
+        return NC_ERR_INVALID_ARGUMENT;
+    hipStream_t st = nc_stream(stream);
+    bool done = false;
+    if (corr_epi_region(fft_h, fft_w, hout, wout) > 0) {
+        if (fft_h == 64)
+            done = launch_corr_epi<64, 64>(st, B, M, hout, wout, pad_h, pad_w, act, neg_slope,
+                                           xhat, ghat, w_eff, s_eff, b_roi, z, parts, mean,
+                                           rstd);
+        else
+            done = launch_corr_epi<32, 64>(st, B, M, hout, wout, pad_h, pad_w, act, neg_slope,
+                                           xhat, ghat, w_eff, s_eff, b_roi, z, parts, mean,
+                                           rstd);
+        if (done) {
+            NC_CHECK_LAUNCH();
+            return NC_OK;
+        }
+    }
+    // other grids: the correlation into z, then the epilogue's partial outputs
+    if (!z) return NC_ERR_INVALID_ARGUMENT;
+    rc = nc_spectral_correlate(stream, B, M, hout, wout, pad_h, pad_w, fft_h, fft_w, xhat, ghat,
+                               z);
+    if (rc != NC_OK) return rc;
+    return nc_epilogue_fwd_parts(stream, B, M, hout, wout, act, neg_slope, 0, z, nullptr, w_eff,
+                                 s_eff, b_roi, parts, mean, rstd, ws, ws_bytes);
 }
 
 size_t nc_fftconv_bwd_workspace_size(int B, int M, int fft_h, int fft_w) {

@@ -75,6 +75,10 @@ _SIGS = {
     "nc_plane_spectrum": (I, [P, I, I, I, I, I, I, I, P, P]),
     "nc_plane_spectra": (I, [P, I, I, I, C.POINTER(SpectrumJob)]),
     "nc_spectral_correlate": (I, [P, I, I, I, I, I, I, I, I, P, P, P]),
+    "nc_fftconv_spectra": (I, [P, I, I, I, I, I, P, I, P, P]),
+    "nc_fftconv_epilogue_partials": (I, [I, I, I, I, I, I]),
+    "nc_fftconv_epilogue_fwd": (I, [P, I, I, I, I, I, I, I, I, P, P, I, F, P, P, P, P, P, P, P,
+                                    P, SZ]),
     "nc_fftconv_bwd_workspace_size": (SZ, [I, I, I, I]),
     "nc_fftconv_bwd": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, I, P, P, I, I, P, SZ]),
     "nc_fftconv_bwd_ex": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, I, P, P, I, I, P, I, P,

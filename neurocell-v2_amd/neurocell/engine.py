@@ -234,7 +234,7 @@ class StepPlan:
         nz = d if self.training else 1
         # step states t >= 1 as the epilogue's uncombined direction-group partials (G planes
         # per sample, summed by the next step's transform as it loads them)
-        self.G = _abi_int("nc_epilogue_fwd_partials", B, M, h, w)
+        self.G = _abi_int("nc_fftconv_epilogue_partials", B, M, h, w, *self.fft)
         self.xs = [self.x0] + [torch.empty(self.G, B, h, w, **f) for _ in range(d - 1)]
         self.zs = [torch.empty(B, M, h, w, **f) for _ in range(nz)]
         # cell spectra: one per step for the reverse pass, one shared buffer for evaluation
@@ -314,6 +314,9 @@ class StepPlan:
             jobs.append((_addr(self.patch), _addr(self.border_hat), None, 1, self.Hp, self.Wp, 0,
                          self.bshift[0], self.bshift[1]))
         call("nc_plane_spectra", s, fh, fw, len(jobs), _abi.spectrum_jobs(*jobs))
+        # hidden steps: the correlation and the epilogue run as one kernel on the 32x64 and
+        # 64x64 grids, where evaluation never materialises z
+        fused = fw == 64 and fh in (32, 64)
         for t in range(self.d):
             last = t == self.d - 1
             z = self.zs[t if self.training else 0]
@@ -324,19 +327,22 @@ class StepPlan:
                     p0 = (self.kh - 1 + r0, self.kw - 1 + c0)
                 else:
                     p0 = self.cp
-                call("nc_spectral_correlate", s, B, M, h, w, p0[0], p0[1], fh, fw, ptr(xh0),
-                     ptr(self.ghat), ptr(z))
+                xh = xh0
             else:
-                call("nc_fftconv_fwd_parts", s, B, M, h, w, h, w, self.cp[0], self.cp[1], fh,
-                     fw, ptr(self.xs[t]), self.G, ptr(self.border_hat), ptr(self.ghat), ptr(z),
-                     ptr(xh))
+                p0 = self.cp
+                # z + delta comes out of the correlation: the border spectrum joins x's
+                call("nc_fftconv_spectra", s, B, h, w, fh, fw, ptr(self.xs[t]), self.G,
+                     ptr(self.border_hat), ptr(xh))
             # z already holds z + delta: the epilogues run without their border term
             if not last:
-                call("nc_epilogue_fwd_parts", s, B, M, h, w, self.act, self.slope, 0, ptr(z), None,
-                     ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi), ptr(self.xs[t + 1]),
-                     ptr(self.mean[t]), ptr(self.rstd[t]), ptr(self.ws_epi),
-                     self.ws_epi.numel() * 4)
+                zk = None if fused and not self.training else z
+                call("nc_fftconv_epilogue_fwd", s, B, M, h, w, p0[0], p0[1], fh, fw, ptr(xh),
+                     ptr(self.ghat), self.act, self.slope, ptr(self.w_eff), ptr(self.s_eff),
+                     ptr(self.b_roi), ptr(zk), ptr(self.xs[t + 1]), ptr(self.mean[t]),
+                     ptr(self.rstd[t]), ptr(self.ws_epi), self.ws_epi.numel() * 4)
             else:
+                call("nc_spectral_correlate", s, B, M, h, w, p0[0], p0[1], fh, fw, ptr(xh),
+                     ptr(self.ghat), ptr(z))
                 call("nc_port_fwd", s, B, M, h, w, 0, self.fact, self.fslope, self.P,
                      ptr(self.port_idx), ptr(z), None, ptr(self.pp), ptr(self.out),
                      ptr(self.zo), ptr(self.mean[t]), ptr(self.rstd[t]), ptr(self.pre),

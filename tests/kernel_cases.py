@@ -402,6 +402,71 @@ def case_epilogue_parts(be, B=3, M=9, h=10, w=12, kh=5, kw=3, FH=16, FW=16, seed
             "xhat_mismatch": int((be.get(x1) != be.get(x2)).sum())}
 
 
+def case_fftconv_epilogue(be, B=3, M=6, h=20, w=27, kh=7, kw=5, FH=32, FW=64, act="tanh",
+                          seed=8):
+    """nc_fftconv_spectra + nc_fftconv_epilogue_fwd (the fused correlation and hidden epilogue)
+    against nc_fftconv_fwd_parts + nc_epilogue_fwd_parts and the oracle.  The cell state comes
+    in two partial planes; M = 6 leaves two idle wavefronts in the last direction group; the
+    call without z must give the same parts/mean/rstd bit for bit as the one with z."""
+    rng = np.random.default_rng(seed)
+    L, s = be.lib, be.stream()
+    ph, pw = (kh - 1) // 2, (kw - 1) // 2
+    x = (rng.normal(size=(B, h, w)) * 0.7).astype(np.float32)
+    x0 = (rng.normal(size=(B, h, w)) * 0.2).astype(np.float32)
+    xp = np.stack([x0, x - x0])  # two partial planes; their fp32 sum is the state the kernels see
+    xs = (xp[0] + xp[1]).astype(np.float32)
+    g = rng.normal(size=(M, 1, kh, kw)).astype(np.float32)
+    wv = rng.normal(size=(h, w)).astype(np.float32)
+    sv = rng.uniform(size=(h, w)).astype(np.float32)
+    bv = rng.normal(size=(h, w)).astype(np.float32)
+    xpd, gd, wd, sd, bd = (be.put(a) for a in (xp, g, wv, sv, bv))
+    aid = _abi.ACT_IDS[act]
+    ghat = be.zeros((M, FH, FW // 2 + 1, 2))
+    _ok(be, L.nc_filter_spectrum_fwd(s, M, kh, kw, FH, FW, be.ptr(gd), be.ptr(ghat)), "spec")
+    xh1, xh2 = be.zeros((B, FH, FW // 2 + 1, 2)), be.zeros((B, FH, FW // 2 + 1, 2))
+    _ok(be, L.nc_fftconv_spectra(s, B, h, w, FH, FW, be.ptr(xpd), 2, None, be.ptr(xh1)),
+        "spectra")
+    # the separate path: correlation (+ spectra) then the epilogue's partial outputs
+    z_ref = be.zeros((B, M, h, w))
+    _ok(be, L.nc_fftconv_fwd_parts(s, B, M, h, w, h, w, ph, pw, FH, FW, be.ptr(xpd), 2, None,
+                                   be.ptr(ghat), be.ptr(z_ref), be.ptr(xh2)), "fwd_parts")
+    Gs = L.nc_epilogue_fwd_partials(B, M, h, w)
+    ws = be.zeros((L.nc_epilogue_workspace_size(B, M, h, w) // 4 + 1,))
+    nb = ws.nbytes if hasattr(ws, "nbytes") else ws.numel() * 4
+    p_ref, m_ref, r_ref = be.zeros((Gs, B, h, w)), be.zeros((B, M)), be.zeros((B, M))
+    _ok(be, L.nc_epilogue_fwd_parts(s, B, M, h, w, aid, 0.01, 0, be.ptr(z_ref), None, be.ptr(wd),
+                                    be.ptr(sd), be.ptr(bd), be.ptr(p_ref), be.ptr(m_ref),
+                                    be.ptr(r_ref), be.ptr(ws), nb), "epi_parts")
+    # the fused path, with and (on the fused grids) without z
+    G = L.nc_fftconv_epilogue_partials(B, M, h, w, FH, FW)
+    fused = FW == 64 and FH in (32, 64)
+    z1 = be.zeros((B, M, h, w))
+    outs = []
+    for zz in ((z1, None) if fused else (z1,)):
+        p, mu, rs = be.zeros((G, B, h, w)), be.zeros((B, M)), be.zeros((B, M))
+        _ok(be, L.nc_fftconv_epilogue_fwd(s, B, M, h, w, ph, pw, FH, FW, be.ptr(xh1),
+                                          be.ptr(ghat), aid, 0.01, be.ptr(wd), be.ptr(sd),
+                                          be.ptr(bd), be.ptr(zz), be.ptr(p), be.ptr(mu),
+                                          be.ptr(rs), be.ptr(ws), nb), "fused")
+        outs.append(tuple(be.get(a) for a in (p, mu, rs)))
+    p1, mu1, rs1 = outs[0]
+    out1 = p1.astype(np.float64).sum(0)
+    out_ref = be.get(p_ref).astype(np.float64).sum(0)
+    zo = O.conv2d_direct(xs, g[:, 0], (ph, pw))
+    o_or, m_or, r_or = O.epilogue_fwd(zo, np.zeros((M, h, w), np.float32), wv, sv, bv, act,
+                                      False)
+    res = {"G": G if fused else -1,
+           "xhat_mismatch": int((be.get(xh1) != be.get(xh2)).sum()),
+           "z": rel_l2(be.get(z1), zo),
+           "z_vs_separate": rel_l2(be.get(z1), be.get(z_ref)),
+           "out": rel_l2(out1, o_or),
+           "out_vs_separate": rel_l2(out1, out_ref),
+           "mean": rel_l2(mu1, m_or), "rstd": rel_l2(rs1, r_or)}
+    if fused:
+        res["no_z_mismatch"] = sum(int((a != b).sum()) for a, b in zip(outs[0], outs[1]))
+    return res
+
+
 def case_port(be, B=3, M=5, h=10, w=12, rows=(2, 3, 4, 2), cols=(5, 5, 5, 5), fact=None,
               seed=3):
     """Output-port forward/backward (rect-like and coordinate ports, duplicates included)."""

@@ -7,6 +7,7 @@ import pytest
 
 from kernel_cases import (CODD_CASES, TOL, HostBackend, case_adaptive, case_border_conv,
                           case_border_fold, case_codd, case_epilogue, case_epilogue_parts,
+                          case_fftconv_epilogue,
                           case_fftconv, case_helpers, case_plane_spectra, case_port)
 
 
@@ -101,3 +102,17 @@ def test_epilogue_parts(be, B, M, h, w, FH, FW):
     assert res["G"] >= 1 and res["out"] < TOL, res
     assert res["parts_sum_mismatch"] == 0 and res["z_mismatch"] == 0, res
     assert res["xhat_mismatch"] == 0, res
+
+
+@pytest.mark.parametrize("B,M,h,w,kh,kw,FH,FW,act", [
+    (3, 6, 20, 27, 7, 5, 32, 64, "tanh"),          # fused, idle wavefronts in the last group
+    (2, 16, 40, 50, 23, 13, 64, 64, "leaky_relu"),  # fused, the ALU geometry
+    (3, 5, 10, 12, 5, 3, 16, 16, "gelu"),           # not fused: correlation + epilogue
+])
+def test_fftconv_epilogue(be, B, M, h, w, kh, kw, FH, FW, act):
+    res = case_fftconv_epilogue(be, B=B, M=M, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW, act=act)
+    if FW == 64:
+        assert res["G"] == (M + 3) // 4 and res["no_z_mismatch"] == 0, res
+    assert res["xhat_mismatch"] == 0, res
+    _assert_small({k: res[k] for k in ("z", "z_vs_separate", "out", "out_vs_separate", "mean",
+                                       "rstd")})
