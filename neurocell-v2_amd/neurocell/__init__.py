@@ -24,6 +24,8 @@ from .propagator import (SUPPORTED_BACKENDS, inject_inputs_roi_2d, propagate_vnn
 from .adaptive_mask import (AdaptiveMaskSpec, compute_adaptive_spatial_mask,
                             estimate_effective_filter_radii)
 from .model import VonNeumannNetwork
+from .datasets import (ALUDeviceDataset, alu_truth_table, generate_arithmetic,
+                       generate_arithmetic_logic, prepare_alu_device_dataset)
 from .trainer import (AdamW, AdamWState, VNNTrainer, adamw, compute_annealed_temperature,
                       constant_schedule, cosine_decay_schedule, default_exact_match_metric,
                       default_mse_loss, linear_schedule, packbits_u8_on_device,
@@ -44,6 +46,8 @@ __all__ = [
     "SUPPORTED_BACKENDS", "select_optimal_backend", "inject_inputs_roi_2d", "propagate_vnn_2d",
     "AdaptiveMaskSpec", "estimate_effective_filter_radii", "compute_adaptive_spatial_mask",
     "VonNeumannNetwork",
+    "ALUDeviceDataset", "generate_arithmetic", "generate_arithmetic_logic",
+    "prepare_alu_device_dataset", "alu_truth_table",
     "VNNTrainer", "AdamW", "AdamWState", "adamw", "constant_schedule", "linear_schedule",
     "cosine_decay_schedule", "warmup_cosine_decay_schedule", "compute_annealed_temperature",
     "packbits_u8_on_device", "default_mse_loss", "default_exact_match_metric",
