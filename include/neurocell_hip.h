@@ -75,7 +75,8 @@ const char* nc_strerror(int status);
  *      ROI (uncropped) row then column indices of the P output-port cells.
  * Out: w_eff, s_eff, b_roi (h,w) for the active sub-ROI (h = r1-r0, w = c1-c0);
  *      border_patch (h+kh-1, w+kw-1) = act(B)*s_prob with the ROI zeroed, cut at grid
- *      offset (r0, c0); port_params (3,P) = [w_eff_out, s_eff_out, b_out]; optional (NULL
+ *      offset (r0, c0) (with pad 0, the SAME / CIRCULAR modes, the ROI is the whole grid:
+ *      the patch is zero on the grid and its cells beyond the grid are left unwritten); port_params (3,P) = [w_eff_out, s_eff_out, b_out]; optional (NULL
  *      to skip) full-grid s_prob, border_2d = act(B)*s_prob and w_pinned, each (H,W).
  * inv_tau is 1/max(tau, 1e-4) rounded to float32 (params.py:63).
  */
@@ -129,6 +130,9 @@ int nc_filter_spectrum_bwd(void* stream, int M, int kh, int kw, int fft_h, int f
  * (the correlation reads it back).
  * Supported spectral grids: fft_h, fft_w both in {16, 32, 64} (wavefront transforms) or
  * both in {64, 128, 256} (workgroup transforms over LDS segments).
+ * The output window is read modulo the grid (pad_h < fft_h, hout <= fft_h, and likewise
+ * for w): with the grid equal to the plane, hin = hout = fft_h, this is the circular
+ * correlation of the reference's CIRCULAR padding mode (propagator.py:284-300).
  */
 int nc_fftconv_fwd(void* stream, int B, int M, int hin, int win, int hout, int wout, int pad_h,
                    int pad_w, int fft_h, int fft_w, const float* x, const float* ghat, float* z,

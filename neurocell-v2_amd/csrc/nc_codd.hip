@@ -382,8 +382,11 @@ int chip_ok(const nc_chip_desc* c) {
     if (c->roi_h <= 0 || c->roi_w <= 0) return 0;
     if (c->r0 < 0 || c->r1 > c->roi_h || c->r0 >= c->r1) return 0;
     if (c->c0 < 0 || c->c1 > c->roi_w || c->c0 >= c->c1) return 0;
-    // the sub-ROI's receptive field must stay inside the grid
-    if (c->r1 + c->kh - 1 > c->H || c->c1 + c->kw - 1 > c->W) return 0;
+    // with a padded ROI (VALID) the sub-ROI's receptive field must stay inside the grid; with
+    // none (SAME / CIRCULAR: the grid is the ROI) there is no border and the patch's cells
+    // beyond the grid are never formed
+    if ((c->pad_h > 0 || c->pad_w > 0) && (c->r1 + c->kh - 1 > c->H || c->c1 + c->kw - 1 > c->W))
+        return 0;
     return 1;
 }
 

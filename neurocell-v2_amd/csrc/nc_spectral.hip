@@ -1320,7 +1320,9 @@ static int fftconv_check(int B, int M, int hin, int win, int hout, int wout, int
         pw < 0)
         return NC_ERR_INVALID_ARGUMENT;
     if (!(pow2_ok(fh) && pow2_ok(fw)) && !nc_large_grid(fh, fw)) return NC_ERR_UNSUPPORTED;
-    if (hin > fh || win > fw || ph + hout > fh || pw + wout > fw) return NC_ERR_INVALID_ARGUMENT;
+    // the output window is read modulo the grid: a circular correlation where it wraps
+    if (hin > fh || win > fw || hout > fh || wout > fw || ph >= fh || pw >= fw)
+        return NC_ERR_INVALID_ARGUMENT;
     return NC_OK;
 }
 

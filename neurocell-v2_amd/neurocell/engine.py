@@ -118,9 +118,6 @@ class StepPlan:
     def __init__(self, topology: ChipTopology2D, batch_size: int, port_shapes: list,
                  roi_bbox=None, activate="tanh", final_activate=None, hard_pin_io=False,
                  training=True, device=None):
-        if topology.padding_mode != "VALID":
-            raise NeurocellError("the MI355X path implements the VALID pure-ROI propagation; "
-                                 f"padding_mode={topology.padding_mode} is not supported")
         if not topology.out_in_roi:
             raise NeurocellError("output port outside the active ROI is not supported")
         self.device = device or require_device()
@@ -140,16 +137,36 @@ class StepPlan:
         h, w = r1 - r0, c1 - c0
         self.H, self.W, self.kh, self.kw, self.M, self.d = H, W, kh, kw, M, d
         self.h, self.w, self.N = h, w, h * w
-        if self.cropped:
-            self.fft = (_npow2(h + kh - 1), _npow2(w + kw - 1))  # adaptive_mask.py:177-180
+        # padding modes (propagator.py:276-341): VALID adds the hoisted border conv to steps
+        # t >= 1; SAME and CIRCULAR take the whole grid as the ROI with no border term, SAME
+        # zero-padding the correlation and CIRCULAR wrapping it round the grid
+        self.mode = topology.padding_mode
+        self.circular = self.mode == "CIRCULAR"
+        self.border = self.mode == "VALID" and d > 1
+        if self.circular:
+            if self.cropped:
+                raise NeurocellError("adaptive crops are not supported in CIRCULAR mode")
+            # the correlation is circular on the grid itself (topology.py:256-258)
+            self.fft = (H, W)
+            if not spectral_grid_supported(H, W):
+                raise NeurocellError(f"CIRCULAR mode runs on the {H}x{W} grid itself: both "
+                                     f"sides in {_WAVE_FFT} or both in {_LARGE_FFT}")
+            if kh > H or kw > W:
+                raise NeurocellError("the filter is larger than the circular grid")
         else:
-            self.fft = tuple(topology.fft_shape)
+            if self.cropped:
+                self.fft = (_npow2(h + kh - 1), _npow2(w + kw - 1))  # adaptive_mask.py:177-180
+            else:
+                self.fft = tuple(topology.fft_shape)
+            # a linear correlation is the same on any grid it fits: grids below 16 points
+            # per axis run on 16
+            self.fft = tuple(max(16, v) for v in self.fft)
+            if not spectral_grid_supported(*self.fft):
+                raise NeurocellError(f"spectral grid {self.fft} is not supported (both axes "
+                                     f"in {_WAVE_FFT} or both in {_LARGE_FFT})")
+            if h + kh - 1 > self.fft[0] or w + kw - 1 > self.fft[1]:
+                raise NeurocellError("linear correlation does not fit the spectral grid")
         fh, fw = self.fft
-        if not spectral_grid_supported(fh, fw):
-            raise NeurocellError(f"spectral grid {self.fft} is not supported (both axes in "
-                                 f"{_WAVE_FFT} or both in {_LARGE_FFT})")
-        if h + kh - 1 > fh or w + kw - 1 > fw:
-            raise NeurocellError("linear correlation does not fit the spectral grid")
         self.F = fh * (fw // 2 + 1)
         self.cp = ((kh - 1) // 2, (kw - 1) // 2)
         self.Hp, self.Wp = h + kh - 1, w + kw - 1
@@ -307,7 +324,7 @@ class StepPlan:
         xh0 = self.xhat[0]
         jobs = [(_addr(filt), _addr(self.ghat), None, M, self.kh, self.kw, 1, 0, 0),
                 (_addr(self.x0), _addr(xh0), None, B, x0h, x0w, 0, 0, 0)]
-        if self.d > 1:
+        if self.border:
             # hoisted VALID border conv (propagator.py:362-366): its delta is added to every
             # step t >= 1's correlation, so the patch spectrum (shifted onto the ROI window)
             # joins those steps' cell spectra and their correlation yields z + delta directly
@@ -332,7 +349,7 @@ class StepPlan:
                 p0 = self.cp
                 # z + delta comes out of the correlation: the border spectrum joins x's
                 call("nc_fftconv_spectra", s, B, h, w, fh, fw, ptr(self.xs[t]), self.G,
-                     ptr(self.border_hat), ptr(xh))
+                     ptr(self.border_hat) if self.border else None, ptr(xh))
             # z already holds z + delta: the epilogues run without their border term
             if not last:
                 zk = None if fused and not self.training else z
@@ -381,7 +398,7 @@ class StepPlan:
             else:
                 # steps t >= 1 carried the border term: their cotangent's batch sum, summed
                 # over those steps in the frequency domain, is the border conv's cotangent
-                hbt = t > 0
+                hbt = t > 0 and self.border
                 call("nc_fftconv_bwd_parts", s, B, M, h, w, h, w, self.cp[0], self.cp[1], fh, fw,
                      ptr(self.gz), ptr(self.xhat[t]), ptr(self.ghat), need_dx,
                      ptr(gy) if need_dx else None, ptr(self.rows["dg"]), int(t < d - 1), 0,
@@ -398,7 +415,7 @@ class StepPlan:
         jobs = []
         if self.npart > 1:
             keys = ([] if only_t0_grid else ["dg"]) + (["dgv"] if valid_acc else []) + \
-                   (["gd"] if d > 1 else [])
+                   (["gd"] if self.border else [])
             outs = {"dg": self.dghat, "dgv": self.dghat_v, "gd": self.gdelta_hat}
             jobs += [(_addr(self.rows[k]), _addr(outs[k]), 2 * M * self.F, 0, self.npart)
                      for k in keys]
@@ -411,7 +428,7 @@ class StepPlan:
             call("nc_filter_spectrum_bwd", s, M, self.kh, self.kw, fh, fw, self.cp[0],
                  self.cp[1], ptr(self.dghat), ptr(g_filt), 0, 0)
         g_patch = None
-        if d > 1:
+        if self.border:
             # border conv reverse: the patch gradient from the cotangent spectra (its dG came
             # with the ROI steps' dghat, through their border-shifted cell spectra)
             call("nc_fftconv_bwd_hat", s, M, self.Hp, self.Wp, self.kh - 1, self.kw - 1, fh, fw,

@@ -207,6 +207,78 @@ class ChipTopology2D:
         return cls.create(grid_shape=(N, N), kernel_size=kernel_size, directions=directions,
                           depth=depth, in_ports=in_ports, out_port=out_port)
 
+    @classmethod
+    def mlp_chip(cls, n=8, layers=5, ctrl_gap=1, kernel_size=(17, 3), directions=8):
+        """topology.py:324-357: the vertical-MLP chip, one (3n + ctrl_gap) x 1 input column
+        and an n x 1 output column 2*layers + 1 cells to its right (depth = that gap)."""
+        N = 2 * n + 2 * max(kernel_size)
+        mid = N // 2
+        span = 2 * layers + 1
+        in_h = 3 * n + ctrl_gap
+        in_r, in_c = mid - in_h // 2, mid - span // 2
+        out_c = in_c + span
+        return cls.create(grid_shape=(N, N), kernel_size=kernel_size, directions=directions,
+                          depth=out_c - in_c,
+                          in_ports=(PortSpec(offset=(in_r, in_c), size=(in_h, 1), name="x_in"),),
+                          out_port=PortSpec(offset=(mid - n // 2, out_c), size=(n, 1),
+                                            name="out"))
+
+    @classmethod
+    def gol_chip(cls, grid_shape=(64, 64), kernel_size=(3, 3), directions=64, depth=2,
+                 padding_mode="VALID", n=None):
+        """topology.py:359-388: a full-grid cellular automaton; the input and output ports
+        are the whole grid (allowed outside a VALID ROI)."""
+        if n is not None:
+            grid_shape = (int(n), int(n))
+        elif isinstance(grid_shape, int):
+            grid_shape = (grid_shape, grid_shape)
+        grid_shape = tuple(int(v) for v in grid_shape)
+        return cls.create(grid_shape=grid_shape, kernel_size=kernel_size, directions=directions,
+                          depth=depth,
+                          in_ports=(PortSpec(offset=(0, 0), size=grid_shape,
+                                             name="universe_in"),),
+                          out_port=PortSpec(offset=(0, 0), size=grid_shape,
+                                            name="universe_out"),
+                          padding_mode=padding_mode, allow_border_output=True)
+
+    @classmethod
+    def clp_chip(cls, grid_shape=(8, 8), in_coords=None, out_coords=None, kernel_size=(3, 3),
+                 directions=1, depth=4, padding_mode="VALID", n=None):
+        """topology.py:390-428: the coordinate-addressed circular layered perceptron; by
+        default two inputs one cell inside the left edge of the ROI and two outputs one cell
+        inside its right edge (top and bottom rows)."""
+        if n is not None:
+            grid_shape = (int(n), int(n))
+        elif isinstance(grid_shape, int):
+            grid_shape = (grid_shape, grid_shape)
+        H, W = (int(v) for v in grid_shape)
+        valid = padding_mode.upper() == "VALID"
+        rh = (kernel_size[0] - 1) // 2 if valid else 0
+        rw = (kernel_size[1] - 1) // 2 if valid else 0
+        top, bottom, left, right = rh + 1, H - rh - 2, rw + 1, W - rw - 2
+        if in_coords is None:
+            in_coords = ((top, left), (bottom, left))
+        if out_coords is None:
+            out_coords = ((top, right), (bottom, right))
+        return cls.create(grid_shape=(H, W), kernel_size=kernel_size, directions=directions,
+                          depth=depth, in_ports=(CoordinatePortSpec(in_coords, name="clp_in"),),
+                          out_port=CoordinatePortSpec(out_coords, name="clp_out"),
+                          padding_mode=padding_mode, allow_border_output=True)
+
+    @classmethod
+    def tm_chip(cls, n=8, kernel_size=(13, 13), directions=16, gap=1):
+        """topology.py:430-455: a Turing-machine tape, a 1 x 2n input row and a 1 x n output
+        row gap cells after it on the centre row (depth = their column distance)."""
+        pad = 2 * max(kernel_size)
+        N = 2 * n + 2 * pad
+        mid = N // 2
+        out_c = pad + 2 * n + gap
+        return cls.create(grid_shape=(N, N), kernel_size=kernel_size, directions=directions,
+                          depth=out_c - pad,
+                          in_ports=(PortSpec(offset=(mid, pad), size=(1, 2 * n),
+                                             name="tape_in"),),
+                          out_port=PortSpec(offset=(mid, out_c), size=(1, n), name="tape_out"))
+
     def out_cells_roi(self) -> tuple:
         """ROI-relative (rows, cols) int arrays of the output cells in port order."""
         if isinstance(self.out_port, CoordinatePortSpec):

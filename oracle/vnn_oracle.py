@@ -152,16 +152,25 @@ class Geometry:
     fft_shape: tuple = (0, 0)
     io_state_mask: np.ndarray = field(default=None, repr=False)
     out_weight_mask: np.ndarray = field(default=None, repr=False)
+    padding_mode: str = "VALID"
 
     def __post_init__(self):
         H, W = self.grid_shape
         kh, kw = self.kernel_size
         if kh % 2 == 0 or kw % 2 == 0:  # topology.py:174-175
             raise ValueError("kernel must be odd")
-        self.pad_h, self.pad_w = (kh - 1) // 2, (kw - 1) // 2  # topology.py:184-186
+        self.padding_mode = self.padding_mode.upper()
+        if self.padding_mode == "VALID":  # topology.py:184-189
+            self.pad_h, self.pad_w = (kh - 1) // 2, (kw - 1) // 2
+        else:
+            self.pad_h, self.pad_w = 0, 0
         self.roi_shape = (H - 2 * self.pad_h, W - 2 * self.pad_w)  # :191-192
         npow2 = lambda v: 1 << (v - 1).bit_length()  # :89-91
-        self.fft_shape = (npow2(self.roi_shape[0] + kh - 1), npow2(self.roi_shape[1] + kw - 1))
+        if self.padding_mode == "CIRCULAR":  # :256-258
+            self.fft_shape = (H, W)
+        else:
+            self.fft_shape = (npow2(self.roi_shape[0] + kh - 1),
+                              npow2(self.roi_shape[1] + kw - 1))
         io = np.zeros((H, W), bool)
         for p in self.in_ports:  # :238-245
             _mark(io, p)
@@ -418,7 +427,19 @@ def conv2d_fft(x, g, pad, out_shape, fft_shape):
     Gh = filter_spectrum(g, fft_shape)
     full = _irfft2(X[:, None] * Gh[None], fft_shape, WORKERS)
     (ho, wo), (r, c) = out_shape, pad
-    return full[..., r:r + ho, c:c + wo], X
+    # the window is read modulo the grid: the same slice where it fits, a circular
+    # correlation where it wraps (the grid equal to the plane)
+    full = np.roll(full, shift=(-r, -c), axis=(-2, -1))
+    return full[..., :ho, :wo], X
+
+
+def conv2d_circular_direct(x, g, pad):
+    """CIRCULAR-mode step convolution as the reference writes it (propagator.py:284-292):
+    the cells wrap-padded by ``pad`` (``jnp.pad(mode="wrap")``), then a brute-force VALID
+    cross-correlation: x (B,H,W), g (M,Kh,Kw) -> (B,M,H,W)."""
+    ph, pw = pad
+    xp = np.pad(np.asarray(x, _dt()), ((0, 0), (ph, ph), (pw, pw)), mode="wrap")
+    return conv2d_direct(xp, g, (0, 0))
 
 
 def conv2d_fft_unshifted_bwd(gz, x, g, pad, fft_shape, need_dx=True):
@@ -588,8 +609,13 @@ def border_patch(border_2d, geom: Geometry, roi_bbox=None):
 def propagate(cell, filters, inputs, geom: Geometry, act="tanh", final_act=None,
               hard_pin_io=False, roi_bbox=None, mode="continuous", tau=1.0,
               active_threshold=0.6, conv="fft"):
-    """Pure-ROI forward of ``propagate_vnn_2d`` for the VALID pallas backends
-    (propagator.py:252-682).  ``filters`` is (M,1,Kh,Kw).  Returns (out, cache)."""
+    """Pure-ROI forward of ``propagate_vnn_2d`` for the pallas backends (propagator.py:252-682)
+    and its CIRCULAR branch (:284-341); SAME and CIRCULAR have the whole grid as ROI and no
+    border term.  ``filters`` is (M,1,Kh,Kw).  Returns (out, cache)."""
+    valid = geom.padding_mode == "VALID"
+    circular = geom.padding_mode == "CIRCULAR"
+    if circular and roi_bbox is not None:
+        raise ValueError("the CIRCULAR branch takes no sub-ROI")
     cell = np.asarray(cell, _dt())
     g = np.asarray(filters, _dt())[:, 0]
     kh, kw = geom.kernel_size
@@ -603,18 +629,22 @@ def propagate(cell, filters, inputs, geom: Geometry, act="tanh", final_act=None,
         fft_shape = (1 << (hv + kh - 2).bit_length(), 1 << (wv + kw - 2).bit_length())
     else:
         fft_shape = geom.fft_shape
-    bp = border_patch(sp["border_2d"], geom, roi_bbox)
-    delta = conv2d_direct(bp[None], g, (0, 0))[0]  # (M, hv, wv), propagator.py:362-366
+    if valid:
+        bp = border_patch(sp["border_2d"], geom, roi_bbox)
+        delta = conv2d_direct(bp[None], g, (0, 0))[0]  # (M, hv, wv), propagator.py:362-366
+    else:  # propagator.py:367-370
+        bp = None
+        delta = np.zeros((geom.directions, hv, wv), _dt())
 
     def _conv(xx):
         if conv == "direct":
-            return conv2d_direct(xx, g, pad)
+            return conv2d_circular_direct(xx, g, pad) if circular else conv2d_direct(xx, g, pad)
         return conv2d_fft(xx, g, pad, (hv, wv), fft_shape)[0]
 
     xs, zs, stats = [x], [], []
     for t in range(d - 1):
         z = _conv(xs[-1])
-        hb = t > 0
+        hb = t > 0 and valid
         out, mean, rstd = epilogue_fwd(z, delta, sp["w_eff_roi"], sp["s_eff_roi"], sp["b_roi"],
                                        act, hb)
         zs.append(z)
@@ -625,7 +655,7 @@ def propagate(cell, filters, inputs, geom: Geometry, act="tanh", final_act=None,
     rows, cols = geom.out_cells_roi
     if roi_bbox is not None:
         rows, cols = rows - roi_bbox[0], cols - roi_bbox[2]
-    hb_final = d > 1
+    hb_final = d > 1 and valid
     out, aux = port_fwd(z, delta, rows, cols, geom.out_size, sp["w_eff_out"], sp["s_eff_out"],
                         sp["b_out"], hb_final, final_act)
     cache = dict(sp=sp, xs=xs, zs=zs, stats=stats, delta=delta, bp=bp, aux=aux, g=g, pad=pad,
@@ -652,7 +682,8 @@ def propagate_vjp(cell, filters, inputs, geom: Geometry, g_out, act="tanh", fina
     g_weff = np.zeros_like(sp["w_eff_roi"])
     g_seff = np.zeros_like(sp["s_eff_roi"])
     g_broi = np.zeros_like(sp["b_roi"])
-    hb_final = d > 1
+    valid = geom.padding_mode == "VALID"
+    hb_final = d > 1 and valid
     gz, gdb, g_wo, g_so, g_bo = port_bwd(c["zs"][-1], c["delta"], c["rows"], c["cols"],
                                          geom.out_size, sp["w_eff_out"], sp["s_eff_out"],
                                          sp["b_out"], c["aux"], np.asarray(g_out, _dt()),
@@ -666,7 +697,7 @@ def propagate_vjp(cell, filters, inputs, geom: Geometry, g_out, act="tanh", fina
         if t == 0:
             break
         mean, rstd = c["stats"][t - 1]
-        hb = (t - 1) > 0
+        hb = (t - 1) > 0 and valid
         gz, gdb, gw, gs, gb = epilogue_bwd(c["zs"][t - 1], c["delta"], sp["w_eff_roi"],
                                            sp["s_eff_roi"], sp["b_roi"], mean, rstd, dx, act, hb)
         g_delta += gdb
@@ -674,21 +705,22 @@ def propagate_vjp(cell, filters, inputs, geom: Geometry, g_out, act="tanh", fina
         g_seff += gs
         g_broi += gb
     g_filt = filter_grad_from_unshifted(dGh, (kh, kw), pad, fs)
-    # border conv (1,1,Hp,Wp) VALID with G -> delta: adjoint by brute force
-    bp = c["bp"]
-    Hp, Wp = bp.shape
-    g_bp = np.zeros_like(bp)
-    hv, wv = g_delta.shape[-2:]
-    for u in range(kh):
-        for v in range(kw):
-            g_bp[u:u + hv, v:v + wv] += np.einsum("mij,m->ij", g_delta, g[:, u, v])
-            g_filt[:, u, v] += np.einsum("mij,ij->m", g_delta, bp[u:u + hv, v:v + wv])
     H, W = geom.grid_shape
     g_border = np.zeros((H, W), _dt())
-    r0, c0 = (roi_bbox[0], roi_bbox[2]) if roi_bbox is not None else (0, 0)
-    g_border[r0:r0 + Hp, c0:c0 + Wp] = g_bp
-    rh, rw = geom.pad_h, geom.pad_w
-    g_border[rh:H - rh, rw:W - rw] = 0.0
+    bp = c["bp"]
+    if bp is not None:
+        # border conv (1,1,Hp,Wp) VALID with G -> delta: adjoint by brute force
+        Hp, Wp = bp.shape
+        g_bp = np.zeros_like(bp)
+        hv, wv = g_delta.shape[-2:]
+        for u in range(kh):
+            for v in range(kw):
+                g_bp[u:u + hv, v:v + wv] += np.einsum("mij,m->ij", g_delta, g[:, u, v])
+                g_filt[:, u, v] += np.einsum("mij,ij->m", g_delta, bp[u:u + hv, v:v + wv])
+        r0, c0 = (roi_bbox[0], roi_bbox[2]) if roi_bbox is not None else (0, 0)
+        g_border[r0:r0 + Hp, c0:c0 + Wp] = g_bp
+        rh, rw = geom.pad_h, geom.pad_w
+        g_border[rh:H - rh, rw:W - rw] = 0.0
     grads = dict(w_eff_roi=g_weff, s_eff_roi=g_seff, b_roi=g_broi, border_2d=g_border,
                  w_eff_out=g_wo, s_eff_out=g_so, b_out=g_bo)
     g_cell = precompute_step_params_vjp(cell, geom, grads, act, hard_pin_io, roi_bbox, mode,

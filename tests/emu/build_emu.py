@@ -1,6 +1,7 @@
 """Builds the CPU-emulated C ABI (tests/emu/_build/libnc_emu.so) from the same kernel
 sources as the gfx950 library, with g++ and the emulation shim in tests/emu/hip/."""
 import concurrent.futures as cf
+import fcntl
 import os
 import subprocess
 
@@ -35,10 +36,15 @@ def build() -> str:
     if not _stale():
         return LIB
     os.makedirs(OUT_DIR, exist_ok=True)
-    with cf.ThreadPoolExecutor(4) as ex:
-        objs = list(ex.map(_obj, SOURCES + [os.path.join(HERE, "emu_main.cpp")]))
-    subprocess.run(["g++", "-shared", "-pthread", "-o", LIB + ".tmp", *objs], check=True)
-    os.replace(LIB + ".tmp", LIB)
+    # one builder at a time (parallel test workers share the build folder)
+    with open(os.path.join(OUT_DIR, ".lock"), "w") as lock:
+        fcntl.flock(lock, fcntl.LOCK_EX)
+        if _stale():
+            with cf.ThreadPoolExecutor(4) as ex:
+                objs = list(ex.map(_obj, SOURCES + [os.path.join(HERE, "emu_main.cpp")]))
+            subprocess.run(["g++", "-shared", "-pthread", "-o", LIB + ".tmp", *objs],
+                           check=True)
+            os.replace(LIB + ".tmp", LIB)
     return LIB
 
 

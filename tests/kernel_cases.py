@@ -467,6 +467,56 @@ def case_fftconv_epilogue(be, B=3, M=6, h=20, w=27, kh=7, kw=5, FH=32, FW=64, ac
     return res
 
 
+def case_fftconv_circular(be, B=2, M=3, H=16, W=16, kh=5, kw=3, seed=9):
+    """CIRCULAR padding mode (propagator.py:284-300): the correlation on the (H, W) grid itself,
+    the output window read modulo the grid, forward (nc_fftconv_fwd and, on the 64-wide grids,
+    the fused correlation + epilogue) and reverse (dx, dG) against the wrap-padded brute-force
+    correlation and its adjoints."""
+    rng = np.random.default_rng(seed)
+    L, s = be.lib, be.stream()
+    pad = ((kh - 1) // 2, (kw - 1) // 2)
+    x = rng.normal(size=(B, H, W)).astype(np.float32)
+    g = rng.normal(size=(M, 1, kh, kw)).astype(np.float32)
+    gz = rng.normal(size=(B, M, H, W)).astype(np.float32)
+    xd, gd, gzd = be.put(x), be.put(g), be.put(gz)
+    F2 = (M, H, W // 2 + 1, 2)
+    ghat = be.zeros(F2)
+    _ok(be, L.nc_filter_spectrum_fwd(s, M, kh, kw, H, W, be.ptr(gd), be.ptr(ghat)), "spec")
+    z, xhat = be.zeros((B, M, H, W)), be.zeros((B, H, W // 2 + 1, 2))
+    _ok(be, L.nc_fftconv_fwd(s, B, M, H, W, H, W, pad[0], pad[1], H, W, be.ptr(xd),
+                             be.ptr(ghat), be.ptr(z), be.ptr(xhat)), "fwd")
+    ws = be.zeros((L.nc_fftconv_bwd_workspace_size(B, M, H, W) // 4 + 1,))
+    nb = ws.nbytes if hasattr(ws, "nbytes") else ws.numel() * 4
+    dx, dgh = be.zeros((B, H, W)), be.zeros(F2)
+    _ok(be, L.nc_fftconv_bwd(s, B, M, H, W, H, W, pad[0], pad[1], H, W, be.ptr(gzd),
+                             be.ptr(xhat), be.ptr(ghat), 1, be.ptr(dx), be.ptr(dgh), 0, 0,
+                             be.ptr(ws), nb), "bwd")
+    gf = be.zeros((M, 1, kh, kw))
+    _ok(be, L.nc_filter_spectrum_bwd(s, M, kh, kw, H, W, pad[0], pad[1], be.ptr(dgh),
+                                     be.ptr(gf), 0, 0), "specbwd")
+    zr = O.conv2d_circular_direct(x, g[:, 0], pad)
+    dxr, dGh = O.conv2d_fft_unshifted_bwd(gz, x, g[:, 0], pad, (H, W))
+    dgr = O.filter_grad_from_unshifted(dGh, (kh, kw), pad, (H, W))
+    res = {"z": rel_l2(be.get(z), zr), "dx": rel_l2(be.get(dx), dxr),
+           "dG": rel_l2(be.get(gf)[:, 0], dgr)}
+    if W == 64 and H in (32, 64):
+        wv = rng.normal(size=(H, W)).astype(np.float32)
+        sv = rng.uniform(size=(H, W)).astype(np.float32)
+        bv = rng.normal(size=(H, W)).astype(np.float32)
+        wd, sd, bd = be.put(wv), be.put(sv), be.put(bv)
+        G = L.nc_fftconv_epilogue_partials(B, M, H, W, H, W)
+        p, mu, rs = be.zeros((G, B, H, W)), be.zeros((B, M)), be.zeros((B, M))
+        z2 = be.zeros((B, M, H, W))
+        _ok(be, L.nc_fftconv_epilogue_fwd(s, B, M, H, W, pad[0], pad[1], H, W, be.ptr(xhat),
+                                          be.ptr(ghat), _abi.ACT_IDS["tanh"], 0.01, be.ptr(wd),
+                                          be.ptr(sd), be.ptr(bd), be.ptr(z2), be.ptr(p),
+                                          be.ptr(mu), be.ptr(rs), None, 0), "fused")
+        o_r = O.epilogue_fwd(zr, np.zeros((M, H, W)), wv, sv, bv, "tanh", False)[0]
+        res["z_fused"] = rel_l2(be.get(z2), zr)
+        res["out_fused"] = rel_l2(be.get(p).astype(np.float64).sum(0), o_r)
+    return res
+
+
 def case_port(be, B=3, M=5, h=10, w=12, rows=(2, 3, 4, 2), cols=(5, 5, 5, 5), fact=None,
               seed=3):
     """Output-port forward/backward (rect-like and coordinate ports, duplicates included)."""

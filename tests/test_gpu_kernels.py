@@ -4,7 +4,7 @@ import pytest
 from kernel_cases import (CODD_CASES, EPILOGUE_SHAPES, PORT_SHAPES, TOL, DeviceBackend,
                           case_adaptive, case_border_conv, case_border_fold, case_codd,
                           case_epilogue, case_epilogue_parts,
-                          case_fftconv_epilogue, case_fftconv, case_helpers,
+                          case_fftconv_circular, case_fftconv_epilogue, case_fftconv, case_helpers,
                           case_plane_spectra, case_port)
 
 pytestmark = pytest.mark.gpu
@@ -118,3 +118,14 @@ def test_fftconv_epilogue(be, B, M, h, w, kh, kw, FH, FW, act):
     assert res["xhat_mismatch"] == 0, res
     _assert_small({k: res[k] for k in ("z", "z_vs_separate", "out", "out_vs_separate", "mean",
                                        "rstd")})
+
+
+@pytest.mark.parametrize("B,M,H,W,kh,kw", [
+    (2, 3, 16, 16, 5, 3),     # wavefront transforms
+    (2, 6, 32, 64, 7, 5),     # lane pairs, fused epilogue with idle wavefronts
+    (2, 4, 64, 64, 9, 9),     # lane pairs + segmented per-sample transforms, 64 values/lane
+    (1, 2, 128, 128, 5, 5),   # workgroup transforms over LDS segments
+])
+def test_fftconv_circular(be, B, M, H, W, kh, kw):
+    res = case_fftconv_circular(be, B=B, M=M, H=H, W=W, kh=kh, kw=kw)
+    _assert_small(res)

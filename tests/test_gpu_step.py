@@ -110,3 +110,57 @@ def test_large_grid_step_parity(name, B, M):
     cell, filt, x, _ = cfg.synthetic(5, batch=B, directions=M)
     check(config_geometry(cfg, directions=M), cfg.topology(directions=M), cell, filt, x,
           cfg.codd_mode, cfg.tau, cfg.roi_bbox)
+
+
+def _mode_case(mode, grid, kernel, M, depth, B=4, seed=30):
+    """Two 4x1 input ports and a 3x2 output port on a (grid) chip in the given padding mode,
+    with config-0 parameter distributions."""
+    from neurocell.topology import ChipTopology2D, PortSpec
+    ins = [((2, 3), (4, 1)), ((9, 5), (4, 1))]
+    outp = ((6, 9), (3, 2))
+    topo = ChipTopology2D.create(grid, kernel, M, depth,
+                                 [PortSpec(offset=o, size=s, name=f"in{i}")
+                                  for i, (o, s) in enumerate(ins)],
+                                 PortSpec(offset=outp[0], size=outp[1], name="out"),
+                                 padding_mode=mode)
+    geom = O.Geometry(tuple(grid), tuple(kernel), M, depth, [("rect", o, s) for o, s in ins],
+                      ("rect",) + outp, padding_mode=mode)
+    rng = np.random.default_rng(seed)
+    H, W = grid
+    kh, kw = kernel
+    cell = np.stack([rng.normal(0, 0.1, (H, W)), rng.normal(0, 0.01, (H, W)),
+                     rng.normal(0, 1.0, (H, W))]).astype(np.float32)
+    filt = rng.normal(0, 1.0 / np.sqrt(kh * kw), (M, 1, kh, kw)).astype(np.float32)
+    x = (rng.random((B, 2, 4, 1)) > 0.5).astype(np.float32)
+    return geom, topo, cell, filt, x
+
+
+@pytest.mark.parametrize("mode,grid,kernel,M,depth", [
+    ("SAME", (16, 16), (5, 3), 3, 3),        # spectral grid 32x32, wavefront transforms
+    ("CIRCULAR", (16, 16), (5, 3), 3, 3),    # the 16x16 grid itself
+    ("CIRCULAR", (32, 64), (7, 5), 6, 3),    # lane pairs, fused epilogue, wrapped windows
+    ("SAME", (32, 32), (23, 13), 16, 3),     # spectral grid 64x64
+    ("CIRCULAR", (64, 64), (9, 9), 4, 2),    # the 64x64 grid itself
+])
+def test_padding_mode_step_parity(mode, grid, kernel, M, depth):
+    """SAME and CIRCULAR padding modes (propagator.py:276-341): whole-grid ROI, no border
+    term; CIRCULAR wraps the correlation round the grid."""
+    geom, topo, cell, filt, x = _mode_case(mode, grid, kernel, M, depth)
+    check(geom, topo, cell, filt, x, "continuous", 1.0, None)
+
+
+@pytest.mark.parametrize("mode,n", [("VALID", 8), ("CIRCULAR", 16), ("SAME", 8)])
+def test_clp_chip_parity(mode, n):
+    """The coordinate-addressed CLP chip (topology.py:391-428; one direction, depth 4, 3x3
+    filters) on its default 8x8 grid (spectral grid 8 raised to 16) and circular at 16x16."""
+    from neurocell.topology import ChipTopology2D
+    topo = ChipTopology2D.clp_chip(n=n, padding_mode=mode)
+    H, W = topo.grid_shape
+    geom = O.Geometry((H, W), (3, 3), 1, 4, [("coords", list(topo.in_ports[0].coords))],
+                      ("coords", list(topo.out_port.coords)), padding_mode=mode)
+    rng = np.random.default_rng(31)
+    cell = np.stack([rng.normal(0, 0.3, (H, W)), rng.normal(0, 0.1, (H, W)),
+                     rng.normal(0, 1.0, (H, W))]).astype(np.float32)
+    filt = rng.normal(0, 1.0 / 3.0, (1, 1, 3, 3)).astype(np.float32)
+    x = (rng.random((8, 2)) > 0.5).astype(np.float32)
+    check(geom, topo, cell, filt, x, "continuous", 1.0, None)

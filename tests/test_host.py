@@ -265,3 +265,23 @@ def test_benchmark_configs_geometry(name):
     cell, filt, x, y = cfg.synthetic(0, batch=2)
     assert cell.shape == (3,) + topo.grid_shape and filt.shape == (cfg.directions, 1) + cfg.kernel
     assert y.shape == (2,) + tuple(topo.out_port.size)
+
+
+def test_chip_constructors_geometry():
+    """topology.py:324-455: the MLP, Game-of-Life, CLP and Turing-machine chips."""
+    from neurocell.topology import ChipTopology2D, CoordinatePortSpec
+    m = ChipTopology2D.mlp_chip()  # n=8, 5 layers, K=17x3: N = 16 + 34
+    assert m.grid_shape == (50, 50) and m.depth == 11
+    assert m.in_ports[0].size == (25, 1) and m.out_port.size == (8, 1)
+    assert m.out_port.offset[1] - m.in_ports[0].offset[1] == m.depth
+    g = ChipTopology2D.gol_chip(n=32, padding_mode="SAME")
+    assert g.grid_shape == (32, 32) and g.in_ports[0].size == (32, 32)
+    assert g.out_port.size == (32, 32) and g.roi_shape == (32, 32)
+    c = ChipTopology2D.clp_chip()
+    assert isinstance(c.in_ports[0], CoordinatePortSpec)
+    assert c.in_ports[0].coords == ((2, 2), (5, 2)) and c.out_port.coords == ((2, 5), (5, 5))
+    cc = ChipTopology2D.clp_chip(n=16, padding_mode="CIRCULAR")
+    assert cc.in_ports[0].coords == ((1, 1), (14, 1)) and cc.fft_shape == (16, 16)
+    t = ChipTopology2D.tm_chip()  # n=8, K=13x13: N = 16 + 52
+    assert t.grid_shape == (68, 68) and t.depth == 17
+    assert t.in_ports[0].size == (1, 16) and t.out_port.offset == (34, 43)

@@ -457,3 +457,80 @@ def test_mse_gradient():
     xt = torch.tensor(x, requires_grad=True)
     F.mse_loss(xt, torch.tensor(y)).backward()
     np.testing.assert_allclose(g, xt.grad.numpy(), rtol=1e-12)
+
+
+# ------------------------------------------------------------------ SAME / CIRCULAR modes
+
+def mode_geometry(mode, depth=3, M=3, kernel=(5, 3), grid=(16, 16)):
+    return O.Geometry(grid, kernel, M, depth, [("rect", (2, 3), (4, 1)), ("rect", (9, 5), (1, 3))],
+                      ("rect", (6, 9), (3, 2)), padding_mode=mode)
+
+
+def test_mode_geometry_known_answers():
+    """topology.py:184-192, 256-265: VALID pads by (k-1)/2; SAME and CIRCULAR take the grid
+    as ROI; CIRCULAR transforms on the grid itself."""
+    v, s, c = (mode_geometry(m, kernel=(5, 3), grid=(16, 16)) for m in ("VALID", "SAME",
+                                                                         "CIRCULAR"))
+    assert (v.pad_h, v.pad_w, v.roi_shape, v.fft_shape) == (2, 1, (12, 14), (16, 16))
+    assert (s.pad_h, s.pad_w, s.roi_shape, s.fft_shape) == (0, 0, (16, 16), (32, 32))
+    assert (c.pad_h, c.pad_w, c.roi_shape, c.fft_shape) == (0, 0, (16, 16), (16, 16))
+
+
+def test_circular_spectral_matches_wrap_padded_direct():
+    """The grid-sized spectral correlation read modulo the grid against the reference's own
+    formulation: jnp.pad(mode='wrap') then a VALID conv (brute force), and against scipy's
+    'wrap' boundary correlation."""
+    rng = np.random.default_rng(21)
+    x, g = rng.normal(size=(2, 16, 32)), rng.normal(size=(3, 5, 7))
+    pad = (2, 3)
+    z_fft = O.conv2d_fft(x, g, pad, (16, 32), (16, 32))[0]
+    z_dir = O.conv2d_circular_direct(x, g, pad)
+    np.testing.assert_allclose(z_fft, z_dir, rtol=0, atol=1e-10)
+    sc = scipy.signal.correlate2d(x[1], g[2], mode="same", boundary="wrap")
+    np.testing.assert_allclose(z_dir[1, 2], sc, rtol=0, atol=1e-10)
+
+
+def test_circular_adjoints():
+    """<conv(x, g), gz> = <x, dx> = <g, dG> for the circular correlation, with dx and dG from
+    the unshifted Plancherel backward on the grid-sized spectrum (no zero padding)."""
+    rng = np.random.default_rng(22)
+    x, g = rng.normal(size=(3, 16, 16)), rng.normal(size=(2, 5, 3))
+    gz = rng.normal(size=(3, 2, 16, 16))
+    pad = (2, 1)
+    z = O.conv2d_circular_direct(x, g, pad)
+    dx, dGh = O.conv2d_fft_unshifted_bwd(gz, x, g, pad, (16, 16))
+    dg = O.filter_grad_from_unshifted(dGh, (5, 3), pad, (16, 16))
+    lhs = float((z * gz).sum())
+    assert abs(lhs - float((x * dx).sum())) <= 1e-9 * max(1.0, abs(lhs))
+    assert abs(lhs - float((g * dg).sum())) <= 1e-9 * max(1.0, abs(lhs))
+
+
+@pytest.mark.parametrize("mode", ["SAME", "CIRCULAR"])
+def test_mode_propagate_fft_equals_direct(mode):
+    g = mode_geometry(mode)
+    rng = np.random.default_rng(23)
+    cell, filt = rand_cell(g, rng), rng.normal(size=(3, 1, 5, 3))
+    x = rand_inputs(g, 2, rng)
+    a, _ = O.propagate(cell, filt, x, g)
+    b, _ = O.propagate(cell, filt, x, g, conv="direct")
+    np.testing.assert_allclose(a, b, rtol=0, atol=1e-9)
+
+
+@pytest.mark.parametrize("mode,final_act", [("SAME", None), ("CIRCULAR", "tanh")])
+def test_mode_propagate_vjp_matches_finite_differences(mode, final_act):
+    g = mode_geometry(mode)
+    rng = np.random.default_rng(24)
+    cell, filt = rand_cell(g, rng), rng.normal(size=(3, 1, 5, 3))
+    x = rand_inputs(g, 2, rng)
+    kw = dict(final_act=final_act)
+    out, _ = O.propagate(cell, filt, x, g, **kw)
+    g_out = rng.normal(size=out.shape)
+    _, gc, gf = O.propagate_vjp(cell, filt, x, g, g_out, **kw)
+    vc, vf = rng.normal(size=cell.shape), rng.normal(size=filt.shape)
+
+    def L(c, f):
+        return float((O.propagate(c, f, x, g, conv="direct", **kw)[0] * g_out).sum())
+    e = 1e-6
+    fd = (L(cell + e * vc, filt + e * vf) - L(cell - e * vc, filt - e * vf)) / (2 * e)
+    an = float((gc * vc).sum() + (gf * vf).sum())
+    assert abs(fd - an) <= 1e-6 * max(1.0, abs(an))
