@@ -334,6 +334,22 @@ int nc_fftconv_epilogue_fwd(void* stream, int B, int M, int hout, int wout, int 
                             float* mean, float* rstd, void* ws, size_t ws_bytes);
 
 /*
+ * The output port when it covers the whole (sub-)ROI in row-major order (P = h*w: the Game of
+ * Life chip's universe port, topology.py:359-388).  pallas_fused_output_port_epilogue
+ * (kernels_pallas.py:1510-1551) for such a port is the hidden epilogue with the port
+ * parameters (w_eff_out, s_eff_out, b_out) and the final activation in its place
+ * (nc_fftconv_epilogue_fwd or nc_epilogue_fwd_parts with act = final_act), finished here:
+ * out (n = B*P) = final_act(sum over g < G of parts[g]), pre (n) = that sum (may be NULL when
+ * final_act is identity: port_out's identity form is the same sum).  Its reverse
+ * nc_port_dense_bwd gives g_pre = g_out * final_act'(pre), the gy of nc_epilogue_bwd_parts.
+ * No counterpart in the reference (whose port kernels gather P cells).
+ */
+int nc_port_dense_fwd(void* stream, int n, int G, int final_act, float neg_slope,
+                      const float* parts, float* out, float* pre);
+int nc_port_dense_bwd(void* stream, int n, int final_act, float neg_slope, const float* pre,
+                      const float* g_out, float* g_pre);
+
+/*
  * pallas_fused_roi_step_epilogue backward rule (kernels_pallas.py:869-1064): writes gz
  * (B,M,h,w), gdb = sum_b gz (M,h,w) when has_border and gdb is not NULL (a caller that forms
  * the border cotangent from the spectra, nc_fftconv_bwd_ex, passes NULL) and gw/gs/gb (h,w).

@@ -1196,6 +1196,54 @@ int nc_epilogue_bwd_parts(void* stream, int B, int M, int h, int w, int act, flo
                         pg_rows, plane_stride, ws, ws_bytes);
 }
 
+namespace {
+
+// The dense port's finish: out = fact(sum of the G direction-group partials), fixed order.
+__global__ __launch_bounds__(256) void k_port_dense_fwd(int n, int G, int fact, float slope,
+                                                        const float* __restrict__ parts,
+                                                        float* __restrict__ out,
+                                                        float* __restrict__ pre) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float y = parts[i];
+    for (int g = 1; g < G; ++g) y += parts[(size_t)g * n + i];
+    if (pre) pre[i] = y;
+    out[i] = fact == NC_ACT_IDENTITY ? y : nc_act(y, fact, slope);
+}
+
+__global__ __launch_bounds__(256) void k_port_dense_bwd(int n, int fact, float slope,
+                                                        const float* __restrict__ pre,
+                                                        const float* __restrict__ g_out,
+                                                        float* __restrict__ g_pre) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float a;
+    g_pre[i] = g_out[i] * nc_act_d(pre[i], fact, slope, &a);
+}
+
+}  // namespace
+
+int nc_port_dense_fwd(void* stream, int n, int G, int final_act, float neg_slope,
+                      const float* parts, float* out, float* pre) {
+    if (n <= 0 || G <= 0 || !parts || !out || final_act < 0 || final_act > 5 ||
+        (final_act != NC_ACT_IDENTITY && !pre))
+        return NC_ERR_INVALID_ARGUMENT;
+    hipLaunchKernelGGL(k_port_dense_fwd, dim3((n + 255) / 256), dim3(256), 0,
+                       nc_stream(stream), n, G, final_act, neg_slope, parts, out, pre);
+    NC_CHECK_LAUNCH();
+    return NC_OK;
+}
+
+int nc_port_dense_bwd(void* stream, int n, int final_act, float neg_slope, const float* pre,
+                      const float* g_out, float* g_pre) {
+    if (n <= 0 || !pre || !g_out || !g_pre || final_act <= NC_ACT_IDENTITY || final_act > 5)
+        return NC_ERR_INVALID_ARGUMENT;
+    hipLaunchKernelGGL(k_port_dense_bwd, dim3((n + 255) / 256), dim3(256), 0,
+                       nc_stream(stream), n, final_act, neg_slope, pre, g_out, g_pre);
+    NC_CHECK_LAUNCH();
+    return NC_OK;
+}
+
 int nc_rows_sum(void* stream, int n_jobs, const nc_rows_job* jobs) {
     if (n_jobs <= 0 || n_jobs > kRedJobs || !jobs) return NC_ERR_INVALID_ARGUMENT;
     RedJob rj[kRedJobs];

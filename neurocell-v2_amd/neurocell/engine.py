@@ -183,8 +183,16 @@ class StepPlan:
         self.out_size = tuple(topology.out_port.size)
         dev = self.device
         self.port_rc = torch.tensor(np.stack([rows, cols]).astype(np.int32), device=dev)
-        self.port_idx = torch.tensor(((rows - r0) * w + (cols - c0)).astype(np.int32),
-                                     device=dev)
+        flat = ((rows - r0) * w + (cols - c0)).astype(np.int32)
+        self.port_idx = torch.tensor(flat, device=dev)
+        # a port that is the whole (sub-)ROI in row-major order (the Game-of-Life universe
+        # port): its epilogue is the hidden one with the port parameters and the final
+        # activation, so it runs on the epilogue kernels at any size
+        self.dense_port = self.P == self.N and np.array_equal(flat, np.arange(self.N))
+        if not self.dense_port and (self.P > 256 or M * self.P > 8192):
+            raise NeurocellError(f"an output port of {self.P} cells must cover the whole ROI "
+                                 "in row-major order (the port kernels gather at most 256 "
+                                 "cells, 8192 per sample over the directions)")
         self.io_mask = torch.tensor(topology.io_state_mask.astype(np.uint8), device=dev)
         self.owm = torch.tensor(topology.out_weight_mask.astype(np.uint8), device=dev)
         # input injection map (gather form)
@@ -259,7 +267,9 @@ class StepPlan:
         self.mean = [torch.empty(B, M, **f) for _ in range(d)]
         self.rstd = [torch.empty(B, M, **f) for _ in range(d)]
         self.out = torch.empty(B, self.P, **f)
-        self.zo = torch.empty(B, M, self.P, **f)
+        self.zo = None if self.dense_port else torch.empty(B, M, self.P, **f)
+        if self.dense_port:  # the port's direction-group partial outputs
+            self.port_parts = torch.empty(self.G, B, h, w, **f)
         self.pre = torch.empty(B, self.P, **f) if self.fact != 0 else None
         n_ep = _abi_size("nc_epilogue_workspace_size", B, M, h, w)
         self.ws_epi = torch.empty(max(1, n_ep // 4), **f)
@@ -286,7 +296,9 @@ class StepPlan:
             self.R = _abi_int("nc_epilogue_bwd_partials", B, M, h, w)
             L = max(1, d - 1)
             self.pg_rows = torch.empty(3, L * self.R, h * w, **f)
-            self.pp_rows = torch.empty(3, B, self.P, **f)
+            # port-parameter partial rows: B per parameter, or the epilogue's R for a dense port
+            self.pp_rows = torch.empty(3, self.R if self.dense_port else B, self.P, **f)
+            self.g_pre = torch.empty(B, self.P, **f) if self.dense_port else None
             self.gw = torch.empty(h, w, **f)
             self.gs = torch.empty(h, w, **f)
             self.gb = torch.empty(h, w, **f)
@@ -357,6 +369,14 @@ class StepPlan:
                      ptr(self.ghat), self.act, self.slope, ptr(self.w_eff), ptr(self.s_eff),
                      ptr(self.b_roi), ptr(zk), ptr(self.xs[t + 1]), ptr(self.mean[t]),
                      ptr(self.rstd[t]), ptr(self.ws_epi), self.ws_epi.numel() * 4)
+            elif self.dense_port:
+                zk = None if fused and not self.training else z
+                call("nc_fftconv_epilogue_fwd", s, B, M, h, w, p0[0], p0[1], fh, fw, ptr(xh),
+                     ptr(self.ghat), self.fact, self.fslope, ptr(self.pp[0]), ptr(self.pp[1]),
+                     ptr(self.pp[2]), ptr(zk), ptr(self.port_parts), ptr(self.mean[t]),
+                     ptr(self.rstd[t]), ptr(self.ws_epi), self.ws_epi.numel() * 4)
+                call("nc_port_dense_fwd", s, B * self.P, self.G, self.fact, self.fslope,
+                     ptr(self.port_parts), ptr(self.out), ptr(self.pre))
             else:
                 call("nc_spectral_correlate", s, B, M, h, w, p0[0], p0[1], fh, fw, ptr(xh),
                      ptr(self.ghat), ptr(z))
@@ -380,10 +400,21 @@ class StepPlan:
         ws_fc, n_fc = ptr(self.ws_fc), self.ws_fc.numel() * 4
         t = d - 1
         N, RN = h * w, self.R * h * w
-        call("nc_port_bwd_parts", s, B, M, h, w, 0, self.fact, self.fslope, self.P,
-             ptr(self.port_idx), ptr(self.zs[t]), None, ptr(self.pp), ptr(self.zo),
-             ptr(self.mean[t]), ptr(self.rstd[t]), ptr(self.pre), ptr(g_out), ptr(self.gz),
-             ptr(self.pp_rows), B * self.P, ws_ep, n_ep)
+        if self.dense_port:
+            gy_port = g_out
+            if self.fact != 0:
+                call("nc_port_dense_bwd", s, B * self.P, self.fact, self.fslope, ptr(self.pre),
+                     ptr(g_out), ptr(self.g_pre))
+                gy_port = self.g_pre
+            call("nc_epilogue_bwd_parts", s, B, M, h, w, self.fact, self.fslope, 0,
+                 ptr(self.zs[t]), None, ptr(self.pp[0]), ptr(self.pp[1]), ptr(self.pp[2]),
+                 ptr(self.mean[t]), ptr(self.rstd[t]), ptr(gy_port), ptr(self.gz),
+                 ptr(self.pp_rows), self.pp_rows[0].numel(), ws_ep, n_ep)
+        else:
+            call("nc_port_bwd_parts", s, B, M, h, w, 0, self.fact, self.fslope, self.P,
+                 ptr(self.port_idx), ptr(self.zs[t]), None, ptr(self.pp), ptr(self.zo),
+                 ptr(self.mean[t]), ptr(self.rstd[t]), ptr(self.pre), ptr(g_out),
+                 ptr(self.gz), ptr(self.pp_rows), B * self.P, ws_ep, n_ep)
         pg_plane = self.pg_rows[0].numel()
         valid_acc = 0
         for t in range(d - 1, -1, -1):
@@ -422,7 +453,8 @@ class StepPlan:
         if d > 1:
             jobs += [(_addr(self.pg_rows[i]), _addr(g), N, 0, (d - 1) * self.R)
                      for i, g in enumerate((self.gw, self.gs, self.gb))]
-        jobs += [(_addr(self.pp_rows[i]), _addr(self.gpp[i]), self.P, 0, B) for i in range(3)]
+        jobs += [(_addr(self.pp_rows[i]), _addr(self.gpp[i]), self.P, 0, self.pp_rows.shape[1])
+                 for i in range(3)]
         call("nc_rows_sum", s, len(jobs), _abi.rows_jobs(*jobs))
         if not only_t0_grid:
             call("nc_filter_spectrum_bwd", s, M, self.kh, self.kw, fh, fw, self.cp[0],

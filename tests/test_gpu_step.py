@@ -164,3 +164,56 @@ def test_clp_chip_parity(mode, n):
     filt = rng.normal(0, 1.0 / 3.0, (1, 1, 3, 3)).astype(np.float32)
     x = (rng.random((8, 2)) > 0.5).astype(np.float32)
     check(geom, topo, cell, filt, x, "continuous", 1.0, None)
+
+
+@pytest.mark.parametrize("mode,n,final_act,act", [
+    ("SAME", 32, "sigmoid", "tanh"),         # spectral grid 64x64: fused kernels, P = 1024
+    ("CIRCULAR", 32, None, "leaky_relu"),    # the 32x32 grid itself: one-lane transforms
+    ("CIRCULAR", 64, "sigmoid", "tanh"),     # the 64x64 grid itself, P = 4096
+    ("SAME", 64, "sigmoid", "tanh"),         # spectral grid 128x128: workgroup transforms
+])
+def test_gol_chip_parity(mode, n, final_act, act):
+    """The Game-of-Life chip (topology.py:359-388, as unit_milestone6_general_vnn.py:114-160:
+    K = 3x3, M = 16, depth 4, sigmoid output, biases N(0, 0.2)): its universe port is the whole
+    grid, run as the dense port (the hidden epilogue with the port parameters)."""
+    from neurocell.engine import StepPlan
+    from neurocell.topology import ChipTopology2D
+    topo = ChipTopology2D.gol_chip(n=n, kernel_size=(3, 3), directions=16, depth=4,
+                                   padding_mode=mode)
+    geom = O.Geometry((n, n), (3, 3), 16, 4, [("rect", (0, 0), (n, n))], ("rect", (0, 0), (n, n)),
+                      padding_mode=mode)
+    rng = np.random.default_rng(32)
+    cell = np.stack([rng.normal(0, 0.1, (n, n)), rng.normal(0, 0.2, (n, n)),
+                     rng.normal(0, 1.0, (n, n))]).astype(np.float32)
+    filt = rng.normal(0, 1.0 / 3.0, (16, 1, 3, 3)).astype(np.float32)
+    x = (rng.random((4, n, n)) > 0.5).astype(np.float32)
+    plan = StepPlan(topo, 4, [(n, n)], activate=act, final_activate=final_act)
+    assert plan.dense_port and plan.P == n * n
+    B = x.shape[0]
+    g_out = rng.normal(size=(B, n, n)).astype(np.float32)
+    dev = torch.device("cuda")
+    c, f = torch.from_numpy(cell).to(dev), torch.from_numpy(filt).to(dev)
+    xt = torch.from_numpy(x).to(dev)
+    from neurocell.engine import flatten_inputs
+    out = plan.forward(c, f, flatten_inputs(xt, topo))
+    gc, gf = torch.empty_like(c), torch.empty_like(f)
+    plan.backward(c, f, torch.from_numpy(g_out.reshape(B, -1)).to(dev), gc, gf)
+    torch.cuda.synchronize()
+    r_out, r_gc, r_gf = O.propagate_vjp(cell, filt, x, geom, g_out, act=act, final_act=final_act)
+    errs = {"out": rel_l2(out.cpu().numpy(), r_out.reshape(B, -1)),
+            "gW": rel_l2(gc.cpu().numpy()[0], r_gc[0]), "gB": rel_l2(gc.cpu().numpy()[1], r_gc[1]),
+            "gS": rel_l2(gc.cpu().numpy()[2], r_gc[2]), "gG": rel_l2(gf.cpu().numpy(), r_gf)}
+    assert errs["out"] < FWD_TOL, errs
+    for k in ("gW", "gB", "gS", "gG"):
+        assert errs[k] < GRAD_TOL, errs
+
+
+def test_gol_valid_universe_port_is_refused():
+    """VALID Game of Life puts its output outside the ROI (the full-grid output path of
+    propagator.py:684-734), which this build does not run: a clear error before any launch."""
+    from neurocell.engine import StepPlan
+    from neurocell._lib import NeurocellError
+    from neurocell.topology import ChipTopology2D
+    topo = ChipTopology2D.gol_chip(n=32, kernel_size=(3, 3), directions=4, depth=2)
+    with pytest.raises(NeurocellError, match="outside the active ROI"):
+        StepPlan(topo, 2, [(32, 32)])
