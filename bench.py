@@ -40,7 +40,8 @@ def algorithmic_bytes(B, M, N, F, hb=0, dx=1, P=16):
     """Per-call algorithmic bytes (each interface operand counted once, 4 B/f32, 8 B/c64).
     spectra: the state x in (once, however many partial planes hold it), the border spectrum
     in, xhat out.  conv_epilogue_fwd: xhat and ghat in, w/s/b in, z out (training), the
-    step's output x' out (once), mean/rstd out.  correlate: xhat, ghat in, z out.
+    step's output x' out (once), mean/rstd out.  conv_port_fwd (the last step): xhat, ghat,
+    port indices and parameters in, z out (training), zo, mean/rstd and the outputs out.
     fftconv_bwd: gz, xhat, ghat in, dx out, dghat read-modify-write, the cotangent spectrum
     sum out.  The step's epilogues run without a border term (hb = 0: it is folded into the
     spectra)."""
@@ -48,7 +49,8 @@ def algorithmic_bytes(B, M, N, F, hb=0, dx=1, P=16):
         "spectra": 4 * B * N + 8 * F + 8 * B * F,
         "conv_epilogue_fwd": 8 * B * F + 8 * M * F + 12 * N + 4 * B * M * N + 4 * B * N
                              + 8 * B * M,
-        "correlate": 8 * B * F + 8 * M * F + 4 * B * M * N,
+        "conv_port_fwd": 8 * B * F + 8 * M * F + 4 * B * M * N + 16 * P + 4 * B * M * P
+                         + 8 * B * M + 4 * B * P,
         "fftconv_bwd": (4 * B * M * N + 8 * B * F + 8 * M * F + dx * 4 * B * N + 16 * M * F
                         + 8 * M * F),
         "epilogue_fwd": 4 * (B * M * N + hb * M * N + 3 * N + B * N + 2 * B * M),
@@ -90,8 +92,11 @@ def kernel_families(ts, torch, reps):
                                           p.slope, ptr(p.w_eff), ptr(p.s_eff), ptr(p.b_roi),
                                           ptr(p.zs[t]), ptr(p.xs[t + 1]), ptr(p.mean[t]),
                                           ptr(p.rstd[t]), ws_ep, n_ep),
-        "correlate": lambda: call("nc_spectral_correlate", s(), B, M, h, w, p.cp[0], p.cp[1],
-                                  fh, fw, ptr(p.xhat[t]), ptr(p.ghat), ptr(p.zs[t])),
+        "conv_port_fwd": lambda: call("nc_fftconv_port_fwd", s(), B, M, h, w, p.cp[0], p.cp[1],
+                                      fh, fw, ptr(p.xhat[t]), ptr(p.ghat), p.fact, p.fslope, p.P,
+                                      ptr(p.port_idx), ptr(p.pp), ptr(p.zs[-1]), ptr(p.out),
+                                      ptr(p.zo), ptr(p.mean[-1]), ptr(p.rstd[-1]), ptr(p.pre),
+                                      ws_ep, n_ep),
         "fftconv_bwd": lambda: call("nc_fftconv_bwd_parts", s(), B, M, h, w, h, w, p.cp[0],
                                     p.cp[1], fh, fw, ptr(p.gz), ptr(p.xhat[t]), ptr(p.ghat), 1,
                                     ptr(p.gy[0]), ptr(p.rows["dg"]), 0, 0, ptr(p.rows["gd"]),
@@ -101,18 +106,14 @@ def kernel_families(ts, torch, reps):
                                      ptr(p.b_roi), ptr(p.mean[t]), ptr(p.rstd[t]),
                                      ptr(p.gy[1]), ptr(p.gz), ptr(p.pg_rows),
                                      p.pg_rows[0].numel(), ws_ep, n_ep),
-        "port_fwd": lambda: call("nc_port_fwd", s(), B, M, h, w, 0, p.fact, p.fslope, p.P,
-                                 ptr(p.port_idx), ptr(p.zs[-1]), None, ptr(p.pp),
-                                 ptr(p.out), ptr(p.zo), ptr(p.mean[-1]), ptr(p.rstd[-1]),
-                                 ptr(p.pre), ws_ep, n_ep),
         "port_bwd": lambda: call("nc_port_bwd_parts", s(), B, M, h, w, 0, p.fact, p.fslope,
                                  p.P, ptr(p.port_idx), ptr(p.zs[-1]), None, ptr(p.pp),
                                  ptr(p.zo), ptr(p.mean[-1]), ptr(p.rstd[-1]), ptr(p.pre),
                                  ptr(p.g_out), ptr(p.gz), ptr(p.pp_rows), B * p.P, ws_ep,
                                  n_ep),
     }
-    per_step = {"spectra": p.d - 1, "conv_epilogue_fwd": p.d - 1, "correlate": 1,
-                "fftconv_bwd": p.d, "epilogue_bwd": p.d - 1, "port_fwd": 1, "port_bwd": 1}
+    per_step = {"spectra": p.d - 1, "conv_epilogue_fwd": p.d - 1, "conv_port_fwd": 1,
+                "fftconv_bwd": p.d, "epilogue_bwd": p.d - 1, "port_bwd": 1}
     return {k: (time_family(f, reps, torch), per_step[k]) for k, f in fams.items()}
 
 
@@ -122,11 +123,11 @@ _FAMILY_KERNELS = {
     "spectra": ("k_wrfft2", "k_lrfft2", "k_prfft2"),
     "conv_epilogue_fwd": ("k_pconv_epi", "k_epi_fwd", "k_group_sum", "k_tile_stats",
                           "k_tile_fwd"),
-    "correlate": ("k_wconv_fwd", "k_linv_conv", "k_pconv_fwd"),
+    "conv_port_fwd": ("k_pconv_port", "k_wconv_fwd", "k_linv_conv", "k_pconv_fwd",
+                      "k_port_fwd", "k_port_combine", "k_port_fwd_tiled"),
     "fftconv_bwd": ("k_wbwd_part", "k_psum", "k_wbwd_dx_fin", "k_wbwd_dg_red", "k_wbwd_dg_sum",
                     "k_lred", "k_linv_dx", "k_pspec", "k_pbwd_red", "k_pdx_half"),
     "epilogue_bwd": ("k_epi_bwd", "k_tile_bwd1", "k_tile_bwd2"),
-    "port_fwd": ("k_port_fwd", "k_port_combine", "k_port_fwd_tiled"),
     "port_bwd": ("k_port_bwd",),
 }
 

@@ -334,6 +334,28 @@ int nc_fftconv_epilogue_fwd(void* stream, int B, int M, int hout, int wout, int 
                             float* mean, float* rstd, void* ws, size_t ws_bytes);
 
 /*
+ * Workspace bytes for nc_fftconv_port_fwd: nc_epilogue_workspace_size, or the fused kernel's
+ * direction-group partial sums (2 * ceil(M/4) * B * n_port floats) where that is larger.
+ */
+size_t nc_fftconv_port_workspace_size(int B, int M, int h, int w, int fft_h, int fft_w,
+                                      int n_port);
+
+/*
+ * The last step's correlation (nc_spectral_correlate) and the output-port epilogue without a
+ * border term (nc_port_fwd with has_border = 0) as one operation - kernels_pallas.py:1779-1791
+ * followed by 1284-1347 and 1510-1551: out (B, P), zo (B, M, P), mean/rstd (B, M), pre (B, P)
+ * as nc_port_fwd.  z (B, M, hout, wout) receives the correlation when not NULL (a training
+ * forward keeps it for the backward); on the 32x64 and 64x64 grids it may be NULL
+ * (evaluation: the planes are standardised on chip and only the port cells leave it),
+ * elsewhere it is required.  n_port <= 256.  No counterpart in the reference (two ops there).
+ */
+int nc_fftconv_port_fwd(void* stream, int B, int M, int hout, int wout, int pad_h, int pad_w,
+                        int fft_h, int fft_w, const float* xhat, const float* ghat,
+                        int final_act, float neg_slope, int n_port, const int32_t* port_idx,
+                        const float* port_params, float* z, float* out, float* zo, float* mean,
+                        float* rstd, float* pre, void* ws, size_t ws_bytes);
+
+/*
  * The output port when it covers the whole (sub-)ROI in row-major order (P = h*w: the Game of
  * Life chip's universe port, topology.py:359-388).  pallas_fused_output_port_epilogue
  * (kernels_pallas.py:1510-1551) for such a port is the hidden epilogue with the port

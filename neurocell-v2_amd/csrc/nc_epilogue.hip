@@ -1363,3 +1363,14 @@ int nc_port_bwd_parts(void* stream, int B, int M, int h, int w, int has_border, 
 }
 
 }  // extern "C"
+
+// The port algebra over G direction-group partial sums part (2, G, B, P), for producers in
+// other translation units (the fused correlation + port of the spectral entry points).
+int nc_port_combine_launch(hipStream_t st, int B, int M, int P, int G, int final_act,
+                           float neg_slope, const float* port_params, const float* part,
+                           float* out, float* pre) {
+    hipLaunchKernelGGL(k_port_combine, dim3((B * P + 255) / 256), dim3(256), 0, st, B, M, P, G,
+                       final_act, neg_slope, port_params, part, out, pre);
+    NC_CHECK_LAUNCH();
+    return NC_OK;
+}

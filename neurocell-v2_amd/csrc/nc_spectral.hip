@@ -23,6 +23,11 @@
 #include <cstdint>
 
 #include "nc_large.h"
+
+// nc_epilogue.hip: the port algebra over direction-group partial sums (2, G, B, P).
+int nc_port_combine_launch(hipStream_t st, int B, int M, int P, int G, int final_act,
+                           float neg_slope, const float* port_params, const float* part,
+                           float* out, float* pre);
 #include "nc_pair.h"
 #include "nc_wave.h"
 
@@ -756,8 +761,8 @@ __global__ __launch_bounds__(256, 2) void k_pconv_epi(int B, int M, int hout, in
         mean[(size_t)b * M + m] = mu;
         rstd[(size_t)b * M + m] = r;
     }
-    // (zhat, act) replace the staging in this wavefront's region: every lane has read the
-    // plane above, and one wavefront's LDS operations complete in order
+    // (zhat, act) replace the staging in this wavefront's region once every lane has read it
+    __syncthreads();
     const float on = live ? 1.f : 0.f;
     float* L = lds;
     float* A = lds + N;
@@ -784,6 +789,124 @@ __global__ __launch_bounds__(256, 2) void k_pconv_epi(int B, int M, int hout, in
             ac += ldsall[(size_t)q * region + N + ec];
         }
         if (e < N) out[e] = wq[i] * lin + sq_[i] * ac;
+    }
+}
+
+// Forward correlation fused with the output-port statistics (kernels_pallas.py:1779-1791
+// then 1284-1347 and 1510-1551): workgroup (b, g) of 4 wavefronts, wavefront w correlating the
+// plane m = 4g + w (stored to z when z is given) and forming its mean and centred variance
+// (population, eps 1e-5), then zo[b][m][k] = (z[port_idx[k]] - mean) rstd for the P port
+// cells.  The workgroup adds its directions' zo (increasing m) into the partial sums
+// part (2, G, B, P) = (Σ zo, Σ final_act(zo + b_out)) that k_port_combine turns into the
+// port outputs, as nc_port_fwd's split does.  The idle wavefronts of the last group repeat
+// m = M - 1 and store nothing.
+template <int FH, int FW, int NE>
+__global__ __launch_bounds__(256) void k_pconv_port(int B, int M, int hout, int wout, int ph,
+                                                    int pw, int nq_off, int region, int P,
+                                                    int fact, float slope,
+                                                    const cpx* __restrict__ xhat,
+                                                    const cpx* __restrict__ ghat,
+                                                    const int* __restrict__ pidx,
+                                                    const float* __restrict__ pp,
+                                                    float* __restrict__ z,
+                                                    float* __restrict__ zo,
+                                                    float* __restrict__ mean,
+                                                    float* __restrict__ rstd,
+                                                    float* __restrict__ part) {
+    using P_ = PGeo<FH, FW>;
+    constexpr int PK = 4;  // port cells per lane (P <= 256)
+    HIP_DYNAMIC_SHARED(float, ldsall)
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float* lds = ldsall + (size_t)wv * region;
+    cpx* T = reinterpret_cast<cpx*>(lds);
+    cpx* NQ = T + nq_off;
+    const int b = blockIdx.x, g = blockIdx.y;
+    const int m = min(g * 4 + wv, M - 1), nm = min(4, M - g * 4);
+    const bool live = g * 4 + wv < M;
+    const int N = hout * wout;
+    const float inv_n = 1.0f / (float)N;
+    const int kc = lane >> 1, t = lane & 1;
+    const cpx* X = xhat + (size_t)b * P_::F;
+    const cpx* Gm = ghat + (size_t)m * P_::F;
+    if (lane < FH) NQ[lane] = cmul(X[lane * P_::SP + FW / 2], Gm[lane * P_::SP + FW / 2]);
+    cpx v[P_::HH];
+#pragma unroll
+    for (int j = 0; j < P_::HH; ++j) {
+        const int e = (2 * j + t) * P_::SP + kc;
+        v[j] = cmul(X[e], Gm[e]);
+    }
+    __syncthreads();
+    if (kc == 0) {
+#pragma unroll
+        for (int j = 0; j < P_::HH; ++j) v[j] = cadd(v[j], cmul_i(NQ[2 * j + t]));
+    }
+    pcol_inv<FH, FW>(v, T);
+    __syncthreads();
+    prow_inv<FH, FW>(T, ph, pw, hout, 1.0f / (float)(FH * FW), lds);
+    __syncthreads();
+    // the port cells' flat indices, requested before the statistics
+    int pe[PK];
+#pragma unroll
+    for (int j = 0; j < PK; ++j) pe[j] = min(max(pidx[min(lane + 64 * j, P - 1)], 0), N - 1);
+    const unsigned inv = ((1u << 20) + wout - 1) / wout;
+    float zv[NE];
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+        const int e = min(lane + 64 * i, N - 1);
+        const int r = (int)(((unsigned)e * inv) >> 20);
+        zv[i] = lds[r * (FW + 1) + (e - r * wout)];
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < NE; ++i) sum += lane + 64 * i < N ? zv[i] : 0.f;
+    if (z && live) {
+        float* zp = z + ((size_t)b * M + m) * N;
+#pragma unroll
+        for (int i = 0; i < NE; ++i)
+            if (lane + 64 * i < N) zp[lane + 64 * i] = zv[i];
+    }
+    const float mu = wave_sum(sum) * inv_n;
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+        const float d = lane + 64 * i < N ? zv[i] - mu : 0.f;
+        ss += d * d;
+    }
+    const float r = 1.0f / sqrtf(wave_sum(ss) * inv_n + 1e-5f);
+    if (lane == 0 && live) {
+        mean[(size_t)b * M + m] = mu;
+        rstd[(size_t)b * M + m] = r;
+    }
+    float pz[PK];
+#pragma unroll
+    for (int j = 0; j < PK; ++j) {
+        const int rr = (int)(((unsigned)pe[j] * inv) >> 20);
+        pz[j] = (lds[rr * (FW + 1) + (pe[j] - rr * wout)] - mu) * r;
+    }
+    // zo, and the wavefront's zo in its region for the direction sums, once every lane has
+    // read the staging
+    __syncthreads();
+    float* zop = zo + ((size_t)b * M + m) * P;
+#pragma unroll
+    for (int j = 0; j < PK; ++j) {
+        const int k = lane + 64 * j;
+        if (k < P) {
+            if (live) zop[k] = pz[j];
+            lds[k] = pz[j];
+        }
+    }
+    __syncthreads();
+    const size_t GBP = (size_t)gridDim.y * B * P;
+    for (int k = threadIdx.x; k < P; k += blockDim.x) {
+        const float bo = pp[2 * P + k];
+        float lin = 0.f, ac = 0.f;
+        for (int q = 0; q < nm; ++q) {
+            const float u = ldsall[(size_t)q * region + k];
+            lin += u;
+            if (fact != NC_ACT_IDENTITY) ac += nc_act(u + bo, fact, slope);
+        }
+        part[((size_t)g * B + b) * P + k] = lin;
+        part[GBP + ((size_t)g * B + b) * P + k] = ac;
     }
 }
 
@@ -1040,6 +1163,35 @@ bool launch_corr_epi(hipStream_t st, int B, int M, int hout, int wout, int ph, i
         }
 #undef NC_CE
 #undef NC_CE2
+        return true;
+    }
+}
+
+template <int FH, int FW>
+bool launch_corr_port(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw, int P,
+                      int fact, float slope, const float* xhat, const float* ghat,
+                      const int32_t* pidx, const float* pp, float* z, float* zo, float* mean,
+                      float* rstd, float* part) {
+    if constexpr (!pair_grid<FH, FW>()) {
+        return false;
+    } else {
+        const PLds l(hout, PGeo<FH, FW>::PITCH, FW, FH, true);
+        const int region = corr_epi_region<FH, FW>(hout, wout);
+        if (region == 0 || region < P) return false;
+        const size_t bytes = (size_t)4 * region * sizeof(float);
+        const dim3 grid(B, (M + 3) / 4);
+#define NC_CP(NE_)                                                                            \
+    do {                                                                                      \
+        lds_limit(k_pconv_port<FH, FW, NE_>, bytes);                                          \
+        hipLaunchKernelGGL((k_pconv_port<FH, FW, NE_>), grid, dim3(256), bytes, st, B, M,     \
+                           hout, wout, ph, pw, l.nq, region, P, fact, slope,                  \
+                           reinterpret_cast<const cpx*>(xhat),                                \
+                           reinterpret_cast<const cpx*>(ghat), pidx, pp, z, zo, mean, rstd,   \
+                           part);                                                             \
+    } while (0)
+        if (FH * FW > 2048 && hout * wout > 2048) NC_CP(FH * FW / 64);
+        else NC_CP(32);
+#undef NC_CP
         return true;
     }
 }
@@ -1430,6 +1582,53 @@ int nc_fftconv_spectra(void* stream, int B, int hin, int win, int fft_h, int fft
     NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
 #undef NC_CALL
     return NC_ERR_UNSUPPORTED;
+}
+
+size_t nc_fftconv_port_workspace_size(int B, int M, int h, int w, int fft_h, int fft_w,
+                                      int n_port) {
+    const size_t epi = nc_epilogue_workspace_size(B, M, h, w);
+    if (B <= 0 || M <= 0 || n_port <= 0 || corr_epi_region(fft_h, fft_w, h, w) == 0) return epi;
+    return std::max(epi, (size_t)2 * ((M + 3) / 4) * B * n_port * sizeof(float));
+}
+
+int nc_fftconv_port_fwd(void* stream, int B, int M, int hout, int wout, int pad_h, int pad_w,
+                        int fft_h, int fft_w, const float* xhat, const float* ghat,
+                        int final_act, float neg_slope, int n_port, const int32_t* port_idx,
+                        const float* port_params, float* z, float* out, float* zo, float* mean,
+                        float* rstd, float* pre, void* ws, size_t ws_bytes) {
+    int rc = fftconv_check(B, M, 1, 1, hout, wout, pad_h, pad_w, fft_h, fft_w);
+    if (rc != NC_OK) return rc;
+    if (!xhat || !ghat || n_port <= 0 || n_port > 256 || M * n_port > 8192 || !port_idx ||
+        !port_params || !out || !zo || !mean || !rstd || final_act < 0 || final_act > 5 ||
+        (final_act != NC_ACT_IDENTITY && !pre))
+        return NC_ERR_INVALID_ARGUMENT;
+    if (ws_bytes < nc_fftconv_port_workspace_size(B, M, hout, wout, fft_h, fft_w, n_port) || !ws)
+        return NC_ERR_WORKSPACE;
+    hipStream_t st = nc_stream(stream);
+    float* part = reinterpret_cast<float*>(ws);
+    bool done = false;
+    if (corr_epi_region(fft_h, fft_w, hout, wout) > 0) {
+        if (fft_h == 64)
+            done = launch_corr_port<64, 64>(st, B, M, hout, wout, pad_h, pad_w, n_port,
+                                            final_act, neg_slope, xhat, ghat, port_idx,
+                                            port_params, z, zo, mean, rstd, part);
+        else
+            done = launch_corr_port<32, 64>(st, B, M, hout, wout, pad_h, pad_w, n_port,
+                                            final_act, neg_slope, xhat, ghat, port_idx,
+                                            port_params, z, zo, mean, rstd, part);
+    }
+    if (done) {
+        NC_CHECK_LAUNCH();
+        return nc_port_combine_launch(st, B, M, n_port, (M + 3) / 4, final_act, neg_slope,
+                                      port_params, part, out, pre);
+    }
+    // other grids: the correlation into z, then the port
+    if (!z) return NC_ERR_INVALID_ARGUMENT;
+    rc = nc_spectral_correlate(stream, B, M, hout, wout, pad_h, pad_w, fft_h, fft_w, xhat, ghat,
+                               z);
+    if (rc != NC_OK) return rc;
+    return nc_port_fwd(stream, B, M, hout, wout, 0, final_act, neg_slope, n_port, port_idx, z,
+                       nullptr, port_params, out, zo, mean, rstd, pre, ws, ws_bytes);
 }
 
 int nc_fftconv_epilogue_partials(int B, int M, int h, int w, int fft_h, int fft_w) {

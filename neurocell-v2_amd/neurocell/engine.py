@@ -271,7 +271,8 @@ class StepPlan:
         if self.dense_port:  # the port's direction-group partial outputs
             self.port_parts = torch.empty(self.G, B, h, w, **f)
         self.pre = torch.empty(B, self.P, **f) if self.fact != 0 else None
-        n_ep = _abi_size("nc_epilogue_workspace_size", B, M, h, w)
+        n_ep = max(_abi_size("nc_epilogue_workspace_size", B, M, h, w),
+                   _abi_size("nc_fftconv_port_workspace_size", B, M, h, w, *self.fft, self.P))
         self.ws_epi = torch.empty(max(1, n_ep // 4), **f)
         if self.training:
             n_fc = max(_abi_size("nc_fftconv_bwd_workspace_size", B, M, *self.fft),
@@ -378,12 +379,13 @@ class StepPlan:
                 call("nc_port_dense_fwd", s, B * self.P, self.G, self.fact, self.fslope,
                      ptr(self.port_parts), ptr(self.out), ptr(self.pre))
             else:
-                call("nc_spectral_correlate", s, B, M, h, w, p0[0], p0[1], fh, fw, ptr(xh),
-                     ptr(self.ghat), ptr(z))
-                call("nc_port_fwd", s, B, M, h, w, 0, self.fact, self.fslope, self.P,
-                     ptr(self.port_idx), ptr(z), None, ptr(self.pp), ptr(self.out),
-                     ptr(self.zo), ptr(self.mean[t]), ptr(self.rstd[t]), ptr(self.pre),
-                     ptr(self.ws_epi), self.ws_epi.numel() * 4)
+                # the correlation and the port statistics in one kernel on the 64-wide grids
+                zk = None if fused and not self.training else z
+                call("nc_fftconv_port_fwd", s, B, M, h, w, p0[0], p0[1], fh, fw, ptr(xh),
+                     ptr(self.ghat), self.fact, self.fslope, self.P, ptr(self.port_idx),
+                     ptr(self.pp), ptr(zk), ptr(self.out), ptr(self.zo), ptr(self.mean[t]),
+                     ptr(self.rstd[t]), ptr(self.pre), ptr(self.ws_epi),
+                     self.ws_epi.numel() * 4)
         return self.out
 
     # ------------------------------------------------------------------ reverse

@@ -467,6 +467,63 @@ def case_fftconv_epilogue(be, B=3, M=6, h=20, w=27, kh=7, kw=5, FH=32, FW=64, ac
     return res
 
 
+def case_fftconv_port(be, B=3, M=6, h=20, w=27, kh=7, kw=5, FH=32, FW=64, fact=None,
+                      rows=(2, 3, 19, 3, 0), cols=(5, 5, 26, 5, 0), seed=11):
+    """nc_fftconv_port_fwd (the last step's correlation and output port in one operation)
+    against nc_spectral_correlate + nc_port_fwd and the oracle: out, zo, mean, rstd, pre and z,
+    with a duplicated port cell and the grid's corners; on the fused grids the call without z
+    must give the same outputs bit for bit."""
+    rng = np.random.default_rng(seed)
+    L, s = be.lib, be.stream()
+    ph, pw = (kh - 1) // 2, (kw - 1) // 2
+    P = len(rows)
+    idx = np.array([r * w + c for r, c in zip(rows, cols)], np.int32)
+    x = rng.normal(size=(B, h, w)).astype(np.float32)
+    g = rng.normal(size=(M, 1, kh, kw)).astype(np.float32)
+    pp = rng.normal(size=(3, P)).astype(np.float32)
+    xd, gd, idd, ppd = be.put(x), be.put(g), be.put(idx, np.int32), be.put(pp)
+    fid = _abi.ACT_IDS["identity" if fact is None else fact]
+    ghat, xhat = be.zeros((M, FH, FW // 2 + 1, 2)), be.zeros((B, FH, FW // 2 + 1, 2))
+    _ok(be, L.nc_filter_spectrum_fwd(s, M, kh, kw, FH, FW, be.ptr(gd), be.ptr(ghat)), "spec")
+    _ok(be, L.nc_fftconv_spectra(s, B, h, w, FH, FW, be.ptr(xd), 1, None, be.ptr(xhat)), "xs")
+    nws = L.nc_fftconv_port_workspace_size(B, M, h, w, FH, FW, P)
+    ws = be.zeros((nws // 4 + 1,))
+    nb = ws.nbytes if hasattr(ws, "nbytes") else ws.numel() * 4
+    res, got = {}, []
+    fused = FW == 64 and FH in (32, 64)
+    for mode in (("ref", "z", "noz") if fused else ("ref", "z")):
+        out, zo = be.zeros((B, P)), be.zeros((B, M, P))
+        mean, rstd, pre, z = be.zeros((B, M)), be.zeros((B, M)), be.zeros((B, P)), \
+            be.zeros((B, M, h, w))
+        if mode == "ref":
+            _ok(be, L.nc_spectral_correlate(s, B, M, h, w, ph, pw, FH, FW, be.ptr(xhat),
+                                            be.ptr(ghat), be.ptr(z)), "corr")
+            _ok(be, L.nc_port_fwd(s, B, M, h, w, 0, fid, 0.01, P, be.ptr(idd), be.ptr(z), None,
+                                  be.ptr(ppd), be.ptr(out), be.ptr(zo), be.ptr(mean),
+                                  be.ptr(rstd), be.ptr(pre), be.ptr(ws), nb), "port")
+        else:
+            _ok(be, L.nc_fftconv_port_fwd(s, B, M, h, w, ph, pw, FH, FW, be.ptr(xhat),
+                                          be.ptr(ghat), fid, 0.01, P, be.ptr(idd), be.ptr(ppd),
+                                          be.ptr(z) if mode == "z" else None, be.ptr(out),
+                                          be.ptr(zo), be.ptr(mean), be.ptr(rstd), be.ptr(pre),
+                                          be.ptr(ws), nb), "fused")
+        got.append({k: be.get(v) for k, v in (("out", out), ("zo", zo), ("mean", mean),
+                                               ("rstd", rstd), ("pre", pre), ("z", z))})
+    ref, fz = got[0], got[1]
+    zr = O.conv2d_direct(x, g[:, 0], (ph, pw))
+    o_r, aux = O.port_fwd(zr, np.zeros((M, h, w)), np.array(rows), np.array(cols), (P, 1),
+                          pp[0][:, None], pp[1][:, None], pp[2][:, None], False, fact)
+    res["out"] = rel_l2(fz["out"], o_r[:, :, 0])
+    res["zo"] = rel_l2(fz["zo"], aux["zo"][..., 0])
+    res["z"] = rel_l2(fz["z"], zr)
+    for k in ("out", "zo", "mean", "rstd", "z") + (("pre",) if fact else ()):
+        res[k + "_vs_separate"] = rel_l2(fz[k], ref[k])
+    if fused:
+        res["no_z_mismatch"] = float(sum(int((got[1][k] != got[2][k]).sum())
+                                         for k in ("out", "zo", "mean", "rstd", "pre")))
+    return res
+
+
 def case_fftconv_circular(be, B=2, M=3, H=16, W=16, kh=5, kw=3, seed=9):
     """CIRCULAR padding mode (propagator.py:284-300): the correlation on the (H, W) grid itself,
     the output window read modulo the grid, forward (nc_fftconv_fwd and, on the 64-wide grids,

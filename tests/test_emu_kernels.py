@@ -7,7 +7,7 @@ import pytest
 
 from kernel_cases import (CODD_CASES, TOL, HostBackend, case_adaptive, case_border_conv,
                           case_border_fold, case_codd, case_epilogue, case_epilogue_parts,
-                          case_fftconv_circular, case_fftconv_epilogue,
+                          case_fftconv_circular, case_fftconv_port, case_fftconv_epilogue,
                           case_fftconv, case_helpers, case_plane_spectra, case_port)
 
 
@@ -126,4 +126,16 @@ def test_fftconv_epilogue(be, B, M, h, w, kh, kw, FH, FW, act):
 ])
 def test_fftconv_circular(be, B, M, H, W, kh, kw):
     res = case_fftconv_circular(be, B=B, M=M, H=H, W=W, kh=kh, kw=kw)
+    _assert_small(res)
+
+
+@pytest.mark.parametrize("B,M,h,w,kh,kw,FH,FW,fact", [
+    (3, 6, 20, 27, 7, 5, 32, 64, None),           # fused, idle wavefronts, identity port
+    (2, 16, 40, 50, 23, 13, 64, 64, "tanh"),      # fused, the ALU geometry, gated port
+    (3, 5, 10, 12, 5, 3, 16, 16, "sigmoid"),      # not fused: correlation then port
+])
+def test_fftconv_port(be, B, M, h, w, kh, kw, FH, FW, fact):
+    rows, cols = (2, 3, h - 1, 3, 0), (5, 5, w - 1, 5, 0)
+    res = case_fftconv_port(be, B=B, M=M, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW, fact=fact,
+                            rows=rows, cols=cols)
     _assert_small(res)
