@@ -120,6 +120,20 @@ int nc_filter_spectrum_bwd(void* stream, int M, int kh, int kw, int fft_h, int f
                            int accumulate, int conj_in);
 
 /*
+ * The end of a reverse pass with a border term in one launch: nc_filter_spectrum_bwd
+ * (dghat -> g_filters) and the border patch's gradient of nc_fftconv_bwd_hat without dghat
+ * (g_patch (hp, wp) = irfft2(sum over m of gz_hat_m * conj(ghat_m)) rolled by
+ * (pshift_h, pshift_w), cropped): the patch spectrum's reduction over m, then one launch for
+ * all M + 1 inverse transforms.  ws: fft_h * (fft_w/2+1) complex values.
+ * No counterpart in the reference.
+ */
+int nc_filter_patch_bwd(void* stream, int M, int kh, int kw, int fft_h, int fft_w,
+                        int shift_h, int shift_w, const float* dghat, float* g_filters,
+                        int accumulate, int conj_in, int hp, int wp, int pshift_h, int pshift_w,
+                        const float* gz_hat, const float* ghat, float* g_patch, void* ws,
+                        size_t ws_bytes);
+
+/*
  * Overlap-save spectral cross-correlation forward: conv2d_pruned_rfft_roi_step /
  * conv2d_roi_rfft_step forward (kernels_pallas.py:1759-1791, kernels_greens.py:316-360) and,
  * with pad = (kh-1, kw-1), conv2d_valid_rfft_precomputed (kernels_greens.py:403-425) and the

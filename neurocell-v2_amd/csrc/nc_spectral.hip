@@ -81,6 +81,42 @@ __global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_filter_spectrum_bwd(
         sm.work, sm.scr, sm.tw);
 }
 
+// The filter gradients and the border patch's gradient in one launch: workgroups m < M as
+// k_filter_spectrum_bwd; workgroup M inverts the patch's cotangent spectrum pspec (unpacked,
+// k_hat_red's sum over m of S_m conj(ghat_m): the one-sample correlation backward of
+// kernels_pallas.py:1794-1812), rolled by (pshift_h, pshift_w) and cropped to (hp, wp).
+template <int FH, int FW>
+__global__ __launch_bounds__((Plane<FH, FW>::NT)) void k_filter_patch_bwd(
+    int M, int kh, int kw, int shift_h, int shift_w, const cpx* __restrict__ dghat,
+    float* __restrict__ gfilt, int accumulate, int conj_in, int hp, int wp, int pshift_h,
+    int pshift_w, const cpx* __restrict__ pspec, float* __restrict__ gpatch) {
+    using P = Plane<FH, FW>;
+    __shared__ Smem<FH, FW> sm;
+    NC_SPECTRAL_PROLOGUE(sm);
+    const int m = blockIdx.x;
+    const float scale = 1.0f / (float)(FH * FW);
+    if (m < M) {
+        const cpx* d = dghat + (size_t)m * P::F;
+        float* out = gfilt + (size_t)m * kh * kw;
+        plane_irfft2<FH, FW>(
+            [&](int a, int b) {
+                const cpx v = d[a * P::SP + b];
+                return conj_in ? cconj(v) : v;
+            },
+            (FH - (shift_h % FH)) & (FH - 1), kh, (FW - (shift_w % FW)) & (FW - 1), kw, scale,
+            [&](int i, int j, float v) {
+                float* o = out + (kh - 1 - i) * kw + (kw - 1 - j);
+                *o = accumulate ? *o + v : v;
+            },
+            sm.work, sm.scr, sm.tw);
+    } else {
+        plane_irfft2<FH, FW>(
+            [&](int a, int b) { return pspec[a * P::SP + b]; },
+            (FH - (pshift_h % FH)) & (FH - 1), hp, (FW - (pshift_w % FW)) & (FW - 1), wp, scale,
+            [&](int i, int j, float v) { gpatch[i * wp + j] = v; }, sm.work, sm.scr, sm.tw);
+    }
+}
+
 // ----------------------------------------------------------------------------------------
 // Wavefront kernels (one 64-lane wavefront per workgroup)
 // ----------------------------------------------------------------------------------------
@@ -1413,6 +1449,25 @@ int launch_spec_bwd(hipStream_t st, int M, int kh, int kw, int sh, int sw, const
 }
 
 template <int FH, int FW>
+int launch_filter_patch(hipStream_t st, int M, int kh, int kw, int sh, int sw,
+                        const float* dghat, float* g, int acc, int conj_in, int hp, int wp,
+                        int psh, int psw, const float* shat, const float* ghat, float* gp,
+                        void* ws) {
+    // the patch's cotangent spectrum (unpacked) into the workspace, then both inverses
+    cpx* pspec = reinterpret_cast<cpx*>(ws);
+    const int np = FH * (FW / 2);
+    hipLaunchKernelGGL(k_hat_red, dim3((np + 255) / 256), dim3(256), 0, st, M, FH, FW / 2, 0,
+                       reinterpret_cast<const cpx*>(shat), nullptr,
+                       reinterpret_cast<const cpx*>(ghat), pspec, nullptr, 0, 0);
+    NC_CHECK_LAUNCH();
+    hipLaunchKernelGGL((k_filter_patch_bwd<FH, FW>), dim3(M + 1), dim3(Plane<FH, FW>::NT), 0, st,
+                       M, kh, kw, sh, sw, reinterpret_cast<const cpx*>(dghat), g, acc, conj_in,
+                       hp, wp, psh, psw, pspec, gp);
+    NC_CHECK_LAUNCH();
+    return NC_OK;
+}
+
+template <int FH, int FW>
 size_t launch_ws(int B, int M) {
     return bwd_ws<FH, FW>(B, M);
 }
@@ -1461,6 +1516,33 @@ int nc_filter_spectrum_bwd(void* stream, int M, int kh, int kw, int fft_h, int f
     if (!pow2_ok(fft_h) || !pow2_ok(fft_w)) return NC_ERR_UNSUPPORTED;
 #define NC_CALL(A, Bv) \
     launch_spec_bwd<A, Bv>(st, M, kh, kw, shift_h, shift_w, dghat, g_filters, accumulate, conj_in)
+    NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
+#undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
+}
+
+int nc_filter_patch_bwd(void* stream, int M, int kh, int kw, int fft_h, int fft_w,
+                        int shift_h, int shift_w, const float* dghat, float* g_filters,
+                        int accumulate, int conj_in, int hp, int wp, int pshift_h, int pshift_w,
+                        const float* gz_hat, const float* ghat, float* g_patch, void* ws,
+                        size_t ws_bytes) {
+    if (M <= 0 || kh <= 0 || kw <= 0 || kh > fft_h || kw > fft_w || !dghat || !g_filters ||
+        shift_h < 0 || shift_w < 0 || hp <= 0 || wp <= 0 || hp > fft_h || wp > fft_w ||
+        pshift_h < 0 || pshift_w < 0 || !gz_hat || !ghat || !g_patch)
+        return NC_ERR_INVALID_ARGUMENT;
+    if (nc_large_grid(fft_h, fft_w) || !pow2_ok(fft_h) || !pow2_ok(fft_w)) {
+        // the workgroup-segment grids: the two operations one after the other
+        const int rc = nc_filter_spectrum_bwd(stream, M, kh, kw, fft_h, fft_w, shift_h, shift_w,
+                                              dghat, g_filters, accumulate, conj_in);
+        if (rc != NC_OK) return rc;
+        return nc_fftconv_bwd_hat(stream, M, hp, wp, pshift_h, pshift_w, fft_h, fft_w, gz_hat,
+                                  nullptr, ghat, g_patch, nullptr, 0, 0, ws, ws_bytes);
+    }
+    if (ws_bytes < (size_t)fft_h * (fft_w / 2 + 1) * sizeof(cpx) || !ws) return NC_ERR_WORKSPACE;
+    hipStream_t st = nc_stream(stream);
+#define NC_CALL(A, Bv)                                                                       \
+    launch_filter_patch<A, Bv>(st, M, kh, kw, shift_h, shift_w, dghat, g_filters, accumulate, \
+                               conj_in, hp, wp, pshift_h, pshift_w, gz_hat, ghat, g_patch, ws)
     NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
 #undef NC_CALL
     return NC_ERR_UNSUPPORTED;

@@ -458,17 +458,19 @@ class StepPlan:
         jobs += [(_addr(self.pp_rows[i]), _addr(self.gpp[i]), self.P, 0, self.pp_rows.shape[1])
                  for i in range(3)]
         call("nc_rows_sum", s, len(jobs), _abi.rows_jobs(*jobs))
-        if not only_t0_grid:
-            call("nc_filter_spectrum_bwd", s, M, self.kh, self.kw, fh, fw, self.cp[0],
-                 self.cp[1], ptr(self.dghat), ptr(g_filt), 0, 0)
         g_patch = None
         if self.border:
-            # border conv reverse: the patch gradient from the cotangent spectra (its dG came
-            # with the ROI steps' dghat, through their border-shifted cell spectra)
-            call("nc_fftconv_bwd_hat", s, M, self.Hp, self.Wp, self.kh - 1, self.kw - 1, fh, fw,
-                 ptr(self.gdelta_hat), None, ptr(self.ghat), ptr(self.gpatch), None, 0, 0,
-                 ws_fc, n_fc)
+            # the filter gradients and the border conv's reverse in one launch: the patch
+            # gradient from the cotangent spectra (its dG came with the ROI steps' dghat,
+            # through their border-shifted cell spectra)
+            call("nc_filter_patch_bwd", s, M, self.kh, self.kw, fh, fw, self.cp[0], self.cp[1],
+                 ptr(self.dghat), ptr(g_filt), 0, 0, self.Hp, self.Wp, self.kh - 1,
+                 self.kw - 1, ptr(self.gdelta_hat), ptr(self.ghat), ptr(self.gpatch), ws_fc,
+                 n_fc)
             g_patch = ptr(self.gpatch)
+        elif not only_t0_grid:
+            call("nc_filter_spectrum_bwd", s, M, self.kh, self.kw, fh, fw, self.cp[0],
+                 self.cp[1], ptr(self.dghat), ptr(g_filt), 0, 0)
         if valid_acc:
             call("nc_filter_spectrum_bwd", s, M, self.kh, self.kw, fh, fw, self.kh - 1,
                  self.kw - 1, ptr(self.dghat_v), ptr(g_filt), int(not only_t0_grid), 0)

@@ -251,6 +251,11 @@ def case_border_fold(be, B=3, M=4, h=12, w=10, kh=7, kw=5, FH=32, FW=16, seed=5)
     gp = be.zeros((1, Hp, Wp))
     _ok(be, L.nc_fftconv_bwd_hat(s, M, Hp, Wp, kh - 1, kw - 1, FH, FW, be.ptr(ssum), None,
                                  be.ptr(ghat), be.ptr(gp), None, 0, 0, be.ptr(ws), nb), "bwd_hat")
+    # both in one launch
+    gf2, gp2 = be.zeros((M, 1, kh, kw)), be.zeros((1, Hp, Wp))
+    _ok(be, L.nc_filter_patch_bwd(s, M, kh, kw, FH, FW, ph, pw, be.ptr(dgh), be.ptr(gf2), 0, 0,
+                                  Hp, Wp, kh - 1, kw - 1, be.ptr(ssum), be.ptr(ghat),
+                                  be.ptr(gp2), be.ptr(ws), nb), "filter_patch")
     # references: the shifted spectrum from NumPy's rfft2 of the rolled plane; the rest from
     # brute-force correlations of the two terms
     grid = np.zeros((FH, FW))
@@ -263,7 +268,9 @@ def case_border_fold(be, B=3, M=4, h=12, w=10, kh=7, kw=5, FH=32, FW=16, seed=5)
     return {"shifted_spectrum": rel_l2(_cplx(be.get(padd))[0], shifted),
             "z": rel_l2(be.get(z), O.conv2d_direct(x, gk, (ph, pw)) + delta),
             "dx": rel_l2(be.get(dx), dxr), "dG": rel_l2(be.get(gf)[:, 0], dgr + dgb),
-            "dpatch": rel_l2(be.get(gp), gpr)}
+            "dpatch": rel_l2(be.get(gp), gpr),
+            "dG_one_launch": rel_l2(be.get(gf2)[:, 0], dgr + dgb),
+            "dpatch_one_launch": rel_l2(be.get(gp2), gpr)}
 
 
 def case_plane_spectra(be, B=3, M=4, h=12, w=10, kh=7, kw=5, FH=32, FW=16, seed=6):
