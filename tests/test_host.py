@@ -49,6 +49,38 @@ def test_library_exports_every_declared_symbol():
     assert lib.nc_fftconv_bwd_workspace_size(128, 16, 64, 64) > 0
 
 
+def test_fused_entry_queries_and_argument_checks():
+    """Host arithmetic of the fused entries' partial counts and workspace sizes, and their
+    argument checks (which return before any HIP call)."""
+    from neurocell import _abi
+    from neurocell._lib import lib_path
+    if not os.path.exists(lib_path()):
+        pytest.skip("native library not built")
+    lib = _abi.declare(ctypes.CDLL(lib_path()))
+    bad = _abi.NC_ERR_INVALID_ARGUMENT
+    # the fused kernels run on the 32x64 / 64x64 grids: 4 directions per workgroup
+    assert lib.nc_fftconv_epilogue_partials(128, 16, 40, 50, 64, 64) == 4
+    assert lib.nc_fftconv_epilogue_partials(128, 6, 20, 27, 32, 64) == 2
+    assert (lib.nc_fftconv_epilogue_partials(128, 16, 10, 12, 16, 16)
+            == lib.nc_epilogue_fwd_partials(128, 16, 10, 12))
+    epi = lib.nc_epilogue_workspace_size(1024, 64, 40, 50)
+    assert lib.nc_fftconv_port_workspace_size(1024, 64, 40, 50, 64, 64, 256) == \
+        max(epi, 2 * 16 * 1024 * 256 * 4)
+    assert lib.nc_fftconv_port_workspace_size(8, 16, 10, 12, 16, 16, 16) == \
+        lib.nc_epilogue_workspace_size(8, 16, 10, 12)
+    # rejected before any launch
+    assert lib.nc_fftconv_port_fwd(None, 2, 4, 40, 50, 11, 6, 64, 64, None, None, 0, 0.0, 0,
+                                   None, None, None, None, None, None, None, None, None,
+                                   0) == bad
+    assert lib.nc_port_dense_fwd(None, 0, 1, 0, 0.0, None, None, None) == bad
+    assert lib.nc_port_dense_bwd(None, 8, 0, 0.0, None, None, None) == bad
+    assert lib.nc_filter_patch_bwd(None, 4, 5, 3, 16, 16, 2, 1, None, None, 0, 0, 17, 10, 4,
+                                   2, None, None, None, None, 0) == bad
+    assert lib.nc_fftconv_epilogue_fwd(None, 2, 4, 40, 50, 11, 6, 64, 64, None, None, 1, 0.0,
+                                       None, None, None, None, None, None, None, None,
+                                       0) == bad
+
+
 def test_product_path_fails_loudly_without_device():
     if torch.cuda.is_available():
         pytest.skip("a device is visible")
