@@ -98,6 +98,14 @@ int nc_codd_fuse_bwd(void* stream, const nc_chip_desc* chip, const float* cell,
                      const float* g_s_eff, const float* g_b_roi, const float* g_border_patch,
                      const float* g_port_params, float* g_cell);
 
+/*
+ * gated_filters (propagator.py:266-267): gated (n) = sigmoid(filters); the reverse turns the
+ * gradient with respect to the gated filters, g_filters (n), into the gradient with respect to
+ * the raw filters in place: g *= gated * (1 - gated).
+ */
+int nc_filter_gate_fwd(void* stream, int n, const float* filters, float* gated);
+int nc_filter_gate_bwd(void* stream, int n, const float* gated, float* g_filters);
+
 /* ---------------- piece 2: Green's-function convolution (spectral) -------------------- */
 
 /*

@@ -370,6 +370,18 @@ __global__ void k_adamw(int n, float* __restrict__ p, const float* __restrict__ 
     p[i] = p[i] - rate * u;
 }
 
+// Gated filters (propagator.py:266-267): sigmoid of the raw filters, and the gradient's
+// chain rule through it in place.
+__global__ void k_gate_fwd(int n, const float* __restrict__ x, float* __restrict__ y) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = nc_sigmoid(x[i]);
+}
+
+__global__ void k_gate_bwd(int n, const float* __restrict__ y, float* __restrict__ g) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) g[i] = g[i] * (y[i] * (1.0f - y[i]));
+}
+
 __global__ void k_count_inc(int* count) {
     if (threadIdx.x == 0 && blockIdx.x == 0) count[0] = count[0] + 1;
 }
@@ -500,6 +512,22 @@ int nc_adamw_step(void* stream, int n, float* p, const float* g, float* m, float
                        n_lr, b1, b2, eps, weight_decay);
     NC_CHECK_LAUNCH();
     hipLaunchKernelGGL(k_count_inc, dim3(1), dim3(64), 0, st, count);
+    NC_CHECK_LAUNCH();
+    return NC_OK;
+}
+
+int nc_filter_gate_fwd(void* stream, int n, const float* filters, float* gated) {
+    if (n <= 0 || !filters || !gated) return NC_ERR_INVALID_ARGUMENT;
+    hipLaunchKernelGGL(k_gate_fwd, dim3((n + 255) / 256), dim3(256), 0, nc_stream(stream), n,
+                       filters, gated);
+    NC_CHECK_LAUNCH();
+    return NC_OK;
+}
+
+int nc_filter_gate_bwd(void* stream, int n, const float* gated, float* g_filters) {
+    if (n <= 0 || !gated || !g_filters) return NC_ERR_INVALID_ARGUMENT;
+    hipLaunchKernelGGL(k_gate_bwd, dim3((n + 255) / 256), dim3(256), 0, nc_stream(stream), n,
+                       gated, g_filters);
     NC_CHECK_LAUNCH();
     return NC_OK;
 }

@@ -77,6 +77,8 @@ _SIGS = {
     "nc_spectral_correlate": (I, [P, I, I, I, I, I, I, I, I, P, P, P]),
     "nc_fftconv_spectra": (I, [P, I, I, I, I, I, P, I, P, P]),
     "nc_port_dense_fwd": (I, [P, I, I, I, F, P, P, P]),
+    "nc_filter_gate_fwd": (I, [P, I, P, P]),
+    "nc_filter_gate_bwd": (I, [P, I, P, P]),
     "nc_filter_patch_bwd": (I, [P, I, I, I, I, I, I, I, P, P, I, I, I, I, I, I, P, P, P, P,
                                 SZ]),
     "nc_fftconv_port_workspace_size": (SZ, [I, I, I, I, I, I, I]),

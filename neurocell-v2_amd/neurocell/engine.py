@@ -117,7 +117,7 @@ class StepPlan:
 
     def __init__(self, topology: ChipTopology2D, batch_size: int, port_shapes: list,
                  roi_bbox=None, activate="tanh", final_activate=None, hard_pin_io=False,
-                 training=True, device=None):
+                 training=True, device=None, gated_filters=False):
         if not topology.out_in_roi:
             raise NeurocellError("output port outside the active ROI is not supported")
         self.device = device or require_device()
@@ -125,6 +125,8 @@ class StepPlan:
         self.B = int(batch_size)
         self.training = bool(training)
         self.hard_pin_io = bool(hard_pin_io)
+        # gated filters (propagator.py:266-267): the steps use sigmoid(filters)
+        self.gated = bool(gated_filters)
         self.act, self.slope = act_id(activate)
         self.fact, self.fslope = act_id(final_activate)
         H, W = topology.grid_shape
@@ -253,6 +255,7 @@ class StepPlan:
         self.patch = torch.empty(self.Hp, self.Wp, **f)
         self.pp = torch.empty(3, self.P, **f)
         self.ghat = torch.empty(M, F, **c)
+        self.filt_g = torch.empty(M, 1, self.kh, self.kw, **f) if self.gated else None
         self.border_hat = torch.empty(1, F, **c)  # shifted border-patch spectrum
         t0_shape = (B, self.H, self.W) if self.t0_grid else (B, h, w)
         self.x0 = torch.empty(*t0_shape, **f)
@@ -335,6 +338,9 @@ class StepPlan:
         # border patch's and the first step's cell spectra
         x0h, x0w = (self.H, self.W) if self.t0_grid else (h, w)
         xh0 = self.xhat[0]
+        if self.gated:
+            call("nc_filter_gate_fwd", s, self.filt_g.numel(), ptr(filt), ptr(self.filt_g))
+            filt = self.filt_g
         jobs = [(_addr(filt), _addr(self.ghat), None, M, self.kh, self.kw, 1, 0, 0),
                 (_addr(self.x0), _addr(xh0), None, B, x0h, x0w, 0, 0, 0)]
         if self.border:
@@ -474,6 +480,8 @@ class StepPlan:
         if valid_acc:
             call("nc_filter_spectrum_bwd", s, M, self.kh, self.kw, fh, fw, self.kh - 1,
                  self.kw - 1, ptr(self.dghat_v), ptr(g_filt), int(not only_t0_grid), 0)
+        if self.gated:  # the chain rule through the gate, in place
+            call("nc_filter_gate_bwd", s, self.filt_g.numel(), ptr(self.filt_g), ptr(g_filt))
         has_epi = d > 1
         mode = _abi.CODD_IDS[codd_mode]
         call("nc_codd_fuse_bwd", s, self.chip, ptr(cell), ptr(self.io_mask), ptr(self.owm), mode,

@@ -40,15 +40,16 @@ class _PlanCache:
         self.plans = {}
 
     def get(self, topology, B, port_shapes, roi_bbox, activate, final_activate, hard_pin_io,
-            training, device):
+            training, device, gated_filters=False):
         key = (id(topology), topology, B, tuple(port_shapes), roi_bbox, str(activate),
-               str(final_activate), bool(hard_pin_io), bool(training), str(device))
+               str(final_activate), bool(hard_pin_io), bool(training), str(device),
+               bool(gated_filters))
         p = self.plans.get(key)
         if p is None:
             p = self.plans[key] = StepPlan(topology, B, port_shapes, roi_bbox=roi_bbox,
                                            activate=activate, final_activate=final_activate,
                                            hard_pin_io=hard_pin_io, training=training,
-                                           device=device)
+                                           device=device, gated_filters=gated_filters)
         return p
 
 
@@ -96,8 +97,8 @@ def propagate_vnn_2d(params, inputs, topology: ChipTopology2D, activate="tanh",
                          f"{SUPPORTED_CODD_MODES}.")
     if not norm:
         raise NeurocellError("norm=False is not part of the MI355X path")
-    if sharpen_filter is not None or gated_filters:
-        raise NeurocellError("sharpen_filter / gated_filters are not part of the MI355X path")
+    if sharpen_filter is not None:
+        raise NeurocellError("sharpen_filter is not part of the MI355X path")
     if return_universe:
         raise NeurocellError("return_universe=True is not supported yet on the MI355X path")
     roi_bbox = None
@@ -107,7 +108,8 @@ def propagate_vnn_2d(params, inputs, topology: ChipTopology2D, activate="tanh",
     cell, filt = params.cell_params, params.greens_filters
     need_grad = torch.is_grad_enabled() and (cell.requires_grad or filt.requires_grad)
     plan = _PLANS.get(topology, x_flat.shape[0], port_input_shapes(inputs, topology), roi_bbox,
-                      activate, final_activate, hard_pin_io, need_grad, cell.device)
+                      activate, final_activate, hard_pin_io, need_grad, cell.device,
+                      gated_filters)
     codd = (codd_mode, inv_tau_f32(float(state_temperature)), float(active_threshold))
     out = _Propagate.apply(cell, filt, x_flat, plan, codd, need_grad)
     oh, ow = topology.out_port.size

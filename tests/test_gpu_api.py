@@ -428,3 +428,23 @@ def test_trained_checkpoint_alu_accuracy():
     ok = ~(np.abs(np.abs(out - np.round(out)) - 0.5) < 1e-4).any(-1)
     assert np.array_equal(host(preds[0])[:, 0][ok], ref[ok])
     assert acc >= 0.98, acc
+
+
+def test_gated_filters_autograd():
+    """gated_filters (propagator.py:266-267): the steps use sigmoid(filters).  Against the
+    oracle run on the gated filters, with the raw filters' gradient by the chain rule through
+    the sigmoid."""
+    from neurocell import VNNParams, propagate_vnn_2d
+    from neurocell.topology import ChipTopology2D
+    geom, cell, filt, x, _ = alu_case(12, B=8)
+    filt = (filt * 8.0).astype(np.float32)  # spread the gate over its range
+    topo = ChipTopology2D.alu_chip(out_width=2)
+    p = VNNParams(dev(cell).requires_grad_(), dev(filt).requires_grad_())
+    out = propagate_vnn_2d(p, dev(x), topo, gated_filters=True)
+    g = np.random.default_rng(13).normal(size=tuple(out.shape)).astype(np.float32)
+    out.backward(dev(g))
+    sg = 1.0 / (1.0 + np.exp(-filt.astype(np.float64)))
+    r_out, r_gc, r_gf = O.propagate_vjp(cell, sg, x, geom, g)
+    assert rel_l2(host(out), r_out) < FWD_TOL
+    assert rel_l2(host(p.cell_params.grad), r_gc) < GRAD_TOL
+    assert rel_l2(host(p.greens_filters.grad), r_gf * sg * (1.0 - sg)) < GRAD_TOL
