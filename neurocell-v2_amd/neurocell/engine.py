@@ -117,7 +117,7 @@ class StepPlan:
 
     def __init__(self, topology: ChipTopology2D, batch_size: int, port_shapes: list,
                  roi_bbox=None, activate="tanh", final_activate=None, hard_pin_io=False,
-                 training=True, device=None, gated_filters=False):
+                 training=True, device=None, gated_filters=False, sharpen=None):
         if not topology.out_in_roi:
             raise NeurocellError("output port outside the active ROI is not supported")
         self.device = device or require_device()
@@ -127,6 +127,8 @@ class StepPlan:
         self.hard_pin_io = bool(hard_pin_io)
         # gated filters (propagator.py:266-267): the steps use sigmoid(filters)
         self.gated = bool(gated_filters)
+        # weight sharpening (params.py:246-247): the Codd fusion sees corr_SAME(W, kernel)
+        self.sharpen = None if sharpen is None else np.ascontiguousarray(sharpen, np.float32)
         self.act, self.slope = act_id(activate)
         self.fact, self.fslope = act_id(final_activate)
         H, W = topology.grid_shape
@@ -196,6 +198,14 @@ class StepPlan:
                                  "in row-major order (the port kernels gather at most 256 "
                                  "cells, 8192 per sample over the directions)")
         self.io_mask = torch.tensor(topology.io_state_mask.astype(np.uint8), device=dev)
+        if self.sharpen is not None:
+            sh, sw = self.sharpen.shape
+            if sh % 2 == 0 or sw % 2 == 0 or sh > H or sw > W:
+                raise NeurocellError(f"sharpen kernel {self.sharpen.shape} must be odd and fit "
+                                     "the grid")
+            self.sh_fft = tuple(max(16, _npow2(v)) for v in (H + sh - 1, W + sw - 1))
+            if not spectral_grid_supported(*self.sh_fft):
+                raise NeurocellError(f"the sharpening grid {self.sh_fft} is not supported")
         self.owm = torch.tensor(topology.out_weight_mask.astype(np.uint8), device=dev)
         # input injection map (gather form)
         self.port_shapes = [tuple(int(v) for v in s) for s in port_shapes]
@@ -256,6 +266,20 @@ class StepPlan:
         self.pp = torch.empty(3, self.P, **f)
         self.ghat = torch.empty(M, F, **c)
         self.filt_g = torch.empty(M, 1, self.kh, self.kw, **f) if self.gated else None
+        if self.sharpen is not None:
+            H, W = self.H, self.W
+            fs = self.sh_fft[0] * (self.sh_fft[1] // 2 + 1)
+            self.cell_s = torch.empty(3, H, W, **f)     # [sharpened W, B, S]
+            self.sh_xhat = torch.empty(1, fs, **c)
+            self.sh_ghat = torch.empty(1, fs, **c)
+            self.sh_k = torch.from_numpy(self.sharpen).to(dev).reshape(1, 1, *self.sharpen.shape)
+            call("nc_filter_spectrum_fwd", stream_ptr(), 1, *self.sharpen.shape, *self.sh_fft,
+                 ptr(self.sh_k), ptr(self.sh_ghat))
+            if self.training:
+                self.g_cell_s = torch.empty(3, H, W, **f)
+                self.sh_dg = torch.empty(1, fs, **c)
+                n_ws = _abi_size("nc_fftconv_bwd_workspace_size", 1, 1, *self.sh_fft)
+                self.sh_ws = torch.empty(max(1, n_ws // 4), **f)
         self.border_hat = torch.empty(1, F, **c)  # shifted border-patch spectrum
         t0_shape = (B, self.H, self.W) if self.t0_grid else (B, h, w)
         self.x0 = torch.empty(*t0_shape, **f)
@@ -328,6 +352,13 @@ class StepPlan:
         if tuple(x_flat.shape) != (B, self.n_in):
             raise NeurocellError(f"inputs must be ({B}, {self.n_in}), got {tuple(x_flat.shape)}")
         mode = _abi.CODD_IDS[codd_mode]
+        if self.sharpen is not None:  # the Codd fusion sees the sharpened weights
+            ks = self.sharpen.shape
+            self.cell_s[1:].copy_(cell[1:])
+            call("nc_fftconv_fwd", s, 1, 1, self.H, self.W, self.H, self.W, (ks[0] - 1) // 2,
+                 (ks[1] - 1) // 2, *self.sh_fft, ptr(cell[0]), ptr(self.sh_ghat),
+                 ptr(self.cell_s[0]), ptr(self.sh_xhat))
+            cell = self.cell_s
         call("nc_codd_fuse_fwd", s, self.chip, ptr(cell), ptr(self.io_mask), ptr(self.owm), mode,
              inv_tau, active_threshold, int(self.hard_pin_io), self.act, self.slope, self.P,
              ptr(self.port_rc), ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
@@ -484,11 +515,20 @@ class StepPlan:
             call("nc_filter_gate_bwd", s, self.filt_g.numel(), ptr(self.filt_g), ptr(g_filt))
         has_epi = d > 1
         mode = _abi.CODD_IDS[codd_mode]
-        call("nc_codd_fuse_bwd", s, self.chip, ptr(cell), ptr(self.io_mask), ptr(self.owm), mode,
-             inv_tau, active_threshold, int(self.hard_pin_io), self.act, self.slope, self.P,
-             ptr(self.port_rc), ptr(self.gw) if has_epi else None,
-             ptr(self.gs) if has_epi else None, ptr(self.gb) if has_epi else None, g_patch,
-             ptr(self.gpp), ptr(g_cell))
+        sharp = self.sharpen is not None
+        call("nc_codd_fuse_bwd", s, self.chip, ptr(self.cell_s if sharp else cell),
+             ptr(self.io_mask), ptr(self.owm), mode, inv_tau, active_threshold,
+             int(self.hard_pin_io), self.act, self.slope, self.P, ptr(self.port_rc),
+             ptr(self.gw) if has_epi else None, ptr(self.gs) if has_epi else None,
+             ptr(self.gb) if has_epi else None, g_patch, ptr(self.gpp),
+             ptr(self.g_cell_s if sharp else g_cell))
+        if sharp:  # the sharpening's adjoint on the weights' gradient
+            ks = self.sharpen.shape
+            g_cell[1:].copy_(self.g_cell_s[1:])
+            call("nc_fftconv_bwd", s, 1, 1, self.H, self.W, self.H, self.W, (ks[0] - 1) // 2,
+                 (ks[1] - 1) // 2, *self.sh_fft, ptr(self.g_cell_s[0]), ptr(self.sh_xhat),
+                 ptr(self.sh_ghat), 1, ptr(g_cell[0]), ptr(self.sh_dg), 0, 0, ptr(self.sh_ws),
+                 self.sh_ws.numel() * 4)
 
     # ------------------------------------------------------------------ loss
     def mse(self, target: torch.Tensor, loss: torch.Tensor | None = None) -> torch.Tensor:

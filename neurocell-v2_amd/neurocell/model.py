@@ -18,6 +18,13 @@ from .propagator import propagate_vnn_2d
 from .topology import ChipTopology2D
 
 
+def sharpen_kernel(norm: bool = True) -> np.ndarray:
+    """filters.py:56-68: the 3x3 sharpening stencil (centre 5, edge neighbours -1), divided
+    by 5 when ``norm``."""
+    k = np.array([[0, -1, 0], [-1, 5, -1], [0, -1, 0]], np.float32)
+    return k / np.float32(5.0) if norm else k
+
+
 class VonNeumannNetwork:
     """model.py:29-159.  ``apply(params, inputs)`` returns the output-port predictions
     (B, out_h, out_w); only the port cells of the last step are evaluated."""
@@ -39,9 +46,8 @@ class VonNeumannNetwork:
         self.codd_mode = codd_mode
         self.state_temperature = state_temperature
         self.active_threshold = active_threshold
-        # the sharpening pre-filter (filters.sharpen) is not part of the MI355X path;
-        # propagate_vnn_2d rejects it explicitly
-        self.sharpen_filter = "sharpen" if sharpen else None
+        # the weight-sharpening pre-filter (model.py:65-67): filters.sharpen, normalised
+        self.sharpen_filter = sharpen_kernel(norm=True) if sharpen else None
 
     def init(self, rng, clear_outside_io: bool = False, legacy_compat: bool = True,
              device=None) -> VNNParams:

@@ -9,6 +9,7 @@ the reference's custom VJPs), giving gradients w.r.t. ``params.cell_params`` and
 """
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from ._lib import NeurocellError
@@ -40,16 +41,18 @@ class _PlanCache:
         self.plans = {}
 
     def get(self, topology, B, port_shapes, roi_bbox, activate, final_activate, hard_pin_io,
-            training, device, gated_filters=False):
+            training, device, gated_filters=False, sharpen=None):
+        sk = None if sharpen is None else np.asarray(sharpen, np.float32)
         key = (id(topology), topology, B, tuple(port_shapes), roi_bbox, str(activate),
                str(final_activate), bool(hard_pin_io), bool(training), str(device),
-               bool(gated_filters))
+               bool(gated_filters), None if sk is None else (sk.shape, sk.tobytes()))
         p = self.plans.get(key)
         if p is None:
             p = self.plans[key] = StepPlan(topology, B, port_shapes, roi_bbox=roi_bbox,
                                            activate=activate, final_activate=final_activate,
                                            hard_pin_io=hard_pin_io, training=training,
-                                           device=device, gated_filters=gated_filters)
+                                           device=device, gated_filters=gated_filters,
+                                           sharpen=sk)
         return p
 
 
@@ -81,6 +84,15 @@ class _Propagate(torch.autograd.Function):
         return g_cell, g_filt, None, None, None, None
 
 
+def _host_kernel(k):
+    """A sharpening stencil (array-like or tensor) as a float32 host array, or None."""
+    if k is None:
+        return None
+    if isinstance(k, torch.Tensor):
+        k = k.detach().cpu().numpy()
+    return np.asarray(k, np.float32)
+
+
 def propagate_vnn_2d(params, inputs, topology: ChipTopology2D, activate="tanh",
                      final_activate=None, norm: bool = True, sharpen_filter=None,
                      gated_filters: bool = False, hard_pin_io: bool = False,
@@ -97,8 +109,6 @@ def propagate_vnn_2d(params, inputs, topology: ChipTopology2D, activate="tanh",
                          f"{SUPPORTED_CODD_MODES}.")
     if not norm:
         raise NeurocellError("norm=False is not part of the MI355X path")
-    if sharpen_filter is not None:
-        raise NeurocellError("sharpen_filter is not part of the MI355X path")
     if return_universe:
         raise NeurocellError("return_universe=True is not supported yet on the MI355X path")
     roi_bbox = None
@@ -109,7 +119,7 @@ def propagate_vnn_2d(params, inputs, topology: ChipTopology2D, activate="tanh",
     need_grad = torch.is_grad_enabled() and (cell.requires_grad or filt.requires_grad)
     plan = _PLANS.get(topology, x_flat.shape[0], port_input_shapes(inputs, topology), roi_bbox,
                       activate, final_activate, hard_pin_io, need_grad, cell.device,
-                      gated_filters)
+                      gated_filters, _host_kernel(sharpen_filter))
     codd = (codd_mode, inv_tau_f32(float(state_temperature)), float(active_threshold))
     out = _Propagate.apply(cell, filt, x_flat, plan, codd, need_grad)
     oh, ow = topology.out_port.size

@@ -345,13 +345,14 @@ class VNNTrainer:
                                             activate=m.activate,
                                             final_activate=m.final_activate,
                                             hard_pin_io=m.hard_pin_io, training=training,
-                                            device=device, gated_filters=m.gated_filters)
+                                            device=device, gated_filters=m.gated_filters,
+                                            sharpen=m.sharpen_filter)
         return p
 
     def _check_model(self):
         m = self.model
-        if not m.norm or m.sharpen:
-            raise NeurocellError("norm=False / sharpen are not part of the MI355X path")
+        if not m.norm:
+            raise NeurocellError("norm=False is not part of the MI355X path")
 
     def _fused_train(self, params, opt_state, xb, yb, bbox, codd, nb):
         """nb optimiser steps over (nb, B, ...) batches; returns per-step losses (nb,)."""

@@ -448,3 +448,31 @@ def test_gated_filters_autograd():
     assert rel_l2(host(out), r_out) < FWD_TOL
     assert rel_l2(host(p.cell_params.grad), r_gc) < GRAD_TOL
     assert rel_l2(host(p.greens_filters.grad), r_gf * sg * (1.0 - sg)) < GRAD_TOL
+
+
+def test_sharpen_autograd():
+    """The weight-sharpening pre-filter (model.py:65-67, params.py:246-247) through the model
+    API: the oracle runs on the weights sharpened by scipy's SAME correlation with the
+    stencil, and the weights' gradient comes back through scipy's SAME convolution (the
+    correlation's adjoint for an odd stencil)."""
+    import scipy.signal
+    from neurocell import VNNParams, VonNeumannNetwork
+    from neurocell.model import sharpen_kernel
+    from neurocell.topology import ChipTopology2D
+    geom, cell, filt, x, _ = alu_case(14, B=8)
+    topo = ChipTopology2D.alu_chip(out_width=2)
+    model = VonNeumannNetwork(topo, sharpen=True)
+    p = VNNParams(dev(cell).requires_grad_(), dev(filt).requires_grad_())
+    out = model.apply(p, dev(x))
+    g = np.random.default_rng(15).normal(size=tuple(out.shape)).astype(np.float32)
+    out.backward(dev(g))
+    k = sharpen_kernel().astype(np.float64)
+    cell_s = cell.astype(np.float64).copy()
+    cell_s[0] = scipy.signal.correlate2d(cell_s[0], k, mode="same")
+    r_out, r_gc, r_gf = O.propagate_vjp(cell_s, filt, x, geom, g)
+    g_w = scipy.signal.convolve2d(r_gc[0], k, mode="same")
+    gc = host(p.cell_params.grad)
+    assert rel_l2(host(out), r_out) < FWD_TOL
+    assert rel_l2(gc[0], g_w) < GRAD_TOL
+    assert rel_l2(gc[1:], r_gc[1:]) < GRAD_TOL
+    assert rel_l2(host(p.greens_filters.grad), r_gf) < GRAD_TOL
