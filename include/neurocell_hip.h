@@ -89,14 +89,47 @@ int nc_codd_fuse_fwd(void* stream, const nc_chip_desc* chip, const float* cell,
 
 /*
  * Reverse of nc_codd_fuse_fwd (the autodiff of params.py:220-322 and of the STE forms of
- * params.py:58-80).  Any gradient input may be NULL (zero).  Writes g_cell (3,H,W).
+ * params.py:58-80).  Any gradient input may be NULL (zero).  g_s_prob and g_b_full (H,W) are
+ * full-grid gradients with respect to s_prob (the reverse of the optional s_prob output) and
+ * to the cell biases B themselves (the final universe's border term).  Writes g_cell (3,H,W).
  */
 int nc_codd_fuse_bwd(void* stream, const nc_chip_desc* chip, const float* cell,
                      const uint8_t* io_mask, const uint8_t* out_weight_mask, int codd_mode,
                      float inv_tau, float active_threshold, int hard_pin_io, int act,
                      float neg_slope, int n_port, const int32_t* port_rc, const float* g_w_eff,
                      const float* g_s_eff, const float* g_b_roi, const float* g_border_patch,
-                     const float* g_port_params, float* g_cell);
+                     const float* g_port_params, const float* g_s_prob,
+                     const float* g_b_full, float* g_cell);
+
+/*
+ * The final universe and the full-grid output port (propagator.py:684-734, with
+ * _extract_output_from_full_grid :194-206): the path taken for return_universe=True and for
+ * an output port outside the VALID ROI (topology.py allow_border_output / full-grid ports).
+ * parts (G,B,h,w) are the direction-group partials of the last step's ROI epilogue run with
+ * the final activation (nc_fftconv_epilogue_fwd with act = final_act); their sum is the
+ * sub-ROI's pre-activation.  Every other grid cell takes final_act(B) * s_prob when
+ * valid_border (VALID mode, b_full = cell[1] and s_prob from nc_codd_fuse_fwd), else 0.
+ * universe (B,H,W) = final_act(pre) over the grid (NULL to skip); out (B,P) = the universe
+ * at port_cells (P grid-flat cell indices, each in [0, H*W)).
+ */
+int nc_universe_fwd(void* stream, const nc_chip_desc* chip, int B, int G, int valid_border,
+                    int final_act, float neg_slope, const float* parts, const float* b_full,
+                    const float* s_prob, int n_port, const int32_t* port_cells, float* universe,
+                    float* out);
+
+/*
+ * Reverse of nc_universe_fwd.  The final cells' cotangent is g_universe (B,H,W; NULL = 0)
+ * plus g_out (B,P; NULL = 0) added at each port's cell: port_head (H*W) holds the first port
+ * at each cell or -1, port_next (P) the next port at the same cell or -1 (an acyclic chain in
+ * port order).  Writes g_roi (B,h,w), the cotangent of the ROI epilogue's output (feed it to
+ * nc_epilogue_bwd_parts with act = final_act); with valid_border also g_s_prob and g_b_full
+ * (H,W) for nc_codd_fuse_bwd (zero on the sub-ROI cells).
+ */
+int nc_universe_bwd(void* stream, const nc_chip_desc* chip, int B, int G, int valid_border,
+                    int final_act, float neg_slope, const float* parts, const float* b_full,
+                    const float* s_prob, int n_port, const int32_t* port_head,
+                    const int32_t* port_next, const float* g_out, const float* g_universe,
+                    float* g_roi, float* g_s_prob, float* g_b_full);
 
 /*
  * gated_filters (propagator.py:266-267): gated (n) = sigmoid(filters); the reverse turns the

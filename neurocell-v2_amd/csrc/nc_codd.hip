@@ -101,6 +101,7 @@ __global__ void k_codd_bwd(nc_chip_desc c, const float* __restrict__ cell,
                            int P, const int* __restrict__ prc, const float* __restrict__ g_weff,
                            const float* __restrict__ g_seff, const float* __restrict__ g_broi,
                            const float* __restrict__ g_patch, const float* __restrict__ g_pp,
+                           const float* __restrict__ g_sprob, const float* __restrict__ g_bfull,
                            float* __restrict__ g_cell) {
     const int HW = c.H * c.W;
     const int q = blockIdx.x * blockDim.x + threadIdx.x;
@@ -133,8 +134,9 @@ __global__ void k_codd_bwd(nc_chip_desc c, const float* __restrict__ cell,
     float a;
     const float da = nc_act_d(e.b, act, slope, &a);
     const float g_wp = inv_m * (1.0f - e.s_prob) * gw;
-    const float g_sp = -inv_m * e.w_pinned * gw + inv_m * gs + a * gbd;
-    const float g_b = gb + da * e.s_prob * gbd;
+    const float g_sp = -inv_m * e.w_pinned * gw + inv_m * gs + a * gbd +
+                       (g_sprob ? g_sprob[q] : 0.0f);
+    const float g_b = gb + da * e.s_prob * gbd + (g_bfull ? g_bfull[q] : 0.0f);
     g_cell[q] = owm[q] ? 0.0f : g_wp;
     g_cell[HW + q] = g_b;
     g_cell[2 * HW + q] = g_sp * e.ds;
@@ -386,6 +388,109 @@ __global__ void k_count_inc(int* count) {
     if (threadIdx.x == 0 && blockIdx.x == 0) count[0] = count[0] + 1;
 }
 
+// ----------------------------------------------------------------------------------------
+// The final universe (propagator.py:684-734): the last step's epilogue output on the active
+// sub-ROI, the VALID border value final_act(B) * s_prob (zero without a VALID border)
+// elsewhere, then the final activation over the whole grid; the output port is gathered
+// from it by grid cell, so a port may lie anywhere on the grid.
+// ----------------------------------------------------------------------------------------
+
+struct UniverseArgs {
+    nc_chip_desc c;
+    int B, G, valid, fact;
+    float slope;
+    const float* parts;  // (G, B, h, w) direction-group partials of the ROI epilogue output
+    const float* bfull;  // (H, W) cell biases
+    const float* sprob;  // (H, W) Codd probabilities
+};
+
+// The activation's argument at (b, grid cell q); *roi says whether q is a sub-ROI cell.
+NC_DEV float universe_pre(const UniverseArgs& a, int b, int q, bool* roi) {
+    const int r = q / a.c.W, col = q % a.c.W;
+    const int h = a.c.r1 - a.c.r0, w = a.c.c1 - a.c.c0;
+    const int ri = r - a.c.pad_h - a.c.r0, ci = col - a.c.pad_w - a.c.c0;
+    *roi = ri >= 0 && ri < h && ci >= 0 && ci < w;
+    if (*roi) {
+        const size_t plane = (size_t)a.B * h * w;
+        const float* p = a.parts + (size_t)b * h * w + ri * w + ci;
+        float v = 0.0f;
+        for (int g = 0; g < a.G; ++g) v += p[g * plane];
+        return v;
+    }
+    return a.valid ? nc_act(a.bfull[q], a.fact, a.slope) * a.sprob[q] : 0.0f;
+}
+
+// Threads [0, B*H*W) write the universe (when requested), threads past them the B*P port
+// outputs, each evaluated from the same operands.
+__global__ void k_universe_fwd(UniverseArgs a, int P, const int* __restrict__ cells,
+                               float* __restrict__ univ, float* __restrict__ out) {
+    const size_t HW = (size_t)a.c.H * a.c.W;
+    const size_t nu = univ ? (size_t)a.B * HW : 0;
+    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    bool roi;
+    if (q < nu) {
+        const int b = (int)(q / HW), cell = (int)(q % HW);
+        univ[q] = nc_act(universe_pre(a, b, cell, &roi), a.fact, a.slope);
+    } else if (q < nu + (size_t)a.B * P) {
+        const size_t k = q - nu;
+        const int b = (int)(k / P), p = (int)(k % P);
+        out[k] = nc_act(universe_pre(a, b, cells[p], &roi), a.fact, a.slope);
+    }
+}
+
+// Cotangent of the final cells at (b, q): the universe's own plus every port output read
+// from q (head/next chain the ports by cell, in port order).
+NC_DEV float universe_cot(int b, int q, size_t HW, int P, const int* head, const int* next,
+                          const float* g_out, const float* g_univ) {
+    float g = g_univ ? g_univ[(size_t)b * HW + q] : 0.0f;
+    if (g_out)
+        for (int p = head[q]; p >= 0; p = next[p]) g += g_out[(size_t)b * P + p];
+    return g;
+}
+
+// Sub-ROI cells: g_roi (B, h, w) = cotangent * final_act'(pre).
+__global__ void k_universe_bwd_roi(UniverseArgs a, int P, const int* __restrict__ head,
+                                   const int* __restrict__ next, const float* __restrict__ g_out,
+                                   const float* __restrict__ g_univ, float* __restrict__ g_roi) {
+    const int h = a.c.r1 - a.c.r0, w = a.c.c1 - a.c.c0;
+    const size_t n = (size_t)h * w;
+    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= (size_t)a.B * n) return;
+    const int b = (int)(q / n), i = (int)(q % n);
+    const int cell = (a.c.pad_h + a.c.r0 + i / w) * a.c.W + a.c.pad_w + a.c.c0 + i % w;
+    bool roi;
+    const float v = universe_pre(a, b, cell, &roi);
+    float y;
+    const float d = nc_act_d(v, a.fact, a.slope, &y);
+    g_roi[q] = universe_cot(b, cell, (size_t)a.c.H * a.c.W, P, head, next, g_out, g_univ) * d;
+}
+
+// Border cells (VALID): the batch-summed cotangent through final_act(final_act(B) * s_prob)
+// onto B and s_prob; zero on the sub-ROI cells.
+__global__ void k_universe_bwd_border(UniverseArgs a, int P, const int* __restrict__ head,
+                                      const int* __restrict__ next,
+                                      const float* __restrict__ g_out,
+                                      const float* __restrict__ g_univ,
+                                      float* __restrict__ g_sprob, float* __restrict__ g_bfull) {
+    const size_t HW = (size_t)a.c.H * a.c.W;
+    const int q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= (int)HW) return;
+    bool roi;
+    const float v = universe_pre(a, 0, q, &roi);
+    float gs = 0.0f, gb = 0.0f;
+    if (!roi) {
+        float gsum = 0.0f;
+        for (int b = 0; b < a.B; ++b) gsum += universe_cot(b, q, HW, P, head, next, g_out, g_univ);
+        float y, ab;
+        const float gv = gsum * nc_act_d(v, a.fact, a.slope, &y);
+        const float dab = nc_act_d(a.bfull[q], a.fact, a.slope, &ab);
+        gs = gv * ab;
+        gb = gv * a.sprob[q] * dab;
+    }
+    g_sprob[q] = gs;
+    g_bfull[q] = gb;
+}
+
 int chip_ok(const nc_chip_desc* c) {
     if (!c) return 0;
     if (c->H <= 0 || c->W <= 0 || c->kh <= 0 || c->kw <= 0 || c->M <= 0) return 0;
@@ -442,7 +547,8 @@ int nc_codd_fuse_bwd(void* stream, const nc_chip_desc* chip, const float* cell,
                      float inv_tau, float active_threshold, int hard_pin_io, int act,
                      float neg_slope, int n_port, const int32_t* port_rc, const float* g_w_eff,
                      const float* g_s_eff, const float* g_b_roi, const float* g_border_patch,
-                     const float* g_port_params, float* g_cell) {
+                     const float* g_port_params, const float* g_s_prob, const float* g_b_full,
+                     float* g_cell) {
     if (!chip_ok(chip) || !cell || !io_mask || !out_weight_mask || codd_mode < 0 ||
         codd_mode > 3 || act < 0 || act > 5 || n_port < 0 || (n_port > 0 && !port_rc) ||
         !g_cell)
@@ -451,7 +557,8 @@ int nc_codd_fuse_bwd(void* stream, const nc_chip_desc* chip, const float* cell,
     hipLaunchKernelGGL(k_codd_bwd, dim3((n + 255) / 256), dim3(256), 0, nc_stream(stream), *chip,
                        cell, io_mask, out_weight_mask, codd_mode, inv_tau, active_threshold,
                        hard_pin_io, act, neg_slope, n_port, port_rc, g_w_eff, g_s_eff, g_b_roi,
-                       g_border_patch, n_port > 0 ? g_port_params : nullptr, g_cell);
+                       g_border_patch, n_port > 0 ? g_port_params : nullptr, g_s_prob,
+                       g_b_full, g_cell);
     NC_CHECK_LAUNCH();
     return NC_OK;
 }
@@ -529,6 +636,49 @@ int nc_filter_gate_bwd(void* stream, int n, const float* gated, float* g_filters
     hipLaunchKernelGGL(k_gate_bwd, dim3((n + 255) / 256), dim3(256), 0, nc_stream(stream), n,
                        gated, g_filters);
     NC_CHECK_LAUNCH();
+    return NC_OK;
+}
+
+int nc_universe_fwd(void* stream, const nc_chip_desc* chip, int B, int G, int valid_border,
+                    int final_act, float neg_slope, const float* parts, const float* b_full,
+                    const float* s_prob, int n_port, const int32_t* port_cells, float* universe,
+                    float* out) {
+    if (!chip_ok(chip) || B <= 0 || G <= 0 || final_act < 0 || final_act > 5 || !parts ||
+        n_port < 0 || (n_port > 0 && (!port_cells || !out)) || (!universe && n_port == 0) ||
+        (valid_border && (!b_full || !s_prob)))
+        return NC_ERR_INVALID_ARGUMENT;
+    const UniverseArgs a{*chip, B, G, valid_border != 0, final_act, neg_slope, parts, b_full,
+                         s_prob};
+    const size_t n = (universe ? (size_t)B * chip->H * chip->W : 0) + (size_t)B * n_port;
+    hipLaunchKernelGGL(k_universe_fwd, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       nc_stream(stream), a, n_port, port_cells, universe, out);
+    NC_CHECK_LAUNCH();
+    return NC_OK;
+}
+
+int nc_universe_bwd(void* stream, const nc_chip_desc* chip, int B, int G, int valid_border,
+                    int final_act, float neg_slope, const float* parts, const float* b_full,
+                    const float* s_prob, int n_port, const int32_t* port_head,
+                    const int32_t* port_next, const float* g_out, const float* g_universe,
+                    float* g_roi, float* g_s_prob, float* g_b_full) {
+    if (!chip_ok(chip) || B <= 0 || G <= 0 || final_act < 0 || final_act > 5 || !parts ||
+        n_port < 0 || (n_port > 0 && g_out && (!port_head || !port_next)) || !g_roi ||
+        (valid_border && (!b_full || !s_prob || !g_s_prob || !g_b_full)))
+        return NC_ERR_INVALID_ARGUMENT;
+    const UniverseArgs a{*chip, B, G, valid_border != 0, final_act, neg_slope, parts, b_full,
+                         s_prob};
+    const int P = g_out ? n_port : 0;
+    const size_t n = (size_t)B * (chip->r1 - chip->r0) * (chip->c1 - chip->c0);
+    hipLaunchKernelGGL(k_universe_bwd_roi, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       nc_stream(stream), a, P, port_head, port_next, g_out, g_universe, g_roi);
+    NC_CHECK_LAUNCH();
+    if (valid_border) {
+        const int hw = chip->H * chip->W;
+        hipLaunchKernelGGL(k_universe_bwd_border, dim3((hw + 255) / 256), dim3(256), 0,
+                           nc_stream(stream), a, P, port_head, port_next, g_out, g_universe,
+                           g_s_prob, g_b_full);
+        NC_CHECK_LAUNCH();
+    }
     return NC_OK;
 }
 

@@ -64,7 +64,10 @@ _SIGS = {
     "nc_codd_fuse_fwd": (I, [P, C.POINTER(ChipDesc), P, P, P, I, F, F, I, I, F, I, P, P, P, P,
                              P, P, P, P, P]),
     "nc_codd_fuse_bwd": (I, [P, C.POINTER(ChipDesc), P, P, P, I, F, F, I, I, F, I, P, P, P, P,
-                             P, P, P]),
+                             P, P, P, P, P]),
+    "nc_universe_fwd": (I, [P, C.POINTER(ChipDesc), I, I, I, I, F, P, P, P, I, P, P, P]),
+    "nc_universe_bwd": (I, [P, C.POINTER(ChipDesc), I, I, I, I, F, P, P, P, I, P, P, P, P, P, P,
+                            P]),
     "nc_filter_spectrum_fwd": (I, [P, I, I, I, I, I, P, P]),
     "nc_filter_spectrum_bwd": (I, [P, I, I, I, I, I, I, I, P, P, I, I]),
     "nc_fftconv_fwd": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, P]),

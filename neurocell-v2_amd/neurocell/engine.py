@@ -117,9 +117,8 @@ class StepPlan:
 
     def __init__(self, topology: ChipTopology2D, batch_size: int, port_shapes: list,
                  roi_bbox=None, activate="tanh", final_activate=None, hard_pin_io=False,
-                 training=True, device=None, gated_filters=False, sharpen=None):
-        if not topology.out_in_roi:
-            raise NeurocellError("output port outside the active ROI is not supported")
+                 training=True, device=None, gated_filters=False, sharpen=None,
+                 universe=False):
         self.device = device or require_device()
         self.topo = topology
         self.B = int(batch_size)
@@ -129,6 +128,11 @@ class StepPlan:
         self.gated = bool(gated_filters)
         # weight sharpening (params.py:246-247): the Codd fusion sees corr_SAME(W, kernel)
         self.sharpen = None if sharpen is None else np.ascontiguousarray(sharpen, np.float32)
+        # the full-grid output path (propagator.py:684-734): return_universe, or an output
+        # port outside the ROI (allow_border_output, full-grid ports), reads the port from the
+        # final universe
+        self.universe = bool(universe) or not topology.out_in_roi
+        self.want_universe = bool(universe)
         self.act, self.slope = act_id(activate)
         self.fact, self.fslope = act_id(final_activate)
         H, W = topology.grid_shape
@@ -181,19 +185,37 @@ class StepPlan:
                                   r0, r1, c0, c1)
         # output port cells
         rows, cols = topology.out_cells_roi()
-        if ((rows < r0) | (rows >= r1) | (cols < c0) | (cols >= c1)).any():
-            raise NeurocellError("output port lies outside the active sub-ROI")
         self.P = int(rows.size)
         self.out_size = tuple(topology.out_port.size)
         dev = self.device
+        if self.universe:
+            gr, gc = topology.out_cells_grid()
+            if ((gr < 0) | (gr >= H) | (gc < 0) | (gc >= W)).any():
+                raise NeurocellError("output port lies outside the grid")
+            cells = (gr * W + gc).astype(np.int32)
+            # port cells by grid cell for the reverse: first port at each cell, next port at
+            # the same cell, in port order
+            head = np.full(H * W, -1, np.int32)
+            nxt = np.full(self.P, -1, np.int32)
+            for k in range(self.P - 1, -1, -1):
+                nxt[k] = head[cells[k]]
+                head[cells[k]] = k
+            self.port_cells = torch.tensor(cells, device=dev)
+            self.port_head = torch.tensor(head, device=dev)
+            self.port_next = torch.tensor(nxt, device=dev)
+            rows = cols = np.zeros(0, np.int32)  # no port parameters on this path
+        elif ((rows < r0) | (rows >= r1) | (cols < c0) | (cols >= c1)).any():
+            raise NeurocellError("output port lies outside the active sub-ROI")
+        self.n_pp = int(rows.size)  # cells with port parameters (the port path's)
         self.port_rc = torch.tensor(np.stack([rows, cols]).astype(np.int32), device=dev)
         flat = ((rows - r0) * w + (cols - c0)).astype(np.int32)
         self.port_idx = torch.tensor(flat, device=dev)
         # a port that is the whole (sub-)ROI in row-major order (the Game-of-Life universe
         # port): its epilogue is the hidden one with the port parameters and the final
         # activation, so it runs on the epilogue kernels at any size
-        self.dense_port = self.P == self.N and np.array_equal(flat, np.arange(self.N))
-        if not self.dense_port and (self.P > 256 or M * self.P > 8192):
+        self.dense_port = (not self.universe and self.P == self.N
+                           and np.array_equal(flat, np.arange(self.N)))
+        if not self.dense_port and not self.universe and (self.P > 256 or M * self.P > 8192):
             raise NeurocellError(f"an output port of {self.P} cells must cover the whole ROI "
                                  "in row-major order (the port kernels gather at most 256 "
                                  "cells, 8192 per sample over the directions)")
@@ -263,7 +285,7 @@ class StepPlan:
         self.s_eff = torch.empty(h, w, **f)
         self.b_roi = torch.empty(h, w, **f)
         self.patch = torch.empty(self.Hp, self.Wp, **f)
-        self.pp = torch.empty(3, self.P, **f)
+        self.pp = torch.empty(3, self.n_pp, **f)
         self.ghat = torch.empty(M, F, **c)
         self.filt_g = torch.empty(M, 1, self.kh, self.kw, **f) if self.gated else None
         if self.sharpen is not None:
@@ -294,12 +316,17 @@ class StepPlan:
         self.mean = [torch.empty(B, M, **f) for _ in range(d)]
         self.rstd = [torch.empty(B, M, **f) for _ in range(d)]
         self.out = torch.empty(B, self.P, **f)
-        self.zo = None if self.dense_port else torch.empty(B, M, self.P, **f)
-        if self.dense_port:  # the port's direction-group partial outputs
+        port_path = not (self.dense_port or self.universe)
+        self.zo = torch.empty(B, M, self.P, **f) if port_path else None
+        if not port_path:  # the last epilogue's direction-group partial outputs
             self.port_parts = torch.empty(self.G, B, h, w, **f)
-        self.pre = torch.empty(B, self.P, **f) if self.fact != 0 else None
+        self.pre = torch.empty(B, self.P, **f) if self.fact != 0 and not self.universe else None
+        if self.universe:
+            self.s_prob = torch.empty(self.H, self.W, **f)
+            self.univ = torch.empty(B, self.H, self.W, **f) if self.want_universe else None
         n_ep = max(_abi_size("nc_epilogue_workspace_size", B, M, h, w),
-                   _abi_size("nc_fftconv_port_workspace_size", B, M, h, w, *self.fft, self.P))
+                   _abi_size("nc_fftconv_port_workspace_size", B, M, h, w, *self.fft, self.P)
+                   if port_path else 0)
         self.ws_epi = torch.empty(max(1, n_ep // 4), **f)
         if self.training:
             n_fc = max(_abi_size("nc_fftconv_bwd_workspace_size", B, M, *self.fft),
@@ -322,15 +349,20 @@ class StepPlan:
             # parameter-gradient partial rows, summed in the same launch: R rows per hidden
             # epilogue step for each of gw / gs / gb, B rows per port parameter
             self.R = _abi_int("nc_epilogue_bwd_partials", B, M, h, w)
-            L = max(1, d - 1)
-            self.pg_rows = torch.empty(3, L * self.R, h * w, **f)
+            # (the universe path's last epilogue takes a block of its own)
+            self.n_epi = d - 1 + int(self.universe)
+            self.pg_rows = torch.empty(3, max(1, self.n_epi) * self.R, h * w, **f)
             # port-parameter partial rows: B per parameter, or the epilogue's R for a dense port
-            self.pp_rows = torch.empty(3, self.R if self.dense_port else B, self.P, **f)
+            self.pp_rows = torch.empty(3, self.R if self.dense_port else B, self.n_pp, **f)
+            if self.universe:
+                self.g_roi = torch.empty(B, h, w, **f)
+                self.g_sprob = torch.empty(self.H, self.W, **f)
+                self.g_bfull = torch.empty(self.H, self.W, **f)
             self.g_pre = torch.empty(B, self.P, **f) if self.dense_port else None
             self.gw = torch.empty(h, w, **f)
             self.gs = torch.empty(h, w, **f)
             self.gb = torch.empty(h, w, **f)
-            self.gpp = torch.empty(3, self.P, **f)
+            self.gpp = torch.empty(3, self.n_pp, **f)
             self.gpatch = torch.empty(self.Hp, self.Wp, **f)
             self.g_out = torch.empty(B, self.P, **f)
             self.loss = torch.empty(1, **f)
@@ -360,9 +392,10 @@ class StepPlan:
                  ptr(self.cell_s[0]), ptr(self.sh_xhat))
             cell = self.cell_s
         call("nc_codd_fuse_fwd", s, self.chip, ptr(cell), ptr(self.io_mask), ptr(self.owm), mode,
-             inv_tau, active_threshold, int(self.hard_pin_io), self.act, self.slope, self.P,
+             inv_tau, active_threshold, int(self.hard_pin_io), self.act, self.slope, self.n_pp,
              ptr(self.port_rc), ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
-             ptr(self.patch), ptr(self.pp), None, None, None)
+             ptr(self.patch), ptr(self.pp), ptr(self.s_prob) if self.universe else None, None,
+             None)
         n_cells = self.x0[0].numel()
         call("nc_inject_roi", s, B, self.n_in, ptr(x_flat), n_cells, ptr(self.src), ptr(self.x0))
         # the independent spectra in one call: filter spectra (kernels_greens.py:240-259), the
@@ -407,6 +440,18 @@ class StepPlan:
                      ptr(self.ghat), self.act, self.slope, ptr(self.w_eff), ptr(self.s_eff),
                      ptr(self.b_roi), ptr(zk), ptr(self.xs[t + 1]), ptr(self.mean[t]),
                      ptr(self.rstd[t]), ptr(self.ws_epi), self.ws_epi.numel() * 4)
+            elif self.universe:
+                # the last epilogue with the final activation on the ROI parameters, then the
+                # universe and the port read from it (propagator.py:684-734)
+                zk = None if fused and not self.training else z
+                call("nc_fftconv_epilogue_fwd", s, B, M, h, w, p0[0], p0[1], fh, fw, ptr(xh),
+                     ptr(self.ghat), self.fact, self.fslope, ptr(self.w_eff), ptr(self.s_eff),
+                     ptr(self.b_roi), ptr(zk), ptr(self.port_parts), ptr(self.mean[t]),
+                     ptr(self.rstd[t]), ptr(self.ws_epi), self.ws_epi.numel() * 4)
+                call("nc_universe_fwd", s, self.chip, B, self.G, int(self.mode == "VALID"),
+                     self.fact, self.fslope, ptr(self.port_parts), _addr(cell) + 4 * self.H *
+                     self.W, ptr(self.s_prob), self.P, ptr(self.port_cells), ptr(self.univ),
+                     ptr(self.out))
             elif self.dense_port:
                 zk = None if fused and not self.training else z
                 call("nc_fftconv_epilogue_fwd", s, B, M, h, w, p0[0], p0[1], fh, fw, ptr(xh),
@@ -426,10 +471,13 @@ class StepPlan:
         return self.out
 
     # ------------------------------------------------------------------ reverse
-    def backward(self, cell: torch.Tensor, filt: torch.Tensor, g_out: torch.Tensor,
+    def backward(self, cell: torch.Tensor, filt: torch.Tensor, g_out: torch.Tensor | None,
                  g_cell: torch.Tensor, g_filt: torch.Tensor, codd_mode: str = "continuous",
-                 inv_tau: float = 1.0, active_threshold: float = 0.6) -> None:
-        """Reverse pass of the last ``forward``: writes g_cell (3,H,W) and g_filt (M,1,kh,kw)."""
+                 inv_tau: float = 1.0, active_threshold: float = 0.6,
+                 g_universe: torch.Tensor | None = None) -> None:
+        """Reverse pass of the last ``forward``: writes g_cell (3,H,W) and g_filt (M,1,kh,kw).
+        On the universe path ``g_universe`` (B,H,W) may add a cotangent on the final
+        universe, and either cotangent may be None (zero)."""
         if not self.training:
             raise NeurocellError("plan was built for evaluation only")
         s = stream_ptr()
@@ -439,7 +487,18 @@ class StepPlan:
         ws_fc, n_fc = ptr(self.ws_fc), self.ws_fc.numel() * 4
         t = d - 1
         N, RN = h * w, self.R * h * w
-        if self.dense_port:
+        valid = int(self.mode == "VALID")
+        if self.universe:
+            b_full = _addr(self.cell_s if self.sharpen is not None else cell) + 4 * self.H * self.W
+            call("nc_universe_bwd", s, self.chip, B, self.G, valid, self.fact, self.fslope,
+                 ptr(self.port_parts), b_full, ptr(self.s_prob), self.P, ptr(self.port_head),
+                 ptr(self.port_next), ptr(g_out), ptr(g_universe), ptr(self.g_roi),
+                 ptr(self.g_sprob) if valid else None, ptr(self.g_bfull) if valid else None)
+            call("nc_epilogue_bwd_parts", s, B, M, h, w, self.fact, self.fslope, 0,
+                 ptr(self.zs[t]), None, ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
+                 ptr(self.mean[t]), ptr(self.rstd[t]), ptr(self.g_roi), ptr(self.gz),
+                 _addr(self.pg_rows) + 4 * (d - 1) * RN, self.pg_rows[0].numel(), ws_ep, n_ep)
+        elif self.dense_port:
             gy_port = g_out
             if self.fact != 0:
                 call("nc_port_dense_bwd", s, B * self.P, self.fact, self.fslope, ptr(self.pre),
@@ -489,12 +548,14 @@ class StepPlan:
             outs = {"dg": self.dghat, "dgv": self.dghat_v, "gd": self.gdelta_hat}
             jobs += [(_addr(self.rows[k]), _addr(outs[k]), 2 * M * self.F, 0, self.npart)
                      for k in keys]
-        if d > 1:
-            jobs += [(_addr(self.pg_rows[i]), _addr(g), N, 0, (d - 1) * self.R)
+        if self.n_epi > 0:
+            jobs += [(_addr(self.pg_rows[i]), _addr(g), N, 0, self.n_epi * self.R)
                      for i, g in enumerate((self.gw, self.gs, self.gb))]
-        jobs += [(_addr(self.pp_rows[i]), _addr(self.gpp[i]), self.P, 0, self.pp_rows.shape[1])
-                 for i in range(3)]
-        call("nc_rows_sum", s, len(jobs), _abi.rows_jobs(*jobs))
+        if self.n_pp > 0:
+            jobs += [(_addr(self.pp_rows[i]), _addr(self.gpp[i]), self.n_pp, 0,
+                      self.pp_rows.shape[1]) for i in range(3)]
+        if jobs:
+            call("nc_rows_sum", s, len(jobs), _abi.rows_jobs(*jobs))
         g_patch = None
         if self.border:
             # the filter gradients and the border conv's reverse in one launch: the patch
@@ -513,14 +574,16 @@ class StepPlan:
                  self.kw - 1, ptr(self.dghat_v), ptr(g_filt), int(not only_t0_grid), 0)
         if self.gated:  # the chain rule through the gate, in place
             call("nc_filter_gate_bwd", s, self.filt_g.numel(), ptr(self.filt_g), ptr(g_filt))
-        has_epi = d > 1
+        has_epi = self.n_epi > 0
         mode = _abi.CODD_IDS[codd_mode]
         sharp = self.sharpen is not None
         call("nc_codd_fuse_bwd", s, self.chip, ptr(self.cell_s if sharp else cell),
              ptr(self.io_mask), ptr(self.owm), mode, inv_tau, active_threshold,
-             int(self.hard_pin_io), self.act, self.slope, self.P, ptr(self.port_rc),
+             int(self.hard_pin_io), self.act, self.slope, self.n_pp, ptr(self.port_rc),
              ptr(self.gw) if has_epi else None, ptr(self.gs) if has_epi else None,
-             ptr(self.gb) if has_epi else None, g_patch, ptr(self.gpp),
+             ptr(self.gb) if has_epi else None, g_patch, ptr(self.gpp) if self.n_pp else None,
+             ptr(self.g_sprob) if self.universe and valid else None,
+             ptr(self.g_bfull) if self.universe and valid else None,
              ptr(self.g_cell_s if sharp else g_cell))
         if sharp:  # the sharpening's adjoint on the weights' gradient
             ks = self.sharpen.shape

@@ -41,18 +41,19 @@ class _PlanCache:
         self.plans = {}
 
     def get(self, topology, B, port_shapes, roi_bbox, activate, final_activate, hard_pin_io,
-            training, device, gated_filters=False, sharpen=None):
+            training, device, gated_filters=False, sharpen=None, universe=False):
         sk = None if sharpen is None else np.asarray(sharpen, np.float32)
         key = (id(topology), topology, B, tuple(port_shapes), roi_bbox, str(activate),
                str(final_activate), bool(hard_pin_io), bool(training), str(device),
-               bool(gated_filters), None if sk is None else (sk.shape, sk.tobytes()))
+               bool(gated_filters), None if sk is None else (sk.shape, sk.tobytes()),
+               bool(universe))
         p = self.plans.get(key)
         if p is None:
             p = self.plans[key] = StepPlan(topology, B, port_shapes, roi_bbox=roi_bbox,
                                            activate=activate, final_activate=final_activate,
                                            hard_pin_io=hard_pin_io, training=training,
                                            device=device, gated_filters=gated_filters,
-                                           sharpen=sk)
+                                           sharpen=sk, universe=universe)
         return p
 
 
@@ -60,8 +61,11 @@ _PLANS = _PlanCache()
 
 
 class _Propagate(torch.autograd.Function):
+    """The d-step forward as one node: outputs the port predictions, and the final universe
+    too when the plan was built with ``return_universe``."""
+
     @staticmethod
-    def forward(ctx, cell, filt, x_flat, plan, codd, need_grad):
+    def forward(ctx, cell, filt, x_flat, plan, codd, need_grad, return_universe):
         mode, it, thr = codd
         cell, filt = cell.contiguous(), filt.contiguous()
         # each call owns its activations so several graphs can be alive at once
@@ -70,18 +74,25 @@ class _Propagate(torch.autograd.Function):
                           active_threshold=thr).clone()
         ctx.run, ctx.codd = run, codd
         ctx.save_for_backward(cell, filt)
+        ctx.set_materialize_grads(False)
+        if return_universe:
+            return out, run.univ.clone()
         return out
 
     @staticmethod
-    def backward(ctx, g_out):
+    def backward(ctx, g_out, g_univ=None):
         cell, filt = ctx.saved_tensors
         mode, it, thr = ctx.codd
+        run = ctx.run
         g_cell = torch.empty_like(cell)
         g_filt = torch.empty_like(filt)
-        ctx.run.backward(cell, filt, g_out.contiguous(), g_cell, g_filt, codd_mode=mode,
-                         inv_tau=it, active_threshold=thr)
+        if g_out is None and not run.universe:
+            g_out = torch.zeros_like(run.out)
+        c = lambda t: None if t is None else t.contiguous()
+        run.backward(cell, filt, c(g_out), g_cell, g_filt, codd_mode=mode, inv_tau=it,
+                     active_threshold=thr, g_universe=c(g_univ))
         ctx.run = None
-        return g_cell, g_filt, None, None, None, None
+        return g_cell, g_filt, None, None, None, None, None
 
 
 def _host_kernel(k):
@@ -100,7 +111,9 @@ def propagate_vnn_2d(params, inputs, topology: ChipTopology2D, activate="tanh",
                      spatial_mask=None, codd_mode: str = "continuous",
                      state_temperature: float = 1.0, active_threshold: float = 0.6):
     """propagator.py:209-734: (B, out_h, out_w) port predictions, differentiable w.r.t. the
-    VNNParams leaves.  ``spatial_mask`` (an AdaptiveMaskSpec) runs on its cropped sub-ROI."""
+    VNNParams leaves.  ``spatial_mask`` (an AdaptiveMaskSpec) runs on its cropped sub-ROI.
+    With ``return_universe`` also the final (B, H, W) universe (propagator.py:684-734), also
+    differentiable; an output port outside the ROI is read from that universe as well."""
     if backend not in SUPPORTED_BACKENDS:
         raise ValueError(f"Unsupported backend '{backend}'; choose from {SUPPORTED_BACKENDS}.")
     from .params import SUPPORTED_CODD_MODES
@@ -109,8 +122,6 @@ def propagate_vnn_2d(params, inputs, topology: ChipTopology2D, activate="tanh",
                          f"{SUPPORTED_CODD_MODES}.")
     if not norm:
         raise NeurocellError("norm=False is not part of the MI355X path")
-    if return_universe:
-        raise NeurocellError("return_universe=True is not supported yet on the MI355X path")
     roi_bbox = None
     if spatial_mask is not None and not spatial_mask.is_full_roi:
         roi_bbox = tuple(int(v) for v in spatial_mask.roi_bbox)
@@ -119,11 +130,14 @@ def propagate_vnn_2d(params, inputs, topology: ChipTopology2D, activate="tanh",
     need_grad = torch.is_grad_enabled() and (cell.requires_grad or filt.requires_grad)
     plan = _PLANS.get(topology, x_flat.shape[0], port_input_shapes(inputs, topology), roi_bbox,
                       activate, final_activate, hard_pin_io, need_grad, cell.device,
-                      gated_filters, _host_kernel(sharpen_filter))
+                      gated_filters, _host_kernel(sharpen_filter), bool(return_universe))
     codd = (codd_mode, inv_tau_f32(float(state_temperature)), float(active_threshold))
-    out = _Propagate.apply(cell, filt, x_flat, plan, codd, need_grad)
+    res = _Propagate.apply(cell, filt, x_flat, plan, codd, need_grad, bool(return_universe))
     oh, ow = topology.out_port.size
-    return out.reshape(out.shape[0], oh, ow)
+    if return_universe:
+        out, univ = res
+        return out.reshape(out.shape[0], oh, ow), univ
+    return res.reshape(res.shape[0], oh, ow)
 
 
 def inject_inputs_roi_2d(inputs, topology: ChipTopology2D, dtype=torch.float32, roi_bbox=None):

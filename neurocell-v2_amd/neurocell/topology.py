@@ -279,6 +279,17 @@ class ChipTopology2D:
                                              name="tape_in"),),
                           out_port=PortSpec(offset=(mid, out_c), size=(1, n), name="tape_out"))
 
+    def out_cells_grid(self) -> tuple:
+        """Grid (rows, cols) int arrays of the output cells in port order (the cells
+        _extract_output_from_full_grid reads, propagator.py:194-206)."""
+        if isinstance(self.out_port, CoordinatePortSpec):
+            return (np.asarray(self.out_port.rows, np.int32),
+                    np.asarray(self.out_port.cols, np.int32))
+        r0, c0 = self.out_port.offset
+        oh, ow = self.out_port.size
+        rr, cc = np.meshgrid(np.arange(oh), np.arange(ow), indexing="ij")
+        return (r0 + rr.ravel()).astype(np.int32), (c0 + cc.ravel()).astype(np.int32)
+
     def out_cells_roi(self) -> tuple:
         """ROI-relative (rows, cols) int arrays of the output cells in port order."""
         if isinstance(self.out_port, CoordinatePortSpec):

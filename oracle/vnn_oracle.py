@@ -193,6 +193,12 @@ class Geometry:
         return (np.asarray(rows) - self.pad_h, np.asarray(cols) - self.pad_w)
 
     @property
+    def out_cells_grid(self):
+        """Grid (rows, cols) of the output port cells in port order."""
+        rows, cols = self.out_cells_roi
+        return rows + self.pad_h, cols + self.pad_w
+
+    @property
     def out_size(self):
         kind, a, *b = self.out_port
         return tuple(b[0]) if kind == "rect" else (len(a), 1)
@@ -288,10 +294,13 @@ def precompute_step_params(cell, geom: Geometry, act="tanh", hard_pin_io=False, 
     border_2d = act_fwd(b_full, act) * s_prob
     rows, cols = geom.out_cells_roi
     oh, ow = geom.out_size
+    # port parameters exist for a port inside the ROI (a border port reads the universe)
+    inside = (rows >= 0) & (rows < w_roi.shape[0]) & (cols >= 0) & (cols < w_roi.shape[1])
+    rows, cols = np.where(inside, rows, 0), np.where(inside, cols, 0)
+    port = lambda a: np.where(inside, a[rows, cols], 0.0).reshape(oh, ow)
     return dict(
         w_eff_roi=w_eff[sub], s_eff_roi=s_eff[sub], b_roi=b_roi[sub], border_2d=border_2d,
-        w_eff_out=w_eff[rows, cols].reshape(oh, ow), s_eff_out=s_eff[rows, cols].reshape(oh, ow),
-        b_out=b_roi[rows, cols].reshape(oh, ow),
+        w_eff_out=port(w_eff), s_eff_out=port(s_eff), b_out=port(b_roi),
         w_pinned=w_pinned, s_prob=s_prob, ds_prob=ds, b_full=b_full,
     )
 
@@ -300,8 +309,9 @@ def precompute_step_params_vjp(cell, geom: Geometry, grads: dict, act="tanh", ha
                                roi_bbox=None, mode="continuous", tau=1.0, active_threshold=0.6):
     """Reverse-mode derivative of :func:`precompute_step_params` (params.py:220-322 by hand).
 
-    ``grads`` may hold ``w_eff_roi``, ``s_eff_roi``, ``b_roi`` (cropped shape), ``border_2d``
-    (H, W), ``w_eff_out``, ``s_eff_out``, ``b_out`` (out_size).  Returns g_cell (3, H, W).
+    ``grads`` may hold ``w_eff_roi``, ``s_eff_roi``, ``b_roi`` (cropped shape), ``border_2d``,
+    ``s_prob``, ``b_full`` (H, W), ``w_eff_out``, ``s_eff_out``, ``b_out`` (out_size).
+    Returns g_cell (3, H, W).
     """
     H, W = geom.grid_shape
     rh, rw = geom.pad_h, geom.pad_w
@@ -322,9 +332,11 @@ def precompute_step_params_vjp(cell, geom: Geometry, grads: dict, act="tanh", ha
     if "b_roi" in grads:
         g_broi[r0:r1, c0:c1] += grads["b_roi"]
     rows, cols = geom.out_cells_roi
+    inside = (rows >= 0) & (rows < hv) & (cols >= 0) & (cols < wv)
     for key, dst in (("w_eff_out", g_weff), ("s_eff_out", g_seff), ("b_out", g_broi)):
         if key in grads:
-            np.add.at(dst, (rows, cols), np.asarray(grads[key]).reshape(-1))
+            np.add.at(dst, (rows[inside], cols[inside]),
+                      np.asarray(grads[key]).reshape(-1)[inside])
     roi = (slice(rh, H - rh), slice(rw, W - rw))
     g_wp = np.zeros((H, W), _dt())
     g_sp = np.zeros((H, W), _dt())
@@ -337,6 +349,10 @@ def precompute_step_params_vjp(cell, geom: Geometry, grads: dict, act="tanh", ha
         gbd = np.asarray(grads["border_2d"], _dt())
         g_b += act_deriv(b_full, act) * s_prob * gbd
         g_sp += act_fwd(b_full, act) * gbd
+    if "s_prob" in grads:  # full-grid gradients on s_prob and on B themselves
+        g_sp += np.asarray(grads["s_prob"], _dt())
+    if "b_full" in grads:
+        g_b += np.asarray(grads["b_full"], _dt())
     g_w = np.where(geom.out_weight_mask, 0.0, g_wp)
     g_s = g_sp * ds
     return np.stack([g_w, g_b, g_s])
@@ -376,6 +392,25 @@ def inject_inputs_roi(port_inputs, geom: Geometry, roi_bbox=None):
             raise ValueError("port outside ROI")
         out[:, r0 - min_r:r0 - min_r + ih, c0 - min_c:c0 - min_c + iw] = val
     return out
+
+
+def inject_inputs_full(port_inputs, geom: Geometry):
+    """``inject_inputs_2d`` (propagator.py:103-132): the port inputs written into a zero
+    (B, H, W) grid (a 3-D per-port input with its own (ih, iw))."""
+    H, W = geom.grid_shape
+    B = np.asarray(port_inputs[0]).shape[0]
+    cells = np.zeros((B, H, W), _dt())
+    for inp, port in zip(port_inputs, geom.in_ports):
+        inp = np.asarray(inp, _dt())
+        kind, a, *b = port
+        if kind == "coords":
+            for k, (r, c) in enumerate(a):
+                cells[:, r, c] = inp.reshape(B, -1)[:, k]
+            continue
+        (r0, c0) = a
+        ih, iw = inp.shape[1:] if inp.ndim == 3 else b[0]
+        cells[:, r0:r0 + ih, c0:c0 + iw] = inp.reshape(B, ih, iw)
+    return cells
 
 
 def split_ports(inputs, geom: Geometry):
@@ -606,12 +641,59 @@ def border_patch(border_2d, geom: Geometry, roi_bbox=None):
     return bo
 
 
+def universe_embed(roi_final, sp, geom: Geometry, final_act=None, roi_bbox=None):
+    """The final universe (propagator.py:700-731): the last step's sub-ROI epilogue output
+    embedded in the grid, whose other cells hold final_act(B) * s_prob in VALID mode (zeros
+    otherwise), then the final activation over the whole grid.  Returns (universe, pre)."""
+    B = roi_final.shape[0]
+    H, W = geom.grid_shape
+    rh, rw = geom.pad_h, geom.pad_w
+    hv, wv = geom.roi_shape
+    r0, r1, c0, c1 = roi_bbox if roi_bbox is not None else (0, hv, 0, wv)
+    if geom.padding_mode == "VALID":
+        border = act_fwd(sp["b_full"], final_act) * sp["s_prob"]
+    else:
+        border = np.zeros((H, W), _dt())
+    pre = np.broadcast_to(border, (B, H, W)).astype(_dt())
+    pre[:, rh + r0:rh + r1, rw + c0:rw + c1] = roi_final
+    return act_fwd(pre, final_act), pre
+
+
+def universe_vjp(pre, g_out, g_universe, sp, geom: Geometry, final_act=None, roi_bbox=None):
+    """Reverse of :func:`universe_embed` and the port read (the autodiff of
+    propagator.py:700-734, :194-206): the port cotangents added at their cells, through the
+    final activation onto the sub-ROI output (g_roi (B,h,w)) and, in VALID mode, the batch
+    sum over the other cells onto s_prob and B (returned as the ``s_prob`` / ``b_full``
+    gradients of :func:`precompute_step_params_vjp`)."""
+    B, H, W = pre.shape
+    g_fc = np.zeros((B, H, W), _dt()) if g_universe is None else np.array(g_universe, _dt())
+    gr, gc = geom.out_cells_grid
+    go = np.asarray(g_out, _dt()).reshape(B, -1)
+    for p in range(go.shape[1]):
+        g_fc[:, gr[p], gc[p]] += go[:, p]
+    g_pre = g_fc * act_deriv(pre, final_act)
+    rh, rw = geom.pad_h, geom.pad_w
+    hv, wv = geom.roi_shape
+    r0, r1, c0, c1 = roi_bbox if roi_bbox is not None else (0, hv, 0, wv)
+    region = (slice(rh + r0, rh + r1), slice(rw + c0, rw + c1))
+    extra = {}
+    if geom.padding_mode == "VALID":
+        gm = g_pre.sum(0)
+        gm[region] = 0.0
+        bf = sp["b_full"]
+        extra = dict(s_prob=gm * act_fwd(bf, final_act),
+                     b_full=gm * sp["s_prob"] * act_deriv(bf, final_act))
+    return g_pre[:, region[0], region[1]], extra
+
+
 def propagate(cell, filters, inputs, geom: Geometry, act="tanh", final_act=None,
               hard_pin_io=False, roi_bbox=None, mode="continuous", tau=1.0,
-              active_threshold=0.6, conv="fft"):
+              active_threshold=0.6, conv="fft", universe=False):
     """Pure-ROI forward of ``propagate_vnn_2d`` for the pallas backends (propagator.py:252-682)
     and its CIRCULAR branch (:284-341); SAME and CIRCULAR have the whole grid as ROI and no
-    border term.  ``filters`` is (M,1,Kh,Kw).  Returns (out, cache)."""
+    border term.  ``filters`` is (M,1,Kh,Kw).  Returns (out, cache).  With ``universe`` the
+    last step runs the full-grid output path (propagator.py:684-734): the port is read from the
+    final universe, kept as ``cache["universe"]``."""
     valid = geom.padding_mode == "VALID"
     circular = geom.padding_mode == "CIRCULAR"
     if circular and roi_bbox is not None:
@@ -623,8 +705,18 @@ def propagate(cell, filters, inputs, geom: Geometry, act="tanh", final_act=None,
     d = geom.depth
     sp = precompute_step_params(cell, geom, act, hard_pin_io, roi_bbox, mode, tau,
                                 active_threshold)
-    x = inject_inputs_roi(split_ports(inputs, geom), geom, roi_bbox)
-    hv, wv = x.shape[-2:]
+    try:
+        x = inject_inputs_roi(split_ports(inputs, geom), geom, roi_bbox)
+        t0_grid = False
+        hv, wv = x.shape[-2:]
+    except ValueError:
+        # inputs outside the ROI: step 0 is the VALID correlation of the full injected grid
+        # (propagator.py:347-352, 631-646)
+        if not valid or roi_bbox is not None:
+            raise
+        x = inject_inputs_full(split_ports(inputs, geom), geom)
+        t0_grid = True
+        hv, wv = geom.roi_shape
     if roi_bbox is not None:
         fft_shape = (1 << (hv + kh - 2).bit_length(), 1 << (wv + kw - 2).bit_length())
     else:
@@ -643,37 +735,49 @@ def propagate(cell, filters, inputs, geom: Geometry, act="tanh", final_act=None,
 
     xs, zs, stats = [x], [], []
     for t in range(d - 1):
-        z = _conv(xs[-1])
+        z = conv2d_direct(x, g, (0, 0)) if t == 0 and t0_grid else _conv(xs[-1])
         hb = t > 0 and valid
         out, mean, rstd = epilogue_fwd(z, delta, sp["w_eff_roi"], sp["s_eff_roi"], sp["b_roi"],
                                        act, hb)
         zs.append(z)
         stats.append((mean, rstd))
         xs.append(out)
-    z = _conv(xs[-1])
+    z = conv2d_direct(x, g, (0, 0)) if d == 1 and t0_grid else _conv(xs[-1])
     zs.append(z)
     rows, cols = geom.out_cells_roi
     if roi_bbox is not None:
         rows, cols = rows - roi_bbox[0], cols - roi_bbox[2]
     hb_final = d > 1 and valid
-    out, aux = port_fwd(z, delta, rows, cols, geom.out_size, sp["w_eff_out"], sp["s_eff_out"],
-                        sp["b_out"], hb_final, final_act)
+    univ = None
+    if universe:
+        roi_final, mean, rstd = epilogue_fwd(z, delta, sp["w_eff_roi"], sp["s_eff_roi"],
+                                             sp["b_roi"], final_act, hb_final)
+        univ, pre = universe_embed(roi_final, sp, geom, final_act, roi_bbox)
+        gr, gc = geom.out_cells_grid
+        out = univ[:, gr, gc].reshape((-1,) + tuple(geom.out_size))
+        aux = dict(mean=mean, rstd=rstd, pre=pre)
+    else:
+        out, aux = port_fwd(z, delta, rows, cols, geom.out_size, sp["w_eff_out"],
+                            sp["s_eff_out"], sp["b_out"], hb_final, final_act)
     cache = dict(sp=sp, xs=xs, zs=zs, stats=stats, delta=delta, bp=bp, aux=aux, g=g, pad=pad,
-                 fft_shape=fft_shape, rows=rows, cols=cols)
+                 fft_shape=fft_shape, rows=rows, cols=cols, universe=univ, roi_bbox=roi_bbox,
+                 t0_grid=t0_grid)
     return out, cache
 
 
 def propagate_vjp(cell, filters, inputs, geom: Geometry, g_out, act="tanh", final_act=None,
                   hard_pin_io=False, roi_bbox=None, mode="continuous", tau=1.0,
-                  active_threshold=0.6, fwd=None):
+                  active_threshold=0.6, fwd=None, universe=False, g_universe=None):
     """Reverse pass of :func:`propagate`: the chain of the reference's custom VJPs
     (kernels_pallas.py:1350-1504, 869-1064, 1794-1821, 1558-1579; propagator.py autodiff of
     the border conv and params.py autodiff of the pre-step fusion).
     ``fwd`` may pass the (out, cache) of a matching :func:`propagate` call to skip the
-    forward.  Returns (out, g_cell (3,H,W), g_filters (M,1,Kh,Kw))."""
+    forward.  With ``universe`` the cotangent is g_out on the port plus ``g_universe``
+    (B,H,W, optional) on the final universe.  Returns (out, g_cell (3,H,W), g_filters
+    (M,1,Kh,Kw))."""
     out, c = fwd if fwd is not None else propagate(
         cell, filters, inputs, geom, act, final_act, hard_pin_io, roi_bbox, mode, tau,
-        active_threshold)
+        active_threshold, universe=universe)
     sp, g, pad, fs = c["sp"], c["g"], c["pad"], c["fft_shape"]
     d = geom.depth
     kh, kw = geom.kernel_size
@@ -684,14 +788,31 @@ def propagate_vjp(cell, filters, inputs, geom: Geometry, g_out, act="tanh", fina
     g_broi = np.zeros_like(sp["b_roi"])
     valid = geom.padding_mode == "VALID"
     hb_final = d > 1 and valid
-    gz, gdb, g_wo, g_so, g_bo = port_bwd(c["zs"][-1], c["delta"], c["rows"], c["cols"],
-                                         geom.out_size, sp["w_eff_out"], sp["s_eff_out"],
-                                         sp["b_out"], c["aux"], np.asarray(g_out, _dt()),
-                                         hb_final, final_act)
+    extra = {}
+    if c["universe"] is not None:
+        aux = c["aux"]
+        g_roi, extra = universe_vjp(aux["pre"], g_out, g_universe, sp, geom, final_act,
+                                    roi_bbox)
+        gz, gdb, gw, gs, gb = epilogue_bwd(c["zs"][-1], c["delta"], sp["w_eff_roi"],
+                                           sp["s_eff_roi"], sp["b_roi"], aux["mean"],
+                                           aux["rstd"], g_roi, final_act, hb_final)
+        g_weff += gw
+        g_seff += gs
+        g_broi += gb
+        g_wo = g_so = g_bo = np.zeros(geom.out_size, _dt())
+    else:
+        gz, gdb, g_wo, g_so, g_bo = port_bwd(c["zs"][-1], c["delta"], c["rows"], c["cols"],
+                                             geom.out_size, sp["w_eff_out"], sp["s_eff_out"],
+                                             sp["b_out"], c["aux"], np.asarray(g_out, _dt()),
+                                             hb_final, final_act)
     g_delta += gdb
     dGh = np.zeros((M, fs[0], fs[1] // 2 + 1), complex)
+    dg0 = 0.0
     for t in range(d - 1, -1, -1):
         x_t = c["xs"][t]
+        if t == 0 and c["t0_grid"]:  # the full-grid VALID step's filter gradient
+            dg0 = conv2d_bwd_direct(gz, x_t, g, (0, 0))[1]
+            break
         dx, dG_t = conv2d_fft_unshifted_bwd(gz, x_t, g, pad, fs, need_dx=t > 0)
         dGh += dG_t
         if t == 0:
@@ -704,7 +825,7 @@ def propagate_vjp(cell, filters, inputs, geom: Geometry, g_out, act="tanh", fina
         g_weff += gw
         g_seff += gs
         g_broi += gb
-    g_filt = filter_grad_from_unshifted(dGh, (kh, kw), pad, fs)
+    g_filt = filter_grad_from_unshifted(dGh, (kh, kw), pad, fs) + dg0
     H, W = geom.grid_shape
     g_border = np.zeros((H, W), _dt())
     bp = c["bp"]
@@ -722,32 +843,27 @@ def propagate_vjp(cell, filters, inputs, geom: Geometry, g_out, act="tanh", fina
         rh, rw = geom.pad_h, geom.pad_w
         g_border[rh:H - rh, rw:W - rw] = 0.0
     grads = dict(w_eff_roi=g_weff, s_eff_roi=g_seff, b_roi=g_broi, border_2d=g_border,
-                 w_eff_out=g_wo, s_eff_out=g_so, b_out=g_bo)
+                 w_eff_out=g_wo, s_eff_out=g_so, b_out=g_bo, **extra)
     g_cell = precompute_step_params_vjp(cell, geom, grads, act, hard_pin_io, roi_bbox, mode,
                                         tau, active_threshold)
     return out, g_cell, g_filt[:, None]
 
 
 def propagate_full_grid(cell, filters, inputs, geom: Geometry, act="tanh", final_act=None,
-                        hard_pin_io=False, mode="continuous", tau=1.0, active_threshold=0.6):
+                        hard_pin_io=False, mode="continuous", tau=1.0, active_threshold=0.6,
+                        return_universe=False):
     """Full-grid semantic definition (contrib/forward.py:737-810, driven as
     contrib/forward.py:162-178) using the v2 pinned/fused parameters: each step is a VALID
     correlation of the whole (B,H,W) grid, standardized, zero-padded back, Codd-gated and
-    averaged over M.  Used to pin the pure-ROI + hoisted-border decomposition."""
+    averaged over M.  Used to pin the pure-ROI + hoisted-border decomposition and the final
+    universe (returned too with ``return_universe``)."""
     sp = precompute_step_params(cell, geom, act, hard_pin_io, None, mode, tau, active_threshold)
     g = np.asarray(filters, _dt())[:, 0]
     H, W = geom.grid_shape
     rh, rw = geom.pad_h, geom.pad_w
     M = geom.directions
-    ports = split_ports(inputs, geom)
-    B = np.asarray(ports[0]).shape[0]
-    cells = np.zeros((B, H, W), _dt())
-    for inp, port in zip(ports, geom.in_ports):
-        kind, a, *b = port
-        (r0, c0) = a
-        inp = np.asarray(inp, _dt())
-        ih, iw = inp.shape[1:] if inp.ndim == 3 else b[0]
-        cells[:, r0:r0 + ih, c0:c0 + iw] = inp.reshape(B, ih, iw)
+    cells = inject_inputs_full(split_ports(inputs, geom), geom)
+    B = cells.shape[0]
     w, bb, s = sp["w_pinned"], sp["b_full"], sp["s_prob"]
 
     def step(cells, a):
@@ -765,8 +881,9 @@ def propagate_full_grid(cell, filters, inputs, geom: Geometry, act="tanh", final
     cells = step(cells, final_act)
     if final_act is not None:
         cells = act_fwd(cells, final_act)
-    kind, (r0, c0), (oh, ow) = geom.out_port
-    return cells[:, r0:r0 + oh, c0:c0 + ow]
+    gr, gc = geom.out_cells_grid
+    out = cells[:, gr, gc].reshape((B,) + tuple(geom.out_size))
+    return (out, cells) if return_universe else out
 
 
 # ---------------------------------------------------------------------------

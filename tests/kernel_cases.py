@@ -227,22 +227,23 @@ def case_border_fold(be, B=3, M=4, h=12, w=10, kh=7, kw=5, FH=32, FW=16, seed=5)
     patch = rng.normal(size=(1, Hp, Wp)).astype(np.float32)
     g = rng.normal(size=(M, 1, kh, kw)).astype(np.float32)
     gz = rng.normal(size=(B, M, h, w)).astype(np.float32)
+    # operands held in names: a device tensor must outlive the launch that reads it
+    gd, patchd, xd, gzd = be.put(g), be.put(patch), be.put(x), be.put(gz)
     ghat = be.zeros((M, FH, FW // 2 + 1, 2))
-    _ok(be, L.nc_filter_spectrum_fwd(s, M, kh, kw, FH, FW, be.ptr(be.put(g)), be.ptr(ghat)),
-        "spec")
+    _ok(be, L.nc_filter_spectrum_fwd(s, M, kh, kw, FH, FW, be.ptr(gd), be.ptr(ghat)), "spec")
     padd = be.zeros((1, FH, FW // 2 + 1, 2))
-    _ok(be, L.nc_plane_spectrum(s, 1, Hp, Wp, FH, FW, sh, sw, be.ptr(be.put(patch)),
+    _ok(be, L.nc_plane_spectrum(s, 1, Hp, Wp, FH, FW, sh, sw, be.ptr(patchd),
                                 be.ptr(padd)), "plane_spectrum")
     z = be.zeros((B, M, h, w))
     xhat = be.zeros((B, FH, FW // 2 + 1, 2))
-    _ok(be, L.nc_fftconv_fwd_ex(s, B, M, h, w, h, w, ph, pw, FH, FW, be.ptr(be.put(x)),
+    _ok(be, L.nc_fftconv_fwd_ex(s, B, M, h, w, h, w, ph, pw, FH, FW, be.ptr(xd),
                                 be.ptr(padd), be.ptr(ghat), be.ptr(z), be.ptr(xhat)), "fwd_ex")
     ws = be.zeros((L.nc_fftconv_bwd_workspace_size(B, M, FH, FW) // 4 + 1,))
     nb = ws.nbytes if hasattr(ws, "nbytes") else ws.numel() * 4
     dx = be.zeros((B, h, w))
     dgh = be.zeros((M, FH, FW // 2 + 1, 2))
     ssum = be.zeros((M, FH, FW // 2 + 1, 2))
-    _ok(be, L.nc_fftconv_bwd_ex(s, B, M, h, w, h, w, ph, pw, FH, FW, be.ptr(be.put(gz)),
+    _ok(be, L.nc_fftconv_bwd_ex(s, B, M, h, w, h, w, ph, pw, FH, FW, be.ptr(gzd),
                                 be.ptr(xhat), be.ptr(ghat), 1, be.ptr(dx), be.ptr(dgh), 0, 0,
                                 be.ptr(ssum), 0, be.ptr(ws), nb), "bwd_ex")
     gf = be.zeros((M, 1, kh, kw))
@@ -668,10 +669,13 @@ def case_codd(be, mode="continuous", bbox=None, hard_pin=0, tau=0.1, seed=4):
     gpp = rng.normal(size=(3, P)).astype(np.float32)
     gid = [be.put(a) for a in gi]
     gpd, gppd = be.put(gpatch), be.put(gpp)
+    gsp, gbf = (rng.normal(size=(H, W)).astype(np.float32) for _ in range(2))
+    gspd, gbfd = be.put(gsp), be.put(gbf)  # held: a device tensor must outlive the launch
     gcell = be.zeros((3, H, W))
     _ok(be, L.nc_codd_fuse_bwd(s, C.byref(chip), be.ptr(cd), be.ptr(io), be.ptr(owm), mid, it,
                                0.6, hard_pin, 1, 0.01, P, be.ptr(prc), *[be.ptr(a) for a in gid],
-                               be.ptr(gpd), be.ptr(gppd), be.ptr(gcell)), "coddb")
+                               be.ptr(gpd), be.ptr(gppd), be.ptr(gspd), be.ptr(gbfd),
+                               be.ptr(gcell)), "coddb")
     gbd = np.zeros((H, W))
     gbd[r0:r0 + gpatch.shape[0], c0:c0 + gpatch.shape[1]] = gpatch
     gbd[geom.pad_h:H - geom.pad_h, geom.pad_w:W - geom.pad_w] = 0
@@ -679,11 +683,61 @@ def case_codd(be, mode="continuous", bbox=None, hard_pin=0, tau=0.1, seed=4):
     ref = O.precompute_step_params_vjp(
         cell, geom, dict(w_eff_roi=gi[0], s_eff_roi=gi[1], b_roi=gi[2], border_2d=gbd,
                          w_eff_out=gpp[0].reshape(oh, ow), s_eff_out=gpp[1].reshape(oh, ow),
-                         b_out=gpp[2].reshape(oh, ow)),
+                         b_out=gpp[2].reshape(oh, ow), s_prob=gsp, b_full=gbf),
         "tanh", bool(hard_pin), bbox, mode, tau, 0.6)
     return {"fwd": rel_l2(fwd_got, fwd_ref), "s_prob": rel_l2(be.get(sp_), sp["s_prob"]),
             "border_2d": rel_l2(be.get(b2d), sp["border_2d"]),
             "w_pinned": rel_l2(be.get(wp), sp["w_pinned"]), "g_cell": rel_l2(be.get(gcell), ref)}
+
+
+def case_universe(be, pmode="VALID", bbox=None, fact="tanh", B=3, G=2, seed=10):
+    """nc_universe_fwd / nc_universe_bwd: the final universe and the full-grid port read from
+    it (propagator.py:684-734), with a port on the border and a cell read twice."""
+    rng = np.random.default_rng(seed)
+    L, s = be.lib, be.stream()
+    out = ("coords", [(0, 0), (1, 5), (8, 7), (15, 13), (6, 9), (8, 7)])
+    geom = O.Geometry((16, 14), (5, 3), 3, 2, [("rect", (5, 3), (4, 1))], out,
+                      padding_mode=pmode)
+    H, W = geom.grid_shape
+    r0, r1, c0, c1 = bbox or (0, geom.roi_shape[0], 0, geom.roi_shape[1])
+    h, w = r1 - r0, c1 - c0
+    chip = _abi.ChipDesc(H, W, 5, 3, 3, geom.pad_h, geom.pad_w, *geom.roi_shape, r0, r1, c0, c1)
+    parts = rng.normal(0, 0.7, size=(G, B, h, w)).astype(np.float32)
+    bf = rng.normal(size=(H, W)).astype(np.float32)
+    sp = rng.random((H, W)).astype(np.float32)
+    gr, gc = geom.out_cells_grid
+    cells = (gr * W + gc).astype(np.int32)
+    P = cells.size
+    head, nxt = np.full(H * W, -1, np.int32), np.full(P, -1, np.int32)
+    for k in range(P - 1, -1, -1):
+        nxt[k], head[cells[k]] = head[cells[k]], k
+    valid = int(pmode == "VALID")
+    fid, slope = _abi.ACT_IDS[fact or "identity"], 0.01
+    # every operand held in a name: a device tensor must outlive the launch
+    pd, bfd, spd = be.put(parts), be.put(bf), be.put(sp)
+    cd, hd, nd = be.put(cells, np.int32), be.put(head, np.int32), be.put(nxt, np.int32)
+    univ, outd = be.zeros((B, H, W)), be.zeros((B, P))
+    _ok(be, L.nc_universe_fwd(s, C.byref(chip), B, G, valid, fid, slope, be.ptr(pd),
+                              be.ptr(bfd), be.ptr(spd), P, be.ptr(cd), be.ptr(univ),
+                              be.ptr(outd)), "universe_fwd")
+    sp_d = dict(b_full=bf.astype(np.float64), s_prob=sp.astype(np.float64))
+    ref_u, pre = O.universe_embed(parts.astype(np.float64).sum(0), sp_d, geom, fact, bbox)
+    g_out = rng.normal(size=(B, P)).astype(np.float32)
+    g_u = rng.normal(size=(B, H, W)).astype(np.float32)
+    god, gud = be.put(g_out), be.put(g_u)
+    g_roi, gsp, gbf = be.zeros((B, h, w)), be.zeros((H, W)), be.zeros((H, W))
+    _ok(be, L.nc_universe_bwd(s, C.byref(chip), B, G, valid, fid, slope, be.ptr(pd),
+                              be.ptr(bfd), be.ptr(spd), P, be.ptr(hd), be.ptr(nd), be.ptr(god),
+                              be.ptr(gud), be.ptr(g_roi), be.ptr(gsp) if valid else None,
+                              be.ptr(gbf) if valid else None), "universe_bwd")
+    ref_g, extra = O.universe_vjp(pre, g_out, g_u, sp_d, geom, fact, bbox)
+    res = {"universe": rel_l2(be.get(univ), ref_u),
+           "out": rel_l2(be.get(outd), ref_u[:, gr, gc]),
+           "g_roi": rel_l2(be.get(g_roi), ref_g)}
+    if valid:
+        res["g_s_prob"] = rel_l2(be.get(gsp), extra["s_prob"])
+        res["g_b_full"] = rel_l2(be.get(gbf), extra["b_full"])
+    return res
 
 
 def case_adaptive(be, seed=5):

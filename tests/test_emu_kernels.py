@@ -8,7 +8,8 @@ import pytest
 from kernel_cases import (CODD_CASES, TOL, HostBackend, case_adaptive, case_border_conv,
                           case_border_fold, case_codd, case_epilogue, case_epilogue_parts,
                           case_fftconv_circular, case_fftconv_port, case_fftconv_epilogue,
-                          case_fftconv, case_helpers, case_plane_spectra, case_port)
+                          case_fftconv, case_helpers, case_plane_spectra, case_port,
+                          case_universe)
 
 
 @pytest.fixture(scope="module")
@@ -139,3 +140,12 @@ def test_fftconv_port(be, B, M, h, w, kh, kw, FH, FW, fact):
     res = case_fftconv_port(be, B=B, M=M, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW, fact=fact,
                             rows=rows, cols=cols)
     _assert_small(res)
+
+
+UNIVERSE_CASES = [("VALID", None, "tanh"), ("VALID", (2, 9, 1, 10), "sigmoid"),
+                  ("VALID", None, None), ("SAME", None, "relu"), ("SAME", (3, 12, 2, 11), "gelu")]
+
+
+@pytest.mark.parametrize("pmode,bbox,fact", UNIVERSE_CASES)
+def test_universe(be, pmode, bbox, fact):
+    _assert_small(case_universe(be, pmode, bbox, fact))

@@ -207,6 +207,35 @@ def test_propagate_autograd(mode, tau, bbox):
     assert rel_l2(host(p.greens_filters.grad), r_gf) < GRAD_TOL
 
 
+@pytest.mark.parametrize("bbox,use_univ", [(None, True), (CROP, True), (None, False)])
+def test_return_universe_autograd(bbox, use_univ):
+    """propagate_vnn_2d(..., return_universe=True) on the ALU chip (unit_vnn_alu_parity.py:
+    76-100): the port equals the stateless call's, the universe is the oracle's final cells,
+    and autograd through either output reaches the parameters."""
+    from neurocell import VNNParams, propagate_vnn_2d
+    from neurocell.topology import ChipTopology2D
+    geom, cell, filt, x, _ = alu_case(12, B=8)
+    topo = ChipTopology2D.alu_chip(out_width=2)
+    p = VNNParams(dev(cell).requires_grad_(), dev(filt).requires_grad_())
+    kw = dict(spatial_mask=mask(bbox), final_activate="sigmoid")
+    out, univ = propagate_vnn_2d(p, dev(x), topo, return_universe=True, **kw)
+    with torch.no_grad():
+        plain = propagate_vnn_2d(p, dev(x), topo, **kw)
+    rng = np.random.default_rng(13)
+    g = rng.normal(size=tuple(out.shape)).astype(np.float32)
+    gu = rng.normal(size=tuple(univ.shape)).astype(np.float32) if use_univ else None
+    loss = (out * dev(g)).sum() + ((univ * dev(gu)).sum() if use_univ else 0.0)
+    loss.backward()
+    ok = dict(roi_bbox=bbox, final_act="sigmoid", universe=True)
+    r_out, r_c = O.propagate(cell, filt, x, geom, **ok)
+    _, r_gc, r_gf = O.propagate_vjp(cell, filt, x, geom, g, g_universe=gu, fwd=(r_out, r_c), **ok)
+    assert rel_l2(host(out), r_out) < FWD_TOL
+    assert rel_l2(host(plain), host(out)) < FWD_TOL
+    assert rel_l2(host(univ), r_c["universe"]) < FWD_TOL
+    assert rel_l2(host(p.cell_params.grad), r_gc) < GRAD_TOL
+    assert rel_l2(host(p.greens_filters.grad), r_gf) < GRAD_TOL
+
+
 def test_two_live_graphs():
     """Two forwards kept alive before their backwards (each call owns its activations)."""
     from neurocell import VNNParams, propagate_vnn_2d

@@ -208,12 +208,84 @@ def test_gol_chip_parity(mode, n, final_act, act):
         assert errs[k] < GRAD_TOL, errs
 
 
-def test_gol_valid_universe_port_is_refused():
-    """VALID Game of Life puts its output outside the ROI (the full-grid output path of
-    propagator.py:684-734), which this build does not run: a clear error before any launch."""
-    from neurocell.engine import StepPlan
-    from neurocell._lib import NeurocellError
+def _universe_check(geom, topo, cell, filt, x, act="tanh", final_act=None, bbox=None,
+                    want_universe=True, seed=40):
+    """The full-grid output path (propagator.py:684-734) through StepPlan: the port, the final
+    universe and the gradients for cotangents on both, against the oracle."""
+    from neurocell.engine import StepPlan, flatten_inputs, port_input_shapes
+    dev = torch.device("cuda")
+    B = x.shape[0]
+    xt = torch.from_numpy(x).to(dev)
+    plan = StepPlan(topo, B, port_input_shapes(xt, topo), roi_bbox=bbox, activate=act,
+                    final_activate=final_act, universe=want_universe)
+    assert plan.universe
+    rng = np.random.default_rng(seed)
+    g_out = rng.normal(size=(B,) + geom.out_size).astype(np.float32)
+    H, W = geom.grid_shape
+    g_u = rng.normal(size=(B, H, W)).astype(np.float32) if want_universe else None
+    c, f = torch.from_numpy(cell).to(dev), torch.from_numpy(filt).to(dev)
+    out = plan.forward(c, f, flatten_inputs(xt, topo))
+    univ = plan.univ.cpu().numpy() if want_universe else None
+    out = out.cpu().numpy()
+    gc, gf = torch.empty_like(c), torch.empty_like(f)
+    plan.backward(c, f, torch.from_numpy(g_out.reshape(B, -1)).to(dev), gc, gf,
+                  g_universe=None if g_u is None else torch.from_numpy(g_u).to(dev))
+    torch.cuda.synchronize()
+    kw = dict(act=act, final_act=final_act, roi_bbox=bbox, universe=True)
+    r_out, r_c = O.propagate(cell, filt, x, geom, **kw)
+    _, r_gc, r_gf = O.propagate_vjp(cell, filt, x, geom, g_out, g_universe=g_u,
+                                    fwd=(r_out, r_c), **kw)
+    gc, gf = gc.cpu().numpy(), gf.cpu().numpy()
+    errs = {"out": rel_l2(out, r_out.reshape(B, -1)), "gW": rel_l2(gc[0], r_gc[0]),
+            "gB": rel_l2(gc[1], r_gc[1]), "gS": rel_l2(gc[2], r_gc[2]), "gG": rel_l2(gf, r_gf)}
+    if want_universe:
+        errs["universe"] = rel_l2(univ, r_c["universe"])
+    assert errs["out"] < FWD_TOL and errs.get("universe", 0.0) < FWD_TOL, errs
+    for k in ("gW", "gB", "gS", "gG"):
+        assert errs[k] < GRAD_TOL, errs
+    return errs
+
+
+@pytest.mark.parametrize("final_act,act", [("sigmoid", "tanh"), (None, "leaky_relu")])
+def test_gol_valid_universe_port_parity(final_act, act):
+    """VALID Game of Life (topology.py:359-388 with allow_border_output): the inputs cover the
+    grid (the full-grid step 0) and the universe port is read from the final universe, border
+    cells final_act(final_act(B) * s_prob) included."""
     from neurocell.topology import ChipTopology2D
-    topo = ChipTopology2D.gol_chip(n=32, kernel_size=(3, 3), directions=4, depth=2)
-    with pytest.raises(NeurocellError, match="outside the active ROI"):
-        StepPlan(topo, 2, [(32, 32)])
+    n = 32
+    topo = ChipTopology2D.gol_chip(n=n, kernel_size=(3, 3), directions=16, depth=4)
+    geom = O.Geometry((n, n), (3, 3), 16, 4, [("rect", (0, 0), (n, n))], ("rect", (0, 0), (n, n)))
+    rng = np.random.default_rng(33)
+    cell = np.stack([rng.normal(0, 0.1, (n, n)), rng.normal(0, 0.2, (n, n)),
+                     rng.normal(0, 1.0, (n, n))]).astype(np.float32)
+    filt = rng.normal(0, 1.0 / 3.0, (16, 1, 3, 3)).astype(np.float32)
+    x = (rng.random((4, n, n)) > 0.5).astype(np.float32)
+    _universe_check(geom, topo, cell, filt, x, act, final_act, want_universe=False)
+
+
+@pytest.mark.parametrize("mode,bbox,final_act", [
+    ("VALID", None, "tanh"), ("VALID", (0, 11, 1, 11), "sigmoid"), ("VALID", None, None),
+    ("SAME", None, "sigmoid"), ("SAME", (1, 14, 0, 13), None), ("CIRCULAR", None, "tanh")])
+def test_return_universe_parity(mode, bbox, final_act):
+    """return_universe=True (propagator.py:684-734): the universe and the port read from it,
+    with a cropped sub-ROI (VALID: the ROI cells outside the crop take the border value; SAME:
+    zeros), and gradients for cotangents on the universe and the port."""
+    geom, topo, cell, filt, x = _mode_case(mode, (16, 16), (5, 3), 3, 3)
+    _universe_check(geom, topo, cell, filt, x, "tanh", final_act, bbox=bbox)
+
+
+def test_clp_border_output_parity():
+    """A CLP chip (topology.py:391-428, allow_border_output) whose output coordinates lie on the
+    VALID border: the port is read from the final universe."""
+    from neurocell.topology import ChipTopology2D
+    outc = ((0, 0), (7, 3), (4, 4), (2, 7))
+    topo = ChipTopology2D.clp_chip(n=8, out_coords=outc)
+    assert not topo.out_in_roi
+    geom = O.Geometry((8, 8), (3, 3), 1, 4, [("coords", list(topo.in_ports[0].coords))],
+                      ("coords", list(outc)))
+    rng = np.random.default_rng(34)
+    cell = np.stack([rng.normal(0, 0.3, (8, 8)), rng.normal(0, 0.1, (8, 8)),
+                     rng.normal(0, 1.0, (8, 8))]).astype(np.float32)
+    filt = rng.normal(0, 1.0 / 3.0, (1, 1, 3, 3)).astype(np.float32)
+    x = (rng.random((8, 2)) > 0.5).astype(np.float32)
+    _universe_check(geom, topo, cell, filt, x, "tanh", "sigmoid", want_universe=False)

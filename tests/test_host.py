@@ -317,3 +317,16 @@ def test_chip_constructors_geometry():
     t = ChipTopology2D.tm_chip()  # n=8, K=13x13: N = 16 + 52
     assert t.grid_shape == (68, 68) and t.depth == 17
     assert t.in_ports[0].size == (1, 16) and t.out_port.offset == (34, 43)
+
+
+def test_out_cells_grid_reads_ports_anywhere():
+    """_extract_output_from_full_grid (propagator.py:194-206) reads the universe at the port's
+    own grid cells: a rectangle on the border (VALID Game of Life) and coordinates."""
+    from neurocell.topology import ChipTopology2D
+    t = ChipTopology2D.gol_chip(n=6, kernel_size=(3, 3), directions=2, depth=2)
+    assert not t.out_in_roi
+    r, c = t.out_cells_grid()
+    assert np.array_equal(r * 6 + c, np.arange(36))
+    t = ChipTopology2D.clp_chip(n=8, out_coords=((0, 0), (7, 3), (4, 4)))
+    r, c = t.out_cells_grid()
+    assert r.tolist() == [0, 7, 4] and c.tolist() == [0, 3, 4]

@@ -344,6 +344,81 @@ def test_propagate_vjp_matches_finite_differences(final_act, mode, bbox, pin):
     assert abs(fd - an) <= 1e-6 * max(1.0, abs(an))
 
 
+BORDER_PORT = ("coords", [(0, 0), (1, 5), (8, 7), (15, 13), (6, 9)])
+
+
+@pytest.mark.parametrize("final_act,out", [(None, None), ("tanh", None), ("sigmoid", BORDER_PORT),
+                                           (None, ("rect", (0, 0), (16, 14)))])
+def test_universe_equals_full_grid(final_act, out):
+    """propagator.py:684-734 (return_universe / an output port on the border): the pure-ROI
+    last step embedded with final_act(B) * s_prob around it is the full-grid VALID propagation
+    (contrib/forward.py:737-810), universe and port alike (unit_vnn_alu_parity.py:76-100)."""
+    g = small_geometry(depth=3) if out is None else small_geometry(depth=3, out=out)
+    rng = np.random.default_rng(21)
+    cell, filt = rand_cell(g, rng), rng.normal(size=(3, 1, 5, 3))
+    x = rand_inputs(g, 2, rng)
+    full, cells = O.propagate_full_grid(cell, filt, x, g, final_act=final_act,
+                                        return_universe=True)
+    roi, c = O.propagate(cell, filt, x, g, final_act=final_act, universe=True)
+    np.testing.assert_allclose(c["universe"], cells, rtol=0, atol=1e-10)
+    np.testing.assert_allclose(roi, full, rtol=0, atol=1e-10)
+    if out is None:  # a port inside the ROI reads the same values on the port path
+        port, _ = O.propagate(cell, filt, x, g, final_act=final_act)
+        np.testing.assert_allclose(roi, port, rtol=0, atol=1e-10)
+
+
+@pytest.mark.parametrize("final_act,bbox,pmode,out", [
+    (None, None, "VALID", BORDER_PORT), ("tanh", (1, 10, 2, 10), "VALID", None),
+    ("sigmoid", None, "SAME", ("rect", (0, 0), (16, 14))), ("tanh", (2, 12, 1, 9), "SAME", None)])
+def test_universe_vjp_matches_finite_differences(final_act, bbox, pmode, out):
+    g = O.Geometry((16, 14), (5, 3), 3, 3, [("rect", (5, 3), (4, 1)), ("rect", (4, 5), (1, 3))],
+                   out or ("rect", (6, 9), (3, 1)), padding_mode=pmode)
+    rng = np.random.default_rng(22)
+    cell, filt = rand_cell(g, rng), rng.normal(size=(3, 1, 5, 3))
+    x = rand_inputs(g, 2, rng)
+    kw = dict(final_act=final_act, tau=0.7, roi_bbox=bbox, universe=True)
+    out_, c = O.propagate(cell, filt, x, g, **kw)
+    g_out = rng.normal(size=out_.shape)
+    g_univ = rng.normal(size=c["universe"].shape)
+    _, gc, gf = O.propagate_vjp(cell, filt, x, g, g_out, g_universe=g_univ, **kw)
+    vc, vf = rng.normal(size=cell.shape), rng.normal(size=filt.shape)
+
+    def L(cc, ff):
+        o, k = O.propagate(cc, ff, x, g, **kw)
+        return float((o * g_out).sum() + (k["universe"] * g_univ).sum())
+    e = 1e-6
+    fd = (L(cell + e * vc, filt + e * vf) - L(cell - e * vc, filt - e * vf)) / (2 * e)
+    an = float((gc * vc).sum() + (gf * vf).sum())
+    assert abs(fd - an) <= 1e-6 * max(1.0, abs(an))
+
+
+@pytest.mark.parametrize("final_act,depth", [("sigmoid", 3), (None, 1)])
+def test_gol_valid_full_grid_inputs_and_universe(final_act, depth):
+    """VALID Game of Life (topology.py:359-388): inputs on the whole grid (the full-grid step
+    0 of propagator.py:347-352) and the universe port read from the final universe equal the
+    full-grid propagation; the reverse matches central finite differences."""
+    n = 10
+    g = O.Geometry((n, n), (3, 3), 2, depth, [("rect", (0, 0), (n, n))],
+                   ("rect", (0, 0), (n, n)))
+    rng = np.random.default_rng(23)
+    cell, filt = rand_cell(g, rng), rng.normal(size=(2, 1, 3, 3))
+    x = [rng.normal(size=(2, n, n))]
+    kw = dict(final_act=final_act, universe=True)
+    out, _ = O.propagate(cell, filt, x, g, **kw)
+    np.testing.assert_allclose(out, O.propagate_full_grid(cell, filt, x, g, final_act=final_act),
+                               rtol=0, atol=1e-10)
+    g_out = rng.normal(size=out.shape)
+    _, gc, gf = O.propagate_vjp(cell, filt, x, g, g_out, **kw)
+    vc, vf = rng.normal(size=cell.shape), rng.normal(size=filt.shape)
+
+    def L(cc, ff):
+        return float((O.propagate(cc, ff, x, g, **kw)[0] * g_out).sum())
+    e = 1e-6
+    fd = (L(cell + e * vc, filt + e * vf) - L(cell - e * vc, filt - e * vf)) / (2 * e)
+    an = float((gc * vc).sum() + (gf * vf).sum())
+    assert abs(fd - an) <= 1e-6 * max(1.0, abs(an))
+
+
 def test_zero_thresholding_gap_ste_ternary():
     """unit_milestone8_pallas_and_codd.py:239-252: replacing S by its discrete role values
     leaves the ste_ternary forward unchanged."""
