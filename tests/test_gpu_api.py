@@ -284,7 +284,8 @@ def test_model_checkpoint_and_states(tmp_path):
 
 # ------------------------------------------------------------------ trainer
 
-def _oracle_steps(cell, filt, xs, ys, geom, lr, n, bbox=None, mode="continuous", tau=1.0):
+def _oracle_steps(cell, filt, xs, ys, geom, lr, n, bbox=None, mode="continuous", tau=1.0,
+                  **kw):
     p = np.concatenate([cell.ravel(), filt.ravel()]).astype(np.float64)
     m = np.zeros_like(p)
     v = np.zeros_like(p)
@@ -293,9 +294,10 @@ def _oracle_steps(cell, filt, xs, ys, geom, lr, n, bbox=None, mode="continuous",
     for i in range(n):
         c = p[:nc].reshape(cell.shape).astype(np.float32)
         f = p[nc:].reshape(filt.shape).astype(np.float32)
-        out, _ = O.propagate(c, f, xs[i], geom, roi_bbox=bbox, mode=mode, tau=tau)
+        out, _ = O.propagate(c, f, xs[i], geom, roi_bbox=bbox, mode=mode, tau=tau, **kw)
         loss, g_out = O.mse_loss(out, ys[i])
-        _, gc, gf = O.propagate_vjp(c, f, xs[i], geom, g_out, roi_bbox=bbox, mode=mode, tau=tau)
+        _, gc, gf = O.propagate_vjp(c, f, xs[i], geom, g_out, roi_bbox=bbox, mode=mode, tau=tau,
+                                    **kw)
         g = np.concatenate([gc.ravel(), gf.ravel()])
         p, m, v, _ = O.adamw_step(p, g, m, v, i, lr(i) if callable(lr) else lr)
         losses.append(loss)
@@ -343,6 +345,35 @@ def test_trainer_steps_vs_oracle(variant):
     assert rel_l2(host(params.cell_params) - cell, r_c - cell) < TRAJ_TOL
     assert rel_l2(host(params.greens_filters) - filt, r_f - filt) < TRAJ_TOL
     assert int(state.count.item()) == 2
+
+
+def test_trainer_gol_valid_universe_port():
+    """Training VALID Game of Life (topology.py:359-388): its universe port lies on the border,
+    so every step reads the port from the final universe (propagator.py:684-734)."""
+    from neurocell import VNNParams, VNNTrainer, VonNeumannNetwork, adamw
+    from neurocell.topology import ChipTopology2D
+    n, M = 16, 4
+    topo = ChipTopology2D.gol_chip(n=n, kernel_size=(3, 3), directions=M, depth=3)
+    geom = O.Geometry((n, n), (3, 3), M, 3, [("rect", (0, 0), (n, n))], ("rect", (0, 0), (n, n)))
+    rng = np.random.default_rng(41)
+    cell = np.stack([rng.normal(0, 0.1, (n, n)), rng.normal(0, 0.2, (n, n)),
+                     rng.normal(0, 1.0, (n, n))]).astype(np.float32)
+    filt = rng.normal(0, 1.0 / 3.0, (M, 1, 3, 3)).astype(np.float32)
+    xs = (rng.random((2, 4, n, n)) > 0.5).astype(np.float32)
+    ys = (rng.random((2, 4, n, n)) > 0.5).astype(np.float32)
+    tr = VNNTrainer(VonNeumannNetwork(topo, final_activate="sigmoid").apply, adamw(0.01),
+                    batch_size=4)
+    params = VNNParams(dev(cell), dev(filt))
+    state = tr.optimizer.init(params)
+    losses = []
+    for i in range(2):
+        params, state, loss = tr.train_step(params, state, dev(xs[i]), dev(ys[i]))
+        losses.append(float(loss))
+    r_c, r_f, r_l = _oracle_steps(cell, filt, xs, ys, geom, 0.01, 2, final_act="sigmoid",
+                                  universe=True)
+    assert rel_l2(losses, r_l) < FWD_TOL
+    assert rel_l2(host(params.cell_params) - cell, r_c - cell) < TRAJ_TOL
+    assert rel_l2(host(params.greens_filters) - filt, r_f - filt) < TRAJ_TOL
 
 
 def test_trainer_graph_replay_matches_eager():
