@@ -88,6 +88,21 @@ int nc_codd_fuse_fwd(void* stream, const nc_chip_desc* chip, const float* cell,
                      float* s_prob, float* border_2d, float* w_pinned);
 
 /*
+ * A step's prologue in one launch: nc_codd_fuse_fwd (without its border_2d and w_pinned
+ * outputs) and nc_inject_roi(B, n_in, inputs, n_roi, src, roi), which are independent.
+ * Same arguments and results as the two calls; src entries must lie in [-1, n_in).
+ * No reference counterpart of its own: it saves one launch of the pre-step work of
+ * propagator.py:252-263 and :344-352.
+ */
+int nc_step_prologue(void* stream, const nc_chip_desc* chip, const float* cell,
+                     const uint8_t* io_mask, const uint8_t* out_weight_mask, int codd_mode,
+                     float inv_tau, float active_threshold, int hard_pin_io, int act,
+                     float neg_slope, int n_port, const int32_t* port_rc, float* w_eff,
+                     float* s_eff, float* b_roi, float* border_patch, float* port_params,
+                     float* s_prob, int B, int n_in, const float* inputs, int n_roi,
+                     const int32_t* src, float* roi);
+
+/*
  * Reverse of nc_codd_fuse_fwd (the autodiff of params.py:220-322 and of the STE forms of
  * params.py:58-80).  Any gradient input may be NULL (zero).  g_s_prob and g_b_full (H,W) are
  * full-grid gradients with respect to s_prob (the reverse of the optional s_prob output) and

@@ -54,16 +54,15 @@ NC_DEV bool in_roi(const nc_chip_desc& c, int r, int col) {
     return r >= c.pad_h && r < c.H - c.pad_h && col >= c.pad_w && col < c.W - c.pad_w;
 }
 
-__global__ void k_codd_fwd(nc_chip_desc c, const float* __restrict__ cell,
-                           const uint8_t* __restrict__ io, const uint8_t* __restrict__ owm,
-                           int mode, float inv_tau, float thr, int hard_pin, int act, float slope,
-                           int P, const int* __restrict__ prc, float* __restrict__ w_eff,
-                           float* __restrict__ s_eff, float* __restrict__ b_roi,
-                           float* __restrict__ patch, float* __restrict__ pp,
-                           float* __restrict__ s_prob, float* __restrict__ border2d,
-                           float* __restrict__ w_pin) {
+NC_DEV void codd_fwd_at(int q, const nc_chip_desc& c, const float* __restrict__ cell,
+                        const uint8_t* __restrict__ io, const uint8_t* __restrict__ owm,
+                        int mode, float inv_tau, float thr, int hard_pin, int act, float slope,
+                        int P, const int* __restrict__ prc, float* __restrict__ w_eff,
+                        float* __restrict__ s_eff, float* __restrict__ b_roi,
+                        float* __restrict__ patch, float* __restrict__ pp,
+                        float* __restrict__ s_prob, float* __restrict__ border2d,
+                        float* __restrict__ w_pin) {
     const int HW = c.H * c.W;
-    const int q = blockIdx.x * blockDim.x + threadIdx.x;
     const float inv_m = 1.0f / (float)c.M;
     if (q < HW) {
         const int r = q / c.W, col = q % c.W;
@@ -92,6 +91,48 @@ __global__ void k_codd_fwd(nc_chip_desc c, const float* __restrict__ cell,
         pp[k] = inv_m * e.w_pinned * (1.0f - e.s_prob);
         pp[P + k] = inv_m * e.s_prob;
         pp[2 * P + k] = e.b;
+    }
+}
+
+__global__ void k_codd_fwd(nc_chip_desc c, const float* __restrict__ cell,
+                           const uint8_t* __restrict__ io, const uint8_t* __restrict__ owm,
+                           int mode, float inv_tau, float thr, int hard_pin, int act, float slope,
+                           int P, const int* __restrict__ prc, float* __restrict__ w_eff,
+                           float* __restrict__ s_eff, float* __restrict__ b_roi,
+                           float* __restrict__ patch, float* __restrict__ pp,
+                           float* __restrict__ s_prob, float* __restrict__ border2d,
+                           float* __restrict__ w_pin) {
+    codd_fwd_at(blockIdx.x * blockDim.x + threadIdx.x, c, cell, io, owm, mode, inv_tau, thr,
+                hard_pin, act, slope, P, prc, w_eff, s_eff, b_roi, patch, pp, s_prob, border2d,
+                w_pin);
+}
+
+struct InjectArgs {
+    int B, n_in, n_roi;
+    const float* in;
+    const int* src;
+    float* roi;
+};
+
+// The step's prologue in one launch: the Codd fusion's H*W + P threads, then one thread per
+// injected cell (k_inject's map), the two being independent.
+__global__ void k_prologue(nc_chip_desc c, const float* __restrict__ cell,
+                           const uint8_t* __restrict__ io, const uint8_t* __restrict__ owm,
+                           int mode, float inv_tau, float thr, int hard_pin, int act, float slope,
+                           int P, const int* __restrict__ prc, float* __restrict__ w_eff,
+                           float* __restrict__ s_eff, float* __restrict__ b_roi,
+                           float* __restrict__ patch, float* __restrict__ pp,
+                           float* __restrict__ s_prob, InjectArgs ia) {
+    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t nc = (size_t)c.H * c.W + P;
+    if (q < nc) {
+        codd_fwd_at((int)q, c, cell, io, owm, mode, inv_tau, thr, hard_pin, act, slope, P, prc,
+                    w_eff, s_eff, b_roi, patch, pp, s_prob, nullptr, nullptr);
+    } else if (q - nc < (size_t)ia.B * ia.n_roi) {
+        const size_t k = q - nc;
+        const int b = (int)(k / ia.n_roi), i = (int)(k % ia.n_roi);
+        const int e = ia.src[i];
+        ia.roi[k] = e >= 0 ? ia.in[(size_t)b * ia.n_in + e] : 0.0f;
     }
 }
 
@@ -679,6 +720,28 @@ int nc_universe_bwd(void* stream, const nc_chip_desc* chip, int B, int G, int va
                            g_s_prob, g_b_full);
         NC_CHECK_LAUNCH();
     }
+    return NC_OK;
+}
+
+int nc_step_prologue(void* stream, const nc_chip_desc* chip, const float* cell,
+                     const uint8_t* io_mask, const uint8_t* out_weight_mask, int codd_mode,
+                     float inv_tau, float active_threshold, int hard_pin_io, int act,
+                     float neg_slope, int n_port, const int32_t* port_rc, float* w_eff,
+                     float* s_eff, float* b_roi, float* border_patch, float* port_params,
+                     float* s_prob, int B, int n_in, const float* inputs, int n_roi,
+                     const int32_t* src, float* roi) {
+    if (!chip_ok(chip) || !cell || !io_mask || !out_weight_mask || codd_mode < 0 ||
+        codd_mode > 3 || act < 0 || act > 5 || n_port < 0 || (n_port > 0 && !port_rc) ||
+        !w_eff || !s_eff || !b_roi || !border_patch || (n_port > 0 && !port_params) || B <= 0 ||
+        n_in <= 0 || n_roi <= 0 || !inputs || !src || !roi)
+        return NC_ERR_INVALID_ARGUMENT;
+    const InjectArgs ia{B, n_in, n_roi, inputs, src, roi};
+    const size_t n = (size_t)chip->H * chip->W + n_port + (size_t)B * n_roi;
+    hipLaunchKernelGGL(k_prologue, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       nc_stream(stream), *chip, cell, io_mask, out_weight_mask, codd_mode,
+                       inv_tau, active_threshold, hard_pin_io, act, neg_slope, n_port, port_rc,
+                       w_eff, s_eff, b_roi, border_patch, port_params, s_prob, ia);
+    NC_CHECK_LAUNCH();
     return NC_OK;
 }
 

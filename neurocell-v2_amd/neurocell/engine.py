@@ -391,13 +391,12 @@ class StepPlan:
                  (ks[1] - 1) // 2, *self.sh_fft, ptr(cell[0]), ptr(self.sh_ghat),
                  ptr(self.cell_s[0]), ptr(self.sh_xhat))
             cell = self.cell_s
-        call("nc_codd_fuse_fwd", s, self.chip, ptr(cell), ptr(self.io_mask), ptr(self.owm), mode,
+        # the Codd fusion and the input injection in one launch
+        call("nc_step_prologue", s, self.chip, ptr(cell), ptr(self.io_mask), ptr(self.owm), mode,
              inv_tau, active_threshold, int(self.hard_pin_io), self.act, self.slope, self.n_pp,
              ptr(self.port_rc), ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
-             ptr(self.patch), ptr(self.pp), ptr(self.s_prob) if self.universe else None, None,
-             None)
-        n_cells = self.x0[0].numel()
-        call("nc_inject_roi", s, B, self.n_in, ptr(x_flat), n_cells, ptr(self.src), ptr(self.x0))
+             ptr(self.patch), ptr(self.pp), ptr(self.s_prob) if self.universe else None, B,
+             self.n_in, ptr(x_flat), self.x0[0].numel(), ptr(self.src), ptr(self.x0))
         # the independent spectra in one call: filter spectra (kernels_greens.py:240-259), the
         # border patch's and the first step's cell spectra
         x0h, x0w = (self.H, self.W) if self.t0_grid else (h, w)

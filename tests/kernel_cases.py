@@ -659,6 +659,20 @@ def case_codd(be, mode="continuous", bbox=None, hard_pin=0, tau=0.1, seed=4):
                                0.6, hard_pin, 1, 0.01, P, be.ptr(prc), be.ptr(we), be.ptr(se),
                                be.ptr(br), be.ptr(patch), be.ptr(pp), be.ptr(sp_), be.ptr(b2d),
                                be.ptr(wp)), "codd")
+    # the fused prologue: the same Codd results bit for bit, and the injection's gather
+    Bi, n_in = 2, 7
+    src = rng.integers(-1, n_in, size=h * w).astype(np.int32)
+    xin = rng.normal(size=(Bi, n_in)).astype(np.float32)
+    srcd, xind, roi = be.put(src, np.int32), be.put(xin), be.zeros((Bi, h * w))
+    f2 = [be.zeros(np.shape(a)) for a in (we, se, br, patch, pp, sp_)]
+    _ok(be, L.nc_step_prologue(s, C.byref(chip), be.ptr(cd), be.ptr(io), be.ptr(owm), mid, it,
+                               0.6, hard_pin, 1, 0.01, P, be.ptr(prc),
+                               *[be.ptr(a) for a in f2], Bi, n_in, be.ptr(xind), h * w,
+                               be.ptr(srcd), be.ptr(roi)), "prologue")
+    pro_ref = np.where(src >= 0, xin[:, np.maximum(src, 0)], 0.0)
+    pro_bad = sum(int((be.get(a) != be.get(b_)).sum())
+                  for a, b_ in zip(f2, (we, se, br, patch, pp, sp_)))
+    pro_bad += int((be.get(roi) != pro_ref).sum())
     sp = O.precompute_step_params(cell, geom, "tanh", bool(hard_pin), bbox, mode, tau, 0.6)
     fwd_got = np.concatenate([be.get(a).ravel() for a in (we, se, br, patch, pp)])
     fwd_ref = np.concatenate([np.ravel(a) for a in (
@@ -687,7 +701,8 @@ def case_codd(be, mode="continuous", bbox=None, hard_pin=0, tau=0.1, seed=4):
         "tanh", bool(hard_pin), bbox, mode, tau, 0.6)
     return {"fwd": rel_l2(fwd_got, fwd_ref), "s_prob": rel_l2(be.get(sp_), sp["s_prob"]),
             "border_2d": rel_l2(be.get(b2d), sp["border_2d"]),
-            "w_pinned": rel_l2(be.get(wp), sp["w_pinned"]), "g_cell": rel_l2(be.get(gcell), ref)}
+            "w_pinned": rel_l2(be.get(wp), sp["w_pinned"]), "g_cell": rel_l2(be.get(gcell), ref),
+            "prologue_mismatch": float(pro_bad)}
 
 
 def case_universe(be, pmode="VALID", bbox=None, fact="tanh", B=3, G=2, seed=10):
