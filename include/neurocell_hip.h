@@ -443,8 +443,9 @@ int nc_port_dense_bwd(void* stream, int n, int final_act, float neg_slope, const
 
 /*
  * pallas_fused_roi_step_epilogue backward rule (kernels_pallas.py:869-1064): writes gz
- * (B,M,h,w), gdb = sum_b gz (M,h,w) when has_border and gdb is not NULL (a caller that forms
- * the border cotangent from the spectra, nc_fftconv_bwd_ex, passes NULL) and gw/gs/gb (h,w).
+ * (B,M,h,w), gdb = sum_b gz (M,h,w) when has_border, exact zeros without the border term
+ * (kernels_pallas.py:1060), when gdb is not NULL (a caller that forms the border
+ * cotangent from the spectra, nc_fftconv_bwd_ex, passes NULL) and gw/gs/gb (h,w).
  * gw/gs/gb are overwritten, or added to when accumulate_params; gdb is overwritten, or added
  * to when accumulate_gdb (a d-step reverse pass sums both over steps).
  */
@@ -490,7 +491,8 @@ int nc_port_fwd(void* stream, int B, int M, int h, int w, int has_border, int fi
 /*
  * Backward of nc_port_fwd (kernels_pallas.py:1350-1504, 1538-1551): dense
  * gz = -rstd*(c1 + zhat*c2) plus rstd*g scattered at the port cells in registers; gdb =
- * sum_b gz when has_border and gdb is not NULL; gdb and g_port_params (3,P) overwritten, or
+ * sum_b gz when has_border (exact zeros without it) and gdb is not NULL; gdb and
+ * g_port_params (3,P) overwritten, or
  * added to when accumulate_params.  With port_params == NULL (standardisation only, kernels_pallas.py:
  * 1350-1504) g_out is the (B,M,P) cotangent of zo and g_port_params is not touched.
  */

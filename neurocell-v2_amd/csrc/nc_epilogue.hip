@@ -241,6 +241,7 @@ __global__ __launch_bounds__(NT) void k_epi_bwd(
 
 // Fixed-order sums over rows, several independent jobs per launch (blockIdx.y = job):
 // job.out[x] = (job.acc ? job.out[x] : 0) + sum over r < job.rows of job.in[r * job.X + x].
+// A job with no input and no rows writes zeros (a cotangent that is identically zero).
 // A workgroup's Q = blockDim.x / 64 waves form Q / qs column groups of 64 columns; the qs
 // waves of a group (qs from the job's row count, about 32 rows per wave) sum fixed contiguous
 // slices of its rows (coalesced) and the qs slice sums are added in fixed order, so the
@@ -271,7 +272,7 @@ __global__ __launch_bounds__(64 * kRedParts) void k_batch_reduce(RedJobs jobs) {
     const int x = blockIdx.x * cols + (w / qs) * 64 + lane;
     const int b0 = (B * q) / qs, b1 = (B * (q + 1)) / qs;
     float s = 0.f;
-    if (x < J.X) {
+    if (x < J.X && b1 > b0) {
         const float* src = J.in + x;
         float a[4] = {0.f, 0.f, 0.f, 0.f};
         int b = b0;
@@ -302,7 +303,7 @@ int launch_batch_reduce(hipStream_t st, const RedJob* jobs, int njobs) {
         return q;
     };
     for (int i = 0; i < njobs; ++i) {
-        if (!jobs[i].in || jobs[i].X <= 0) continue;
+        if (!jobs[i].out || jobs[i].X <= 0 || (!jobs[i].in && jobs[i].rows > 0)) continue;
         pack.j[n++] = jobs[i];
         rmax = std::max(rmax, jobs[i].rows);
     }
@@ -1171,7 +1172,8 @@ static int epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float
     const RedJob jobs[4] = {{own ? pg : nullptr, gw, N, accumulate_params, rows},
                             {own ? pg + RN : nullptr, gs, N, accumulate_params, rows},
                             {own ? pg + 2 * RN : nullptr, gb, N, accumulate_params, rows},
-                            {has_border && gdb ? gz : nullptr, gdb, M * N, accumulate_gdb, B}};
+                            {has_border ? gz : nullptr, gdb, M * N, accumulate_gdb,
+                             has_border ? B : 0}};  // without the border term gdb = 0
     return launch_batch_reduce(st, jobs, 4);
 }
 
@@ -1335,7 +1337,7 @@ static int port_bwd(void* stream, int B, int M, int h, int w, int has_border, in
         {pj ? ppart + ps : nullptr, g_port_params + n_port, n_port, accumulate_params, B},
         {pj ? ppart + 2 * ps : nullptr, g_port_params + 2 * n_port, n_port, accumulate_params,
          B},
-        {has_border && gdb ? gz : nullptr, gdb, M * N, accumulate_params, B}};
+        {has_border ? gz : nullptr, gdb, M * N, accumulate_params, has_border ? B : 0}};
     return launch_batch_reduce(st, jobs, 4);
 }
 

@@ -9,6 +9,8 @@ the reference's custom VJPs), giving gradients w.r.t. ``params.cell_params`` and
 """
 from __future__ import annotations
 
+from collections import OrderedDict
+
 import numpy as np
 import torch
 
@@ -34,16 +36,29 @@ def select_optimal_backend(topology: ChipTopology2D) -> str:
     return "pallas_fused"
 
 
-class _PlanCache:
-    """Static launch plans per (topology, B, sub-ROI, port shapes, activations)."""
+def cropped_bbox(spatial_mask, topology: ChipTopology2D):
+    """The sub-ROI a spatial mask selects (propagator.py:235-241): its ``roi_bbox``, or None
+    without a mask, for a full-ROI mask, and in CIRCULAR mode (the reference ignores the
+    crop there and runs the whole grid)."""
+    if (spatial_mask is None or spatial_mask.is_full_roi
+            or topology.padding_mode == "CIRCULAR"):
+        return None
+    return tuple(int(v) for v in spatial_mask.roi_bbox)
 
-    def __init__(self):
-        self.plans = {}
+
+class _PlanCache:
+    """Static launch plans per (topology, B, sub-ROI, port shapes, activations), least
+    recently used first out.  A plan holds its bucket's whole activation set in HBM, so the
+    cache keeps at most ``capacity`` of them; topologies compare by value."""
+
+    def __init__(self, capacity: int = 16):
+        self.plans = OrderedDict()
+        self.capacity = int(capacity)
 
     def get(self, topology, B, port_shapes, roi_bbox, activate, final_activate, hard_pin_io,
             training, device, gated_filters=False, sharpen=None, universe=False):
         sk = None if sharpen is None else np.asarray(sharpen, np.float32)
-        key = (id(topology), topology, B, tuple(port_shapes), roi_bbox, str(activate),
+        key = (topology, B, tuple(port_shapes), roi_bbox, str(activate),
                str(final_activate), bool(hard_pin_io), bool(training), str(device),
                bool(gated_filters), None if sk is None else (sk.shape, sk.tobytes()),
                bool(universe))
@@ -54,6 +69,10 @@ class _PlanCache:
                                            hard_pin_io=hard_pin_io, training=training,
                                            device=device, gated_filters=gated_filters,
                                            sharpen=sk, universe=universe)
+            while len(self.plans) > self.capacity:
+                self.plans.popitem(last=False)
+        else:
+            self.plans.move_to_end(key)
         return p
 
 
@@ -122,9 +141,7 @@ def propagate_vnn_2d(params, inputs, topology: ChipTopology2D, activate="tanh",
                          f"{SUPPORTED_CODD_MODES}.")
     if not norm:
         raise NeurocellError("norm=False is not part of the MI355X path")
-    roi_bbox = None
-    if spatial_mask is not None and not spatial_mask.is_full_roi:
-        roi_bbox = tuple(int(v) for v in spatial_mask.roi_bbox)
+    roi_bbox = cropped_bbox(spatial_mask, topology)
     x_flat = flatten_inputs(inputs, topology)
     cell, filt = params.cell_params, params.greens_filters
     need_grad = torch.is_grad_enabled() and (cell.requires_grad or filt.requires_grad)

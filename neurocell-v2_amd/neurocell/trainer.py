@@ -30,6 +30,7 @@ import torch
 from ._lib import NeurocellError, call, ptr, stream_ptr
 from .engine import ParamState, StepPlan, TrainState, inv_tau_f32, port_input_shapes
 from .params import VNNParams
+from .propagator import cropped_bbox
 
 BIT_WEIGHTS_U8 = (128, 64, 32, 16, 8, 4, 2, 1)
 
@@ -412,8 +413,7 @@ class VNNTrainer:
 
     def _train(self, params, opt_state, xb, yb, mask_spec, codd_mode, temperature, nb,
                annealed):
-        bbox = None if mask_spec is None or mask_spec.is_full_roi else \
-            tuple(int(v) for v in mask_spec.roi_bbox)
+        bbox = cropped_bbox(mask_spec, self.model.topology) if self.fused else None
         if self.fused:
             codd = self._codd(codd_mode, temperature)
             losses = self._fused_train(params, opt_state, xb, yb, bbox, codd, nb)
@@ -435,8 +435,7 @@ class VNNTrainer:
         nb, B = xb.shape[0], xb.shape[1]
         if self.fused:
             self._check_model()
-            bbox = None if mask_spec is None or mask_spec.is_full_roi else \
-                tuple(int(v) for v in mask_spec.roi_bbox)
+            bbox = cropped_bbox(mask_spec, self.model.topology)
             shapes = port_input_shapes(xb[0], self.model.topology)
             plan = self._plan(B, bbox, False, shapes, params.cell_params.device)
             x = _flat_batches(xb, nb, B)

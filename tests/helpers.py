@@ -43,3 +43,43 @@ def config_geometry(cfg, depth=None, directions=None):
     (orr, oc), osz = cfg.out_port
     return O.Geometry(tuple(cfg.grid), tuple(cfg.kernel), m, d,
                       [("rect", (ir, ic), tuple(isz))], ("rect", (orr, oc), tuple(osz)))
+
+
+def _chunks(B, chunk, threads):
+    if chunk is None:  # small chunks keep the oracle's arrays in cache
+        chunk = max(1, min(32, -(-B // threads)))
+    return [(i, min(B, i + chunk)) for i in range(0, B, chunk)]
+
+
+def oracle_forward_batched(cell, filt, x, geom, chunk=None, threads=8, states=False, **kw):
+    """``oracle.propagate`` over sample chunks on a thread pool (NumPy and scipy.fft release
+    the GIL).  Samples are independent in the forward pass (every standardisation is per
+    (b, m) plane), so the concatenated outputs equal one call on the whole batch.  With
+    ``states`` also returns the step states x_t (t = 0..d-1) as a list of (B, h, w)."""
+    from concurrent.futures import ThreadPoolExecutor
+    from oracle import vnn_oracle as O
+    parts = _chunks(x.shape[0], chunk, threads)
+    with ThreadPoolExecutor(threads) as ex:
+        res = list(ex.map(lambda p: O.propagate(cell, filt, x[p[0]:p[1]], geom, **kw), parts))
+    out = np.concatenate([r[0] for r in res], axis=0)
+    if not states:
+        return out
+    xs = [np.concatenate([r[1]["xs"][t] for r in res], axis=0)
+          for t in range(len(res[0][1]["xs"]))]
+    return out, xs
+
+
+def oracle_vjp_batched(cell, filt, x, geom, g_out, chunk=None, threads=8, **kw):
+    """``oracle.propagate_vjp`` over sample chunks on a thread pool.  The loss is a sum over
+    samples and the parameters are shared, so the parameter gradients of the whole batch are
+    the sums of the chunks' gradients (added in float64)."""
+    from concurrent.futures import ThreadPoolExecutor
+    from oracle import vnn_oracle as O
+    parts = _chunks(x.shape[0], chunk, threads)
+    with ThreadPoolExecutor(threads) as ex:
+        res = list(ex.map(lambda p: O.propagate_vjp(cell, filt, x[p[0]:p[1]], geom,
+                                                    g_out[p[0]:p[1]], **kw), parts))
+    out = np.concatenate([r[0] for r in res], axis=0)
+    gc = np.sum([np.asarray(r[1], np.float64) for r in res], axis=0)
+    gf = np.sum([np.asarray(r[2], np.float64) for r in res], axis=0)
+    return out, gc, gf

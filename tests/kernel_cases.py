@@ -330,7 +330,9 @@ def case_epilogue(be, B=3, M=5, h=10, w=12, act="tanh", has_border=1, seed=2):
     _ok(be, L.nc_epilogue_fwd(s, B, M, h, w, aid, 0.01, has_border, be.ptr(zd), be.ptr(dd),
                               be.ptr(wd), be.ptr(sd), be.ptr(bd), be.ptr(out), be.ptr(mean),
                               be.ptr(rstd), be.ptr(ws), nb), "epi")
-    gz, gdb = be.zeros((B, M, h, w)), be.zeros((M, h, w))
+    # gdb starts non-zero: without the border term the entry point writes exact zeros
+    # (the reference's zeros_like cotangent, unit_milestone6_general_vnn.py:107-110)
+    gz, gdb = be.zeros((B, M, h, w)), be.put(np.full((M, h, w), 7.0, np.float32))
     gw, gs, gb = be.zeros((h, w)), be.zeros((h, w)), be.zeros((h, w))
     _ok(be, L.nc_epilogue_bwd(s, B, M, h, w, aid, 0.01, has_border, be.ptr(zd), be.ptr(dd),
                               be.ptr(wd), be.ptr(sd), be.ptr(bd), be.ptr(mean), be.ptr(rstd),
@@ -361,6 +363,7 @@ def case_epilogue(be, B=3, M=5, h=10, w=12, act="tanh", has_border=1, seed=2):
                                              for i, t in enumerate((gw, gs, gb))))
     for k, a, b in zip(("gz", "gdb", "gw", "gs", "gb"), (gz, gdb, gw, gs, gb), r):
         if k == "gdb" and not has_border:
+            res["gdb_nonzero"] = float((be.get(gdb) != 0.0).sum())
             continue
         res[k] = rel_l2(be.get(a), b)
     return res
@@ -583,8 +586,9 @@ def case_fftconv_circular(be, B=2, M=3, H=16, W=16, kh=5, kw=3, seed=9):
 
 
 def case_port(be, B=3, M=5, h=10, w=12, rows=(2, 3, 4, 2), cols=(5, 5, 5, 5), fact=None,
-              seed=3):
-    """Output-port forward/backward (rect-like and coordinate ports, duplicates included)."""
+              seed=3, has_border=1):
+    """Output-port forward/backward (rect-like and coordinate ports, duplicates included).
+    Without the border term gdb must come back as exact zeros."""
     rng = np.random.default_rng(seed)
     L, s = be.lib, be.stream()
     P = len(rows)
@@ -599,33 +603,38 @@ def case_port(be, B=3, M=5, h=10, w=12, rows=(2, 3, 4, 2), cols=(5, 5, 5, 5), fa
     ws = be.zeros((L.nc_epilogue_workspace_size(B, M, h, w) // 4 + 1,))
     nb = ws.nbytes if hasattr(ws, "nbytes") else ws.numel() * 4
     fid = _abi.ACT_IDS["identity" if fact is None else fact]
-    _ok(be, L.nc_port_fwd(s, B, M, h, w, 1, fid, 0.01, P, be.ptr(idd), be.ptr(zd), be.ptr(dd),
+    hb = int(has_border)
+    dptr = be.ptr(dd) if hb else None
+    _ok(be, L.nc_port_fwd(s, B, M, h, w, hb, fid, 0.01, P, be.ptr(idd), be.ptr(zd), dptr,
                           be.ptr(ppd), be.ptr(out), be.ptr(zo), be.ptr(mean), be.ptr(rstd),
                           be.ptr(pre), be.ptr(ws), nb), "portf")
-    gz, gdb, gpp = be.zeros((B, M, h, w)), be.zeros((M, h, w)), be.zeros((3, P))
-    _ok(be, L.nc_port_bwd(s, B, M, h, w, 1, fid, 0.01, P, be.ptr(idd), be.ptr(zd), be.ptr(dd),
+    gz, gpp = be.zeros((B, M, h, w)), be.zeros((3, P))
+    gdb = be.put(np.full((M, h, w), 7.0, np.float32))
+    _ok(be, L.nc_port_bwd(s, B, M, h, w, hb, fid, 0.01, P, be.ptr(idd), be.ptr(zd), dptr,
                           be.ptr(ppd), be.ptr(zo), be.ptr(mean), be.ptr(rstd), be.ptr(pre),
                           be.ptr(god), be.ptr(gz), be.ptr(gdb), be.ptr(gpp), 0, be.ptr(ws), nb),
         "portb")
     R, Cc = np.array(rows), np.array(cols)
     o_r, aux = O.port_fwd(z, d, R, Cc, (P, 1), pp[0][:, None], pp[1][:, None], pp[2][:, None],
-                          True, fact)
+                          bool(hb), fact)
     r = O.port_bwd(z, d, R, Cc, (P, 1), pp[0][:, None], pp[1][:, None], pp[2][:, None], aux,
-                   go[:, :, None], True, fact)
+                   go[:, :, None], bool(hb), fact)
     g = be.get(gpp)
     # the row-stack variant (padded plane stride), summed by nc_rows_sum: the same reduction
     # over the same rows, so bit for bit the same gradients
     stride = B * P + 7
     prow, gz2, gpp2 = be.zeros((3 * stride,)), be.zeros((B, M, h, w)), be.zeros((3, P))
-    _ok(be, L.nc_port_bwd_parts(s, B, M, h, w, 1, fid, 0.01, P, be.ptr(idd), be.ptr(zd),
-                                be.ptr(dd), be.ptr(ppd), be.ptr(zo), be.ptr(mean), be.ptr(rstd),
+    _ok(be, L.nc_port_bwd_parts(s, B, M, h, w, hb, fid, 0.01, P, be.ptr(idd), be.ptr(zd),
+                                dptr, be.ptr(ppd), be.ptr(zo), be.ptr(mean), be.ptr(rstd),
                                 be.ptr(pre), be.ptr(god), be.ptr(gz2), be.ptr(prow), stride,
                                 be.ptr(ws), nb), "portb_parts")
     a = lambda t, off=0: be.ptr(t).value + 4 * off
     jobs = _abi.rows_jobs(*[(a(prow, i * stride), a(gpp2, i * P), P, 0, B) for i in range(3)])
     _ok(be, L.nc_rows_sum(s, 3, jobs), "rows_sum")
     return {"out": rel_l2(be.get(out), o_r[:, :, 0]), "zo": rel_l2(be.get(zo), aux["zo"][..., 0]),
-            "gz": rel_l2(be.get(gz), r[0]), "gdb": rel_l2(be.get(gdb), r[1]),
+            "gz": rel_l2(be.get(gz), r[0]),
+            ("gdb" if hb else "gdb_nonzero"): (rel_l2(be.get(gdb), r[1]) if hb else
+                                               float((be.get(gdb) != 0.0).sum())),
             "gw_out": rel_l2(g[0], r[2][:, 0]), "gs_out": rel_l2(g[1], r[3][:, 0]),
             "gb_out": rel_l2(g[2], r[4][:, 0]),
             "parts_gz_mismatch": float((be.get(gz2) != be.get(gz)).sum()),
@@ -836,9 +845,11 @@ EPILOGUE_SHAPES = [
 ]
 
 PORT_SHAPES = [
-    (3, 5, 10, 12, (2, 3, 4, 2), (5, 5, 5, 5), None),
-    (2, 16, 40, 50, tuple(range(16, 24)) * 2, (35,) * 8 + (36,) * 8, None),
-    (2, 3, 96, 100, (10, 50, 95), (3, 99, 0), "tanh"),
+    # (B, M, h, w, rows, cols, final activation, has_border)
+    (3, 5, 10, 12, (2, 3, 4, 2), (5, 5, 5, 5), None, 1),
+    (2, 16, 40, 50, tuple(range(16, 24)) * 2, (35,) * 8 + (36,) * 8, None, 1),
+    (2, 3, 96, 100, (10, 50, 95), (3, 99, 0), "tanh", 1),
+    (3, 4, 12, 10, (1, 7, 7), (2, 3, 3), "sigmoid", 0),
 ]
 
 CODD_CASES = [(m, b, hp) for m in O.CODD_MODES for b in (None, (6, 30, 10, 42)) for hp in (0, 1)]

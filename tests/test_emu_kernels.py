@@ -76,10 +76,11 @@ def test_epilogue(be, shape):
 @pytest.mark.parametrize("shape", [
     (2, 3, 10, 12, (2, 3, 4, 2), (5, 5, 5, 5), None),
     (3, 9, 10, 12, (2, 3, 4, 2), (5, 5, 5, 5), "tanh"),  # split port forward, ticket combine
-    (1, 2, 96, 100, (10, 50, 95), (3, 99, 0), "tanh")])
+    (1, 2, 96, 100, (10, 50, 95), (3, 99, 0), "tanh"),
+    (2, 3, 12, 10, (1, 7, 7), (2, 3, 3), "sigmoid", 0)])  # no border term: gdb = 0
 def test_port(be, shape):
-    B, M, h, w, rows, cols, fact = shape
-    _assert_small(case_port(be, B, M, h, w, rows, cols, fact))
+    B, M, h, w, rows, cols, fact, *hb = shape
+    _assert_small(case_port(be, B, M, h, w, rows, cols, fact, has_border=hb[0] if hb else 1))
 
 
 @pytest.mark.parametrize("mode,bbox,hard_pin", CODD_CASES[::3])

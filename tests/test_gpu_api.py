@@ -150,6 +150,100 @@ def test_batched_nchw(padding):
     assert rel_l2(host(z), ref) < FWD_TOL
 
 
+def test_need_dx_false_gives_exact_zero_dx():
+    """unit_kernels_greens.py:151-156: with need_dx=False the cell cotangent is identically
+    zero while the filter gradient still matches the direct correlation's."""
+    from neurocell import conv2d_pruned_rfft_roi_step, hoist_filter_rfft2_nopad
+    x, g, gz, pad = _conv_case(seed=6)
+    fs = (32, 32)
+    res = {}
+    for need in (True, False):
+        xt, gt = dev(x).requires_grad_(), dev(g).requires_grad_()
+        kf = hoist_filter_rfft2_nopad(gt, g.shape[-2:], pad, fs)
+        z = conv2d_pruned_rfft_roi_step(xt, kf, x.shape[-2:], pad, fs, need)
+        z.backward(dev(gz))
+        res[need] = (host(xt.grad), host(gt.grad))
+    with O.precision(np.float64):
+        r_dx, r_dg = O.conv2d_bwd_direct(gz, x, g[:, 0], pad)
+    assert float(np.abs(res[False][0]).max()) == 0.0
+    assert rel_l2(res[True][0], r_dx) < GRAD_TOL
+    assert rel_l2(res[False][1][:, 0], r_dg) < 1e-5
+    assert rel_l2(res[False][1], res[True][1]) < 1e-6
+
+
+def test_no_border_gives_exact_zero_gdb():
+    """unit_milestone6_general_vnn.py:107-110: without the border term (has_border=False)
+    the border cotangent is identically zero, for the hidden epilogue and the port."""
+    from neurocell import pallas_fused_roi_step_epilogue, pallas_standardize_output_port
+    rng = np.random.default_rng(8)
+    B, M, h, w = 3, 4, 16, 20
+    z = rng.normal(size=(B, M, h, w)).astype(np.float32)
+    d = rng.normal(size=(1, M, h, w)).astype(np.float32)
+    ws, ss, bs = (rng.normal(size=(h, w)).astype(np.float32) for _ in range(3))
+    ts = [dev(a).requires_grad_() for a in (z, d, ws, ss, bs)]
+    out = pallas_fused_roi_step_epilogue(*ts, activate="tanh", has_border=False)
+    out.backward(dev(rng.normal(size=(B, h, w)).astype(np.float32)))
+    assert float(ts[1].grad.abs().max()) == 0.0
+    assert float(ts[0].grad.abs().max()) > 0.0
+    zt, dt = dev(z).requires_grad_(), dev(d).requires_grad_()
+    zo = pallas_standardize_output_port(zt, dt, (3, 5), (4, 2), False)
+    zo.backward(dev(rng.normal(size=tuple(zo.shape)).astype(np.float32)))
+    assert float(dt.grad.abs().max()) == 0.0
+    assert float(zt.grad.abs().max()) > 0.0
+
+
+def test_ste_ternary_zero_thresholding_gap():
+    """unit_milestone8_pallas_and_codd.py:240-252 on the device: replacing the raw Codd states
+    by discrete values in each ternary regime (1.0 active, 0.3 passive, -1.0 inactive, from
+    ``threshold_states``) leaves the ste_ternary forward exactly unchanged."""
+    from neurocell import VNNParams, VonNeumannNetwork
+    from neurocell.topology import ChipTopology2D
+    geom, cell, filt, x, _ = alu_case(21, B=8)
+    rng = np.random.default_rng(22)
+    cell[2] = rng.uniform(-1.5, 1.5, size=cell[2].shape).astype(np.float32)
+    model = VonNeumannNetwork(ChipTopology2D.alu_chip(out_width=2))
+    p = VNNParams(dev(cell), dev(filt))
+    out_t = model.apply(p, dev(x), codd_mode="ste_ternary", state_temperature=0.25)
+    roles = VonNeumannNetwork.threshold_states(p.cell_params[2], active_threshold=0.6)
+    one = torch.ones_like(roles)
+    s_disc = torch.where(roles >= 2.0, one, torch.where(roles > 0.0, 0.3 * one, -one))
+    assert set(np.unique(host(s_disc)).tolist()) == {-1.0, np.float32(0.3), 1.0}
+    cell_d = p.cell_params.clone()
+    cell_d[2] = s_disc
+    out_d = model.apply(VNNParams(cell_d, p.greens_filters), dev(x), codd_mode="ste_ternary",
+                        state_temperature=0.25)
+    assert float((out_t - out_d).abs().max()) == 0.0
+    r_out = O.propagate(cell, filt, x, geom, mode="ste_ternary", tau=0.25)[0]
+    assert rel_l2(host(out_t), r_out) < FWD_TOL
+
+
+def test_circular_ignores_adaptive_crop():
+    """propagator.py:235-241: in CIRCULAR mode a spatial mask's crop is ignored and the whole
+    grid runs, through propagate_vnn_2d and through the trainer's evaluation."""
+    from neurocell import VNNParams, VNNTrainer, VonNeumannNetwork, adamw, propagate_vnn_2d
+    from neurocell.topology import ChipTopology2D
+    topo = ChipTopology2D.clp_chip(n=16, padding_mode="CIRCULAR")
+    H, W = topo.grid_shape
+    rng = np.random.default_rng(23)
+    cell = np.stack([rng.normal(0, 0.3, (H, W)), rng.normal(0, 0.1, (H, W)),
+                     rng.normal(0, 1.0, (H, W))]).astype(np.float32)
+    filt = rng.normal(0, 1.0 / 3.0, (1, 1, 3, 3)).astype(np.float32)
+    x = (rng.random((8, 2)) > 0.5).astype(np.float32)
+    p = VNNParams(dev(cell), dev(filt))
+    full = propagate_vnn_2d(p, dev(x), topo)
+    crop = propagate_vnn_2d(p, dev(x), topo, spatial_mask=mask((1, 10, 2, 12)))
+    assert np.array_equal(host(full), host(crop))
+    geom = O.Geometry((H, W), (3, 3), 1, 4, [("coords", list(topo.in_ports[0].coords))],
+                      ("coords", list(topo.out_port.coords)), padding_mode="CIRCULAR")
+    assert rel_l2(host(full), O.propagate(cell, filt, x, geom)[0]) < FWD_TOL
+    model = VonNeumannNetwork(topo)
+    tr = VNNTrainer(model.apply, adamw(0.01), batch_size=8)
+    y = dev(rng.integers(0, 2, size=(1,) + tuple(full.shape)).astype(np.float32))
+    m_full = tr.evaluate_metric(p, dev(x[None]), y)
+    m_crop = tr.evaluate_metric_adaptive(p, dev(x[None]), y, mask((1, 10, 2, 12)))
+    assert float(m_full) == float(m_crop)
+
+
 @pytest.mark.parametrize("mode,bbox", [("continuous", None), ("ste_ternary", CROP),
                                        ("annealed", None)])
 def test_precompute_step_params_autograd(mode, bbox):

@@ -75,10 +75,19 @@ def test_epilogue_alu_batch(be):
     _assert_small(case_epilogue(be, 128, 16, 40, 50, "tanh", 1))
 
 
+@pytest.mark.parametrize("hb", [1, 0])
+def test_epilogue_wide_batch(be, hb):
+    """Config 4's epilogue shape at its benchmark batch: B = 512 >= the wide-batch threshold,
+    so the forward and the backward run one workgroup per sample with all 16 directions in
+    registers (the branch the B <= 128 cases never reach)."""
+    assert be.lib.nc_epilogue_bwd_partials(512, 16, 24, 32) == 512
+    _assert_small(case_epilogue(be, 512, 16, 24, 32, "tanh", hb))
+
+
 @pytest.mark.parametrize("shape", PORT_SHAPES)
 def test_port(be, shape):
-    B, M, h, w, rows, cols, fact = shape
-    _assert_small(case_port(be, B, M, h, w, rows, cols, fact))
+    B, M, h, w, rows, cols, fact, hb = shape
+    _assert_small(case_port(be, B, M, h, w, rows, cols, fact, has_border=hb))
 
 
 @pytest.mark.parametrize("mode,bbox,hard_pin", CODD_CASES)
