@@ -34,6 +34,11 @@ extern "C" {
 #define NC_ERR_INVALID_ARGUMENT (-1)
 #define NC_ERR_UNSUPPORTED (-2)
 #define NC_ERR_WORKSPACE (-3)
+#define NC_ERR_SCRATCH_LIMIT (-4) /* shapes beyond the allocation-free scratch maximum */
+
+/* Bytes of the file-scope device scratch behind the allocation-free entry points (one array
+ * per GPU, held until the process ends). */
+#define NC_NOALLOC_SCRATCH_BYTES (16u << 20)
 
 /* Activation ids: kernels_pallas.py:76-99 (_resolve_activation_spec). */
 #define NC_ACT_IDENTITY 0
@@ -454,6 +459,25 @@ int nc_epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg
                     const float* s_eff, const float* b_roi, const float* mean, const float* rstd,
                     const float* gy, float* gz, float* gdb, float* gw, float* gs, float* gb,
                     int accumulate_params, int accumulate_gdb, void* ws, size_t ws_bytes);
+
+/*
+ * nc_epilogue_bwd without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation).  No counterpart in the reference.  Same arguments (minus ws, ws_bytes) and
+ * results as nc_epilogue_bwd; its scratch is a file-scope device array of
+ * NC_NOALLOC_SCRATCH_BYTES per GPU (16 MiB: the 40x50 ROI at B = 128 needs 11.7 MB, the
+ * 24x32 crop at B = 512 9.0 MB, the 112x112 ROI at B = 64 13.4 MB), so shapes whose
+ * nc_epilogue_workspace_size exceeds it (e.g. 224x224 at B = 32, M = 32: 26.7 MB) return
+ * NC_ERR_SCRATCH_LIMIT.  Runs on the current device; a non-NULL stream must belong to it
+ * (NC_ERR_INVALID_ARGUMENT otherwise).  Calls no allocator.  All calls on one GPU share its
+ * scratch: calls that overlap on one GPU (concurrent streams or host threads) race.
+ */
+int nc_epilogue_bwd_noalloc(void* stream, int B, int M, int h, int w, int act, float neg_slope,
+                            int has_border, const float* z, const float* delta,
+                            const float* w_eff, const float* s_eff, const float* b_roi,
+                            const float* mean, const float* rstd, const float* gy, float* gz,
+                            float* gdb, float* gw, float* gs, float* gb, int accumulate_params,
+                            int accumulate_gdb);
 
 /* The partial rows per parameter plane nc_epilogue_bwd_parts writes at these shapes. */
 int nc_epilogue_bwd_partials(int B, int M, int h, int w);

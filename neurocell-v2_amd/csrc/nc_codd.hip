@@ -560,6 +560,8 @@ const char* nc_strerror(int status) {
         case NC_ERR_INVALID_ARGUMENT: return "invalid argument";
         case NC_ERR_UNSUPPORTED: return "unsupported shape or configuration";
         case NC_ERR_WORKSPACE: return "workspace missing or too small";
+        case NC_ERR_SCRATCH_LIMIT:
+            return "shapes exceed the allocation-free entry point's scratch maximum";
         default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown status";
     }
 }

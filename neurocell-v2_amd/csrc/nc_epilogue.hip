@@ -13,6 +13,7 @@
 // an LDS pixel->slot map, one workgroup per (b, tile).
 // B-reductions (gw/gs/gb, gdb, port parameters) are fixed-order column sums: no atomics.
 #include <algorithm>
+#include <mutex>
 
 #include "nc_common.h"
 
@@ -1185,6 +1186,70 @@ int nc_epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg
     return epilogue_bwd(stream, B, M, h, w, act, neg_slope, has_border, z, delta, w_eff, s_eff,
                         b_roi, mean, rstd, gy, gz, gdb, gw, gs, gb, accumulate_params,
                         accumulate_gdb, nullptr, 0, ws, ws_bytes);
+}
+
+// ----------------------------------------------------------------------------------------
+// Allocation-free variant of nc_epilogue_bwd: its scratch (the per-(group, sample) partial
+// rows and the tile statistics, nc_epilogue_workspace_size bytes) lives in file-scope device
+// memory instead of a caller workspace.  Each GPU holds its own copy of the array from the
+// library's load until the process ends.  The host-side name `scratch` is only a stand-in
+// symbol: its device address is looked up once per device (hipGetSymbolAddress, that device
+// current) and that address is what the kernels receive.  Every call on a GPU shares the
+// GPU's array: calls that overlap on one GPU race.  No kernel here needs the scratch zeroed:
+// every partial row and tile statistic is written before it is read.
+// ----------------------------------------------------------------------------------------
+
+static __device__ __align__(256) unsigned char scratch[NC_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxScratchDevices] = {};
+
+// The current device's address of `scratch`, looked up on its first use on that device.
+int scratch_address(void** addr) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= kMaxScratchDevices) return NC_ERR_UNSUPPORTED;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_addr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        if (!p) return NC_ERR_WORKSPACE;
+        g_scratch_addr[dev] = p;
+    }
+    *addr = g_scratch_addr[dev];
+    return NC_OK;
+}
+
+}  // namespace
+
+int nc_epilogue_bwd_noalloc(void* stream, int B, int M, int h, int w, int act, float neg_slope,
+                            int has_border, const float* z, const float* delta,
+                            const float* w_eff, const float* s_eff, const float* b_roi,
+                            const float* mean, const float* rstd, const float* gy, float* gz,
+                            float* gdb, float* gw, float* gs, float* gb, int accumulate_params,
+                            int accumulate_gdb) {
+    if (B <= 0 || M <= 0 || h <= 0 || w <= 0) return NC_ERR_INVALID_ARGUMENT;
+    const size_t need = nc_epilogue_workspace_size(B, M, h, w);
+    if (need > sizeof(scratch)) return NC_ERR_SCRATCH_LIMIT;
+    if (stream) {  // the stream must belong to the current device, whose scratch is used
+        int sdev = -1, cur = -1;
+        hipError_t e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
+        if (e != hipSuccess) return (int)e;
+        e = hipGetDevice(&cur);
+        if (e != hipSuccess) return (int)e;
+        if (sdev != cur) return NC_ERR_INVALID_ARGUMENT;
+    }
+    void* ws = nullptr;
+    const int rc = scratch_address(&ws);
+    if (rc != NC_OK) return rc;
+    return epilogue_bwd(stream, B, M, h, w, act, neg_slope, has_border, z, delta, w_eff, s_eff,
+                        b_roi, mean, rstd, gy, gz, gdb, gw, gs, gb, accumulate_params,
+                        accumulate_gdb, nullptr, 0, ws, sizeof(scratch));
 }
 
 int nc_epilogue_bwd_parts(void* stream, int B, int M, int h, int w, int act, float neg_slope,

@@ -17,6 +17,8 @@ NC_OK = 0
 NC_ERR_INVALID_ARGUMENT = -1
 NC_ERR_UNSUPPORTED = -2
 NC_ERR_WORKSPACE = -3
+NC_ERR_SCRATCH_LIMIT = -4
+NOALLOC_SCRATCH_BYTES = 16 << 20
 
 ACT_IDS = {"identity": 0, "tanh": 1, "sigmoid": 2, "relu": 3, "leaky_relu": 4, "gelu": 5}
 CODD_IDS = {"continuous": 0, "annealed": 1, "ste_binary": 2, "ste_ternary": 3}
@@ -105,6 +107,8 @@ _SIGS = {
     "nc_epilogue_fwd": (I, [P, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, SZ]),
     "nc_epilogue_bwd": (I, [P, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, P, P, P, P, I,
                             I, P, SZ]),
+    "nc_epilogue_bwd_noalloc": (I, [P, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, P, P,
+                                    P, P, I, I]),
     "nc_epilogue_bwd_partials": (I, [I, I, I, I]),
     "nc_epilogue_bwd_parts": (I, [P, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, P, SZ, P,
                                   SZ]),

@@ -73,6 +73,15 @@ enum { hipFuncAttributeMaxDynamicSharedMemorySize = 8 };
 #define NC_PIN(x) ((void)0)
 #define NC_FENCE() ((void)0)
 inline hipError_t hipFuncSetAttribute(const void*, int, int) { return 0; }
+#define __align__(n) alignas(n)
+#define HIP_SYMBOL(X) X
+inline hipError_t hipGetDevice(int* d) { *d = 0; return 0; }
+inline hipError_t hipStreamGetDevice(hipStream_t, int* d) { *d = 0; return 0; }
+template <typename T>
+inline hipError_t hipGetSymbolAddress(void** p, const T& sym) {
+    *p = (void*)&sym;
+    return 0;
+}
 inline const char* hipGetErrorString(hipError_t e) {
     return e == 1 ? "emulated launch touched LDS past its dynamic allocation" : "emulated";
 }
