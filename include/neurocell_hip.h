@@ -269,6 +269,36 @@ int nc_plane_spectra(void* stream, int fft_h, int fft_w, int n_jobs, const nc_sp
 int nc_spectral_correlate(void* stream, int B, int M, int hout, int wout, int pad_h, int pad_w,
                           int fft_h, int fft_w, const float* xhat, const float* ghat, float* z);
 
+/*
+ * rfft2_pruned (kernels_greens.py:25-44) is nc_plane_spectrum with shift (0, 0): the
+ * half-spectra of real planes zero-padded to the grid.
+ *
+ * irfft2_pruned (kernels_greens.py:47-66): out (nplanes, hout, wout) = irfft2(xhat)[pad_h :
+ * pad_h+hout, pad_w : pad_w+wout] (the window read modulo the grid), xhat (nplanes, fft_h,
+ * fft_w/2+1) complex.  As a real inverse transform does, only the Hermitian parts of the DC
+ * and Nyquist columns enter.  Grids as nc_fftconv_fwd; ws sized by
+ * nc_irfft2_pruned_workspace_size.
+ */
+size_t nc_irfft2_pruned_workspace_size(int nplanes, int fft_h, int fft_w);
+int nc_irfft2_pruned(void* stream, int nplanes, int hout, int wout, int pad_h, int pad_w,
+                     int fft_h, int fft_w, const float* xhat, float* out, void* ws,
+                     size_t ws_bytes);
+
+/*
+ * Elementwise map of nplanes half-spectra (fft_h, fft_w/2+1) complex, any power-of-two grid:
+ * out = phase(shift) * scale * H(conj_in ? conj(in) : in), where H replaces the DC and Nyquist
+ * columns by their Hermitian parts along the column when herm_edges ((v[k] + conj(v[-k]))/2;
+ * out must not alias in then), scale is edge_scale on those two columns and interior_scale
+ * elsewhere, and phase(shift) = W^(kh*shift_h) W^(kw*shift_w), W = exp(-2 pi i / grid) (the
+ * spectrum of the plane circularly shifted by shift).  in == NULL maps the constant 1.
+ * It turns the unshifted Plancherel cotangent into the shifted one of conv2d_roi_rfft_step
+ * (kernels_greens.py:363-400; the padded-gz spectrum is the unpadded one times the phase of
+ * the pad) and gives the adjoints of rfft2_pruned / irfft2_pruned their column weights.
+ */
+int nc_spectrum_map(void* stream, int nplanes, int fft_h, int fft_w, int shift_h, int shift_w,
+                    int herm_edges, float edge_scale, float interior_scale, int conj_in,
+                    const float* in, float* out);
+
 /* Workspace bytes needed by nc_fftconv_bwd for these shapes. */
 size_t nc_fftconv_bwd_workspace_size(int B, int M, int fft_h, int fft_w);
 
@@ -445,6 +475,17 @@ int nc_port_dense_fwd(void* stream, int n, int G, int final_act, float neg_slope
                       const float* parts, float* out, float* pre);
 int nc_port_dense_bwd(void* stream, int n, int final_act, float neg_slope, const float* pre,
                       const float* g_out, float* g_pre);
+
+/*
+ * standardize_spatial_nchw (epilogue.py:20-25, jax.nn.standardize over the plane axes):
+ * out = (x - mean) * rstd per plane, nplanes planes of n contiguous floats, with two-pass
+ * population statistics and rstd = 1/sqrt(var + 1e-5) saved (nplanes each).  The reverse:
+ * gx = rstd * (g - mean(g) - zhat * mean(g * zhat)), zhat recomputed from x, mean, rstd.
+ */
+int nc_standardize_fwd(void* stream, int nplanes, int n, const float* x, float* out,
+                       float* mean, float* rstd);
+int nc_standardize_bwd(void* stream, int nplanes, int n, const float* x, const float* mean,
+                       const float* rstd, const float* g, float* gx);
 
 /*
  * pallas_fused_roi_step_epilogue backward rule (kernels_pallas.py:869-1064): writes gz

@@ -1189,6 +1189,88 @@ int nc_epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float neg
 }
 
 // ----------------------------------------------------------------------------------------
+// Plain per-plane standardisation (epilogue.py:20-25 standardize_spatial_nchw) and its
+// reverse: one 256-thread workgroup per (b, m) plane, two-pass population statistics with
+// eps = 1e-5 inside the square root, as every epilogue kernel here; the reverse recomputes
+// zhat from the saved (mean, rstd).
+// ----------------------------------------------------------------------------------------
+
+namespace {
+
+constexpr int kStdNT = 256;
+
+__global__ __launch_bounds__(kStdNT) void k_std_fwd(int n, const float* __restrict__ x,
+                                                    float* __restrict__ out,
+                                                    float* __restrict__ mean,
+                                                    float* __restrict__ rstd) {
+    __shared__ float red[2 * (kStdNT / NC_WAVE) + 2];
+    const size_t base = (size_t)blockIdx.x * n;
+    const float* xp = x + base;
+    float v[1] = {0.0f};
+    for (int i = threadIdx.x; i < n; i += kStdNT) v[0] += xp[i];
+    block_sum<1, kStdNT>(v, red);
+    const float inv_n = 1.0f / (float)n;
+    const float mu = v[0] * inv_n;
+    v[0] = 0.0f;
+    for (int i = threadIdx.x; i < n; i += kStdNT) {
+        const float d = xp[i] - mu;
+        v[0] = fmaf(d, d, v[0]);
+    }
+    block_sum<1, kStdNT>(v, red);
+    const float r = 1.0f / sqrtf(v[0] * inv_n + 1e-5f);
+    for (int i = threadIdx.x; i < n; i += kStdNT) out[base + i] = (xp[i] - mu) * r;
+    if (threadIdx.x == 0) {
+        mean[blockIdx.x] = mu;
+        rstd[blockIdx.x] = r;
+    }
+}
+
+// gx = rstd * (g - mean(g) - zhat * mean(g * zhat)), zhat = (x - mean) * rstd.
+__global__ __launch_bounds__(kStdNT) void k_std_bwd(int n, const float* __restrict__ x,
+                                                    const float* __restrict__ mean,
+                                                    const float* __restrict__ rstd,
+                                                    const float* __restrict__ g,
+                                                    float* __restrict__ gx) {
+    __shared__ float red[2 * (kStdNT / NC_WAVE) + 4];
+    const size_t base = (size_t)blockIdx.x * n;
+    const float mu = mean[blockIdx.x], r = rstd[blockIdx.x];
+    float v[2] = {0.0f, 0.0f};
+    for (int i = threadIdx.x; i < n; i += kStdNT) {
+        const float gi = g[base + i];
+        v[0] += gi;
+        v[1] = fmaf(gi, (x[base + i] - mu) * r, v[1]);
+    }
+    block_sum<2, kStdNT>(v, red);
+    const float inv_n = 1.0f / (float)n;
+    const float c1 = v[0] * inv_n, c2 = v[1] * inv_n;
+    for (int i = threadIdx.x; i < n; i += kStdNT) {
+        const float zh = (x[base + i] - mu) * r;
+        gx[base + i] = r * (g[base + i] - c1 - zh * c2);
+    }
+}
+
+}  // namespace
+
+int nc_standardize_fwd(void* stream, int nplanes, int n, const float* x, float* out,
+                       float* mean, float* rstd) {
+    if (nplanes <= 0 || n <= 0 || !x || !out || !mean || !rstd) return NC_ERR_INVALID_ARGUMENT;
+    hipLaunchKernelGGL(k_std_fwd, dim3(nplanes), dim3(kStdNT), 0, nc_stream(stream), n, x, out,
+                       mean, rstd);
+    NC_CHECK_LAUNCH();
+    return NC_OK;
+}
+
+int nc_standardize_bwd(void* stream, int nplanes, int n, const float* x, const float* mean,
+                       const float* rstd, const float* g, float* gx) {
+    if (nplanes <= 0 || n <= 0 || !x || !mean || !rstd || !g || !gx)
+        return NC_ERR_INVALID_ARGUMENT;
+    hipLaunchKernelGGL(k_std_bwd, dim3(nplanes), dim3(kStdNT), 0, nc_stream(stream), n, x, mean,
+                       rstd, g, gx);
+    NC_CHECK_LAUNCH();
+    return NC_OK;
+}
+
+// ----------------------------------------------------------------------------------------
 // Allocation-free variant of nc_epilogue_bwd: its scratch (the per-(group, sample) partial
 // rows and the tile statistics, nc_epilogue_workspace_size bytes) lives in file-scope device
 // memory instead of a caller workspace.  Each GPU holds its own copy of the array from the

@@ -1487,6 +1487,52 @@ size_t launch_ws(int B, int M) {
 
 }  // namespace
 
+namespace {
+
+// Elementwise map of nplanes (FH, FWh+1) half-spectra (FWh = FW/2): conjugate the input
+// (conj_in), replace the DC and Nyquist columns by their Hermitian parts along the column
+// (herm: (v[kh] + conj(v[-kh])) / 2), scale the edge columns by `edge` and the others by
+// `interior`, and multiply by the phase ramp W^(kh*sh) W^(kw*sw), W = exp(-2 pi i / grid)
+// (the spectrum of the plane circularly shifted by (sh, sw)).  in == NULL maps the constant
+// spectrum 1.  One thread per bin.
+__global__ __launch_bounds__(256) void k_spectrum_map(int nplanes, int FH, int FWh, int sh,
+                                                      int sw, int herm, float edge,
+                                                      float interior, int conj_in,
+                                                      const cpx* in, cpx* out) {
+    const int SP = FWh + 1, F = FH * SP;
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)nplanes * F) return;
+    const size_t p = i / F;
+    const int e = (int)(i - p * F), kh = e / SP, kw = e - kh * SP;
+    const bool ec = kw == 0 || kw == FWh;
+    cpx v = in ? in[i] : cmk(1.0f, 0.0f);
+    if (conj_in) v.y = -v.y;
+    if (herm && ec && in) {
+        cpx m = in[p * F + (size_t)((FH - kh) & (FH - 1)) * SP + kw];
+        if (conj_in) m.y = -m.y;
+        v = cmk(0.5f * (v.x + m.x), 0.5f * (v.y - m.y));
+    }
+    v = cscale(v, ec ? edge : interior);
+    if (sh | sw) {
+        // exact integer phase indices; the angles are exact binary fractions of pi
+        const int a = (int)(((long long)kh * sh) & (FH - 1));
+        const int b = (int)(((long long)kw * sw) & (2 * FWh - 1));
+        float s1, c1, s2, c2;
+        sincospif(-2.0f * (float)a / (float)FH, &s1, &c1);
+        sincospif(-(float)b / (float)FWh, &s2, &c2);
+        v = cmul(v, cmk(c1 * c2 - s1 * s2, s1 * c2 + c1 * s2));
+    }
+    out[i] = v;
+}
+
+bool any_pow2(int n) { return n >= 2 && n <= 4096 && (n & (n - 1)) == 0; }
+
+size_t spec_bytes(int nplanes, int fh, int fw) {
+    return ((size_t)nplanes * fh * (fw / 2 + 1) * sizeof(cpx) + 255) / 256 * 256;
+}
+
+}  // namespace
+
 extern "C" {
 
 int nc_filter_spectrum_fwd(void* stream, int M, int kh, int kw, int fft_h, int fft_w,
@@ -1852,6 +1898,47 @@ int nc_fftconv_bwd_hat(void* stream, int M, int hin, int win, int pad_h, int pad
     NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);
 #undef NC_CALL
     return NC_ERR_UNSUPPORTED;
+}
+
+int nc_spectrum_map(void* stream, int nplanes, int fft_h, int fft_w, int shift_h, int shift_w,
+                    int herm_edges, float edge_scale, float interior_scale, int conj_in,
+                    const float* in, float* out) {
+    if (nplanes <= 0 || !any_pow2(fft_h) || !any_pow2(fft_w) || shift_h < 0 || shift_w < 0 ||
+        shift_h >= fft_h || shift_w >= fft_w || !out || (herm_edges && in == out))
+        return NC_ERR_INVALID_ARGUMENT;
+    const size_t n = (size_t)nplanes * fft_h * (fft_w / 2 + 1);
+    hipLaunchKernelGGL(k_spectrum_map, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       nc_stream(stream), nplanes, fft_h, fft_w / 2, shift_h, shift_w,
+                       herm_edges, edge_scale, interior_scale, conj_in,
+                       reinterpret_cast<const cpx*>(in), reinterpret_cast<cpx*>(out));
+    NC_CHECK_LAUNCH();
+    return NC_OK;
+}
+
+size_t nc_irfft2_pruned_workspace_size(int nplanes, int fft_h, int fft_w) {
+    if (nplanes <= 0 || fft_h <= 0 || fft_w <= 0) return 0;
+    return spec_bytes(nplanes, fft_h, fft_w) + spec_bytes(1, fft_h, fft_w);
+}
+
+int nc_irfft2_pruned(void* stream, int nplanes, int hout, int wout, int pad_h, int pad_w,
+                     int fft_h, int fft_w, const float* xhat, float* out, void* ws,
+                     size_t ws_bytes) {
+    int rc = fftconv_check(nplanes, 1, 1, 1, hout, wout, pad_h, pad_w, fft_h, fft_w);
+    if (rc != NC_OK) return rc;
+    if (!xhat || !out) return NC_ERR_INVALID_ARGUMENT;
+    if (!ws || ws_bytes < nc_irfft2_pruned_workspace_size(nplanes, fft_h, fft_w))
+        return NC_ERR_WORKSPACE;
+    // the Hermitian parts of the edge columns (what a real inverse keeps of them), then the
+    // correlation of those spectra with the constant spectrum 1 over the output window
+    float* proj = reinterpret_cast<float*>(ws);
+    float* ones = reinterpret_cast<float*>(static_cast<char*>(ws) +
+                                           spec_bytes(nplanes, fft_h, fft_w));
+    rc = nc_spectrum_map(stream, nplanes, fft_h, fft_w, 0, 0, 1, 1.0f, 1.0f, 0, xhat, proj);
+    if (rc != NC_OK) return rc;
+    rc = nc_spectrum_map(stream, 1, fft_h, fft_w, 0, 0, 0, 1.0f, 1.0f, 0, nullptr, ones);
+    if (rc != NC_OK) return rc;
+    return nc_spectral_correlate(stream, nplanes, 1, hout, wout, pad_h, pad_w, fft_h, fft_w,
+                                 proj, ones, out);
 }
 
 }  // extern "C"

@@ -12,15 +12,18 @@ from .topology import ChipTopology2D, CoordinatePortSpec, PortSpec
 from .params import (STATE_ACTIVE, STATE_ACTIVE_VALUE, STATE_SIGNAL, STATE_SIGNAL_VALUE,
                      SUPPORTED_CODD_MODES, PrecomputedStepParams, VNNParams,
                      compute_codd_state_probs, init_vnn_params, precompute_step_params)
-from .ops import (conv2d_batched_nchw, conv2d_hybrid_nopad_roi_step, conv2d_pruned_rfft_roi_step,
-                  conv2d_small_kernel_roi_step, fused_output_port_epilogue,
-                  fused_roi_step_epilogue, hoist_filter_rfft2_nopad,
-                  hoist_filter_rfft2_zero_nopad, is_supported_pallas_activation,
+from .ops import (conv2d_batched_nchw, conv2d_grouped_filter_grad, conv2d_hybrid_nopad_roi_step,
+                  conv2d_hybrid_roi_step, conv2d_pruned_rfft_roi_step, conv2d_roi_rfft_step,
+                  conv2d_small_kernel_roi_step, conv2d_valid_rfft_precomputed,
+                  fused_output_port_epilogue, fused_roi_epilogue, fused_roi_step_epilogue,
+                  hoist_filter_rfft2, hoist_filter_rfft2_nopad, hoist_filter_rfft2_zero_fwd,
+                  hoist_filter_rfft2_zero_nopad, irfft2_pruned, is_supported_pallas_activation,
                   pallas_fused_output_port_epilogue, pallas_fused_roi_step_epilogue,
                   pallas_standardize_output_port, precompute_filter_rfft2,
-                  rfft2_unshifted_filter_grad_to_oihw)
-from .propagator import (SUPPORTED_BACKENDS, inject_inputs_roi_2d, propagate_vnn_2d,
-                         select_optimal_backend)
+                  rfft2_filter_grad_to_oihw, rfft2_pruned, rfft2_unshifted_filter_grad_to_oihw,
+                  standardize_spatial_nchw)
+from .propagator import (SUPPORTED_BACKENDS, inject_inputs_2d, inject_inputs_roi_2d,
+                         propagate_vnn_2d, select_optimal_backend)
 from .adaptive_mask import (AdaptiveMaskSpec, compute_adaptive_spatial_mask,
                             estimate_effective_filter_radii)
 from .model import VonNeumannNetwork
@@ -37,13 +40,18 @@ __all__ = [
     "STATE_ACTIVE", "STATE_SIGNAL", "STATE_ACTIVE_VALUE", "STATE_SIGNAL_VALUE",
     "SUPPORTED_CODD_MODES", "VNNParams", "PrecomputedStepParams", "compute_codd_state_probs",
     "init_vnn_params", "precompute_step_params",
-    "precompute_filter_rfft2", "rfft2_unshifted_filter_grad_to_oihw", "conv2d_batched_nchw",
+    "rfft2_pruned", "irfft2_pruned", "conv2d_grouped_filter_grad", "conv2d_batched_nchw",
+    "precompute_filter_rfft2", "rfft2_filter_grad_to_oihw", "hoist_filter_rfft2",
+    "conv2d_roi_rfft_step", "conv2d_valid_rfft_precomputed", "hoist_filter_rfft2_zero_fwd",
+    "conv2d_hybrid_roi_step", "rfft2_unshifted_filter_grad_to_oihw",
     "is_supported_pallas_activation", "pallas_fused_roi_step_epilogue",
     "pallas_standardize_output_port", "pallas_fused_output_port_epilogue",
     "hoist_filter_rfft2_nopad", "hoist_filter_rfft2_zero_nopad", "conv2d_hybrid_nopad_roi_step",
     "conv2d_small_kernel_roi_step", "conv2d_pruned_rfft_roi_step",
-    "fused_roi_step_epilogue", "fused_output_port_epilogue",
-    "SUPPORTED_BACKENDS", "select_optimal_backend", "inject_inputs_roi_2d", "propagate_vnn_2d",
+    "standardize_spatial_nchw", "fused_roi_step_epilogue", "fused_roi_epilogue",
+    "fused_output_port_epilogue",
+    "SUPPORTED_BACKENDS", "select_optimal_backend", "inject_inputs_2d", "inject_inputs_roi_2d",
+    "propagate_vnn_2d",
     "AdaptiveMaskSpec", "estimate_effective_filter_radii", "compute_adaptive_spatial_mask",
     "VonNeumannNetwork",
     "ALUDeviceDataset", "generate_arithmetic", "generate_arithmetic_logic",

@@ -95,6 +95,11 @@ _SIGS = {
     "nc_fftconv_epilogue_partials": (I, [I, I, I, I, I, I]),
     "nc_fftconv_epilogue_fwd": (I, [P, I, I, I, I, I, I, I, I, P, P, I, F, P, P, P, P, P, P, P,
                                     P, SZ]),
+    "nc_irfft2_pruned_workspace_size": (SZ, [I, I, I]),
+    "nc_irfft2_pruned": (I, [P, I, I, I, I, I, I, I, P, P, P, SZ]),
+    "nc_spectrum_map": (I, [P, I, I, I, I, I, I, F, F, I, P, P]),
+    "nc_standardize_fwd": (I, [P, I, I, P, P, P, P]),
+    "nc_standardize_bwd": (I, [P, I, I, P, P, P, P, P]),
     "nc_fftconv_bwd_workspace_size": (SZ, [I, I, I, I]),
     "nc_fftconv_bwd": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, I, P, P, I, I, P, SZ]),
     "nc_fftconv_bwd_ex": (I, [P, I, I, I, I, I, I, I, I, I, I, P, P, P, I, P, P, I, I, P, I, P,

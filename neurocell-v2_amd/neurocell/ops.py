@@ -22,6 +22,20 @@ conv2d_hybrid_nopad_roi_step :1634-1697    ``conv2d_hybrid_nopad_roi_step``
 conv2d_small_kernel_roi_step :1700-1756    ``conv2d_small_kernel_roi_step``
 conv2d_batched_nchw greens:177-217         ``conv2d_batched_nchw`` (VALID / SAME, via the
                                              spectral correlation)
+rfft2_pruned / irfft2_pruned greens:25-66  ``rfft2_pruned`` (nc_plane_spectrum),
+                                             ``irfft2_pruned`` (nc_irfft2_pruned); each the
+                                             other's adjoint up to column weights
+conv2d_grouped_filter_grad greens:84-123   ``conv2d_grouped_filter_grad`` (the Plancherel
+                                             dG: nc_fftconv_bwd + nc_filter_spectrum_bwd)
+rfft2_filter_grad_to_oihw greens:262-275   ``rfft2_filter_grad_to_oihw``
+hoist_filter_rfft2 greens:278-313          ``hoist_filter_rfft2`` (bwd without a roll)
+conv2d_roi_rfft_step greens:316-400        ``conv2d_roi_rfft_step`` (shifted cotangent:
+                                             nc_spectrum_map of the unshifted one)
+conv2d_valid_rfft_precomputed :403-425     ``conv2d_valid_rfft_precomputed``
+hoist_filter_rfft2_zero_fwd :428-465       ``hoist_filter_rfft2_zero_fwd``
+conv2d_hybrid_roi_step greens:468-551      ``conv2d_hybrid_roi_step``
+standardize_spatial_nchw epilogue.py:20-25 ``standardize_spatial_nchw`` (nc_standardize_*)
+fused_roi_epilogue epilogue.py:59-79       ``fused_roi_epilogue``
 =========================================  ===============================================
 
 Complex spectra are complex64 tensors (interleaved re/im, the C ABI's layout).  Autograd
@@ -270,17 +284,29 @@ def precompute_filter_rfft2(filters_oihw, fft_shape=(64, 64)):
     return out
 
 
+def _filter_grad(g, kernel_size, shift, fft_shape, conj):
+    """flip(crop(roll(irfft2(conj? conj(g) : g), shift))) -> (M, 1, Kh, Kw).  The spectrum is
+    first reduced to what a real inverse transform keeps of it (the Hermitian parts of its DC
+    and Nyquist columns), so any complex cotangent gives NumPy's / JAX's irfft2 result."""
+    _spec_ok(fft_shape)
+    g = g.contiguous()
+    fh, fw = (int(v) for v in fft_shape)
+    M = g.shape[0]
+    kh, kw = kernel_size
+    t = torch.empty_like(g)
+    call("nc_spectrum_map", stream_ptr(), M, fh, fw, 0, 0, 1, 1.0, 1.0, int(conj), ptr(g),
+         ptr(t))
+    out = torch.empty(M, 1, kh, kw, device=g.device, dtype=torch.float32)
+    call("nc_filter_spectrum_bwd", stream_ptr(), M, kh, kw, fh, fw, int(shift[0]) % fh,
+         int(shift[1]) % fw, ptr(t), ptr(out), 0, 0)
+    return out
+
+
 def rfft2_unshifted_filter_grad_to_oihw(grad_ker_freq_unshifted_mhw, kernel_size=(23, 13),
                                         pad_hw=(11, 6), fft_shape=(64, 64), _torch_conj=False):
     """kernels_pallas.py:1558-1579: (M, Fh, Fw/2+1) complex cotangent -> (M, 1, Kh, Kw)."""
-    _spec_ok(fft_shape)
-    g = grad_ker_freq_unshifted_mhw.contiguous()
-    M = g.shape[0]
-    kh, kw = kernel_size
-    out = torch.empty(M, 1, kh, kw, device=g.device, dtype=torch.float32)
-    call("nc_filter_spectrum_bwd", stream_ptr(), M, kh, kw, fft_shape[0], fft_shape[1],
-         int(pad_hw[0]), int(pad_hw[1]), ptr(g), ptr(out), 0, int(_torch_conj))
-    return out
+    return _filter_grad(grad_ker_freq_unshifted_mhw, kernel_size, pad_hw, fft_shape,
+                        _torch_conj)
 
 
 class _HoistNopad(torch.autograd.Function):
@@ -314,10 +340,12 @@ def hoist_filter_rfft2_zero_nopad(filters_oihw, kernel_size=(23, 13), pad_hw=(11
 
 class _PrunedConv(torch.autograd.Function):
     """conv2d_pruned_rfft_roi_step: z = irfft2(rfft2(x) * ker_freq) cropped at pad_hw;
-    residuals (cell_freq, ker_freq); cotangents (g_cells, g_ker_freq_unshifted)."""
+    residuals (cell_freq, ker_freq); cotangents (g_cells, g_ker_freq_unshifted).  With
+    ``shifted`` the ker_freq cotangent is conv2d_roi_rfft_step's (gz zero-padded to its window
+    before the transform), the unshifted one times the phase of the pad."""
 
     @staticmethod
-    def forward(ctx, x, ker_freq, roi_shape, pad_hw, fft_shape, need_dx):
+    def forward(ctx, x, ker_freq, roi_shape, pad_hw, fft_shape, need_dx, shifted=False):
         _spec_ok(fft_shape)
         x = _f32(x)
         kf = ker_freq.contiguous()
@@ -330,13 +358,14 @@ class _PrunedConv(torch.autograd.Function):
         call("nc_fftconv_fwd", stream_ptr(), B, M, hin, win, hout, wout, int(pad_hw[0]),
              int(pad_hw[1]), fft_shape[0], fft_shape[1], ptr(x), ptr(kf), ptr(z), ptr(xhat))
         ctx.save_for_backward(xhat, kf)
-        ctx.args = (B, M, hin, win, hout, wout, tuple(pad_hw), tuple(fft_shape), bool(need_dx))
+        ctx.args = (B, M, hin, win, hout, wout, tuple(pad_hw), tuple(fft_shape), bool(need_dx),
+                    bool(shifted))
         return z
 
     @staticmethod
     def backward(ctx, gz):
         xhat, kf = ctx.saved_tensors
-        B, M, hin, win, hout, wout, pad, fs, need_dx = ctx.args
+        B, M, hin, win, hout, wout, pad, fs, need_dx, shifted = ctx.args
         dev = xhat.device
         dx = torch.zeros(B, hin, win, device=dev, dtype=torch.float32)
         dkf = torch.empty_like(kf)
@@ -345,7 +374,12 @@ class _PrunedConv(torch.autograd.Function):
         call("nc_fftconv_bwd", stream_ptr(), B, M, hin, win, hout, wout, pad[0], pad[1], fs[0],
              fs[1], ptr(_f32(gz)), ptr(xhat), ptr(kf), int(need_dx),
              ptr(dx) if need_dx else None, ptr(dkf), 0, 1, ptr(ws), ws.numel() * 4)
-        return dx, dkf, None, None, None, None
+        if shifted:
+            # rfft2(pad(gz)) = rfft2(gz) * W^(k.pad); in the conjugate (autograd) convention
+            # the cotangent takes the conjugate phase, W^(-k.pad)
+            call("nc_spectrum_map", stream_ptr(), M, fs[0], fs[1], (-pad[0]) % fs[0],
+                 (-pad[1]) % fs[1], 0, 1.0, 1.0, 0, ptr(dkf), ptr(dkf))
+        return dx, dkf, None, None, None, None, None
 
 
 def conv2d_pruned_rfft_roi_step(roi_cells_bhw, ker_freq_mhw, roi_shape=(40, 50), pad_hw=(11, 6),
@@ -407,3 +441,258 @@ def conv2d_batched_nchw(cells_nchw, filters_oihw, padding="VALID", **unused):
     if padding == "SAME":
         return conv2d_small_kernel_roi_step(x, filters_oihw, ((kh - 1) // 2, (kw - 1) // 2))
     raise NeurocellError(f"padding {padding!r} is not supported")
+
+
+# ------------------------------------------------------------------ kernels_greens.py operators
+
+def _planes(shape):
+    n = 1
+    for v in shape:
+        n *= int(v)
+    return n
+
+
+def _grid_for(h: int, w: int):
+    """The smallest supported spectral grid holding an h x w linear correlation support."""
+    gh, gw = max(16, _npow2(h)), max(16, _npow2(w))
+    if gh <= 64 and gw <= 64:
+        return gh, gw
+    gh, gw = max(64, gh), max(64, gw)
+    if gh > 256 or gw > 256:
+        raise NeurocellError(f"a {h}x{w} correlation support exceeds the 256x256 grid")
+    return gh, gw
+
+
+class _Rfft2(torch.autograd.Function):
+    """rfft2_pruned: half-spectra of the real planes zero-padded to the grid.  Its adjoint
+    (the autograd convention, dL/dRe + i dL/dIm) is Re sum over the half-spectrum of
+    g e^{+i theta}: N * irfft2 of g with the interior columns halved (and the edge columns'
+    Hermitian parts, which is all a real inverse keeps of them)."""
+
+    @staticmethod
+    def forward(ctx, x, fft_shape):
+        _spec_ok(fft_shape)
+        x = _f32(x)
+        fh, fw = (int(v) for v in fft_shape)
+        h, w = x.shape[-2:]
+        n = _planes(x.shape[:-2])
+        out = torch.empty(*x.shape[:-2], fh, fw // 2 + 1, device=x.device,
+                          dtype=torch.complex64)
+        call("nc_plane_spectrum", stream_ptr(), n, h, w, fh, fw, 0, 0, ptr(x), ptr(out))
+        ctx.args = (tuple(x.shape), (fh, fw))
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        shape, (fh, fw) = ctx.args
+        n, N = _planes(shape[:-2]), float(fh * fw)
+        g = g.contiguous()
+        t = torch.empty_like(g)
+        call("nc_spectrum_map", stream_ptr(), n, fh, fw, 0, 0, 1, N, 0.5 * N, 0, ptr(g), ptr(t))
+        gx = torch.empty(shape, device=g.device, dtype=torch.float32)
+        ws = _ws(lib().nc_irfft2_pruned_workspace_size(n, fh, fw), g.device)
+        call("nc_irfft2_pruned", stream_ptr(), n, shape[-2], shape[-1], 0, 0, fh, fw, ptr(t),
+             ptr(gx), ptr(ws), ws.numel() * 4)
+        return gx, None
+
+
+def rfft2_pruned(x, fft_shape=(64, 64)):
+    """kernels_greens.py:25-44: rfft2 of the (..., H_in, W_in) planes zero-padded to
+    ``fft_shape`` (H_in <= Fh, W_in <= Fw), as (..., Fh, Fw/2+1) complex64; differentiable."""
+    return _Rfft2.apply(x, tuple(fft_shape))
+
+
+class _Irfft2(torch.autograd.Function):
+    """irfft2_pruned; its adjoint is (c_k / N) rfft2 of the cotangent placed at the window,
+    c_k = 1 on the DC and Nyquist columns and 2 elsewhere."""
+
+    @staticmethod
+    def forward(ctx, xf, roi_shape, pad_hw, fft_shape):
+        _spec_ok(fft_shape)
+        if xf.dtype != torch.complex64 or not xf.is_cuda:
+            raise NeurocellError("expected a complex64 device tensor")
+        xf = xf.contiguous()
+        fh, fw = (int(v) for v in fft_shape)
+        if tuple(xf.shape[-2:]) != (fh, fw // 2 + 1):
+            raise NeurocellError(f"spectrum shape {tuple(xf.shape[-2:])} does not match the "
+                                 f"grid {fh}x{fw}")
+        rh, rw = (int(v) for v in roi_shape)
+        ph, pw = (int(v) for v in pad_hw)
+        n = _planes(xf.shape[:-2])
+        out = torch.empty(*xf.shape[:-2], rh, rw, device=xf.device, dtype=torch.float32)
+        ws = _ws(lib().nc_irfft2_pruned_workspace_size(n, fh, fw), xf.device)
+        call("nc_irfft2_pruned", stream_ptr(), n, rh, rw, ph, pw, fh, fw, ptr(xf), ptr(out),
+             ptr(ws), ws.numel() * 4)
+        ctx.args = (tuple(xf.shape[:-2]), (rh, rw), (ph, pw), (fh, fw))
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        lead, (rh, rw), (ph, pw), (fh, fw) = ctx.args
+        n, N = _planes(lead), float(fh * fw)
+        gx = torch.empty(*lead, fh, fw // 2 + 1, device=g.device, dtype=torch.complex64)
+        call("nc_plane_spectrum", stream_ptr(), n, rh, rw, fh, fw, ph, pw, ptr(_f32(g)),
+             ptr(gx))
+        call("nc_spectrum_map", stream_ptr(), n, fh, fw, 0, 0, 0, 1.0 / N, 2.0 / N, 0, ptr(gx),
+             ptr(gx))
+        return gx, None, None, None
+
+
+def irfft2_pruned(x_freq, roi_shape, pad_hw, fft_shape=(64, 64)):
+    """kernels_greens.py:47-66: irfft2 on ``fft_shape`` sliced to
+    [..., r_h : r_h + roi_h, r_w : r_w + roi_w]; differentiable."""
+    return _Irfft2.apply(x_freq, tuple(roi_shape), tuple(pad_hw), tuple(fft_shape))
+
+
+def _select_batch_groups(batch_size: int, max_groups: int = 8) -> int:
+    """kernels_greens.py:69-81 (kept for API compatibility: the MI355X filter gradient sums
+    every sample in one fixed-order frequency-domain reduction, so no grouping is needed)."""
+    eff = min(batch_size, max_groups)
+    if batch_size >= 16:
+        eff = min(eff, max(1, batch_size // 16))
+    for g in range(eff, 0, -1):
+        if batch_size % g == 0:
+            return g
+    return 1
+
+
+def conv2d_grouped_filter_grad(roi_cells_bhw, g_z_roi, pad_hw, max_groups: int = 8):
+    """kernels_greens.py:84-123: the filter gradient dG (M, 1, Kh, Kw) of
+    conv2d(roi_cells[:, None], filters, padding=((r_h, r_h), (r_w, r_w))) for the output
+    cotangent g_z_roi (B, M, h_out, w_out), Kh = h_in + 2 r_h - h_out + 1.  Here the batch sum
+    runs in the frequency domain (unshifted Plancherel, nc_fftconv_bwd without dx) and one
+    inverse per direction realigns it (nc_filter_spectrum_bwd, roll Kh - 1 - r_h);
+    ``max_groups`` is accepted and has no effect on the result."""
+    x, gz = _f32(roi_cells_bhw), _f32(g_z_roi)
+    B, hin, win = x.shape
+    Bz, M, hout, wout = gz.shape
+    if Bz != B:
+        raise ValueError("batch sizes of the cells and the cotangent differ")
+    rh, rw = (int(v) for v in pad_hw)
+    kh, kw = hin + 2 * rh - hout + 1, win + 2 * rw - wout + 1
+    if kh <= 0 or kw <= 0 or rh < 0 or rw < 0:
+        raise ValueError("inconsistent shapes for the filter gradient")
+    fh, fw = _grid_for(max(hin + rh, hout, kh), max(win + rw, wout, kw))
+    F = fh * (fw // 2 + 1)
+    dev = x.device
+    xhat = torch.empty(B, F, device=dev, dtype=torch.complex64)
+    call("nc_plane_spectrum", stream_ptr(), B, hin, win, fh, fw, 0, 0, ptr(x), ptr(xhat))
+    ghat = torch.zeros(M, F, device=dev, dtype=torch.complex64)  # unused without dx
+    dgh = torch.empty(M, F, device=dev, dtype=torch.complex64)
+    ws = _ws(lib().nc_fftconv_bwd_workspace_size(B, M, fh, fw), dev)
+    call("nc_fftconv_bwd", stream_ptr(), B, M, hin, win, hout, wout, 0, 0, fh, fw, ptr(gz),
+         ptr(xhat), ptr(ghat), 0, None, ptr(dgh), 0, 0, ptr(ws), ws.numel() * 4)
+    out = torch.empty(M, 1, kh, kw, device=dev, dtype=torch.float32)
+    call("nc_filter_spectrum_bwd", stream_ptr(), M, kh, kw, fh, fw, (kh - 1 - rh) % fh,
+         (kw - 1 - rw) % fw, ptr(dgh), ptr(out), 0, 0)
+    return out
+
+
+def rfft2_filter_grad_to_oihw(grad_ker_freq_mhw, kernel_size=(23, 13), fft_shape=(64, 64)):
+    """kernels_greens.py:262-275: irfft2 of the (M, Fh, Fw/2+1) frequency cotangent, cropped
+    to (Kh, Kw) and flipped -> (M, 1, Kh, Kw) (no roll: the shifted convention)."""
+    return _filter_grad(grad_ker_freq_mhw, kernel_size, (0, 0), fft_shape, False)
+
+
+def hoist_filter_rfft2(filters_oihw, kernel_size=(23, 13), fft_shape=(64, 64)):
+    """kernels_greens.py:278-313: precompute_filter_rfft2 whose backward turns the shifted
+    frequency cotangent into OIHW filter gradients (rfft2_filter_grad_to_oihw)."""
+    return _HoistNopad.apply(filters_oihw, tuple(kernel_size), (0, 0), tuple(fft_shape), False)
+
+
+def hoist_filter_rfft2_zero_fwd(filters_oihw, kernel_size=(23, 13), fft_shape=(64, 64)):
+    """kernels_greens.py:428-465: zeros forward, rfft2_filter_grad_to_oihw backward."""
+    return _HoistNopad.apply(filters_oihw, tuple(kernel_size), (0, 0), tuple(fft_shape), True)
+
+
+def conv2d_roi_rfft_step(roi_cells_bhw, ker_freq_mhw, roi_shape=(40, 50), pad_hw=(11, 6),
+                         fft_shape=(64, 64), need_dx: bool = True):
+    """kernels_greens.py:316-400: the SAME ROI correlation of the cells with the hoisted filter
+    spectra; residuals (cell_freq, ker_freq); cotangents (g_cells, g_ker_freq) with the
+    reference's shifted ker_freq cotangent (gz zero-padded at pad_hw before its transform)."""
+    return _PrunedConv.apply(roi_cells_bhw, ker_freq_mhw, tuple(roi_shape), tuple(pad_hw),
+                             tuple(fft_shape), bool(need_dx), True)
+
+
+def conv2d_valid_rfft_precomputed(cells_bhw, ker_freq_mhw, roi_shape=(40, 50),
+                                  kernel_size=(23, 13), fft_shape=(64, 64)):
+    """kernels_greens.py:403-425: the VALID correlation of the full (B, H, W) grid read at
+    offset (Kh - 1, Kw - 1)."""
+    kh, kw = kernel_size
+    return conv2d_roi_rfft_step(cells_bhw, ker_freq_mhw, roi_shape, (kh - 1, kw - 1),
+                                fft_shape, True)
+
+
+class _HybridRoi(torch.autograd.Function):
+    """conv2d_hybrid_roi_step: forward on the filters (the reference's direct conv; here the
+    same spectral correlation), cotangents (g_cells, zeros for the filters, the shifted
+    spectral cotangent for the token)."""
+
+    @staticmethod
+    def forward(ctx, x, filters, token, pad_hw, fft_shape, need_dx):
+        kf = precompute_filter_rfft2(filters, fft_shape)
+        h, w = x.shape[-2:]
+        ctx.fshape = tuple(filters.shape)
+        return _PrunedConv.forward(ctx, x, kf, (h, w), pad_hw, fft_shape, need_dx, True)
+
+    @staticmethod
+    def backward(ctx, gz):
+        dx, dkf, *_ = _PrunedConv.backward(ctx, gz)
+        gf = torch.zeros(ctx.fshape, device=dx.device, dtype=torch.float32)
+        return dx, gf, dkf, None, None, None
+
+
+def conv2d_hybrid_roi_step(roi_cells_bhw, filters_oihw, ker_freq_token, pad_hw=(11, 6),
+                           fft_shape=(64, 64), need_dx: bool = True):
+    """kernels_greens.py:468-551 with ``hoist_filter_rfft2_zero_fwd``'s token.  The reference's
+    rule pairs a direct conv padded by pad_hw with a spectral cotangent shifted by pad_hw, which
+    agree only for SAME pads (2 r = K - 1); other pads raise."""
+    kh, kw = filters_oihw.shape[-2:]
+    if 2 * int(pad_hw[0]) != kh - 1 or 2 * int(pad_hw[1]) != kw - 1:
+        raise NeurocellError("conv2d_hybrid_roi_step takes SAME pads ((Kh-1)/2, (Kw-1)/2)")
+    return _HybridRoi.apply(roi_cells_bhw, filters_oihw, ker_freq_token, tuple(pad_hw),
+                            tuple(fft_shape), bool(need_dx))
+
+
+# ------------------------------------------------------------------ epilogue.py operators
+
+class _Standardize(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, z):
+        z = _f32(z)
+        n = z.shape[-1] * z.shape[-2]
+        planes = _planes(z.shape[:-2])
+        out = torch.empty_like(z)
+        mean = torch.empty(planes, device=z.device, dtype=torch.float32)
+        rstd = torch.empty_like(mean)
+        call("nc_standardize_fwd", stream_ptr(), planes, n, ptr(z), ptr(out), ptr(mean),
+             ptr(rstd))
+        ctx.save_for_backward(z, mean, rstd)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        z, mean, rstd = ctx.saved_tensors
+        gx = torch.empty_like(z)
+        call("nc_standardize_bwd", stream_ptr(), mean.numel(), z.shape[-1] * z.shape[-2], ptr(z),
+             ptr(mean), ptr(rstd), ptr(_f32(g)), ptr(gx))
+        return gx
+
+
+def standardize_spatial_nchw(z_bmhw):
+    """epilogue.py:20-25: each (b, m) plane standardised to zero mean and unit variance
+    (population variance, eps 1e-5); differentiable."""
+    return _Standardize.apply(z_bmhw)
+
+
+def fused_roi_epilogue(z_roi_bmhw, step_params, c_border_bhw, topology, activate="tanh",
+                       norm: bool = True):
+    """epilogue.py:59-79: the ROI update of ``fused_roi_step_epilogue`` embedded into the
+    full-grid border template (B, H, W) at the ROI; differentiable w.r.t. z, the step
+    parameters and the template's border cells."""
+    roi_next = fused_roi_step_epilogue(z_roi_bmhw, step_params, activate, norm)
+    rh, rw = topology.pad_h, topology.pad_w
+    H, W = topology.grid_shape
+    out = c_border_bhw.clone()
+    out[:, rh:H - rh, rw:W - rw] = roi_next
+    return out

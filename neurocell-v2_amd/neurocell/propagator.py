@@ -170,3 +170,56 @@ def inject_inputs_roi_2d(inputs, topology: ChipTopology2D, dtype=torch.float32, 
     call("nc_inject_roi", stream_ptr(), x_flat.shape[0], plan.n_in, ptr(x_flat), plan.h * plan.w,
          ptr(plan.src), ptr(roi))
     return roi, True
+
+
+_GRID_MAPS = OrderedDict()
+
+
+def _grid_inject_map(topology: ChipTopology2D, port_shapes, device):
+    """Gather map (H*W,) of the full-grid injection: for each grid cell the index of the
+    flattened input written there, or -1.  Later ports overwrite earlier ones at a shared
+    cell, as the reference's successive ``.at[].set`` do."""
+    key = (topology, tuple(port_shapes), str(device))
+    m = _GRID_MAPS.get(key)
+    if m is not None:
+        _GRID_MAPS.move_to_end(key)
+        return m
+    H, W = topology.grid_shape
+    src = np.full(H * W, -1, np.int32)
+    e = 0
+    for port, (ih, iw) in zip(topology.in_ports, port_shapes):
+        if isinstance(port, CoordinatePortSpec):
+            for k, (r, c) in enumerate(port.coords):
+                src[r * W + c] = e + k
+            e += port.num_points
+            continue
+        r0, c0 = port.offset
+        if r0 < 0 or c0 < 0 or r0 + ih > H or c0 + iw > W:
+            raise ValueError(f"input port {port.name!r} of {ih}x{iw} at {port.offset} lies "
+                             "outside the grid")
+        for i in range(ih):
+            src[(r0 + i) * W + c0:(r0 + i) * W + c0 + iw] = e + i * iw + np.arange(iw)
+        e += ih * iw
+    m = _GRID_MAPS[key] = (torch.tensor(src, device=device), e)
+    while len(_GRID_MAPS) > 32:
+        _GRID_MAPS.popitem(last=False)
+    return m
+
+
+def inject_inputs_2d(inputs, topology: ChipTopology2D, dtype=torch.float32):
+    """propagator.py:103-132: the batched port inputs written into a zero (B, H, W) field
+    (rectangular ports at their offsets - a 3-D per-port input with its own (ih, iw) -
+    coordinate ports at their cells).  Runs the executor's gather kernel over the grid."""
+    from ._lib import call, ptr, stream_ptr
+    if dtype != torch.float32:
+        raise NeurocellError("the MI355X path injects float32 fields")
+    x_flat = flatten_inputs(inputs, topology)
+    src, n_in = _grid_inject_map(topology, port_input_shapes(inputs, topology), x_flat.device)
+    if n_in != x_flat.shape[1]:
+        raise NeurocellError(f"inputs carry {x_flat.shape[1]} values per sample, the ports "
+                             f"take {n_in}")
+    H, W = topology.grid_shape
+    cells = torch.empty(x_flat.shape[0], H, W, device=x_flat.device, dtype=dtype)
+    call("nc_inject_roi", stream_ptr(), x_flat.shape[0], n_in, ptr(x_flat), H * W, ptr(src),
+         ptr(cells))
+    return cells

@@ -74,6 +74,11 @@ enum { hipFuncAttributeMaxDynamicSharedMemorySize = 8 };
 #define NC_FENCE() ((void)0)
 inline hipError_t hipFuncSetAttribute(const void*, int, int) { return 0; }
 #define __align__(n) alignas(n)
+inline void sincospif(float x, float* s, float* c) {
+    const double a = 3.14159265358979323846 * (double)x;
+    *s = (float)sin(a);
+    *c = (float)cos(a);
+}
 #define HIP_SYMBOL(X) X
 inline hipError_t hipGetDevice(int* d) { *d = 0; return 0; }
 inline hipError_t hipStreamGetDevice(hipStream_t, int* d) { *d = 0; return 0; }

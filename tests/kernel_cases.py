@@ -791,6 +791,68 @@ def case_adaptive(be, seed=5):
             "mask_mismatch": float((be.get(dil).astype(bool) != dil_r).sum())}
 
 
+def case_spectral_ops(be, n=3, FH=32, FW=16, roi=(12, 10), pad=(5, 3), shift=(7, 5), seed=11):
+    """nc_spectrum_map (phase ramp, Hermitian edge parts, column scales, conjugation),
+    nc_irfft2_pruned on non-Hermitian spectra (NumPy's inverse keeps only the edge columns'
+    Hermitian parts) and nc_standardize_fwd/bwd against float64 NumPy."""
+    rng = np.random.default_rng(seed)
+    L, s = be.lib, be.stream()
+    Fh = FW // 2 + 1
+    X = rng.normal(size=(n, FH, Fh)) + 1j * rng.normal(size=(n, FH, Fh))
+    Xf = np.stack([X.real, X.imag], -1).astype(np.float32)
+    xd = be.put(Xf)
+    out = be.zeros((n, FH, Fh, 2))
+    # conj, herm edges, scales 0.5 / 2, phase of a circular shift
+    _ok(be, L.nc_spectrum_map(s, n, FH, FW, shift[0], shift[1], 1, 0.5, 2.0, 1, be.ptr(xd),
+                              be.ptr(out)), "spectrum_map")
+    Y = np.conj(X)
+    H = Y.copy()
+    for c in (0, FW // 2):
+        H[:, :, c] = 0.5 * (Y[:, :, c] + np.conj(Y[:, (-np.arange(FH)) % FH, c]))
+    scale = np.full(Fh, 2.0)
+    scale[[0, -1]] = 0.5
+    kh, kw = np.arange(FH)[:, None], np.arange(Fh)[None, :]
+    phase = np.exp(-2j * np.pi * (kh * shift[0] / FH + kw * shift[1] / FW))
+    ref_map = H * scale * phase
+    res = {"spectrum_map": rel_l2(_cplx(be.get(out)), ref_map)}
+    # the phase ramp equals the spectrum of the circularly shifted plane
+    pl = rng.normal(size=(FH, FW))
+    P = np.fft.rfft2(pl)
+    pd, po = be.put(np.stack([P.real, P.imag], -1)), be.zeros((1, FH, Fh, 2))
+    _ok(be, L.nc_spectrum_map(s, 1, FH, FW, shift[0], shift[1], 0, 1.0, 1.0, 0, be.ptr(pd),
+                              be.ptr(po)), "spectrum_map_shift")
+    res["phase_is_shift"] = rel_l2(_cplx(be.get(po))[0], np.fft.rfft2(np.roll(pl, shift, (0, 1))))
+    # irfft2_pruned
+    rh, rw = roi
+    z = be.zeros((n, rh, rw))
+    ws = be.zeros((L.nc_irfft2_pruned_workspace_size(n, FH, FW) // 4 + 1,))
+    nb = ws.nbytes if hasattr(ws, "nbytes") else ws.numel() * 4
+    _ok(be, L.nc_irfft2_pruned(s, n, rh, rw, pad[0], pad[1], FH, FW, be.ptr(xd), be.ptr(z),
+                               be.ptr(ws), nb), "irfft2_pruned")
+    full = np.fft.irfft2(X, s=(FH, FW))
+    res["irfft2_pruned"] = rel_l2(be.get(z), full[:, pad[0]:pad[0] + rh, pad[1]:pad[1] + rw])
+    # standardize
+    planes, npx = 5, 7 * 9
+    x = (rng.normal(size=(planes, npx)) * 2 + 1).astype(np.float32)
+    g = rng.normal(size=(planes, npx)).astype(np.float32)
+    xd2, gd = be.put(x), be.put(g)
+    o, mu, rs, gx = (be.zeros((planes, npx)), be.zeros((planes,)), be.zeros((planes,)),
+                     be.zeros((planes, npx)))
+    _ok(be, L.nc_standardize_fwd(s, planes, npx, be.ptr(xd2), be.ptr(o), be.ptr(mu),
+                                 be.ptr(rs)), "std_fwd")
+    _ok(be, L.nc_standardize_bwd(s, planes, npx, be.ptr(xd2), be.ptr(mu), be.ptr(rs),
+                                 be.ptr(gd), be.ptr(gx)), "std_bwd")
+    x64 = x.astype(np.float64)
+    m = x64.mean(-1, keepdims=True)
+    r = 1.0 / np.sqrt(((x64 - m) ** 2).mean(-1, keepdims=True) + 1e-5)
+    zh = (x64 - m) * r
+    c1, c2 = g.mean(-1, keepdims=True), (g * zh).mean(-1, keepdims=True)
+    res["std_fwd"] = rel_l2(be.get(o), zh)
+    res["std_rstd"] = rel_l2(be.get(rs), r[:, 0])
+    res["std_bwd"] = rel_l2(be.get(gx), r * (g - c1 - zh * c2))
+    return res
+
+
 def case_helpers(be, seed=6):
     """Input injection (exact), MSE loss and three AdamW steps."""
     rng = np.random.default_rng(seed)

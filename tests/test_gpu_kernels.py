@@ -6,6 +6,7 @@ from kernel_cases import (CODD_CASES, EPILOGUE_SHAPES, PORT_SHAPES, TOL, DeviceB
                           case_epilogue, case_epilogue_parts,
                           case_fftconv_circular, case_fftconv_port, case_fftconv_epilogue,
                           case_fftconv, case_helpers, case_plane_spectra, case_port,
+                          case_spectral_ops,
                           case_universe)
 
 pytestmark = pytest.mark.gpu
@@ -160,3 +161,10 @@ UNIVERSE_CASES = [("VALID", None, "tanh"), ("VALID", (2, 9, 1, 10), "sigmoid"),
 @pytest.mark.parametrize("pmode,bbox,fact", UNIVERSE_CASES)
 def test_universe(be, pmode, bbox, fact):
     _assert_small(case_universe(be, pmode, bbox, fact))
+
+
+@pytest.mark.parametrize("FH,FW,roi,pad,shift", [(32, 16, (12, 10), (5, 3), (7, 5)),
+                                                 (64, 64, (40, 50), (11, 6), (63, 1)),
+                                                 (256, 128, (200, 100), (30, 20), (255, 3))])
+def test_spectral_ops(be, FH, FW, roi, pad, shift):
+    _assert_small(case_spectral_ops(be, FH=FH, FW=FW, roi=roi, pad=pad, shift=shift))
