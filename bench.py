@@ -37,31 +37,38 @@ def synthetic(name, seed, B=None):
 
 
 def algorithmic_bytes(B, M, N, F, hb=0, dx=1, P=16):
-    """Per-call algorithmic bytes (each interface operand counted once, 4 B/f32, 8 B/c64).
-    spectra: the state x in (once, however many partial planes hold it), the border spectrum
-    in, xhat out.  conv_epilogue_fwd: xhat and ghat in, w/s/b in, z out (training), the
-    step's output x' out (once), mean/rstd out.  conv_port_fwd (the last step): xhat, ghat,
-    port indices and parameters in, z out (training), zo, mean/rstd and the outputs out.
-    fftconv_bwd: gz, xhat, ghat in, dx out, dghat read-modify-write, the cotangent spectrum
-    sum out.  The step's epilogues run without a border term (hb = 0: it is folded into the
-    spectra)."""
+    """Per-call algorithmic bytes: each logical operand at the kernel interface counted once
+    (4 B per f32, 8 B per c64), with the per-family formulas of the measurement plan:
+      FFT conv fwd   4BN + 8MF + 4BMN          (x in, filter spectra in, z out)
+      FFT conv bwd   4BMN + 4BN + 8MF + dx 4BN + 16MF
+                     (gz in, x in, filter spectra in, dx out, dG spectra read-modify-write)
+      epilogue fwd   4(BMN + hb MN + 3N + BN + 2BM)
+      epilogue bwd   4(2BMN + 2hb MN + 6N + 2BM + BN)
+      port fwd       4(BMN + hb MN + 2BM + BMP)
+      port bwd       4(2BMN + 2hb MN + 4BM + BMP)
+    The step runs the conv forward as two launches and fuses it with the epilogue: spectra
+    (x in, its spectrum out: 4BN + 8BF) and conv_epilogue_fwd / conv_port_fwd (the cell
+    spectrum in, 8BF, in place of x, plus the conv forward and the epilogue or port forward
+    without the z they pass on chip: z is still written once in training).  hb = 0 in the
+    step: the border term is folded into the spectra."""
+    conv_fwd = 4 * B * N + 8 * M * F + 4 * B * M * N
+    epi_fwd = 4 * (B * M * N + hb * M * N + 3 * N + B * N + 2 * B * M)
+    port_fwd = 4 * (B * M * N + hb * M * N + 2 * B * M + B * M * P)
     return {
-        "spectra": 4 * B * N + 8 * F + 8 * B * F,
-        "conv_epilogue_fwd": 8 * B * F + 8 * M * F + 12 * N + 4 * B * M * N + 4 * B * N
-                             + 8 * B * M,
-        "conv_port_fwd": 8 * B * F + 8 * M * F + 4 * B * M * N + 16 * P + 4 * B * M * P
-                         + 8 * B * M + 4 * B * P,
-        "fftconv_bwd": (4 * B * M * N + 8 * B * F + 8 * M * F + dx * 4 * B * N + 16 * M * F
-                        + 8 * M * F),
-        "epilogue_fwd": 4 * (B * M * N + hb * M * N + 3 * N + B * N + 2 * B * M),
-        "epilogue_bwd": 4 * (2 * B * M * N + hb * M * N + 6 * N + 2 * B * M + B * N),
-        "port_fwd": 4 * (B * M * N + hb * M * N + 2 * B * M + B * M * P),
-        "port_bwd": 4 * (2 * B * M * N + hb * M * N + 4 * B * M + B * M * P),
+        "spectra": 4 * B * N + 8 * B * F,
+        "conv_epilogue_fwd": conv_fwd - 4 * B * N + 8 * B * F + epi_fwd - 4 * B * M * N,
+        "conv_port_fwd": conv_fwd - 4 * B * N + 8 * B * F + port_fwd - 4 * B * M * N,
+        "fftconv_bwd": 4 * B * M * N + 4 * B * N + 8 * M * F + dx * 4 * B * N + 16 * M * F,
+        "epilogue_fwd": epi_fwd,
+        "epilogue_bwd": 4 * (2 * B * M * N + 2 * hb * M * N + 6 * N + 2 * B * M + B * N),
+        "port_fwd": port_fwd,
+        "port_bwd": 4 * (2 * B * M * N + 2 * hb * M * N + 4 * B * M + B * M * P),
     }
 
 
 def time_family(fn, reps, torch):
-    """Average device time of fn() over reps back-to-back launches on the current stream."""
+    """Average device time of fn() over reps back-to-back launches on the current stream
+    (warm: the operands stay in the 256 MB MALL between calls)."""
     fn()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -73,9 +80,31 @@ def time_family(fn, reps, torch):
     return e0.elapsed_time(e1) / reps * 1e3  # us
 
 
-def kernel_families(ts, torch, reps):
+_FLUSH = {}
+
+
+def time_family_flushed(fn, reps, torch):
+    """Median device time of single fn() calls, each after 1 GiB of unrelated HBM traffic (a
+    512 MiB buffer rewritten) has evicted the operands from the MALL; the flush is outside the
+    timed events."""
+    if "buf" not in _FLUSH:
+        _FLUSH["buf"] = torch.empty(128 << 20, device="cuda", dtype=torch.float32)
+    buf = _FLUSH["buf"]
+    ts = []
+    for _ in range(reps):
+        buf.add_(1.0)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1e3)
+    return float(np.median(ts))
+
+
+def kernel_families(ts, torch, reps, flushed=False):
     """Device time per call of each C-ABI family at the step's shapes (after a step, so every
-    operand holds real data)."""
+    operand holds real data); MALL-flushed single calls with ``flushed``."""
     from neurocell._lib import call, ptr, stream_ptr
     p = ts.plan
     B, M, h, w = p.B, p.M, p.h, p.w
@@ -114,7 +143,8 @@ def kernel_families(ts, torch, reps):
     }
     per_step = {"spectra": p.d - 1, "conv_epilogue_fwd": p.d - 1, "conv_port_fwd": 1,
                 "fftconv_bwd": p.d, "epilogue_bwd": p.d - 1, "port_bwd": 1}
-    return {k: (time_family(f, reps, torch), per_step[k]) for k, f in fams.items()}
+    timer = time_family_flushed if flushed else time_family
+    return {k: (timer(f, reps, torch), per_step[k]) for k, f in fams.items()}
 
 
 # C-ABI family of each kernel of a --families-only run (k_batch_reduce belongs to whichever
@@ -181,38 +211,184 @@ def traffic_summary(fetch_dir, write_dir, reps, out_path):
     return out
 
 
-def cpu_baseline(seed, B, budget_s):
+def _cpu_cores():
+    """The host cores this process may run on (the box's CPU share), pinned: the process
+    affinity is fixed to exactly these cores for the CPU legs, one worker thread per core."""
+    cores = sorted(os.sched_getaffinity(0))
+    os.sched_setaffinity(0, cores)
+    return len(cores)
+
+
+def _chunks(B, threads):
+    c = max(1, -(-B // threads))
+    return [(i, min(B, i + c)) for i in range(0, B, c)]
+
+
+def _short_kernel(name):
+    """'void (anonymous namespace)::k_pspec<64, 64>(int, ...)' -> 'k_pspec<64, 64>'."""
+    n = name.replace("void ", "").replace("(anonymous namespace)::", "")
+    depth, out = 0, []
+    for ch in n:
+        if ch == "(" and depth == 0:
+            break
+        depth += ch == "<"
+        depth -= ch == ">"
+        out.append(ch)
+    return "".join(out).strip()
+
+
+def _pmc_dispatches(db):
+    """Per-dispatch counter values {dispatch: (kernel, {counter: value})} from a rocprofv3
+    rocpd database (the counters_collection view; instances summed)."""
+    import sqlite3
+    con = sqlite3.connect(db)
+    per = {}
+    for d, k, cn, v in con.execute(
+            "select dispatch_id, kernel_name, counter_name, value from counters_collection"):
+        kern, vals = per.setdefault(d, (_short_kernel(k), {}))
+        vals[cn] = vals.get(cn, 0.0) + v
+    return per
+
+
+def counter_summary(dirs, out_path, cu_num=256, xcds=8):
+    """Per-kernel rocprofv3 counter summary of a `bench.py --families-only` run from one or
+    more pass folders (each holding run_results.db): instruction mix per wavefront, VALU busy,
+    LDS activity and bank conflicts, and HBM bytes per dispatch (FETCH_SIZE / WRITE_SIZE
+    scaled by what they read for the run's 256 MiB copies).  Writes a markdown table."""
+    import glob
+    merged = {}
+    for d in dirs:
+        db = sorted(glob.glob(os.path.join(d, "**", "*.db"), recursive=True))[0]
+        for disp, (kern, vals) in _pmc_dispatches(db).items():
+            merged.setdefault(kern, []).append(vals)
+    agg = {}
+    for kern, lst in merged.items():
+        keys = set().union(*lst)
+        agg[kern] = {k: float(np.mean([v[k] for v in lst if k in v])) for k in keys}
+        agg[kern]["_n"] = len(lst)
+    copy = agg.get("__amd_rocclr_copyBuffer", {})
+    big = [v for v in merged.get("__amd_rocclr_copyBuffer", []) if v.get("FETCH_SIZE", 0) > 1e5]
+    fscale = (256 << 20) / (float(np.median([v["FETCH_SIZE"] for v in big])) * 1024.0) \
+        if big else None
+    bigw = [v for v in merged.get("__amd_rocclr_copyBuffer", []) if v.get("WRITE_SIZE", 0) > 1e5]
+    wscale = (256 << 20) / (float(np.median([v["WRITE_SIZE"] for v in bigw])) * 1024.0) \
+        if bigw else None
+    # GRBM_GUI_ACTIVE reads once per XCD; the counters_collection view sums the 8 instances
+    for a in agg.values():
+        if "GRBM_GUI_ACTIVE" in a:
+            a["GRBM_GUI_ACTIVE"] /= xcds
+    lines = ["| kernel | dispatches | waves | VALU inst/wave | FP32 share of VALU | VALU busy % "
+             "| SALU inst/wave | LDS inst/wave | LDS active % | LDS bank-conflict % | "
+             "VMEM rd/wr per wave | HBM read MB | HBM write MB |",
+             "|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    keep = [k for k in agg if k.startswith("k_")]
+    for k in sorted(keep, key=lambda k: -agg[k].get("GRBM_GUI_ACTIVE", 0.0)):
+        a = agg[k]
+        w = max(a.get("SQ_WAVES", 0.0), 1.0)
+        gui = max(a.get("GRBM_GUI_ACTIVE", 0.0), 1.0)
+        fp = sum(a.get(c, 0.0) for c in ("SQ_INSTS_VALU_ADD_F32", "SQ_INSTS_VALU_MUL_F32",
+                                         "SQ_INSTS_VALU_FMA_F32", "SQ_INSTS_VALU_TRANS_F32"))
+        valu = a.get("SQ_INSTS_VALU", 0.0)
+        fmt = lambda v, f="{:.0f}": "-" if v is None else f.format(v)
+        lines.append(
+            f"| `{k}` | {a['_n']} | {w:.0f} | {fmt(valu / w if valu else None)} | "
+            f"{fmt(fp / valu if valu and fp else None, '{:.2f}')} | "
+            f"{fmt(100 * a['SQ_ACTIVE_INST_VALU'] / cu_num / gui if 'SQ_ACTIVE_INST_VALU' in a else None, '{:.1f}')} | "
+            f"{fmt(a['SQ_INSTS_SALU'] / w if 'SQ_INSTS_SALU' in a else None)} | "
+            f"{fmt(a['SQ_INSTS_LDS'] / w if 'SQ_INSTS_LDS' in a else None)} | "
+            f"{fmt(100 * a['SQ_LDS_IDX_ACTIVE'] / cu_num / gui if 'SQ_LDS_IDX_ACTIVE' in a else None, '{:.1f}')} | "
+            f"{fmt(100 * a['SQ_LDS_BANK_CONFLICT'] / cu_num / gui if 'SQ_LDS_BANK_CONFLICT' in a else None, '{:.2f}')} | "
+            f"{fmt(a['SQ_INSTS_VMEM_RD'] / w if 'SQ_INSTS_VMEM_RD' in a else None)} / "
+            f"{fmt(a['SQ_INSTS_VMEM_WR'] / w if 'SQ_INSTS_VMEM_WR' in a else None)} | "
+            f"{fmt(a['FETCH_SIZE'] * 1024 * fscale / 1e6 if fscale and 'FETCH_SIZE' in a else None, '{:.2f}')} | "
+            f"{fmt(a['WRITE_SIZE'] * 1024 * wscale / 1e6 if wscale and 'WRITE_SIZE' in a else None, '{:.2f}')} |")
+    with open(out_path, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    return agg, fscale, wscale
+
+
+def cpu_baseline(seed, B, budget_s, warmup=2):
     """Float32 NumPy + scipy.fft restatement (oracle/) of one config-0 train step on this
-    host's cores: forward, MSE loss, reverse pass and AdamW.  Timed over a bounded sample."""
+    host's cores: forward, MSE loss, reverse pass and AdamW.  The batch is split over one
+    thread per core (NumPy and pocketfft release the GIL; the parameter gradients are sums
+    over samples).  ``warmup`` untimed steps, then a bounded sample; median reported."""
+    from concurrent.futures import ThreadPoolExecutor
     from oracle import vnn_oracle as O
-    cores = len(os.sched_getaffinity(0))
+    cores = _cpu_cores()
     cell, filt, x, y = synthetic("config0", seed, B)
     geom = O.alu_geometry(out_width=2)
     m = np.zeros(cell.size + filt.size, np.float32)
     v = np.zeros_like(m)
     theta = np.concatenate([cell.ravel(), filt.ravel()])
+    parts = _chunks(B, cores)
     times = []
-    with O.precision(np.float32, workers=cores):
-        t_end = time.perf_counter() + budget_s
+    with O.precision(np.float32, workers=1), ThreadPoolExecutor(cores) as ex:
         count = 0
-        while True:
-            t0 = time.perf_counter()
+
+        def step(theta, m, v, count):
             c = theta[:cell.size].reshape(cell.shape)
             f = theta[cell.size:].reshape(filt.shape)
-            fwd = O.propagate(c, f, x, geom)
-            _, g_out = O.mse_loss(fwd[0], y)
-            _, gc, gf = O.propagate_vjp(c, f, x, geom, g_out.astype(np.float32), fwd=fwd)
+
+            def one(p):
+                fwd = O.propagate(c, f, x[p[0]:p[1]], geom)
+                # the batch-mean MSE's cotangent, restricted to the chunk
+                _, g_out = O.mse_loss(fwd[0], y[p[0]:p[1]])
+                g_out = g_out * ((p[1] - p[0]) / B)
+                return O.propagate_vjp(c, f, x[p[0]:p[1]], geom, g_out.astype(np.float32),
+                                       fwd=fwd)
+            res = list(ex.map(one, parts))
+            gc = np.sum([r[1] for r in res], axis=0)
+            gf = np.sum([r[2] for r in res], axis=0)
             g = np.concatenate([gc.ravel(), gf.ravel()]).astype(np.float32)
             theta, m, v, count = O.adamw_step(theta, g, m, v, count, 1e-3)
-            theta = theta.astype(np.float32)
+            return theta.astype(np.float32), m, v, count
+
+        for _ in range(warmup):
+            theta, m, v, count = step(theta, m, v, count)
+        t_end = time.perf_counter() + budget_s
+        while True:
+            t0 = time.perf_counter()
+            theta, m, v, count = step(theta, m, v, count)
             times.append(time.perf_counter() - t0)
-            if time.perf_counter() > t_end and len(times) >= 2:
+            if time.perf_counter() > t_end and len(times) >= 3:
                 break
     return {"value": round(1e3 * float(np.median(times)), 3), "unit": "ms/step", "cores": cores,
             "kind": "port",
-            "sample": f"{len(times)} config-0 train steps (B={B}, fwd+bwd+AdamW), float32 "
-                      f"NumPy + scipy.fft restatement in oracle/, scipy.fft workers={cores}, "
-                      "median reported"}
+            "sample": f"{warmup} warm-up + {len(times)} timed config-0 train steps (B={B}, "
+                      f"fwd+MSE+bwd+AdamW), float32 NumPy + scipy.fft restatement in oracle/, "
+                      f"batch split over {cores} threads pinned to {cores} cores, median"}
+
+
+def cpu_baseline_eval(seed, B, budget_s, warmup=3):
+    """The same restatement's forward evaluation of config 1 (B = 1024, ste_ternary at
+    tau = 0.1): samples/s on this host's cores, batch split over one thread per core."""
+    from concurrent.futures import ThreadPoolExecutor
+    from oracle import vnn_oracle as O
+    cores = _cpu_cores()
+    cell, filt, x, _ = synthetic("config1", seed, B)
+    geom = O.alu_geometry(out_width=2)
+    parts = _chunks(B, cores)
+    times = []
+    with O.precision(np.float32, workers=1), ThreadPoolExecutor(cores) as ex:
+        def fwd():
+            return list(ex.map(lambda p: O.propagate(cell, filt, x[p[0]:p[1]], geom,
+                                                     mode="ste_ternary", tau=0.1)[0], parts))
+        for _ in range(warmup):
+            fwd()
+        t_end = time.perf_counter() + budget_s
+        while True:
+            t0 = time.perf_counter()
+            fwd()
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() > t_end and len(times) >= 3:
+                break
+    sec = float(np.median(times))
+    return {"value": round(B / sec, 1), "unit": "samples/s", "cores": cores, "kind": "port",
+            "ms_per_batch": round(1e3 * sec, 2),
+            "sample": f"{warmup} warm-up + {len(times)} timed config-1 forward batches "
+                      f"(B={B}, ste_ternary, tau=0.1), float32 NumPy + scipy.fft restatement "
+                      f"in oracle/, batch split over {cores} threads pinned to {cores} cores, "
+                      "median"}
 
 
 def run_config(name, args, torch):
@@ -291,6 +467,10 @@ def main():
     ap.add_argument("--traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"), default=None,
                     help="summarise two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) of a "
                          "--families-only run into profiles/traffic_config0.json and exit")
+    ap.add_argument("--counters", nargs="+", metavar="PASS_DIR", default=None,
+                    help="summarise rocprofv3 --pmc passes (rocpd databases) of a "
+                         "--families-only run into the markdown table --counters-out and exit")
+    ap.add_argument("--counters-out", default=os.path.join("gpurun_out", "counters.md"))
     ap.add_argument("--families-only", action="store_true",
                     help="profiling aid: one eager train step, a 256 MiB device copy (the "
                          "traffic-counter calibration), then --kernel-reps calls of each "
@@ -301,6 +481,10 @@ def main():
               "the data-parallel sharding over B is described in DESIGN.md", file=sys.stderr)
         sys.exit(2)
 
+    if args.counters:
+        counter_summary(args.counters, args.counters_out)
+        print(open(args.counters_out).read())
+        return
     if args.traffic:
         out = traffic_summary(args.traffic[0], args.traffic[1], args.kernel_reps,
                               os.path.join(ROOT, "profiles", "traffic_config0.json"))
@@ -380,8 +564,9 @@ def main():
         ms = (time.perf_counter() - t0) * 1e3 / reps
         evals[name] = {"ms_per_batch": round(ms, 4), "samples_per_s": round(eb / ms * 1e3, 1)}
 
-    # per-family device times and the roofline of the dominant one
+    # per-family device times (warm and MALL-flushed) and the roofline of the dominant one
     fams = kernel_families(ts, torch, args.kernel_reps)
+    fams_cold = kernel_families(ts, torch, max(10, args.kernel_reps // 10), flushed=True)
     F = plan.F
     ab = algorithmic_bytes(B, plan.M, plan.N, F, P=plan.P)
     share = {k: us * n for k, (us, n) in fams.items()}
@@ -391,7 +576,10 @@ def main():
     kernels = {k: {"us_per_call": round(us_, 2), "calls_per_step": n,
                    "algorithmic_MB": round(ab[k] / 1e6, 3),
                    "GBps": round(ab[k] / (us_ * 1e-6) / 1e9, 1),
-                   "frac_hbm": round(ab[k] / (us_ * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+                   "frac_hbm": round(ab[k] / (us_ * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                   "us_per_call_mall_flushed": round(fams_cold[k][0], 2),
+                   "frac_hbm_mall_flushed": round(ab[k] / (fams_cold[k][0] * 1e-6) / 1e9
+                                                  / HBM_PEAK_GBS, 4)}
                for k, (us_, n) in fams.items()}
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic_config0.json")
@@ -405,6 +593,7 @@ def main():
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(0, B, args.cpu_budget)
+        cpu["config1_eval"] = cpu_baseline_eval(1, 1024, args.cpu_budget)
 
     rec = {
         "metric": METRIC,
