@@ -66,12 +66,34 @@ def algorithmic_bytes(B, M, N, F, hb=0, dx=1, P=16):
     }
 
 
-def time_family(fn, reps, torch):
-    """Average device time of fn() over reps back-to-back launches on the current stream
-    (warm: the operands stay in the 256 MB MALL between calls)."""
+def time_family(fn, reps, torch, graph=True):
+    """Average device time of fn() over back-to-back launches on the current stream (warm:
+    the operands stay in the 256 MB MALL between calls).  With ``graph`` the calls are
+    captured once in a HIP graph (as in the train step) and the graph is replayed, so the
+    host's per-call launch cost is not timed."""
     fn()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if graph:
+        per = min(reps, 50)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(per):
+                fn()
+        g.replay()
+        torch.cuda.synchronize()
+        n = max(1, reps // per)
+        e0.record()
+        for _ in range(n):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / (n * per) * 1e3  # us
     e0.record()
     for _ in range(reps):
         fn()
@@ -102,7 +124,7 @@ def time_family_flushed(fn, reps, torch):
     return float(np.median(ts))
 
 
-def kernel_families(ts, torch, reps, flushed=False):
+def kernel_families(ts, torch, reps, flushed=False, graph=True):
     """Device time per call of each C-ABI family at the step's shapes (after a step, so every
     operand holds real data); MALL-flushed single calls with ``flushed``."""
     from neurocell._lib import call, ptr, stream_ptr
@@ -143,8 +165,9 @@ def kernel_families(ts, torch, reps, flushed=False):
     }
     per_step = {"spectra": p.d - 1, "conv_epilogue_fwd": p.d - 1, "conv_port_fwd": 1,
                 "fftconv_bwd": p.d, "epilogue_bwd": p.d - 1, "port_bwd": 1}
-    timer = time_family_flushed if flushed else time_family
-    return {k: (timer(f, reps, torch), per_step[k]) for k, f in fams.items()}
+    if flushed:
+        return {k: (time_family_flushed(f, reps, torch), per_step[k]) for k, f in fams.items()}
+    return {k: (time_family(f, reps, torch, graph), per_step[k]) for k, f in fams.items()}
 
 
 # C-ABI family of each kernel of a --families-only run (k_batch_reduce belongs to whichever
@@ -517,7 +540,7 @@ def main():
         dst = torch.empty_like(src)
         for _ in range(3):
             dst.copy_(src)
-        fams = kernel_families(ts, torch, args.kernel_reps)
+        fams = kernel_families(ts, torch, args.kernel_reps, graph=False)
         torch.cuda.synchronize()
         print("families-only: copy 256 MiB x3; " + ", ".join(
             f"{k} {us:.1f} us" for k, (us, _) in fams.items()))

@@ -16,6 +16,12 @@
 #define NC_PIN(x) asm volatile("" : "+v"(x))
 #define NC_FENCE() asm volatile("" ::: "memory")
 #endif
+// Orders LDS accesses between the lanes of one wavefront: a wavefront's LDS operations
+// complete in issue order, so keeping the compiler from moving them across this point is
+// enough (no s_barrier).  Every lane of the wavefront must reach it.
+#ifndef NC_WAVE_SYNC
+#define NC_WAVE_SYNC() asm volatile("" ::: "memory")
+#endif
 #define NC_WAVE 64
 
 // Status of a launch sequence: the first failing HIP call's code, else NC_OK.

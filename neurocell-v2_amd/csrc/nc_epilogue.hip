@@ -24,6 +24,9 @@ constexpr int kTileN = 1024;         // kernels_pallas.py:58
 constexpr int kPortTile = 2048;
 constexpr int kMaxM = 64;
 
+// 16-byte loads and stores need 16-byte aligned planes.
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 // The border term z + hb * delta is read branch-free: with hb == 0 the kernels read z's own
 // (cached) pixels through `dl` and scale them by 0.  A uniform `if (hb)` inside the unrolled
 // element loops would make the compiler wait for every element's loads before issuing the
@@ -154,52 +157,111 @@ __global__ __launch_bounds__(256) void k_group_sum(int G, size_t n, const float*
 
 // Backward: gz of the workgroup's directions and its partial gw/gs/gb over them, written as
 // row (g, b) of pg (3, G*B, N) and reduced over all G*B rows afterwards.
-template <int NT, int PPT, int MC, int ACT>
+//
+// The workgroup's directions run in register chunks of MC, software-pipelined: the next
+// chunk's planes are loaded before the current chunk's arithmetic, block reduction and gz
+// stores (its barriers wait for LDS only, so the loads stay in flight), and the chunks
+// alternate between two register tiles.  With VEC (N % 4 == 0, PPT a multiple of 4) a thread
+// owns runs of 4 consecutive pixels, moved as 16-byte loads and stores.
+template <int NT, int PPT, bool VEC>
+struct EpiPix {
+    // pixel of register slot k
+    static NC_DEV int at(int tid, int k) {
+        if constexpr (VEC) return 4 * (tid + (k >> 2) * NT) + (k & 3);
+        else return tid + k * NT;
+    }
+};
+
+// t[q][k] = z (+ delta) of plane row `zrow(q)` (delta row `drow(q)`) at the thread's pixels,
+// clamped to the plane; all loads issue together.
+template <int NT, int PPT, int MC, bool VEC, class ZR, class DR>
+NC_DEV void load_chunk(float (&t)[MC][PPT], int hb, int N, const float* __restrict__ z,
+                       const float* __restrict__ delta, int tid, ZR zrow, DR drow) {
+    if constexpr (VEC) {
+        const int nv = N >> 2;
+        if (hb) {
+#pragma unroll
+            for (int q = 0; q < MC; ++q) {
+                const float4* zp = reinterpret_cast<const float4*>(z + zrow(q));
+                const float4* dp = reinterpret_cast<const float4*>(delta + drow(q));
+#pragma unroll
+                for (int j = 0; j < PPT / 4; ++j) {
+                    const int v = min(tid + j * NT, nv - 1);
+                    const float4 a = zp[v], d = dp[v];
+                    t[q][4 * j] = a.x + d.x;
+                    t[q][4 * j + 1] = a.y + d.y;
+                    t[q][4 * j + 2] = a.z + d.z;
+                    t[q][4 * j + 3] = a.w + d.w;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < MC; ++q) {
+                const float4* zp = reinterpret_cast<const float4*>(z + zrow(q));
+#pragma unroll
+                for (int j = 0; j < PPT / 4; ++j) {
+                    const float4 a = zp[min(tid + j * NT, nv - 1)];
+                    t[q][4 * j] = a.x;
+                    t[q][4 * j + 1] = a.y;
+                    t[q][4 * j + 2] = a.z;
+                    t[q][4 * j + 3] = a.w;
+                }
+            }
+        }
+    } else {
+        load_tile<MC, PPT>(
+            t, hb, z, delta, [&](int q, int k) { return zrow(q) + min(tid + k * NT, N - 1); },
+            [&](int q, int k) { return drow(q) + min(tid + k * NT, N - 1); });
+    }
+}
+
+template <int NT, int PPT, int MC, int ACT, bool VEC>
 __global__ __launch_bounds__(NT) void k_epi_bwd(
     int M, int N, int mpg, float slope, int hb, const float* __restrict__ z,
     const float* __restrict__ delta, const float* __restrict__ w, const float* __restrict__ s,
     const float* __restrict__ bb, const float* __restrict__ mean, const float* __restrict__ rstd,
     const float* __restrict__ gy, float* __restrict__ gz, float* __restrict__ pg, size_t GBN) {
+    using Px = EpiPix<NT, PPT, VEC>;
     __shared__ float red[2 * MC * (NT / 64) + 2 * MC];
     const int b = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
     const int mb = g * mpg, me = min(M, mb + mpg);
     const float inv_n = 1.0f / (float)N;
+    auto zrow = [&](int m0) {
+        return [=](int q) { return ((size_t)b * M + min(m0 + q, me - 1)) * N; };
+    };
+    auto drow = [&](int m0) { return [=](int q) { return (size_t)min(m0 + q, me - 1) * N; }; };
+    float ta[MC][PPT], tb[MC][PPT];
+    load_chunk<NT, PPT, MC, VEC>(ta, hb, N, z, delta, tid, zrow(mb), drow(mb));
     float lin[PPT], ac[PPT], dbs[PPT], bv[PPT], wv[PPT], sv[PPT], gv[PPT];
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
-        const int pc = min(tid + k * NT, N - 1);
+        const int pc = min(Px::at(tid, k), N - 1);
         lin[k] = ac[k] = dbs[k] = 0.f;
         bv[k] = bb[pc];
         wv[k] = w[pc];
         sv[k] = s[pc];
         const float gl = gy[(size_t)b * N + pc];
-        gv[k] = tid + k * NT < N ? gl : 0.f;  // zero cotangent outside the plane
+        gv[k] = Px::at(tid, k) < N ? gl : 0.f;  // zero cotangent outside the plane
     }
-    for (int m0 = mb; m0 < me; m0 += MC) {
-        float zn[MC][PPT], gzn[MC][PPT];
-        float c[2 * MC];
-        float mr[MC], rr[MC];
+    // one chunk: its arithmetic on `cur` with the next chunk's loads into `nxt` in flight
+    auto chunk = [&](float (&cur)[MC][PPT], float (&nxt)[MC][PPT], int m0) {
+        if (m0 + MC < me)
+            load_chunk<NT, PPT, MC, VEC>(nxt, hb, N, z, delta, tid, zrow(m0 + MC),
+                                         drow(m0 + MC));
+        float c[2 * MC], mr[MC], rr[MC], gzn[MC][PPT];
 #pragma unroll
         for (int q = 0; q < MC; ++q) {
             const int m = min(m0 + q, me - 1);
             mr[q] = mean[(size_t)b * M + m];
             rr[q] = rstd[(size_t)b * M + m];
         }
-        load_tile<MC, PPT>(
-            zn, hb, z, delta,
-            [&](int q, int k) {
-                return ((size_t)b * M + min(m0 + q, me - 1)) * N + min(tid + k * NT, N - 1);
-            },
-            [&](int q, int k) {
-                return (size_t)min(m0 + q, me - 1) * N + min(tid + k * NT, N - 1);
-            });
 #pragma unroll
         for (int q = 0; q < MC; ++q) {
             const bool mv = m0 + q < me;
             c[q] = c[MC + q] = 0.f;
 #pragma unroll
             for (int k = 0; k < PPT; ++k) {
-                const float nz = (zn[q][k] - mr[q]) * rr[q];
+                const float nz = (cur[q][k] - mr[q]) * rr[q];
                 float a;
                 const float da = act_fd<ACT>(nz + bv[k], slope, &a);
                 const float gn = mv ? gv[k] * (wv[k] + sv[k] * da) : 0.f;
@@ -208,7 +270,7 @@ __global__ __launch_bounds__(NT) void k_epi_bwd(
                     ac[k] += a;
                     dbs[k] += sv[k] * gv[k] * da;
                 }
-                zn[q][k] = nz;
+                cur[q][k] = nz;
                 gzn[q][k] = gn;
                 c[q] += gn;
                 c[MC + q] += gn * nz;
@@ -220,22 +282,61 @@ __global__ __launch_bounds__(NT) void k_epi_bwd(
             const int m = m0 + q;
             if (m >= me) break;
             const float c1 = c[q] * inv_n, c2 = c[MC + q] * inv_n;
+            float o[PPT];
 #pragma unroll
-            for (int k = 0; k < PPT; ++k) {
-                const int p = tid + k * NT;
-                if (p < N)
-                    gz[((size_t)b * M + m) * N + p] = rr[q] * (gzn[q][k] - c1 - zn[q][k] * c2);
+            for (int k = 0; k < PPT; ++k) o[k] = rr[q] * (gzn[q][k] - c1 - cur[q][k] * c2);
+            float* dst = gz + ((size_t)b * M + m) * N;
+            if constexpr (VEC) {
+#pragma unroll
+                for (int j = 0; j < PPT / 4; ++j) {
+                    const int v = tid + j * NT;
+                    if (4 * v < N)
+                        reinterpret_cast<float4*>(dst)[v] =
+                            make_float4(o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]);
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < PPT; ++k) {
+                    const int p = tid + k * NT;
+                    if (p < N) dst[p] = o[k];
+                }
             }
         }
+    };
+    for (int m0 = mb; m0 < me; m0 += 2 * MC) {
+        chunk(ta, tb, m0);
+        if (m0 + MC < me) chunk(tb, ta, m0 + MC);
     }
     const size_t row = ((size_t)g * gridDim.x + b) * N;  // GBN: the gw / gs / gb plane stride
+    float o0[PPT], o1[PPT];
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
-        const int p = tid + k * NT;
-        if (p < N) {
-            pg[row + p] = gv[k] * lin[k];
-            pg[GBN + row + p] = gv[k] * ac[k];
-            pg[2 * GBN + row + p] = dbs[k];
+        o0[k] = gv[k] * lin[k];
+        o1[k] = gv[k] * ac[k];
+    }
+    const bool pg_vec = ((reinterpret_cast<uintptr_t>(pg + row) | (GBN * 4)) & 15) == 0;
+    if (VEC && pg_vec) {
+#pragma unroll
+        for (int j = 0; j < PPT / 4; ++j) {
+            const int v = tid + j * NT;
+            if (4 * v < N) {
+                float4* p0 = reinterpret_cast<float4*>(pg + row);
+                float4* p1 = reinterpret_cast<float4*>(pg + GBN + row);
+                float4* p2 = reinterpret_cast<float4*>(pg + 2 * GBN + row);
+                p0[v] = make_float4(o0[4 * j], o0[4 * j + 1], o0[4 * j + 2], o0[4 * j + 3]);
+                p1[v] = make_float4(o1[4 * j], o1[4 * j + 1], o1[4 * j + 2], o1[4 * j + 3]);
+                p2[v] = make_float4(dbs[4 * j], dbs[4 * j + 1], dbs[4 * j + 2], dbs[4 * j + 3]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < PPT; ++k) {
+            const int p = Px::at(tid, k);
+            if (p < N) {
+                pg[row + p] = o0[k];
+                pg[GBN + row + p] = o1[k];
+                pg[2 * GBN + row + p] = dbs[k];
+            }
         }
     }
 }
@@ -763,6 +864,7 @@ constexpr int kPortNT = 256;
 constexpr int kPortPPT = kPortTile / kPortNT;
 constexpr int kPortMC = 4;
 
+template <bool VEC>
 __global__ __launch_bounds__(kPortNT) void k_port_bwd(
     int M, int N, int P, int hb, int fact, float slope, const int* __restrict__ pidx,
     const float* __restrict__ z, const float* __restrict__ delta, const float* __restrict__ pp,
@@ -772,14 +874,30 @@ __global__ __launch_bounds__(kPortNT) void k_port_bwd(
     HIP_DYNAMIC_SHARED(float, dyn)
     float* gzo = dyn;                          // M*P: port cotangent per (m, k)
     float* gsum = dyn + M * P;                 // M*P: summed per first-occurrence slot
-    int* slot = reinterpret_cast<int*>(dyn + 2 * M * P);  // kPortTile
+    float* zos = dyn + 2 * M * P;              // M*P: this sample's standardised port values
+    int* slot = reinterpret_cast<int*>(dyn + 3 * M * P);  // kPortTile
     __shared__ float c1s[kMaxM], c2s[kMaxM];
     __shared__ int first[256];
     const int t = blockIdx.x, mg = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
     const float* zob = zo + (size_t)b * M * P;
+    const int base = t * kPortTile;
+    const int ntile = min(kPortTile, N - base);
+    const int m0 = mg * kPortMC;
+    // 0. the dense tile's loads first: they depend on nothing below, so their latency hides
+    //    the port bookkeeping (thread pixels: strided, or runs of 4 with VEC)
+    auto pix = [&](int k) {
+        return VEC ? 4 * (tid + (k >> 2) * kPortNT) + (k & 3) : tid + k * kPortNT;
+    };
+    float v[kPortMC][kPortPPT];
+    load_chunk<kPortNT, kPortPPT, kPortMC, VEC>(
+        v, hb, ntile, z + base, delta + (hb ? base : 0), tid,
+        [&](int q) { return ((size_t)b * M + min(m0 + q, M - 1)) * N; },
+        [&](int q) { return (size_t)min(m0 + q, M - 1) * N; });
     // 1. port cotangents (given directly as (B,M,P) in standardisation-only mode)
     for (int q = tid; q < M * P; q += kPortNT) {
         gsum[q] = 0.f;
+        const float zq = zob[q];
+        zos[q] = zq;
         if (!pp) {
             gzo[q] = gout[(size_t)b * M * P + q];
             continue;
@@ -787,18 +905,16 @@ __global__ __launch_bounds__(kPortNT) void k_port_bwd(
         const int k = q % P;
         const float wo = pp[k], so = pp[P + k], bo = pp[2 * P + k];
         const float go = gout[(size_t)b * P + k];
-        float v;
+        float val;
         if (fact == NC_ACT_IDENTITY) {
-            v = go * (wo + so);
+            val = go * (wo + so);
         } else {
             float a;
             const float gp = go * nc_act_d(pre[(size_t)b * P + k], fact, slope, &a);
-            v = gp * (wo + so * nc_act_d(zob[q] + bo, fact, slope, &a));
+            val = gp * (wo + so * nc_act_d(zq + bo, fact, slope, &a));
         }
-        gzo[q] = v;
+        gzo[q] = val;
     }
-    const int base = t * kPortTile;
-    const int ntile = min(kPortTile, N - base);
     for (int i = tid; i < ntile; i += kPortNT) slot[i] = -1;
     __syncthreads();
     // 2. first-occurrence slots of the port cells inside this tile (sequential: duplicates
@@ -820,7 +936,7 @@ __global__ __launch_bounds__(kPortNT) void k_port_bwd(
         for (int k = 0; k < P; ++k) {
             const float g = gzo[m * P + k];
             a1 += g;
-            a2 += g * zob[m * P + k];
+            a2 += g * zos[m * P + k];
             if (first[k] >= 0) gsum[m * P + first[k]] += g;
         }
         c1s[m] = a1 / (float)N;
@@ -828,31 +944,36 @@ __global__ __launch_bounds__(kPortNT) void k_port_bwd(
     }
     __syncthreads();
     // 3. dense gz of this group's directions over the tile
-    const int m0 = mg * kPortMC;
-    int pc[kPortPPT], sl[kPortPPT];
+    int sl[kPortPPT];
 #pragma unroll
-    for (int k = 0; k < kPortPPT; ++k) {
-        const int i = min(tid + k * kPortNT, ntile - 1);
-        pc[k] = base + i;
-        sl[k] = slot[i];
-    }
-    float v[kPortMC][kPortPPT];
-    load_tile<kPortMC, kPortPPT>(
-        v, hb, z, delta,
-        [&](int q, int k) { return ((size_t)b * M + min(m0 + q, M - 1)) * N + pc[k]; },
-        [&](int q, int k) { return (size_t)min(m0 + q, M - 1) * N + pc[k]; });
+    for (int k = 0; k < kPortPPT; ++k) sl[k] = slot[min(pix(k), ntile - 1)];
 #pragma unroll
     for (int q = 0; q < kPortMC; ++q) {
         const int m = m0 + q;
         if (m >= M) break;
         const float mu = mean[(size_t)b * M + m], r = rstd[(size_t)b * M + m];
         const float c1 = c1s[m], c2 = c2s[m];
+        float o[kPortPPT];
 #pragma unroll
         for (int k = 0; k < kPortPPT; ++k) {
             const float zn = (v[q][k] - mu) * r;
             float gv = -r * (c1 + zn * c2);
             if (sl[k] >= 0) gv += r * gsum[m * P + sl[k]];
-            if (tid + k * kPortNT < ntile) gz[((size_t)b * M + m) * N + pc[k]] = gv;
+            o[k] = gv;
+        }
+        float* dst = gz + ((size_t)b * M + m) * N + base;
+        if constexpr (VEC) {
+#pragma unroll
+            for (int j = 0; j < kPortPPT / 4; ++j) {
+                const int vv = tid + j * kPortNT;
+                if (4 * vv < ntile)
+                    reinterpret_cast<float4*>(dst)[vv] =
+                        make_float4(o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]);
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < kPortPPT; ++k)
+                if (tid + k * kPortNT < ntile) dst[tid + k * kPortNT] = o[k];
         }
     }
     // 4. per-sample port-parameter partials
@@ -1005,16 +1126,30 @@ EpiWs epi_ws(void* ws, int B, int M, int N) {
         }                                                                                       \
     } while (0)
 
-#define NC_BWD_DISPATCH(P_, KER, ...)                                                           \
+#define NC_LAUNCH_BWD(NT_, PPT_, MC_, VEC_, ...) \
+    hipLaunchKernelGGL((k_epi_bwd<NT_, PPT_, MC_, ACT, VEC_>), __VA_ARGS__)
+// Backward dispatch: register chunks of half the plan's group size (two or more pipelined
+// chunks per workgroup), 16-byte pixel runs when N % 4 == 0 and PPT is a multiple of 4.
+#define NC_BWD_DISPATCH(P_, VEC_OK, ...)                                                        \
     do {                                                                                        \
         const SingleCfg c_ = P_.c;                                                              \
-        if (c_.nt == 256 && c_.ppt == 1) NC_LAUNCH_ACT(KER, 256, 1, 8, __VA_ARGS__);            \
-        else if (c_.nt == 256 && c_.ppt == 2) NC_LAUNCH_ACT(KER, 256, 2, 8, __VA_ARGS__);       \
-        else if (c_.nt == 256 && c_.ppt == 3) NC_LAUNCH_ACT(KER, 256, 3, 8, __VA_ARGS__);       \
-        else if (c_.nt == 256 && c_.ppt == 4) NC_LAUNCH_ACT(KER, 256, 4, 8, __VA_ARGS__);       \
-        else if (c_.nt == 512) NC_LAUNCH_ACT(KER, 512, 4, 8, __VA_ARGS__);                      \
-        else if (c_.ppt == 4) NC_LAUNCH_ACT(KER, 1024, 4, 4, __VA_ARGS__);                      \
-        else NC_LAUNCH_ACT(KER, 1024, 8, 2, __VA_ARGS__);                                       \
+        const bool v_ = (VEC_OK);                                                               \
+        if (c_.nt == 256 && c_.ppt == 1) NC_LAUNCH_BWD(256, 1, 4, false, __VA_ARGS__);          \
+        else if (c_.nt == 256 && c_.ppt == 2) NC_LAUNCH_BWD(256, 2, 4, false, __VA_ARGS__);     \
+        else if (c_.nt == 256 && c_.ppt == 3) NC_LAUNCH_BWD(256, 3, 4, false, __VA_ARGS__);     \
+        else if (c_.nt == 256 && c_.ppt == 4) {                                                 \
+            if (v_) NC_LAUNCH_BWD(256, 4, 4, true, __VA_ARGS__);                                \
+            else NC_LAUNCH_BWD(256, 4, 4, false, __VA_ARGS__);                                  \
+        } else if (c_.nt == 512) {                                                              \
+            if (v_) NC_LAUNCH_BWD(512, 4, 4, true, __VA_ARGS__);                                \
+            else NC_LAUNCH_BWD(512, 4, 4, false, __VA_ARGS__);                                  \
+        } else if (c_.ppt == 4) {                                                               \
+            if (v_) NC_LAUNCH_BWD(1024, 4, 2, true, __VA_ARGS__);                               \
+            else NC_LAUNCH_BWD(1024, 4, 2, false, __VA_ARGS__);                                 \
+        } else {                                                                                \
+            if (v_) NC_LAUNCH_BWD(1024, 8, 1, true, __VA_ARGS__);                               \
+            else NC_LAUNCH_BWD(1024, 8, 1, false, __VA_ARGS__);                                 \
+        }                                                                                       \
     } while (0)
 
 // The port forward has no per-pixel activation.
@@ -1149,7 +1284,11 @@ static int epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float
     int rc = dispatch_act(act, [&]<int ACT>() {
         if (N <= kSingleMaxPix) {
             const DirPlan P = bwd_plan(B, M, N);
-            NC_BWD_DISPATCH(P, k_epi_bwd, dim3(B, P.G), dim3(P.c.nt), 0, st, M, N, P.mpg,
+            // the pixel mapping (and so the reduction order) depends only on z, gz, delta:
+            // both forms of the entry point give bit-identical results
+            const bool vec = N % 4 == 0 && aligned16(z) && aligned16(gz) &&
+                             (!has_border || aligned16(delta));
+            NC_BWD_DISPATCH(P, vec, dim3(B, P.G), dim3(P.c.nt), 0, st, M, N, P.mpg,
                             neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, mean, rstd, gy,
                             gz, pg, RN);
             NC_CHECK_LAUNCH();
@@ -1472,10 +1611,16 @@ static int port_bwd(void* stream, int B, int M, int h, int w, int has_border, in
     const EpiWs e = epi_ws(ws, B, M, N);
     float* ppart = pp_rows ? pp_rows : e.pport;
     const size_t ps = pp_rows ? plane_stride : (size_t)B * n_port;
-    const size_t shm = (size_t)2 * M * n_port * sizeof(float) + (size_t)kPortTile * sizeof(int);
-    hipLaunchKernelGGL(k_port_bwd, dim3(T, (M + kPortMC - 1) / kPortMC, B), dim3(kPortNT), shm,
-                       st, M, N, n_port, has_border, final_act, neg_slope, port_idx, z, delta,
-                       port_params, zo, mean, rstd, pre, g_out, gz, ppart, ps);
+    const size_t shm = (size_t)3 * M * n_port * sizeof(float) + (size_t)kPortTile * sizeof(int);
+    const dim3 grid(T, (M + kPortMC - 1) / kPortMC, B);
+    if (N % 4 == 0 && aligned16(z) && aligned16(gz) && (!has_border || aligned16(delta)))
+        hipLaunchKernelGGL(k_port_bwd<true>, grid, dim3(kPortNT), shm, st, M, N, n_port,
+                           has_border, final_act, neg_slope, port_idx, z, delta, port_params, zo,
+                           mean, rstd, pre, g_out, gz, ppart, ps);
+    else
+        hipLaunchKernelGGL(k_port_bwd<false>, grid, dim3(kPortNT), shm, st, M, N, n_port,
+                           has_border, final_act, neg_slope, port_idx, z, delta, port_params, zo,
+                           mean, rstd, pre, g_out, gz, ppart, ps);
     NC_CHECK_LAUNCH();
     // port-parameter gradients (3 rows of P) and the border cotangent, in one launch
     const bool pj = port_params != nullptr && pp_rows == nullptr;

@@ -29,6 +29,7 @@ int nc_port_combine_launch(hipStream_t st, int B, int M, int P, int G, int final
                            float neg_slope, const float* port_params, const float* part,
                            float* out, float* pre);
 #include "nc_pair.h"
+#include "nc_r8.h"
 #include "nc_wave.h"
 
 namespace {
@@ -556,6 +557,67 @@ __global__ __launch_bounds__(64) void k_pspec(int B, int M, int hout, int wout, 
     prfft2_plane<FH, FW, false, kPostNone>(gz + (size_t)g * hout * wout, hout, wout, vec, lds,
                                            spec + ((size_t)m * B + b) * spec_pitch<FH, FW>(),
                                            SpecPost{});
+}
+
+// Backward, first stage on the 64 x 64 grid: the half-spectrum of every cotangent plane
+// gz_bm (g = b*M + m) into spec (M, B, pitch), one 256-thread workgroup per plane (8-lane
+// 64-point transforms, nc_r8.h): the plane is staged in LDS with coalesced loads, transformed,
+// and its half-spectrum stored with 16-byte stores.
+__global__ __launch_bounds__(r8::kNT) void k_r8spec(int B, int M, int hout, int wout,
+                                                    const float* __restrict__ gz,
+                                                    cpx* __restrict__ spec) {
+    HIP_DYNAMIC_SHARED(float, lds)
+    const int g = blockIdx.x, b = g / M, m = g - b * M, tid = threadIdx.x;
+    const r8::Tw tw = r8::twiddles(tid & 7);
+    float* S = lds + 2 * r8::kExCpx;
+    const float* src = gz + (size_t)g * hout * wout;
+    const int n = hout * wout;
+    // the plane's n floats as 16-byte loads, all issued together (at most 4096 floats: four
+    // per thread), then scattered into the staging rows; the columns past wout are zeroed
+    constexpr int U = 4;
+    const bool vec = (n & 3) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0;
+    float4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int q = tid + u * r8::kNT;
+        if (vec) {
+            v[u] = 4 * q < n ? reinterpret_cast<const float4*>(src)[q] : float4{0.f, 0.f, 0.f, 0.f};
+        } else {
+            float e[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) e[j] = 4 * q + j < n ? src[4 * q + j] : 0.f;
+            v[u] = float4{e[0], e[1], e[2], e[3]};
+        }
+    }
+    for (int e = tid; e < hout * (64 - wout); e += r8::kNT) {
+        const int r = e / (64 - wout);
+        S[r * r8::kSP + wout + (e - r * (64 - wout))] = 0.f;
+    }
+    const unsigned inv = ((1u << 20) + wout - 1) / wout;  // exact floor(f / wout), f < 4096
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int q = tid + u * r8::kNT;
+        const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int f = 4 * q + j;
+            if (f < n) {
+                const int r = (int)(((unsigned)f * inv) >> 20);
+                S[r * r8::kSP + (f - r * wout)] = e[j];
+            }
+        }
+    }
+    r8::fwd_plane(lds, hout, tw);
+    const cpx* O = reinterpret_cast<const cpx*>(S);
+    cpx* dst = spec + ((size_t)m * B + b) * spec_pitch<64, 64>();
+#pragma unroll
+    for (int u = 0; u < (r8::kF + r8::kNT - 1) / r8::kNT; ++u) {
+        const int e = tid + u * r8::kNT;
+        if (e < r8::kF) {
+            const int kh = e / 33, kw = e - 33 * kh;
+            dst[e] = O[kh * r8::kOP + kw];
+        }
+    }
 }
 
 // Backward, both frequency-domain reductions in one pass over the stored cotangent spectra
@@ -1329,10 +1391,16 @@ int launch_pbwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wo
     cpx* spec = reinterpret_cast<cpx*>(ws);
     cpx* dxs = spec + (size_t)M * B * spec_pitch<FH, FW>();
     cpx* rows = dxs + (size_t)B * P::F;  // chunk rows when they are not the caller's
-    const PLds ls(hout, P::PITCH, FW, FH, false);
-    lds_limit(k_pspec<FH, FW>, ls.bytes);
-    hipLaunchKernelGGL((k_pspec<FH, FW>), dim3(B * M), dim3(64), ls.bytes, st, B, M, hout, wout,
-                       vec_ok(gz, (size_t)hout * wout), gz, spec);
+    if constexpr (FH == 64) {
+        lds_limit(k_r8spec, r8::kFwdLdsBytes);
+        hipLaunchKernelGGL(k_r8spec, dim3(B * M), dim3(r8::kNT), r8::kFwdLdsBytes, st, B, M,
+                           hout, wout, gz, spec);
+    } else {
+        const PLds ls(hout, P::PITCH, FW, FH, false);
+        lds_limit(k_pspec<FH, FW>, ls.bytes);
+        hipLaunchKernelGGL((k_pspec<FH, FW>), dim3(B * M), dim3(64), ls.bytes, st, B, M, hout,
+                           wout, vec_ok(gz, (size_t)hout * wout), gz, spec);
+    }
     NC_CHECK_LAUNCH();
     // the chunk rows: the caller's row stacks, the outputs themselves (one chunk), or the
     // workspace rows summed below

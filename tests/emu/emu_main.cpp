@@ -3,10 +3,12 @@
 #include <hip/hip_runtime.h>
 
 #include <cstring>
+#include <memory>
 
 thread_local dim3 threadIdx;
 dim3 blockDim, blockIdx, gridDim;
 std::barrier<>* g_bar;
+std::barrier<>* g_wbar[16];
 alignas(16) unsigned char emu_dyn_lds[EMU_LDS_BYTES];
 static hipError_t g_last_error = hipSuccess;
 
@@ -33,6 +35,11 @@ void emu_launch(std::function<void()> f, dim3 g, dim3 b, size_t shm) {
     const size_t nblocks = (size_t)g.x * g.y * g.z;
     std::barrier<> bar(nt);
     g_bar = &bar;
+    std::vector<std::unique_ptr<std::barrier<>>> wbars;
+    for (int w = 0; w * 64 < nt && w < 16; ++w) {
+        wbars.emplace_back(new std::barrier<>(std::min(64, nt - 64 * w)));
+        g_wbar[w] = wbars.back().get();
+    }
     // One pool of nt work-item threads per launch steps through the workgroups (x fastest,
     // then y, then z).  The step barrier's completion runs once between workgroups: it checks
     // the finished workgroup's LDS tail and sets up the next one.

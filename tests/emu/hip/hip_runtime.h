@@ -40,6 +40,11 @@ extern thread_local dim3 threadIdx;
 extern dim3 blockDim, blockIdx, gridDim;
 extern std::barrier<>* g_bar;
 inline void __syncthreads() { g_bar->arrive_and_wait(); }
+// One barrier per 64-lane wavefront of the workgroup: the lanes of a wavefront run in
+// lockstep on the device, here they meet at NC_WAVE_SYNC.
+extern std::barrier<>* g_wbar[16];
+inline void emu_wave_sync() { g_wbar[threadIdx.x / 64]->arrive_and_wait(); }
+#define NC_WAVE_SYNC() emu_wave_sync()
 // Cross-lane exchange; every work-item of the workgroup must call it together.
 inline float __shfl_xor(float v, int off, int) {
     static float buf[1024];
