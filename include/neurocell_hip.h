@@ -299,6 +299,44 @@ int nc_spectrum_map(void* stream, int nplanes, int fft_h, int fft_w, int shift_h
                     int herm_edges, float edge_scale, float interior_scale, int conj_in,
                     const float* in, float* out);
 
+/*
+ * Direct (spatial) correlation for small filters (kh * kw <= 64, M <= 64, plane widths <=
+ * 256): conv2d_batched_nchw and the reference's small-kernel path (kernels_greens.py:177-217,
+ * 84-123; propagator.py:373-386, 521-540), where a spectral grid would be mostly padding.
+ *   z[b, m, i, j] = sum over u < kh, v < kw of x[b, i + oh + u, j + ow + v] * G[m, u, v]
+ * x (n_parts, B, hin, win): the sum of n_parts partial planes (1 for a plain input), zero
+ * outside the plane, or read modulo it when `circular` (then hin = hout, win = wout: the
+ * CIRCULAR padding mode).  (oh, ow) = (-(kh-1)/2, -(kw-1)/2) gives the SAME ROI step, (0, 0)
+ * a VALID correlation.  filters (M, 1, kh, kw), z (B, M, hout, wout).
+ */
+int nc_direct_conv_fwd(void* stream, int B, int M, int hin, int win, int hout, int wout, int oh,
+                       int ow, int kh, int kw, int circular, const float* x, int n_parts,
+                       const float* filters, float* z);
+
+/*
+ * 1 when the direct correlation runs at these shapes (kh * kw <= 64, M <= 64, planes up to
+ * 256 wide and each kernel's one-row band within the workgroup's LDS; with reverse also the
+ * reverse kernels'), else 0.  Host logic choosing between it and the spectral path
+ * (propagator.py:373-386 takes the direct conv for kh * kw <= 64).
+ */
+int nc_direct_conv_fits(int M, int hin, int win, int hout, int wout, int kh, int kw,
+                        int circular, int reverse);
+
+/* Rows of the filter-gradient partials nc_direct_conv_bwd writes at these shapes. */
+int nc_direct_conv_dg_partials(int B, int M, int hout, int wout, int kh, int kw);
+
+/*
+ * Reverse of nc_direct_conv_fwd for the output cotangent gz (B, M, hout, wout): dx (B, hin,
+ * win) when need_dx (the correlation's adjoint; dx may be NULL otherwise) and the filter
+ * gradient as nc_direct_conv_dg_partials(...) partial rows dg_parts (rows, M * kh * kw), each
+ * a fixed-order sum over one band of one sample's pixels; their sum (nc_rows_sum) is
+ * dG (M, 1, kh, kw).  kernels_greens.py:84-123 (conv2d_grouped_filter_grad) for the gradient.
+ */
+int nc_direct_conv_bwd(void* stream, int B, int M, int hin, int win, int hout, int wout, int oh,
+                       int ow, int kh, int kw, int circular, const float* gz, const float* x,
+                       int n_parts, const float* filters, int need_dx, float* dx,
+                       float* dg_parts);
+
 /* Workspace bytes needed by nc_fftconv_bwd for these shapes. */
 size_t nc_fftconv_bwd_workspace_size(int B, int M, int fft_h, int fft_w);
 

@@ -15,7 +15,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "neurocell", "libneurocell_hip.so")
 BUILD = os.path.join(HERE, "_build")
-SOURCES = ("nc_codd.hip", "nc_epilogue.hip", "nc_spectral.hip", "nc_spectral_large.hip")
+SOURCES = ("nc_codd.hip", "nc_epilogue.hip", "nc_spectral.hip", "nc_spectral_large.hip",
+           "nc_direct.hip")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["-O3", "-std=c++20", "--offload-arch=gfx950", "-fPIC",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]

@@ -95,6 +95,10 @@ _SIGS = {
     "nc_fftconv_epilogue_partials": (I, [I, I, I, I, I, I]),
     "nc_fftconv_epilogue_fwd": (I, [P, I, I, I, I, I, I, I, I, P, P, I, F, P, P, P, P, P, P, P,
                                     P, SZ]),
+    "nc_direct_conv_fwd": (I, [P, I, I, I, I, I, I, I, I, I, I, I, P, I, P, P]),
+    "nc_direct_conv_fits": (I, [I, I, I, I, I, I, I, I, I]),
+    "nc_direct_conv_dg_partials": (I, [I, I, I, I, I, I]),
+    "nc_direct_conv_bwd": (I, [P, I, I, I, I, I, I, I, I, I, I, I, P, P, I, P, I, P, P]),
     "nc_irfft2_pruned_workspace_size": (SZ, [I, I, I]),
     "nc_irfft2_pruned": (I, [P, I, I, I, I, I, I, I, P, P, P, SZ]),
     "nc_spectrum_map": (I, [P, I, I, I, I, I, I, F, F, I, P, P]),

@@ -18,6 +18,14 @@ Reverse: port bwd -> d x [spectral conv bwd (dx, dG in the frequency domain)
     -> hidden epilogue bwd] -> filter-spectrum bwd -> border conv bwd -> codd fusion bwd.
 The border conv's cotangent sum_{t>=1} sum_b gz_t is formed in the frequency domain by the
 steps' dG reductions (linearity of rfft2), so the cotangent planes are not re-read for it.
+
+Small filters (kh * kw <= 64, e.g. the 3 x 3 Game-of-Life and CLP chips) take the direct
+correlation instead (propagator.py:373-386), whose spectral grid would be mostly padding:
+    codd fusion -> inject -> border conv (VALID, B = 1) ->
+    d-1 x [direct conv -> hidden epilogue (+ delta)] -> direct conv -> port epilogue (+ delta)
+Reverse: port bwd (-> border cotangent) -> d x [direct conv bwd (dx, dG partial rows)
+    -> hidden epilogue bwd (+= border cotangent)] -> border conv bwd -> dG row sum ->
+    codd fusion bwd.
 """
 from __future__ import annotations
 
@@ -27,10 +35,11 @@ import numpy as np
 import torch
 
 from . import _abi
-from ._lib import NeurocellError, call, ptr, stream_ptr, require_device
+from ._lib import NeurocellError, call, lib, ptr, stream_ptr, require_device
 from .topology import ChipTopology2D, CoordinatePortSpec
 
 _WAVE_FFT = (16, 32, 64)        # wavefront transforms (a plane per lane group)
+_DIRECT_MAX_K = 64              # filters up to this many taps run the direct correlation
 _LARGE_FFT = (64, 128, 256)     # workgroup transforms over LDS segments
 
 
@@ -118,7 +127,7 @@ class StepPlan:
     def __init__(self, topology: ChipTopology2D, batch_size: int, port_shapes: list,
                  roi_bbox=None, activate="tanh", final_activate=None, hard_pin_io=False,
                  training=True, device=None, gated_filters=False, sharpen=None,
-                 universe=False):
+                 universe=False, conv="auto"):
         self.device = device or require_device()
         self.topo = topology
         self.B = int(batch_size)
@@ -151,7 +160,25 @@ class StepPlan:
         self.mode = topology.padding_mode
         self.circular = self.mode == "CIRCULAR"
         self.border = self.mode == "VALID" and d > 1
-        if self.circular:
+        # the correlation: spectral, or direct for small filters (propagator.py:373-386 uses a
+        # direct conv for kh * kw <= 64), whose FFT grid would be mostly padding
+        if conv not in ("auto", "spectral", "direct"):
+            raise NeurocellError(f"conv must be 'auto', 'spectral' or 'direct', got {conv!r}")
+        def fits(hin, win):  # the ROI steps, the full-grid t=0 step, the border conv
+            return lib().nc_direct_conv_fits(M, hin, win, h, w, kh, kw, int(self.circular),
+                                             int(self.training)) == 1
+        direct_ok = (kh * kw <= _DIRECT_MAX_K and not (self.circular and self.cropped)
+                     and fits(h, w) and fits(H, W)
+                     and (not self.border or fits(h + kh - 1, w + kw - 1)))
+        if conv == "direct" and not direct_ok:
+            raise NeurocellError("the direct correlation takes kh * kw <= 64, M <= 64 and "
+                                 "planes up to 256 wide whose bands fit the workgroup's LDS")
+        self.direct = conv == "direct" or (conv == "auto" and direct_ok)
+        if self.direct:
+            if self.circular and self.cropped:
+                raise NeurocellError("adaptive crops are not supported in CIRCULAR mode")
+            self.fft = None
+        elif self.circular:
             if self.cropped:
                 raise NeurocellError("adaptive crops are not supported in CIRCULAR mode")
             # the correlation is circular on the grid itself (topology.py:256-258)
@@ -174,13 +201,14 @@ class StepPlan:
                                      f"in {_WAVE_FFT} or both in {_LARGE_FFT})")
             if h + kh - 1 > self.fft[0] or w + kw - 1 > self.fft[1]:
                 raise NeurocellError("linear correlation does not fit the spectral grid")
-        fh, fw = self.fft
+        fh, fw = self.fft if self.fft else (0, 0)
         self.F = fh * (fw // 2 + 1)
         self.cp = ((kh - 1) // 2, (kw - 1) // 2)
         self.Hp, self.Wp = h + kh - 1, w + kw - 1
         # circular shift taking the border conv's VALID window (kh-1, kw-1) onto the ROI
         # steps' window cp: the patch spectrum shifted by it joins every ROI step's spectrum
-        self.bshift = ((self.cp[0] - (kh - 1)) % fh, (self.cp[1] - (kw - 1)) % fw)
+        self.bshift = (((self.cp[0] - (kh - 1)) % fh, (self.cp[1] - (kw - 1)) % fw)
+                       if self.fft else (0, 0))
         self.chip = _abi.ChipDesc(H, W, kh, kw, M, topology.pad_h, topology.pad_w, roi_h, roi_w,
                                   r0, r1, c0, c1)
         # output port cells
@@ -259,7 +287,7 @@ class StepPlan:
         else:
             if self.cropped:
                 raise NeurocellError("inputs outside a cropped sub-ROI are not supported")
-            if self.H > self.fft[0] or self.W > self.fft[1]:
+            if self.fft and (self.H > self.fft[0] or self.W > self.fft[1]):
                 raise NeurocellError("full-grid t=0 step does not fit the spectral grid")
             base_r, base_c, hh, ww = 0, 0, self.H, self.W
         src = np.full(hh * ww, -1, np.int32)
@@ -278,6 +306,8 @@ class StepPlan:
         return src, not fits
 
     def _alloc(self):
+        if self.direct:
+            return self._alloc_direct()
         dev, B, M, d, h, w, F = self.device, self.B, self.M, self.d, self.h, self.w, self.F
         f = dict(device=dev, dtype=torch.float32)
         c = dict(device=dev, dtype=torch.complex64)
@@ -288,20 +318,7 @@ class StepPlan:
         self.pp = torch.empty(3, self.n_pp, **f)
         self.ghat = torch.empty(M, F, **c)
         self.filt_g = torch.empty(M, 1, self.kh, self.kw, **f) if self.gated else None
-        if self.sharpen is not None:
-            H, W = self.H, self.W
-            fs = self.sh_fft[0] * (self.sh_fft[1] // 2 + 1)
-            self.cell_s = torch.empty(3, H, W, **f)     # [sharpened W, B, S]
-            self.sh_xhat = torch.empty(1, fs, **c)
-            self.sh_ghat = torch.empty(1, fs, **c)
-            self.sh_k = torch.from_numpy(self.sharpen).to(dev).reshape(1, 1, *self.sharpen.shape)
-            call("nc_filter_spectrum_fwd", stream_ptr(), 1, *self.sharpen.shape, *self.sh_fft,
-                 ptr(self.sh_k), ptr(self.sh_ghat))
-            if self.training:
-                self.g_cell_s = torch.empty(3, H, W, **f)
-                self.sh_dg = torch.empty(1, fs, **c)
-                n_ws = _abi_size("nc_fftconv_bwd_workspace_size", 1, 1, *self.sh_fft)
-                self.sh_ws = torch.empty(max(1, n_ws // 4), **f)
+        self._alloc_sharpen()
         self.border_hat = torch.empty(1, F, **c)  # shifted border-patch spectrum
         t0_shape = (B, self.H, self.W) if self.t0_grid else (B, h, w)
         self.x0 = torch.empty(*t0_shape, **f)
@@ -367,6 +384,93 @@ class StepPlan:
             self.g_out = torch.empty(B, self.P, **f)
             self.loss = torch.empty(1, **f)
 
+    def _alloc_sharpen(self):
+        """The sharpening's filter spectrum and its buffers (both correlation paths run the
+        SAME sharpening on its own spectral grid)."""
+        if self.sharpen is None:
+            return
+        dev, H, W = self.device, self.H, self.W
+        f = dict(device=dev, dtype=torch.float32)
+        c = dict(device=dev, dtype=torch.complex64)
+        fs = self.sh_fft[0] * (self.sh_fft[1] // 2 + 1)
+        self.cell_s = torch.empty(3, H, W, **f)     # [sharpened W, B, S]
+        self.sh_xhat = torch.empty(1, fs, **c)
+        self.sh_ghat = torch.empty(1, fs, **c)
+        self.sh_k = torch.from_numpy(self.sharpen).to(dev).reshape(1, 1, *self.sharpen.shape)
+        call("nc_filter_spectrum_fwd", stream_ptr(), 1, *self.sharpen.shape, *self.sh_fft,
+             ptr(self.sh_k), ptr(self.sh_ghat))
+        if self.training:
+            self.g_cell_s = torch.empty(3, H, W, **f)
+            self.sh_dg = torch.empty(1, fs, **c)
+            n_ws = _abi_size("nc_fftconv_bwd_workspace_size", 1, 1, *self.sh_fft)
+            self.sh_ws = torch.empty(max(1, n_ws // 4), **f)
+
+    def _alloc_common(self, G):
+        """Buffers both correlation paths share: parameters, step states, z, statistics,
+        port outputs and the reverse pass's gradient accumulators."""
+        dev, B, M, d, h, w = self.device, self.B, self.M, self.d, self.h, self.w
+        f = dict(device=dev, dtype=torch.float32)
+        self.w_eff = torch.empty(h, w, **f)
+        self.s_eff = torch.empty(h, w, **f)
+        self.b_roi = torch.empty(h, w, **f)
+        self.patch = torch.empty(self.Hp, self.Wp, **f)
+        self.pp = torch.empty(3, self.n_pp, **f)
+        self.filt_g = torch.empty(M, 1, self.kh, self.kw, **f) if self.gated else None
+        self._alloc_sharpen()
+        t0_shape = (B, self.H, self.W) if self.t0_grid else (B, h, w)
+        self.x0 = torch.empty(*t0_shape, **f)
+        self.G = G
+        self.xs = [self.x0] + [torch.empty(G, B, h, w, **f) for _ in range(d - 1)]
+        self.zs = [torch.empty(B, M, h, w, **f) for _ in range(d if self.training else 1)]
+        self.mean = [torch.empty(B, M, **f) for _ in range(d)]
+        self.rstd = [torch.empty(B, M, **f) for _ in range(d)]
+        self.out = torch.empty(B, self.P, **f)
+        port_path = not (self.dense_port or self.universe)
+        self.zo = torch.empty(B, M, self.P, **f) if port_path else None
+        if not port_path:
+            self.port_parts = torch.empty(G, B, h, w, **f)
+        self.pre = torch.empty(B, self.P, **f) if self.fact != 0 and not self.universe else None
+        if self.universe:
+            self.s_prob = torch.empty(self.H, self.W, **f)
+            self.univ = torch.empty(B, self.H, self.W, **f) if self.want_universe else None
+        self.n_epi = d - 1 + int(self.universe)
+        if self.training:
+            self.gz = torch.empty(B, M, h, w, **f)
+            self.gy = [torch.empty(B, h, w, **f) for _ in range(2)]
+            if self.universe:
+                self.g_roi = torch.empty(B, h, w, **f)
+                self.g_sprob = torch.empty(self.H, self.W, **f)
+                self.g_bfull = torch.empty(self.H, self.W, **f)
+            self.g_pre = torch.empty(B, self.P, **f) if self.dense_port else None
+            self.gw = torch.empty(h, w, **f)
+            self.gs = torch.empty(h, w, **f)
+            self.gb = torch.empty(h, w, **f)
+            self.gpp = torch.empty(3, self.n_pp, **f)
+            self.gpatch = torch.empty(self.Hp, self.Wp, **f)
+            self.g_out = torch.empty(B, self.P, **f)
+            self.loss = torch.empty(1, **f)
+        return port_path
+
+    def _alloc_direct(self):
+        """Buffers of the direct path: the hoisted border conv's delta (VALID), the filter
+        gradient's partial rows (each step's bands, then the border conv's) and the border
+        cotangent sum_b gz over the steps that carry the border term."""
+        dev, B, M, d, h, w = self.device, self.B, self.M, self.d, self.h, self.w
+        f = dict(device=dev, dtype=torch.float32)
+        port_path = self._alloc_common(_abi_int("nc_epilogue_fwd_partials", B, M, h, w))
+        self.delta = torch.empty(M, h, w, **f) if self.border else None
+        self.ws_epi = torch.empty(max(1, _abi_size("nc_epilogue_workspace_size", B, M, h, w) // 4),
+                                  **f)
+        del port_path
+        if self.training:
+            K = self.kh * self.kw
+            self.dg_step_rows = _abi_int("nc_direct_conv_dg_partials", B, M, h, w, self.kh,
+                                         self.kw)
+            self.dg_border_rows = (_abi_int("nc_direct_conv_dg_partials", 1, M, h, w, self.kh,
+                                            self.kw) if self.border else 0)
+            self.dg_rows = torch.empty(d * self.dg_step_rows + self.dg_border_rows, M * K, **f)
+            self.gdelta = torch.empty(M, h, w, **f) if self.border else None
+
     def fresh(self) -> "StepPlan":
         """A plan sharing this one's static maps with its own activation buffers."""
         p = copy.copy(self)
@@ -380,7 +484,7 @@ class StepPlan:
         """Runs the d-step forward for inputs (B, n_in); returns the (B, P) port outputs."""
         s = stream_ptr()
         B, M, h, w = self.B, self.M, self.h, self.w
-        fh, fw = self.fft
+        fh, fw = self.fft if self.fft else (0, 0)
         if tuple(x_flat.shape) != (B, self.n_in):
             raise NeurocellError(f"inputs must be ({B}, {self.n_in}), got {tuple(x_flat.shape)}")
         mode = _abi.CODD_IDS[codd_mode]
@@ -397,13 +501,15 @@ class StepPlan:
              ptr(self.port_rc), ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
              ptr(self.patch), ptr(self.pp), ptr(self.s_prob) if self.universe else None, B,
              self.n_in, ptr(x_flat), self.x0[0].numel(), ptr(self.src), ptr(self.x0))
+        if self.gated:
+            call("nc_filter_gate_fwd", s, self.filt_g.numel(), ptr(filt), ptr(self.filt_g))
+            filt = self.filt_g
+        if self.direct:
+            return self._forward_direct(s, cell, filt)
         # the independent spectra in one call: filter spectra (kernels_greens.py:240-259), the
         # border patch's and the first step's cell spectra
         x0h, x0w = (self.H, self.W) if self.t0_grid else (h, w)
         xh0 = self.xhat[0]
-        if self.gated:
-            call("nc_filter_gate_fwd", s, self.filt_g.numel(), ptr(filt), ptr(self.filt_g))
-            filt = self.filt_g
         jobs = [(_addr(filt), _addr(self.ghat), None, M, self.kh, self.kw, 1, 0, 0),
                 (_addr(self.x0), _addr(xh0), None, B, x0h, x0w, 0, 0, 0)]
         if self.border:
@@ -469,6 +575,150 @@ class StepPlan:
                      self.ws_epi.numel() * 4)
         return self.out
 
+    def _conv_input(self, t):
+        """(x, n_parts, hin, win, oh, ow) of step t's direct correlation."""
+        kh, kw = self.kh, self.kw
+        if t == 0:
+            if self.t0_grid:  # VALID correlation of the full grid, read at the sub-ROI
+                return self.x0, 1, self.H, self.W, self.bbox[0], self.bbox[2]
+            return self.x0, 1, self.h, self.w, -((kh - 1) // 2), -((kw - 1) // 2)
+        return self.xs[t], self.G, self.h, self.w, -((kh - 1) // 2), -((kw - 1) // 2)
+
+    def _forward_direct(self, s, cell, filt):
+        """The d-step forward on the direct correlation: each step's z from the (summed)
+        previous state, then the non-fused epilogue (or port) with the hoisted border conv's
+        delta as its border term (propagator.py:343-682)."""
+        B, M, h, w, d = self.B, self.M, self.h, self.w, self.d
+        kh, kw = self.kh, self.kw
+        circ = int(self.circular)
+        ws, nws = ptr(self.ws_epi), self.ws_epi.numel() * 4
+        if self.border:  # propagator.py:362-366: conv_VALID(border patch, G)
+            call("nc_direct_conv_fwd", s, 1, M, self.Hp, self.Wp, h, w, 0, 0, kh, kw, 0,
+                 ptr(self.patch), 1, ptr(filt), ptr(self.delta))
+        dl = ptr(self.delta) if self.border else None
+        for t in range(d):
+            z = self.zs[t if self.training else 0]
+            x, n_parts, hin, win, oh, ow = self._conv_input(t)
+            call("nc_direct_conv_fwd", s, B, M, hin, win, h, w, oh, ow, kh, kw, circ, ptr(x),
+                 n_parts, ptr(filt), ptr(z))
+            if t < d - 1:
+                hb = int(self.border and t > 0)
+                call("nc_epilogue_fwd_parts", s, B, M, h, w, self.act, self.slope, hb, ptr(z),
+                     dl if hb else None, ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
+                     ptr(self.xs[t + 1]), ptr(self.mean[t]), ptr(self.rstd[t]), ws, nws)
+                continue
+            hb = int(self.border)
+            if self.universe:
+                call("nc_epilogue_fwd_parts", s, B, M, h, w, self.fact, self.fslope, hb, ptr(z),
+                     dl if hb else None, ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
+                     ptr(self.port_parts), ptr(self.mean[t]), ptr(self.rstd[t]), ws, nws)
+                call("nc_universe_fwd", s, self.chip, B, self.G, int(self.mode == "VALID"),
+                     self.fact, self.fslope, ptr(self.port_parts), _addr(cell) + 4 * self.H *
+                     self.W, ptr(self.s_prob), self.P, ptr(self.port_cells), ptr(self.univ),
+                     ptr(self.out))
+            elif self.dense_port:
+                call("nc_epilogue_fwd_parts", s, B, M, h, w, self.fact, self.fslope, hb, ptr(z),
+                     dl if hb else None, ptr(self.pp[0]), ptr(self.pp[1]), ptr(self.pp[2]),
+                     ptr(self.port_parts), ptr(self.mean[t]), ptr(self.rstd[t]), ws, nws)
+                call("nc_port_dense_fwd", s, B * self.P, self.G, self.fact, self.fslope,
+                     ptr(self.port_parts), ptr(self.out), ptr(self.pre))
+            else:
+                call("nc_port_fwd", s, B, M, h, w, hb, self.fact, self.fslope, self.P,
+                     ptr(self.port_idx), ptr(z), dl if hb else None, ptr(self.pp), ptr(self.out),
+                     ptr(self.zo), ptr(self.mean[t]), ptr(self.rstd[t]), ptr(self.pre), ws, nws)
+        return self.out
+
+    def _backward_direct(self, s, cell, filt_used, g_out, g_cell, g_filt, codd, g_universe):
+        """Reverse of _forward_direct: the port (or universe) backward, then per step the
+        direct correlation's input and filter gradients and the epilogue backward, the border
+        conv's reverse from the border cotangent, one sum of the filter-gradient rows."""
+        B, M, h, w, d = self.B, self.M, self.h, self.w, self.d
+        kh, kw, K = self.kh, self.kw, self.kh * self.kw
+        circ = int(self.circular)
+        ws, nws = ptr(self.ws_epi), self.ws_epi.numel() * 4
+        valid = int(self.mode == "VALID")
+        t = d - 1
+        hb = int(self.border)
+        dl = ptr(self.delta) if self.border else None
+        gd = ptr(self.gdelta) if self.border else None
+        params_written = False
+        if self.universe:
+            b_full = _addr(self.cell_s if self.sharpen is not None else cell) + 4 * self.H * self.W
+            call("nc_universe_bwd", s, self.chip, B, self.G, valid, self.fact, self.fslope,
+                 ptr(self.port_parts), b_full, ptr(self.s_prob), self.P, ptr(self.port_head),
+                 ptr(self.port_next), ptr(g_out), ptr(g_universe), ptr(self.g_roi),
+                 ptr(self.g_sprob) if valid else None, ptr(self.g_bfull) if valid else None)
+            call("nc_epilogue_bwd", s, B, M, h, w, self.fact, self.fslope, hb, ptr(self.zs[t]),
+                 dl if hb else None, ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
+                 ptr(self.mean[t]), ptr(self.rstd[t]), ptr(self.g_roi), ptr(self.gz),
+                 gd if hb else None, ptr(self.gw), ptr(self.gs), ptr(self.gb), 0, 0, ws, nws)
+            params_written = True
+        elif self.dense_port:
+            gy_port = g_out
+            if self.fact != 0:
+                call("nc_port_dense_bwd", s, B * self.P, self.fact, self.fslope, ptr(self.pre),
+                     ptr(g_out), ptr(self.g_pre))
+                gy_port = self.g_pre
+            call("nc_epilogue_bwd", s, B, M, h, w, self.fact, self.fslope, hb, ptr(self.zs[t]),
+                 dl if hb else None, ptr(self.pp[0]), ptr(self.pp[1]), ptr(self.pp[2]),
+                 ptr(self.mean[t]), ptr(self.rstd[t]), ptr(gy_port), ptr(self.gz),
+                 gd if hb else None, ptr(self.gpp[0]), ptr(self.gpp[1]), ptr(self.gpp[2]), 0, 0,
+                 ws, nws)
+        else:
+            call("nc_port_bwd", s, B, M, h, w, hb, self.fact, self.fslope, self.P,
+                 ptr(self.port_idx), ptr(self.zs[t]), dl if hb else None, ptr(self.pp),
+                 ptr(self.zo), ptr(self.mean[t]), ptr(self.rstd[t]), ptr(self.pre), ptr(g_out),
+                 ptr(self.gz), gd if hb else None, ptr(self.gpp) if self.n_pp else None, 0, ws,
+                 nws)
+        rows = _addr(self.dg_rows)
+        step_bytes = 4 * self.dg_step_rows * M * K
+        for t in range(d - 1, -1, -1):
+            gy = self.gy[t % 2]
+            x, n_parts, hin, win, oh, ow = self._conv_input(t)
+            call("nc_direct_conv_bwd", s, B, M, hin, win, h, w, oh, ow, kh, kw, circ,
+                 ptr(self.gz), ptr(x), n_parts, ptr(filt_used), int(t > 0),
+                 ptr(gy) if t > 0 else None, rows + t * step_bytes)
+            if t == 0:
+                break
+            te = t - 1
+            hbe = int(self.border and te > 0)
+            call("nc_epilogue_bwd", s, B, M, h, w, self.act, self.slope, hbe, ptr(self.zs[te]),
+                 dl if hbe else None, ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
+                 ptr(self.mean[te]), ptr(self.rstd[te]), ptr(gy), ptr(self.gz),
+                 gd if hbe else None, ptr(self.gw), ptr(self.gs), ptr(self.gb),
+                 int(params_written), 1, ws, nws)
+            params_written = True
+        if self.border:  # the border conv's reverse: patch gradient and its filter rows
+            call("nc_direct_conv_bwd", s, 1, M, self.Hp, self.Wp, h, w, 0, 0, kh, kw, 0,
+                 ptr(self.gdelta), ptr(self.patch), 1, ptr(filt_used), 1, ptr(self.gpatch),
+                 rows + d * step_bytes)
+        call("nc_rows_sum", s, 1, _abi.rows_jobs((rows, _addr(g_filt), M * K, 0,
+                                                  self.dg_rows.shape[0])))
+        if self.gated:
+            call("nc_filter_gate_bwd", s, self.filt_g.numel(), ptr(self.filt_g), ptr(g_filt))
+        mode, inv_tau, active_threshold = codd
+        sharp = self.sharpen is not None
+        call("nc_codd_fuse_bwd", s, self.chip, ptr(self.cell_s if sharp else cell),
+             ptr(self.io_mask), ptr(self.owm), mode, inv_tau, active_threshold,
+             int(self.hard_pin_io), self.act, self.slope, self.n_pp, ptr(self.port_rc),
+             ptr(self.gw) if params_written else None, ptr(self.gs) if params_written else None,
+             ptr(self.gb) if params_written else None, ptr(self.gpatch) if self.border else None,
+             ptr(self.gpp) if self.n_pp else None,
+             ptr(self.g_sprob) if self.universe and valid else None,
+             ptr(self.g_bfull) if self.universe and valid else None,
+             ptr(self.g_cell_s if sharp else g_cell))
+        if sharp:
+            self._sharpen_bwd(s, g_cell)
+
+    def _sharpen_bwd(self, s, g_cell):
+        """The sharpening's adjoint on the weights' gradient."""
+        ks = self.sharpen.shape
+        g_cell[1:].copy_(self.g_cell_s[1:])
+        call("nc_fftconv_bwd", s, 1, 1, self.H, self.W, self.H, self.W, (ks[0] - 1) // 2,
+             (ks[1] - 1) // 2, *self.sh_fft, ptr(self.g_cell_s[0]), ptr(self.sh_xhat),
+             ptr(self.sh_ghat), 1, ptr(g_cell[0]), ptr(self.sh_dg), 0, 0, ptr(self.sh_ws),
+             self.sh_ws.numel() * 4)
+
     # ------------------------------------------------------------------ reverse
     def backward(self, cell: torch.Tensor, filt: torch.Tensor, g_out: torch.Tensor | None,
                  g_cell: torch.Tensor, g_filt: torch.Tensor, codd_mode: str = "continuous",
@@ -480,6 +730,10 @@ class StepPlan:
         if not self.training:
             raise NeurocellError("plan was built for evaluation only")
         s = stream_ptr()
+        if self.direct:
+            return self._backward_direct(s, cell, self.filt_g if self.gated else filt, g_out,
+                                         g_cell, g_filt, (_abi.CODD_IDS[codd_mode], inv_tau,
+                                                          active_threshold), g_universe)
         B, M, h, w, d = self.B, self.M, self.h, self.w, self.d
         fh, fw = self.fft
         ws_ep, n_ep = ptr(self.ws_epi), self.ws_epi.numel() * 4
@@ -584,13 +838,8 @@ class StepPlan:
              ptr(self.g_sprob) if self.universe and valid else None,
              ptr(self.g_bfull) if self.universe and valid else None,
              ptr(self.g_cell_s if sharp else g_cell))
-        if sharp:  # the sharpening's adjoint on the weights' gradient
-            ks = self.sharpen.shape
-            g_cell[1:].copy_(self.g_cell_s[1:])
-            call("nc_fftconv_bwd", s, 1, 1, self.H, self.W, self.H, self.W, (ks[0] - 1) // 2,
-                 (ks[1] - 1) // 2, *self.sh_fft, ptr(self.g_cell_s[0]), ptr(self.sh_xhat),
-                 ptr(self.sh_ghat), 1, ptr(g_cell[0]), ptr(self.sh_dg), 0, 0, ptr(self.sh_ws),
-                 self.sh_ws.numel() * 4)
+        if sharp:
+            self._sharpen_bwd(s, g_cell)
 
     # ------------------------------------------------------------------ loss
     def mse(self, target: torch.Tensor, loss: torch.Tensor | None = None) -> torch.Tensor:
@@ -608,7 +857,6 @@ def _addr(t: torch.Tensor) -> int:
 
 
 def _abi_int(name: str, *args) -> int:
-    from ._lib import lib
     v = int(getattr(lib(), name)(*args))
     if v <= 0:
         raise NeurocellError(f"{name}{args} failed")

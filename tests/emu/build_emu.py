@@ -11,7 +11,7 @@ CSRC = os.path.join(ROOT, "neurocell-v2_amd", "csrc")
 OUT_DIR = os.path.join(HERE, "_build")
 LIB = os.path.join(OUT_DIR, "libnc_emu.so")
 SOURCES = [os.path.join(CSRC, f) for f in ("nc_codd.hip", "nc_epilogue.hip", "nc_spectral.hip",
-                                                   "nc_spectral_large.hip")]
+                                                   "nc_spectral_large.hip", "nc_direct.hip")]
 FLAGS = ["g++", "-std=c++20", "-O1", "-fPIC", "-pthread", "-I", HERE]
 
 

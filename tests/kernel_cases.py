@@ -853,6 +853,51 @@ def case_spectral_ops(be, n=3, FH=32, FW=16, roi=(12, 10), pad=(5, 3), shift=(7,
     return res
 
 
+def case_direct_conv(be, B=3, M=5, H=12, W=14, kh=3, kw=3, mode="SAME", n_parts=2, seed=12):
+    """Direct small-filter correlation forward, input and filter gradients against the
+    oracle's brute-force correlations: SAME (zero padding), VALID and CIRCULAR (wrap), with
+    the input given as partial planes."""
+    rng = np.random.default_rng(seed)
+    L, s = be.lib, be.stream()
+    parts = rng.normal(size=(n_parts, B, H, W)).astype(np.float32)
+    x = parts.astype(np.float64).sum(0)
+    g = rng.normal(size=(M, 1, kh, kw)).astype(np.float32)
+    if mode == "VALID":
+        ho, wo, oh, ow = H - kh + 1, W - kw + 1, 0, 0
+    else:
+        ho, wo, oh, ow = H, W, -((kh - 1) // 2), -((kw - 1) // 2)
+    circ = int(mode == "CIRCULAR")
+    gz = rng.normal(size=(B, M, ho, wo)).astype(np.float32)
+    xd, gd, gzd = be.put(parts), be.put(g), be.put(gz)
+    z, dx = be.zeros((B, M, ho, wo)), be.zeros((B, H, W))
+    R = L.nc_direct_conv_dg_partials(B, M, ho, wo, kh, kw)
+    part = be.zeros((R, M * kh * kw))
+    _ok(be, L.nc_direct_conv_fwd(s, B, M, H, W, ho, wo, oh, ow, kh, kw, circ, be.ptr(xd),
+                                 n_parts, be.ptr(gd), be.ptr(z)), "dconv_fwd")
+    _ok(be, L.nc_direct_conv_bwd(s, B, M, H, W, ho, wo, oh, ow, kh, kw, circ, be.ptr(gzd),
+                                 be.ptr(xd), n_parts, be.ptr(gd), 1, be.ptr(dx), be.ptr(part)),
+        "dconv_bwd")
+    dg = be.zeros((M * kh * kw,))
+    a = lambda t: be.ptr(t).value
+    _ok(be, L.nc_rows_sum(s, 1, _abi.rows_jobs((a(part), a(dg), M * kh * kw, 0, R))), "rows_sum")
+    with O.precision(np.float64):
+        if mode == "CIRCULAR":
+            r_z = O.conv2d_circular_direct(x, g[:, 0], (-oh, -ow))
+            # the circular correlation's adjoints: the same wrap on the padded input
+            xp = np.pad(x, ((0, 0), (-oh, -oh), (-ow, -ow)), mode="wrap")
+            r_dxp, r_dg = O.conv2d_bwd_direct(gz, xp, g[:, 0], (0, 0))
+            r_dx = np.zeros_like(x)
+            Hp, Wp = xp.shape[1:]
+            for i in range(Hp):
+                for j in range(Wp):
+                    r_dx[:, (i + oh) % H, (j + ow) % W] += r_dxp[:, i, j]
+        else:
+            r_z = O.conv2d_direct(x, g[:, 0], (-oh, -ow))
+            r_dx, r_dg = O.conv2d_bwd_direct(gz, x, g[:, 0], (-oh, -ow))
+    return {"z": rel_l2(be.get(z), r_z), "dx": rel_l2(be.get(dx), r_dx),
+            "dg": rel_l2(be.get(dg).reshape(M, kh, kw), r_dg)}
+
+
 def case_helpers(be, seed=6):
     """Input injection (exact), MSE loss and three AdamW steps."""
     rng = np.random.default_rng(seed)

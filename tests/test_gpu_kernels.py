@@ -6,7 +6,7 @@ from kernel_cases import (CODD_CASES, EPILOGUE_SHAPES, PORT_SHAPES, TOL, DeviceB
                           case_epilogue, case_epilogue_parts,
                           case_fftconv_circular, case_fftconv_port, case_fftconv_epilogue,
                           case_fftconv, case_helpers, case_plane_spectra, case_port,
-                          case_spectral_ops,
+                          case_spectral_ops, case_direct_conv,
                           case_universe)
 
 pytestmark = pytest.mark.gpu
@@ -168,3 +168,11 @@ def test_universe(be, pmode, bbox, fact):
                                                  (256, 128, (200, 100), (30, 20), (255, 3))])
 def test_spectral_ops(be, FH, FW, roi, pad, shift):
     _assert_small(case_spectral_ops(be, FH=FH, FW=FW, roi=roi, pad=pad, shift=shift))
+
+
+@pytest.mark.parametrize("B,M,H,W,kh,kw,mode,n_parts", [
+    (3, 5, 12, 14, 3, 3, "SAME", 2), (2, 4, 16, 16, 3, 3, "CIRCULAR", 1),
+    (2, 3, 20, 18, 5, 3, "VALID", 1), (2, 16, 32, 32, 3, 3, "SAME", 4),
+    (1, 2, 9, 40, 17, 3, "SAME", 1), (2, 3, 16, 16, 3, 5, "CIRCULAR", 2)])
+def test_direct_conv(be, B, M, H, W, kh, kw, mode, n_parts):
+    _assert_small(case_direct_conv(be, B, M, H, W, kh, kw, mode, n_parts))

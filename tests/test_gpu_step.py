@@ -19,12 +19,13 @@ GRAD_TOL = 1e-4
 
 
 def run_plan(topo, cell, filt, x, g_out, mode="continuous", tau=1.0, bbox=None,
-             final_act=None, hard_pin=False):
+             final_act=None, hard_pin=False, conv="auto"):
     from neurocell.engine import StepPlan, flatten_inputs, inv_tau_f32, port_input_shapes
     dev = torch.device("cuda")
     xt = torch.from_numpy(x).to(dev)
     plan = StepPlan(topo, x.shape[0], port_input_shapes(xt, topo), roi_bbox=bbox,
-                    final_activate=final_act, hard_pin_io=hard_pin, training=True)
+                    final_activate=final_act, hard_pin_io=hard_pin, training=True, conv=conv)
+    assert conv == "auto" or plan.direct == (conv == "direct")
     c = torch.from_numpy(cell).to(dev)
     f = torch.from_numpy(filt).to(dev)
     it = inv_tau_f32(tau)
@@ -37,11 +38,13 @@ def run_plan(topo, cell, filt, x, g_out, mode="continuous", tau=1.0, bbox=None,
     return out.cpu().numpy(), gc.cpu().numpy(), gf.cpu().numpy()
 
 
-def check(geom, topo, cell, filt, x, mode, tau, bbox, final_act=None, hard_pin=False, seed=0):
+def check(geom, topo, cell, filt, x, mode, tau, bbox, final_act=None, hard_pin=False, seed=0,
+          conv="auto"):
     B = x.shape[0]
     rng = np.random.default_rng(seed + 100)
     g_out = rng.normal(size=(B,) + geom.out_size).astype(np.float32)
-    out, gc, gf = run_plan(topo, cell, filt, x, g_out, mode, tau, bbox, final_act, hard_pin)
+    out, gc, gf = run_plan(topo, cell, filt, x, g_out, mode, tau, bbox, final_act, hard_pin,
+                           conv)
     r_out, r_gc, r_gf = O.propagate_vjp(cell, filt, x, geom, g_out, act="tanh",
                                         final_act=final_act, hard_pin_io=hard_pin,
                                         roi_bbox=bbox, mode=mode, tau=tau)
@@ -135,22 +138,46 @@ def _mode_case(mode, grid, kernel, M, depth, B=4, seed=30):
     return geom, topo, cell, filt, x
 
 
-@pytest.mark.parametrize("mode,grid,kernel,M,depth", [
-    ("SAME", (16, 16), (5, 3), 3, 3),        # spectral grid 32x32, wavefront transforms
-    ("CIRCULAR", (16, 16), (5, 3), 3, 3),    # the 16x16 grid itself
-    ("CIRCULAR", (32, 64), (7, 5), 6, 3),    # lane pairs, fused epilogue, wrapped windows
-    ("SAME", (32, 32), (23, 13), 16, 3),     # spectral grid 64x64
-    ("CIRCULAR", (64, 64), (9, 9), 4, 2),    # the 64x64 grid itself
+@pytest.mark.parametrize("mode,grid,kernel,M,depth,conv", [
+    ("SAME", (16, 16), (5, 3), 3, 3, "spectral"),      # spectral grid 32x32, wavefront transforms
+    ("SAME", (16, 16), (5, 3), 3, 3, "direct"),
+    ("CIRCULAR", (16, 16), (5, 3), 3, 3, "spectral"),  # the 16x16 grid itself
+    ("CIRCULAR", (16, 16), (5, 3), 3, 3, "direct"),    # wrapped direct windows
+    ("CIRCULAR", (32, 64), (7, 5), 6, 3, "spectral"),  # lane pairs, fused epilogue
+    ("CIRCULAR", (32, 64), (7, 5), 6, 3, "direct"),
+    ("VALID", (32, 64), (7, 9), 5, 3, "direct"),       # border conv, K = 63
+    ("SAME", (32, 32), (23, 13), 16, 3, "auto"),       # spectral grid 64x64
+    ("CIRCULAR", (64, 64), (9, 9), 4, 2, "auto"),      # the 64x64 grid itself
 ])
-def test_padding_mode_step_parity(mode, grid, kernel, M, depth):
-    """SAME and CIRCULAR padding modes (propagator.py:276-341): whole-grid ROI, no border
-    term; CIRCULAR wraps the correlation round the grid."""
+def test_padding_mode_step_parity(mode, grid, kernel, M, depth, conv):
+    """SAME, CIRCULAR and VALID padding modes (propagator.py:276-341): whole-grid ROI, no
+    border term for SAME / CIRCULAR, CIRCULAR wrapping the correlation round the grid; small
+    filters through both the spectral and the direct correlation."""
     geom, topo, cell, filt, x = _mode_case(mode, grid, kernel, M, depth)
-    check(geom, topo, cell, filt, x, "continuous", 1.0, None)
+    check(geom, topo, cell, filt, x, "continuous", 1.0, None, conv=conv)
 
 
+@pytest.mark.parametrize("kernel,bbox,mode,conv", [
+    ((7, 7), None, "continuous", "direct"),             # inputs outside the ROI: full-grid t=0
+    ((7, 7), None, "continuous", "spectral"),
+    ((5, 9), None, "ste_binary", "direct"),             # border conv + ROI steps
+    ((5, 9), (1, 25, 3, 26), "annealed", "direct"),     # cropped sub-ROI
+    ((5, 9), (1, 25, 3, 26), "annealed", "spectral"),
+])
+def test_small_kernel_alu_parity(kernel, bbox, mode, conv):
+    """The ALU chip with small filters (kh * kw <= 64, where the reference takes its direct
+    conv, propagator.py:373-386) through both correlation paths: VALID border term, the gathered
+    output port, the full-grid first step and a cropped sub-ROI."""
+    from neurocell.topology import ChipTopology2D
+    geom, cell, filt, x, _ = alu_case(7, B=8, kernel_size=kernel)
+    topo = ChipTopology2D.alu_chip(kernel_size=kernel, out_width=2)
+    check(geom, topo, cell, filt, x, mode, 0.1 if mode != "continuous" else 1.0, bbox,
+          conv=conv)
+
+
+@pytest.mark.parametrize("conv", ["spectral", "direct"])
 @pytest.mark.parametrize("mode,n", [("VALID", 8), ("CIRCULAR", 16), ("SAME", 8)])
-def test_clp_chip_parity(mode, n):
+def test_clp_chip_parity(mode, n, conv):
     """The coordinate-addressed CLP chip (topology.py:391-428; one direction, depth 4, 3x3
     filters) on its default 8x8 grid (spectral grid 8 raised to 16) and circular at 16x16."""
     from neurocell.topology import ChipTopology2D
@@ -163,16 +190,17 @@ def test_clp_chip_parity(mode, n):
                      rng.normal(0, 1.0, (H, W))]).astype(np.float32)
     filt = rng.normal(0, 1.0 / 3.0, (1, 1, 3, 3)).astype(np.float32)
     x = (rng.random((8, 2)) > 0.5).astype(np.float32)
-    check(geom, topo, cell, filt, x, "continuous", 1.0, None)
+    check(geom, topo, cell, filt, x, "continuous", 1.0, None, conv=conv)
 
 
+@pytest.mark.parametrize("conv", ["spectral", "direct"])
 @pytest.mark.parametrize("mode,n,final_act,act", [
     ("SAME", 32, "sigmoid", "tanh"),         # spectral grid 64x64: fused kernels, P = 1024
     ("CIRCULAR", 32, None, "leaky_relu"),    # the 32x32 grid itself: one-lane transforms
     ("CIRCULAR", 64, "sigmoid", "tanh"),     # the 64x64 grid itself, P = 4096
     ("SAME", 64, "sigmoid", "tanh"),         # spectral grid 128x128: workgroup transforms
 ])
-def test_gol_chip_parity(mode, n, final_act, act):
+def test_gol_chip_parity(mode, n, final_act, act, conv):
     """The Game-of-Life chip (topology.py:359-388, as unit_milestone6_general_vnn.py:114-160:
     K = 3x3, M = 16, depth 4, sigmoid output, biases N(0, 0.2)): its universe port is the whole
     grid, run as the dense port (the hidden epilogue with the port parameters)."""
@@ -187,8 +215,8 @@ def test_gol_chip_parity(mode, n, final_act, act):
                      rng.normal(0, 1.0, (n, n))]).astype(np.float32)
     filt = rng.normal(0, 1.0 / 3.0, (16, 1, 3, 3)).astype(np.float32)
     x = (rng.random((4, n, n)) > 0.5).astype(np.float32)
-    plan = StepPlan(topo, 4, [(n, n)], activate=act, final_activate=final_act)
-    assert plan.dense_port and plan.P == n * n
+    plan = StepPlan(topo, 4, [(n, n)], activate=act, final_activate=final_act, conv=conv)
+    assert plan.dense_port and plan.P == n * n and plan.direct == (conv == "direct")
     B = x.shape[0]
     g_out = rng.normal(size=(B, n, n)).astype(np.float32)
     dev = torch.device("cuda")
@@ -209,7 +237,7 @@ def test_gol_chip_parity(mode, n, final_act, act):
 
 
 def _universe_check(geom, topo, cell, filt, x, act="tanh", final_act=None, bbox=None,
-                    want_universe=True, seed=40):
+                    want_universe=True, seed=40, conv="auto"):
     """The full-grid output path (propagator.py:684-734) through StepPlan: the port, the final
     universe and the gradients for cotangents on both, against the oracle."""
     from neurocell.engine import StepPlan, flatten_inputs, port_input_shapes
@@ -217,8 +245,8 @@ def _universe_check(geom, topo, cell, filt, x, act="tanh", final_act=None, bbox=
     B = x.shape[0]
     xt = torch.from_numpy(x).to(dev)
     plan = StepPlan(topo, B, port_input_shapes(xt, topo), roi_bbox=bbox, activate=act,
-                    final_activate=final_act, universe=want_universe)
-    assert plan.universe
+                    final_activate=final_act, universe=want_universe, conv=conv)
+    assert plan.universe and (conv == "auto" or plan.direct == (conv == "direct"))
     rng = np.random.default_rng(seed)
     g_out = rng.normal(size=(B,) + geom.out_size).astype(np.float32)
     H, W = geom.grid_shape
@@ -246,8 +274,9 @@ def _universe_check(geom, topo, cell, filt, x, act="tanh", final_act=None, bbox=
     return errs
 
 
+@pytest.mark.parametrize("conv", ["spectral", "direct"])
 @pytest.mark.parametrize("final_act,act", [("sigmoid", "tanh"), (None, "leaky_relu")])
-def test_gol_valid_universe_port_parity(final_act, act):
+def test_gol_valid_universe_port_parity(final_act, act, conv):
     """VALID Game of Life (topology.py:359-388 with allow_border_output): the inputs cover the
     grid (the full-grid step 0) and the universe port is read from the final universe, border
     cells final_act(final_act(B) * s_prob) included."""
@@ -260,21 +289,23 @@ def test_gol_valid_universe_port_parity(final_act, act):
                      rng.normal(0, 1.0, (n, n))]).astype(np.float32)
     filt = rng.normal(0, 1.0 / 3.0, (16, 1, 3, 3)).astype(np.float32)
     x = (rng.random((4, n, n)) > 0.5).astype(np.float32)
-    _universe_check(geom, topo, cell, filt, x, act, final_act, want_universe=False)
+    _universe_check(geom, topo, cell, filt, x, act, final_act, want_universe=False, conv=conv)
 
 
+@pytest.mark.parametrize("conv", ["spectral", "direct"])
 @pytest.mark.parametrize("mode,bbox,final_act", [
     ("VALID", None, "tanh"), ("VALID", (0, 11, 1, 11), "sigmoid"), ("VALID", None, None),
     ("SAME", None, "sigmoid"), ("SAME", (1, 14, 0, 13), None), ("CIRCULAR", None, "tanh")])
-def test_return_universe_parity(mode, bbox, final_act):
+def test_return_universe_parity(mode, bbox, final_act, conv):
     """return_universe=True (propagator.py:684-734): the universe and the port read from it,
     with a cropped sub-ROI (VALID: the ROI cells outside the crop take the border value; SAME:
     zeros), and gradients for cotangents on the universe and the port."""
     geom, topo, cell, filt, x = _mode_case(mode, (16, 16), (5, 3), 3, 3)
-    _universe_check(geom, topo, cell, filt, x, "tanh", final_act, bbox=bbox)
+    _universe_check(geom, topo, cell, filt, x, "tanh", final_act, bbox=bbox, conv=conv)
 
 
-def test_clp_border_output_parity():
+@pytest.mark.parametrize("conv", ["spectral", "direct"])
+def test_clp_border_output_parity(conv):
     """A CLP chip (topology.py:391-428, allow_border_output) whose output coordinates lie on the
     VALID border: the port is read from the final universe."""
     from neurocell.topology import ChipTopology2D
@@ -288,4 +319,71 @@ def test_clp_border_output_parity():
                      rng.normal(0, 1.0, (8, 8))]).astype(np.float32)
     filt = rng.normal(0, 1.0 / 3.0, (1, 1, 3, 3)).astype(np.float32)
     x = (rng.random((8, 2)) > 0.5).astype(np.float32)
-    _universe_check(geom, topo, cell, filt, x, "tanh", "sigmoid", want_universe=False)
+    _universe_check(geom, topo, cell, filt, x, "tanh", "sigmoid", want_universe=False,
+                    conv=conv)
+
+
+def test_direct_eval_graph_replay():
+    """The direct path's evaluation plan (training=False: one z buffer for every step) against
+    the oracle, eager and replayed from a captured HIP graph (bit-equal to eager)."""
+    from neurocell.engine import EvalState, StepPlan, flatten_inputs
+    from neurocell.topology import ChipTopology2D
+    n = 32
+    topo = ChipTopology2D.gol_chip(n=n, kernel_size=(3, 3), directions=16, depth=4,
+                                   padding_mode="SAME")
+    geom = O.Geometry((n, n), (3, 3), 16, 4, [("rect", (0, 0), (n, n))], ("rect", (0, 0), (n, n)),
+                      padding_mode="SAME")
+    rng = np.random.default_rng(35)
+    cell = np.stack([rng.normal(0, 0.1, (n, n)), rng.normal(0, 0.2, (n, n)),
+                     rng.normal(0, 1.0, (n, n))]).astype(np.float32)
+    filt = rng.normal(0, 1.0 / 3.0, (16, 1, 3, 3)).astype(np.float32)
+    x = (rng.random((64, n, n)) > 0.5).astype(np.float32)
+    dev = torch.device("cuda")
+    plan = StepPlan(topo, 64, [(n, n)], final_activate="sigmoid", training=False)
+    assert plan.direct
+    c, f = torch.from_numpy(cell).to(dev), torch.from_numpy(filt).to(dev)
+    ev = EvalState(plan, c, f, "ste_ternary", 0.1)
+    ev.x.copy_(flatten_inputs(torch.from_numpy(x).to(dev), topo))
+    out = ev.run().cpu().numpy()
+    ev.capture()
+    reps = []
+    for _ in range(3):
+        reps.append(ev.run().cpu().numpy())
+        torch.cuda.synchronize()
+    ref, _ = O.propagate(cell, filt, x, geom, final_act="sigmoid", mode="ste_ternary", tau=0.1)
+    assert rel_l2(out, ref.reshape(64, -1)) < FWD_TOL
+    for r in reps:
+        assert np.array_equal(r, out)
+
+
+def test_direct_train_graph_replay():
+    """Train steps on the direct path (the VALID ALU chip with 5x9 filters: border conv,
+    gathered port) launched eagerly and replayed from a captured HIP graph: bit-identical
+    parameters and losses, with unrelated eager work between the replays."""
+    from neurocell.engine import (ParamState, StepPlan, TrainState, flatten_inputs,
+                                  port_input_shapes)
+    from neurocell.topology import ChipTopology2D
+    geom, cell, filt, x, y = alu_case(8, B=8, kernel_size=(5, 9))
+    topo = ChipTopology2D.alu_chip(kernel_size=(5, 9), out_width=2)
+    dev = torch.device("cuda")
+    xt = torch.from_numpy(x).to(dev)
+    res = []
+    for graph in (False, True):
+        plan = StepPlan(topo, 8, port_input_shapes(xt, topo))
+        assert plan.direct and plan.border
+        ps = ParamState(torch.from_numpy(cell).to(dev), torch.from_numpy(filt).to(dev), 0.01)
+        ts = TrainState(plan, ps)
+        ts.x.copy_(flatten_inputs(xt, topo))
+        ts.y.copy_(torch.from_numpy(y.reshape(8, -1)).to(dev))
+        losses = [float(ts.step())]          # eager step 1
+        if graph:
+            ts.capture()                      # the warm-up inside is step 2
+        else:
+            ts.step()
+        for _ in range(3):
+            losses.append(float(ts.step()))
+            torch.cuda.synchronize()
+            _ = torch.ones(1000, device="cuda").sum()
+        res.append((ps.theta.cpu().numpy(), ps.m.cpu().numpy(), np.array(losses)))
+    for a, b in zip(*res):
+        assert np.array_equal(a, b)
