@@ -474,6 +474,73 @@ def run_config(name, args, torch):
     print(json.dumps(rec))
 
 
+def conv_compare(torch, reps=100):
+    """The spectral and the direct correlation on the small-filter chips (kh * kw <= 64): one
+    graph-replayed train step (forward, MSE, reverse, AdamW) and one evaluation forward per
+    path, ms per call; one JSON line per chip.  The data behind StepPlan's conv="auto" rule."""
+    from neurocell.engine import (EvalState, ParamState, StepPlan, TrainState, flatten_inputs,
+                                  port_input_shapes)
+    from neurocell.topology import ChipTopology2D
+    dev = torch.device("cuda")
+
+    def timed(fn):
+        g = _graph_of(fn, torch)
+        for _ in range(3):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return round(e0.elapsed_time(e1) / reps, 4)
+
+    chips = [(f"gol SAME {n}x{n}", ChipTopology2D.gol_chip(n=n, kernel_size=(3, 3), directions=16,
+                                                          depth=4, padding_mode="SAME"), B, (n, n))
+             for n, B in ((32, 128), (64, 128), (32, 512))]
+    chips.append(("gol CIRCULAR 64x64", ChipTopology2D.gol_chip(
+        n=64, kernel_size=(3, 3), directions=16, depth=4, padding_mode="CIRCULAR"), 128, (64, 64)))
+    chips.append(("clp VALID 8x8", ChipTopology2D.clp_chip(n=8), 1024, (2,)))
+    chips += [(f"alu {k[0]}x{k[1]}", ChipTopology2D.alu_chip(kernel_size=k, out_width=2), 128,
+               (3, 8, 1)) for k in ((3, 7), (5, 7), (5, 9), (7, 7), (7, 9))]
+    for name, topo, B, xshape in chips:
+        H, W = topo.grid_shape
+        kh, kw = topo.kernel_size
+        rng = np.random.default_rng(0)
+        cell = torch.from_numpy(np.stack([rng.normal(0, .1, (H, W)), rng.normal(0, .2, (H, W)),
+                                          rng.normal(0, 1, (H, W))]).astype(np.float32)).to(dev)
+        filt = torch.from_numpy(rng.normal(0, 1 / np.sqrt(kh * kw), (topo.directions, 1, kh, kw))
+                                .astype(np.float32)).to(dev)
+        xn = torch.from_numpy((rng.random((B,) + xshape) > .5).astype(np.float32)).to(dev)
+        rec = {"chip": name, "B": B, "K": kh * kw, "M": topo.directions}
+        for conv in ("spectral", "direct"):
+            plan = StepPlan(topo, B, port_input_shapes(xn, topo), training=True, conv=conv)
+            ts = TrainState(plan, ParamState(cell, filt, 1e-3))
+            ts.x.copy_(flatten_inputs(xn, topo))
+            ev = EvalState(StepPlan(topo, B, port_input_shapes(xn, topo), training=False,
+                                    conv=conv), cell, filt)
+            ev.x.copy_(flatten_inputs(xn, topo))
+            rec[conv] = {"train_ms": timed(ts.launch), "eval_ms": timed(ev.launch)}
+        for training, key in ((True, "auto_train"), (False, "auto_eval")):
+            rec[key] = "direct" if StepPlan(topo, B, port_input_shapes(xn, topo),
+                                            training=training).direct else "spectral"
+        print(json.dumps(rec), flush=True)
+
+
+def _graph_of(fn, torch):
+    """fn captured in a HIP graph (after one warm-up launch on a side stream)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -494,6 +561,9 @@ def main():
                     help="summarise rocprofv3 --pmc passes (rocpd databases) of a "
                          "--families-only run into the markdown table --counters-out and exit")
     ap.add_argument("--counters-out", default=os.path.join("gpurun_out", "counters.md"))
+    ap.add_argument("--conv-compare", action="store_true",
+                    help="time the spectral and the direct correlation on the small-filter "
+                         "chips (one JSON line per chip) and exit")
     ap.add_argument("--families-only", action="store_true",
                     help="profiling aid: one eager train step, a 256 MiB device copy (the "
                          "traffic-counter calibration), then --kernel-reps calls of each "
@@ -517,6 +587,9 @@ def main():
     import torch
     if args.config:
         run_config(args.config, args, torch)
+        return
+    if args.conv_compare:
+        conv_compare(torch)
         return
     from neurocell.engine import (EvalState, ParamState, StepPlan, TrainState, flatten_inputs,
                                   port_input_shapes)

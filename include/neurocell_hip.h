@@ -112,14 +112,19 @@ int nc_step_prologue(void* stream, const nc_chip_desc* chip, const float* cell,
  * params.py:58-80).  Any gradient input may be NULL (zero).  g_s_prob and g_b_full (H,W) are
  * full-grid gradients with respect to s_prob (the reverse of the optional s_prob output) and
  * to the cell biases B themselves (the final universe's border term).  Writes g_cell (3,H,W).
+ * port_cell_start (roi_h*roi_w + 1) / port_cell_list (n_port), both NULL or both given: the
+ * port indices by ROI cell (cell o's ports are list[start[o] .. start[o+1]), in increasing
+ * port order), so each cell gathers its port-parameter gradients without scanning port_rc;
+ * the sums are the same either way.
  */
 int nc_codd_fuse_bwd(void* stream, const nc_chip_desc* chip, const float* cell,
                      const uint8_t* io_mask, const uint8_t* out_weight_mask, int codd_mode,
                      float inv_tau, float active_threshold, int hard_pin_io, int act,
-                     float neg_slope, int n_port, const int32_t* port_rc, const float* g_w_eff,
-                     const float* g_s_eff, const float* g_b_roi, const float* g_border_patch,
-                     const float* g_port_params, const float* g_s_prob,
-                     const float* g_b_full, float* g_cell);
+                     float neg_slope, int n_port, const int32_t* port_rc,
+                     const int32_t* port_cell_start, const int32_t* port_cell_list,
+                     const float* g_w_eff, const float* g_s_eff, const float* g_b_roi,
+                     const float* g_border_patch, const float* g_port_params,
+                     const float* g_s_prob, const float* g_b_full, float* g_cell);
 
 /*
  * The final universe and the full-grid output port (propagator.py:684-734, with

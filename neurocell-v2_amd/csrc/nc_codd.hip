@@ -139,7 +139,9 @@ __global__ void k_prologue(nc_chip_desc c, const float* __restrict__ cell,
 __global__ void k_codd_bwd(nc_chip_desc c, const float* __restrict__ cell,
                            const uint8_t* __restrict__ io, const uint8_t* __restrict__ owm,
                            int mode, float inv_tau, float thr, int hard_pin, int act, float slope,
-                           int P, const int* __restrict__ prc, const float* __restrict__ g_weff,
+                           int P, const int* __restrict__ prc,
+                           const int* __restrict__ pc_start, const int* __restrict__ pc_list,
+                           const float* __restrict__ g_weff,
                            const float* __restrict__ g_seff, const float* __restrict__ g_broi,
                            const float* __restrict__ g_patch, const float* __restrict__ g_pp,
                            const float* __restrict__ g_sprob, const float* __restrict__ g_bfull,
@@ -161,12 +163,22 @@ __global__ void k_codd_bwd(nc_chip_desc c, const float* __restrict__ cell,
     }
     if (g_pp && in_roi(c, r, col)) {
         const int rr = r - c.pad_h, cc = col - c.pad_w;
-        for (int k = 0; k < P; ++k)  // fixed order; duplicates of a port cell add up
-            if (prc[k] == rr && prc[P + k] == cc) {
+        if (pc_start) {  // this cell's ports, in increasing port order
+            const int o = rr * c.roi_w + cc;
+            for (int i = pc_start[o]; i < pc_start[o + 1]; ++i) {
+                const int k = pc_list[i];
                 gw += g_pp[k];
                 gs += g_pp[P + k];
                 gb += g_pp[2 * P + k];
             }
+        } else {
+            for (int k = 0; k < P; ++k)  // fixed order; duplicates of a port cell add up
+                if (prc[k] == rr && prc[P + k] == cc) {
+                    gw += g_pp[k];
+                    gs += g_pp[P + k];
+                    gb += g_pp[2 * P + k];
+                }
+        }
     }
     const int Hp = h + c.kh - 1, Wp = w + c.kw - 1;
     const int pi = r - c.r0, pj = col - c.c0;
@@ -588,18 +600,20 @@ int nc_codd_fuse_fwd(void* stream, const nc_chip_desc* chip, const float* cell,
 int nc_codd_fuse_bwd(void* stream, const nc_chip_desc* chip, const float* cell,
                      const uint8_t* io_mask, const uint8_t* out_weight_mask, int codd_mode,
                      float inv_tau, float active_threshold, int hard_pin_io, int act,
-                     float neg_slope, int n_port, const int32_t* port_rc, const float* g_w_eff,
-                     const float* g_s_eff, const float* g_b_roi, const float* g_border_patch,
-                     const float* g_port_params, const float* g_s_prob, const float* g_b_full,
-                     float* g_cell) {
+                     float neg_slope, int n_port, const int32_t* port_rc,
+                     const int32_t* port_cell_start, const int32_t* port_cell_list,
+                     const float* g_w_eff, const float* g_s_eff, const float* g_b_roi,
+                     const float* g_border_patch, const float* g_port_params,
+                     const float* g_s_prob, const float* g_b_full, float* g_cell) {
     if (!chip_ok(chip) || !cell || !io_mask || !out_weight_mask || codd_mode < 0 ||
         codd_mode > 3 || act < 0 || act > 5 || n_port < 0 || (n_port > 0 && !port_rc) ||
-        !g_cell)
+        !g_cell || (!port_cell_start != !port_cell_list))
         return NC_ERR_INVALID_ARGUMENT;
     const int n = chip->H * chip->W;
     hipLaunchKernelGGL(k_codd_bwd, dim3((n + 255) / 256), dim3(256), 0, nc_stream(stream), *chip,
                        cell, io_mask, out_weight_mask, codd_mode, inv_tau, active_threshold,
-                       hard_pin_io, act, neg_slope, n_port, port_rc, g_w_eff, g_s_eff, g_b_roi,
+                       hard_pin_io, act, neg_slope, n_port, port_rc, port_cell_start,
+                       port_cell_list, g_w_eff, g_s_eff, g_b_roi,
                        g_border_patch, n_port > 0 ? g_port_params : nullptr, g_s_prob,
                        g_b_full, g_cell);
     NC_CHECK_LAUNCH();

@@ -66,7 +66,7 @@ _SIGS = {
     "nc_codd_fuse_fwd": (I, [P, C.POINTER(ChipDesc), P, P, P, I, F, F, I, I, F, I, P, P, P, P,
                              P, P, P, P, P]),
     "nc_codd_fuse_bwd": (I, [P, C.POINTER(ChipDesc), P, P, P, I, F, F, I, I, F, I, P, P, P, P,
-                             P, P, P, P, P]),
+                             P, P, P, P, P, P, P]),
     "nc_step_prologue": (I, [P, C.POINTER(ChipDesc), P, P, P, I, F, F, I, I, F, I, P, P, P, P,
                              P, P, P, I, I, P, I, P, P]),
     "nc_universe_fwd": (I, [P, C.POINTER(ChipDesc), I, I, I, I, F, P, P, P, I, P, P, P]),

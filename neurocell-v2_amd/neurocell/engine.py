@@ -39,7 +39,13 @@ from ._lib import NeurocellError, call, lib, ptr, stream_ptr, require_device
 from .topology import ChipTopology2D, CoordinatePortSpec
 
 _WAVE_FFT = (16, 32, 64)        # wavefront transforms (a plane per lane group)
-_DIRECT_MAX_K = 64              # filters up to this many taps run the direct correlation
+# filters up to this many taps run the direct correlation (the reference's rule,
+# propagator.py:373-386); a train step only up to 36 taps and with at least 4 directions, where
+# its spatial reverse (input and filter gradients) measured faster than the spectral one on
+# MI355X (bench.py --conv-compare)
+_DIRECT_MAX_K = 64
+_DIRECT_MAX_K_TRAIN = 36
+_DIRECT_MIN_M_TRAIN = 4
 _LARGE_FFT = (64, 128, 256)     # workgroup transforms over LDS segments
 
 
@@ -173,7 +179,9 @@ class StepPlan:
         if conv == "direct" and not direct_ok:
             raise NeurocellError("the direct correlation takes kh * kw <= 64, M <= 64 and "
                                  "planes up to 256 wide whose bands fit the workgroup's LDS")
-        self.direct = conv == "direct" or (conv == "auto" and direct_ok)
+        auto = (kh * kw <= _DIRECT_MAX_K_TRAIN and M >= _DIRECT_MIN_M_TRAIN
+                if self.training else True)
+        self.direct = conv == "direct" or (conv == "auto" and direct_ok and auto)
         if self.direct:
             if self.circular and self.cropped:
                 raise NeurocellError("adaptive crops are not supported in CIRCULAR mode")
@@ -236,6 +244,12 @@ class StepPlan:
             raise NeurocellError("output port lies outside the active sub-ROI")
         self.n_pp = int(rows.size)  # cells with port parameters (the port path's)
         self.port_rc = torch.tensor(np.stack([rows, cols]).astype(np.int32), device=dev)
+        # the port indices by ROI cell, for the reverse's gather of port-parameter gradients
+        cell_of = (rows * roi_w + cols).astype(np.int64)
+        order = np.argsort(cell_of, kind="stable")
+        start = np.searchsorted(cell_of[order], np.arange(roi_h * roi_w + 1))
+        self.pp_start = torch.tensor(start.astype(np.int32), device=dev)
+        self.pp_list = torch.tensor(order.astype(np.int32), device=dev)
         flat = ((rows - r0) * w + (cols - c0)).astype(np.int32)
         self.port_idx = torch.tensor(flat, device=dev)
         # a port that is the whole (sub-)ROI in row-major order (the Game-of-Life universe
@@ -701,14 +715,18 @@ class StepPlan:
         call("nc_codd_fuse_bwd", s, self.chip, ptr(self.cell_s if sharp else cell),
              ptr(self.io_mask), ptr(self.owm), mode, inv_tau, active_threshold,
              int(self.hard_pin_io), self.act, self.slope, self.n_pp, ptr(self.port_rc),
-             ptr(self.gw) if params_written else None, ptr(self.gs) if params_written else None,
-             ptr(self.gb) if params_written else None, ptr(self.gpatch) if self.border else None,
-             ptr(self.gpp) if self.n_pp else None,
+             *self._pp_csr(), ptr(self.gw) if params_written else None,
+             ptr(self.gs) if params_written else None, ptr(self.gb) if params_written else None,
+             ptr(self.gpatch) if self.border else None, ptr(self.gpp) if self.n_pp else None,
              ptr(self.g_sprob) if self.universe and valid else None,
              ptr(self.g_bfull) if self.universe and valid else None,
              ptr(self.g_cell_s if sharp else g_cell))
         if sharp:
             self._sharpen_bwd(s, g_cell)
+
+    def _pp_csr(self):
+        """The port-by-cell lists for nc_codd_fuse_bwd (none without port parameters)."""
+        return (ptr(self.pp_start), ptr(self.pp_list)) if self.n_pp else (None, None)
 
     def _sharpen_bwd(self, s, g_cell):
         """The sharpening's adjoint on the weights' gradient."""
@@ -833,8 +851,9 @@ class StepPlan:
         call("nc_codd_fuse_bwd", s, self.chip, ptr(self.cell_s if sharp else cell),
              ptr(self.io_mask), ptr(self.owm), mode, inv_tau, active_threshold,
              int(self.hard_pin_io), self.act, self.slope, self.n_pp, ptr(self.port_rc),
-             ptr(self.gw) if has_epi else None, ptr(self.gs) if has_epi else None,
-             ptr(self.gb) if has_epi else None, g_patch, ptr(self.gpp) if self.n_pp else None,
+             *self._pp_csr(), ptr(self.gw) if has_epi else None,
+             ptr(self.gs) if has_epi else None, ptr(self.gb) if has_epi else None, g_patch,
+             ptr(self.gpp) if self.n_pp else None,
              ptr(self.g_sprob) if self.universe and valid else None,
              ptr(self.g_bfull) if self.universe and valid else None,
              ptr(self.g_cell_s if sharp else g_cell))

@@ -190,8 +190,8 @@ class _CoddFuse(torch.autograd.Function):
         c = lambda t: None if t is None else t.contiguous()
         call("nc_codd_fuse_bwd", stream_ptr(), geo.chip, ptr(cell), ptr(geo.io), ptr(geo.owm),
              _abi.CODD_IDS[mode], inv_tau, thr, int(hard_pin), act, slope, geo.P,
-             ptr(geo.port_rc), ptr(c(g_weff)), ptr(c(g_seff)), ptr(c(g_broi)), ptr(c(g_patch)),
-             ptr(c(g_pp)), None, None, ptr(g_cell))
+             ptr(geo.port_rc), None, None, ptr(c(g_weff)), ptr(c(g_seff)), ptr(c(g_broi)),
+             ptr(c(g_patch)), ptr(c(g_pp)), None, None, ptr(g_cell))
         return g_cell, None, None, None, None, None, None, None
 
 

@@ -696,9 +696,21 @@ def case_codd(be, mode="continuous", bbox=None, hard_pin=0, tau=0.1, seed=4):
     gspd, gbfd = be.put(gsp), be.put(gbf)  # held: a device tensor must outlive the launch
     gcell = be.zeros((3, H, W))
     _ok(be, L.nc_codd_fuse_bwd(s, C.byref(chip), be.ptr(cd), be.ptr(io), be.ptr(owm), mid, it,
-                               0.6, hard_pin, 1, 0.01, P, be.ptr(prc), *[be.ptr(a) for a in gid],
-                               be.ptr(gpd), be.ptr(gppd), be.ptr(gspd), be.ptr(gbfd),
-                               be.ptr(gcell)), "coddb")
+                               0.6, hard_pin, 1, 0.01, P, be.ptr(prc), None, None,
+                               *[be.ptr(a) for a in gid], be.ptr(gpd), be.ptr(gppd), be.ptr(gspd),
+                               be.ptr(gbfd), be.ptr(gcell)), "coddb")
+    # the same with the ports listed by ROI cell (the step executor's form): equal bit for bit
+    prc_h = be.get(prc).astype(np.int64)
+    cell_of = prc_h[0] * geom.roi_shape[1] + prc_h[1]
+    order = np.argsort(cell_of, kind="stable")
+    start = np.searchsorted(cell_of[order], np.arange(geom.roi_shape[0] * geom.roi_shape[1] + 1))
+    std, lsd = be.put(start.astype(np.int32), np.int32), be.put(order.astype(np.int32), np.int32)
+    gcell2 = be.zeros((3, H, W))
+    _ok(be, L.nc_codd_fuse_bwd(s, C.byref(chip), be.ptr(cd), be.ptr(io), be.ptr(owm), mid, it,
+                               0.6, hard_pin, 1, 0.01, P, be.ptr(prc), be.ptr(std), be.ptr(lsd),
+                               *[be.ptr(a) for a in gid], be.ptr(gpd), be.ptr(gppd), be.ptr(gspd),
+                               be.ptr(gbfd), be.ptr(gcell2)), "coddb_csr")
+    pro_bad += int((be.get(gcell2) != be.get(gcell)).sum())
     gbd = np.zeros((H, W))
     gbd[r0:r0 + gpatch.shape[0], c0:c0 + gpatch.shape[1]] = gpatch
     gbd[geom.pad_h:H - geom.pad_h, geom.pad_w:W - geom.pad_w] = 0

@@ -162,6 +162,10 @@ def test_spectral_ops(be, FH, FW, roi, pad, shift):
 @pytest.mark.parametrize("B,M,H,W,kh,kw,mode,n_parts", [
     (3, 5, 12, 14, 3, 3, "SAME", 2), (2, 4, 16, 16, 3, 3, "CIRCULAR", 1),
     (2, 3, 20, 18, 5, 3, "VALID", 1), (2, 16, 32, 32, 3, 3, "SAME", 4),
-    (1, 2, 9, 40, 17, 3, "SAME", 1), (2, 3, 16, 16, 3, 5, "CIRCULAR", 2)])
+    (1, 2, 9, 40, 17, 3, "SAME", 1), (2, 3, 16, 16, 3, 5, "CIRCULAR", 2),
+    (2, 1, 8, 8, 3, 3, "VALID", 1),          # one direction (a one-direction register tile)
+    (1, 64, 12, 16, 7, 9, "SAME", 2),        # K = 63, M = 64: chunked cotangent staging
+    (1, 3, 6, 200, 3, 5, "SAME", 1),         # a 200-wide plane: one row group per band
+    (600, 2, 6, 6, 3, 3, "CIRCULAR", 1)])    # many samples: the smaller register tiles
 def test_direct_conv(be, B, M, H, W, kh, kw, mode, n_parts):
     _assert_small(case_direct_conv(be, B, M, H, W, kh, kw, mode, n_parts))

@@ -369,7 +369,7 @@ def test_direct_train_graph_replay():
     xt = torch.from_numpy(x).to(dev)
     res = []
     for graph in (False, True):
-        plan = StepPlan(topo, 8, port_input_shapes(xt, topo))
+        plan = StepPlan(topo, 8, port_input_shapes(xt, topo), conv="direct")
         assert plan.direct and plan.border
         ps = ParamState(torch.from_numpy(cell).to(dev), torch.from_numpy(filt).to(dev), 0.01)
         ts = TrainState(plan, ps)
