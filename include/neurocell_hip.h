@@ -473,7 +473,9 @@ int nc_fftconv_epilogue_partials(int B, int M, int h, int w, int fft_h, int fft_
  * correlation when not NULL (a training forward keeps it for the backward); on the 64-wide
  * grids it may be NULL (evaluation), elsewhere it is required as the epilogue's input.  ws:
  * nc_epilogue_workspace_size(B, M, hout, wout) bytes where the fused kernel does not run
- * (unused, may be NULL, where it does).  No counterpart in the reference (two ops there).
+ * (unused, may be NULL, where it does); on the 128- and 256-point grids a ws of at least
+ * nc_fftconv_correlate_workspace_size bytes as well lets the correlation run as two
+ * transform passes through it.  No counterpart in the reference (two ops there).
  */
 int nc_fftconv_epilogue_fwd(void* stream, int B, int M, int hout, int wout, int pad_h,
                             int pad_w, int fft_h, int fft_w, const float* xhat,
@@ -482,8 +484,20 @@ int nc_fftconv_epilogue_fwd(void* stream, int B, int M, int hout, int wout, int 
                             float* mean, float* rstd, void* ws, size_t ws_bytes);
 
 /*
+ * Workspace bytes that let nc_fftconv_epilogue_fwd and nc_fftconv_port_fwd run a large-grid
+ * correlation (an axis of 128 or 256 points) as two transform passes - a column pass over
+ * the B*M products xhat_b * ghat_m, then a row pass, B*M*hout*fft_w/2 complex values in
+ * between - instead of one workgroup per plane segment; 0 on the other grids.  The same
+ * results to rounding (the passes and their bin order are the same).  No counterpart in the
+ * reference.
+ */
+size_t nc_fftconv_correlate_workspace_size(int B, int M, int hout, int wout, int fft_h,
+                                           int fft_w);
+
+/*
  * Workspace bytes for nc_fftconv_port_fwd: nc_epilogue_workspace_size, or the fused kernel's
  * direction-group partial sums (2 * ceil(M/4) * B * n_port floats) where that is larger.
+ * (nc_fftconv_correlate_workspace_size on top enables the two-pass large-grid correlation.)
  */
 size_t nc_fftconv_port_workspace_size(int B, int M, int h, int w, int fft_h, int fft_w,
                                       int n_port);

@@ -38,8 +38,13 @@ int nc_seg_rfft2(hipStream_t st, int fft_h, int fft_w, int nplanes, int hin, int
 int nc_seg_dx(hipStream_t st, int B, int nchunk, int hin, int win, int pad_h, int pad_w,
               int fft_h, int fft_w, const void* dx_spectra, float* dx);
 
+// z = the correlation's window of irfft2(xhat_b * ghat_m); with a workspace of at least
+// nc_large_correlate_ws bytes, by the two-pass transform (column pass, then row pass, the
+// intermediate in ws), else one workgroup per plane segment.
 int nc_large_correlate(hipStream_t st, int B, int M, int hout, int wout, int pad_h, int pad_w,
-                       int fft_h, int fft_w, const float* xhat, const float* ghat, float* z);
+                       int fft_h, int fft_w, const float* xhat, const float* ghat, float* z,
+                       void* ws = nullptr, size_t ws_bytes = 0);
+size_t nc_large_correlate_ws(int B, int M, int hout, int fft_h, int fft_w);
 
 size_t nc_large_fftconv_bwd_ws(int B, int M, int fft_h, int fft_w);
 

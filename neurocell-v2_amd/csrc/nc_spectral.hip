@@ -1780,6 +1780,34 @@ int nc_fftconv_spectra(void* stream, int B, int hin, int win, int fft_h, int fft
     return NC_ERR_UNSUPPORTED;
 }
 
+size_t nc_fftconv_correlate_workspace_size(int B, int M, int hout, int wout, int fft_h,
+                                           int fft_w) {
+    if (B <= 0 || M <= 0 || hout <= 0 || wout <= 0 || !nc_large_grid(fft_h, fft_w)) return 0;
+    return nc_large_correlate_ws(B, M, hout, fft_h, fft_w);
+}
+
+}  // extern "C"
+
+namespace {
+// nc_spectral_correlate, by the two-pass large-grid transform when ws holds its intermediate.
+int correlate_ws(void* stream, int B, int M, int hout, int wout, int pad_h, int pad_w, int fft_h,
+                 int fft_w, const float* xhat, const float* ghat, float* z, void* ws,
+                 size_t ws_bytes) {
+    if (ws && nc_large_grid(fft_h, fft_w) &&
+        ws_bytes >= nc_fftconv_correlate_workspace_size(B, M, hout, wout, fft_h, fft_w)) {
+        int rc = fftconv_check(B, M, 1, 1, hout, wout, pad_h, pad_w, fft_h, fft_w);
+        if (rc != NC_OK) return rc;
+        if (!xhat || !ghat || !z) return NC_ERR_INVALID_ARGUMENT;
+        return nc_large_correlate(nc_stream(stream), B, M, hout, wout, pad_h, pad_w, fft_h, fft_w,
+                                  xhat, ghat, z, ws, ws_bytes);
+    }
+    return nc_spectral_correlate(stream, B, M, hout, wout, pad_h, pad_w, fft_h, fft_w, xhat, ghat,
+                                 z);
+}
+}  // namespace
+
+extern "C" {
+
 size_t nc_fftconv_port_workspace_size(int B, int M, int h, int w, int fft_h, int fft_w,
                                       int n_port) {
     const size_t epi = nc_epilogue_workspace_size(B, M, h, w);
@@ -1818,10 +1846,11 @@ int nc_fftconv_port_fwd(void* stream, int B, int M, int hout, int wout, int pad_
         return nc_port_combine_launch(st, B, M, n_port, (M + 3) / 4, final_act, neg_slope,
                                       port_params, part, out, pre);
     }
-    // other grids: the correlation into z, then the port
+    // other grids: the correlation into z (two-pass through ws when it is large enough), then
+    // the port
     if (!z) return NC_ERR_INVALID_ARGUMENT;
-    rc = nc_spectral_correlate(stream, B, M, hout, wout, pad_h, pad_w, fft_h, fft_w, xhat, ghat,
-                               z);
+    rc = correlate_ws(stream, B, M, hout, wout, pad_h, pad_w, fft_h, fft_w, xhat, ghat, z, ws,
+                      ws_bytes);
     if (rc != NC_OK) return rc;
     return nc_port_fwd(stream, B, M, hout, wout, 0, final_act, neg_slope, n_port, port_idx, z,
                        nullptr, port_params, out, zo, mean, rstd, pre, ws, ws_bytes);
@@ -1859,10 +1888,11 @@ int nc_fftconv_epilogue_fwd(void* stream, int B, int M, int hout, int wout, int 
             return NC_OK;
         }
     }
-    // other grids: the correlation into z, then the epilogue's partial outputs
+    // other grids: the correlation into z (two-pass through ws when it is large enough), then
+    // the epilogue's partial outputs
     if (!z) return NC_ERR_INVALID_ARGUMENT;
-    rc = nc_spectral_correlate(stream, B, M, hout, wout, pad_h, pad_w, fft_h, fft_w, xhat, ghat,
-                               z);
+    rc = correlate_ws(stream, B, M, hout, wout, pad_h, pad_w, fft_h, fft_w, xhat, ghat, z, ws,
+                      ws_bytes);
     if (rc != NC_OK) return rc;
     return nc_epilogue_fwd_parts(stream, B, M, hout, wout, act, neg_slope, 0, z, nullptr, w_eff,
                                  s_eff, b_roi, parts, mean, rstd, ws, ws_bytes);

@@ -169,6 +169,194 @@ __global__ __launch_bounds__(kNT) void k_linv_conv(int M, int hout, int wout, in
         [&](int i, int j, float v) { zo[i * wout + j] = v; }, P.seg, P.scr, P.tw);
 }
 
+// ---------------------------------------------------------------------------------------
+// Two-pass transforms for many planes (the B*M correlation planes and cotangent planes of
+// configs 2 and 3): one kernel per axis, the intermediate in HBM, so each kernel keeps ~37 KB
+// of LDS (four workgroups per CU) instead of one plane's whole segment (one per CU), and no
+// pass is repeated per segment.  Same transforms and bin order as lplane_irfft2 /
+// lplane_rfft2; the row pass of the inverse applies the same output window.
+// ---------------------------------------------------------------------------------------
+
+// Inverse column pass of the correlation: plane g = b*M + m, packed columns
+// [blockIdx.x * CPW, +CPW) of S = xhat_b * ghat_m (column 0: DC + i*Nyquist), inverse over kh,
+// rows i = (kh - ph) mod FH < hout kept: T[(g * hout + i) * NC + kw].
+template <int FH, int FW>
+__global__ __launch_bounds__(kNT) void k_linv_cols(int M, int hout, int ph,
+                                                   const cpx* __restrict__ xhat,
+                                                   const cpx* __restrict__ ghat,
+                                                   cpx* __restrict__ T) {
+    using L = LG<FH, FW>;
+    constexpr int EH = L::GH::E, GH = L::GH::G, CPW = kNT / GH;
+    __shared__ cpx tw[NC_TW_N];
+    __shared__ cpx scr[CPW * L::GH::SCR];
+    load_twiddles(tw);
+    __syncthreads();
+    const int tid = threadIdx.x, g = tid % CPW, t = tid / CPW;
+    const int kw = blockIdx.x * CPW + g, plane = blockIdx.y;
+    const int b = plane / M, m = plane - b * M;
+    const cpx* X = xhat + (size_t)b * L::F;
+    const cpx* G = ghat + (size_t)m * L::F;
+    cpx v[EH];
+#pragma unroll
+    for (int n1 = 0; n1 < EH; ++n1)
+        v[n1] = packed_at<FW>([&](int e) { return cmul(X[e], G[e]); }, t + GH * n1, kw);
+    cpx* sc = scr + g * L::GH::SCR;
+    gfft_stage1<FH, true>(v, t, sc, tw);
+    __syncthreads();
+    gfft_stage2<FH, true>(v, t, sc);
+    cpx* To = T + (size_t)plane * hout * L::NC + kw;
+#pragma unroll
+    for (int s = 0; s < EH; ++s) {
+        const int i = (L::GH::bin(t, s) - ph) & (FH - 1);
+        if (i < hout) To[(size_t)i * L::NC] = v[s];
+    }
+}
+
+// Inverse row pass: rows (2p, 2p + 1) of T as one complex transform, p in
+// [blockIdx.x * PPW, +PPW); output columns j = (c - pw) mod FW < wout, times scale.
+template <int FH, int FW>
+__global__ __launch_bounds__(kNT) void k_linv_rows(int hout, int wout, int pw, float scale,
+                                                   const cpx* __restrict__ T,
+                                                   float* __restrict__ z) {
+    using L = LG<FH, FW>;
+    constexpr int EW = L::GW::E, GW = L::GW::G, PPW = kNT / GW, NC = L::NC;
+    __shared__ cpx tw[NC_TW_N];
+    __shared__ cpx scr[PPW * L::GW::SCR];
+    load_twiddles(tw);
+    __syncthreads();
+    const int tid = threadIdx.x, g = tid / GW, t = tid % GW, plane = blockIdx.y;
+    const int p = blockIdx.x * PPW + g, npairs = (hout + 1) >> 1;
+    const bool on = p < npairs;
+    const int ia = 2 * p, ib = 2 * p + 1;
+    const bool hasb = ib < hout;
+    const cpx* ta = T + ((size_t)plane * hout + (on ? ia : 0)) * NC;
+    const cpx* tb = T + ((size_t)plane * hout + (on && hasb ? ib : (on ? ia : 0))) * NC;
+    const float bs = hasb ? 1.f : 0.f;
+    cpx v[EW];
+#pragma unroll
+    for (int n1 = 0; n1 < EW; ++n1) {
+        const int k = t + GW * n1;
+        cpx a, bb;
+        if (n1 < EW / 2) {  // k < FW/2
+            if (k == 0) {
+                a = cmk(ta[0].x, 0.f);
+                bb = cmk(tb[0].x, 0.f);
+            } else {
+                a = ta[k];
+                bb = tb[k];
+            }
+        } else {  // k >= FW/2
+            if (k == FW / 2) {
+                a = cmk(ta[0].y, 0.f);
+                bb = cmk(tb[0].y, 0.f);
+            } else {
+                a = cconj(ta[FW - k]);
+                bb = cconj(tb[FW - k]);
+            }
+        }
+        v[n1] = cadd(a, cmul_i(cscale(bb, bs)));
+    }
+    cpx* sc = scr + g * L::GW::SCR;
+    gfft_stage1<FW, true>(v, t, sc, tw);
+    __syncthreads();
+    gfft_stage2<FW, true>(v, t, sc);
+    if (!on) return;
+    float* za = z + ((size_t)plane * hout + ia) * wout;
+#pragma unroll
+    for (int s = 0; s < EW; ++s) {
+        const int j = (L::GW::bin(t, s) - pw) & (FW - 1);
+        if (j < wout) {
+            za[j] = v[s].x * scale;
+            if (hasb) za[wout + j] = v[s].y * scale;
+        }
+    }
+}
+
+// Forward row pass of real planes (plane g at x + g * pstride, hin x win at the grid origin):
+// rows (2p, 2p + 1) as one complex transform, split into the two rows' half-spectra, written
+// as rows 2p, 2p + 1 of the plane's (FH, SP) half-spectrum region of U.  Rows >= hin are not
+// written (the column pass reads them as zeros).
+template <int FH, int FW>
+__global__ __launch_bounds__(kNT) void k_lrfft_rows(int hin, int win, size_t pstride,
+                                                    const float* __restrict__ x,
+                                                    cpx* __restrict__ U) {
+    using L = LG<FH, FW>;
+    constexpr int EW = L::GW::E, GW = L::GW::G, PPW = kNT / GW, SP = L::SP;
+    __shared__ cpx tw[NC_TW_N];
+    __shared__ cpx scr[PPW * L::GW::SCR];
+    load_twiddles(tw);
+    __syncthreads();
+    const int tid = threadIdx.x, g = tid / GW, t = tid % GW, plane = blockIdx.y;
+    const int p = blockIdx.x * PPW + g, npairs = (hin + 1) >> 1;
+    const bool on = p < npairs;
+    const int ra = 2 * p, rb = 2 * p + 1;
+    const bool hasb = on && rb < hin;
+    const float* xa = x + (size_t)plane * pstride + (size_t)(on ? ra : 0) * win;
+    const float* xb = x + (size_t)plane * pstride + (size_t)(hasb ? rb : 0) * win;
+    cpx v[EW];
+#pragma unroll
+    for (int n1 = 0; n1 < EW; ++n1) {
+        const int c = t + GW * n1;
+        float a = 0.f, b = 0.f;
+        if (on && c < win) {
+            a = xa[c];
+            if (hasb) b = xb[c];
+        }
+        v[n1] = cmk(a, b);
+    }
+    cpx* sc = scr + g * L::GW::SCR;
+    gfft_stage1<FW, false>(v, t, sc, tw);
+    __syncthreads();
+    gfft_stage2<FW, false>(v, t, sc);
+    __syncthreads();  // the stage-2 reads of the scratch are done: it holds Z for the split
+#pragma unroll
+    for (int s = 0; s < EW; ++s) sc[L::GW::bin(t, s)] = v[s];
+    __syncthreads();
+    if (!on) return;
+    cpx* ua = U + (size_t)plane * L::F + (size_t)ra * SP;
+#pragma unroll
+    for (int s = 0; s < EW; ++s) {
+        const int k = L::GW::bin(t, s);
+        if (k <= FW / 2) {
+            // A[k] = (Z[k] + conj Z[-k]) / 2, B[k] = -i (Z[k] - conj Z[-k]) / 2
+            const cpx zk = v[s], zm = sc[(FW - k) & (FW - 1)];
+            ua[k] = cmk(0.5f * (zk.x + zm.x), 0.5f * (zk.y - zm.y));
+            if (hasb) ua[SP + k] = cmk(0.5f * (zk.y + zm.y), 0.5f * (zm.x - zk.x));
+        }
+    }
+}
+
+// Forward column pass, in place: columns [blockIdx.x * CPW, +CPW) (< SP) of plane g's
+// row-transformed rows r < hin (rows >= hin are zero), transformed over r into every bin kh.
+// A column belongs to one thread group of one workgroup, and the workgroup's barrier orders
+// all its reads before its writes.
+template <int FH, int FW>
+__global__ __launch_bounds__(kNT) void k_lrfft_cols(int hin, cpx* __restrict__ U) {
+    using L = LG<FH, FW>;
+    constexpr int EH = L::GH::E, GH = L::GH::G, CPW = kNT / GH, SP = L::SP;
+    __shared__ cpx tw[NC_TW_N];
+    __shared__ cpx scr[CPW * L::GH::SCR];
+    load_twiddles(tw);
+    __syncthreads();
+    const int tid = threadIdx.x, g = tid % CPW, t = tid / CPW;
+    const int kw = blockIdx.x * CPW + g;
+    const bool on = kw < SP;
+    cpx* col = U + (size_t)blockIdx.y * L::F + (on ? kw : 0);
+    cpx v[EH];
+#pragma unroll
+    for (int n1 = 0; n1 < EH; ++n1) {
+        const int r = t + GH * n1;
+        v[n1] = on && r < hin ? col[(size_t)r * SP] : cmk(0.f, 0.f);
+    }
+    cpx* sc = scr + g * L::GH::SCR;
+    gfft_stage1<FH, false>(v, t, sc, tw);
+    __syncthreads();
+    gfft_stage2<FH, false>(v, t, sc);
+    if (!on) return;
+#pragma unroll
+    for (int s = 0; s < EH; ++s) col[(size_t)L::GH::bin(t, s) * SP] = v[s];
+}
+
 // Both reductions of the backward in one pass over the cotangent spectra sp (B, M, F):
 //   dxpart[c][b] = sum over the chunk's directions m of sp_bm * conj(ghat_m)   (need_dx)
 //   dghat[m]     = (+=) sum over b of sp_bm * conj(xhat_b)  (conjugated when conj_out)
@@ -390,7 +578,7 @@ int spec_bwd(hipStream_t st, int M, int kh, int kw, int sh, int sw, const float*
 
 template <int FH, int FW>
 int corr(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw, const float* xhat,
-         const float* ghat, float* z);
+         const float* ghat, float* z, void* ws = nullptr, size_t ws_bytes = 0);
 
 template <int FH, int FW>
 int conv_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph, int pw,
@@ -404,9 +592,51 @@ int conv_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout,
     return corr<FH, FW>(st, B, M, hout, wout, ph, pw, xhat, ghat, z);
 }
 
+// Bytes of the two-pass correlation's intermediate (B*M planes of hout x FW/2 cpx).
+template <int FH, int FW>
+size_t corr2_ws(int B, int M, int hout) {
+    return (size_t)B * M * hout * LG<FH, FW>::NC * sizeof(cpx);
+}
+
+template <int FH, int FW>
+int corr2(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw, const float* xhat,
+          const float* ghat, float* z, void* ws) {
+    using L = LG<FH, FW>;
+    constexpr int CPW = kNT / L::GH::G, PPW = kNT / L::GW::G;
+    cpx* T = reinterpret_cast<cpx*>(ws);
+    hipLaunchKernelGGL((k_linv_cols<FH, FW>), dim3(L::NC / CPW, B * M), dim3(kNT), 0, st, M, hout,
+                       ph, reinterpret_cast<const cpx*>(xhat), reinterpret_cast<const cpx*>(ghat),
+                       T);
+    NC_CHECK_LAUNCH();
+    const int npairs = (hout + 1) / 2;
+    hipLaunchKernelGGL((k_linv_rows<FH, FW>), dim3((npairs + PPW - 1) / PPW, B * M), dim3(kNT), 0,
+                       st, hout, wout, pw, 1.0f / (float)(FH * FW), T, z);
+    NC_CHECK_LAUNCH();
+    return NC_OK;
+}
+
+// Half-spectra of nplanes real planes (hin x win, pstride floats apart) by the two-pass
+// transform, rows then columns in place in out.
+template <int FH, int FW>
+int rfft2_two_pass(hipStream_t st, int nplanes, int hin, int win, size_t pstride, const float* x,
+                   cpx* out) {
+    using L = LG<FH, FW>;
+    constexpr int CPW = kNT / L::GH::G, PPW = kNT / L::GW::G;
+    const int npairs = (hin + 1) / 2;
+    hipLaunchKernelGGL((k_lrfft_rows<FH, FW>), dim3((npairs + PPW - 1) / PPW, nplanes), dim3(kNT),
+                       0, st, hin, win, pstride, x, out);
+    NC_CHECK_LAUNCH();
+    hipLaunchKernelGGL((k_lrfft_cols<FH, FW>), dim3((L::SP + CPW - 1) / CPW, nplanes), dim3(kNT),
+                       0, st, hin, out);
+    NC_CHECK_LAUNCH();
+    return NC_OK;
+}
+
 template <int FH, int FW>
 int corr(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw, const float* xhat,
-         const float* ghat, float* z) {
+         const float* ghat, float* z, void* ws, size_t ws_bytes) {
+    if (ws && ws_bytes >= corr2_ws<FH, FW>(B, M, hout) && (size_t)B * M <= 65535)
+        return corr2<FH, FW>(st, B, M, hout, wout, ph, pw, xhat, ghat, z, ws);
     const int rs = inv_rows<FH, FW>(hout);
     const size_t lds = linv_lds_bytes<FH, FW, kNT>(rs);
     set_lds(k_linv_conv<FH, FW>, lds);
@@ -435,7 +665,9 @@ int conv_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout,
     const int nchunk = (M + kRedMC - 1) / kRedMC;
     cpx* sp = reinterpret_cast<cpx*>(ws);
     cpx* part = sp + (size_t)B * M * L::F;
-    int rc = rfft2_planes<FH, FW>(st, B * M, hout, wout, (size_t)hout * wout, false, gz, sp);
+    int rc = (size_t)B * M <= 65535
+                 ? rfft2_two_pass<FH, FW>(st, B * M, hout, wout, (size_t)hout * wout, gz, sp)
+                 : rfft2_planes<FH, FW>(st, B * M, hout, wout, (size_t)hout * wout, false, gz, sp);
     if (rc != NC_OK) return rc;
     hipLaunchKernelGGL((k_lred<kRedMC>), dim3((L::F + 255) / 256, nchunk), dim3(256), 0, st, B,
                        M, L::F, need_dx, sp, reinterpret_cast<const cpx*>(xhat),
@@ -586,11 +818,19 @@ int nc_seg_dx(hipStream_t st, int B, int nchunk, int hin, int win, int ph, int p
 }
 
 int nc_large_correlate(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw, int fh,
-                       int fw, const float* xhat, const float* ghat, float* z) {
-#define NC_CALL(A, Bv) corr<A, Bv>(st, B, M, hout, wout, ph, pw, xhat, ghat, z)
+                       int fw, const float* xhat, const float* ghat, float* z, void* ws,
+                       size_t ws_bytes) {
+#define NC_CALL(A, Bv) corr<A, Bv>(st, B, M, hout, wout, ph, pw, xhat, ghat, z, ws, ws_bytes)
     NC_DISPATCH_LARGE(fh, fw, NC_CALL);
 #undef NC_CALL
     return NC_ERR_UNSUPPORTED;
+}
+
+size_t nc_large_correlate_ws(int B, int M, int hout, int fh, int fw) {
+#define NC_CALL(A, Bv) corr2_ws<A, Bv>(B, M, hout)
+    NC_DISPATCH_LARGE(fh, fw, NC_CALL);
+#undef NC_CALL
+    return 0;
 }
 
 int nc_large_plane_spectrum(hipStream_t st, int nplanes, int hin, int win, int fh, int fw, int sh,

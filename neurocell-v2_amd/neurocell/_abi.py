@@ -88,6 +88,7 @@ _SIGS = {
     "nc_filter_gate_bwd": (I, [P, I, P, P]),
     "nc_filter_patch_bwd": (I, [P, I, I, I, I, I, I, I, P, P, I, I, I, I, I, I, P, P, P, P,
                                 SZ]),
+    "nc_fftconv_correlate_workspace_size": (SZ, [I, I, I, I, I, I]),
     "nc_fftconv_port_workspace_size": (SZ, [I, I, I, I, I, I, I]),
     "nc_fftconv_port_fwd": (I, [P, I, I, I, I, I, I, I, I, P, P, I, F, I, P, P, P, P, P, P, P,
                                 P, P, SZ]),

@@ -355,9 +355,12 @@ class StepPlan:
         if self.universe:
             self.s_prob = torch.empty(self.H, self.W, **f)
             self.univ = torch.empty(B, self.H, self.W, **f) if self.want_universe else None
+        # on the 128/256-point grids the workspace also holds the two-pass correlation's
+        # intermediate (the epilogue's scratch reuses it once z is written)
         n_ep = max(_abi_size("nc_epilogue_workspace_size", B, M, h, w),
                    _abi_size("nc_fftconv_port_workspace_size", B, M, h, w, *self.fft, self.P)
-                   if port_path else 0)
+                   if port_path else 0,
+                   lib().nc_fftconv_correlate_workspace_size(B, M, h, w, *self.fft))
         self.ws_epi = torch.empty(max(1, n_ep // 4), **f)
         if self.training:
             n_fc = max(_abi_size("nc_fftconv_bwd_workspace_size", B, M, *self.fft),

@@ -414,11 +414,14 @@ def case_epilogue_parts(be, B=3, M=9, h=10, w=12, kh=5, kw=3, FH=16, FW=16, seed
 
 
 def case_fftconv_epilogue(be, B=3, M=6, h=20, w=27, kh=7, kw=5, FH=32, FW=64, act="tanh",
-                          seed=8):
+                          seed=8, two_pass=False):
     """nc_fftconv_spectra + nc_fftconv_epilogue_fwd (the fused correlation and hidden epilogue)
     against nc_fftconv_fwd_parts + nc_epilogue_fwd_parts and the oracle.  The cell state comes
     in two partial planes; M = 6 leaves two idle wavefronts in the last direction group; the
-    call without z must give the same parts/mean/rstd bit for bit as the one with z."""
+    call without z must give the same parts/mean/rstd bit for bit as the one with z.  With
+    two_pass the workspace also holds nc_fftconv_correlate_workspace_size bytes, so a large
+    grid's correlation runs as the two transform passes (the separate path keeps the
+    segmented one)."""
     rng = np.random.default_rng(seed)
     L, s = be.lib, be.stream()
     ph, pw = (kh - 1) // 2, (kw - 1) // 2
@@ -442,7 +445,11 @@ def case_fftconv_epilogue(be, B=3, M=6, h=20, w=27, kh=7, kw=5, FH=32, FW=64, ac
     _ok(be, L.nc_fftconv_fwd_parts(s, B, M, h, w, h, w, ph, pw, FH, FW, be.ptr(xpd), 2, None,
                                    be.ptr(ghat), be.ptr(z_ref), be.ptr(xh2)), "fwd_parts")
     Gs = L.nc_epilogue_fwd_partials(B, M, h, w)
-    ws = be.zeros((L.nc_epilogue_workspace_size(B, M, h, w) // 4 + 1,))
+    nws = L.nc_epilogue_workspace_size(B, M, h, w)
+    if two_pass:
+        assert L.nc_fftconv_correlate_workspace_size(B, M, h, w, FH, FW) > 0
+        nws = max(nws, L.nc_fftconv_correlate_workspace_size(B, M, h, w, FH, FW))
+    ws = be.zeros((nws // 4 + 1,))
     nb = ws.nbytes if hasattr(ws, "nbytes") else ws.numel() * 4
     p_ref, m_ref, r_ref = be.zeros((Gs, B, h, w)), be.zeros((B, M)), be.zeros((B, M))
     _ok(be, L.nc_epilogue_fwd_parts(s, B, M, h, w, aid, 0.01, 0, be.ptr(z_ref), None, be.ptr(wd),
@@ -479,7 +486,7 @@ def case_fftconv_epilogue(be, B=3, M=6, h=20, w=27, kh=7, kw=5, FH=32, FW=64, ac
 
 
 def case_fftconv_port(be, B=3, M=6, h=20, w=27, kh=7, kw=5, FH=32, FW=64, fact=None,
-                      rows=(2, 3, 19, 3, 0), cols=(5, 5, 26, 5, 0), seed=11):
+                      rows=(2, 3, 19, 3, 0), cols=(5, 5, 26, 5, 0), seed=11, two_pass=False):
     """nc_fftconv_port_fwd (the last step's correlation and output port in one operation)
     against nc_spectral_correlate + nc_port_fwd and the oracle: out, zo, mean, rstd, pre and z,
     with a duplicated port cell and the grid's corners; on the fused grids the call without z
@@ -498,6 +505,9 @@ def case_fftconv_port(be, B=3, M=6, h=20, w=27, kh=7, kw=5, FH=32, FW=64, fact=N
     _ok(be, L.nc_filter_spectrum_fwd(s, M, kh, kw, FH, FW, be.ptr(gd), be.ptr(ghat)), "spec")
     _ok(be, L.nc_fftconv_spectra(s, B, h, w, FH, FW, be.ptr(xd), 1, None, be.ptr(xhat)), "xs")
     nws = L.nc_fftconv_port_workspace_size(B, M, h, w, FH, FW, P)
+    if two_pass:  # room for the two-pass large-grid correlation as well
+        assert L.nc_fftconv_correlate_workspace_size(B, M, h, w, FH, FW) > 0
+        nws = max(nws, L.nc_fftconv_correlate_workspace_size(B, M, h, w, FH, FW))
     ws = be.zeros((nws // 4 + 1,))
     nb = ws.nbytes if hasattr(ws, "nbytes") else ws.numel() * 4
     res, got = {}, []

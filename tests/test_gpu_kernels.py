@@ -117,14 +117,20 @@ def test_epilogue_parts(be, B, M, h, w, FH, FW):
     assert res["xhat_mismatch"] == 0, res
 
 
-@pytest.mark.parametrize("B,M,h,w,kh,kw,FH,FW,act", [
-    (3, 6, 20, 27, 7, 5, 32, 64, "tanh"),          # fused, idle wavefronts in the last group
-    (2, 16, 40, 50, 23, 13, 64, 64, "leaky_relu"),  # fused, the ALU geometry
-    (3, 5, 10, 12, 5, 3, 16, 16, "gelu"),           # not fused: correlation + epilogue
+@pytest.mark.parametrize("B,M,h,w,kh,kw,FH,FW,act,two_pass", [
+    (3, 6, 20, 27, 7, 5, 32, 64, "tanh", False),          # fused, idle wavefronts
+    (2, 16, 40, 50, 23, 13, 64, 64, "leaky_relu", False),  # fused, the ALU geometry
+    (3, 5, 10, 12, 5, 3, 16, 16, "gelu", False),           # not fused: correlation + epilogue
+    (2, 3, 60, 50, 31, 13, 128, 64, "tanh", True),     # two-pass large-grid correlation
+    (2, 5, 224, 224, 31, 31, 256, 256, "tanh", True),  # config-3 planes, two passes
+    (2, 3, 224, 224, 31, 31, 256, 256, "tanh", False),  # the same, segmented
+    (1, 3, 40, 150, 13, 63, 64, 256, "gelu", True),    # asymmetric grid, two passes
+    (2, 4, 112, 112, 63, 63, 256, 256, "leaky_relu", True),  # config 2
 ])
-def test_fftconv_epilogue(be, B, M, h, w, kh, kw, FH, FW, act):
-    res = case_fftconv_epilogue(be, B=B, M=M, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW, act=act)
-    if FW == 64:
+def test_fftconv_epilogue(be, B, M, h, w, kh, kw, FH, FW, act, two_pass):
+    res = case_fftconv_epilogue(be, B=B, M=M, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW, act=act,
+                                two_pass=two_pass)
+    if FW == 64 and FH in (32, 64):
         assert res["G"] == (M + 3) // 4 and res["no_z_mismatch"] == 0, res
     assert res["xhat_mismatch"] == 0, res
     _assert_small({k: res[k] for k in ("z", "z_vs_separate", "out", "out_vs_separate", "mean",
@@ -142,15 +148,18 @@ def test_fftconv_circular(be, B, M, H, W, kh, kw):
     _assert_small(res)
 
 
-@pytest.mark.parametrize("B,M,h,w,kh,kw,FH,FW,fact", [
-    (3, 6, 20, 27, 7, 5, 32, 64, None),           # fused, idle wavefronts, identity port
-    (2, 16, 40, 50, 23, 13, 64, 64, "tanh"),      # fused, the ALU geometry, gated port
-    (3, 5, 10, 12, 5, 3, 16, 16, "sigmoid"),      # not fused: correlation then port
+@pytest.mark.parametrize("B,M,h,w,kh,kw,FH,FW,fact,two_pass", [
+    (3, 6, 20, 27, 7, 5, 32, 64, None, False),           # fused, idle wavefronts, identity port
+    (2, 16, 40, 50, 23, 13, 64, 64, "tanh", False),      # fused, the ALU geometry, gated port
+    (3, 5, 10, 12, 5, 3, 16, 16, "sigmoid", False),      # not fused: correlation then port
+    (2, 3, 60, 50, 31, 13, 128, 64, "tanh", True),      # two-pass large-grid correlation
+    (2, 5, 224, 224, 31, 31, 256, 256, None, True),
+    (2, 4, 112, 112, 63, 63, 256, 256, "sigmoid", True),
 ])
-def test_fftconv_port(be, B, M, h, w, kh, kw, FH, FW, fact):
+def test_fftconv_port(be, B, M, h, w, kh, kw, FH, FW, fact, two_pass):
     rows, cols = (2, 3, h - 1, 3, 0), (5, 5, w - 1, 5, 0)
     res = case_fftconv_port(be, B=B, M=M, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW, fact=fact,
-                            rows=rows, cols=cols)
+                            rows=rows, cols=cols, two_pass=two_pass)
     _assert_small(res)
 
 
