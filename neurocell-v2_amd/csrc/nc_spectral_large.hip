@@ -177,13 +177,17 @@ __global__ __launch_bounds__(kNT) void k_linv_conv(int M, int hout, int wout, in
 // lplane_rfft2; the row pass of the inverse applies the same output window.
 // ---------------------------------------------------------------------------------------
 
-// Inverse column pass of the correlation: plane g = b*M + m, packed columns
-// [blockIdx.x * CPW, +CPW) of S = xhat_b * ghat_m (column 0: DC + i*Nyquist), inverse over kh,
-// rows i = (kh - ph) mod FH < hout kept: T[(g * hout + i) * NC + kw].
-template <int FH, int FW>
-__global__ __launch_bounds__(kNT) void k_linv_cols(int M, int hout, int ph,
-                                                   const cpx* __restrict__ xhat,
-                                                   const cpx* __restrict__ ghat,
+// Inverse column pass: packed columns [blockIdx.x * CPW, +CPW) (column 0: DC + i*Nyquist) of
+// plane g's spectrum S_g, inverse over kh, rows i = (kh - row0) mod FH < hout kept:
+// T[(g * hout + i) * NC + kw], grid (column tiles, g).  SRC 0, the correlation:
+// S_g = A_b * B_m for g = b*n + m; SRC 1, the dx spectra: S_g = the sum of the n chunk
+// partials A[c * cstride + g * F].
+enum { kSrcProduct = 0, kSrcChunks = 1 };
+
+template <int FH, int FW, int SRC>
+__global__ __launch_bounds__(kNT) void k_linv_cols(int n, size_t cstride, int hout, int row0,
+                                                   const cpx* __restrict__ A,
+                                                   const cpx* __restrict__ Bm,
                                                    cpx* __restrict__ T) {
     using L = LG<FH, FW>;
     constexpr int EH = L::GH::E, GH = L::GH::G, CPW = kNT / GH;
@@ -193,13 +197,26 @@ __global__ __launch_bounds__(kNT) void k_linv_cols(int M, int hout, int ph,
     __syncthreads();
     const int tid = threadIdx.x, g = tid % CPW, t = tid / CPW;
     const int kw = blockIdx.x * CPW + g, plane = blockIdx.y;
-    const int b = plane / M, m = plane - b * M;
-    const cpx* X = xhat + (size_t)b * L::F;
-    const cpx* G = ghat + (size_t)m * L::F;
     cpx v[EH];
+    if constexpr (SRC == kSrcProduct) {
+        const int b = plane / n, m = plane - b * n;
+        const cpx* X = A + (size_t)b * L::F;
+        const cpx* G = Bm + (size_t)m * L::F;
 #pragma unroll
-    for (int n1 = 0; n1 < EH; ++n1)
-        v[n1] = packed_at<FW>([&](int e) { return cmul(X[e], G[e]); }, t + GH * n1, kw);
+        for (int n1 = 0; n1 < EH; ++n1)
+            v[n1] = packed_at<FW>([&](int e) { return cmul(X[e], G[e]); }, t + GH * n1, kw);
+    } else {
+        const cpx* src = A + (size_t)plane * L::F;
+#pragma unroll
+        for (int n1 = 0; n1 < EH; ++n1)
+            v[n1] = packed_at<FW>(
+                [&](int e) {
+                    cpx s = src[e];
+                    for (int c = 1; c < n; ++c) s = cadd(s, src[c * cstride + e]);
+                    return s;
+                },
+                t + GH * n1, kw);
+    }
     cpx* sc = scr + g * L::GH::SCR;
     gfft_stage1<FH, true>(v, t, sc, tw);
     __syncthreads();
@@ -207,15 +224,15 @@ __global__ __launch_bounds__(kNT) void k_linv_cols(int M, int hout, int ph,
     cpx* To = T + (size_t)plane * hout * L::NC + kw;
 #pragma unroll
     for (int s = 0; s < EH; ++s) {
-        const int i = (L::GH::bin(t, s) - ph) & (FH - 1);
+        const int i = (L::GH::bin(t, s) - row0) & (FH - 1);
         if (i < hout) To[(size_t)i * L::NC] = v[s];
     }
 }
 
 // Inverse row pass: rows (2p, 2p + 1) of T as one complex transform, p in
-// [blockIdx.x * PPW, +PPW); output columns j = (c - pw) mod FW < wout, times scale.
+// [blockIdx.x * PPW, +PPW); output columns j = (c - col0) mod FW < wout, times scale.
 template <int FH, int FW>
-__global__ __launch_bounds__(kNT) void k_linv_rows(int hout, int wout, int pw, float scale,
+__global__ __launch_bounds__(kNT) void k_linv_rows(int hout, int wout, int col0, float scale,
                                                    const cpx* __restrict__ T,
                                                    float* __restrict__ z) {
     using L = LG<FH, FW>;
@@ -264,7 +281,7 @@ __global__ __launch_bounds__(kNT) void k_linv_rows(int hout, int wout, int pw, f
     float* za = z + ((size_t)plane * hout + ia) * wout;
 #pragma unroll
     for (int s = 0; s < EW; ++s) {
-        const int j = (L::GW::bin(t, s) - pw) & (FW - 1);
+        const int j = (L::GW::bin(t, s) - col0) & (FW - 1);
         if (j < wout) {
             za[j] = v[s].x * scale;
             if (hasb) za[wout + j] = v[s].y * scale;
@@ -272,13 +289,14 @@ __global__ __launch_bounds__(kNT) void k_linv_rows(int hout, int wout, int pw, f
     }
 }
 
-// Forward row pass of real planes (plane g at x + g * pstride, hin x win at the grid origin):
-// rows (2p, 2p + 1) as one complex transform, split into the two rows' half-spectra, written
-// as rows 2p, 2p + 1 of the plane's (FH, SP) half-spectrum region of U.  Rows >= hin are not
+// Forward row pass of real planes (plane g at x + g * pstride, hin x win at the grid origin,
+// each value the sum of nq partial planes qstride floats apart, in increasing order): rows
+// (2p, 2p + 1) as one complex transform, split into the two rows' half-spectra, written as
+// rows 2p, 2p + 1 of the plane's (FH, SP) half-spectrum region of U.  Rows >= hin are not
 // written (the column pass reads them as zeros).
 template <int FH, int FW>
-__global__ __launch_bounds__(kNT) void k_lrfft_rows(int hin, int win, size_t pstride,
-                                                    const float* __restrict__ x,
+__global__ __launch_bounds__(kNT) void k_lrfft_rows(int hin, int win, size_t pstride, int nq,
+                                                    size_t qstride, const float* __restrict__ x,
                                                     cpx* __restrict__ U) {
     using L = LG<FH, FW>;
     constexpr int EW = L::GW::E, GW = L::GW::G, PPW = kNT / GW, SP = L::SP;
@@ -300,7 +318,11 @@ __global__ __launch_bounds__(kNT) void k_lrfft_rows(int hin, int win, size_t pst
         float a = 0.f, b = 0.f;
         if (on && c < win) {
             a = xa[c];
-            if (hasb) b = xb[c];
+            for (int q = 1; q < nq; ++q) a += xa[q * qstride + c];
+            if (hasb) {
+                b = xb[c];
+                for (int q = 1; q < nq; ++q) b += xb[q * qstride + c];
+            }
         }
         v[n1] = cmk(a, b);
     }
@@ -327,11 +349,13 @@ __global__ __launch_bounds__(kNT) void k_lrfft_rows(int hin, int win, size_t pst
 }
 
 // Forward column pass, in place: columns [blockIdx.x * CPW, +CPW) (< SP) of plane g's
-// row-transformed rows r < hin (rows >= hin are zero), transformed over r into every bin kh.
-// A column belongs to one thread group of one workgroup, and the workgroup's barrier orders
-// all its reads before its writes.
+// row-transformed rows r < hin (rows >= hin are zero), transformed over r into every bin kh,
+// plus add[kh * SP + kw] when add is given (one spectrum for every plane).  A column belongs
+// to one thread group of one workgroup, and the workgroup's barrier orders all its reads
+// before its writes.
 template <int FH, int FW>
-__global__ __launch_bounds__(kNT) void k_lrfft_cols(int hin, cpx* __restrict__ U) {
+__global__ __launch_bounds__(kNT) void k_lrfft_cols(int hin, const cpx* __restrict__ add,
+                                                    cpx* __restrict__ U) {
     using L = LG<FH, FW>;
     constexpr int EH = L::GH::E, GH = L::GH::G, CPW = kNT / GH, SP = L::SP;
     __shared__ cpx tw[NC_TW_N];
@@ -354,7 +378,10 @@ __global__ __launch_bounds__(kNT) void k_lrfft_cols(int hin, cpx* __restrict__ U
     gfft_stage2<FH, false>(v, t, sc);
     if (!on) return;
 #pragma unroll
-    for (int s = 0; s < EH; ++s) col[(size_t)L::GH::bin(t, s) * SP] = v[s];
+    for (int s = 0; s < EH; ++s) {
+        const int kh = L::GH::bin(t, s);
+        col[(size_t)kh * SP] = add ? cadd(v[s], add[kh * SP + kw]) : v[s];
+    }
 }
 
 // Both reductions of the backward in one pass over the cotangent spectra sp (B, M, F):
@@ -581,13 +608,16 @@ int corr(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw, const
          const float* ghat, float* z, void* ws = nullptr, size_t ws_bytes = 0);
 
 template <int FH, int FW>
+int rfft2_two_pass(hipStream_t st, int nplanes, int hin, int win, size_t pstride, const float* x,
+                   cpx* out, int nq = 1, size_t qstride = 0, const cpx* add = nullptr);
+
+template <int FH, int FW>
 int conv_fwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph, int pw,
              const float* x, int nq, const float* xhat_add, const float* ghat, float* z,
              float* xhat) {
-    const SpecPost post{reinterpret_cast<const cpx*>(xhat_add), 0, 0};
-    int rc = rfft2_planes<FH, FW>(st, B, hin, win, (size_t)hin * win, false, x,
-                                  reinterpret_cast<cpx*>(xhat), xhat_add ? kPostAdd : kPostNone,
-                                  post, nq, (size_t)B * hin * win);
+    int rc = rfft2_two_pass<FH, FW>(st, B, hin, win, (size_t)hin * win, x,
+                                    reinterpret_cast<cpx*>(xhat), nq, (size_t)B * hin * win,
+                                    reinterpret_cast<const cpx*>(xhat_add));
     if (rc != NC_OK) return rc;
     return corr<FH, FW>(st, B, M, hout, wout, ph, pw, xhat, ghat, z);
 }
@@ -604,9 +634,9 @@ int corr2(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw, cons
     using L = LG<FH, FW>;
     constexpr int CPW = kNT / L::GH::G, PPW = kNT / L::GW::G;
     cpx* T = reinterpret_cast<cpx*>(ws);
-    hipLaunchKernelGGL((k_linv_cols<FH, FW>), dim3(L::NC / CPW, B * M), dim3(kNT), 0, st, M, hout,
-                       ph, reinterpret_cast<const cpx*>(xhat), reinterpret_cast<const cpx*>(ghat),
-                       T);
+    hipLaunchKernelGGL((k_linv_cols<FH, FW, kSrcProduct>), dim3(L::NC / CPW, B * M), dim3(kNT), 0,
+                       st, M, (size_t)0, hout, ph, reinterpret_cast<const cpx*>(xhat),
+                       reinterpret_cast<const cpx*>(ghat), T);
     NC_CHECK_LAUNCH();
     const int npairs = (hout + 1) / 2;
     hipLaunchKernelGGL((k_linv_rows<FH, FW>), dim3((npairs + PPW - 1) / PPW, B * M), dim3(kNT), 0,
@@ -619,15 +649,37 @@ int corr2(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw, cons
 // transform, rows then columns in place in out.
 template <int FH, int FW>
 int rfft2_two_pass(hipStream_t st, int nplanes, int hin, int win, size_t pstride, const float* x,
-                   cpx* out) {
+                   cpx* out, int nq, size_t qstride, const cpx* add) {
     using L = LG<FH, FW>;
     constexpr int CPW = kNT / L::GH::G, PPW = kNT / L::GW::G;
+    if (nplanes > 65535)  // the grid's y extent: one workgroup per plane segment instead
+        return rfft2_planes<FH, FW>(st, nplanes, hin, win, pstride, false, x, out,
+                                    add ? kPostAdd : kPostNone, SpecPost{add, 0, 0}, nq, qstride);
     const int npairs = (hin + 1) / 2;
     hipLaunchKernelGGL((k_lrfft_rows<FH, FW>), dim3((npairs + PPW - 1) / PPW, nplanes), dim3(kNT),
-                       0, st, hin, win, pstride, x, out);
+                       0, st, hin, win, pstride, nq, qstride, x, out);
     NC_CHECK_LAUNCH();
     hipLaunchKernelGGL((k_lrfft_cols<FH, FW>), dim3((L::SP + CPW - 1) / CPW, nplanes), dim3(kNT),
-                       0, st, hin, out);
+                       0, st, hin, add, out);
+    NC_CHECK_LAUNCH();
+    return NC_OK;
+}
+
+// dx_b by the two-pass inverse: the sum of the nchunk partial spectra (nchunk, B, F), window
+// rows / columns from the unshifted roll (FH - ph, FW - pw); T (B * hin * FW/2 cpx) is
+// scratch.
+template <int FH, int FW>
+int dx_two_pass(hipStream_t st, int B, int nchunk, int hin, int win, int ph, int pw,
+                const cpx* dxs, cpx* T, float* dx) {
+    using L = LG<FH, FW>;
+    constexpr int CPW = kNT / L::GH::G, PPW = kNT / L::GW::G;
+    hipLaunchKernelGGL((k_linv_cols<FH, FW, kSrcChunks>), dim3(L::NC / CPW, B), dim3(kNT), 0, st,
+                       nchunk, (size_t)B * L::F, hin, (FH - ph) & (FH - 1), dxs,
+                       (const cpx*)nullptr, T);
+    NC_CHECK_LAUNCH();
+    const int npairs = (hin + 1) / 2;
+    hipLaunchKernelGGL((k_linv_rows<FH, FW>), dim3((npairs + PPW - 1) / PPW, B), dim3(kNT), 0, st,
+                       hin, win, (FW - pw) & (FW - 1), 1.0f / (float)(FH * FW), T, dx);
     NC_CHECK_LAUNCH();
     return NC_OK;
 }
@@ -665,16 +717,15 @@ int conv_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout,
     const int nchunk = (M + kRedMC - 1) / kRedMC;
     cpx* sp = reinterpret_cast<cpx*>(ws);
     cpx* part = sp + (size_t)B * M * L::F;
-    int rc = (size_t)B * M <= 65535
-                 ? rfft2_two_pass<FH, FW>(st, B * M, hout, wout, (size_t)hout * wout, gz, sp)
-                 : rfft2_planes<FH, FW>(st, B * M, hout, wout, (size_t)hout * wout, false, gz, sp);
+    int rc = rfft2_two_pass<FH, FW>(st, B * M, hout, wout, (size_t)hout * wout, gz, sp);
     if (rc != NC_OK) return rc;
     hipLaunchKernelGGL((k_lred<kRedMC>), dim3((L::F + 255) / 256, nchunk), dim3(256), 0, st, B,
                        M, L::F, need_dx, sp, reinterpret_cast<const cpx*>(xhat),
                        reinterpret_cast<const cpx*>(ghat), part, reinterpret_cast<cpx*>(dghat),
                        accumulate, conj_out, reinterpret_cast<cpx*>(ssum), sum_acc);
     NC_CHECK_LAUNCH();
-    if (need_dx) return seg_dx<FH, FW>(st, B, nchunk, hin, win, ph, pw, part, dx);
+    // the cotangent spectra are consumed: their region holds the dx passes' intermediate
+    if (need_dx) return dx_two_pass<FH, FW>(st, B, nchunk, hin, win, ph, pw, part, sp, dx);
     return NC_OK;
 }
 
@@ -798,6 +849,15 @@ int nc_large_plane_spectra(hipStream_t st, int fh, int fw, int n, const nc_spect
 int nc_seg_rfft2(hipStream_t st, int fh, int fw, int nplanes, int hin, int win, int flip,
                  const float* x, void* xhat, const void* add, int sh, int sw, int nparts,
                  size_t qstride) {
+    // large grids: the two-pass transform (rows, then columns in place)
+    if (nc_large_grid(fh, fw) && !flip && !(sh | sw)) {
+#define NC_CALL(A, Bv)                                                                        \
+    rfft2_two_pass<A, Bv>(st, nplanes, hin, win, (size_t)hin * win, x,                       \
+                          reinterpret_cast<cpx*>(xhat), nparts, qstride,                     \
+                          reinterpret_cast<const cpx*>(add))
+        NC_DISPATCH_LARGE(fh, fw, NC_CALL);
+#undef NC_CALL
+    }
     const SpecPost post{reinterpret_cast<const cpx*>(add), sh, sw};
     const int kind = add ? kPostAdd : (sh | sw) ? kPostShift : kPostNone;
 #define NC_CALL(A, Bv)                                                                    \
