@@ -48,11 +48,15 @@ size_t nc_large_correlate_ws(int B, int M, int hout, int fft_h, int fft_w);
 
 size_t nc_large_fftconv_bwd_ws(int B, int M, int fft_h, int fft_w);
 
+// parts: dghat / gz_hat_sum are nc_large_red_splits(...) row stacks (one row per sample
+// slice of the reduction, each accumulated into when accumulate / sum_accumulate), else
+// single sums.
 int nc_large_fftconv_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout,
                          int pad_h, int pad_w, int fft_h, int fft_w, const float* gz,
                          const float* xhat, const float* ghat, int need_dx, float* dx,
                          float* dghat, int accumulate, int conj_dghat, float* gz_hat_sum,
-                         int sum_accumulate, void* ws);
+                         int sum_accumulate, int parts, void* ws);
+int nc_large_red_splits(int B, int M, int fft_h, int fft_w);
 
 // dx = the inverse of one sample's unpacked dx half-spectrum with the unshifted roll.
 int nc_large_hat_dx(hipStream_t st, int hin, int win, int pad_h, int pad_w, int fft_h, int fft_w,

@@ -35,7 +35,13 @@ struct LGeo {
     static_assert(NT % GH::G == 0 && NT % GW::G == 0, "whole groups");
     static constexpr int NGH = NT / GH::G;  // column transforms in flight
     static constexpr int NGW = NT / GW::G;  // row-pair transforms in flight
-    static constexpr int SCR_H = NGH * GH::SCR;
+    // Column groups interleave lane by lane (group g = tid % NGH, so a wavefront holds
+    // min(NGH, 64) groups and 64 / that lanes of each); their exchange slots lie SCR_HS cpx
+    // apart with SCR_HS = 64 / min(NGH, 64) (mod 32), so the wavefront's 8-byte accesses
+    // spread over every bank pair (two passes) instead of a few.
+    static constexpr int GPW = NGH < 64 ? NGH : 64;
+    static constexpr int SCR_HS = GH::SCR + ((64 / GPW - GH::SCR % 32) % 32 + 32) % 32;
+    static constexpr int SCR_H = NGH * SCR_HS;
     static constexpr int SCR_W = NGW * GW::SCR;
     static constexpr int SCR = SCR_H > SCR_W ? SCR_H : SCR_W;  // exchange scratch (cpx)
 };
@@ -115,7 +121,7 @@ NC_DEV void lplane_rfft2(Load load, int hin, int win, int c0, int cs, Out out, c
         const int g = tid % L::NGH, t = tid / L::NGH, jj = j0 + g;
         const bool on = jj < cs;
         const int kw = c0 + jj;
-        cpx* sc = scr + g * L::GH::SCR;
+        cpx* sc = scr + g * L::SCR_HS;
         cpx v[EH];
         if (on) {
 #pragma unroll
@@ -179,7 +185,7 @@ NC_DEV void lplane_irfft2(SpecP specp, int row0, int rows, int col0, int cols, f
     for (int k0 = 0; k0 < L::NC; k0 += L::NGH) {
         const int g = tid % L::NGH, t = tid / L::NGH, kw = k0 + g;
         const bool on = kw < L::NC;
-        cpx* sc = scr + g * L::GH::SCR;
+        cpx* sc = scr + g * L::SCR_HS;
         cpx v[EH];
         if (on) {
 #pragma unroll

@@ -1922,7 +1922,7 @@ static int fftconv_bwd(void* stream, int B, int M, int hin, int win, int hout, i
     if (nc_large_grid(fft_h, fft_w))
         return nc_large_fftconv_bwd(st, B, M, hin, win, hout, wout, pad_h, pad_w, fft_h, fft_w,
                                     gz, xhat, ghat, need_dx, dx, dghat, accumulate, conj_dghat,
-                                    gz_hat_sum, sum_accumulate, ws);
+                                    gz_hat_sum, sum_accumulate, parts ? 1 : 0, ws);
 #define NC_CALL(A, Bv)                                                                     \
     launch_bwd<A, Bv>(st, B, M, hin, win, hout, wout, pad_h, pad_w, gz, xhat, ghat, need_dx, \
                       dx, dghat, accumulate, conj_dghat, gz_hat_sum, sum_accumulate, parts, ws)
@@ -1943,7 +1943,7 @@ int nc_fftconv_bwd_ex(void* stream, int B, int M, int hin, int win, int hout, in
 
 int nc_fftconv_bwd_partials(int B, int M, int fft_h, int fft_w) {
     if (B <= 0 || M <= 0) return 0;
-    if (nc_large_grid(fft_h, fft_w)) return 1;
+    if (nc_large_grid(fft_h, fft_w)) return nc_large_red_splits(B, M, fft_h, fft_w);
     if (!pow2_ok(fft_h) || !pow2_ok(fft_w)) return 0;
 #define NC_CALL(A, Bv) dg_parts<A, Bv>(B, M)
     NC_DISPATCH_FFT(fft_h, fft_w, NC_CALL);

@@ -192,7 +192,7 @@ __global__ __launch_bounds__(kNT) void k_linv_cols(int n, size_t cstride, int ho
     using L = LG<FH, FW>;
     constexpr int EH = L::GH::E, GH = L::GH::G, CPW = kNT / GH;
     __shared__ cpx tw[NC_TW_N];
-    __shared__ cpx scr[CPW * L::GH::SCR];
+    __shared__ cpx scr[CPW * L::SCR_HS];
     load_twiddles(tw);
     __syncthreads();
     const int tid = threadIdx.x, g = tid % CPW, t = tid / CPW;
@@ -217,7 +217,7 @@ __global__ __launch_bounds__(kNT) void k_linv_cols(int n, size_t cstride, int ho
                 },
                 t + GH * n1, kw);
     }
-    cpx* sc = scr + g * L::GH::SCR;
+    cpx* sc = scr + g * L::SCR_HS;
     gfft_stage1<FH, true>(v, t, sc, tw);
     __syncthreads();
     gfft_stage2<FH, true>(v, t, sc);
@@ -359,7 +359,7 @@ __global__ __launch_bounds__(kNT) void k_lrfft_cols(int hin, const cpx* __restri
     using L = LG<FH, FW>;
     constexpr int EH = L::GH::E, GH = L::GH::G, CPW = kNT / GH, SP = L::SP;
     __shared__ cpx tw[NC_TW_N];
-    __shared__ cpx scr[CPW * L::GH::SCR];
+    __shared__ cpx scr[CPW * L::SCR_HS];
     load_twiddles(tw);
     __syncthreads();
     const int tid = threadIdx.x, g = tid % CPW, t = tid / CPW;
@@ -372,7 +372,7 @@ __global__ __launch_bounds__(kNT) void k_lrfft_cols(int hin, const cpx* __restri
         const int r = t + GH * n1;
         v[n1] = on && r < hin ? col[(size_t)r * SP] : cmk(0.f, 0.f);
     }
-    cpx* sc = scr + g * L::GH::SCR;
+    cpx* sc = scr + g * L::SCR_HS;
     gfft_stage1<FH, false>(v, t, sc, tw);
     __syncthreads();
     gfft_stage2<FH, false>(v, t, sc);
@@ -388,7 +388,8 @@ __global__ __launch_bounds__(kNT) void k_lrfft_cols(int hin, const cpx* __restri
 //   dxpart[c][b] = sum over the chunk's directions m of sp_bm * conj(ghat_m)   (need_dx)
 //   dghat[m]     = (+=) sum over b of sp_bm * conj(xhat_b)  (conjugated when conj_out)
 //   ssum[m]      = (+=, sum_acc) sum over b of sp_bm, the spectrum of sum_b gz_bm  (with ssum)
-// Thread = one bin; directions m0 .. m0+MC-1 of chunk c = blockIdx.y; b in increasing order.
+// Thread = one bin; directions m0 .. m0+MC-1 of chunk c = blockIdx.y; b in increasing order
+// over sample slice blockIdx.z, whose sums go to row blockIdx.z of dghat / ssum (M*F each).
 template <int MC>
 __global__ __launch_bounds__(256) void k_lred(int B, int M, int F, int need_dx,
                                               const cpx* __restrict__ sp,
@@ -401,6 +402,10 @@ __global__ __launch_bounds__(256) void k_lred(int B, int M, int F, int need_dx,
     if (e >= F) return;
     const int m0 = blockIdx.y * MC;
     const int nm = min(MC, M - m0);
+    // sample slice z = blockIdx.z: b in [b0, b1), its sums into row z of dghat / ssum
+    const int bc = (B + gridDim.z - 1) / gridDim.z, b0 = blockIdx.z * bc, b1 = min(B, b0 + bc);
+    dghat += (size_t)blockIdx.z * M * F;
+    if (ssum) ssum += (size_t)blockIdx.z * M * F;
     cpx G[MC], acc[MC], sacc[MC];
 #pragma unroll
     for (int q = 0; q < MC; ++q) {
@@ -408,7 +413,7 @@ __global__ __launch_bounds__(256) void k_lred(int B, int M, int F, int need_dx,
         acc[q] = cmk(0.f, 0.f);
         sacc[q] = cmk(0.f, 0.f);
     }
-    for (int b = 0; b < B; ++b) {
+    for (int b = b0; b < b1; ++b) {
         const cpx X = xhat[(size_t)b * F + e];
         const cpx* s = sp + ((size_t)b * M + m0) * F + e;
         cpx v[MC];
@@ -712,15 +717,16 @@ int seg_dx(hipStream_t st, int B, int nchunk, int hin, int win, int ph, int pw, 
 template <int FH, int FW>
 int conv_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph, int pw,
              const float* gz, const float* xhat, const float* ghat, int need_dx, float* dx,
-             float* dghat, int accumulate, int conj_out, float* ssum, int sum_acc, void* ws) {
+             float* dghat, int accumulate, int conj_out, float* ssum, int sum_acc, int splits,
+             void* ws) {
     using L = LG<FH, FW>;
     const int nchunk = (M + kRedMC - 1) / kRedMC;
     cpx* sp = reinterpret_cast<cpx*>(ws);
     cpx* part = sp + (size_t)B * M * L::F;
     int rc = rfft2_two_pass<FH, FW>(st, B * M, hout, wout, (size_t)hout * wout, gz, sp);
     if (rc != NC_OK) return rc;
-    hipLaunchKernelGGL((k_lred<kRedMC>), dim3((L::F + 255) / 256, nchunk), dim3(256), 0, st, B,
-                       M, L::F, need_dx, sp, reinterpret_cast<const cpx*>(xhat),
+    hipLaunchKernelGGL((k_lred<kRedMC>), dim3((L::F + 255) / 256, nchunk, splits), dim3(256), 0,
+                       st, B, M, L::F, need_dx, sp, reinterpret_cast<const cpx*>(xhat),
                        reinterpret_cast<const cpx*>(ghat), part, reinterpret_cast<cpx*>(dghat),
                        accumulate, conj_out, reinterpret_cast<cpx*>(ssum), sum_acc);
     NC_CHECK_LAUNCH();
@@ -911,13 +917,24 @@ size_t nc_large_fftconv_bwd_ws(int B, int M, int fh, int fw) {
     return 0;
 }
 
+int nc_large_red_splits(int B, int M, int fh, int fw) {
+    if (B <= 0 || M <= 0 || !nc_large_grid(fh, fw)) return 0;
+    // sample slices that bring the reduction's grid to ~1024 workgroups
+    const int wgs = ((fh * (fw / 2 + 1) + 255) / 256) * ((M + kRedMC - 1) / kRedMC);
+    const int want = std::max(1, std::min(B, (1024 + wgs - 1) / wgs));
+    const int bc = (B + want - 1) / want;
+    return (B + bc - 1) / bc;
+}
+
 int nc_large_fftconv_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout,
                          int ph, int pw, int fh, int fw, const float* gz, const float* xhat,
                          const float* ghat, int need_dx, float* dx, float* dghat, int accumulate,
-                         int conj_dghat, float* gz_hat_sum, int sum_accumulate, void* ws) {
+                         int conj_dghat, float* gz_hat_sum, int sum_accumulate, int parts,
+                         void* ws) {
+    const int splits = parts ? nc_large_red_splits(B, M, fh, fw) : 1;
 #define NC_CALL(A, Bv)                                                                     \
     conv_bwd<A, Bv>(st, B, M, hin, win, hout, wout, ph, pw, gz, xhat, ghat, need_dx, dx, dghat, \
-                    accumulate, conj_dghat, gz_hat_sum, sum_accumulate, ws)
+                    accumulate, conj_dghat, gz_hat_sum, sum_accumulate, splits, ws)
     NC_DISPATCH_LARGE(fh, fw, NC_CALL);
 #undef NC_CALL
     return NC_ERR_UNSUPPORTED;
