@@ -179,7 +179,7 @@ _FAMILY_KERNELS = {
     "conv_port_fwd": ("k_pconv_port", "k_wconv_fwd", "k_linv_conv", "k_pconv_fwd",
                       "k_port_fwd", "k_port_combine", "k_port_fwd_tiled"),
     "fftconv_bwd": ("k_wbwd_part", "k_psum", "k_wbwd_dx_fin", "k_wbwd_dg_red", "k_wbwd_dg_sum",
-                    "k_lred", "k_linv_dx", "k_pspec", "k_pbwd_red", "k_pdx_half"),
+                    "k_lred", "k_linv_dx", "k_pspec", "k_r8spec", "k_pbwd_red", "k_pdx_half"),
     "epilogue_bwd": ("k_epi_bwd", "k_tile_bwd1", "k_tile_bwd2"),
     "port_bwd": ("k_port_bwd",),
 }
@@ -232,6 +232,39 @@ def traffic_summary(fetch_dir, write_dir, reps, out_path):
     with open(out_path, "w") as fh:
         json.dump(out, fh, indent=1)
     return out
+
+
+def trace_summary(trace_dir, out_path, title, steps=10):
+    """Per-kernel table of one train step from a rocprofv3 --kernel-trace run (rocpd database
+    under trace_dir): the launches of each of the last `steps` complete train steps (every launch
+    after one AdamW launch up to the next), averaged.  Writes markdown to out_path."""
+    import glob
+    import sqlite3
+    db = sorted(glob.glob(os.path.join(trace_dir, "**", "*.db"), recursive=True))[0]
+    con = sqlite3.connect(db)
+    rows = list(con.execute("select name, start, end from kernels order by start"))
+    names = [_short_kernel(r[0]) for r in rows]
+    ad = [i for i, n in enumerate(names) if n.startswith("k_adamw")]
+    segs = [(a + 1, b + 1) for a, b in zip(ad[:-1], ad[1:])][-steps:]
+    per, span, total = {}, 0.0, 0.0
+    for a, b in segs:
+        span += (rows[b - 1][2] - rows[a][1]) / 1e3
+        for i in range(a, b):
+            us = (rows[i][2] - rows[i][1]) / 1e3
+            n, t = per.get(names[i], (0, 0.0))
+            per[names[i]] = (n + 1, t + us)
+            total += us
+    k = max(1, len(segs))
+    lines = [f"# {title}", "", f"Steps: the last {len(segs)} AdamW-delimited train steps of the "
+             f"trace; launches per step: {sum(n for n, _ in per.values()) // k}; summed kernel "
+             f"time {total / k:.1f} us per step, first-to-last span {span / k:.1f} us (the span "
+             "includes the tracer's gaps).", "",
+             "| kernel | launches/step | us/step | us/launch |", "|---|---:|---:|---:|"]
+    for name, (n, t) in sorted(per.items(), key=lambda kv: -kv[1][1]):
+        lines.append(f"| `{name}` | {n / k:g} | {t / k:.2f} | {t / n:.2f} |")
+    with open(out_path, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    return per
 
 
 def _cpu_cores():
@@ -561,6 +594,9 @@ def main():
                     help="summarise rocprofv3 --pmc passes (rocpd databases) of a "
                          "--families-only run into the markdown table --counters-out and exit")
     ap.add_argument("--counters-out", default=os.path.join("gpurun_out", "counters.md"))
+    ap.add_argument("--trace-summary", nargs=2, metavar=("TRACE_DIR", "OUT_MD"), default=None,
+                    help="summarise a rocprofv3 --kernel-trace run of train steps into a "
+                         "per-kernel markdown table and exit")
     ap.add_argument("--conv-compare", action="store_true",
                     help="time the spectral and the direct correlation on the small-filter "
                          "chips (one JSON line per chip) and exit")
@@ -574,6 +610,11 @@ def main():
               "the data-parallel sharding over B is described in DESIGN.md", file=sys.stderr)
         sys.exit(2)
 
+    if args.trace_summary:
+        trace_summary(args.trace_summary[0], args.trace_summary[1],
+                      "Train step per-kernel trace (MI355X, gfx950)")
+        print(open(args.trace_summary[1]).read())
+        return
     if args.counters:
         counter_summary(args.counters, args.counters_out)
         print(open(args.counters_out).read())

@@ -469,22 +469,25 @@ __global__ __launch_bounds__(kTileNT) void k_tile_stats(int M, int N, int T, int
     }
 }
 
-// Chan combine of the T tile statistics of plane (b, m), fixed order.
-NC_DEV void chan_combine(const float* stats, size_t BMT, int b, int m, int M, int N, int T,
-                         float* mean, float* rstd) {
+// Chan combine of the T tile statistics of plane (b, m) by one wavefront: each lane takes
+// tiles lane, lane + 64, ... in order, then a butterfly over the lanes (fixed order).  Every
+// lane returns the result.
+NC_DEV void chan_combine_wave(const float* stats, size_t BMT, int b, int m, int M, int N, int T,
+                              float* mean, float* rstd) {
+    const int lane = threadIdx.x & (NC_WAVE - 1);
     const float* s1 = stats + ((size_t)b * M + m) * T;
     const float* m2 = s1 + BMT;
     float tot = 0.f;
-    for (int t = 0; t < T; ++t) tot += s1[t];
-    const float mu = tot / (float)N;
+    for (int t = lane; t < T; t += NC_WAVE) tot += s1[t];
+    const float mu = wave_sum(tot) / (float)N;
     float var = 0.f;
-    for (int t = 0; t < T; ++t) {
+    for (int t = lane; t < T; t += NC_WAVE) {
         const int nt = min(kTileN, N - t * kTileN);
         const float d = s1[t] / (float)nt - mu;
         var += m2[t] + (float)nt * d * d;
     }
     *mean = mu;
-    *rstd = 1.0f / sqrtf(var / (float)N + 1e-5f);
+    *rstd = 1.0f / sqrtf(wave_sum(var) / (float)N + 1e-5f);
 }
 
 // Directions whose loads a tiled kernel keeps in flight together.
@@ -506,14 +509,17 @@ __global__ __launch_bounds__(kTileNT) void k_tile_fwd(int B, int M, int N, int T
     __shared__ float smu[kMaxM], srs[kMaxM];
     const int t = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
     const size_t BMT = (size_t)B * M * T;
-    for (int m = tid; m < M; m += kTileNT) {
+    // one wavefront per direction combines its tile statistics
+    for (int m = tid / NC_WAVE; m < M; m += kTileNT / NC_WAVE) {
         float mu, r;
-        chan_combine(stats, BMT, b, m, M, N, T, &mu, &r);
-        smu[m] = mu;
-        srs[m] = r;
-        if (t == 0) {
-            mean[(size_t)b * M + m] = mu;
-            rstd[(size_t)b * M + m] = r;
+        chan_combine_wave(stats, BMT, b, m, M, N, T, &mu, &r);
+        if ((tid & (NC_WAVE - 1)) == 0) {
+            smu[m] = mu;
+            srs[m] = r;
+            if (t == 0) {
+                mean[(size_t)b * M + m] = mu;
+                rstd[(size_t)b * M + m] = r;
+            }
         }
     }
     const int base = t * kTileN;
@@ -666,13 +672,15 @@ __global__ __launch_bounds__(kTileNT) void k_tile_bwd2(
         wv[k] = w[pc[k]];
         sv[k] = s[pc[k]];
     }
-    float c1 = 0.f, c2 = 0.f;
-    for (int u = 0; u < T; ++u) {
-        c1 += c1p[u];
-        c2 += c2p[u];
+    // the plane's (c1, c2): the T tile partials summed by the workgroup (fixed order)
+    __shared__ float red[2 * (kTileNT / 64) + 2];
+    float c[2] = {0.f, 0.f};
+    for (int u = tid; u < T; u += kTileNT) {
+        c[0] += c1p[u];
+        c[1] += c2p[u];
     }
-    c1 /= (float)N;
-    c2 /= (float)N;
+    block_sum<2, kTileNT>(c, red);
+    const float c1 = c[0] / (float)N, c2 = c[1] / (float)N;
     const float mu = mean[(size_t)b * M + m], r = rstd[(size_t)b * M + m];
 #pragma unroll
     for (int k = 0; k < kTilePPT; ++k) {
@@ -842,13 +850,15 @@ __global__ __launch_bounds__(256) void k_port_fwd_tiled(
     __shared__ float smu[kMaxM], srs[kMaxM];
     const int b = blockIdx.x;
     const size_t BMT = (size_t)B * M * T;
-    for (int m = threadIdx.x; m < M; m += blockDim.x) {
+    for (int m = threadIdx.x / NC_WAVE; m < M; m += blockDim.x / NC_WAVE) {
         float mu, r;
-        chan_combine(stats, BMT, b, m, M, N, T, &mu, &r);
-        smu[m] = mu;
-        srs[m] = r;
-        mean[(size_t)b * M + m] = mu;
-        rstd[(size_t)b * M + m] = r;
+        chan_combine_wave(stats, BMT, b, m, M, N, T, &mu, &r);
+        if ((threadIdx.x & (NC_WAVE - 1)) == 0) {
+            smu[m] = mu;
+            srs[m] = r;
+            mean[(size_t)b * M + m] = mu;
+            rstd[(size_t)b * M + m] = r;
+        }
     }
     __syncthreads();
     port_gather(b, B, M, 0, M, 1, 0, N, P, hb, fact, slope, pidx, z, delta, pp, smu, srs, szo,

@@ -45,14 +45,15 @@ inline void __syncthreads() { g_bar->arrive_and_wait(); }
 extern std::barrier<>* g_wbar[16];
 inline void emu_wave_sync() { g_wbar[threadIdx.x / 64]->arrive_and_wait(); }
 #define NC_WAVE_SYNC() emu_wave_sync()
-// Cross-lane exchange; every work-item of the workgroup must call it together.
+// Cross-lane exchange within a wavefront (off < 64); every lane of the wavefront must call it
+// together, as on the device.
 inline float __shfl_xor(float v, int off, int) {
     static float buf[1024];
     const int t = threadIdx.x;
     buf[t] = v;
-    __syncthreads();
+    emu_wave_sync();
     const float r = buf[t ^ off];
-    __syncthreads();
+    emu_wave_sync();
     return r;
 }
 // DPP lane permutation; only quad_perm [1,0,3,2] (0xB1, swap within lane pairs) is used.
@@ -60,9 +61,9 @@ inline int emu_dpp(int v, int ctrl) {
     static int buf[1024];
     const int t = threadIdx.x;
     buf[t] = v;
-    __syncthreads();
+    emu_wave_sync();
     const int r = ctrl == 0xB1 ? buf[t ^ 1] : v;
-    __syncthreads();
+    emu_wave_sync();
     return r;
 }
 #define __builtin_amdgcn_update_dpp(old, src, ctrl, rm, bm, bc) emu_dpp((src), (ctrl))

@@ -39,7 +39,7 @@ def run_plan(topo, cell, filt, x, g_out, mode="continuous", tau=1.0, bbox=None,
 
 
 def check(geom, topo, cell, filt, x, mode, tau, bbox, final_act=None, hard_pin=False, seed=0,
-          conv="auto"):
+          conv="auto", out_tol=FWD_TOL):
     B = x.shape[0]
     rng = np.random.default_rng(seed + 100)
     g_out = rng.normal(size=(B,) + geom.out_size).astype(np.float32)
@@ -51,7 +51,7 @@ def check(geom, topo, cell, filt, x, mode, tau, bbox, final_act=None, hard_pin=F
     errs = {"out": rel_l2(out, r_out.reshape(B, -1)), "gW": rel_l2(gc[0], r_gc[0]),
             "gB": rel_l2(gc[1], r_gc[1]), "gS": rel_l2(gc[2], r_gc[2]),
             "gG": rel_l2(gf, r_gf)}
-    assert errs["out"] < FWD_TOL, errs
+    assert errs["out"] < out_tol, errs
     for k in ("gW", "gB", "gS", "gG"):
         assert errs[k] < GRAD_TOL, errs
     return errs
@@ -106,13 +106,25 @@ def test_trained_checkpoint_parameters():
 def test_large_grid_step_parity(name, B, M):
     """Configs 2 and 3 (256x256 spectral grids, tiled epilogues; config 3 cropped to 224x224)
     and the literal 128x128 config 2, at their full depth with a reduced batch and direction
-    count so the float64 oracle stays quick."""
+    count so the float64 oracle stays quick.  Config 3's port outputs (8 steps of 256x256
+    correlations) carry about 1e-5 of rounding in any fp32 evaluation: they are held to the
+    larger of 1e-5 and 1.25x the error of the oracle's own algorithm run in float32."""
     from helpers import config_geometry
     from neurocell.configs import CONFIGS
     cfg = CONFIGS[name]
     cell, filt, x, _ = cfg.synthetic(5, batch=B, directions=M)
-    check(config_geometry(cfg, directions=M), cfg.topology(directions=M), cell, filt, x,
-          cfg.codd_mode, cfg.tau, cfg.roi_bbox)
+    geom = config_geometry(cfg, directions=M)
+    out_tol = FWD_TOL
+    if name == "config3":
+        ref = O.propagate(cell, filt, x, geom, roi_bbox=cfg.roi_bbox, mode=cfg.codd_mode,
+                          tau=cfg.tau)[0]
+        with O.precision(np.float32, workers=8):
+            f32 = O.propagate(cell, filt, x, geom, roi_bbox=cfg.roi_bbox, mode=cfg.codd_mode,
+                              tau=cfg.tau)[0]
+        out_tol = max(FWD_TOL, 1.25 * rel_l2(f32, ref))
+        print(f"[config3] fp32 restatement port rel-L2 {out_tol / 1.25:.3e}", flush=True)
+    check(geom, cfg.topology(directions=M), cell, filt, x, cfg.codd_mode, cfg.tau, cfg.roi_bbox,
+          out_tol=out_tol)
 
 
 def _mode_case(mode, grid, kernel, M, depth, B=4, seed=30):
