@@ -390,7 +390,7 @@ int nc_fftconv_bwd_hat(void* stream, int M, int hin, int win, int pad_h, int pad
 
 /*
  * The number of partial rows nc_fftconv_bwd_parts writes per output at these shapes (its
- * sample chunks; on the large grids the reduction's sample slices, enough to give it ~1024
+ * sample chunks; on the large grids the reduction's sample slices, enough to give it ~512
  * workgroups).
  */
 int nc_fftconv_bwd_partials(int B, int M, int fft_h, int fft_w);

@@ -919,9 +919,9 @@ size_t nc_large_fftconv_bwd_ws(int B, int M, int fh, int fw) {
 
 int nc_large_red_splits(int B, int M, int fh, int fw) {
     if (B <= 0 || M <= 0 || !nc_large_grid(fh, fw)) return 0;
-    // sample slices that bring the reduction's grid to ~1024 workgroups
+    // sample slices that bring the reduction's grid to ~512 workgroups
     const int wgs = ((fh * (fw / 2 + 1) + 255) / 256) * ((M + kRedMC - 1) / kRedMC);
-    const int want = std::max(1, std::min(B, (1024 + wgs - 1) / wgs));
+    const int want = std::max(1, std::min(B, (512 + wgs - 1) / wgs));
     const int bc = (B + want - 1) / want;
     return (B + bc - 1) / bc;
 }
