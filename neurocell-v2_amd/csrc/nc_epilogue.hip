@@ -571,8 +571,12 @@ __global__ __launch_bounds__(kTileNT) void k_tile_bwd1(
     const float* __restrict__ delta, const float* __restrict__ w, const float* __restrict__ s,
     const float* __restrict__ bb, const float* __restrict__ mean, const float* __restrict__ rstd,
     const float* __restrict__ gy, float* __restrict__ cpart, float* __restrict__ pg, size_t BN) {
-    __shared__ float red[2 * kTileMC * (kTileNT / 64) + 2 * kTileMC];
+    // per-wavefront (c1, c2) sums of every direction, red[wave][c1 | c2][m], added over the
+    // wavefronts once after the direction loop
+    constexpr int NWV = kTileNT / 64;
+    __shared__ float red[NWV * 2 * kMaxM];
     const int t = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
     const int base = t * kTileN;
     const int nt = min(kTileN, N - base);
     const float* dl = border_src(hb, delta, z);
@@ -622,19 +626,23 @@ __global__ __launch_bounds__(kTileNT) void k_tile_bwd1(
                 c[kTileMC + q] += gn * zn;
             }
         }
-        block_sum<2 * kTileMC, kTileNT>(c, red);
-        if (tid < kTileMC && m0 + tid < M) {
-            const size_t o = ((size_t)b * M + m0 + tid) * T + t;
-            float c1 = c[0], c2 = c[kTileMC];
+        // wavefront sums now (no barrier), the workgroup sum after the loop
 #pragma unroll
-            for (int q = 1; q < kTileMC; ++q)
-                if (tid == q) {
-                    c1 = c[q];
-                    c2 = c[kTileMC + q];
-                }
-            cpart[o] = c1;
-            cpart[BMT + o] = c2;
+        for (int q = 0; q < kTileMC; ++q) {
+            const float a1 = wave_sum(c[q]), a2 = wave_sum(c[kTileMC + q]);
+            if (lane == 0 && m0 + q < M) {
+                red[wave * 2 * kMaxM + m0 + q] = a1;
+                red[wave * 2 * kMaxM + kMaxM + m0 + q] = a2;
+            }
         }
+    }
+    __syncthreads();
+    for (int e = tid; e < 2 * M; e += kTileNT) {
+        const int k = e / M, m = e - k * M;  // k: c1 or c2
+        float v = 0.f;
+#pragma unroll
+        for (int w2 = 0; w2 < NWV; ++w2) v += red[w2 * 2 * kMaxM + k * kMaxM + m];
+        cpart[(size_t)k * BMT + ((size_t)b * M + m) * T + t] = v;
     }
 #pragma unroll
     for (int k = 0; k < kTilePPT; ++k) {  // BN: the gw / gs / gb plane stride
