@@ -177,26 +177,34 @@ __global__ __launch_bounds__(kDNT) void k_dconv_fwd(int M, int hin, int win, int
 //   dx[b, y, c] = sum over m, u, v of gz[b, m, y - oh - u, c - ow - v] * G[m, u, v]
 // LDS: the filters gs[(m * kh + u) * kwp + v], then MCH directions' cotangent bands, staged
 // chunk by chunk: TR + kh - 1 rows of win + kwp - 1 columns, staged row rz / column cz holding
-// gz row y0 - oh - (kh - 1) + rz, column -ow - (kwp - 1) + cz.
-template <int R>
+// gz row y0 - oh - (kh - 1) + rz, column -ow - (kwp - 1) + cz; with NQ > 1 then NQ x PT x R
+// floats for the direction groups' partial sums.  The workgroup's PT = 256 / NQ pixel
+// threads are laid over the band as (row group, column), R rows each; thread group q < NQ
+// takes directions m = q, q + NQ, ... of every chunk, and the NQ partial sums of a pixel
+// are added in increasing q.  NQ = 4 on planes up to 64 wide gives four times the
+// workgroups of NQ = 1 at the same work per pixel.
+template <int R, int NQ>
 __global__ __launch_bounds__(kDNT) void k_dconv_dx(int M, int hin, int win, int hout, int wout,
                                                    int oh, int ow, int kh, int kw, int circ,
                                                    int TR, int MCH, const float* __restrict__ gz,
                                                    const float* __restrict__ g,
                                                    float* __restrict__ dx) {
     HIP_DYNAMIC_SHARED(float, lds)
+    constexpr int PT = kDNT / NQ;
     const int kwp = pad4(kw), ng = M * kh * kwp;
-    float* gs = lds;
-    float* zs = lds + ng;
     const int b = blockIdx.y, y0 = blockIdx.x * TR, tid = threadIdx.x;
     const int rows = min(TR, hin - y0);
     const int zr = rows + kh - 1, zc = win + kwp - 1, zplane = (TR + kh - 1) * zc;
+    float* gs = lds;
+    float* zs = lds + ng;
+    float* red = zs + (size_t)MCH * zplane;
     const int r_lo = y0 - oh - (kh - 1), c_lo = -ow - (kwp - 1);
     for (int e = tid; e < ng; e += kDNT) {
         const int t = e / kwp, v = e - t * kwp;  // t = m * kh + u
         gs[e] = v < kw ? g[(size_t)t * kw + v] : 0.f;
     }
-    const int j = tid % win, rb = (tid / win) * R;
+    const int pt = tid % PT, q = tid / PT;
+    const int j = pt % win, rb = (pt / win) * R;
     const bool active = rb < rows;
     float acc[R];
 #pragma unroll
@@ -228,20 +236,34 @@ __global__ __launch_bounds__(kDNT) void k_dconv_dx(int M, int hin, int win, int 
                 const float* zu = z0 - u * zc - v0;
                 const float* gu = g0 + u * kwp + v0;
 #pragma unroll 4
-                for (int m = 0; m < nm; ++m) {
+                for (int m = q; m < nm; m += NQ) {
                     float zv[4][R], gv[4];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) gv[q] = gu[m * kh * kwp + q];
+                    for (int e = 0; e < 4; ++e) gv[e] = gu[m * kh * kwp + e];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q)
+                    for (int e = 0; e < 4; ++e)
 #pragma unroll
-                        for (int r = 0; r < R; ++r) zv[q][r] = zu[m * zplane + r * zc - q];
+                        for (int r = 0; r < R; ++r) zv[e][r] = zu[m * zplane + r * zc - e];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q)
+                    for (int e = 0; e < 4; ++e)
 #pragma unroll
-                        for (int r = 0; r < R; ++r) acc[r] = fmaf(zv[q][r], gv[q], acc[r]);
+                        for (int r = 0; r < R; ++r) acc[r] = fmaf(zv[e][r], gv[e], acc[r]);
                 }
             }
+        }
+    }
+    if constexpr (NQ > 1) {
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < R; ++r) red[(q * PT + pt) * R + r] = acc[r];
+        __syncthreads();
+        if (q != 0) return;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float v = red[pt * R + r];
+#pragma unroll
+            for (int q2 = 1; q2 < NQ; ++q2) v += red[(q2 * PT + pt) * R + r];
+            acc[r] = v;
         }
     }
     if (!active) return;
@@ -376,27 +398,30 @@ bool fwd_shape(int B, int M, int hout, int wout, int kh, int kw, FwdShape* f) {
     return found;
 }
 
-// Input gradient: R = 4, 2 or 1, the first whose grid reaches 2048 workgroups (else the last
-// that fits); MCH directions per staged chunk, as many as the LDS holds.
+// Input gradient: NQ = 4 direction groups on planes up to 64 wide (else 1); R = 4, 2 or 1,
+// the first whose grid reaches 1024 workgroups (else the last that fits); MCH directions per
+// staged chunk, as many as the LDS holds.
 struct DxShape {
-    int R, TR, bands, MCH;
+    int R, NQ, TR, bands, MCH;
     size_t shm;
 };
 
 bool dx_shape(int B, int M, int hin, int win, int kh, int kw, DxShape* d) {
     const size_t ng = (size_t)M * kh * pad4h(kw);
-    const int zc = win + pad4h(kw) - 1, ngrp = kDNT / win;
+    const int NQ = win <= 64 ? 4 : 1, ngrp = (kDNT / NQ) / win;
+    const int zc = win + pad4h(kw) - 1;
     bool found = false;
     for (int R = 4; R >= 1; R /= 2) {
         const int TR = ngrp * R;
         const size_t plane = (size_t)(TR + kh - 1) * zc;
-        if (ng * 4 >= kDLds) return false;
-        const size_t room = kDLds / 4 - ng;
+        const size_t red = NQ > 1 ? (size_t)kDNT * R : 0;
+        if ((ng + red) * 4 >= kDLds) return found;
+        const size_t room = kDLds / 4 - ng - red;
         if (room < plane) continue;
         const int MCH = (int)std::min<size_t>(M, room / plane);
-        *d = DxShape{R, TR, (hin + TR - 1) / TR, MCH, (ng + MCH * plane) * 4};
+        *d = DxShape{R, NQ, TR, (hin + TR - 1) / TR, MCH, (ng + MCH * plane + red) * 4};
         found = true;
-        if ((size_t)B * d->bands >= 2048) break;
+        if ((size_t)B * d->bands >= 1024) break;
     }
     return found;
 }
@@ -478,12 +503,18 @@ int nc_direct_conv_bwd(void* stream, int B, int M, int hin, int win, int hout, i
     if (!TR || (need_dx && !dx_shape(B, M, hin, win, kh, kw, &d))) return NC_ERR_UNSUPPORTED;
     if (need_dx) {
         const dim3 grid(d.bands, B);
-#define NC_DDX(R_)                                                                             \
-    hipLaunchKernelGGL((k_dconv_dx<R_>), grid, dim3(kDNT), d.shm, st, M, hin, win, hout, wout,  \
-                       oh, ow, kh, kw, circular, d.TR, d.MCH, gz, filters, dx)
-        if (d.R == 4) NC_DDX(4);
-        else if (d.R == 2) NC_DDX(2);
-        else NC_DDX(1);
+#define NC_DDX(R_, NQ_)                                                                        \
+    hipLaunchKernelGGL((k_dconv_dx<R_, NQ_>), grid, dim3(kDNT), d.shm, st, M, hin, win, hout,   \
+                       wout, oh, ow, kh, kw, circular, d.TR, d.MCH, gz, filters, dx)
+        if (d.NQ == 4) {
+            if (d.R == 4) NC_DDX(4, 4);
+            else if (d.R == 2) NC_DDX(2, 4);
+            else NC_DDX(1, 4);
+        } else {
+            if (d.R == 4) NC_DDX(4, 1);
+            else if (d.R == 2) NC_DDX(2, 1);
+            else NC_DDX(1, 1);
+        }
 #undef NC_DDX
         NC_CHECK_LAUNCH();
     }

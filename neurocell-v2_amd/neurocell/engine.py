@@ -40,9 +40,9 @@ from .topology import ChipTopology2D, CoordinatePortSpec
 
 _WAVE_FFT = (16, 32, 64)        # wavefront transforms (a plane per lane group)
 # filters up to this many taps run the direct correlation (the reference's rule,
-# propagator.py:373-386); a train step only up to 36 taps and with at least 4 directions, where
-# its spatial reverse (input and filter gradients) measured faster than the spectral one on
-# MI355X (bench.py --conv-compare)
+# propagator.py:373-386); a train step only with at least 4 directions and up to 36 taps (or
+# up to 64 where the spectral grid is not a fused one), where its spatial reverse (input and
+# filter gradients) measured faster than the spectral one on MI355X (bench.py --conv-compare)
 _DIRECT_MAX_K = 64
 _DIRECT_MAX_K_TRAIN = 36
 _DIRECT_MIN_M_TRAIN = 4
@@ -179,8 +179,15 @@ class StepPlan:
         if conv == "direct" and not direct_ok:
             raise NeurocellError("the direct correlation takes kh * kw <= 64, M <= 64 and "
                                  "planes up to 256 wide whose bands fit the workgroup's LDS")
-        auto = (kh * kw <= _DIRECT_MAX_K_TRAIN and M >= _DIRECT_MIN_M_TRAIN
-                if self.training else True)
+        auto = True
+        if self.training:  # measured: the direct reverse pays up to 36 taps, or up to 64
+            # where the spectral grid is not one of the fused 32x64 / 64x64 ones
+            sg = (H, W) if self.circular else (
+                (_npow2(h + kh - 1), _npow2(w + kw - 1)) if self.cropped
+                else tuple(topology.fft_shape))
+            sg = tuple(max(16, v) for v in sg)
+            fused_grid = sg[1] == 64 and sg[0] in (32, 64)
+            auto = M >= _DIRECT_MIN_M_TRAIN and (kh * kw <= _DIRECT_MAX_K_TRAIN or not fused_grid)
         self.direct = conv == "direct" or (conv == "auto" and direct_ok and auto)
         if self.direct:
             if self.circular and self.cropped:
