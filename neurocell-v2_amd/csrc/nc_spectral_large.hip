@@ -570,7 +570,9 @@ template <int FH, int FW>
 int rfft2_planes(hipStream_t st, int nplanes, int hin, int win, size_t pstride, bool flip,
                  const float* x, cpx* out, int post_kind = kPostNone,
                  const SpecPost& post = SpecPost{}, int nq = 1, size_t qstride = 0) {
-    const int cs = fwd_cols<FH, FW>(hin);
+    int cs = fwd_cols<FH, FW>(hin);
+    // few planes: more column segments (the row pass repeats per segment) to fill the CUs
+    while (cs > 8 && (size_t)nplanes * (LG<FH, FW>::NC / cs) < 256) cs >>= 1;
     const size_t lds = lfwd_lds_bytes<FH, FW, kNT>(hin, cs);
     if (lds > kLdsMax) return NC_ERR_UNSUPPORTED;
     const dim3 grid(nplanes, LG<FH, FW>::NC / cs);
@@ -740,7 +742,9 @@ int conv_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout,
 template <int FH, int FW, int NCH>
 void seg_dx_launch(hipStream_t st, int B, int nchunk, int hin, int win, int ph, int pw,
                    const cpx* dxs, float* dx) {
-    const int rs = inv_rows<FH, FW>(hin);
+    int rs = inv_rows<FH, FW>(hin);
+    // few planes: more row segments (the column pass repeats per segment) to fill the CUs
+    while (rs > 8 && (size_t)B * ((hin + rs - 1) / rs) < 256) rs = (rs + 1) / 2;
     const size_t lds = linv_lds_bytes<FH, FW, kNT>(rs);
     set_lds(k_linv_dx<FH, FW, NCH>, lds);
     hipLaunchKernelGGL((k_linv_dx<FH, FW, NCH>), dim3(B, (hin + rs - 1) / rs), dim3(kNT), lds, st,
