@@ -429,11 +429,61 @@ int launch_batch_reduce(hipStream_t st, const RedJob* jobs, int njobs) {
 constexpr int kTileNT = 256;
 constexpr int kTilePPT = kTileN / kTileNT;
 
+// A thread's kTilePPT pixels of a tile: with VEC four consecutive pixels, moved as one 16-byte
+// access per plane (N % 4 == 0, so every tile holds a multiple of 4 pixels), otherwise pixels
+// kTileNT apart.  Loads are clamped into the tile; `in` says which pixels are real.
+static_assert(kTilePPT == 4, "one 16-byte access per plane and thread");
+
+template <bool VEC>
+struct TilePx {
+    static NC_DEV bool in(int tid, int k, int nt) {
+        return VEC ? 4 * tid < nt : tid + k * kTileNT < nt;
+    }
+    // p: the plane's tile base
+    static NC_DEV void load(const float* __restrict__ p, int tid, int nt,
+                            float (&v)[kTilePPT]) {
+        if constexpr (VEC) {
+            const float4 a = reinterpret_cast<const float4*>(p)[min(tid, (nt >> 2) - 1)];
+            v[0] = a.x;
+            v[1] = a.y;
+            v[2] = a.z;
+            v[3] = a.w;
+        } else {
+#pragma unroll
+            for (int k = 0; k < kTilePPT; ++k) v[k] = p[min(tid + k * kTileNT, nt - 1)];
+        }
+    }
+    // the real pixels only; 16-byte stores when p is 16-byte aligned (a uniform test)
+    static NC_DEV void store(float* __restrict__ p, int tid, int nt,
+                             const float (&v)[kTilePPT]) {
+        if (VEC && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+            if (4 * tid < nt)
+                reinterpret_cast<float4*>(p)[tid] = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < kTilePPT; ++k) {
+                const int i = VEC ? 4 * tid + k : tid + k * kTileNT;
+                if (i < nt) p[i] = v[k];
+            }
+        }
+    }
+};
+
+// 16-byte accesses apply when every plane the tiled kernels read that way is 16-byte aligned
+// (the pixel mapping, and so the reduction order, then depends on the inputs only).
+inline bool tile_vec(int N, int hb, const float* z, const float* delta, const float* w,
+                     const float* s, const float* bb, const float* gy = nullptr) {
+    return N % 4 == 0 && aligned16(z) && (!hb || aligned16(delta)) && aligned16(w) &&
+           aligned16(s) && aligned16(bb) && (!gy || aligned16(gy));
+}
+
 // Per-(b, m, tile) sum and centred sum of squares; stats layout (2, B, M, T).
+template <bool VEC>
 __global__ __launch_bounds__(kTileNT) void k_tile_stats(int M, int N, int T, int hb,
                                                         const float* __restrict__ z,
                                                         const float* __restrict__ delta,
                                                         float* __restrict__ stats) {
+    using Px = TilePx<VEC>;
     __shared__ float red[kTileNT / 64 + 1];
     const int t = blockIdx.x, m = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
     const int base = t * kTileN;
@@ -441,14 +491,13 @@ __global__ __launch_bounds__(kTileNT) void k_tile_stats(int M, int N, int T, int
     const float* zp = z + ((size_t)b * M + m) * N + base;
     const float* dp = border_src(hb, delta + (size_t)m * N, z + ((size_t)b * M + m) * N) + base;
     const float hbf = hb ? 1.f : 0.f;
-    float v[kTilePPT];
+    float v[kTilePPT], d[kTilePPT];
+    Px::load(zp, tid, nt, v);
+    Px::load(dp, tid, nt, d);
     float s1 = 0.f;
 #pragma unroll
     for (int k = 0; k < kTilePPT; ++k) {
-        const int i = tid + k * kTileNT;
-        const int ic = min(i, nt - 1);
-        const float x = zp[ic] + hbf * dp[ic];
-        v[k] = i < nt ? x : 0.f;
+        v[k] = Px::in(tid, k, nt) ? v[k] + hbf * d[k] : 0.f;
         s1 += v[k];
     }
     block_sum<1, kTileNT>(&s1, red);
@@ -456,9 +505,8 @@ __global__ __launch_bounds__(kTileNT) void k_tile_stats(int M, int N, int T, int
     float m2 = 0.f;
 #pragma unroll
     for (int k = 0; k < kTilePPT; ++k) {
-        const int i = tid + k * kTileNT;
-        const float d = i < nt ? v[k] - mu : 0.f;
-        m2 += d * d;
+        const float dv = Px::in(tid, k, nt) ? v[k] - mu : 0.f;
+        m2 += dv * dv;
     }
     block_sum<1, kTileNT>(&m2, red);
     if (tid == 0) {
@@ -467,6 +515,16 @@ __global__ __launch_bounds__(kTileNT) void k_tile_stats(int M, int N, int T, int
         stats[o] = s1;
         stats[BMT + o] = m2;
     }
+}
+
+void tile_stats(hipStream_t st, bool vec, int B, int M, int N, int T, int hb, const float* z,
+                const float* delta, float* stats) {
+    if (vec)
+        hipLaunchKernelGGL(k_tile_stats<true>, dim3(T, M, B), dim3(kTileNT), 0, st, M, N, T, hb,
+                           z, delta, stats);
+    else
+        hipLaunchKernelGGL(k_tile_stats<false>, dim3(T, M, B), dim3(kTileNT), 0, st, M, N, T, hb,
+                           z, delta, stats);
 }
 
 // Chan combine of the T tile statistics of plane (b, m) by one wavefront: each lane takes
@@ -494,7 +552,7 @@ NC_DEV void chan_combine_wave(const float* stats, size_t BMT, int b, int m, int 
 constexpr int kTileMC = 4;
 
 // Per-(tile, b): statistics from the Chan partials, then standardise + Codd + sum over M.
-template <int ACT>
+template <int ACT, bool VEC>
 __global__ __launch_bounds__(kTileNT) void k_tile_fwd(int B, int M, int N, int T, float slope,
                                                       int hb,
                                                       const float* __restrict__ z,
@@ -506,6 +564,7 @@ __global__ __launch_bounds__(kTileNT) void k_tile_fwd(int B, int M, int N, int T
                                                       float* __restrict__ out,
                                                       float* __restrict__ mean,
                                                       float* __restrict__ rstd) {
+    using Px = TilePx<VEC>;
     __shared__ float smu[kMaxM], srs[kMaxM];
     const int t = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
     const size_t BMT = (size_t)B * M * T;
@@ -526,25 +585,20 @@ __global__ __launch_bounds__(kTileNT) void k_tile_fwd(int B, int M, int N, int T
     const int nt = min(kTileN, N - base);
     const float* dl = border_src(hb, delta, z);
     const float hbf = hb ? 1.f : 0.f;
-    int pc[kTilePPT];
     float lin[kTilePPT], ac[kTilePPT], bv[kTilePPT], wv[kTilePPT], sv[kTilePPT];
+    Px::load(bb + base, tid, nt, bv);
+    Px::load(w + base, tid, nt, wv);
+    Px::load(s + base, tid, nt, sv);
 #pragma unroll
-    for (int k = 0; k < kTilePPT; ++k) {
-        pc[k] = base + min(tid + k * kTileNT, nt - 1);
-        lin[k] = ac[k] = 0.f;
-        bv[k] = bb[pc[k]];
-        wv[k] = w[pc[k]];
-        sv[k] = s[pc[k]];
-    }
+    for (int k = 0; k < kTilePPT; ++k) lin[k] = ac[k] = 0.f;
     __syncthreads();
     for (int m0 = 0; m0 < M; m0 += kTileMC) {
-        float v[kTileMC][kTilePPT];
+        float v[kTileMC][kTilePPT], d[kTileMC][kTilePPT];
 #pragma unroll
         for (int q = 0; q < kTileMC; ++q) {
             const int m = min(m0 + q, M - 1);
-#pragma unroll
-            for (int k = 0; k < kTilePPT; ++k)
-                v[q][k] = z[((size_t)b * M + m) * N + pc[k]] + hbf * dl[(size_t)m * N + pc[k]];
+            Px::load(z + ((size_t)b * M + m) * N + base, tid, nt, v[q]);
+            Px::load(dl + (size_t)m * N + base, tid, nt, d[q]);
         }
 #pragma unroll
         for (int q = 0; q < kTileMC; ++q) {
@@ -552,25 +606,27 @@ __global__ __launch_bounds__(kTileNT) void k_tile_fwd(int B, int M, int N, int T
             const float mu = smu[m0 + q], r = srs[m0 + q];
 #pragma unroll
             for (int k = 0; k < kTilePPT; ++k) {
-                const float zn = (v[q][k] - mu) * r;
+                const float zn = (v[q][k] + hbf * d[q][k] - mu) * r;
                 lin[k] += zn;
                 ac[k] += act_f<ACT>(zn + bv[k], slope);
             }
         }
     }
+    float o[kTilePPT];
 #pragma unroll
-    for (int k = 0; k < kTilePPT; ++k)
-        if (tid + k * kTileNT < nt) out[(size_t)b * N + pc[k]] = wv[k] * lin[k] + sv[k] * ac[k];
+    for (int k = 0; k < kTilePPT; ++k) o[k] = wv[k] * lin[k] + sv[k] * ac[k];
+    Px::store(out + (size_t)b * N + base, tid, nt, o);
 }
 
 // Backward stage 1 per (tile, b): per-tile partial c1/c2 (layout (2, B, M, T)) and the
 // per-sample gw/gs/gb partials pg (3, B, N).
-template <int ACT>
+template <int ACT, bool VEC>
 __global__ __launch_bounds__(kTileNT) void k_tile_bwd1(
     int B, int M, int N, int T, float slope, int hb, const float* __restrict__ z,
     const float* __restrict__ delta, const float* __restrict__ w, const float* __restrict__ s,
     const float* __restrict__ bb, const float* __restrict__ mean, const float* __restrict__ rstd,
     const float* __restrict__ gy, float* __restrict__ cpart, float* __restrict__ pg, size_t BN) {
+    using Px = TilePx<VEC>;
     // per-wavefront (c1, c2) sums of every direction, red[wave][c1 | c2][m], added over the
     // wavefronts once after the direction loop
     constexpr int NWV = kTileNT / 64;
@@ -581,31 +637,28 @@ __global__ __launch_bounds__(kTileNT) void k_tile_bwd1(
     const int nt = min(kTileN, N - base);
     const float* dl = border_src(hb, delta, z);
     const float hbf = hb ? 1.f : 0.f;
-    int pc[kTilePPT];
     float lin[kTilePPT], ac[kTilePPT], dbs[kTilePPT], g[kTilePPT], wv[kTilePPT], sv[kTilePPT],
         bv[kTilePPT];
+    Px::load(gy + (size_t)b * N + base, tid, nt, g);
+    Px::load(w + base, tid, nt, wv);
+    Px::load(s + base, tid, nt, sv);
+    Px::load(bb + base, tid, nt, bv);
 #pragma unroll
     for (int k = 0; k < kTilePPT; ++k) {
-        const bool in = tid + k * kTileNT < nt;
-        pc[k] = base + min(tid + k * kTileNT, nt - 1);
         lin[k] = ac[k] = dbs[k] = 0.f;
-        const float gv = gy[(size_t)b * N + pc[k]];
-        g[k] = in ? gv : 0.f;  // zero cotangent outside the tile
-        wv[k] = w[pc[k]];
-        sv[k] = s[pc[k]];
-        bv[k] = bb[pc[k]];
+        if (!Px::in(tid, k, nt)) g[k] = 0.f;  // zero cotangent outside the tile
     }
     const size_t BMT = (size_t)B * M * T;
     for (int m0 = 0; m0 < M; m0 += kTileMC) {
-        float v[kTileMC][kTilePPT], mu[kTileMC], r[kTileMC], c[2 * kTileMC];
+        float v[kTileMC][kTilePPT], d[kTileMC][kTilePPT], mu[kTileMC], r[kTileMC],
+            c[2 * kTileMC];
 #pragma unroll
         for (int q = 0; q < kTileMC; ++q) {
             const int m = min(m0 + q, M - 1);
             mu[q] = mean[(size_t)b * M + m];
             r[q] = rstd[(size_t)b * M + m];
-#pragma unroll
-            for (int k = 0; k < kTilePPT; ++k)
-                v[q][k] = z[((size_t)b * M + m) * N + pc[k]] + hbf * dl[(size_t)m * N + pc[k]];
+            Px::load(z + ((size_t)b * M + m) * N + base, tid, nt, v[q]);
+            Px::load(dl + (size_t)m * N + base, tid, nt, d[q]);
         }
 #pragma unroll
         for (int q = 0; q < kTileMC; ++q) {
@@ -613,7 +666,7 @@ __global__ __launch_bounds__(kTileNT) void k_tile_bwd1(
             c[q] = c[kTileMC + q] = 0.f;
 #pragma unroll
             for (int k = 0; k < kTilePPT; ++k) {
-                const float zn = (v[q][k] - mu[q]) * r[q];
+                const float zn = (v[q][k] + hbf * d[q][k] - mu[q]) * r[q];
                 float a;
                 const float da = act_fd<ACT>(zn + bv[k], slope, &a);
                 const float gn = mv ? g[k] * (wv[k] + sv[k] * da) : 0.f;
@@ -644,22 +697,26 @@ __global__ __launch_bounds__(kTileNT) void k_tile_bwd1(
         for (int w2 = 0; w2 < NWV; ++w2) v += red[w2 * 2 * kMaxM + k * kMaxM + m];
         cpart[(size_t)k * BMT + ((size_t)b * M + m) * T + t] = v;
     }
+    float o0[kTilePPT], o1[kTilePPT];
 #pragma unroll
-    for (int k = 0; k < kTilePPT; ++k) {  // BN: the gw / gs / gb plane stride
-        if (tid + k * kTileNT >= nt) continue;
-        pg[(size_t)b * N + pc[k]] = g[k] * lin[k];
-        pg[BN + (size_t)b * N + pc[k]] = g[k] * ac[k];
-        pg[2 * BN + (size_t)b * N + pc[k]] = dbs[k];
+    for (int k = 0; k < kTilePPT; ++k) {
+        o0[k] = g[k] * lin[k];
+        o1[k] = g[k] * ac[k];
     }
+    float* p = pg + (size_t)b * N + base;  // BN: the gw / gs / gb plane stride
+    Px::store(p, tid, nt, o0);
+    Px::store(p + BN, tid, nt, o1);
+    Px::store(p + 2 * BN, tid, nt, dbs);
 }
 
 // Backward stage 2 per (tile, m, b): gz = rstd * (gzn - c1 - zn * c2).
-template <int ACT>
+template <int ACT, bool VEC>
 __global__ __launch_bounds__(kTileNT) void k_tile_bwd2(
     int B, int M, int N, int T, float slope, int hb, const float* __restrict__ z,
     const float* __restrict__ delta, const float* __restrict__ w, const float* __restrict__ s,
     const float* __restrict__ bb, const float* __restrict__ mean, const float* __restrict__ rstd,
     const float* __restrict__ gy, const float* __restrict__ cpart, float* __restrict__ gz) {
+    using Px = TilePx<VEC>;
     const int t = blockIdx.x, m = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
     const size_t BMT = (size_t)B * M * T;
     const float* c1p = cpart + ((size_t)b * M + m) * T;
@@ -669,17 +726,13 @@ __global__ __launch_bounds__(kTileNT) void k_tile_bwd2(
     const float* zp = z + ((size_t)b * M + m) * N;
     const float* dp = border_src(hb, delta + (size_t)m * N, zp);
     const float hbf = hb ? 1.f : 0.f;
-    int pc[kTilePPT];
-    float v[kTilePPT], bv[kTilePPT], g[kTilePPT], wv[kTilePPT], sv[kTilePPT];
-#pragma unroll
-    for (int k = 0; k < kTilePPT; ++k) {
-        pc[k] = base + min(tid + k * kTileNT, nt - 1);
-        v[k] = zp[pc[k]] + hbf * dp[pc[k]];
-        bv[k] = bb[pc[k]];
-        g[k] = gy[(size_t)b * N + pc[k]];
-        wv[k] = w[pc[k]];
-        sv[k] = s[pc[k]];
-    }
+    float v[kTilePPT], d[kTilePPT], bv[kTilePPT], g[kTilePPT], wv[kTilePPT], sv[kTilePPT];
+    Px::load(zp + base, tid, nt, v);
+    Px::load(dp + base, tid, nt, d);
+    Px::load(bb + base, tid, nt, bv);
+    Px::load(gy + (size_t)b * N + base, tid, nt, g);
+    Px::load(w + base, tid, nt, wv);
+    Px::load(s + base, tid, nt, sv);
     // the plane's (c1, c2): the T tile partials summed by the workgroup (fixed order)
     __shared__ float red[2 * (kTileNT / 64) + 2];
     float c[2] = {0.f, 0.f};
@@ -690,14 +743,16 @@ __global__ __launch_bounds__(kTileNT) void k_tile_bwd2(
     block_sum<2, kTileNT>(c, red);
     const float c1 = c[0] / (float)N, c2 = c[1] / (float)N;
     const float mu = mean[(size_t)b * M + m], r = rstd[(size_t)b * M + m];
+    float o[kTilePPT];
 #pragma unroll
     for (int k = 0; k < kTilePPT; ++k) {
-        const float zn = (v[k] - mu) * r;
+        const float zn = (v[k] + hbf * d[k] - mu) * r;
         float a;
         const float da = act_fd<ACT>(zn + bv[k], slope, &a);
         const float gn = g[k] * (wv[k] + sv[k] * da);
-        if (tid + k * kTileNT < nt) gz[((size_t)b * M + m) * N + pc[k]] = r * (gn - c1 - zn * c2);
+        o[k] = r * (gn - c1 - zn * c2);
     }
+    Px::store(gz + ((size_t)b * M + m) * N + base, tid, nt, o);
 }
 
 // ----------------------------------------------------------------------------------------
@@ -1244,13 +1299,18 @@ static int epilogue_fwd(void* stream, int B, int M, int h, int w, int act, float
         });
     }
     const int T = tiles_of(N);
-    hipLaunchKernelGGL(k_tile_stats, dim3(T, M, B), dim3(kTileNT), 0, st, M, N, T, has_border,
-                       z, delta, e.stats);
+    const bool vec = tile_vec(N, has_border, z, delta, w_eff, s_eff, b_roi);
+    tile_stats(st, vec, B, M, N, T, has_border, z, delta, e.stats);
     NC_CHECK_LAUNCH();
     return dispatch_act(act, [&]<int ACT>() {
-        hipLaunchKernelGGL((k_tile_fwd<ACT>), dim3(T, B), dim3(kTileNT), 0, st, B, M, N, T,
-                           neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, e.stats, out,
-                           mean, rstd);
+        if (vec)
+            hipLaunchKernelGGL((k_tile_fwd<ACT, true>), dim3(T, B), dim3(kTileNT), 0, st, B, M,
+                               N, T, neg_slope, has_border, z, delta, w_eff, s_eff, b_roi,
+                               e.stats, out, mean, rstd);
+        else
+            hipLaunchKernelGGL((k_tile_fwd<ACT, false>), dim3(T, B), dim3(kTileNT), 0, st, B, M,
+                               N, T, neg_slope, has_border, z, delta, w_eff, s_eff, b_roi,
+                               e.stats, out, mean, rstd);
         NC_CHECK_LAUNCH();
         return NC_OK;
     });
@@ -1313,14 +1373,21 @@ static int epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float
             return NC_OK;
         }
         const int T = tiles_of(N);
-        hipLaunchKernelGGL((k_tile_bwd1<ACT>), dim3(T, B), dim3(kTileNT), 0, st, B, M, N, T,
-                           neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, mean, rstd, gy,
-                           e.stats, pg, RN);
-        NC_CHECK_LAUNCH();
-        hipLaunchKernelGGL((k_tile_bwd2<ACT>), dim3(T, M, B), dim3(kTileNT), 0, st, B, M, N, T,
-                           neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, mean, rstd, gy,
-                           e.stats, gz);
-        NC_CHECK_LAUNCH();
+        const bool tv = tile_vec(N, has_border, z, delta, w_eff, s_eff, b_roi, gy);
+#define NC_TILE_BWD(V_)                                                                       \
+    do {                                                                                      \
+        hipLaunchKernelGGL((k_tile_bwd1<ACT, V_>), dim3(T, B), dim3(kTileNT), 0, st, B, M, N, \
+                           T, neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, mean,     \
+                           rstd, gy, e.stats, pg, RN);                                        \
+        NC_CHECK_LAUNCH();                                                                    \
+        hipLaunchKernelGGL((k_tile_bwd2<ACT, V_>), dim3(T, M, B), dim3(kTileNT), 0, st, B, M, \
+                           N, T, neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, mean,  \
+                           rstd, gy, e.stats, gz);                                            \
+        NC_CHECK_LAUNCH();                                                                    \
+    } while (0)
+        if (tv) NC_TILE_BWD(true);
+        else NC_TILE_BWD(false);
+#undef NC_TILE_BWD
         return NC_OK;
     });
     if (rc != NC_OK) return rc;
@@ -1598,8 +1665,8 @@ int nc_port_fwd(void* stream, int B, int M, int h, int w, int has_border, int fi
         return NC_OK;
     }
     const int T = tiles_of(N);
-    hipLaunchKernelGGL(k_tile_stats, dim3(T, M, B), dim3(kTileNT), 0, st, M, N, T, has_border,
-                       z, delta, e.stats);
+    tile_stats(st, N % 4 == 0 && aligned16(z) && (!has_border || aligned16(delta)), B, M, N, T,
+               has_border, z, delta, e.stats);
     NC_CHECK_LAUNCH();
     const size_t shm = (size_t)M * n_port * sizeof(float);
     hipLaunchKernelGGL(k_port_fwd_tiled, dim3(B), dim3(256), shm, st, B, M, N, T, n_port,

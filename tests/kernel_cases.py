@@ -971,6 +971,7 @@ EPILOGUE_SHAPES = [
     (2, 3, 33, 47, "relu", 1),
     (2, 3, 96, 100, "gelu", 1),
     (1, 2, 90, 92, "identity", 0),
+    (2, 3, 91, 91, "tanh", 1),  # tiled with N % 4 != 0: the per-pixel (non-vector) tiles
 ]
 
 PORT_SHAPES = [

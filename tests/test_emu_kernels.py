@@ -66,7 +66,7 @@ def test_plane_spectra(be, FH, FW, h, w, kh, kw):
 
 
 @pytest.mark.parametrize("shape", [(2, 3, 10, 12, "tanh", 1), (2, 3, 20, 40, "leaky_relu", 0),
-                                   (1, 2, 96, 90, "gelu", 1),
+                                   (1, 2, 96, 90, "gelu", 1), (1, 2, 91, 91, "tanh", 1),
                                    # directions split over workgroups (forward groups of 4,
                                    # backward groups of 8), the last group partial
                                    (3, 9, 10, 12, "tanh", 1), (2, 17, 6, 7, "sigmoid", 0)])
