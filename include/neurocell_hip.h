@@ -489,8 +489,10 @@ int nc_fftconv_epilogue_fwd(void* stream, int B, int M, int hout, int wout, int 
  * correlation (an axis of 128 or 256 points) as two transform passes - a column pass over
  * the B*M products xhat_b * ghat_m, then a row pass, B*M*hout*fft_w/2 complex values in
  * between - instead of one workgroup per plane segment; 0 on the other grids.  The same
- * results to rounding (the passes and their bin order are the same).  No counterpart in the
- * reference.
+ * results to rounding (the passes and their bin order are the same).  It also holds the
+ * per-band plane statistics with which nc_fftconv_epilogue_fwd's row pass hands the tiled
+ * epilogue (hout*wout > 8192) its mean and variance, so that epilogue reads z once instead
+ * of twice.  No counterpart in the reference.
  */
 size_t nc_fftconv_correlate_workspace_size(int B, int M, int hout, int wout, int fft_h,
                                            int fft_w);

@@ -16,6 +16,7 @@
 #include <mutex>
 
 #include "nc_common.h"
+#include "nc_large.h"
 
 namespace {
 
@@ -529,9 +530,9 @@ void tile_stats(hipStream_t st, bool vec, int B, int M, int N, int T, int hb, co
 
 // Chan combine of the T tile statistics of plane (b, m) by one wavefront: each lane takes
 // tiles lane, lane + 64, ... in order, then a butterfly over the lanes (fixed order).  Every
-// lane returns the result.
+// lane returns the result.  Tiles hold tn consecutive pixels, the last one the rest.
 NC_DEV void chan_combine_wave(const float* stats, size_t BMT, int b, int m, int M, int N, int T,
-                              float* mean, float* rstd) {
+                              int tn, float* mean, float* rstd) {
     const int lane = threadIdx.x & (NC_WAVE - 1);
     const float* s1 = stats + ((size_t)b * M + m) * T;
     const float* m2 = s1 + BMT;
@@ -540,7 +541,7 @@ NC_DEV void chan_combine_wave(const float* stats, size_t BMT, int b, int m, int 
     const float mu = wave_sum(tot) / (float)N;
     float var = 0.f;
     for (int t = lane; t < T; t += NC_WAVE) {
-        const int nt = min(kTileN, N - t * kTileN);
+        const int nt = min(tn, N - t * tn);
         const float d = s1[t] / (float)nt - mu;
         var += m2[t] + (float)nt * d * d;
     }
@@ -551,10 +552,11 @@ NC_DEV void chan_combine_wave(const float* stats, size_t BMT, int b, int m, int 
 // Directions whose loads a tiled kernel keeps in flight together.
 constexpr int kTileMC = 4;
 
-// Per-(tile, b): statistics from the Chan partials, then standardise + Codd + sum over M.
+// Per-(tile, b): statistics from the Chan partials (Ts tiles of tn pixels per plane), then
+// standardise + Codd + sum over M.
 template <int ACT, bool VEC>
-__global__ __launch_bounds__(kTileNT) void k_tile_fwd(int B, int M, int N, int T, float slope,
-                                                      int hb,
+__global__ __launch_bounds__(kTileNT) void k_tile_fwd(int B, int M, int N, int Ts, int tn,
+                                                      float slope, int hb,
                                                       const float* __restrict__ z,
                                                       const float* __restrict__ delta,
                                                       const float* __restrict__ w,
@@ -567,11 +569,11 @@ __global__ __launch_bounds__(kTileNT) void k_tile_fwd(int B, int M, int N, int T
     using Px = TilePx<VEC>;
     __shared__ float smu[kMaxM], srs[kMaxM];
     const int t = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-    const size_t BMT = (size_t)B * M * T;
+    const size_t BMT = (size_t)B * M * Ts;
     // one wavefront per direction combines its tile statistics
     for (int m = tid / NC_WAVE; m < M; m += kTileNT / NC_WAVE) {
         float mu, r;
-        chan_combine_wave(stats, BMT, b, m, M, N, T, &mu, &r);
+        chan_combine_wave(stats, BMT, b, m, M, N, Ts, tn, &mu, &r);
         if ((tid & (NC_WAVE - 1)) == 0) {
             smu[m] = mu;
             srs[m] = r;
@@ -915,7 +917,7 @@ __global__ __launch_bounds__(256) void k_port_fwd_tiled(
     const size_t BMT = (size_t)B * M * T;
     for (int m = threadIdx.x / NC_WAVE; m < M; m += blockDim.x / NC_WAVE) {
         float mu, r;
-        chan_combine_wave(stats, BMT, b, m, M, N, T, &mu, &r);
+        chan_combine_wave(stats, BMT, b, m, M, N, T, kTileN, &mu, &r);
         if ((threadIdx.x & (NC_WAVE - 1)) == 0) {
             smu[m] = mu;
             srs[m] = r;
@@ -1268,6 +1270,26 @@ int nc_epilogue_fwd_partials(int B, int M, int h, int w) {
     return h * w <= kSingleMaxPix ? fwd_plan(B, M, h * w).G : 1;
 }
 
+// The tiled forward's second stage from tile statistics (Ts tiles of tn pixels per plane).
+static int tile_fwd(hipStream_t st, bool vec, int act, int B, int M, int N, int Ts, int tn,
+             float neg_slope, int has_border, const float* z, const float* delta,
+             const float* w_eff, const float* s_eff, const float* b_roi, const float* stats,
+             float* out, float* mean, float* rstd) {
+    const int T = tiles_of(N);
+    return dispatch_act(act, [&]<int ACT>() {
+        if (vec)
+            hipLaunchKernelGGL((k_tile_fwd<ACT, true>), dim3(T, B), dim3(kTileNT), 0, st, B, M,
+                               N, Ts, tn, neg_slope, has_border, z, delta, w_eff, s_eff, b_roi,
+                               stats, out, mean, rstd);
+        else
+            hipLaunchKernelGGL((k_tile_fwd<ACT, false>), dim3(T, B), dim3(kTileNT), 0, st, B, M,
+                               N, Ts, tn, neg_slope, has_border, z, delta, w_eff, s_eff, b_roi,
+                               stats, out, mean, rstd);
+        NC_CHECK_LAUNCH();
+        return NC_OK;
+    });
+}
+
 // parts != nullptr: the G direction-group partial outputs go there, uncombined.
 static int epilogue_fwd(void* stream, int B, int M, int h, int w, int act, float neg_slope,
                         int has_border, const float* z, const float* delta, const float* w_eff,
@@ -1302,18 +1324,8 @@ static int epilogue_fwd(void* stream, int B, int M, int h, int w, int act, float
     const bool vec = tile_vec(N, has_border, z, delta, w_eff, s_eff, b_roi);
     tile_stats(st, vec, B, M, N, T, has_border, z, delta, e.stats);
     NC_CHECK_LAUNCH();
-    return dispatch_act(act, [&]<int ACT>() {
-        if (vec)
-            hipLaunchKernelGGL((k_tile_fwd<ACT, true>), dim3(T, B), dim3(kTileNT), 0, st, B, M,
-                               N, T, neg_slope, has_border, z, delta, w_eff, s_eff, b_roi,
-                               e.stats, out, mean, rstd);
-        else
-            hipLaunchKernelGGL((k_tile_fwd<ACT, false>), dim3(T, B), dim3(kTileNT), 0, st, B, M,
-                               N, T, neg_slope, has_border, z, delta, w_eff, s_eff, b_roi,
-                               e.stats, out, mean, rstd);
-        NC_CHECK_LAUNCH();
-        return NC_OK;
-    });
+    return tile_fwd(st, vec, act, B, M, N, T, kTileN, neg_slope, has_border, z, delta, w_eff,
+                    s_eff, b_roi, e.stats, out, mean, rstd);
 }
 
 int nc_epilogue_fwd(void* stream, int B, int M, int h, int w, int act, float neg_slope,
@@ -1742,6 +1754,22 @@ int nc_port_bwd_parts(void* stream, int B, int M, int h, int w, int has_border, 
 }
 
 }  // extern "C"
+
+bool nc_epilogue_tiled(int n_pix) { return n_pix > kSingleMaxPix; }
+
+int nc_epilogue_fwd_from_stats(hipStream_t st, int B, int M, int h, int w, int act,
+                               float neg_slope, const float* z, const float* w_eff,
+                               const float* s_eff, const float* b_roi, const float* stats,
+                               int n_tiles, int tile_pix, float* out, float* mean, float* rstd) {
+    const int N = h * w;
+    if (B <= 0 || M <= 0 || M > kMaxM || !nc_epilogue_tiled(N) || !z || !w_eff || !s_eff ||
+        !b_roi || !stats || !out || !mean || !rstd || act < 0 || act > 5 || tile_pix <= 0 ||
+        n_tiles != (N + tile_pix - 1) / tile_pix)
+        return NC_ERR_INVALID_ARGUMENT;
+    return tile_fwd(st, tile_vec(N, 0, z, nullptr, w_eff, s_eff, b_roi), act, B, M, N, n_tiles,
+                    tile_pix, neg_slope, 0, z, nullptr, w_eff, s_eff, b_roi, stats, out, mean,
+                    rstd);
+}
 
 // The port algebra over G direction-group partial sums part (2, G, B, P), for producers in
 // other translation units (the fused correlation + port of the spectral entry points).

@@ -40,11 +40,26 @@ int nc_seg_dx(hipStream_t st, int B, int nchunk, int hin, int win, int pad_h, in
 
 // z = the correlation's window of irfft2(xhat_b * ghat_m); with a workspace of at least
 // nc_large_correlate_ws bytes, by the two-pass transform (column pass, then row pass, the
-// intermediate in ws), else one workgroup per plane segment.
+// intermediate in ws), else one workgroup per plane segment.  band_stats (two-pass only,
+// else NC_ERR_UNSUPPORTED): the row pass also writes each plane's band statistics, layout
+// (2, B*M, ceil(hout / nc_large_band_rows)) of (sum, centred sum of squares), a band being
+// nc_large_band_rows consecutive output rows; the workspace keeps them at
+// nc_large_band_stats_offset bytes, past the intermediate.
 int nc_large_correlate(hipStream_t st, int B, int M, int hout, int wout, int pad_h, int pad_w,
                        int fft_h, int fft_w, const float* xhat, const float* ghat, float* z,
-                       void* ws = nullptr, size_t ws_bytes = 0);
+                       void* ws = nullptr, size_t ws_bytes = 0, float* band_stats = nullptr);
 size_t nc_large_correlate_ws(int B, int M, int hout, int fft_h, int fft_w);
+int nc_large_band_rows(int fft_h, int fft_w);
+size_t nc_large_band_stats_offset(int B, int M, int hout, int fft_h, int fft_w);
+
+// Implemented in nc_epilogue.hip: whether an (n_pix)-pixel plane takes the tiled epilogue,
+// and its forward from given tile statistics (2, B*M, T) of tiles of tile_pix consecutive
+// pixels (the last one partial), without a border term: out (B, N), mean / rstd (B, M).
+bool nc_epilogue_tiled(int n_pix);
+int nc_epilogue_fwd_from_stats(hipStream_t st, int B, int M, int h, int w, int act,
+                               float neg_slope, const float* z, const float* w_eff,
+                               const float* s_eff, const float* b_roi, const float* stats,
+                               int n_tiles, int tile_pix, float* out, float* mean, float* rstd);
 
 size_t nc_large_fftconv_bwd_ws(int B, int M, int fft_h, int fft_w);
 

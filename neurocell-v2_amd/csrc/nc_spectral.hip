@@ -1891,6 +1891,21 @@ int nc_fftconv_epilogue_fwd(void* stream, int B, int M, int hout, int wout, int 
     // other grids: the correlation into z (two-pass through ws when it is large enough), then
     // the epilogue's partial outputs
     if (!z) return NC_ERR_INVALID_ARGUMENT;
+    if (nc_large_grid(fft_h, fft_w) && nc_epilogue_tiled(hout * wout) && ws &&
+        ws_bytes >= nc_fftconv_correlate_workspace_size(B, M, hout, wout, fft_h, fft_w) &&
+        (size_t)B * M <= 65535) {
+        // the two-pass correlation's row pass also forms the tiled epilogue's statistics, per
+        // band of rows (kept in ws past the intermediate), so z is read once more, not twice
+        const int br = nc_large_band_rows(fft_h, fft_w);
+        float* stats = reinterpret_cast<float*>(
+            static_cast<char*>(ws) + nc_large_band_stats_offset(B, M, hout, fft_h, fft_w));
+        rc = nc_large_correlate(st, B, M, hout, wout, pad_h, pad_w, fft_h, fft_w, xhat, ghat, z,
+                                ws, ws_bytes, stats);
+        if (rc != NC_OK) return rc;
+        return nc_epilogue_fwd_from_stats(st, B, M, hout, wout, act, neg_slope, z, w_eff, s_eff,
+                                          b_roi, stats, (hout + br - 1) / br, br * wout, parts,
+                                          mean, rstd);
+    }
     rc = correlate_ws(stream, B, M, hout, wout, pad_h, pad_w, fft_h, fft_w, xhat, ghat, z, ws,
                       ws_bytes);
     if (rc != NC_OK) return rc;

@@ -231,10 +231,16 @@ __global__ __launch_bounds__(kNT) void k_linv_cols(int n, size_t cstride, int ho
 
 // Inverse row pass: rows (2p, 2p + 1) of T as one complex transform, p in
 // [blockIdx.x * PPW, +PPW); output columns j = (c - col0) mod FW < wout, times scale.
-template <int FH, int FW>
+// STATS: the workgroup also forms its band's statistics, the band being its output rows
+// [2 PPW blockIdx.x, +2 PPW) of the plane: the sum and the centred sum of squares about the
+// band mean, both as fixed-order workgroup sums, at stats[plane * nbands + band] and
+// stats[nplanes * nbands + plane * nbands + band] (the tile-statistics layout (2, B*M, T) of
+// the tiled epilogue, with bands for tiles).
+template <int FH, int FW, bool STATS = false>
 __global__ __launch_bounds__(kNT) void k_linv_rows(int hout, int wout, int col0, float scale,
                                                    const cpx* __restrict__ T,
-                                                   float* __restrict__ z) {
+                                                   float* __restrict__ z,
+                                                   float* __restrict__ stats) {
     using L = LG<FH, FW>;
     constexpr int EW = L::GW::E, GW = L::GW::G, PPW = kNT / GW, NC = L::NC;
     __shared__ cpx tw[NC_TW_N];
@@ -277,6 +283,33 @@ __global__ __launch_bounds__(kNT) void k_linv_rows(int hout, int wout, int col0,
     gfft_stage1<FW, true>(v, t, sc, tw);
     __syncthreads();
     gfft_stage2<FW, true>(v, t, sc);
+    if constexpr (STATS) {
+        __shared__ float red[kNT / 64 + 1];
+        float s1 = 0.f;
+#pragma unroll
+        for (int s = 0; s < EW; ++s) {
+            const int j = (L::GW::bin(t, s) - col0) & (FW - 1);
+            if (on && j < wout) s1 += v[s].x * scale + (hasb ? v[s].y * scale : 0.f);
+        }
+        block_sum<1, kNT>(&s1, red);
+        const int rows = min(2 * PPW, hout - 2 * PPW * (int)blockIdx.x);
+        const float mu = s1 / (float)(rows * wout);
+        float m2 = 0.f;
+#pragma unroll
+        for (int s = 0; s < EW; ++s) {
+            const int j = (L::GW::bin(t, s) - col0) & (FW - 1);
+            if (on && j < wout) {
+                const float da = v[s].x * scale - mu, db = hasb ? v[s].y * scale - mu : 0.f;
+                m2 += da * da + db * db;
+            }
+        }
+        block_sum<1, kNT>(&m2, red);
+        if (threadIdx.x == 0) {
+            const size_t o = (size_t)plane * gridDim.x + blockIdx.x;
+            stats[o] = s1;
+            stats[(size_t)gridDim.y * gridDim.x + o] = m2;
+        }
+    }
     if (!on) return;
     float* za = z + ((size_t)plane * hout + ia) * wout;
 #pragma unroll
@@ -612,7 +645,8 @@ int spec_bwd(hipStream_t st, int M, int kh, int kw, int sh, int sw, const float*
 
 template <int FH, int FW>
 int corr(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw, const float* xhat,
-         const float* ghat, float* z, void* ws = nullptr, size_t ws_bytes = 0);
+         const float* ghat, float* z, void* ws = nullptr, size_t ws_bytes = 0,
+         float* stats = nullptr);
 
 template <int FH, int FW>
 int rfft2_two_pass(hipStream_t st, int nplanes, int hin, int win, size_t pstride, const float* x,
@@ -635,9 +669,15 @@ size_t corr2_ws(int B, int M, int hout) {
     return (size_t)B * M * hout * LG<FH, FW>::NC * sizeof(cpx);
 }
 
+// Output rows per band of the row pass (the rows one workgroup finishes).
+template <int FH, int FW>
+constexpr int band_rows() {
+    return 2 * (kNT / LG<FH, FW>::GW::G);
+}
+
 template <int FH, int FW>
 int corr2(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw, const float* xhat,
-          const float* ghat, float* z, void* ws) {
+          const float* ghat, float* z, void* ws, float* stats) {
     using L = LG<FH, FW>;
     constexpr int CPW = kNT / L::GH::G, PPW = kNT / L::GW::G;
     cpx* T = reinterpret_cast<cpx*>(ws);
@@ -646,8 +686,13 @@ int corr2(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw, cons
                        reinterpret_cast<const cpx*>(ghat), T);
     NC_CHECK_LAUNCH();
     const int npairs = (hout + 1) / 2;
-    hipLaunchKernelGGL((k_linv_rows<FH, FW>), dim3((npairs + PPW - 1) / PPW, B * M), dim3(kNT), 0,
-                       st, hout, wout, pw, 1.0f / (float)(FH * FW), T, z);
+    const dim3 grid((npairs + PPW - 1) / PPW, B * M);
+    if (stats)
+        hipLaunchKernelGGL((k_linv_rows<FH, FW, true>), grid, dim3(kNT), 0, st, hout, wout, pw,
+                           1.0f / (float)(FH * FW), T, z, stats);
+    else
+        hipLaunchKernelGGL((k_linv_rows<FH, FW>), grid, dim3(kNT), 0, st, hout, wout, pw,
+                           1.0f / (float)(FH * FW), T, z, nullptr);
     NC_CHECK_LAUNCH();
     return NC_OK;
 }
@@ -686,16 +731,17 @@ int dx_two_pass(hipStream_t st, int B, int nchunk, int hin, int win, int ph, int
     NC_CHECK_LAUNCH();
     const int npairs = (hin + 1) / 2;
     hipLaunchKernelGGL((k_linv_rows<FH, FW>), dim3((npairs + PPW - 1) / PPW, B), dim3(kNT), 0, st,
-                       hin, win, (FW - pw) & (FW - 1), 1.0f / (float)(FH * FW), T, dx);
+                       hin, win, (FW - pw) & (FW - 1), 1.0f / (float)(FH * FW), T, dx, nullptr);
     NC_CHECK_LAUNCH();
     return NC_OK;
 }
 
 template <int FH, int FW>
 int corr(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw, const float* xhat,
-         const float* ghat, float* z, void* ws, size_t ws_bytes) {
+         const float* ghat, float* z, void* ws, size_t ws_bytes, float* stats) {
     if (ws && ws_bytes >= corr2_ws<FH, FW>(B, M, hout) && (size_t)B * M <= 65535)
-        return corr2<FH, FW>(st, B, M, hout, wout, ph, pw, xhat, ghat, z, ws);
+        return corr2<FH, FW>(st, B, M, hout, wout, ph, pw, xhat, ghat, z, ws, stats);
+    if (stats) return NC_ERR_UNSUPPORTED;  // band statistics come from the two-pass row pass
     const int rs = inv_rows<FH, FW>(hout);
     const size_t lds = linv_lds_bytes<FH, FW, kNT>(rs);
     set_lds(k_linv_conv<FH, FW>, lds);
@@ -889,18 +935,33 @@ int nc_seg_dx(hipStream_t st, int B, int nchunk, int hin, int win, int ph, int p
 
 int nc_large_correlate(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw, int fh,
                        int fw, const float* xhat, const float* ghat, float* z, void* ws,
-                       size_t ws_bytes) {
-#define NC_CALL(A, Bv) corr<A, Bv>(st, B, M, hout, wout, ph, pw, xhat, ghat, z, ws, ws_bytes)
+                       size_t ws_bytes, float* band_stats) {
+#define NC_CALL(A, Bv) \
+    corr<A, Bv>(st, B, M, hout, wout, ph, pw, xhat, ghat, z, ws, ws_bytes, band_stats)
     NC_DISPATCH_LARGE(fh, fw, NC_CALL);
 #undef NC_CALL
     return NC_ERR_UNSUPPORTED;
 }
 
-size_t nc_large_correlate_ws(int B, int M, int hout, int fh, int fw) {
-#define NC_CALL(A, Bv) corr2_ws<A, Bv>(B, M, hout)
+int nc_large_band_rows(int fh, int fw) {
+#define NC_CALL(A, Bv) band_rows<A, Bv>()
     NC_DISPATCH_LARGE(fh, fw, NC_CALL);
 #undef NC_CALL
     return 0;
+}
+
+size_t nc_large_band_stats_offset(int B, int M, int hout, int fh, int fw) {
+#define NC_CALL(A, Bv) (corr2_ws<A, Bv>(B, M, hout) + 255) / 256 * 256
+    NC_DISPATCH_LARGE(fh, fw, NC_CALL);
+#undef NC_CALL
+    return 0;
+}
+
+size_t nc_large_correlate_ws(int B, int M, int hout, int fh, int fw) {
+    const int br = nc_large_band_rows(fh, fw);
+    if (br == 0) return 0;
+    const size_t bands = (size_t)(hout + br - 1) / br;
+    return nc_large_band_stats_offset(B, M, hout, fh, fw) + 2 * (size_t)B * M * bands * 4;
 }
 
 int nc_large_plane_spectrum(hipStream_t st, int nplanes, int hin, int win, int fh, int fw, int sh,

@@ -35,7 +35,8 @@ def test_fftconv(be, FH, FW, hin, win, kh, kw):
     (2, 16, 256, 256, 112, 112, 63, 63),  # config-2 planes (one LDS segment per pass)
     (2, 33, 256, 256, 224, 224, 31, 31),  # config-3 planes: two column / row segments, three
                                           # direction chunks in the backward reduction
-    (3, 5, 64, 256, 30, 150, 13, 63), (3, 5, 256, 128, 150, 40, 63, 13)])
+    (3, 5, 64, 256, 30, 150, 13, 63), (3, 5, 256, 128, 150, 40, 63, 13),
+    (16, 16, 256, 256, 40, 44, 9, 7)])   # 256 direction planes, small windows
 def test_fftconv_large(be, B, M, FH, FW, hin, win, kh, kw):
     _assert_small(case_fftconv(be, B=B, M=M, hin=hin, win=win, kh=kh, kw=kw, FH=FH, FW=FW))
 
