@@ -36,11 +36,15 @@ struct LGeo {
     static constexpr int NGH = NT / GH::G;  // column transforms in flight
     static constexpr int NGW = NT / GW::G;  // row-pair transforms in flight
     // Column groups interleave lane by lane (group g = tid % NGH, so a wavefront holds
-    // min(NGH, 64) groups and 64 / that lanes of each); their exchange slots lie SCR_HS cpx
-    // apart with SCR_HS = 64 / min(NGH, 64) (mod 32), so the wavefront's 8-byte accesses
-    // spread over every bank pair (two passes) instead of a few.
+    // min(NGH, 64) groups and 64 / that lanes of each).  A wavefront's 8-byte LDS accesses
+    // run as two half-wavefront passes over the 32 bank pairs (a cpx at index a sits in pair
+    // a mod 32), so each half's 32 lanes must hit 32 different pairs: the exchange slots lie
+    // SCR_HS cpx apart with SCR_HS = 32 / min(NGH, 32) (mod 32), which spreads the half's
+    // groups and its lanes within a group (consecutive rows t) over every pair, both for the
+    // stage-1 writes (row k1, column t) and the stage-2 reads (row t, column t2).
     static constexpr int GPW = NGH < 64 ? NGH : 64;
-    static constexpr int SCR_HS = GH::SCR + ((64 / GPW - GH::SCR % 32) % 32 + 32) % 32;
+    static constexpr int SCR_HS =
+        GH::SCR + (((GPW >= 32 ? 1 : 32 / GPW) - GH::SCR % 32) % 32 + 32) % 32;
     static constexpr int SCR_H = NGH * SCR_HS;
     static constexpr int SCR_W = NGW * GW::SCR;
     static constexpr int SCR = SCR_H > SCR_W ? SCR_H : SCR_W;  // exchange scratch (cpx)

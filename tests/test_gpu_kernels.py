@@ -127,6 +127,7 @@ def test_epilogue_parts(be, B, M, h, w, FH, FW):
     (2, 3, 224, 224, 31, 31, 256, 256, "tanh", False),  # the same, segmented
     (1, 3, 40, 150, 13, 63, 64, 256, "gelu", True),    # asymmetric grid, two passes
     (2, 4, 112, 112, 63, 63, 256, 256, "leaky_relu", True),  # config 2
+    (32, 16, 112, 112, 63, 63, 256, 256, "tanh", True),  # config 2 at half its batch
 ])
 def test_fftconv_epilogue(be, B, M, h, w, kh, kw, FH, FW, act, two_pass):
     res = case_fftconv_epilogue(be, B=B, M=M, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW, act=act,
