@@ -411,6 +411,28 @@ int nc_fftconv_bwd_parts(void* stream, int B, int M, int hin, int win, int hout,
                          float* gz_hat_sum_parts, int sum_accumulate, void* ws, size_t ws_bytes);
 
 
+/*
+ * One reverse step of a hidden layer as one operation: nc_epilogue_bwd_parts (has_border = 0,
+ * hidden planes h x w) on gy, then nc_fftconv_bwd_parts on the gz it gives (hout = h, wout =
+ * w) - kernels_pallas.py:869-1064 followed by 1794-1821.  On the 128- and 256-point grids
+ * with planes above 8192 pixels the cotangent spectra's first transform pass forms gz from
+ * z, gy, the plane statistics and the epilogue's (c1, c2) sums as it reads them (the same
+ * arithmetic as the epilogue's own last stage), so gz is neither stored nor read back and may
+ * be NULL; elsewhere gz (B, M, h, w) is required and the two entries run in turn.  Results as
+ * the two calls.  ws_epi / ws_fc: the two entries' workspaces (nc_epilogue_workspace_size,
+ * nc_fftconv_bwd_workspace_size), distinct.  No counterpart in the reference.
+ */
+int nc_epilogue_fftconv_bwd_parts(void* stream, int B, int M, int h, int w, int act,
+                                  float neg_slope, const float* z, const float* w_eff,
+                                  const float* s_eff, const float* b_roi, const float* mean,
+                                  const float* rstd, const float* gy, float* gz, float* pg_rows,
+                                  size_t plane_stride, int hin, int win, int pad_h, int pad_w,
+                                  int fft_h, int fft_w, const float* xhat, const float* ghat,
+                                  int need_dx, float* dx, float* dghat_parts, int accumulate,
+                                  int conj_dghat, float* gz_hat_sum_parts, int sum_accumulate,
+                                  void* ws_epi, size_t ws_epi_bytes, void* ws_fc,
+                                  size_t ws_fc_bytes);
+
 /* ---------------- piece 3: hidden-step epilogue and output-port epilogue --------------- */
 
 /*

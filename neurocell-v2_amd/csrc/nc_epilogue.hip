@@ -1757,6 +1757,38 @@ int nc_port_bwd_parts(void* stream, int B, int M, int h, int w, int has_border, 
 
 bool nc_epilogue_tiled(int n_pix) { return n_pix > kSingleMaxPix; }
 
+int nc_epilogue_bwd_stage1(hipStream_t st, int B, int M, int h, int w, int act, float neg_slope,
+                           const float* z, const float* w_eff, const float* s_eff,
+                           const float* b_roi, const float* mean, const float* rstd,
+                           const float* gy, float* pg_rows, size_t plane_stride, void* ws,
+                           size_t ws_bytes, const float** cpart, int* n_tiles) {
+    const int N = h * w;
+    if (B <= 0 || M <= 0 || M > kMaxM || h <= 0 || w <= 0 || !nc_epilogue_tiled(N) || !z ||
+        !w_eff || !s_eff || !b_roi || !mean || !rstd || !gy || !pg_rows || act < 0 || act > 5 ||
+        plane_stride < (size_t)B * N || !cpart || !n_tiles)
+        return NC_ERR_INVALID_ARGUMENT;
+    if (ws_bytes < nc_epilogue_workspace_size(B, M, h, w) || !ws) return NC_ERR_WORKSPACE;
+    const EpiWs e = epi_ws(ws, B, M, N);
+    const int T = tiles_of(N);
+    // the same pixel mapping (and so the same c1 / c2 partials) as nc_epilogue_bwd_parts
+    const bool tv = tile_vec(N, 0, z, nullptr, w_eff, s_eff, b_roi, gy);
+    int rc = dispatch_act(act, [&]<int ACT>() {
+        if (tv)
+            hipLaunchKernelGGL((k_tile_bwd1<ACT, true>), dim3(T, B), dim3(kTileNT), 0, st, B, M,
+                               N, T, neg_slope, 0, z, nullptr, w_eff, s_eff, b_roi, mean, rstd,
+                               gy, e.stats, pg_rows, plane_stride);
+        else
+            hipLaunchKernelGGL((k_tile_bwd1<ACT, false>), dim3(T, B), dim3(kTileNT), 0, st, B,
+                               M, N, T, neg_slope, 0, z, nullptr, w_eff, s_eff, b_roi, mean,
+                               rstd, gy, e.stats, pg_rows, plane_stride);
+        NC_CHECK_LAUNCH();
+        return NC_OK;
+    });
+    *cpart = e.stats;
+    *n_tiles = T;
+    return rc;
+}
+
 int nc_epilogue_fwd_from_stats(hipStream_t st, int B, int M, int h, int w, int act,
                                float neg_slope, const float* z, const float* w_eff,
                                const float* s_eff, const float* b_roi, const float* stats,

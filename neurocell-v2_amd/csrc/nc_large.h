@@ -56,6 +56,30 @@ size_t nc_large_band_stats_offset(int B, int M, int hout, int fft_h, int fft_w);
 // and its forward from given tile statistics (2, B*M, T) of tiles of tile_pix consecutive
 // pixels (the last one partial), without a border term: out (B, N), mean / rstd (B, M).
 bool nc_epilogue_tiled(int n_pix);
+// The tiled epilogue backward's first stage alone (no border term), for a caller that forms
+// gz itself: the gw / gs / gb partial rows into pg_rows (nc_epilogue_bwd_parts' layout) and
+// the per-tile (c1, c2) partials, layout (2, B, M, *n_tiles), at *cpart inside ws.
+int nc_epilogue_bwd_stage1(hipStream_t st, int B, int M, int h, int w, int act, float neg_slope,
+                           const float* z, const float* w_eff, const float* s_eff,
+                           const float* b_roi, const float* mean, const float* rstd,
+                           const float* gy, float* pg_rows, size_t plane_stride, void* ws,
+                           size_t ws_bytes, const float** cpart, int* n_tiles);
+
+// gz of the tiled epilogue backward, formed where it is read (the arithmetic of its second
+// stage): gz = rstd * (gy * (w + s * act'(zhat + b)) - c1 - zhat * c2), zhat = (z - mean) *
+// rstd, (c1, c2) = the plane's tile partials summed over its n_tiles tiles, divided by h*w.
+struct nc_epi_gz {
+    const float *z, *w_eff, *s_eff, *b_roi, *gy, *mean, *rstd, *cpart;
+    int n_tiles, act;
+    float neg_slope;
+};
+// nc_large_fftconv_bwd with its cotangent planes gz given that way (hout x wout planes).
+int nc_large_fftconv_bwd_epi(hipStream_t st, int B, int M, int hin, int win, int hout,
+                             int wout, int pad_h, int pad_w, int fft_h, int fft_w,
+                             const nc_epi_gz& gz, const float* xhat, const float* ghat,
+                             int need_dx, float* dx, float* dghat, int accumulate,
+                             int conj_dghat, float* gz_hat_sum, int sum_accumulate, int parts,
+                             void* ws);
 int nc_epilogue_fwd_from_stats(hipStream_t st, int B, int M, int h, int w, int act,
                                float neg_slope, const float* z, const float* w_eff,
                                const float* s_eff, const float* b_roi, const float* stats,

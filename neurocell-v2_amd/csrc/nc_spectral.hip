@@ -1976,6 +1976,43 @@ int nc_fftconv_bwd_parts(void* stream, int B, int M, int hin, int win, int hout,
                        sum_accumulate, true, ws, ws_bytes);
 }
 
+int nc_epilogue_fftconv_bwd_parts(void* stream, int B, int M, int h, int w, int act,
+                                  float neg_slope, const float* z, const float* w_eff,
+                                  const float* s_eff, const float* b_roi, const float* mean,
+                                  const float* rstd, const float* gy, float* gz, float* pg_rows,
+                                  size_t plane_stride, int hin, int win, int pad_h, int pad_w,
+                                  int fft_h, int fft_w, const float* xhat, const float* ghat,
+                                  int need_dx, float* dx, float* dghat_parts, int accumulate,
+                                  int conj_dghat, float* gz_hat_sum_parts, int sum_accumulate,
+                                  void* ws_epi, size_t ws_epi_bytes, void* ws_fc,
+                                  size_t ws_fc_bytes) {
+    int rc = fftconv_check(B, M, hin, win, h, w, pad_h, pad_w, fft_h, fft_w);
+    if (rc != NC_OK) return rc;
+    if (nc_large_grid(fft_h, fft_w) && nc_epilogue_tiled(h * w) && (size_t)B * M <= 65535) {
+        // the cotangent spectra's row pass forms gz from the epilogue's inputs: gz is neither
+        // stored nor read back
+        if (!xhat || !ghat || !dghat_parts || (need_dx && !dx)) return NC_ERR_INVALID_ARGUMENT;
+        if (ws_fc_bytes < nc_fftconv_bwd_workspace_size(B, M, fft_h, fft_w) || !ws_fc)
+            return NC_ERR_WORKSPACE;
+        hipStream_t st = nc_stream(stream);
+        nc_epi_gz e{z, w_eff, s_eff, b_roi, gy, mean, rstd, nullptr, 0, act, neg_slope};
+        rc = nc_epilogue_bwd_stage1(st, B, M, h, w, act, neg_slope, z, w_eff, s_eff, b_roi, mean,
+                                    rstd, gy, pg_rows, plane_stride, ws_epi, ws_epi_bytes,
+                                    &e.cpart, &e.n_tiles);
+        if (rc != NC_OK) return rc;
+        return nc_large_fftconv_bwd_epi(st, B, M, hin, win, h, w, pad_h, pad_w, fft_h, fft_w, e,
+                                        xhat, ghat, need_dx, dx, dghat_parts, accumulate,
+                                        conj_dghat, gz_hat_sum_parts, sum_accumulate, 1, ws_fc);
+    }
+    rc = nc_epilogue_bwd_parts(stream, B, M, h, w, act, neg_slope, 0, z, nullptr, w_eff, s_eff,
+                               b_roi, mean, rstd, gy, gz, pg_rows, plane_stride, ws_epi,
+                               ws_epi_bytes);
+    if (rc != NC_OK) return rc;
+    return nc_fftconv_bwd_parts(stream, B, M, hin, win, h, w, pad_h, pad_w, fft_h, fft_w, gz,
+                                xhat, ghat, need_dx, dx, dghat_parts, accumulate, conj_dghat,
+                                gz_hat_sum_parts, sum_accumulate, ws_fc, ws_fc_bytes);
+}
+
 int nc_fftconv_bwd(void* stream, int B, int M, int hin, int win, int hout, int wout, int pad_h,
                    int pad_w, int fft_h, int fft_w, const float* gz, const float* xhat,
                    const float* ghat, int need_dx, float* dx, float* dghat, int accumulate,

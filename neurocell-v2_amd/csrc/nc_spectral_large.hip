@@ -381,6 +381,127 @@ __global__ __launch_bounds__(kNT) void k_lrfft_rows(int hin, int win, size_t pst
     }
 }
 
+// The workgroup's band of gz (rows [r0, r0 + nr) of plane g, pixel offset p0 = r0 * win) into
+// LDS, row-major with pitch win: coalesced loads of z, gy and the per-pixel parameters, four
+// consecutive pixels per 16-byte load with VEC.
+template <int ACT, bool VEC, int NT>
+NC_DEV void epi_gz_band(float* S, const nc_epi_gz& e, size_t zo, size_t go, int p0, int n,
+                        float mu, float r, float c1, float c2) {
+    const int tid = threadIdx.x;
+    if constexpr (VEC) {
+        const float4* z4 = reinterpret_cast<const float4*>(e.z + zo + p0);
+        const float4* g4 = reinterpret_cast<const float4*>(e.gy + go + p0);
+        const float4* w4 = reinterpret_cast<const float4*>(e.w_eff + p0);
+        const float4* s4 = reinterpret_cast<const float4*>(e.s_eff + p0);
+        const float4* b4 = reinterpret_cast<const float4*>(e.b_roi + p0);
+#pragma unroll 2
+        for (int i = tid; i < (n >> 2); i += NT) {
+            const float4 zv = z4[i], gv = g4[i], wv = w4[i], sv = s4[i], bv = b4[i];
+            const float zz[4] = {zv.x, zv.y, zv.z, zv.w}, gg[4] = {gv.x, gv.y, gv.z, gv.w};
+            const float ww[4] = {wv.x, wv.y, wv.z, wv.w}, ss[4] = {sv.x, sv.y, sv.z, sv.w};
+            const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
+            float o[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float zn = (zz[k] - mu) * r;
+                float a;
+                const float da = act_fd<ACT>(zn + bb[k], e.neg_slope, &a);
+                const float gn = gg[k] * (ww[k] + ss[k] * da);
+                o[k] = r * (gn - c1 - zn * c2);
+            }
+            reinterpret_cast<float4*>(S)[i] = make_float4(o[0], o[1], o[2], o[3]);
+        }
+    } else {
+        for (int i = tid; i < n; i += NT) {
+            const float zn = (e.z[zo + p0 + i] - mu) * r;
+            float a;
+            const float da = act_fd<ACT>(zn + e.b_roi[p0 + i], e.neg_slope, &a);
+            const float gn = e.gy[go + p0 + i] * (e.w_eff[p0 + i] + e.s_eff[p0 + i] * da);
+            S[i] = r * (gn - c1 - zn * c2);
+        }
+    }
+}
+
+// k_lrfft_rows over the cotangent planes of the tiled epilogue backward, formed as they are
+// read (nc_epi_gz; each workgroup stages its band of rows in LDS first): plane g = b*M + m's
+// value at pixel p is
+//   rstd_g * (gy_b[p] * (w[p] + s[p] * act'(zhat + b_roi[p])) - c1 - zhat * c2),
+//   zhat = (z_g[p] - mean_g) * rstd_g,
+// with (c1, c2) the plane's tile partials summed by the workgroup in the order the
+// epilogue's own second stage sums them, so the values equal the gz it would have stored.
+template <int FH, int FW>
+__global__ __launch_bounds__(kNT) void k_lrfft_rows_epi(int M, int hin, int win, int vec,
+                                                        nc_epi_gz e, cpx* __restrict__ U) {
+    using L = LG<FH, FW>;
+    constexpr int EW = L::GW::E, GW = L::GW::G, PPW = kNT / GW, SP = L::SP;
+    static_assert((size_t)2 * PPW * FW * sizeof(float) <= PPW * L::GW::SCR * sizeof(cpx),
+                  "the band staging fits the exchange scratch");
+    __shared__ cpx tw[NC_TW_N];
+    __shared__ cpx scr[PPW * L::GW::SCR];  // first the band's gz staging, then the exchange
+    __shared__ float red[2 * (kNT / 64) + 2];
+    float* S = reinterpret_cast<float*>(scr);
+    load_twiddles(tw);
+    const int tid = threadIdx.x, g = tid / GW, t = tid % GW, plane = blockIdx.y;
+    const int b = plane / M, N = hin * win;
+    const size_t BMT = (size_t)gridDim.y * e.n_tiles;
+    float c[2] = {0.f, 0.f};
+    for (int u = tid; u < e.n_tiles; u += kNT) {
+        c[0] += e.cpart[(size_t)plane * e.n_tiles + u];
+        c[1] += e.cpart[BMT + (size_t)plane * e.n_tiles + u];
+    }
+    block_sum<2, kNT>(c, red);  // its barriers also order the twiddle copy
+    const float c1 = c[0] / (float)N, c2 = c[1] / (float)N;
+    const float mu = e.mean[plane], r = e.rstd[plane];
+    const int r0 = blockIdx.x * 2 * PPW, nr = min(2 * PPW, hin - r0);
+    const size_t zo = (size_t)plane * N, go = (size_t)b * N;
+#define NC_BAND(A_)                                                                            \
+    (vec ? epi_gz_band<A_, true, kNT>(S, e, zo, go, r0 * win, nr * win, mu, r, c1, c2)        \
+         : epi_gz_band<A_, false, kNT>(S, e, zo, go, r0 * win, nr * win, mu, r, c1, c2))
+    switch (e.act) {  // uniform over the launch
+        case NC_ACT_TANH: NC_BAND(NC_ACT_TANH); break;
+        case NC_ACT_SIGMOID: NC_BAND(NC_ACT_SIGMOID); break;
+        case NC_ACT_RELU: NC_BAND(NC_ACT_RELU); break;
+        case NC_ACT_LEAKY_RELU: NC_BAND(NC_ACT_LEAKY_RELU); break;
+        case NC_ACT_GELU: NC_BAND(NC_ACT_GELU); break;
+        default: NC_BAND(NC_ACT_IDENTITY);
+    }
+#undef NC_BAND
+    __syncthreads();
+    const int p = blockIdx.x * PPW + g, npairs = (hin + 1) >> 1;
+    const bool on = p < npairs;
+    const int ra = 2 * p, rb = 2 * p + 1;
+    const bool hasb = on && rb < hin;
+    const float* sa = S + (on ? ra - r0 : 0) * win;
+    const float* sb = S + (hasb ? rb - r0 : 0) * win;
+    cpx v[EW];
+#pragma unroll
+    for (int n1 = 0; n1 < EW; ++n1) {
+        const int col = t + GW * n1;
+        const bool in = on && col < win;
+        v[n1] = cmk(in ? sa[col] : 0.f, in && hasb ? sb[col] : 0.f);
+    }
+    __syncthreads();  // the staging is rewritten by the exchange
+    cpx* sc = scr + g * L::GW::SCR;
+    gfft_stage1<FW, false>(v, t, sc, tw);
+    __syncthreads();
+    gfft_stage2<FW, false>(v, t, sc);
+    __syncthreads();  // the stage-2 reads of the scratch are done: it holds Z for the split
+#pragma unroll
+    for (int s = 0; s < EW; ++s) sc[L::GW::bin(t, s)] = v[s];
+    __syncthreads();
+    if (!on) return;
+    cpx* ua = U + (size_t)plane * L::F + (size_t)ra * SP;
+#pragma unroll
+    for (int s = 0; s < EW; ++s) {
+        const int k = L::GW::bin(t, s);
+        if (k <= FW / 2) {
+            const cpx zk = v[s], zm = sc[(FW - k) & (FW - 1)];
+            ua[k] = cmk(0.5f * (zk.x + zm.x), 0.5f * (zk.y - zm.y));
+            if (hasb) ua[SP + k] = cmk(0.5f * (zk.y + zm.y), 0.5f * (zm.x - zk.x));
+        }
+    }
+}
+
 // Forward column pass, in place: columns [blockIdx.x * CPW, +CPW) (< SP) of plane g's
 // row-transformed rows r < hin (rows >= hin are zero), transformed over r into every bin kh,
 // plus add[kh * SP + kw] when add is given (one spectrum for every plane).  A column belongs
@@ -762,17 +883,34 @@ template <int FH, int FW>
 int seg_dx(hipStream_t st, int B, int nchunk, int hin, int win, int ph, int pw, const cpx* dxs,
            float* dx);
 
+// epi: the cotangent planes are formed from the epilogue's inputs as the row pass reads them
+// (gz unused), else read from gz.
 template <int FH, int FW>
 int conv_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout, int ph, int pw,
              const float* gz, const float* xhat, const float* ghat, int need_dx, float* dx,
              float* dghat, int accumulate, int conj_out, float* ssum, int sum_acc, int splits,
-             void* ws) {
+             void* ws, const nc_epi_gz* epi = nullptr) {
     using L = LG<FH, FW>;
     const int nchunk = (M + kRedMC - 1) / kRedMC;
     cpx* sp = reinterpret_cast<cpx*>(ws);
     cpx* part = sp + (size_t)B * M * L::F;
-    int rc = rfft2_two_pass<FH, FW>(st, B * M, hout, wout, (size_t)hout * wout, gz, sp);
-    if (rc != NC_OK) return rc;
+    if (epi) {
+        if ((size_t)B * M > 65535) return NC_ERR_UNSUPPORTED;
+        constexpr int CPW = kNT / L::GH::G, PPW = kNT / L::GW::G;
+        const int npairs = (hout + 1) / 2;
+        auto al = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+        const int vec = wout % 4 == 0 && al(epi->z) && al(epi->gy) && al(epi->w_eff) &&
+                        al(epi->s_eff) && al(epi->b_roi);
+        hipLaunchKernelGGL((k_lrfft_rows_epi<FH, FW>), dim3((npairs + PPW - 1) / PPW, B * M),
+                           dim3(kNT), 0, st, M, hout, wout, vec, *epi, sp);
+        NC_CHECK_LAUNCH();
+        hipLaunchKernelGGL((k_lrfft_cols<FH, FW>), dim3((L::SP + CPW - 1) / CPW, B * M),
+                           dim3(kNT), 0, st, hout, (const cpx*)nullptr, sp);
+        NC_CHECK_LAUNCH();
+    } else {
+        int rc = rfft2_two_pass<FH, FW>(st, B * M, hout, wout, (size_t)hout * wout, gz, sp);
+        if (rc != NC_OK) return rc;
+    }
     hipLaunchKernelGGL((k_lred<kRedMC>), dim3((L::F + 255) / 256, nchunk, splits), dim3(256), 0,
                        st, B, M, L::F, need_dx, sp, reinterpret_cast<const cpx*>(xhat),
                        reinterpret_cast<const cpx*>(ghat), part, reinterpret_cast<cpx*>(dghat),
@@ -1000,6 +1138,20 @@ int nc_large_fftconv_bwd(hipStream_t st, int B, int M, int hin, int win, int hou
 #define NC_CALL(A, Bv)                                                                     \
     conv_bwd<A, Bv>(st, B, M, hin, win, hout, wout, ph, pw, gz, xhat, ghat, need_dx, dx, dghat, \
                     accumulate, conj_dghat, gz_hat_sum, sum_accumulate, splits, ws)
+    NC_DISPATCH_LARGE(fh, fw, NC_CALL);
+#undef NC_CALL
+    return NC_ERR_UNSUPPORTED;
+}
+
+int nc_large_fftconv_bwd_epi(hipStream_t st, int B, int M, int hin, int win, int hout,
+                             int wout, int ph, int pw, int fh, int fw, const nc_epi_gz& gz,
+                             const float* xhat, const float* ghat, int need_dx, float* dx,
+                             float* dghat, int accumulate, int conj_dghat, float* gz_hat_sum,
+                             int sum_accumulate, int parts, void* ws) {
+    const int splits = parts ? nc_large_red_splits(B, M, fh, fw) : 1;
+#define NC_CALL(A, Bv)                                                                        \
+    conv_bwd<A, Bv>(st, B, M, hin, win, hout, wout, ph, pw, nullptr, xhat, ghat, need_dx, dx,  \
+                    dghat, accumulate, conj_dghat, gz_hat_sum, sum_accumulate, splits, ws, &gz)
     NC_DISPATCH_LARGE(fh, fw, NC_CALL);
 #undef NC_CALL
     return NC_ERR_UNSUPPORTED;

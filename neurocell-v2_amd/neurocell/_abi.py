@@ -124,6 +124,9 @@ _SIGS = {
                                   SZ]),
     "nc_port_bwd_parts": (I, [P, I, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, P, P, SZ, P,
                               SZ]),
+    "nc_epilogue_fftconv_bwd_parts": (I, [P, I, I, I, I, I, F, P, P, P, P, P, P, P, P, P, SZ, I,
+                                          I, I, I, I, I, P, P, I, P, P, I, I, P, I, P, SZ, P,
+                                          SZ]),
     "nc_rows_sum": (I, [P, I, C.POINTER(RowsJob)]),
     "nc_port_fwd": (I, [P, I, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, P, SZ]),
     "nc_port_bwd": (I, [P, I, I, I, I, I, I, F, I, P, P, P, P, P, P, P, P, P, P, P, P, I, P,

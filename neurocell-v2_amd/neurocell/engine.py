@@ -796,10 +796,13 @@ class StepPlan:
                  ptr(self.gz), ptr(self.pp_rows), B * self.P, ws_ep, n_ep)
         pg_plane = self.pg_rows[0].numel()
         valid_acc = 0
+        gy_epi = None  # the cotangent of step t's output, whose epilogue reverse is pending
         for t in range(d - 1, -1, -1):
             gy = self.gy[t % 2]
             need_dx = int(t > 0)
             if t == 0 and self.t0_grid:  # VALID full-grid step: its own spectral shift
+                if gy_epi is not None:
+                    self._epilogue_bwd_parts(s, 0, gy_epi, RN, pg_plane, ws_ep, n_ep)
                 r0, _, c0, _ = self.bbox
                 call("nc_fftconv_bwd_parts", s, B, M, self.H, self.W, h, w, self.kh - 1 + r0,
                      self.kw - 1 + c0, fh, fw, ptr(self.gz), ptr(self.xhat[0]), ptr(self.ghat),
@@ -809,17 +812,21 @@ class StepPlan:
                 # steps t >= 1 carried the border term: their cotangent's batch sum, summed
                 # over those steps in the frequency domain, is the border conv's cotangent
                 hbt = t > 0 and self.border
-                call("nc_fftconv_bwd_parts", s, B, M, h, w, h, w, self.cp[0], self.cp[1], fh, fw,
-                     ptr(self.gz), ptr(self.xhat[t]), ptr(self.ghat), need_dx,
-                     ptr(gy) if need_dx else None, ptr(self.rows["dg"]), int(t < d - 1), 0,
-                     ptr(self.rows["gd"]) if hbt else None, int(t < d - 1), ws_fc, n_fc)
+                tail = (ptr(self.xhat[t]), ptr(self.ghat), need_dx, ptr(gy) if need_dx else None,
+                        ptr(self.rows["dg"]), int(t < d - 1), 0,
+                        ptr(self.rows["gd"]) if hbt else None, int(t < d - 1))
+                if gy_epi is None:  # the output step: gz came from the port's reverse
+                    call("nc_fftconv_bwd_parts", s, B, M, h, w, h, w, self.cp[0], self.cp[1],
+                         fh, fw, ptr(self.gz), *tail, ws_fc, n_fc)
+                else:  # step t's epilogue reverse and its correlation reverse in one call
+                    call("nc_epilogue_fftconv_bwd_parts", s, B, M, h, w, self.act, self.slope,
+                         ptr(self.zs[t]), ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
+                         ptr(self.mean[t]), ptr(self.rstd[t]), ptr(gy_epi), ptr(self.gz),
+                         _addr(self.pg_rows) + 4 * t * RN, pg_plane, h, w, self.cp[0],
+                         self.cp[1], fh, fw, *tail, ws_ep, n_ep, ws_fc, n_fc)
             if t == 0:
                 break
-            te = t - 1  # its own R rows of the gw / gs / gb stacks
-            call("nc_epilogue_bwd_parts", s, B, M, h, w, self.act, self.slope, 0,
-                 ptr(self.zs[te]), None, ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
-                 ptr(self.mean[te]), ptr(self.rstd[te]), ptr(gy), ptr(self.gz),
-                 _addr(self.pg_rows) + 4 * te * RN, pg_plane, ws_ep, n_ep)
+            gy_epi = gy  # step t - 1's epilogue reverse runs with the next correlation reverse
         only_t0_grid = self.t0_grid and d == 1
         # every row stack written above, summed in one launch
         jobs = []
@@ -869,6 +876,15 @@ class StepPlan:
              ptr(self.g_cell_s if sharp else g_cell))
         if sharp:
             self._sharpen_bwd(s, g_cell)
+
+    def _epilogue_bwd_parts(self, s, te, gy, RN, pg_plane, ws_ep, n_ep):
+        """Step te's hidden epilogue reverse into gz and its own R rows of the gw / gs / gb
+        stacks."""
+        B, M, h, w = self.B, self.M, self.h, self.w
+        call("nc_epilogue_bwd_parts", s, B, M, h, w, self.act, self.slope, 0,
+             ptr(self.zs[te]), None, ptr(self.w_eff), ptr(self.s_eff), ptr(self.b_roi),
+             ptr(self.mean[te]), ptr(self.rstd[te]), ptr(gy), ptr(self.gz),
+             _addr(self.pg_rows) + 4 * te * RN, pg_plane, ws_ep, n_ep)
 
     # ------------------------------------------------------------------ loss
     def mse(self, target: torch.Tensor, loss: torch.Tensor | None = None) -> torch.Tensor:

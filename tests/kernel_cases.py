@@ -312,6 +312,75 @@ def case_plane_spectra(be, B=3, M=4, h=12, w=10, kh=7, kw=5, FH=32, FW=16, seed=
             "z": rel_l2(be.get(z), O.conv2d_direct(x, g[:, 0], (ph, pw)))}
 
 
+def case_epilogue_fftconv_bwd(be, B=2, M=3, h=112, w=112, kh=31, kw=21, FH=256, FW=256,
+                              act="tanh", seed=12):
+    """One hidden layer's reverse step through nc_epilogue_fftconv_bwd_parts against its two
+    entries run in turn (nc_epilogue_bwd_parts writing gz, nc_fftconv_bwd_parts reading it):
+    max |difference| / max |value| of dx, the dghat and gz_hat_sum rows and the gw/gs/gb rows
+    (0 where gz's values are formed by the same arithmetic), plus the fused path's dx against
+    the oracle's correlation backward of the oracle epilogue's gz."""
+    rng = np.random.default_rng(seed)
+    L, s = be.lib, be.stream()
+    ph, pw = (kh - 1) // 2, (kw - 1) // 2
+    N = h * w
+    x = rng.normal(size=(B, h, w)).astype(np.float32)
+    g = rng.normal(size=(M, 1, kh, kw)).astype(np.float32)
+    xd, gd = be.put(x), be.put(g)
+    ghat = be.zeros((M, FH, FW // 2 + 1, 2))
+    _ok(be, L.nc_filter_spectrum_fwd(s, M, kh, kw, FH, FW, be.ptr(gd), be.ptr(ghat)), "spec")
+    zd, xhat = be.zeros((B, M, h, w)), be.zeros((B, FH, FW // 2 + 1, 2))
+    _ok(be, L.nc_fftconv_fwd(s, B, M, h, w, h, w, ph, pw, FH, FW, be.ptr(xd), be.ptr(ghat),
+                             be.ptr(zd), be.ptr(xhat)), "fwd")
+    wv = rng.normal(size=(h, w)).astype(np.float32)
+    sv = rng.uniform(size=(h, w)).astype(np.float32)
+    bv = rng.normal(size=(h, w)).astype(np.float32)
+    gy = rng.normal(size=(B, h, w)).astype(np.float32)
+    wd, sd, bd, gyd = (be.put(a) for a in (wv, sv, bv, gy))
+    aid = _abi.ACT_IDS[act]
+    n_epi = L.nc_epilogue_workspace_size(B, M, h, w)
+    ws_e = be.zeros((n_epi // 4 + 1,))
+    out, mean, rstd = be.zeros((B, h, w)), be.zeros((B, M)), be.zeros((B, M))
+    _ok(be, L.nc_epilogue_fwd(s, B, M, h, w, aid, 0.01, 0, be.ptr(zd), None, be.ptr(wd),
+                              be.ptr(sd), be.ptr(bd), be.ptr(out), be.ptr(mean), be.ptr(rstd),
+                              be.ptr(ws_e), n_epi), "epi")
+    n_fc = L.nc_fftconv_bwd_workspace_size(B, M, FH, FW)
+    ws_f = be.zeros((n_fc // 4 + 1,))
+    R, npart = L.nc_epilogue_bwd_partials(B, M, h, w), L.nc_fftconv_bwd_partials(B, M, FH, FW)
+    spec = (npart, M, FH, FW // 2 + 1, 2)
+    res = {}
+    outs = []
+    for fused in (False, True):
+        pg, dx = be.zeros((3, R * N)), be.zeros((B, h, w))
+        dg, ss = be.zeros(spec), be.zeros(spec)
+        gz = be.zeros((B, M, h, w))
+        if fused:
+            _ok(be, L.nc_epilogue_fftconv_bwd_parts(
+                s, B, M, h, w, aid, 0.01, be.ptr(zd), be.ptr(wd), be.ptr(sd), be.ptr(bd),
+                be.ptr(mean), be.ptr(rstd), be.ptr(gyd), be.ptr(gz), be.ptr(pg), R * N, h, w,
+                ph, pw, FH, FW, be.ptr(xhat), be.ptr(ghat), 1, be.ptr(dx), be.ptr(dg), 0, 0,
+                be.ptr(ss), 0, be.ptr(ws_e), n_epi, be.ptr(ws_f), n_fc), "fused")
+        else:
+            _ok(be, L.nc_epilogue_bwd_parts(s, B, M, h, w, aid, 0.01, 0, be.ptr(zd), None,
+                                            be.ptr(wd), be.ptr(sd), be.ptr(bd), be.ptr(mean),
+                                            be.ptr(rstd), be.ptr(gyd), be.ptr(gz), be.ptr(pg),
+                                            R * N, be.ptr(ws_e), n_epi), "epib_parts")
+            _ok(be, L.nc_fftconv_bwd_parts(s, B, M, h, w, h, w, ph, pw, FH, FW, be.ptr(gz),
+                                           be.ptr(xhat), be.ptr(ghat), 1, be.ptr(dx),
+                                           be.ptr(dg), 0, 0, be.ptr(ss), 0, be.ptr(ws_f), n_fc),
+                "bwd_parts")
+            gz_sep = be.get(gz)
+        outs.append([be.get(a) for a in (dx, dg, ss, pg)])
+    for name, a, b in zip(("dx", "dghat_rows", "gz_hat_sum_rows", "pg_rows"), *outs):
+        res[name] = float(np.abs(b - a).max() / max(np.abs(a).max(), 1e-30))
+    # the oracle's gz (its epilogue backward on the same z) through the oracle correlation
+    gz_r = O.epilogue_bwd(be.get(zd), np.zeros((M, h, w), np.float32), wv, sv, bv,
+                          be.get(mean), be.get(rstd), gy, act, False)[0]
+    dxr, _ = O.conv2d_bwd_direct(gz_r, x, g[:, 0], (ph, pw))
+    res["dx_vs_oracle"] = rel_l2(outs[1][0], dxr)
+    res["gz_vs_oracle"] = rel_l2(gz_sep, gz_r)
+    return res
+
+
 def case_epilogue(be, B=3, M=5, h=10, w=12, act="tanh", has_border=1, seed=2):
     """Hidden-step epilogue forward/backward (single-pass N <= 8192, tiled above)."""
     rng = np.random.default_rng(seed)

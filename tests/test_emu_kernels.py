@@ -9,7 +9,7 @@ from kernel_cases import (CODD_CASES, TOL, HostBackend, case_adaptive, case_bord
                           case_border_fold, case_codd, case_epilogue, case_epilogue_parts,
                           case_fftconv_circular, case_fftconv_port, case_fftconv_epilogue,
                           case_fftconv, case_helpers, case_plane_spectra, case_port,
-                          case_spectral_ops, case_direct_conv,
+                          case_spectral_ops, case_direct_conv, case_epilogue_fftconv_bwd,
                           case_universe)
 
 
@@ -175,3 +175,13 @@ def test_spectral_ops(be, FH, FW, roi, pad, shift):
     (600, 2, 6, 6, 3, 3, "CIRCULAR", 1)])    # many samples: the smaller register tiles
 def test_direct_conv(be, B, M, H, W, kh, kw, mode, n_parts):
     _assert_small(case_direct_conv(be, B, M, H, W, kh, kw, mode, n_parts))
+
+
+@pytest.mark.parametrize("B,M,h,w,kh,kw,FH,FW,act", [
+    (1, 2, 112, 112, 31, 21, 256, 256, "tanh"),   # fused: gz formed in the row pass
+    (2, 3, 20, 24, 7, 5, 64, 64, "gelu")])        # small grid: the two entries in turn
+def test_epilogue_fftconv_bwd(be, B, M, h, w, kh, kw, FH, FW, act):
+    res = case_epilogue_fftconv_bwd(be, B=B, M=M, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW, act=act)
+    _assert_small({k: res[k] for k in ("dx", "dghat_rows", "gz_hat_sum_rows", "pg_rows")},
+                  tol=1e-6)
+    _assert_small({k: res[k] for k in ("dx_vs_oracle", "gz_vs_oracle")})

@@ -6,7 +6,7 @@ from kernel_cases import (CODD_CASES, EPILOGUE_SHAPES, PORT_SHAPES, TOL, DeviceB
                           case_epilogue, case_epilogue_parts,
                           case_fftconv_circular, case_fftconv_port, case_fftconv_epilogue,
                           case_fftconv, case_helpers, case_plane_spectra, case_port,
-                          case_spectral_ops, case_direct_conv,
+                          case_spectral_ops, case_direct_conv, case_epilogue_fftconv_bwd,
                           case_universe)
 
 pytestmark = pytest.mark.gpu
@@ -191,3 +191,17 @@ def test_spectral_ops(be, FH, FW, roi, pad, shift):
     (600, 2, 6, 6, 3, 3, "CIRCULAR", 1)])    # many samples: the smaller register tiles
 def test_direct_conv(be, B, M, H, W, kh, kw, mode, n_parts):
     _assert_small(case_direct_conv(be, B, M, H, W, kh, kw, mode, n_parts))
+
+
+@pytest.mark.parametrize("B,M,h,w,kh,kw,FH,FW,act", [
+    (2, 3, 112, 112, 63, 63, 256, 256, "tanh"),       # fused: gz formed in the row pass
+    (2, 5, 224, 224, 31, 31, 256, 256, "leaky_relu"),  # config-3 planes, fused
+    (16, 16, 112, 112, 63, 63, 256, 256, "tanh"),     # 256 planes, several tiles per plane
+    (3, 4, 40, 50, 23, 13, 64, 64, "gelu")])          # small grid: the two entries in turn
+def test_epilogue_fftconv_bwd(be, B, M, h, w, kh, kw, FH, FW, act):
+    res = case_epilogue_fftconv_bwd(be, B=B, M=M, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW, act=act)
+    # the fused step forms gz with the epilogue's own arithmetic: equal up to how the compiler
+    # contracts the two kernels' expressions
+    _assert_small({k: res[k] for k in ("dx", "dghat_rows", "gz_hat_sum_rows", "pg_rows")},
+                  tol=1e-6)
+    _assert_small({k: res[k] for k in ("dx_vs_oracle", "gz_vs_oracle")})
