@@ -33,6 +33,14 @@ constexpr int kRedMC = 16;           // directions per reduction workgroup
 template <int FH, int FW>
 using LG = LGeo<FH, FW, kNT>;
 
+// Row pitch (cpx) of the reverse pass's cotangent half-spectra in the workspace: SP rounded up
+// to 16 cpx, so every row starts on a 128-byte line and the column passes' 16- or 32-column
+// tiles move whole lines (SP = FW/2 + 1 leaves every row but one in 16 straddling lines).
+template <int FH, int FW>
+constexpr int spec_pitch_ws() {
+    return (LG<FH, FW>::SP + 15) / 16 * 16;
+}
+
 // LDS carve-up of the transform kernels, in the order lfwd_lds_bytes / linv_lds_bytes count
 // it: twiddles | exchange scratch | (forward only) packed-column staging C0 | Y or T.
 struct LdsParts {
@@ -325,14 +333,14 @@ __global__ __launch_bounds__(kNT) void k_linv_rows(int hout, int wout, int col0,
 // Forward row pass of real planes (plane g at x + g * pstride, hin x win at the grid origin,
 // each value the sum of nq partial planes qstride floats apart, in increasing order): rows
 // (2p, 2p + 1) as one complex transform, split into the two rows' half-spectra, written as
-// rows 2p, 2p + 1 of the plane's (FH, SP) half-spectrum region of U.  Rows >= hin are not
-// written (the column pass reads them as zeros).
-template <int FH, int FW>
+// rows 2p, 2p + 1 of the plane's (FH, PITCH) half-spectrum region of U (bins kw <= FW/2 of a
+// row; PITCH >= SP).  Rows >= hin are not written (the column pass reads them as zeros).
+template <int FH, int FW, int PITCH = LG<FH, FW>::SP>
 __global__ __launch_bounds__(kNT) void k_lrfft_rows(int hin, int win, size_t pstride, int nq,
                                                     size_t qstride, const float* __restrict__ x,
                                                     cpx* __restrict__ U) {
     using L = LG<FH, FW>;
-    constexpr int EW = L::GW::E, GW = L::GW::G, PPW = kNT / GW, SP = L::SP;
+    constexpr int EW = L::GW::E, GW = L::GW::G, PPW = kNT / GW, SP = PITCH;
     __shared__ cpx tw[NC_TW_N];
     __shared__ cpx scr[PPW * L::GW::SCR];
     load_twiddles(tw);
@@ -368,7 +376,7 @@ __global__ __launch_bounds__(kNT) void k_lrfft_rows(int hin, int win, size_t pst
     for (int s = 0; s < EW; ++s) sc[L::GW::bin(t, s)] = v[s];
     __syncthreads();
     if (!on) return;
-    cpx* ua = U + (size_t)plane * L::F + (size_t)ra * SP;
+    cpx* ua = U + (size_t)plane * FH * SP + (size_t)ra * SP;
 #pragma unroll
     for (int s = 0; s < EW; ++s) {
         const int k = L::GW::bin(t, s);
@@ -429,11 +437,11 @@ NC_DEV void epi_gz_band(float* S, const nc_epi_gz& e, size_t zo, size_t go, int 
 //   zhat = (z_g[p] - mean_g) * rstd_g,
 // with (c1, c2) the plane's tile partials summed by the workgroup in the order the
 // epilogue's own second stage sums them, so the values equal the gz it would have stored.
-template <int FH, int FW>
+template <int FH, int FW, int PITCH>
 __global__ __launch_bounds__(kNT) void k_lrfft_rows_epi(int M, int hin, int win, int vec,
                                                         nc_epi_gz e, cpx* __restrict__ U) {
     using L = LG<FH, FW>;
-    constexpr int EW = L::GW::E, GW = L::GW::G, PPW = kNT / GW, SP = L::SP;
+    constexpr int EW = L::GW::E, GW = L::GW::G, PPW = kNT / GW, SP = PITCH;
     static_assert((size_t)2 * PPW * FW * sizeof(float) <= PPW * L::GW::SCR * sizeof(cpx),
                   "the band staging fits the exchange scratch");
     __shared__ cpx tw[NC_TW_N];
@@ -490,7 +498,7 @@ __global__ __launch_bounds__(kNT) void k_lrfft_rows_epi(int M, int hin, int win,
     for (int s = 0; s < EW; ++s) sc[L::GW::bin(t, s)] = v[s];
     __syncthreads();
     if (!on) return;
-    cpx* ua = U + (size_t)plane * L::F + (size_t)ra * SP;
+    cpx* ua = U + (size_t)plane * FH * SP + (size_t)ra * SP;
 #pragma unroll
     for (int s = 0; s < EW; ++s) {
         const int k = L::GW::bin(t, s);
@@ -506,8 +514,8 @@ __global__ __launch_bounds__(kNT) void k_lrfft_rows_epi(int M, int hin, int win,
 // row-transformed rows r < hin (rows >= hin are zero), transformed over r into every bin kh,
 // plus add[kh * SP + kw] when add is given (one spectrum for every plane).  A column belongs
 // to one thread group of one workgroup, and the workgroup's barrier orders all its reads
-// before its writes.
-template <int FH, int FW>
+// before its writes.  Planes are FH rows of PITCH cpx apart.
+template <int FH, int FW, int PITCH = LG<FH, FW>::SP>
 __global__ __launch_bounds__(kNT) void k_lrfft_cols(int hin, const cpx* __restrict__ add,
                                                     cpx* __restrict__ U) {
     using L = LG<FH, FW>;
@@ -519,12 +527,12 @@ __global__ __launch_bounds__(kNT) void k_lrfft_cols(int hin, const cpx* __restri
     const int tid = threadIdx.x, g = tid % CPW, t = tid / CPW;
     const int kw = blockIdx.x * CPW + g;
     const bool on = kw < SP;
-    cpx* col = U + (size_t)blockIdx.y * L::F + (on ? kw : 0);
+    cpx* col = U + (size_t)blockIdx.y * FH * PITCH + (on ? kw : 0);
     cpx v[EH];
 #pragma unroll
     for (int n1 = 0; n1 < EH; ++n1) {
         const int r = t + GH * n1;
-        v[n1] = on && r < hin ? col[(size_t)r * SP] : cmk(0.f, 0.f);
+        v[n1] = on && r < hin ? col[(size_t)r * PITCH] : cmk(0.f, 0.f);
     }
     cpx* sc = scr + g * L::SCR_HS;
     gfft_stage1<FH, false>(v, t, sc, tw);
@@ -534,26 +542,32 @@ __global__ __launch_bounds__(kNT) void k_lrfft_cols(int hin, const cpx* __restri
 #pragma unroll
     for (int s = 0; s < EH; ++s) {
         const int kh = L::GH::bin(t, s);
-        col[(size_t)kh * SP] = add ? cadd(v[s], add[kh * SP + kw]) : v[s];
+        col[(size_t)kh * PITCH] = add ? cadd(v[s], add[kh * SP + kw]) : v[s];
     }
 }
 
-// Both reductions of the backward in one pass over the cotangent spectra sp (B, M, F):
+// Both reductions of the backward in one pass over the cotangent spectra sp (B, M, FH rows of
+// sp_pitch cpx, the first spw of each row the bins kw = 0 .. FW/2):
 //   dxpart[c][b] = sum over the chunk's directions m of sp_bm * conj(ghat_m)   (need_dx)
 //   dghat[m]     = (+=) sum over b of sp_bm * conj(xhat_b)  (conjugated when conj_out)
 //   ssum[m]      = (+=, sum_acc) sum over b of sp_bm, the spectrum of sum_b gz_bm  (with ssum)
 // Thread = one bin; directions m0 .. m0+MC-1 of chunk c = blockIdx.y; b in increasing order
 // over sample slice blockIdx.z, whose sums go to row blockIdx.z of dghat / ssum (M*F each).
 template <int MC>
-__global__ __launch_bounds__(256) void k_lred(int B, int M, int F, int need_dx,
-                                              const cpx* __restrict__ sp,
+__global__ __launch_bounds__(256) void k_lred(int B, int M, int F, int spw, int sp_pitch,
+                                              int need_dx, const cpx* __restrict__ sp,
                                               const cpx* __restrict__ xhat,
                                               const cpx* __restrict__ ghat,
                                               cpx* __restrict__ dxpart, cpx* __restrict__ dghat,
                                               int accumulate, int conj_out,
                                               cpx* __restrict__ ssum, int sum_acc) {
-    const int e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= F) return;
+    // threads walk sp's rows (pitch sp_pitch, so a wavefront's loads are whole aligned lines);
+    // the pitch's padding columns have no bin
+    const int es = blockIdx.x * blockDim.x + threadIdx.x;
+    const int kh = es / sp_pitch, kw = es - kh * sp_pitch;
+    if (kw >= spw || kh >= F / spw) return;
+    const int e = kh * spw + kw;                     // the bin in the other arrays
+    const size_t FP = (size_t)(F / spw) * sp_pitch;  // sp's plane stride
     const int m0 = blockIdx.y * MC;
     const int nm = min(MC, M - m0);
     // sample slice z = blockIdx.z: b in [b0, b1), its sums into row z of dghat / ssum
@@ -569,10 +583,10 @@ __global__ __launch_bounds__(256) void k_lred(int B, int M, int F, int need_dx,
     }
     for (int b = b0; b < b1; ++b) {
         const cpx X = xhat[(size_t)b * F + e];
-        const cpx* s = sp + ((size_t)b * M + m0) * F + e;
+        const cpx* s = sp + ((size_t)b * M + m0) * FP + es;
         cpx v[MC];
 #pragma unroll
-        for (int q = 0; q < MC; ++q) v[q] = s[(size_t)min(q, nm - 1) * F];
+        for (int q = 0; q < MC; ++q) v[q] = s[(size_t)min(q, nm - 1) * FP];
         cpx d = cmk(0.f, 0.f);
 #pragma unroll
         for (int q = 0; q < MC; ++q) {
@@ -876,7 +890,8 @@ int corr(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw, const
 template <int FH, int FW>
 size_t bwd_ws(int B, int M) {
     const int nchunk = (M + kRedMC - 1) / kRedMC;
-    return ((size_t)B * M + (size_t)nchunk * B) * LG<FH, FW>::F * sizeof(cpx);
+    return ((size_t)B * M * FH * spec_pitch_ws<FH, FW>() + (size_t)nchunk * B * LG<FH, FW>::F) *
+           sizeof(cpx);
 }
 
 template <int FH, int FW>
@@ -891,28 +906,39 @@ int conv_bwd(hipStream_t st, int B, int M, int hin, int win, int hout, int wout,
              float* dghat, int accumulate, int conj_out, float* ssum, int sum_acc, int splits,
              void* ws, const nc_epi_gz* epi = nullptr) {
     using L = LG<FH, FW>;
+    constexpr int SPP = spec_pitch_ws<FH, FW>();
     const int nchunk = (M + kRedMC - 1) / kRedMC;
     cpx* sp = reinterpret_cast<cpx*>(ws);
-    cpx* part = sp + (size_t)B * M * L::F;
-    if (epi) {
-        if ((size_t)B * M > 65535) return NC_ERR_UNSUPPORTED;
-        constexpr int CPW = kNT / L::GH::G, PPW = kNT / L::GW::G;
-        const int npairs = (hout + 1) / 2;
+    cpx* part = sp + (size_t)B * M * FH * SPP;
+    constexpr int CPW = kNT / L::GH::G, PPW = kNT / L::GW::G;
+    const int npairs = (hout + 1) / 2;
+    int pitch = SPP;
+    if ((size_t)B * M > 65535) {  // beyond the passes' grid y extent: the segmented transform
+        if (epi) return NC_ERR_UNSUPPORTED;
+        int rc = rfft2_planes<FH, FW>(st, B * M, hout, wout, (size_t)hout * wout, false, gz, sp);
+        if (rc != NC_OK) return rc;
+        pitch = L::SP;
+    } else if (epi) {
         auto al = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
         const int vec = wout % 4 == 0 && al(epi->z) && al(epi->gy) && al(epi->w_eff) &&
                         al(epi->s_eff) && al(epi->b_roi);
-        hipLaunchKernelGGL((k_lrfft_rows_epi<FH, FW>), dim3((npairs + PPW - 1) / PPW, B * M),
-                           dim3(kNT), 0, st, M, hout, wout, vec, *epi, sp);
+        hipLaunchKernelGGL((k_lrfft_rows_epi<FH, FW, SPP>),
+                           dim3((npairs + PPW - 1) / PPW, B * M), dim3(kNT), 0, st, M, hout,
+                           wout, vec, *epi, sp);
+    } else {
+        hipLaunchKernelGGL((k_lrfft_rows<FH, FW, SPP>), dim3((npairs + PPW - 1) / PPW, B * M),
+                           dim3(kNT), 0, st, hout, wout, (size_t)hout * wout, 1, (size_t)0, gz,
+                           sp);
+    }
+    if (pitch == SPP) {
         NC_CHECK_LAUNCH();
-        hipLaunchKernelGGL((k_lrfft_cols<FH, FW>), dim3((L::SP + CPW - 1) / CPW, B * M),
+        hipLaunchKernelGGL((k_lrfft_cols<FH, FW, SPP>), dim3((L::SP + CPW - 1) / CPW, B * M),
                            dim3(kNT), 0, st, hout, (const cpx*)nullptr, sp);
         NC_CHECK_LAUNCH();
-    } else {
-        int rc = rfft2_two_pass<FH, FW>(st, B * M, hout, wout, (size_t)hout * wout, gz, sp);
-        if (rc != NC_OK) return rc;
     }
-    hipLaunchKernelGGL((k_lred<kRedMC>), dim3((L::F + 255) / 256, nchunk, splits), dim3(256), 0,
-                       st, B, M, L::F, need_dx, sp, reinterpret_cast<const cpx*>(xhat),
+    hipLaunchKernelGGL((k_lred<kRedMC>), dim3((FH * pitch + 255) / 256, nchunk, splits),
+                       dim3(256), 0, st, B, M, L::F, L::SP, pitch, need_dx, sp,
+                       reinterpret_cast<const cpx*>(xhat),
                        reinterpret_cast<const cpx*>(ghat), part, reinterpret_cast<cpx*>(dghat),
                        accumulate, conj_out, reinterpret_cast<cpx*>(ssum), sum_acc);
     NC_CHECK_LAUNCH();
