@@ -35,16 +35,13 @@ struct LGeo {
     static_assert(NT % GH::G == 0 && NT % GW::G == 0, "whole groups");
     static constexpr int NGH = NT / GH::G;  // column transforms in flight
     static constexpr int NGW = NT / GW::G;  // row-pair transforms in flight
-    // Column groups interleave lane by lane (group g = tid % NGH, so a wavefront holds
-    // min(NGH, 64) groups and 64 / that lanes of each).  A wavefront's 8-byte LDS accesses
-    // run as two half-wavefront passes over the 32 bank pairs (a cpx at index a sits in pair
-    // a mod 32), so each half's 32 lanes must hit 32 different pairs: the exchange slots lie
-    // SCR_HS cpx apart with SCR_HS = 32 / min(NGH, 32) (mod 32), which spreads the half's
-    // groups and its lanes within a group (consecutive rows t) over every pair, both for the
+    // Column groups interleave lane by lane (group g = tid % NGH, so each 16-lane quarter of
+    // a wavefront holds 16 groups at one row t).  The LDS serves 8-byte accesses 16 lanes per
+    // pass over 16 bank pairs (a cpx at index a sits in pair a mod 16, as the bank-conflict
+    // counters of these passes bear out), so the exchange slots lie SCR_HS cpx apart with
+    // SCR_HS odd (1 mod 32): a quarter's 16 groups then hit 16 different pairs, both for the
     // stage-1 writes (row k1, column t) and the stage-2 reads (row t, column t2).
-    static constexpr int GPW = NGH < 64 ? NGH : 64;
-    static constexpr int SCR_HS =
-        GH::SCR + (((GPW >= 32 ? 1 : 32 / GPW) - GH::SCR % 32) % 32 + 32) % 32;
+    static constexpr int SCR_HS = GH::SCR + ((1 - GH::SCR % 32) % 32 + 32) % 32;
     static constexpr int SCR_H = NGH * SCR_HS;
     static constexpr int SCR_W = NGW * GW::SCR;
     static constexpr int SCR = SCR_H > SCR_W ? SCR_H : SCR_W;  // exchange scratch (cpx)
