@@ -114,6 +114,8 @@ def test_epilogue_parts(be, B, M, h, w, FH, FW):
     (2, 3, 60, 50, 31, 13, 128, 64, "tanh", True),     # two-pass large-grid correlation
     (1, 2, 224, 224, 31, 31, 256, 256, "tanh", True),  # config-3 planes, two passes
     (1, 3, 40, 150, 13, 63, 64, 256, "gelu", True),    # asymmetric grid, two passes
+    (1, 3, 100, 100, 9, 9, 128, 128, "tanh", True),    # band statistics, 64-row bands
+    (1, 2, 150, 80, 31, 13, 256, 128, "sigmoid", True),  # band statistics, 256 x 128 grid
 ])
 def test_fftconv_epilogue(be, B, M, h, w, kh, kw, FH, FW, act, two_pass):
     res = case_fftconv_epilogue(be, B=B, M=M, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW, act=act,
@@ -179,6 +181,8 @@ def test_direct_conv(be, B, M, H, W, kh, kw, mode, n_parts):
 
 @pytest.mark.parametrize("B,M,h,w,kh,kw,FH,FW,act", [
     (1, 2, 112, 112, 31, 21, 256, 256, "tanh"),   # fused: gz formed in the row pass
+    (1, 2, 100, 100, 9, 9, 128, 128, "relu"),     # fused, 64-row bands
+    (1, 2, 150, 82, 31, 13, 256, 128, "gelu"),    # fused, rows not a multiple of 4 wide
     (2, 3, 20, 24, 7, 5, 64, 64, "gelu")])        # small grid: the two entries in turn
 def test_epilogue_fftconv_bwd(be, B, M, h, w, kh, kw, FH, FW, act):
     res = case_epilogue_fftconv_bwd(be, B=B, M=M, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW, act=act)

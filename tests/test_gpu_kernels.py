@@ -128,6 +128,8 @@ def test_epilogue_parts(be, B, M, h, w, FH, FW):
     (1, 3, 40, 150, 13, 63, 64, 256, "gelu", True),    # asymmetric grid, two passes
     (2, 4, 112, 112, 63, 63, 256, 256, "leaky_relu", True),  # config 2
     (32, 16, 112, 112, 63, 63, 256, 256, "tanh", True),  # config 2 at half its batch
+    (3, 5, 100, 100, 9, 9, 128, 128, "gelu", True),    # band statistics, 64-row bands
+    (2, 4, 150, 80, 31, 13, 256, 128, "sigmoid", True),  # band statistics, 256 x 128 grid
 ])
 def test_fftconv_epilogue(be, B, M, h, w, kh, kw, FH, FW, act, two_pass):
     res = case_fftconv_epilogue(be, B=B, M=M, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW, act=act,
@@ -197,6 +199,8 @@ def test_direct_conv(be, B, M, H, W, kh, kw, mode, n_parts):
     (2, 3, 112, 112, 63, 63, 256, 256, "tanh"),       # fused: gz formed in the row pass
     (2, 5, 224, 224, 31, 31, 256, 256, "leaky_relu"),  # config-3 planes, fused
     (16, 16, 112, 112, 63, 63, 256, 256, "tanh"),     # 256 planes, several tiles per plane
+    (2, 3, 100, 100, 9, 9, 128, 128, "relu"),         # fused, 64-row bands
+    (2, 3, 150, 82, 31, 13, 256, 128, "identity"),    # fused, rows not a multiple of 4 wide
     (3, 4, 40, 50, 23, 13, 64, 64, "gelu")])          # small grid: the two entries in turn
 def test_epilogue_fftconv_bwd(be, B, M, h, w, kh, kw, FH, FW, act):
     res = case_epilogue_fftconv_bwd(be, B=B, M=M, h=h, w=w, kh=kh, kw=kw, FH=FH, FW=FW, act=act)
