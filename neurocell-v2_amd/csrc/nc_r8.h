@@ -21,21 +21,26 @@ namespace r8 {
 
 constexpr int kNT = 256;       // threads per plane
 constexpr int kGroups = 32;    // 8-lane groups per plane
-// LDS pitches, chosen against bank conflicts (64 banks of 4 bytes; a wavefront's 8-byte
-// accesses take at least two passes): a group's exchange slot is 8 x 9 cpx (an 8 x 8
-// transpose with a row pitch of 9 keeps both the row writes and the column reads in two
-// passes) and slots lie 144 dwords apart, rows of the transformed plane 80 dwords apart.
+// LDS pitches, chosen against bank conflicts.  The LDS serves 8-byte accesses 16 lanes (two
+// groups) per pass over 16 bank pairs, a cpx at index a in pair a mod 16:
+// - a group's exchange slot is 8 x 9 cpx and slots lie 72 cpx apart: the 8 x 8 transpose's
+//   row writes (k1 * 9 + t) and column reads (t * 9 + n2) of two groups hit 16 pairs;
+// - the row-transformed rows and the half-spectrum staging lie 34 cpx apart: the column
+//   pass reads R[r * 34 + g] and writes O[kh * 34 + g] with r, kh = t + 8 * k (t = lane in
+//   group), 2t + g distinct over the 16 lanes; the row pass's writes R[(2g + i) * 34 + k]
+//   meet two lanes per pair (no pitch serves both patterns without a conflict).
 constexpr int kEx = 72;        // cpx per group exchange slot (8 rows of 9)
 constexpr int kXP = 9;         // exchange row pitch (cpx)
 constexpr int kSP = 64 + 4;    // staging pitch (floats) of real rows
-constexpr int kRP = 40;        // pitch (cpx) of the row-transformed rows (bins 0..32)
-constexpr int kOP = 40;        // pitch (cpx) of the half-spectrum staging (bins 0..32)
+constexpr int kRP = 34;        // pitch (cpx) of the row-transformed rows (bins 0..32)
+constexpr int kOP = 34;        // pitch (cpx) of the half-spectrum staging (bins 0..32)
 constexpr int kF = 64 * 33;    // half-spectrum bins
 
 // LDS layout of the forward plane transform (cpx units): the exchange slots, then one region
 // shared in turn by the real input staging, the row-transformed rows and the output.
 constexpr int kExCpx = kGroups * kEx;
-constexpr int kRegionCpx = 64 * kRP > 64 * kOP ? 64 * kRP : 64 * kOP;
+constexpr int kMaxCpx(int a, int b) { return a > b ? a : b; }
+constexpr int kRegionCpx = kMaxCpx(kMaxCpx(64 * kRP, 64 * kOP), 64 * kSP / 2);
 constexpr size_t kFwdLdsBytes = (size_t)(kExCpx + kRegionCpx) * sizeof(cpx);
 
 // Per-lane twiddles W64^(t k1), k1 = 0..7 (forward sign), from the 256-point table.

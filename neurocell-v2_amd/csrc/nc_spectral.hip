@@ -572,22 +572,15 @@ __global__ __launch_bounds__(r8::kNT) void k_r8spec(int B, int M, int hout, int 
     float* S = lds + 2 * r8::kExCpx;
     const float* src = gz + (size_t)g * hout * wout;
     const int n = hout * wout;
-    // the plane's n floats as 16-byte loads, all issued together (at most 4096 floats: four
-    // per thread), then scattered into the staging rows; the columns past wout are zeroed
-    constexpr int U = 4;
-    const bool vec = (n & 3) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0;
-    float4 v[U];
+    // the plane's n floats, lane by lane (element f = tid + 256 u, at most 4096 floats), all
+    // issued together, then written to the staging rows: consecutive lanes write consecutive
+    // columns, so the stores meet no bank conflicts; the columns past wout are zeroed
+    constexpr int U = 16;
+    float v[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int q = tid + u * r8::kNT;
-        if (vec) {
-            v[u] = 4 * q < n ? reinterpret_cast<const float4*>(src)[q] : float4{0.f, 0.f, 0.f, 0.f};
-        } else {
-            float e[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) e[j] = 4 * q + j < n ? src[4 * q + j] : 0.f;
-            v[u] = float4{e[0], e[1], e[2], e[3]};
-        }
+        const int f = tid + u * r8::kNT;
+        v[u] = f < n ? src[f] : 0.f;
     }
     for (int e = tid; e < hout * (64 - wout); e += r8::kNT) {
         const int r = e / (64 - wout);
@@ -596,15 +589,10 @@ __global__ __launch_bounds__(r8::kNT) void k_r8spec(int B, int M, int hout, int 
     const unsigned inv = ((1u << 20) + wout - 1) / wout;  // exact floor(f / wout), f < 4096
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int q = tid + u * r8::kNT;
-        const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int f = 4 * q + j;
-            if (f < n) {
-                const int r = (int)(((unsigned)f * inv) >> 20);
-                S[r * r8::kSP + (f - r * wout)] = e[j];
-            }
+        const int f = tid + u * r8::kNT;
+        if (f < n) {
+            const int r = (int)(((unsigned)f * inv) >> 20);
+            S[r * r8::kSP + (f - r * wout)] = v[u];
         }
     }
     r8::fwd_plane(lds, hout, tw);
