@@ -14,10 +14,15 @@
 //                Hermitian split of the packed pair needs each bin's mirror, which sits in the
 //                partner lane at slot N/2 - k: one DPP swap per bin.
 //
-// LDS: T holds the transposed half-spectrum rows (pitch FW/2 + 1 cpx).  The forward keeps the
+// LDS: T holds the transposed half-spectrum rows (pitch FW/2 + 2 cpx).  The forward keeps the
 // live rows plus a trash row and a zero row (as in nc_wave.h); the inverse keeps all FH rows so
 // its stores have constant offsets, and the row pass applies the window's row offset.  Stores
-// are never predicated per element.
+// are never predicated per element.  The LDS serves 8-byte accesses 16 lanes per pass over 16
+// bank pairs (a cpx at index a in pair a mod 16): with the pitch even (2 mod 16) the row pass's
+// reads of 8 consecutive rows by lane pairs (row, t) hit 16 pairs, and the inverse's second
+// row half starts kPairGap cpx further on, so the column pass's stores from the two lanes of a
+// pair (rows k and FH/2 + k of column kc) land 8 pairs apart.
+constexpr int kPairGap = 8;
 #pragma once
 
 #include "nc_wave.h"
@@ -54,10 +59,12 @@ struct PGeo {
     static constexpr int SP = FW / 2 + 1;  // half-spectrum row pitch (cpx)
     static constexpr int F = FH * SP;      // half-spectrum size (cpx)
     static constexpr int NC = FW / 2;      // packed columns = lane pairs of the column pass
-    static constexpr int PITCH = NC + 1;   // LDS pitch of a transposed row (cpx)
+    static constexpr int PITCH = NC + 2;   // LDS pitch of a transposed row (cpx)
     static constexpr int PF = FH * NC;     // packed spectrum size (cpx)
     static constexpr int HH = FH / 2;      // column samples per lane
     static constexpr int HW = FW / 2;      // row samples per lane
+    // offset (cpx) of row r of the inverse's T: rows FH/2 .. FH-1 follow a kPairGap gap
+    static NC_DEV int trow(int r) { return r * PITCH + (r >= HH ? kPairGap : 0); }
 };
 
 // The mirror partner of slot k for a spectrum held as lane t: bin t*N/2 + k.  The bin's mirror
@@ -128,14 +135,14 @@ NC_DEV void pcol_fwd(const cpx* T, int rows, cpx* v) {
 }
 
 // Inverse column pass: v holds lane pair kc's packed spectrum column at rows 2j + t; every
-// output row r lands in T row r (T: FH x PITCH cpx), so each store has a constant offset; the
-// row pass applies the window's row offset.
+// output row r lands in T row r (at P::trow(r): FH x PITCH cpx plus the gap), so each store
+// has a constant offset; the row pass applies the window's row offset.
 template <int FH, int FW>
 NC_DEV void pcol_inv(cpx* v, cpx* T) {
     using P = PGeo<FH, FW>;
     const int lane = threadIdx.x & 63, kc = lane >> 1, t = lane & 1;
     fft_pair<FH, true>(v, t);
-    cpx* tc = T + t * P::HH * P::PITCH + kc;
+    cpx* tc = T + P::trow(t * P::HH) + kc;
 #pragma unroll
     for (int k = 0; k < P::HH; ++k) tc[k * P::PITCH] = v[k];
 }
@@ -153,8 +160,8 @@ NC_DEV void prow_inv(const cpx* T, int row0, int col0, int rows, float scale, fl
     const int q = on ? q0 : 0;
     const int ib = q + NR;
     const bool hb = on && ib < rows;
-    const cpx* ta = T + ((q + row0) & (FH - 1)) * P::PITCH;
-    const cpx* tb = T + (((hb ? ib : q) + row0) & (FH - 1)) * P::PITCH;
+    const cpx* ta = T + P::trow((q + row0) & (FH - 1));
+    const cpx* tb = T + P::trow(((hb ? ib : q) + row0) & (FH - 1));
     const float bs = hb ? 1.f : 0.f;
     cpx v[P::HW];
 #pragma unroll

@@ -491,7 +491,9 @@ struct PLds {
     size_t bytes;
     int nq;  // cpx offset of the Nyquist staging
     PLds(int rows, int pitch, int fw, int fh, bool inverse) {
-        const size_t t = (size_t)(inverse ? fh : rows + 2) * pitch * sizeof(cpx);
+        // the inverse's T: all fh rows and the gap between its two row halves
+        const size_t t = ((size_t)(inverse ? fh : rows + 2) * pitch + (inverse ? kPairGap : 0)) *
+                         sizeof(cpx);
         const size_t o = (size_t)(rows + 1) * (fw + 1) * sizeof(float);
         const size_t main = (std::max(t, o) + 15) / 16 * 16;
         nq = (int)(main / sizeof(cpx));
