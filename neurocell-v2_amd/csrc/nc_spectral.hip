@@ -561,6 +561,48 @@ __global__ __launch_bounds__(64) void k_pspec(int B, int M, int hout, int wout, 
                                            SpecPost{});
 }
 
+// Stages one (hin x win) real plane at the origin of the 64 x 64 grid into the radix-8 input
+// staging S (hin rows of r8::kSP floats, columns win..63 zero), as r8::fwd_plane expects it.
+// The plane's n <= 4096 floats are read lane by lane (element f = tid + 256 u), all loads
+// issued together; with NP != 1 each element is the sum of the partial planes qstride floats
+// apart, in increasing order (NP == 0: nq of them).  Consecutive lanes write consecutive
+// columns, so the stores meet no bank conflicts.
+template <int NP>
+NC_DEV void r8_stage_plane(const float* __restrict__ src, int hin, int win, size_t qstride,
+                           int nq, float* S) {
+    const int tid = threadIdx.x, n = hin * win;
+    constexpr int U = 16;
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int f = tid + u * r8::kNT;
+        float a = 0.f;
+        if (f < n) {
+            a = src[f];
+            if constexpr (NP > 1) {
+#pragma unroll
+                for (int q = 1; q < NP; ++q) a += src[q * qstride + f];
+            } else if constexpr (NP == 0) {
+                for (int q = 1; q < nq; ++q) a += src[q * qstride + f];
+            }
+        }
+        v[u] = a;
+    }
+    for (int e = tid; e < hin * (64 - win); e += r8::kNT) {
+        const int r = e / (64 - win);
+        S[r * r8::kSP + win + (e - r * (64 - win))] = 0.f;
+    }
+    const unsigned inv = ((1u << 20) + win - 1) / win;  // exact floor(f / win), f < 4096
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int f = tid + u * r8::kNT;
+        if (f < n) {
+            const int r = (int)(((unsigned)f * inv) >> 20);
+            S[r * r8::kSP + (f - r * win)] = v[u];
+        }
+    }
+}
+
 // Backward, first stage on the 64 x 64 grid: the half-spectrum of every cotangent plane
 // gz_bm (g = b*M + m) into spec (M, B, pitch), one 256-thread workgroup per plane (8-lane
 // 64-point transforms, nc_r8.h): the plane is staged in LDS with coalesced loads, transformed,
@@ -571,34 +613,9 @@ __global__ __launch_bounds__(r8::kNT) void k_r8spec(int B, int M, int hout, int 
     HIP_DYNAMIC_SHARED(float, lds)
     const int g = blockIdx.x, b = g / M, m = g - b * M, tid = threadIdx.x;
     const r8::Tw tw = r8::twiddles(tid & 7);
-    float* S = lds + 2 * r8::kExCpx;
-    const float* src = gz + (size_t)g * hout * wout;
-    const int n = hout * wout;
-    // the plane's n floats, lane by lane (element f = tid + 256 u, at most 4096 floats), all
-    // issued together, then written to the staging rows: consecutive lanes write consecutive
-    // columns, so the stores meet no bank conflicts; the columns past wout are zeroed
-    constexpr int U = 16;
-    float v[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int f = tid + u * r8::kNT;
-        v[u] = f < n ? src[f] : 0.f;
-    }
-    for (int e = tid; e < hout * (64 - wout); e += r8::kNT) {
-        const int r = e / (64 - wout);
-        S[r * r8::kSP + wout + (e - r * (64 - wout))] = 0.f;
-    }
-    const unsigned inv = ((1u << 20) + wout - 1) / wout;  // exact floor(f / wout), f < 4096
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int f = tid + u * r8::kNT;
-        if (f < n) {
-            const int r = (int)(((unsigned)f * inv) >> 20);
-            S[r * r8::kSP + (f - r * wout)] = v[u];
-        }
-    }
+    r8_stage_plane<1>(gz + (size_t)g * hout * wout, hout, wout, 0, 1, lds + 2 * r8::kExCpx);
     r8::fwd_plane(lds, hout, tw);
-    const cpx* O = reinterpret_cast<const cpx*>(S);
+    const cpx* O = reinterpret_cast<const cpx*>(lds + 2 * r8::kExCpx);
     cpx* dst = spec + ((size_t)m * B + b) * spec_pitch<64, 64>();
 #pragma unroll
     for (int u = 0; u < (r8::kF + r8::kNT - 1) / r8::kNT; ++u) {
@@ -606,6 +623,31 @@ __global__ __launch_bounds__(r8::kNT) void k_r8spec(int B, int M, int hout, int 
         if (e < r8::kF) {
             const int kh = e / 33, kw = e - 33 * kh;
             dst[e] = O[kh * r8::kOP + kw];
+        }
+    }
+}
+
+// Half-spectra (64, 33) of real (hin x win) planes on the 64 x 64 grid, one 256-thread
+// workgroup per plane (the cell spectra of a propagation step: each plane the sum of the
+// previous step's direction-group partial outputs, kernels_pallas.py:1779-1791), each bin
+// through spec_post<POST> (kPostNone or kPostAdd: plus the shared border-patch spectrum).
+template <int POST, int NP>
+__global__ __launch_bounds__(r8::kNT) void k_r8rfft2(int hin, int win, size_t qstride, int nq,
+                                                     const float* __restrict__ x,
+                                                     cpx* __restrict__ out, SpecPost post) {
+    HIP_DYNAMIC_SHARED(float, lds)
+    const int g = blockIdx.x, tid = threadIdx.x;
+    const r8::Tw tw = r8::twiddles(tid & 7);
+    r8_stage_plane<NP>(x + (size_t)g * hin * win, hin, win, qstride, nq, lds + 2 * r8::kExCpx);
+    r8::fwd_plane(lds, hin, tw);
+    const cpx* O = reinterpret_cast<const cpx*>(lds + 2 * r8::kExCpx);
+    cpx* dst = out + (size_t)g * r8::kF;
+#pragma unroll
+    for (int u = 0; u < (r8::kF + r8::kNT - 1) / r8::kNT; ++u) {
+        const int e = tid + u * r8::kNT;
+        if (e < r8::kF) {
+            const int kh = e / 33, kw = e - 33 * kh;
+            dst[e] = spec_post<POST, 64, 64>(O[kh * r8::kOP + kw], kh, kw, post);
         }
     }
 }
@@ -1144,17 +1186,43 @@ void launch_rfft2_np(hipStream_t st, int nplanes, int hin, int win, const float*
                                                      qstride, nq);
 }
 
+// k_r8rfft2 over nplanes planes of at most 64 x 64 (nparts partial planes each).
+template <int POST>
+void launch_r8rfft2(hipStream_t st, int nplanes, int hin, int win, const float* x, cpx* out,
+                    const SpecPost& post, int nparts, size_t qstride) {
+#define NC_R8(NP_)                                                                          \
+    do {                                                                                    \
+        lds_limit(k_r8rfft2<POST, NP_>, r8::kFwdLdsBytes);                                  \
+        hipLaunchKernelGGL((k_r8rfft2<POST, NP_>), dim3(nplanes), dim3(r8::kNT),            \
+                           r8::kFwdLdsBytes, st, hin, win, qstride, nparts, x, out, post); \
+    } while (0)
+    if (nparts == 1) NC_R8(1);
+    else if (nparts == 4) NC_R8(4);
+    else NC_R8(0);
+#undef NC_R8
+}
+
 // Half-spectra of nplanes real planes; flip (the filter spectra) takes no post-operation.
 // nparts > 1: each plane is the sum of nparts partial planes qstride floats apart.
 template <int FH, int FW>
 int launch_rfft2(hipStream_t st, int nplanes, int hin, int win, bool flip, const float* x,
                  cpx* out, int post_kind = kPostNone, const SpecPost& post = SpecPost{},
                  int nparts = 1, size_t qstride = 0) {
-    if constexpr (seg_grid<FH, FW>())
+    if constexpr (seg_grid<FH, FW>()) {
+        // unflipped planes without a phase ramp: one radix-8 workgroup per plane
+        if (!flip && post_kind != kPostShift) {
+            if (post_kind == kPostAdd)
+                launch_r8rfft2<kPostAdd>(st, nplanes, hin, win, x, out, post, nparts, qstride);
+            else
+                launch_r8rfft2<kPostNone>(st, nplanes, hin, win, x, out, post, nparts, qstride);
+            NC_CHECK_LAUNCH();
+            return NC_OK;
+        }
         return nc_seg_rfft2(st, FH, FW, nplanes, hin, win, flip ? 1 : 0, x, out,
                             post_kind == kPostAdd ? post.add : nullptr,
                             post_kind == kPostShift ? post.sh : 0,
                             post_kind == kPostShift ? post.sw : 0, nparts, qstride);
+    }
     if (flip)
         launch_rfft2_k<FH, FW, true, kPostNone, 1>(st, nplanes, hin, win, x, out, post, 0, 1);
     else if (nparts == 1)
