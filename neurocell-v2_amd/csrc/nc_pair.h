@@ -147,6 +147,22 @@ NC_DEV void pcol_inv(cpx* v, cpx* T) {
     for (int k = 0; k < P::HH; ++k) tc[k * P::PITCH] = v[k];
 }
 
+// Inverse column pass keeping only a window of output rows: row r lands in T row
+// (r - row0) mod FH when that is below `rows`, and is dropped otherwise, so T holds `rows`
+// rows (the row pass then reads them with row0 = 0).  The stores are predicated per element,
+// but the LDS holds fewer rows, which leaves room for more workgroups per CU.
+template <int FH, int FW>
+NC_DEV void pcol_inv_rows(cpx* v, cpx* T, int row0, int rows) {
+    using P = PGeo<FH, FW>;
+    const int lane = threadIdx.x & 63, kc = lane >> 1, t = lane & 1;
+    fft_pair<FH, true>(v, t);
+#pragma unroll
+    for (int k = 0; k < P::HH; ++k) {
+        const int i = (t * P::HH + k - row0) & (FH - 1);
+        if (i < rows) T[P::trow(i) + kc] = v[k];
+    }
+}
+
 // Inverse row pass: output rows i < rows, taken from T row (i + row0) mod FH (packed
 // half-spectrum rows), times scale, into the staging O (row i at O[i * (FW + 1)], every one of
 // the FW columns stored at (c - col0) mod FW; row `rows` is the trash row).  All lanes must call

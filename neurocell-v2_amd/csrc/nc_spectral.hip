@@ -490,10 +490,11 @@ constexpr bool seg_grid() {
 struct PLds {
     size_t bytes;
     int nq;  // cpx offset of the Nyquist staging
-    PLds(int rows, int pitch, int fw, int fh, bool inverse) {
-        // the inverse's T: all fh rows and the gap between its two row halves
-        const size_t t = ((size_t)(inverse ? fh : rows + 2) * pitch + (inverse ? kPairGap : 0)) *
-                         sizeof(cpx);
+    PLds(int rows, int pitch, int fw, int fh, bool inverse, bool window = false) {
+        // the inverse's T: all fh rows (only the window's `rows` with pcol_inv_rows) and the
+        // gap between its two row halves
+        const int trows = inverse ? (window ? rows : fh) : rows + 2;
+        const size_t t = ((size_t)trows * pitch + (inverse ? kPairGap : 0)) * sizeof(cpx);
         const size_t o = (size_t)(rows + 1) * (fw + 1) * sizeof(float);
         const size_t main = (std::max(t, o) + 15) / 16 * 16;
         nq = (int)(main / sizeof(cpx));
@@ -801,12 +802,12 @@ __global__ __launch_bounds__(64) void k_pconv_fwd(int M, int hout, int wout, int
 // 163-291): workgroup (b, g) of 4 wavefronts, wavefront w computing the plane m = 4g + w as
 // k_pconv_fwd does (storing it to z when z is given), then its plane statistics (mean, then
 // the centred sum of squares: population variance, eps 1e-5), zhat and act(zhat + b_roi).
-// Each wavefront leaves (zhat, act) in its own LDS region; the workgroup adds the four in
+// Each wavefront leaves zhat, then act, in its own LDS region; the workgroup adds the four in
 // increasing m and writes the direction group's partial output
 // parts[g][b] = w_eff * sum zhat + s_eff * sum act, the layout of nc_epilogue_fwd_parts.
 // NE >= ceil(N / 64) plane values per lane; every loop runs NE (or NE / 4) times with clamped
 // loads, so a wavefront's loads issue together.
-template <int FH, int FW, int ACT, int NE>
+template <int FH, int FW, int ACT, int NE, bool WIN>
 __global__ __launch_bounds__(256, 2) void k_pconv_epi(int B, int M, int hout, int wout, int ph,
                                                    int pw, int nq_off, int region, float slope,
                                                    const cpx* __restrict__ xhat,
@@ -847,9 +848,15 @@ __global__ __launch_bounds__(256, 2) void k_pconv_epi(int B, int M, int hout, in
 #pragma unroll
         for (int j = 0; j < P::HH; ++j) v[j] = cadd(v[j], cmul_i(NQ[2 * j + t]));
     }
-    pcol_inv<FH, FW>(v, T);
-    __syncthreads();
-    prow_inv<FH, FW>(T, ph, pw, hout, 1.0f / (float)(FH * FW), lds);
+    if constexpr (WIN) {
+        pcol_inv_rows<FH, FW>(v, T, ph, hout);
+        __syncthreads();
+        prow_inv<FH, FW>(T, 0, pw, hout, 1.0f / (float)(FH * FW), lds);
+    } else {
+        pcol_inv<FH, FW>(v, T);
+        __syncthreads();
+        prow_inv<FH, FW>(T, ph, pw, hout, 1.0f / (float)(FH * FW), lds);
+    }
     __syncthreads();
     // the per-pixel parameters, requested together; their latency hides behind the statistics
     float bv[NE], wq[NC], sq_[NC];
@@ -891,20 +898,61 @@ __global__ __launch_bounds__(256, 2) void k_pconv_epi(int B, int M, int hout, in
         mean[(size_t)b * M + m] = mu;
         rstd[(size_t)b * M + m] = r;
     }
-    // (zhat, act) replace the staging in this wavefront's region once every lane has read it
+    // (zhat, act(zhat + b_roi)) replace the staging in this wavefront's region once every lane
+    // has read it (WIN: zhat, then act, one plane of N floats at a time); the workgroup sums
+    // each over its four directions in increasing m
     __syncthreads();
     const float on = live ? 1.f : 0.f;
-    float* L = lds;
-    float* A = lds + N;
+    if constexpr (!WIN) {
+        float* L = lds;
+        float* A = lds + N;
+#pragma unroll
+        for (int i = 0; i < NE; ++i) {
+            const int e = lane + 64 * i;
+            const float zn = (zv[i] - mu) * r;
+            const float a = act_f<ACT>(zn + bv[i], slope);
+            if (e < N) {
+                L[e] = zn * on;
+                A[e] = a * on;
+            }
+        }
+        __syncthreads();
+        float* out = parts + ((size_t)g * B + b) * N;
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const int e = (int)threadIdx.x + 256 * i;
+            const int ec = min(e, N - 1);
+            float lin = ldsall[ec], ac = ldsall[N + ec];
+#pragma unroll
+            for (int q = 1; q < 4; ++q) {
+                lin += ldsall[(size_t)q * region + ec];
+                ac += ldsall[(size_t)q * region + N + ec];
+            }
+            if (e < N) out[e] = wq[i] * lin + sq_[i] * ac;
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < NE; ++i) {
         const int e = lane + 64 * i;
-        const float zn = (zv[i] - mu) * r;
-        const float a = act_f<ACT>(zn + bv[i], slope);
-        if (e < N) {
-            L[e] = zn * on;
-            A[e] = a * on;
-        }
+        zv[i] = (zv[i] - mu) * r;
+        if (e < N) lds[e] = zv[i] * on;
+    }
+    __syncthreads();
+    float lin[NC];
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+        const int ec = min((int)threadIdx.x + 256 * i, N - 1);
+        lin[i] = ldsall[ec];
+#pragma unroll
+        for (int q = 1; q < 4; ++q) lin[i] += ldsall[(size_t)q * region + ec];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+        const int e = lane + 64 * i;
+        const float a = act_f<ACT>(zv[i] + bv[i], slope);
+        if (e < N) lds[e] = a * on;
     }
     __syncthreads();
     float* out = parts + ((size_t)g * B + b) * N;
@@ -912,13 +960,10 @@ __global__ __launch_bounds__(256, 2) void k_pconv_epi(int B, int M, int hout, in
     for (int i = 0; i < NC; ++i) {
         const int e = (int)threadIdx.x + 256 * i;
         const int ec = min(e, N - 1);
-        float lin = ldsall[ec], ac = ldsall[N + ec];
+        float ac = ldsall[ec];
 #pragma unroll
-        for (int q = 1; q < 4; ++q) {
-            lin += ldsall[(size_t)q * region + ec];
-            ac += ldsall[(size_t)q * region + N + ec];
-        }
-        if (e < N) out[e] = wq[i] * lin + sq_[i] * ac;
+        for (int q = 1; q < 4; ++q) ac += ldsall[(size_t)q * region + ec];
+        if (e < N) out[e] = wq[i] * lin[i] + sq_[i] * ac;
     }
 }
 
@@ -930,8 +975,8 @@ __global__ __launch_bounds__(256, 2) void k_pconv_epi(int B, int M, int hout, in
 // part (2, G, B, P) = (Σ zo, Σ final_act(zo + b_out)) that k_port_combine turns into the
 // port outputs, as nc_port_fwd's split does.  The idle wavefronts of the last group repeat
 // m = M - 1 and store nothing.
-template <int FH, int FW, int NE>
-__global__ __launch_bounds__(256) void k_pconv_port(int B, int M, int hout, int wout, int ph,
+template <int FH, int FW, int NE, bool WIN>
+__global__ __launch_bounds__(256, 2) void k_pconv_port(int B, int M, int hout, int wout, int ph,
                                                     int pw, int nq_off, int region, int P,
                                                     int fact, float slope,
                                                     const cpx* __restrict__ xhat,
@@ -970,9 +1015,15 @@ __global__ __launch_bounds__(256) void k_pconv_port(int B, int M, int hout, int 
 #pragma unroll
         for (int j = 0; j < P_::HH; ++j) v[j] = cadd(v[j], cmul_i(NQ[2 * j + t]));
     }
-    pcol_inv<FH, FW>(v, T);
-    __syncthreads();
-    prow_inv<FH, FW>(T, ph, pw, hout, 1.0f / (float)(FH * FW), lds);
+    if constexpr (WIN) {
+        pcol_inv_rows<FH, FW>(v, T, ph, hout);
+        __syncthreads();
+        prow_inv<FH, FW>(T, 0, pw, hout, 1.0f / (float)(FH * FW), lds);
+    } else {
+        pcol_inv<FH, FW>(v, T);
+        __syncthreads();
+        prow_inv<FH, FW>(T, ph, pw, hout, 1.0f / (float)(FH * FW), lds);
+    }
     __syncthreads();
     // the port cells' flat indices, requested before the statistics
     int pe[PK];
@@ -1072,6 +1123,21 @@ struct WLds {
 // float4 moves need 16-byte aligned planes.
 inline int vec_ok(const void* p, size_t n) {
     return (n % 4 == 0) && (reinterpret_cast<uintptr_t>(p) % 16 == 0);
+}
+
+// Compute units of the current device (queried once per device).
+int cu_count() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
 }
 
 template <class K>
@@ -1262,12 +1328,13 @@ int launch_corr(hipStream_t st, int B, int M, int hout, int wout, int ph, int pw
 }
 
 // Per-wavefront LDS region (floats) of the fused correlation + hidden epilogue: the inverse
-// transform's staging, or the plane's (zhat, act) pair, whichever is larger; 0 when four
-// regions do not fit one workgroup's LDS.
+// transform's staging, or the plane's (zhat, act) pair, whichever is larger; WIN: the staging
+// over the output window's rows only (pcol_inv_rows), or one plane (zhat, then act).  0 when
+// four regions do not fit one workgroup's LDS.
 template <int FH, int FW>
-int corr_epi_region(int hout, int wout) {
-    const PLds l(hout, PGeo<FH, FW>::PITCH, FW, FH, true);
-    const size_t fl = std::max(l.bytes / sizeof(float), (size_t)2 * hout * wout);
+int corr_epi_region(int hout, int wout, bool win = false) {
+    const PLds l(hout, PGeo<FH, FW>::PITCH, FW, FH, true, win);
+    const size_t fl = std::max(l.bytes / sizeof(float), (size_t)(win ? 1 : 2) * hout * wout);
     const size_t region = (fl + 15) / 16 * 16;
     return 4 * region * sizeof(float) <= 163840 ? (int)region : 0;
 }
@@ -1277,6 +1344,14 @@ int corr_epi_region(int fft_h, int fft_w, int hout, int wout) {
     if (fft_h == 64) return corr_epi_region<64, 64>(hout, wout);
     if (fft_h == 32) return corr_epi_region<32, 64>(hout, wout);
     return 0;
+}
+
+// The windowed form of the fused kernels (a smaller LDS region: three workgroups per CU
+// instead of two) for grids of more than two workgroups per CU.  At two or fewer per CU its
+// extra barriers and predicated stores cost more than the occupancy gains (config 0: 25.0 ->
+// 27.3 us per hidden step), while a B = 1024 evaluation gains a fifth in throughput.
+bool corr_windowed(const dim3& grid) {
+    return (size_t)grid.x * grid.y > 2 * (size_t)cu_count();
 }
 
 // The fused correlation + hidden epilogue on the lane-pair grids; false when the plane is
@@ -1289,20 +1364,26 @@ bool launch_corr_epi(hipStream_t st, int B, int M, int hout, int wout, int ph, i
     if constexpr (!pair_grid<FH, FW>()) {
         return false;
     } else {
-        const PLds l(hout, PGeo<FH, FW>::PITCH, FW, FH, true);
-        const int region = corr_epi_region<FH, FW>(hout, wout);
-        if (region == 0) return false;
-        const size_t bytes = (size_t)4 * region * sizeof(float);
+        if (corr_epi_region<FH, FW>(hout, wout) == 0) return false;
         const dim3 grid(B, (M + 3) / 4);
+        const bool win = corr_windowed(grid);
+        const PLds l(hout, PGeo<FH, FW>::PITCH, FW, FH, true, win);
+        const int region = corr_epi_region<FH, FW>(hout, wout, win);
+        const size_t bytes = (size_t)4 * region * sizeof(float);
         const int N = hout * wout;
-#define NC_CE2(A_, NE_)                                                                        \
+#define NC_CE3(A_, NE_, W_)                                                                    \
     do {                                                                                       \
-        lds_limit(k_pconv_epi<FH, FW, A_, NE_>, bytes);                                        \
-        hipLaunchKernelGGL((k_pconv_epi<FH, FW, A_, NE_>), grid, dim3(256), bytes, st, B, M,   \
-                           hout, wout, ph, pw, l.nq, region, slope,                            \
+        lds_limit(k_pconv_epi<FH, FW, A_, NE_, W_>, bytes);                                    \
+        hipLaunchKernelGGL((k_pconv_epi<FH, FW, A_, NE_, W_>), grid, dim3(256), bytes, st, B,  \
+                           M, hout, wout, ph, pw, l.nq, region, slope,                         \
                            reinterpret_cast<const cpx*>(xhat),                                 \
                            reinterpret_cast<const cpx*>(ghat), w_eff, s_eff, b_roi, z, parts,  \
                            mean, rstd);                                                        \
+    } while (0)
+#define NC_CE2(A_, NE_)                         \
+    do {                                        \
+        if (win) NC_CE3(A_, NE_, true);         \
+        else NC_CE3(A_, NE_, false);            \
     } while (0)
 #define NC_CE(A_)                                                        \
     do {                                                                 \
@@ -1319,6 +1400,7 @@ bool launch_corr_epi(hipStream_t st, int B, int M, int hout, int wout, int ph, i
         }
 #undef NC_CE
 #undef NC_CE2
+#undef NC_CE3
         return true;
     }
 }
@@ -1331,23 +1413,31 @@ bool launch_corr_port(hipStream_t st, int B, int M, int hout, int wout, int ph, 
     if constexpr (!pair_grid<FH, FW>()) {
         return false;
     } else {
-        const PLds l(hout, PGeo<FH, FW>::PITCH, FW, FH, true);
-        const int region = corr_epi_region<FH, FW>(hout, wout);
-        if (region == 0 || region < P) return false;
-        const size_t bytes = (size_t)4 * region * sizeof(float);
+        const int full = corr_epi_region<FH, FW>(hout, wout);
+        if (full == 0 || full < P) return false;
         const dim3 grid(B, (M + 3) / 4);
-#define NC_CP(NE_)                                                                            \
+        const bool win = corr_windowed(grid) && corr_epi_region<FH, FW>(hout, wout, true) >= P;
+        const PLds l(hout, PGeo<FH, FW>::PITCH, FW, FH, true, win);
+        const int region = win ? corr_epi_region<FH, FW>(hout, wout, true) : full;
+        const size_t bytes = (size_t)4 * region * sizeof(float);
+#define NC_CP2(NE_, W_)                                                                       \
     do {                                                                                      \
-        lds_limit(k_pconv_port<FH, FW, NE_>, bytes);                                          \
-        hipLaunchKernelGGL((k_pconv_port<FH, FW, NE_>), grid, dim3(256), bytes, st, B, M,     \
+        lds_limit(k_pconv_port<FH, FW, NE_, W_>, bytes);                                      \
+        hipLaunchKernelGGL((k_pconv_port<FH, FW, NE_, W_>), grid, dim3(256), bytes, st, B, M, \
                            hout, wout, ph, pw, l.nq, region, P, fact, slope,                  \
                            reinterpret_cast<const cpx*>(xhat),                                \
                            reinterpret_cast<const cpx*>(ghat), pidx, pp, z, zo, mean, rstd,   \
                            part);                                                             \
     } while (0)
+#define NC_CP(NE_)                     \
+    do {                               \
+        if (win) NC_CP2(NE_, true);    \
+        else NC_CP2(NE_, false);       \
+    } while (0)
         if (FH * FW > 2048 && hout * wout > 2048) NC_CP(FH * FW / 64);
         else NC_CP(32);
 #undef NC_CP
+#undef NC_CP2
         return true;
     }
 }

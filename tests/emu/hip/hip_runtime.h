@@ -87,6 +87,13 @@ inline void sincospif(float x, float* s, float* c) {
 }
 #define HIP_SYMBOL(X) X
 inline hipError_t hipGetDevice(int* d) { *d = 0; return 0; }
+// The emulated device reports two compute units, so launch choices that depend on the grid
+// filling the device (the fused correlation's windowed form) are reached by small cases.
+enum hipDeviceAttribute_t { hipDeviceAttributeMultiprocessorCount = 0 };
+inline hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t, int) {
+    *v = 2;
+    return 0;
+}
 inline hipError_t hipStreamGetDevice(hipStream_t, int* d) { *d = 0; return 0; }
 template <typename T>
 inline hipError_t hipGetSymbolAddress(void** p, const T& sym) {
