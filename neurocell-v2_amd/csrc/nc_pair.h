@@ -16,12 +16,14 @@
 //
 // LDS: T holds the transposed half-spectrum rows (pitch FW/2 + 2 cpx).  The forward keeps the
 // live rows plus a trash row and a zero row (as in nc_wave.h); the inverse keeps all FH rows so
-// its stores have constant offsets, and the row pass applies the window's row offset.  Stores
-// are never predicated per element.  The LDS serves 8-byte accesses 16 lanes per pass over 16
-// bank pairs (a cpx at index a in pair a mod 16): with the pitch even (2 mod 16) the row pass's
-// reads of 8 consecutive rows by lane pairs (row, t) hit 16 pairs, and the inverse's second
-// row half starts kPairGap cpx further on, so the column pass's stores from the two lanes of a
-// pair (rows k and FH/2 + k of column kc) land 8 pairs apart.
+// its stores have constant offsets, and the row pass applies the window's row offset (the
+// windowed column pass, pcol_inv_rows, keeps only the window's rows with predicated stores,
+// for kernels that trade those for a smaller LDS footprint).  The LDS serves 8-byte accesses
+// 16 lanes per pass over 16 bank pairs (a cpx at index a in pair a mod 16): with the pitch
+// even (2 mod 16) the row pass's reads of 8 consecutive rows by lane pairs (row, t) hit 16
+// pairs, and the inverse's second row half starts kPairGap cpx further on, so the column
+// pass's stores from the two lanes of a pair (rows k and FH/2 + k of column kc) land 8 pairs
+// apart.
 constexpr int kPairGap = 8;
 #pragma once
 
