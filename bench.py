@@ -173,7 +173,7 @@ def kernel_families(ts, torch, reps, flushed=False, graph=True):
 # C-ABI family of each kernel of a --families-only run (k_batch_reduce belongs to whichever
 # backward family launched it: the preceding kernel decides).
 _FAMILY_KERNELS = {
-    "spectra": ("k_wrfft2", "k_lrfft2", "k_prfft2"),
+    "spectra": ("k_wrfft2", "k_lrfft2", "k_prfft2", "k_r8rfft2"),
     "conv_epilogue_fwd": ("k_pconv_epi", "k_epi_fwd", "k_group_sum", "k_tile_stats",
                           "k_tile_fwd"),
     "conv_port_fwd": ("k_pconv_port", "k_wconv_fwd", "k_linv_conv", "k_pconv_fwd",
