@@ -554,6 +554,57 @@ def case_fftconv_epilogue(be, B=3, M=6, h=20, w=27, kh=7, kw=5, FH=32, FW=64, ac
     return res
 
 
+def case_fused_forms(be, B_small, B_large, M=16, h=40, w=50, kh=23, kw=13, FH=64, FW=64,
+                     act="tanh", seed=21):
+    """The fused correlation + epilogue's two forms compute the same thing.  The launch takes
+    the windowed form (the inverse's column pass keeps only the window's rows, zhat and act
+    staged one plane at a time) when the grid holds more than two workgroups per CU, the
+    full-row form otherwise; the same B_small samples run once alone (B_small * G at most
+    twice the CU count) and once as the first samples of a B_large batch (above it).  Each
+    sample's results depend on that sample only, so any difference is the forms': the same
+    arithmetic in two compilations, which hipcc may contract differently (the CPU emulation
+    gives equal bits).  Returns the largest rel-L2 difference over z, the partial outputs,
+    mean and rstd ("forms"), the elements that differ at all, and the windowed z against
+    the oracle."""
+    rng = np.random.default_rng(seed)
+    L, s = be.lib, be.stream()
+    ph, pw = (kh - 1) // 2, (kw - 1) // 2
+    xs = (rng.normal(size=(B_small, h, w)) * 0.7).astype(np.float32)
+    xl = np.concatenate([xs] + [(rng.normal(size=(B_large - B_small, h, w)) * 0.7)
+                                .astype(np.float32)])
+    g = rng.normal(size=(M, 1, kh, kw)).astype(np.float32) / np.sqrt(kh * kw)
+    wv = rng.normal(size=(h, w)).astype(np.float32)
+    sv = rng.uniform(size=(h, w)).astype(np.float32)
+    bv = rng.normal(size=(h, w)).astype(np.float32)
+    gd, wd, sd, bd = (be.put(a) for a in (g, wv, sv, bv))
+    aid = _abi.ACT_IDS[act]
+    ghat = be.zeros((M, FH, FW // 2 + 1, 2))
+    _ok(be, L.nc_filter_spectrum_fwd(s, M, kh, kw, FH, FW, be.ptr(gd), be.ptr(ghat)), "spec")
+    outs = []
+    for x in (xs, xl):
+        B = x.shape[0]
+        xd = be.put(x)
+        xh = be.zeros((B, FH, FW // 2 + 1, 2))
+        _ok(be, L.nc_fftconv_spectra(s, B, h, w, FH, FW, be.ptr(xd), 1, None, be.ptr(xh)),
+            "spectra")
+        G = L.nc_fftconv_epilogue_partials(B, M, h, w, FH, FW)
+        nws = L.nc_epilogue_workspace_size(B, M, h, w)
+        ws = be.zeros((nws // 4 + 1,))
+        nb = ws.nbytes if hasattr(ws, "nbytes") else ws.numel() * 4
+        z, p = be.zeros((B, M, h, w)), be.zeros((G, B, h, w))
+        mu, rs = be.zeros((B, M)), be.zeros((B, M))
+        _ok(be, L.nc_fftconv_epilogue_fwd(s, B, M, h, w, ph, pw, FH, FW, be.ptr(xh),
+                                          be.ptr(ghat), aid, 0.01, be.ptr(wd), be.ptr(sd),
+                                          be.ptr(bd), be.ptr(z), be.ptr(p), be.ptr(mu),
+                                          be.ptr(rs), be.ptr(ws), nb), "fused")
+        outs.append((be.get(z)[:B_small], be.get(p)[:, :B_small], be.get(mu)[:B_small],
+                     be.get(rs)[:B_small]))
+    zo = O.conv2d_direct(xs, g[:, 0], (ph, pw))
+    return {"forms": max(rel_l2(a, b) for a, b in zip(outs[0], outs[1])),
+            "mismatch": sum(int((a != b).sum()) for a, b in zip(outs[0], outs[1])),
+            "z": rel_l2(outs[1][0], zo)}
+
+
 def case_fftconv_port(be, B=3, M=6, h=20, w=27, kh=7, kw=5, FH=32, FW=64, fact=None,
                       rows=(2, 3, 19, 3, 0), cols=(5, 5, 26, 5, 0), seed=11, two_pass=False):
     """nc_fftconv_port_fwd (the last step's correlation and output port in one operation)

@@ -10,7 +10,7 @@ from kernel_cases import (CODD_CASES, TOL, HostBackend, case_adaptive, case_bord
                           case_fftconv_circular, case_fftconv_port, case_fftconv_epilogue,
                           case_fftconv, case_helpers, case_plane_spectra, case_port,
                           case_spectral_ops, case_direct_conv, case_epilogue_fftconv_bwd,
-                          case_universe)
+                          case_universe, case_fused_forms)
 
 
 @pytest.fixture(scope="module")
@@ -125,6 +125,13 @@ def test_fftconv_epilogue(be, B, M, h, w, kh, kw, FH, FW, act, two_pass):
     assert res["xhat_mismatch"] == 0, res
     _assert_small({k: res[k] for k in ("z", "z_vs_separate", "out", "out_vs_separate", "mean",
                                        "rstd")})
+
+
+def test_fused_forward_forms(be):
+    """The fused forward's two forms agree bit for bit (the emulated device has two CUs: one
+    sample's four workgroups take the full-row form, three samples' twelve the windowed)."""
+    res = case_fused_forms(be, 1, 3)
+    assert res["mismatch"] == 0 and res["z"] < TOL, res
 
 
 @pytest.mark.parametrize("B,M,H,W,kh,kw", [

@@ -7,7 +7,7 @@ from kernel_cases import (CODD_CASES, EPILOGUE_SHAPES, PORT_SHAPES, TOL, DeviceB
                           case_fftconv_circular, case_fftconv_port, case_fftconv_epilogue,
                           case_fftconv, case_helpers, case_plane_spectra, case_port,
                           case_spectral_ops, case_direct_conv, case_epilogue_fftconv_bwd,
-                          case_universe)
+                          case_universe, case_fused_forms)
 
 pytestmark = pytest.mark.gpu
 
@@ -139,6 +139,17 @@ def test_fftconv_epilogue(be, B, M, h, w, kh, kw, FH, FW, act, two_pass):
     assert res["xhat_mismatch"] == 0, res
     _assert_small({k: res[k] for k in ("z", "z_vs_separate", "out", "out_vs_separate", "mean",
                                        "rstd")})
+
+
+def test_fused_forward_forms(be):
+    """The fused forward's full-row and windowed forms agree to rounding (rel-L2 1e-6): the
+    config-0 shapes at B = 128 (512 workgroups, two per CU of the MI355X's 256) and as the
+    first samples of B = 160 (640 workgroups: the windowed form)."""
+    import torch
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    small, large = 2 * cus // 4, 2 * cus // 4 + 32
+    res = case_fused_forms(be, small, large)
+    assert res["forms"] < 1e-6 and res["z"] < TOL, res
 
 
 @pytest.mark.parametrize("B,M,H,W,kh,kw", [
