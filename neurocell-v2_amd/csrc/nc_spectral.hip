@@ -1275,8 +1275,10 @@ int launch_rfft2(hipStream_t st, int nplanes, int hin, int win, bool flip, const
                  cpx* out, int post_kind = kPostNone, const SpecPost& post = SpecPost{},
                  int nparts = 1, size_t qstride = 0) {
     if constexpr (seg_grid<FH, FW>()) {
-        // unflipped planes without a phase ramp: one radix-8 workgroup per plane
-        if (!flip && post_kind != kPostShift) {
+        // unflipped planes without a phase ramp: one radix-8 workgroup per plane once there
+        // are more planes than CUs; below that the segmented transform's two column segments
+        // per plane give the CUs more workgroups (config 0, 128 planes: 7.19 -> 7.12 us)
+        if (!flip && post_kind != kPostShift && nplanes > cu_count()) {
             if (post_kind == kPostAdd)
                 launch_r8rfft2<kPostAdd>(st, nplanes, hin, win, x, out, post, nparts, qstride);
             else
