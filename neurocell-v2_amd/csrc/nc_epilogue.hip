@@ -234,15 +234,39 @@ __global__ __launch_bounds__(NT) void k_epi_bwd(
     float ta[MC][PPT], tb[MC][PPT];
     load_chunk<NT, PPT, MC, VEC>(ta, hb, N, z, delta, tid, zrow(mb), drow(mb));
     float lin[PPT], ac[PPT], dbs[PPT], bv[PPT], wv[PPT], sv[PPT], gv[PPT];
+    if constexpr (VEC) {  // runs of 4 pixels: one 16-byte load per operand
+        const int nv = N >> 2;
 #pragma unroll
-    for (int k = 0; k < PPT; ++k) {
-        const int pc = min(Px::at(tid, k), N - 1);
-        lin[k] = ac[k] = dbs[k] = 0.f;
-        bv[k] = bb[pc];
-        wv[k] = w[pc];
-        sv[k] = s[pc];
-        const float gl = gy[(size_t)b * N + pc];
-        gv[k] = Px::at(tid, k) < N ? gl : 0.f;  // zero cotangent outside the plane
+        for (int j = 0; j < PPT / 4; ++j) {
+            const int v = min(tid + j * NT, nv - 1);
+            const bool in = tid + j * NT < nv;
+            const float4 b4 = reinterpret_cast<const float4*>(bb)[v];
+            const float4 w4 = reinterpret_cast<const float4*>(w)[v];
+            const float4 s4 = reinterpret_cast<const float4*>(s)[v];
+            const float4 g4 = reinterpret_cast<const float4*>(gy + (size_t)b * N)[v];
+            const float bq[4] = {b4.x, b4.y, b4.z, b4.w}, wq[4] = {w4.x, w4.y, w4.z, w4.w};
+            const float sq[4] = {s4.x, s4.y, s4.z, s4.w}, gq[4] = {g4.x, g4.y, g4.z, g4.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int k = 4 * j + u;
+                lin[k] = ac[k] = dbs[k] = 0.f;
+                bv[k] = bq[u];
+                wv[k] = wq[u];
+                sv[k] = sq[u];
+                gv[k] = in ? gq[u] : 0.f;  // zero cotangent outside the plane
+            }
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < PPT; ++k) {
+            const int pc = min(Px::at(tid, k), N - 1);
+            lin[k] = ac[k] = dbs[k] = 0.f;
+            bv[k] = bb[pc];
+            wv[k] = w[pc];
+            sv[k] = s[pc];
+            const float gl = gy[(size_t)b * N + pc];
+            gv[k] = Px::at(tid, k) < N ? gl : 0.f;  // zero cotangent outside the plane
+        }
     }
     // one chunk: its arithmetic on `cur` with the next chunk's loads into `nxt` in flight
     auto chunk = [&](float (&cur)[MC][PPT], float (&nxt)[MC][PPT], int m0) {
@@ -1374,10 +1398,11 @@ static int epilogue_bwd(void* stream, int B, int M, int h, int w, int act, float
     int rc = dispatch_act(act, [&]<int ACT>() {
         if (N <= kSingleMaxPix) {
             const DirPlan P = bwd_plan(B, M, N);
-            // the pixel mapping (and so the reduction order) depends only on z, gz, delta:
-            // both forms of the entry point give bit-identical results
+            // the pixel mapping (and so the reduction order) depends only on the operands'
+            // alignment: both forms of the entry point give bit-identical results
             const bool vec = N % 4 == 0 && aligned16(z) && aligned16(gz) &&
-                             (!has_border || aligned16(delta));
+                             (!has_border || aligned16(delta)) && aligned16(w_eff) &&
+                             aligned16(s_eff) && aligned16(b_roi) && aligned16(gy);
             NC_BWD_DISPATCH(P, vec, dim3(B, P.G), dim3(P.c.nt), 0, st, M, N, P.mpg,
                             neg_slope, has_border, z, delta, w_eff, s_eff, b_roi, mean, rstd, gy,
                             gz, pg, RN);
