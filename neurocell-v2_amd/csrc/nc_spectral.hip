@@ -805,8 +805,9 @@ __global__ __launch_bounds__(64) void k_pconv_fwd(int M, int hout, int wout, int
 // Each wavefront leaves zhat, then act, in its own LDS region; the workgroup adds the four in
 // increasing m and writes the direction group's partial output
 // parts[g][b] = w_eff * sum zhat + s_eff * sum act, the layout of nc_epilogue_fwd_parts.
-// NE >= ceil(N / 64) plane values per lane; every loop runs NE (or NE / 4) times with clamped
-// loads, so a wavefront's loads issue together.
+// NE >= ceil(N / 64) plane values per lane (the full-row form: in runs of 4 consecutive
+// pixels, 16-byte moves of b_roi and z when N % 4 == 0); every loop runs NE (or NE / 4) times
+// with clamped loads, so a wavefront's loads issue together.
 template <int FH, int FW, int ACT, int NE, bool WIN>
 __global__ __launch_bounds__(256, 2) void k_pconv_epi(int B, int M, int hout, int wout, int ph,
                                                    int pw, int nq_off, int region, float slope,
@@ -859,38 +860,68 @@ __global__ __launch_bounds__(256, 2) void k_pconv_epi(int B, int M, int hout, in
     }
     __syncthreads();
     // the per-pixel parameters, requested together; their latency hides behind the statistics
+    // plane value i of a lane is element pe(i): in the full-row form runs of 4 consecutive
+    // pixels, moved as 16-byte loads and stores when the plane size and the operands allow
+    // (in the windowed form, whose registers must leave room for three workgroups per CU,
+    // element lane + 64 i)
+    auto pe = [&](int i) {
+        if constexpr (WIN) return lane + 64 * i;
+        else return 4 * (lane + 64 * (i >> 2)) + (i & 3);
+    };
+    const bool v4 = !WIN && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(b_roi) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(z) & 15) == 0;
     float bv[NE], wq[NC], sq_[NC];
+    if (v4) {
 #pragma unroll
-    for (int i = 0; i < NE; ++i) bv[i] = b_roi[min(lane + 64 * i, N - 1)];
+        for (int j = 0; j < NE / 4; ++j) {
+            const float4 b4 =
+                reinterpret_cast<const float4*>(b_roi)[min(lane + 64 * j, (N >> 2) - 1)];
+            bv[4 * j] = b4.x;
+            bv[4 * j + 1] = b4.y;
+            bv[4 * j + 2] = b4.z;
+            bv[4 * j + 3] = b4.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NE; ++i) bv[i] = b_roi[min(pe(i), N - 1)];
+    }
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
         const int e = min((int)threadIdx.x + 256 * i, N - 1);
         wq[i] = w_eff[e];
         sq_[i] = s_eff[e];
     }
-    // the plane, element e = lane + 64 i at (e / wout, e % wout) of the staging
+    // the plane, element e = pe(i) at (e / wout, e % wout) of the staging
     const unsigned inv = ((1u << 20) + wout - 1) / wout;
     float zv[NE];
 #pragma unroll
     for (int i = 0; i < NE; ++i) {
-        const int e = min(lane + 64 * i, N - 1);
+        const int e = min(pe(i), N - 1);
         const int r = (int)(((unsigned)e * inv) >> 20);
         zv[i] = lds[r * (FW + 1) + (e - r * wout)];
     }
     float sum = 0.f;
 #pragma unroll
-    for (int i = 0; i < NE; ++i) sum += lane + 64 * i < N ? zv[i] : 0.f;
+    for (int i = 0; i < NE; ++i) sum += pe(i) < N ? zv[i] : 0.f;
     if (z && live) {
         float* zo = z + ((size_t)b * M + m) * N;
+        if (v4) {
 #pragma unroll
-        for (int i = 0; i < NE; ++i)
-            if (lane + 64 * i < N) zo[lane + 64 * i] = zv[i];
+            for (int j = 0; j < NE / 4; ++j)
+                if (4 * (lane + 64 * j) < N)
+                    reinterpret_cast<float4*>(zo)[lane + 64 * j] =
+                        make_float4(zv[4 * j], zv[4 * j + 1], zv[4 * j + 2], zv[4 * j + 3]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < NE; ++i)
+                if (pe(i) < N) zo[pe(i)] = zv[i];
+        }
     }
     const float mu = wave_sum(sum) * inv_n;
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < NE; ++i) {
-        const float d = lane + 64 * i < N ? zv[i] - mu : 0.f;
+        const float d = pe(i) < N ? zv[i] - mu : 0.f;
         ss += d * d;
     }
     const float r = 1.0f / sqrtf(wave_sum(ss) * inv_n + 1e-5f);
@@ -908,7 +939,7 @@ __global__ __launch_bounds__(256, 2) void k_pconv_epi(int B, int M, int hout, in
         float* A = lds + N;
 #pragma unroll
         for (int i = 0; i < NE; ++i) {
-            const int e = lane + 64 * i;
+            const int e = pe(i);
             const float zn = (zv[i] - mu) * r;
             const float a = act_f<ACT>(zn + bv[i], slope);
             if (e < N) {
@@ -934,7 +965,7 @@ __global__ __launch_bounds__(256, 2) void k_pconv_epi(int B, int M, int hout, in
     }
 #pragma unroll
     for (int i = 0; i < NE; ++i) {
-        const int e = lane + 64 * i;
+        const int e = pe(i);
         zv[i] = (zv[i] - mu) * r;
         if (e < N) lds[e] = zv[i] * on;
     }
@@ -950,7 +981,7 @@ __global__ __launch_bounds__(256, 2) void k_pconv_epi(int B, int M, int hout, in
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < NE; ++i) {
-        const int e = lane + 64 * i;
+        const int e = pe(i);
         const float a = act_f<ACT>(zv[i] + bv[i], slope);
         if (e < N) lds[e] = a * on;
     }

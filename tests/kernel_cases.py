@@ -561,11 +561,12 @@ def case_fused_forms(be, B_small, B_large, M=16, h=40, w=50, kh=23, kw=13, FH=64
     staged one plane at a time) when the grid holds more than two workgroups per CU, the
     full-row form otherwise; the same B_small samples run once alone (B_small * G at most
     twice the CU count) and once as the first samples of a B_large batch (above it).  Each
-    sample's results depend on that sample only, so any difference is the forms': the same
-    arithmetic in two compilations, which hipcc may contract differently (the CPU emulation
-    gives equal bits).  Returns the largest rel-L2 difference over z, the partial outputs,
-    mean and rstd ("forms"), the elements that differ at all, and the windowed z against
-    the oracle."""
+    sample's results depend on that sample only, so any difference is the forms': the
+    full-row form's lanes hold runs of four pixels and the windowed form's single pixels, so
+    their plane statistics are summed in different orders (and hipcc contracts the two
+    compilations differently).  Returns the largest rel-L2 difference over z, the partial
+    outputs, mean and rstd ("forms"), the elements that differ at all, and the windowed z
+    against the oracle."""
     rng = np.random.default_rng(seed)
     L, s = be.lib, be.stream()
     ph, pw = (kh - 1) // 2, (kw - 1) // 2

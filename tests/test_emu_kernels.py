@@ -128,10 +128,11 @@ def test_fftconv_epilogue(be, B, M, h, w, kh, kw, FH, FW, act, two_pass):
 
 
 def test_fused_forward_forms(be):
-    """The fused forward's two forms agree bit for bit (the emulated device has two CUs: one
-    sample's four workgroups take the full-row form, three samples' twelve the windowed)."""
+    """The fused forward's two forms agree to rounding, rel-L2 1e-6 (the emulated device has
+    two CUs: one sample's four workgroups take the full-row form, three samples' twelve the
+    windowed; their lanes sum the plane statistics in different pixel orders)."""
     res = case_fused_forms(be, 1, 3)
-    assert res["mismatch"] == 0 and res["z"] < TOL, res
+    assert res["forms"] < 1e-6 and res["z"] < TOL, res
 
 
 @pytest.mark.parametrize("B,M,H,W,kh,kw", [
