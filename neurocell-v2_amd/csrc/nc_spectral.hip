@@ -1060,28 +1060,44 @@ __global__ __launch_bounds__(256, 2) void k_pconv_port(int B, int M, int hout, i
     int pe[PK];
 #pragma unroll
     for (int j = 0; j < PK; ++j) pe[j] = min(max(pidx[min(lane + 64 * j, P - 1)], 0), N - 1);
+    // plane value i of a lane is element px(i): in the full-row form runs of 4 consecutive
+    // pixels, z stored as 16-byte moves when the plane size and z allow (in the windowed form
+    // element lane + 64 i)
+    auto px = [&](int i) {
+        if constexpr (WIN) return lane + 64 * i;
+        else return 4 * (lane + 64 * (i >> 2)) + (i & 3);
+    };
+    const bool v4 = !WIN && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(z) & 15) == 0;
     const unsigned inv = ((1u << 20) + wout - 1) / wout;
     float zv[NE];
 #pragma unroll
     for (int i = 0; i < NE; ++i) {
-        const int e = min(lane + 64 * i, N - 1);
+        const int e = min(px(i), N - 1);
         const int r = (int)(((unsigned)e * inv) >> 20);
         zv[i] = lds[r * (FW + 1) + (e - r * wout)];
     }
     float sum = 0.f;
 #pragma unroll
-    for (int i = 0; i < NE; ++i) sum += lane + 64 * i < N ? zv[i] : 0.f;
+    for (int i = 0; i < NE; ++i) sum += px(i) < N ? zv[i] : 0.f;
     if (z && live) {
         float* zp = z + ((size_t)b * M + m) * N;
+        if (v4) {
 #pragma unroll
-        for (int i = 0; i < NE; ++i)
-            if (lane + 64 * i < N) zp[lane + 64 * i] = zv[i];
+            for (int j = 0; j < NE / 4; ++j)
+                if (4 * (lane + 64 * j) < N)
+                    reinterpret_cast<float4*>(zp)[lane + 64 * j] =
+                        make_float4(zv[4 * j], zv[4 * j + 1], zv[4 * j + 2], zv[4 * j + 3]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < NE; ++i)
+                if (px(i) < N) zp[px(i)] = zv[i];
+        }
     }
     const float mu = wave_sum(sum) * inv_n;
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < NE; ++i) {
-        const float d = lane + 64 * i < N ? zv[i] - mu : 0.f;
+        const float d = px(i) < N ? zv[i] - mu : 0.f;
         ss += d * d;
     }
     const float r = 1.0f / sqrtf(wave_sum(ss) * inv_n + 1e-5f);
